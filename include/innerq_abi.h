@@ -1,0 +1,191 @@
+/* innerq_abi.h -- C ABI of libinnerq_hip.so, the MI355X (gfx950) InnerQ KV-cache hot path.
+ *
+ * The reference (mthcom/innerq) has no native FFI: its boundary is the Python
+ * API of src/innerq/quant.py and src/innerq/cache.py, backed by torch ops.
+ * Each entry point below replaces the torch work behind one piece of that API
+ * (cited per function).  The Python package innerq_amd binds these through
+ * ctypes; INTEGRATION.md shows the binding a maintainer of the reference adds.
+ *
+ * Conventions
+ *  - All tensor arguments are device pointers (hipMalloc'd or from a torch
+ *    CUDA tensor), plain sizes and element strides; no torch types.
+ *  - fp16 tensors are passed as `const void*` / `void*` (IEEE binary16).
+ *  - `stream` is a hipStream_t passed as `void*` (NULL = default stream).
+ *    Every call is asynchronous and stream ordered.  Nothing allocates: the
+ *    caller passes any workspace, sized by the matching *_workspace_bytes().
+ *  - Every entry point validates its arguments on the host before any launch
+ *    and returns 0 (IQ_OK) or a negative IQ_ERR_* code; iq_strerror() names it.
+ *  - bits in {2,3,4}; group in {32,64,128}; head_dim D in {64,128};
+ *    query heads per KV head (Hq/Hkv) in {1,2,4,8}; mode IQ_MODE_ASYM or
+ *    IQ_MODE_SYM (quant.py:43-56 'asymmetric' / 'symmetric').
+ *
+ * Packed stores (layout owned by this library)
+ *  K store, groups along head_dim (quant.py:75-77 channeldim):
+ *     codes  uint32 [B, H, t_cap/64, D/G, 64, G*bits/32]
+ *     meta   uint16 [B, H, t_cap/64, D/G, 64, M]      M = 2 (scale, zero) asym, 1 (scale) sym
+ *  V store, groups along tokens (quant.py:79-81 tokendim):
+ *     codes  uint32 [B, H, t_cap/G, D, G*bits/32]
+ *     meta   uint16 [B, H, t_cap/G, D, M]
+ *  Inside a group, code i occupies bits [bits*i, bits*i+bits) LSB first
+ *  (speedtest/benchmark_quantization.cu:25-84); asym stores the code, sym the
+ *  two's complement of sign*magnitude.
+ */
+#ifndef INNERQ_ABI_H
+#define INNERQ_ABI_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define IQ_ABI_VERSION 1
+#define IQ_TOKEN_BLOCK 64
+
+enum iq_status {
+  IQ_OK = 0,
+  IQ_ERR_NULL = -1,       /* a required pointer is NULL */
+  IQ_ERR_BITS = -2,       /* bits not in {2,3,4} */
+  IQ_ERR_GROUP = -3,      /* group not in {32,64,128} or does not divide the grouped axis */
+  IQ_ERR_SHAPE = -4,      /* a size is negative / zero where not allowed / unsupported head_dim or GQA ratio */
+  IQ_ERR_ALIGN = -5,      /* pointer or stride not aligned as the kernel needs */
+  IQ_ERR_WORKSPACE = -6,  /* workspace missing or smaller than *_workspace_bytes() */
+  IQ_ERR_MODE = -7,       /* mode not IQ_MODE_ASYM / IQ_MODE_SYM */
+  IQ_ERR_RANGE = -8,      /* token offset + count exceeds the store capacity */
+  IQ_ERR_HIP = -9         /* a HIP launch failed */
+};
+
+enum iq_mode { IQ_MODE_ASYM = 0, IQ_MODE_SYM = 1 };
+
+/* ABI version (IQ_ABI_VERSION) and error names. */
+int iq_abi_version(void);
+const char* iq_strerror(int status);
+
+/* Byte sizes of a packed store with capacity t_cap tokens (K: t_cap % 64 == 0,
+ * V: t_cap % group == 0).  Replaces the int32 code tensors and fp16
+ * scale/zero tensors the reference keeps per layer (cache.py:190-210). */
+int iq_k_store_bytes(int64_t B, int64_t H, int64_t t_cap, int64_t D, int group, int bits, int mode,
+                     int64_t* codes_bytes, int64_t* meta_bytes);
+int iq_v_store_bytes(int64_t B, int64_t H, int64_t t_cap, int64_t D, int group, int bits, int mode,
+                     int64_t* codes_bytes, int64_t* meta_bytes);
+
+/* Quantize n new tokens x[B,H,n,D] (fp16; element strides sx_b, sx_h, sx_t;
+ * D contiguous) with groups along D and write them at token offset t_off of a
+ * K store.  Replaces quantize_channeldim_{asym,sym} (quant.py:58-77, 95-115)
+ * plus the torch.cat append of cache.py:314-339 (quantize_new_keys).
+ * norm: optional fp16 [B,H,D] key-normalization factor; x is divided by it
+ * in fp16 first (cache.py:121-126).  Codes are bit-exact to quant.py.
+ * Optional dense outputs (NULL to skip), contiguous:
+ *   codes_i32 int32 [B,H,n,D]   exactly quant.py's codes (INT32_MIN for NaN);
+ *                               for sym the magnitude codes
+ *   scale16 fp16 [B,H,n,D/G], zero16 fp16 [B,H,n,D/G] (asym only),
+ *   signs16 fp16 [B,H,n,D] (sym only; torch.sign of the normalized input). */
+int iq_quantize_k(const void* x, int64_t sx_b, int64_t sx_h, int64_t sx_t, const void* norm,
+                  int B, int H, int n, int D, int group, int bits, int mode,
+                  uint32_t* k_codes, uint16_t* k_meta, int64_t t_cap, int64_t t_off,
+                  int32_t* codes_i32, void* scale16, void* zero16, void* signs16, void* stream);
+
+/* Quantize n new tokens x[B,H,n,D] with groups along the token axis (n % group
+ * == 0, t_off % group == 0) into a V store.  Replaces
+ * quantize_tokendim_{asym,sym} (quant.py:79-81, 117-119) plus the append of
+ * cache.py:341-365 (quantize_new_values).  Dense outputs as iq_quantize_k but
+ * scale16/zero16 are [B,H,n/G,D]. */
+int iq_quantize_v(const void* x, int64_t sx_b, int64_t sx_h, int64_t sx_t,
+                  int B, int H, int n, int D, int group, int bits, int mode,
+                  uint32_t* v_codes, uint16_t* v_meta, int64_t t_cap, int64_t t_off,
+                  int32_t* codes_i32, void* scale16, void* zero16, void* signs16, void* stream);
+
+/* Dense dequantized K [B,H,T,D] of store tokens [t0, t0+T) (fp32 c*s + z, or
+ * c*s for sym, then * norm when given), written as fp16 (out16) and/or fp32
+ * (out32) with element strides so_b, so_h, so_t.  Replaces
+ * dequantize_channeldim_{asym,sym} (quant.py:83-87, 121-125) and the
+ * unnormalize step of cache.py:241-250 (get_keys_deq). */
+int iq_dequant_k(const uint32_t* k_codes, const uint16_t* k_meta, int64_t t_cap, const void* norm,
+                 int B, int H, int t0, int T, int D, int group, int bits, int mode,
+                 void* out16, float* out32, int64_t so_b, int64_t so_h, int64_t so_t, void* stream);
+
+/* Dense dequantized V, as iq_dequant_k (quant.py:89-93, 127-131; cache.py:263-271).
+ * t0 and T multiples of group. */
+int iq_dequant_v(const uint32_t* v_codes, const uint16_t* v_meta, int64_t t_cap,
+                 int B, int H, int t0, int T, int D, int group, int bits, int mode,
+                 void* out16, float* out32, int64_t so_b, int64_t so_h, int64_t so_t, void* stream);
+
+/* Dequantize dense int32 codes (the unpacked form quant.py returns):
+ * tensor [outer, n, inner] grouped along n (channeldim: inner = 1; tokendim:
+ * n = tokens, inner = head_dim); scale16 fp16 [outer, n/G, inner]; zs16 is the
+ * fp16 zero point [outer, n/G, inner] (asym) or the fp16 sign tensor
+ * [outer, n, inner] (sym).  out is fp32 (out_f16 = 0) or fp16 (out_f16 = 1),
+ * computed in that dtype with one rounding per op.  Replaces
+ * dequantize_{channeldim,tokendim}_{asym,sym} (quant.py:83-93, 121-131) for
+ * callers holding reference-format codes. */
+int iq_dequant_dense(const int32_t* codes, const void* scale16, const void* zs16, int64_t outer, int64_t n,
+                     int64_t inner, int group, int mode, int out_f16, void* out, void* stream);
+
+/* Decode QK^T GEMV over a packed K store: for store tokens [t0, t0+T),
+ *   out[b, h, t] = scale * sum_g ( s_g * sum_{i in g} q'[b,h,i] c[t,i] + z_g * sum_{i in g} q'[b,h,i] )
+ * with KV head h / (Hq/Hkv) (repeat_kv), q' = q (or q * norm, folding the key
+ * normalization of cache.py:249 into the query), fp32 accumulation.
+ * q fp16 [B,Hq,D] (strides sq_b, sq_h; D contiguous); out fp32 with strides
+ * so_b, so_h (token index contiguous).  Replaces matmul(q, repeat_kv(K_deq)^T)
+ * * scaling (TF/models/llama/modeling_llama.py:201-204) over the quantized
+ * segment, without materializing K_deq. */
+int iq_qk_gemv(const void* q, int64_t sq_b, int64_t sq_h, const void* norm,
+               const uint32_t* k_codes, const uint16_t* k_meta, int64_t t_cap,
+               int B, int Hq, int Hkv, int t0, int T, int D, int group, int bits, int mode, float scale,
+               float* out, int64_t so_b, int64_t so_h, void* stream);
+
+/* Workspace for iq_av_gemv: fp32 split-T partials. */
+size_t iq_av_workspace_bytes(int B, int Hq, int T, int D, int group);
+
+/* Decode attn.V GEMV over a packed V store: for store tokens [t0, t0+T)
+ * (multiples of group),
+ *   out[b, h, d] = sum_g ( s[g,d] * sum_{t in g} p[b,h,t] c[t,d] + z[g,d] * sum_{t in g} p[b,h,t] )
+ * p fp16 [B,Hq,T] (strides sp_b, sp_h; tokens contiguous).  Split-T partials
+ * go to the workspace and an atomic-free second pass sums them.  If accumulate
+ * is nonzero the result is added to out32 (fp32 [B,Hq,D], strides so_*)
+ * instead of overwriting it.  out16 (fp16, same strides) optional.  Replaces
+ * matmul(p, repeat_kv(V_deq)) (TF/models/llama/modeling_llama.py:210). */
+int iq_av_gemv(const void* p, int64_t sp_b, int64_t sp_h,
+               const uint32_t* v_codes, const uint16_t* v_meta, int64_t t_cap,
+               int B, int Hq, int Hkv, int t0, int T, int D, int group, int bits, int mode,
+               float* out32, void* out16, int64_t so_b, int64_t so_h, int accumulate,
+               void* workspace, size_t workspace_bytes, void* stream);
+
+/* One K or V segment of a decode step. Segments are laid end to end in token
+ * order: sink (fp16) | quantized (store) | recent (fp16), as concatenated by
+ * cache.py:235-276.  An fp16 segment is x[B,Hkv,n,D] with strides
+ * (s_b, s_h, s_t), D contiguous.  A quantized segment names a store and its
+ * first token. */
+typedef struct iq_segment {
+  const void* dense;          /* fp16 segment or NULL */
+  int64_t s_b, s_h, s_t;
+  int n;                      /* tokens in this segment (0 = absent) */
+  const uint32_t* codes;      /* packed store (quantized segment) or NULL */
+  const uint16_t* meta;
+  int64_t t_cap;
+  int t0;
+  int bits, group, mode;
+} iq_segment;
+
+size_t iq_decode_workspace_bytes(int B, int Hq, int T, int D);
+
+/* Full decode attention for one layer and one new query token per sequence:
+ * logits over K = [ks | kq | kr] (QK^T, scaled), fp32 softmax cast to fp16
+ * (TF/models/llama/modeling_llama.py:208), then p.V over V = [vs | vq | vr].
+ * k[3] / v[3] are the sink, quantized and recent segments; the token counts of
+ * K and V must each sum to T.  norm: optional fp16 [B,Hkv,D] key
+ * normalization factor of the quantized K segment.  out fp16 [B,Hq,D]
+ * (strides so_b, so_h).  Replaces update()'s dense read path (cache.py:278-281,
+ * 395) plus the eager attention of TF/models/llama/modeling_llama.py:201-210. */
+int iq_decode_attention(const void* q, int64_t sq_b, int64_t sq_h, const void* norm,
+                        const iq_segment* k, const iq_segment* v,
+                        int B, int Hq, int Hkv, int T, int D, float scale,
+                        void* out, int64_t so_b, int64_t so_h,
+                        void* workspace, size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* INNERQ_ABI_H */

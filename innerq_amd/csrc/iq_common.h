@@ -1,0 +1,51 @@
+// Host-side helpers shared by the C-ABI entry points: argument validation
+// (done before any launch, so every error path is testable without a GPU),
+// compile-time dispatch over (bits, group, head_dim, GQA ratio).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/innerq_abi.h"
+
+namespace iq {
+
+inline bool bits_ok(int bits) { return bits == 2 || bits == 3 || bits == 4; }
+inline bool group_ok(int g) { return g == 32 || g == 64 || g == 128; }
+inline bool mode_ok(int m) { return m == IQ_MODE_ASYM || m == IQ_MODE_SYM; }
+inline bool d_ok(int d) { return d == 64 || d == 128; }
+inline bool nrep_ok(int r) { return r == 1 || r == 2 || r == 4 || r == 8; }
+inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
+
+#define IQ_CHECK(cond, err) \
+  do {                      \
+    if (!(cond)) return (err); \
+  } while (0)
+
+inline int check_common(int bits, int group, int mode) {
+  IQ_CHECK(bits_ok(bits), IQ_ERR_BITS);
+  IQ_CHECK(group_ok(group), IQ_ERR_GROUP);
+  IQ_CHECK(mode_ok(mode), IQ_ERR_MODE);
+  return IQ_OK;
+}
+
+inline int launch_status() {
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? IQ_OK : IQ_ERR_HIP;
+}
+
+inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+// Dispatch helpers: call f.template operator()<BITS, G>() for runtime (bits, group).
+template <typename F>
+int dispatch_bits_group(int bits, int group, F&& f) {
+#define IQ_CASE(B_, G_) \
+  if (bits == B_ && group == G_) return f.template operator()<B_, G_>();
+  IQ_CASE(2, 32) IQ_CASE(2, 64) IQ_CASE(2, 128)
+  IQ_CASE(3, 32) IQ_CASE(3, 64) IQ_CASE(3, 128)
+  IQ_CASE(4, 32) IQ_CASE(4, 64) IQ_CASE(4, 128)
+#undef IQ_CASE
+  return IQ_ERR_BITS;
+}
+
+}  // namespace iq

@@ -1,0 +1,144 @@
+// Device-side building blocks for the InnerQ gfx950 kernels.
+//
+// Packed group format (one quantization group of G codes, b bits each):
+// code i sits at bits [b*i, b*i+b) of a little-endian bit string stored as
+// G*b/32 32-bit words, LSB first (the convention of the reference's speedtest
+// kernels, speedtest/benchmark_quantization.cu:25-84).  Asym codes are the
+// unsigned field; sym codes are the b-bit two's complement of sign*magnitude.
+//
+// In-register unpack ("pair plans").  A GEMV never converts codes one by one.
+// A window of the group's bit string (a word, a shifted word, or an alignbit
+// of two words) is masked and OR-ed with an fp16 exponent pattern in one
+// v_and_or_b32, which yields two fp16 values {bias_a + c_a, bias_b + c_b}
+// exactly (field LSB weight 1, bias 2^(10-p) for a field at in-half bit p).
+// One v_dot2_f32_f16 then multiplies the pair with the matching pair of the
+// fp16 operand (q for QK^T, p for attn.V) and accumulates in fp32.  The bias
+// contribution sum(operand * bias) is a per-(group, head) constant and is
+// subtracted by starting the accumulation at -beta.  Sym codes are turned
+// into offset binary with one XOR per word (u = signed + 2^(b-1)), so
+// sum(q*signed) = sum(q*u) - 2^(b-1)*sum(q), folded into the zero term.
+//
+// Plans (windows counted as extra VALU ops, aligned words are free):
+//   4-bit, per word (8 codes):   s=0 {(0,4),(1,5)}, s=8 {(2,6),(3,7)}
+//   2-bit, per word (16 codes):  s=0 {(i,i+8) i<5},  s=10 {(i,i+8) 5<=i<8}
+//   3-bit, per 3 words (32 codes): distance-5 pairs in two 10-code blocks,
+//          distance-6 pairs for the last 12 codes; windows
+//          s in {-1, 8, 29, 38, 60, 66, 72}.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+#include <stdint.h>
+
+namespace iq {
+
+typedef _Float16 h2_t __attribute__((ext_vector_type(2)));
+
+constexpr int TOKEN_BLOCK = 64;
+
+// ---------------------------------------------------------------------------
+// pair plans
+// ---------------------------------------------------------------------------
+template <int BITS> struct Plan;
+
+template <> struct Plan<4> {
+  static constexpr int WORDS = 1, CODES = 8, NPAIR = 4;
+  static constexpr int S[NPAIR] = {0, 0, 8, 8};
+  static constexpr int A[NPAIR] = {0, 1, 2, 3};
+  static constexpr int C[NPAIR] = {4, 5, 6, 7};
+  static constexpr uint32_t SIGN[WORDS] = {0x88888888u};
+};
+template <> struct Plan<2> {
+  static constexpr int WORDS = 1, CODES = 16, NPAIR = 8;
+  static constexpr int S[NPAIR] = {0, 0, 0, 0, 0, 10, 10, 10};
+  static constexpr int A[NPAIR] = {0, 1, 2, 3, 4, 5, 6, 7};
+  static constexpr int C[NPAIR] = {8, 9, 10, 11, 12, 13, 14, 15};
+  static constexpr uint32_t SIGN[WORDS] = {0xAAAAAAAAu};
+};
+template <> struct Plan<3> {
+  static constexpr int WORDS = 3, CODES = 32, NPAIR = 16;
+  static constexpr int S[NPAIR] = {-1, -1, -1, 8, 8, 29, 29, 29, 38, 38, 60, 60, 66, 66, 72, 72};
+  static constexpr int A[NPAIR] = {0, 1, 2, 3, 4, 10, 11, 12, 13, 14, 20, 21, 22, 23, 24, 25};
+  static constexpr int C[NPAIR] = {5, 6, 7, 8, 9, 15, 16, 17, 18, 19, 26, 27, 28, 29, 30, 31};
+  static constexpr uint32_t SIGN[WORDS] = {0x24924924u, 0x49249249u, 0x92492492u};
+};
+
+template <int BITS> __host__ __device__ constexpr int pa_of(int k) { return BITS * Plan<BITS>::A[k] - Plan<BITS>::S[k]; }
+template <int BITS> __host__ __device__ constexpr int pc_of(int k) { return BITS * Plan<BITS>::C[k] - Plan<BITS>::S[k] - 16; }
+template <int BITS> __host__ __device__ constexpr uint32_t mask_of(int k) {
+  return (((1u << BITS) - 1u) << pa_of<BITS>(k)) | (((1u << BITS) - 1u) << (16 + pc_of<BITS>(k)));
+}
+template <int BITS> __host__ __device__ constexpr uint32_t magic_of(int k) {
+  return (uint32_t(25 - pa_of<BITS>(k)) << 10) | (uint32_t(25 - pc_of<BITS>(k)) << 26);
+}
+template <int BITS> __host__ __device__ constexpr float bias_a(int k) { return float(1 << (10 - pa_of<BITS>(k))); }
+template <int BITS> __host__ __device__ constexpr float bias_c(int k) { return float(1 << (10 - pc_of<BITS>(k))); }
+
+// window of the super-block's bit string starting at bit S (S may be -1..-9:
+// a left shift of word 0; windows past the end are zero-filled).
+template <int BITS, int S>
+__device__ __forceinline__ uint32_t window(const uint32_t* w) {
+  constexpr int NW = Plan<BITS>::WORDS;
+  if constexpr (S < 0) {
+    return w[0] << (-S);
+  } else if constexpr ((S & 31) == 0) {
+    return w[S >> 5];
+  } else if constexpr ((S >> 5) + 1 < NW) {
+    return __builtin_amdgcn_alignbit(w[(S >> 5) + 1], w[S >> 5], S & 31);
+  } else {
+    return w[S >> 5] >> (S & 31);
+  }
+}
+
+// (x & m) | c in one v_and_or_b32.  gfx9 VOP3 has no literal operand, so the
+// mask and the exponent pattern are passed in VGPRs (materialized once per
+// kernel); written with VALU inline asm because the compiler otherwise
+// splits it into v_and_b32 + v_or_b32 with literals.
+__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t c) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(m), "v"(c));
+  return r;
+}
+
+template <int BITS, int K>
+__device__ __forceinline__ h2_t extract_pair(const uint32_t* w) {
+  constexpr int S = Plan<BITS>::S[K];
+  const uint32_t x = and_or(window<BITS, S>(w), mask_of<BITS>(K), magic_of<BITS>(K));
+  return __builtin_bit_cast(h2_t, x);
+}
+
+__device__ __forceinline__ float dot2(h2_t a, h2_t b, float c) {
+  return __builtin_amdgcn_fdot2(a, b, c, false);
+}
+
+__device__ __forceinline__ h2_t h2_from_halves(__half a, __half b) {
+  h2_t r;
+  r.x = __builtin_bit_cast(_Float16, a);
+  r.y = __builtin_bit_cast(_Float16, b);
+  return r;
+}
+
+__device__ __forceinline__ float h2f(uint16_t bits) {
+  return __half2float(__ushort_as_half(bits));
+}
+
+// fp16 result of an fp32 value, round to nearest even (v_cvt_f16_f32).
+__device__ __forceinline__ float round_f16(float x) {
+  return __half2float(__float2half_rn(x));
+}
+
+// ---------------------------------------------------------------------------
+// wave64 reductions (DPP/permute through the compiler's shuffle lowering)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+
+}  // namespace iq

@@ -1,0 +1,539 @@
+// Quantize-on-append and dense dequantization kernels (gfx950).
+//
+// Quantization restates src/innerq/quant.py op by op: every fp16 op of the
+// reference (sub, division by the int level count, division by the scale) is
+// an fp32 op rounded to fp16 with round-to-nearest-even (exact for + - * /
+// because fp32 has more than 2*11+2 significand bits), the clamp keeps NaN,
+// the rounding is half-to-even (v_rndne_f32), and NaN becomes INT32_MIN in the
+// dense int32 output (0 in the packed field).  Division is IEEE (hipcc's
+// default correctly rounded fp32 divide; no fast-math anywhere in this build).
+//
+// One thread owns one quantization group: the group's min/max (or max |x|)
+// is a serial loop over G registers, which keeps the rounding order trivially
+// identical to the reference and needs no cross-lane traffic.  Appends are a
+// few hundred groups per decode step and prefill is a streaming pass, so this
+// kernel is latency- resp. HBM-bound either way.
+#include "iq_common.h"
+#include "iq_device.h"
+
+using namespace iq;
+
+namespace {
+
+constexpr int32_t I32_MIN = (int32_t)0x80000000u;
+
+struct QuantOut {
+  uint32_t* codes;     // packed store codes (or null)
+  uint16_t* meta;      // packed store meta
+  int64_t cap_units;   // K: t_cap/64 blocks, V: t_cap/G groups
+  int64_t t_off;       // first token written in the store
+  int32_t* codes_i32;  // dense outputs (optional)
+  uint16_t* scale16;
+  uint16_t* zero16;
+  uint16_t* signs16;
+};
+
+__device__ __forceinline__ bool is_nan(float v) { return v != v; }
+
+// clamp(y, 0, L) keeping NaN, then half-to-even round.  Returns the dense
+// int32 code (INT32_MIN for NaN, as torch's float->int32 on x86).
+__device__ __forceinline__ int32_t code_of(float y, float L) {
+  if (is_nan(y)) return I32_MIN;
+  y = fminf(fmaxf(y, 0.0f), L);
+  return (int32_t)rintf(y);
+}
+
+// Quantize G values held as fp32 copies of fp16 numbers.  fields[] receives
+// the b-bit stored field, codes[] the dense reference code, sgn[] the sign.
+template <int BITS, int G>
+__device__ __forceinline__ void quantize_group(const float* v, bool sym, uint32_t* fields, int32_t* codes,
+                                               float* sgn, float& s_out, float& z_out) {
+  constexpr uint32_t FMASK = (1u << BITS) - 1u;
+  if (!sym) {
+    float mn = v[0], mx = v[0];
+    bool nan = false;
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+      nan |= is_nan(v[i]);
+      mn = fminf(mn, v[i]);
+      mx = fmaxf(mx, v[i]);
+    }
+    if (nan) { mn = __builtin_nanf(""); mx = mn; }
+    const float L = float((1 << BITS) - 1);
+    const float s = round_f16(round_f16(mx - mn) / L);          // quant.py:68
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+      const float y = round_f16(round_f16(v[i] - mn) / s);      // quant.py:69-70
+      const int32_t c = code_of(y, L);                          // quant.py:71
+      codes[i] = c;
+      fields[i] = (c == I32_MIN) ? 0u : (uint32_t(c) & FMASK);
+      sgn[i] = 0.f;
+    }
+    s_out = s;
+    z_out = mn;
+  } else {
+    float mx = 0.f;
+    bool nan = false;
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+      nan |= is_nan(v[i]);
+      mx = fmaxf(mx, fabsf(v[i]));
+    }
+    if (nan) mx = __builtin_nanf("");
+    const float L = float((1 << (BITS - 1)) - 1);
+    const float s = round_f16(mx / L);                          // quant.py:107
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+      const float y = round_f16(fabsf(v[i]) / s);               // quant.py:108
+      const int32_t c = code_of(y, L);                          // quant.py:109
+      const float sg = v[i] > 0.f ? 1.f : (v[i] < 0.f ? -1.f : 0.f);  // torch.sign
+      codes[i] = c;
+      const int32_t sc = (c == I32_MIN) ? 0 : (sg > 0.f ? c : (sg < 0.f ? -c : 0));
+      fields[i] = uint32_t(sc) & FMASK;
+      sgn[i] = sg;
+    }
+    s_out = s;
+    z_out = 0.f;
+  }
+}
+
+template <int BITS, int G>
+__device__ __forceinline__ void pack_fields(const uint32_t* f, uint32_t* w) {
+  constexpr int W = G * BITS / 32;
+#pragma unroll
+  for (int j = 0; j < W; ++j) w[j] = 0u;
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    constexpr int dummy = 0;
+    (void)dummy;
+    const int bit = BITS * i;
+    const int wi = bit >> 5, o = bit & 31;
+    w[wi] |= f[i] << o;
+    if (o + BITS > 32) w[wi + 1] |= f[i] >> (32 - o);
+  }
+}
+
+template <int BITS, int G>
+__device__ __forceinline__ void unpack_fields(const uint32_t* w, bool sym, int32_t* c) {
+  constexpr uint32_t FMASK = (1u << BITS) - 1u;
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    const int bit = BITS * i;
+    const int wi = bit >> 5, o = bit & 31;
+    uint32_t f = w[wi] >> o;
+    if (o + BITS > 32) f |= w[wi + 1] << (32 - o);
+    f &= FMASK;
+    int32_t v = int32_t(f);
+    if (sym && (f >> (BITS - 1))) v -= (1 << BITS);
+    c[i] = v;
+  }
+}
+
+// ---- K: groups along head_dim, one thread per (b, h, t, g) ----------------
+template <int BITS, int G>
+__global__ __launch_bounds__(256) void quant_k_kernel(const uint16_t* __restrict__ x, int64_t sxb, int64_t sxh,
+                                                      int64_t sxt, const uint16_t* __restrict__ norm, int B,
+                                                      int H, int n, int D, int sym, QuantOut o) {
+  constexpr int W = G * BITS / 32;
+  const int ng = D / G;
+  const int64_t gid = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t total = int64_t(B) * H * n * ng;
+  if (gid >= total) return;
+  const int g = int(gid % ng);
+  int64_t r = gid / ng;
+  const int t = int(r % n);
+  r /= n;
+  const int h = int(r % H);
+  const int b = int(r / H);
+
+  const uint16_t* xp = x + b * sxb + h * sxh + t * sxt + g * G;
+  float v[G];
+#pragma unroll
+  for (int i = 0; i < G; i += 8) {
+    const uint4 u = *reinterpret_cast<const uint4*>(xp + i);
+    const uint32_t uu[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      v[i + 2 * j] = h2f(uint16_t(uu[j] & 0xffffu));
+      v[i + 2 * j + 1] = h2f(uint16_t(uu[j] >> 16));
+    }
+  }
+  if (norm) {  // cache.py:125  key_states / key_normalization_factor (fp16)
+    const uint16_t* np_ = norm + (int64_t(b) * H + h) * D + g * G;
+#pragma unroll
+    for (int i = 0; i < G; ++i) v[i] = round_f16(v[i] / h2f(np_[i]));
+  }
+  uint32_t f[G];
+  int32_t c[G];
+  float sg[G];
+  float s, z;
+  quantize_group<BITS, G>(v, sym != 0, f, c, sg, s, z);
+
+  const int64_t bh = int64_t(b) * H + h;
+  if (o.codes) {
+    uint32_t w[W];
+    pack_fields<BITS, G>(f, w);
+    const int64_t tt = o.t_off + t;
+    const int64_t blk = tt / TOKEN_BLOCK, row = tt % TOKEN_BLOCK;
+    const int64_t unit = ((bh * o.cap_units + blk) * ng + g) * TOKEN_BLOCK + row;
+    uint32_t* cp = o.codes + unit * W;
+#pragma unroll
+    for (int j = 0; j < W; ++j) cp[j] = w[j];
+    if (sym) {
+      o.meta[unit] = __half_as_ushort(__float2half_rn(s));
+    } else {
+      const uint32_t sz = uint32_t(__half_as_ushort(__float2half_rn(s))) |
+                          (uint32_t(__half_as_ushort(__float2half_rn(z))) << 16);
+      reinterpret_cast<uint32_t*>(o.meta)[unit] = sz;
+    }
+  }
+  const int64_t row_el = (bh * n + t) * D + g * G;
+  if (o.codes_i32) {
+#pragma unroll
+    for (int i = 0; i < G; ++i) o.codes_i32[row_el + i] = c[i];
+  }
+  if (o.signs16) {
+#pragma unroll
+    for (int i = 0; i < G; ++i) o.signs16[row_el + i] = __half_as_ushort(__float2half_rn(sg[i]));
+  }
+  const int64_t red = (bh * n + t) * ng + g;
+  if (o.scale16) o.scale16[red] = __half_as_ushort(__float2half_rn(s));
+  if (o.zero16) o.zero16[red] = __half_as_ushort(__float2half_rn(z));
+}
+
+// ---- V: groups along tokens, one thread per (b, h, token-group, d) --------
+template <int BITS, int G>
+__global__ __launch_bounds__(256) void quant_v_kernel(const uint16_t* __restrict__ x, int64_t sxb, int64_t sxh,
+                                                      int64_t sxt, int B, int H, int n, int D, int sym,
+                                                      QuantOut o) {
+  constexpr int W = G * BITS / 32;
+  const int ngn = n / G;
+  const int64_t gid = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t total = int64_t(B) * H * ngn * D;
+  if (gid >= total) return;
+  const int d = int(gid % D);
+  int64_t r = gid / D;
+  const int gi = int(r % ngn);
+  r /= ngn;
+  const int h = int(r % H);
+  const int b = int(r / H);
+
+  const uint16_t* xp = x + b * sxb + h * sxh + int64_t(gi) * G * sxt + d;
+  float v[G];
+#pragma unroll
+  for (int i = 0; i < G; ++i) v[i] = h2f(xp[i * sxt]);
+  uint32_t f[G];
+  int32_t c[G];
+  float sg[G];
+  float s, z;
+  quantize_group<BITS, G>(v, sym != 0, f, c, sg, s, z);
+
+  const int64_t bh = int64_t(b) * H + h;
+  if (o.codes) {
+    uint32_t w[W];
+    pack_fields<BITS, G>(f, w);
+    const int64_t gabs = o.t_off / G + gi;
+    const int64_t unit = (bh * o.cap_units + gabs) * D + d;
+    uint32_t* cp = o.codes + unit * W;
+#pragma unroll
+    for (int j = 0; j < W; ++j) cp[j] = w[j];
+    if (sym) {
+      o.meta[unit] = __half_as_ushort(__float2half_rn(s));
+    } else {
+      const uint32_t sz = uint32_t(__half_as_ushort(__float2half_rn(s))) |
+                          (uint32_t(__half_as_ushort(__float2half_rn(z))) << 16);
+      reinterpret_cast<uint32_t*>(o.meta)[unit] = sz;
+    }
+  }
+  if (o.codes_i32 || o.signs16) {
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+      const int64_t el = (bh * n + int64_t(gi) * G + i) * D + d;
+      if (o.codes_i32) o.codes_i32[el] = c[i];
+      if (o.signs16) o.signs16[el] = __half_as_ushort(__float2half_rn(sg[i]));
+    }
+  }
+  const int64_t red = (bh * ngn + gi) * D + d;
+  if (o.scale16) o.scale16[red] = __half_as_ushort(__float2half_rn(s));
+  if (o.zero16) o.zero16[red] = __half_as_ushort(__float2half_rn(z));
+}
+
+// ---- dequantization (dense read path) --------------------------------------
+struct DeqOut {
+  uint16_t* out16;
+  float* out32;
+  int64_t sob, soh, sot;
+};
+
+__device__ __forceinline__ void put(const DeqOut& o, int64_t off, float v) {
+  if (o.out16) o.out16[off] = __half_as_ushort(__float2half_rn(v));
+  if (o.out32) o.out32[off] = v;
+}
+
+template <int BITS, int G>
+__global__ __launch_bounds__(256) void dequant_k_kernel(const uint32_t* __restrict__ kc,
+                                                        const uint16_t* __restrict__ km, int64_t cap_blocks,
+                                                        const uint16_t* __restrict__ norm, int B, int H, int t0,
+                                                        int T, int D, int sym, DeqOut o) {
+  constexpr int W = G * BITS / 32;
+  const int ng = D / G;
+  const int64_t gid = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t total = int64_t(B) * H * T * ng;
+  if (gid >= total) return;
+  const int g = int(gid % ng);
+  int64_t r = gid / ng;
+  const int t = int(r % T);
+  r /= T;
+  const int h = int(r % H);
+  const int b = int(r / H);
+  const int64_t bh = int64_t(b) * H + h;
+  const int64_t tt = int64_t(t0) + t;
+  const int64_t unit = ((bh * cap_blocks + tt / TOKEN_BLOCK) * ng + g) * TOKEN_BLOCK + tt % TOKEN_BLOCK;
+  uint32_t w[W];
+#pragma unroll
+  for (int j = 0; j < W; ++j) w[j] = kc[unit * W + j];
+  int32_t c[G];
+  unpack_fields<BITS, G>(w, sym != 0, c);
+  float s, z = 0.f;
+  if (sym) {
+    s = h2f(km[unit]);
+  } else {
+    const uint32_t sz = reinterpret_cast<const uint32_t*>(km)[unit];
+    s = h2f(uint16_t(sz & 0xffffu));
+    z = h2f(uint16_t(sz >> 16));
+  }
+  const int64_t base = b * o.sob + h * o.soh + t * o.sot + g * G;
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    float v = __fadd_rn(__fmul_rn(float(c[i]), s), z);       // quant.py:84-85 (c*s exact)
+    if (norm) v = __fmul_rn(v, h2f(norm[bh * D + g * G + i]));  // cache.py:132
+    put(o, base + i, v);
+  }
+}
+
+template <int BITS, int G>
+__global__ __launch_bounds__(256) void dequant_v_kernel(const uint32_t* __restrict__ vc,
+                                                        const uint16_t* __restrict__ vm, int64_t cap_groups,
+                                                        int B, int H, int g0, int ngT, int D, int sym, DeqOut o) {
+  constexpr int W = G * BITS / 32;
+  const int64_t gid = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t total = int64_t(B) * H * ngT * D;
+  if (gid >= total) return;
+  const int d = int(gid % D);
+  int64_t r = gid / D;
+  const int gi = int(r % ngT);
+  r /= ngT;
+  const int h = int(r % H);
+  const int b = int(r / H);
+  const int64_t bh = int64_t(b) * H + h;
+  const int64_t unit = (bh * cap_groups + g0 + gi) * D + d;
+  uint32_t w[W];
+#pragma unroll
+  for (int j = 0; j < W; ++j) w[j] = vc[unit * W + j];
+  int32_t c[G];
+  unpack_fields<BITS, G>(w, sym != 0, c);
+  float s, z = 0.f;
+  if (sym) {
+    s = h2f(vm[unit]);
+  } else {
+    const uint32_t sz = reinterpret_cast<const uint32_t*>(vm)[unit];
+    s = h2f(uint16_t(sz & 0xffffu));
+    z = h2f(uint16_t(sz >> 16));
+  }
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    const float v = __fadd_rn(__fmul_rn(float(c[i]), s), z);  // quant.py:90-91
+    put(o, b * o.sob + h * o.soh + (int64_t(gi) * G + i) * o.sot + d, v);
+  }
+}
+
+// ---- dense int32 codes -> values (the quant.py dequantize_* API) ----------
+// tensor [outer, n, inner] grouped along n; scale/zero [outer, n/G, inner];
+// signs [outer, n, inner].  op in fp32 (out_f16 = 0) or fp16 (out_f16 = 1),
+// one rounding per op as torch does for that dtype (quant.py:83-93, 121-131).
+__global__ __launch_bounds__(256) void dequant_dense_kernel(const int32_t* __restrict__ codes,
+                                                            const uint16_t* __restrict__ scale,
+                                                            const uint16_t* __restrict__ zs, int64_t outer,
+                                                            int64_t n, int64_t inner, int G, int sym, int out_f16,
+                                                            void* out) {
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= outer * n * inner) return;
+  const int64_t j = i % inner;
+  const int64_t t = (i / inner) % n;
+  const int64_t o = i / (inner * n);
+  const int64_t red = (o * (n / G) + t / G) * inner + j;
+  const float c = float(codes[i]);
+  const float s = h2f(scale[red]);
+  float v;
+  if (!out_f16) {
+    v = __fmul_rn(c, s);
+    v = sym ? __fmul_rn(v, h2f(zs[i])) : __fadd_rn(v, h2f(zs[red]));
+    reinterpret_cast<float*>(out)[i] = v;
+  } else {
+    v = round_f16(__fmul_rn(round_f16(c), s));
+    v = sym ? round_f16(__fmul_rn(v, h2f(zs[i]))) : round_f16(__fadd_rn(v, h2f(zs[red])));
+    reinterpret_cast<uint16_t*>(out)[i] = __half_as_ushort(__float2half_rn(v));
+  }
+}
+
+}  // namespace
+
+// =============================================================================
+// C ABI
+// =============================================================================
+extern "C" {
+
+int iq_abi_version(void) { return IQ_ABI_VERSION; }
+
+const char* iq_strerror(int status) {
+  switch (status) {
+    case IQ_OK: return "ok";
+    case IQ_ERR_NULL: return "null pointer argument";
+    case IQ_ERR_BITS: return "bits must be 2, 3 or 4";
+    case IQ_ERR_GROUP: return "group must be 32, 64 or 128 and divide the grouped axis";
+    case IQ_ERR_SHAPE: return "unsupported or invalid shape";
+    case IQ_ERR_ALIGN: return "pointer or stride misaligned";
+    case IQ_ERR_WORKSPACE: return "workspace missing or too small";
+    case IQ_ERR_MODE: return "mode must be IQ_MODE_ASYM or IQ_MODE_SYM";
+    case IQ_ERR_RANGE: return "token range exceeds store capacity";
+    case IQ_ERR_HIP: return "HIP launch failed";
+    default: return "unknown status";
+  }
+}
+
+int iq_k_store_bytes(int64_t B, int64_t H, int64_t t_cap, int64_t D, int group, int bits, int mode,
+                     int64_t* codes_bytes, int64_t* meta_bytes) {
+  IQ_CHECK(codes_bytes && meta_bytes, IQ_ERR_NULL);
+  if (int e = check_common(bits, group, mode)) return e;
+  IQ_CHECK(B >= 0 && H >= 0 && t_cap >= 0 && D > 0, IQ_ERR_SHAPE);
+  IQ_CHECK(D % group == 0, IQ_ERR_GROUP);
+  IQ_CHECK(t_cap % TOKEN_BLOCK == 0, IQ_ERR_ALIGN);
+  *codes_bytes = B * H * t_cap * D * bits / 8;
+  *meta_bytes = B * H * t_cap * (D / group) * (mode == IQ_MODE_SYM ? 2 : 4);
+  return IQ_OK;
+}
+
+int iq_v_store_bytes(int64_t B, int64_t H, int64_t t_cap, int64_t D, int group, int bits, int mode,
+                     int64_t* codes_bytes, int64_t* meta_bytes) {
+  IQ_CHECK(codes_bytes && meta_bytes, IQ_ERR_NULL);
+  if (int e = check_common(bits, group, mode)) return e;
+  IQ_CHECK(B >= 0 && H >= 0 && t_cap >= 0 && D > 0, IQ_ERR_SHAPE);
+  IQ_CHECK(t_cap % group == 0, IQ_ERR_GROUP);
+  *codes_bytes = B * H * t_cap * D * bits / 8;
+  *meta_bytes = B * H * (t_cap / group) * D * (mode == IQ_MODE_SYM ? 2 : 4);
+  return IQ_OK;
+}
+
+int iq_quantize_k(const void* x, int64_t sx_b, int64_t sx_h, int64_t sx_t, const void* norm, int B, int H,
+                  int n, int D, int group, int bits, int mode, uint32_t* k_codes, uint16_t* k_meta,
+                  int64_t t_cap, int64_t t_off, int32_t* codes_i32, void* scale16, void* zero16, void* signs16,
+                  void* stream) {
+  IQ_CHECK(x, IQ_ERR_NULL);
+  if (int e = check_common(bits, group, mode)) return e;
+  IQ_CHECK(B >= 0 && H >= 0 && n >= 0 && D > 0, IQ_ERR_SHAPE);
+  IQ_CHECK(D % group == 0, IQ_ERR_GROUP);
+  IQ_CHECK(aligned(x, 16) && sx_b % 8 == 0 && sx_h % 8 == 0 && sx_t % 8 == 0, IQ_ERR_ALIGN);
+  IQ_CHECK((k_codes == nullptr) == (k_meta == nullptr), IQ_ERR_NULL);
+  if (k_codes) {
+    IQ_CHECK(t_cap % TOKEN_BLOCK == 0 && t_off >= 0, IQ_ERR_ALIGN);
+    IQ_CHECK(t_off + n <= t_cap, IQ_ERR_RANGE);
+    IQ_CHECK(aligned(k_codes, 4) && aligned(k_meta, 4), IQ_ERR_ALIGN);
+  }
+  IQ_CHECK(!(mode == IQ_MODE_SYM && zero16), IQ_ERR_MODE);
+  IQ_CHECK(!(mode == IQ_MODE_ASYM && signs16), IQ_ERR_MODE);
+  const int64_t total = int64_t(B) * H * n * (D / group);
+  if (total == 0) return IQ_OK;
+  QuantOut o{k_codes, k_meta, t_cap / TOKEN_BLOCK, t_off, codes_i32, (uint16_t*)scale16, (uint16_t*)zero16,
+             (uint16_t*)signs16};
+  const int sym = mode == IQ_MODE_SYM;
+  return dispatch_bits_group(bits, group, [&]<int BITS, int G>() {
+    quant_k_kernel<BITS, G><<<dim3(unsigned(ceil_div(total, 256))), 256, 0, (hipStream_t)stream>>>(
+        (const uint16_t*)x, sx_b, sx_h, sx_t, (const uint16_t*)norm, B, H, n, D, sym, o);
+    return launch_status();
+  });
+}
+
+int iq_quantize_v(const void* x, int64_t sx_b, int64_t sx_h, int64_t sx_t, int B, int H, int n, int D,
+                  int group, int bits, int mode, uint32_t* v_codes, uint16_t* v_meta, int64_t t_cap,
+                  int64_t t_off, int32_t* codes_i32, void* scale16, void* zero16, void* signs16, void* stream) {
+  IQ_CHECK(x, IQ_ERR_NULL);
+  if (int e = check_common(bits, group, mode)) return e;
+  IQ_CHECK(B >= 0 && H >= 0 && n >= 0 && D > 0, IQ_ERR_SHAPE);
+  IQ_CHECK(n % group == 0, IQ_ERR_GROUP);
+  IQ_CHECK(aligned(x, 2), IQ_ERR_ALIGN);
+  IQ_CHECK((v_codes == nullptr) == (v_meta == nullptr), IQ_ERR_NULL);
+  if (v_codes) {
+    IQ_CHECK(t_cap % group == 0 && t_off % group == 0 && t_off >= 0, IQ_ERR_ALIGN);
+    IQ_CHECK(t_off + n <= t_cap, IQ_ERR_RANGE);
+    IQ_CHECK(aligned(v_codes, 4) && aligned(v_meta, 4), IQ_ERR_ALIGN);
+  }
+  IQ_CHECK(!(mode == IQ_MODE_SYM && zero16), IQ_ERR_MODE);
+  IQ_CHECK(!(mode == IQ_MODE_ASYM && signs16), IQ_ERR_MODE);
+  const int64_t total = int64_t(B) * H * (n / group) * D;
+  if (total == 0) return IQ_OK;
+  QuantOut o{v_codes, v_meta, t_cap / group, t_off, codes_i32, (uint16_t*)scale16, (uint16_t*)zero16,
+             (uint16_t*)signs16};
+  const int sym = mode == IQ_MODE_SYM;
+  return dispatch_bits_group(bits, group, [&]<int BITS, int G>() {
+    quant_v_kernel<BITS, G><<<dim3(unsigned(ceil_div(total, 256))), 256, 0, (hipStream_t)stream>>>(
+        (const uint16_t*)x, sx_b, sx_h, sx_t, B, H, n, D, sym, o);
+    return launch_status();
+  });
+}
+
+int iq_dequant_k(const uint32_t* k_codes, const uint16_t* k_meta, int64_t t_cap, const void* norm, int B, int H,
+                 int t0, int T, int D, int group, int bits, int mode, void* out16, float* out32, int64_t so_b,
+                 int64_t so_h, int64_t so_t, void* stream) {
+  IQ_CHECK(k_codes && k_meta, IQ_ERR_NULL);
+  IQ_CHECK(out16 || out32, IQ_ERR_NULL);
+  if (int e = check_common(bits, group, mode)) return e;
+  IQ_CHECK(B >= 0 && H >= 0 && T >= 0 && t0 >= 0 && D > 0, IQ_ERR_SHAPE);
+  IQ_CHECK(D % group == 0, IQ_ERR_GROUP);
+  IQ_CHECK(t_cap % TOKEN_BLOCK == 0, IQ_ERR_ALIGN);
+  IQ_CHECK(int64_t(t0) + T <= t_cap, IQ_ERR_RANGE);
+  const int64_t total = int64_t(B) * H * T * (D / group);
+  if (total == 0) return IQ_OK;
+  DeqOut o{(uint16_t*)out16, out32, so_b, so_h, so_t};
+  const int sym = mode == IQ_MODE_SYM;
+  return dispatch_bits_group(bits, group, [&]<int BITS, int G>() {
+    dequant_k_kernel<BITS, G><<<dim3(unsigned(ceil_div(total, 256))), 256, 0, (hipStream_t)stream>>>(
+        k_codes, k_meta, t_cap / TOKEN_BLOCK, (const uint16_t*)norm, B, H, t0, T, D, sym, o);
+    return launch_status();
+  });
+}
+
+int iq_dequant_v(const uint32_t* v_codes, const uint16_t* v_meta, int64_t t_cap, int B, int H, int t0, int T,
+                 int D, int group, int bits, int mode, void* out16, float* out32, int64_t so_b, int64_t so_h,
+                 int64_t so_t, void* stream) {
+  IQ_CHECK(v_codes && v_meta, IQ_ERR_NULL);
+  IQ_CHECK(out16 || out32, IQ_ERR_NULL);
+  if (int e = check_common(bits, group, mode)) return e;
+  IQ_CHECK(B >= 0 && H >= 0 && T >= 0 && t0 >= 0 && D > 0, IQ_ERR_SHAPE);
+  IQ_CHECK(T % group == 0 && t0 % group == 0 && t_cap % group == 0, IQ_ERR_GROUP);
+  IQ_CHECK(int64_t(t0) + T <= t_cap, IQ_ERR_RANGE);
+  const int64_t total = int64_t(B) * H * (T / group) * D;
+  if (total == 0) return IQ_OK;
+  DeqOut o{(uint16_t*)out16, out32, so_b, so_h, so_t};
+  const int sym = mode == IQ_MODE_SYM;
+  return dispatch_bits_group(bits, group, [&]<int BITS, int G>() {
+    dequant_v_kernel<BITS, G><<<dim3(unsigned(ceil_div(total, 256))), 256, 0, (hipStream_t)stream>>>(
+        v_codes, v_meta, t_cap / G, B, H, t0 / G, T / G, D, sym, o);
+    return launch_status();
+  });
+}
+
+int iq_dequant_dense(const int32_t* codes, const void* scale16, const void* zs16, int64_t outer, int64_t n,
+                     int64_t inner, int group, int mode, int out_f16, void* out, void* stream) {
+  IQ_CHECK(codes && scale16 && zs16 && out, IQ_ERR_NULL);
+  IQ_CHECK(mode_ok(mode), IQ_ERR_MODE);
+  IQ_CHECK(outer >= 0 && n >= 0 && inner >= 0 && (out_f16 == 0 || out_f16 == 1), IQ_ERR_SHAPE);
+  IQ_CHECK(group > 0 && n % group == 0, IQ_ERR_GROUP);
+  const int64_t total = outer * n * inner;
+  if (total == 0) return IQ_OK;
+  dequant_dense_kernel<<<dim3(unsigned(ceil_div(total, 256))), 256, 0, (hipStream_t)stream>>>(
+      codes, (const uint16_t*)scale16, (const uint16_t*)zs16, outer, n, inner, group, mode == IQ_MODE_SYM, out_f16,
+      out);
+  return launch_status();
+}
+
+}  // extern "C"

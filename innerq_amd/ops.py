@@ -1,0 +1,303 @@
+"""torch-facing wrappers of the C ABI (device memory and streams only).
+
+Every function here checks that its tensors live on a HIP device and calls one
+entry point of libinnerq_hip.so on the current torch stream.  There is no CPU
+path: a CPU tensor or a missing library raises.
+"""
+from __future__ import annotations
+
+import ctypes
+from typing import Optional, Sequence
+
+import torch
+
+from . import _lib
+from ._lib import IQ_MODE_ASYM, IQ_MODE_SYM, TOKEN_BLOCK, call
+
+MODES = {"asymmetric": IQ_MODE_ASYM, "symmetric": IQ_MODE_SYM}
+
+
+def _p(t: Optional[torch.Tensor]):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(device: torch.device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+def require_device(t: torch.Tensor, name: str, dtype=torch.float16) -> None:
+    if not isinstance(t, torch.Tensor) or not t.is_cuda:
+        raise TypeError(f"{name} must be a HIP device tensor (innerq_amd has no CPU path)")
+    if dtype is not None and t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+
+
+def mode_id(mode) -> int:
+    if isinstance(mode, int):
+        return mode
+    m = getattr(mode, "value", mode)
+    if m not in MODES:
+        raise ValueError(f"packed kernels support 'asymmetric' and 'symmetric', not {m!r}")
+    return MODES[m]
+
+
+class PackedStore:
+    """Packed codes + fp16 metadata of one quantized K or V segment.
+
+    axis='channel': groups along head_dim, K-store layout (what QK^T reads);
+    axis='token':   groups along tokens, V-store layout (what attn.V reads).
+    Capacity grows geometrically; ``length`` tokens are valid.
+    """
+
+    def __init__(self, axis: str, B: int, H: int, D: int, group: int, bits: int, mode, device,
+                 t_cap: int = 0):
+        if axis not in ("channel", "token"):
+            raise ValueError(axis)
+        self.axis, self.B, self.H, self.D = axis, B, H, D
+        self.group, self.bits, self.mode = group, bits, mode_id(mode)
+        self.device = torch.device(device)
+        self.length = 0
+        self.t_cap = 0
+        self.codes = torch.empty(0, dtype=torch.int32, device=self.device)
+        self.meta = torch.empty(0, dtype=torch.int16, device=self.device)
+        self.reserve(t_cap)
+
+    @property
+    def unit(self) -> int:
+        return TOKEN_BLOCK if self.axis == "channel" else self.group
+
+    def _bytes(self, t_cap: int):
+        cb, mb = ctypes.c_int64(), ctypes.c_int64()
+        fn = "iq_k_store_bytes" if self.axis == "channel" else "iq_v_store_bytes"
+        call(fn, self.B, self.H, t_cap, self.D, self.group, self.bits, self.mode, ctypes.byref(cb), ctypes.byref(mb))
+        return cb.value, mb.value
+
+    def reserve(self, n_tokens: int) -> None:
+        """Ensure capacity for ``n_tokens`` tokens (amortized doubling; old data is kept)."""
+        u = self.unit
+        need = -(-max(n_tokens, 0) // u) * u
+        if need <= self.t_cap:
+            return
+        new_cap = max(need, 2 * self.t_cap, 4 * u)
+        new_cap = -(-new_cap // u) * u
+        cb, mb = self._bytes(new_cap)
+        codes = torch.empty(cb // 4, dtype=torch.int32, device=self.device)
+        meta = torch.empty(mb // 2, dtype=torch.int16, device=self.device)
+        if self.t_cap:
+            ou, nu = self.t_cap // u, new_cap // u
+            codes.view(self.B * self.H, nu, -1)[:, :ou].copy_(self.codes.view(self.B * self.H, ou, -1))
+            meta.view(self.B * self.H, nu, -1)[:, :ou].copy_(self.meta.view(self.B * self.H, ou, -1))
+        self.codes, self.meta, self.t_cap = codes, meta, new_cap
+
+    def nbytes(self, n_tokens: Optional[int] = None) -> int:
+        """Packed code + metadata bytes of ``n_tokens`` (default: length) tokens."""
+        n = self.length if n_tokens is None else n_tokens
+        m = 2 if self.mode == IQ_MODE_SYM else 4
+        groups = n * (self.D // self.group) if self.axis == "channel" else (n // self.group) * self.D
+        return self.B * self.H * (n * self.D * self.bits // 8 + groups * m)
+
+    # --- writes -------------------------------------------------------------
+    def append(self, x: torch.Tensor, norm: Optional[torch.Tensor] = None) -> None:
+        """Quantize x [B,H,n,D] fp16 and append it (quantize-on-append)."""
+        require_device(x, "x")
+        B, H, n, D = x.shape
+        assert (B, H, D) == (self.B, self.H, self.D), "store shape mismatch"
+        if n == 0:
+            return
+        self.reserve(self.length + n)
+        if self.axis == "channel":
+            if x.stride(-1) != 1 or x.data_ptr() % 16 or any(s % 8 for s in x.stride()[:3]):
+                x = x.contiguous()
+            if norm is not None:
+                require_device(norm, "norm")
+                norm = norm.reshape(B, H, D).contiguous()
+            call("iq_quantize_k", _p(x), x.stride(0), x.stride(1), x.stride(2), _p(norm), B, H, n, D, self.group,
+                 self.bits, self.mode, _p(self.codes), _p(self.meta), self.t_cap, self.length, None, None, None, None,
+                 _stream(x.device))
+        else:
+            if x.stride(-1) != 1:
+                x = x.contiguous()
+            call("iq_quantize_v", _p(x), x.stride(0), x.stride(1), x.stride(2), B, H, n, D, self.group, self.bits,
+                 self.mode, _p(self.codes), _p(self.meta), self.t_cap, self.length, None, None, None, None,
+                 _stream(x.device))
+        self.length += n
+
+    # --- reads --------------------------------------------------------------
+    def dequant(self, t0: int = 0, T: Optional[int] = None, out: Optional[torch.Tensor] = None,
+                norm: Optional[torch.Tensor] = None, dtype=torch.float16) -> torch.Tensor:
+        """Dense [B,H,T,D] values of tokens [t0, t0+T) (fp16 or fp32); ``out`` may be a strided view."""
+        T = self.length - t0 if T is None else T
+        if out is None:
+            out = torch.empty(self.B, self.H, T, self.D, dtype=dtype, device=self.device)
+        assert out.shape == (self.B, self.H, T, self.D) and out.stride(-1) == 1
+        o16 = _p(out) if out.dtype == torch.float16 else None
+        o32 = _p(out) if out.dtype == torch.float32 else None
+        if o16 is None and o32 is None:
+            raise TypeError("dequant output must be fp16 or fp32")
+        st = out.stride()
+        if self.axis == "channel":
+            if norm is not None:
+                norm = norm.reshape(self.B, self.H, self.D).contiguous()
+            call("iq_dequant_k", _p(self.codes), _p(self.meta), self.t_cap, _p(norm), self.B, self.H, t0, T, self.D,
+                 self.group, self.bits, self.mode, o16, o32, st[0], st[1], st[2], _stream(out.device))
+        else:
+            assert norm is None
+            call("iq_dequant_v", _p(self.codes), _p(self.meta), self.t_cap, self.B, self.H, t0, T, self.D,
+                 self.group, self.bits, self.mode, o16, o32, st[0], st[1], st[2], _stream(out.device))
+        return out
+
+
+def quantize_dense(x: torch.Tensor, group: int, bits: int, mode, axis: str):
+    """Reference-format quantization of a [rows, n, inner]-viewable fp16 tensor.
+
+    Returns (codes int32 like x, scale fp16, zero fp16 | signs fp16) exactly as
+    quant.py's quantize_{channeldim,tokendim}_{asym,sym}.
+    """
+    require_device(x, "tensor")
+    m = mode_id(mode)
+    shape = tuple(x.shape)
+    x = x.contiguous()
+    dev = x.device
+    codes = torch.empty(shape, dtype=torch.int32, device=dev)
+    if axis == "channel":
+        n = shape[-1]
+        rows = x.numel() // max(n, 1)
+        red = shape[:-1] + (n // group,)
+        scale = torch.empty(red, dtype=torch.float16, device=dev)
+        zs = torch.empty(red if m == IQ_MODE_ASYM else shape, dtype=torch.float16, device=dev)
+        call("iq_quantize_k", _p(x), 0, 0, n, None, 1, 1, rows, n, group, bits, m, None, None, 0, 0,
+             _p(codes), _p(scale), _p(zs) if m == IQ_MODE_ASYM else None, _p(zs) if m == IQ_MODE_SYM else None,
+             _stream(dev))
+    else:
+        n, inner = shape[-2], shape[-1]
+        outer = x.numel() // max(n * inner, 1)
+        red = shape[:-2] + (n // group, inner)
+        scale = torch.empty(red, dtype=torch.float16, device=dev)
+        zs = torch.empty(red if m == IQ_MODE_ASYM else shape, dtype=torch.float16, device=dev)
+        call("iq_quantize_v", _p(x), 0, n * inner, inner, 1, outer, n, inner, group, bits, m, None, None, 0, 0,
+             _p(codes), _p(scale), _p(zs) if m == IQ_MODE_ASYM else None, _p(zs) if m == IQ_MODE_SYM else None,
+             _stream(dev))
+    return codes, scale, zs
+
+
+def dequantize_dense(codes: torch.Tensor, scale: torch.Tensor, zs: torch.Tensor, group: int, mode, axis: str,
+                     dtype=torch.float32) -> torch.Tensor:
+    require_device(codes, "tensor", torch.int32)
+    require_device(scale, "scale")
+    require_device(zs, "zero_points/signs")
+    shape = tuple(codes.shape)
+    if axis == "channel":
+        outer, n, inner = codes.numel() // max(shape[-1], 1), shape[-1], 1
+    else:
+        n, inner = shape[-2], shape[-1]
+        outer = codes.numel() // max(n * inner, 1)
+    out = torch.empty(shape, dtype=dtype, device=codes.device)
+    if dtype not in (torch.float32, torch.float16):
+        raise TypeError("op_dtype must be torch.float32 or torch.float16")
+    call("iq_dequant_dense", _p(codes.contiguous()), _p(scale.contiguous()), _p(zs.contiguous()), outer, n, inner,
+         group, mode_id(mode), 1 if dtype == torch.float16 else 0, _p(out), _stream(codes.device))
+    return out
+
+
+_WS = {}
+
+
+def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    key = (device.index, torch.cuda.current_stream(device).cuda_stream)
+    ws = _WS.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(max(nbytes, 256), dtype=torch.uint8, device=device)
+        _WS[key] = ws
+    return ws
+
+
+def qk_gemv(q: torch.Tensor, k: PackedStore, scale: float, norm: Optional[torch.Tensor] = None, t0: int = 0,
+            T: Optional[int] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """logits [B,Hq,T] fp32 = scale * q . K[t0:t0+T] over a channel-grouped store."""
+    require_device(q, "q")
+    assert k.axis == "channel"
+    B, Hq, D = q.shape
+    T = k.length - t0 if T is None else T
+    if q.stride(-1) != 1:
+        q = q.contiguous()
+    if out is None:
+        out = torch.empty(B, Hq, T, dtype=torch.float32, device=q.device)
+    assert out.stride(-1) == 1 and out.dtype == torch.float32
+    if norm is not None:
+        norm = norm.reshape(k.B, k.H, D).contiguous()
+    call("iq_qk_gemv", _p(q), q.stride(0), q.stride(1), _p(norm), _p(k.codes), _p(k.meta), k.t_cap, B, Hq, k.H, t0,
+         T, D, k.group, k.bits, k.mode, float(scale), _p(out), out.stride(0), out.stride(1), _stream(q.device))
+    return out
+
+
+def av_gemv(p: torch.Tensor, v: PackedStore, t0: int = 0, T: Optional[int] = None,
+            out: Optional[torch.Tensor] = None, out32: Optional[torch.Tensor] = None,
+            accumulate: bool = False) -> torch.Tensor:
+    """out [B,Hq,D] = p . V[t0:t0+T] over a token-grouped store (fp16 and/or fp32 outputs)."""
+    require_device(p, "p")
+    assert v.axis == "token"
+    B, Hq, Tp = p.shape
+    T = v.length - t0 if T is None else T
+    if p.stride(-1) != 1:
+        p = p.contiguous()
+    if out is None and out32 is None:
+        out = torch.empty(B, Hq, v.D, dtype=torch.float16, device=p.device)
+    ref = out if out is not None else out32
+    if out is not None and out32 is not None:
+        assert out.stride() == out32.stride()
+    nbytes = _lib.lib().iq_av_workspace_bytes(B, Hq, T, v.D, v.group)
+    ws = _workspace(p.device, nbytes)
+    call("iq_av_gemv", _p(p), p.stride(0), p.stride(1), _p(v.codes), _p(v.meta), v.t_cap, B, Hq, v.H, t0, T, v.D,
+         v.group, v.bits, v.mode, _p(out32), _p(out), ref.stride(0), ref.stride(1), 1 if accumulate else 0, _p(ws),
+         ws.numel(), _stream(p.device))
+    return out if out is not None else out32
+
+
+def _segment(dense: Optional[torch.Tensor], store: Optional[PackedStore], n: int, t0: int = 0):
+    s = _lib.iq_segment()
+    s.n = n
+    if n == 0:
+        return s
+    if store is not None:
+        s.codes, s.meta, s.t_cap, s.t0 = store.codes.data_ptr(), store.meta.data_ptr(), store.t_cap, t0
+        s.bits, s.group, s.mode = store.bits, store.group, store.mode
+    else:
+        require_device(dense, "segment")
+        assert dense.stride(-1) == 1
+        s.dense = dense.data_ptr()
+        s.s_b, s.s_h, s.s_t = dense.stride(0), dense.stride(1), dense.stride(2)
+    return s
+
+
+def decode_attention(q: torch.Tensor, k_sink: Optional[torch.Tensor], k_store: Optional[PackedStore],
+                     k_recent: Optional[torch.Tensor], v_sink: Optional[torch.Tensor],
+                     v_store: Optional[PackedStore], v_recent: Optional[torch.Tensor], scale: float,
+                     norm: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """One decode step of attention for q [B,Hq,D] over [sink | packed | recent] K and V."""
+    require_device(q, "q")
+    B, Hq, D = q.shape
+    if q.stride(-1) != 1:
+        q = q.contiguous()
+
+    def n_of(t):
+        return 0 if t is None else t.shape[2]
+
+    kn = [n_of(k_sink), k_store.length if k_store is not None else 0, n_of(k_recent)]
+    vn = [n_of(v_sink), v_store.length if v_store is not None else 0, n_of(v_recent)]
+    T = sum(kn)
+    if sum(vn) != T:
+        raise ValueError(f"K has {T} tokens but V has {sum(vn)}")
+    Hkv = (k_store.H if k_store is not None else (k_sink if k_sink is not None else k_recent).shape[1])
+    ks = (_lib.iq_segment * 3)(_segment(k_sink, None, kn[0]), _segment(None, k_store, kn[1]),
+                               _segment(k_recent, None, kn[2]))
+    vs = (_lib.iq_segment * 3)(_segment(v_sink, None, vn[0]), _segment(None, v_store, vn[1]),
+                               _segment(v_recent, None, vn[2]))
+    if out is None:
+        out = torch.empty(B, Hq, D, dtype=torch.float16, device=q.device)
+    if norm is not None:
+        norm = norm.reshape(B, Hkv, D).contiguous()
+    nbytes = _lib.lib().iq_decode_workspace_bytes(B, Hq, T, D)
+    ws = _workspace(q.device, nbytes)
+    call("iq_decode_attention", _p(q), q.stride(0), q.stride(1), _p(norm), ks, vs, B, Hq, Hkv, T, D, float(scale),
+         _p(out), out.stride(0), out.stride(1), _p(ws), ws.numel(), _stream(q.device))
+    return out

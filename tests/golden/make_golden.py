@@ -1,0 +1,189 @@
+"""Write golden vectors from the live reference (run in the build container only).
+
+Imports mthcom/innerq's ``src/innerq/quant.py`` and ``src/innerq/cache.py`` by
+file path (``import innerq`` itself pulls in lm_eval, which is absent) and
+records small input/output vectors as ``.npz`` fixtures next to this script.
+The reference never travels: only these data files are committed, and the
+tests read them, never the reference.
+
+Fixtures
+--------
+quant_golden.npz    quantize_{channeldim,tokendim}_{asym,sym} outputs for
+                    bits 2/3/4, group 32/64 on a [1,2,64,128] fp16 input with
+                    outlier channels, constant groups and rounding ties; the
+                    hybrid quantizer for bits 3/4; config-0 SHA-256 digests.
+cache_golden.npz    InnerqDynamicLayer.update() traces: prefill + decode steps
+                    for several presets (inputs regenerated from the stored
+                    seed with innerq_amd.synth); full dense K/V of the last
+                    decode call, SHA-256 of every call's K/V bytes,
+                    and the recent-window lengths after every call.
+
+Usage:  python tests/golden/make_golden.py [/root/reference]
+"""
+from __future__ import annotations
+
+import hashlib
+import importlib.util
+import os
+import sys
+import types
+
+import numpy as np
+import torch
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.dirname(os.path.dirname(HERE)))
+from innerq_amd import synth  # noqa: E402
+
+
+def load_reference(root):
+    pkg_dir = os.path.join(root, "src", "innerq")
+    pkg = types.ModuleType("_innerq_reference")
+    pkg.__path__ = [pkg_dir]
+    sys.modules["_innerq_reference"] = pkg
+    mods = {}
+    for name in ("quant", "cache"):
+        spec = importlib.util.spec_from_file_location(f"_innerq_reference.{name}",
+                                                      os.path.join(pkg_dir, f"{name}.py"))
+        mod = importlib.util.module_from_spec(spec)
+        sys.modules[spec.name] = mod
+        spec.loader.exec_module(mod)
+        mods[name] = mod
+    return mods["quant"], mods["cache"]
+
+
+def f16(a):
+    return a.detach().cpu().numpy().astype(np.float16).view(np.uint16)
+
+
+def codes8(a):
+    c = a.detach().cpu().numpy().astype(np.int64)
+    assert np.all(((c > -128) & (c < 128)) | (c == -2147483648)), "unexpected code"
+    c = np.where(c == -2147483648, -128, c)   # INT32_MIN sentinel
+    return c.astype(np.int8)
+
+
+def digest(arr):
+    return np.frombuffer(hashlib.sha256(np.ascontiguousarray(arr).tobytes()).digest(), dtype=np.uint8)
+
+
+def quant_input():
+    x = synth.kv_tensor(1, 2, 64, 128, seed=1234, n_out=4, factor=10.0).astype(np.float32)
+    # constant groups (channel-dim group 0 of token 5; token-dim group of channel 7)
+    x[0, 0, 5, 0:32] = 0.75
+    x[0, 1, 0:32, 7] = -1.5
+    # exact ties: ramp with known halves
+    x[0, 0, 9, 32:64] = np.arange(32) % 4 - 2.0
+    x[0, 1, 11, 64:96] = (np.arange(32) % 16) * 0.5
+    return x.astype(np.float16)
+
+
+def main(root):
+    quant, cache = load_reference(root)
+    out = {}
+    x = quant_input()
+    out["x"] = x.view(np.uint16)
+    xt = torch.from_numpy(x)
+    for axis, fa, fs in (("channel", quant.quantize_channeldim_asym, quant.quantize_channeldim_sym),
+                         ("token", quant.quantize_tokendim_asym, quant.quantize_tokendim_sym)):
+        for bits in (2, 3, 4):
+            for G in (32, 64):
+                c, s, z = fa(xt.clone(), G, bits)
+                key = f"{axis}_asym_b{bits}_g{G}"
+                out[key + "_codes"] = codes8(c)
+                out[key + "_scale"] = f16(s)
+                out[key + "_zero"] = f16(z)
+                c, s, sg = fs(xt.clone(), G, bits)
+                key = f"{axis}_sym_b{bits}_g{G}"
+                out[key + "_codes"] = codes8(c)
+                out[key + "_scale"] = f16(s)
+                out[key + "_signs"] = f16(sg)
+                # dequantize outputs (fp32) for the asym/sym functions
+    for axis in ("channel", "token"):
+        qa = getattr(quant, f"quantize_{axis}dim_asym")
+        qs = getattr(quant, f"quantize_{axis}dim_sym")
+        da = getattr(quant, f"dequantize_{axis}dim_asym")
+        ds = getattr(quant, f"dequantize_{axis}dim_sym")
+        hq = quant.quantize_hybrid(qa, qs, da, ds)
+        hd = quant.dequantize_hybrid(da, ds)
+        for bits in (3, 4):
+            c, s, z = hq(xt.clone(), 32, bits)
+            key = f"{axis}_hybrid_b{bits}_g32"
+            out[key + "_mask"] = s["mask"].cpu().numpy()
+            out[key + "_deq_sha256"] = digest(hd(c, s, z, 32).cpu().numpy().astype(np.float32))
+        c, s, z = qa(xt.clone(), 32, 4)
+        out[f"{axis}_asym_b4_g32_deq_sha256"] = digest(da(c, s, z, 32).cpu().numpy().astype(np.float32))
+        c, s, z = qs(xt.clone(), 32, 3)
+        out[f"{axis}_sym_b3_g32_deq_sha256"] = digest(ds(c, s, z, 32).cpu().numpy().astype(np.float32))
+
+    # config 0: K,V fp16 [1,8,4096,128], 4 outlier channels/head x10, 4-bit asym G=32
+    k0 = torch.from_numpy(synth.kv_tensor(1, 8, 4096, 128, seed=0, n_out=4, factor=10.0))
+    v0 = torch.from_numpy(synth.kv_tensor(1, 8, 4096, 128, seed=1, n_out=4, factor=10.0))
+    for name, t, fn in (("k", k0, quant.quantize_channeldim_asym), ("v", v0, quant.quantize_tokendim_asym)):
+        c, s, z = fn(t.clone(), 32, 4)
+        for part, arr in (("codes", c.numpy().astype(np.int32)), ("scale", f16(s)), ("zero", f16(z))):
+            out[f"cfg0_{name}_{part}_sha256"] = digest(arr)
+    np.savez_compressed(os.path.join(HERE, "quant_golden.npz"), **out)
+
+    # ---------------- cache traces ----------------
+    class Layer(cache.InnerqDynamicLayer):
+        def get_max_length(self):   # abstract in the installed transformers
+            return -1
+
+    class Cfg:
+        pass
+
+    presets = {
+        "innerq_base": dict(k_bits=3, v_bits=3, key_flush_size=1, value_flush_size=32, key_group_size=32,
+                            value_group_size=32, key_w_recent=96, value_w_recent=96, key_w_sink=32,
+                            value_w_sink=32, key_normalize=True, key_quantize_over_token=False,
+                            value_quantize_over_token=True, key_quantize_mode="symmetric",
+                            value_quantize_mode="symmetric"),
+        "asym4_nosink": dict(k_bits=4, v_bits=4, key_flush_size=1, value_flush_size=32, key_group_size=32,
+                             value_group_size=32, key_w_recent=32, value_w_recent=64, key_w_sink=0,
+                             value_w_sink=0, key_normalize=False, key_quantize_over_token=False,
+                             value_quantize_over_token=True, key_quantize_mode="asymmetric",
+                             value_quantize_mode="asymmetric"),
+        "mixed_k2v4_flush32": dict(k_bits=2, v_bits=4, key_flush_size=32, value_flush_size=64,
+                                   key_group_size=32, value_group_size=32, key_w_recent=40, value_w_recent=70,
+                                   key_w_sink=4, value_w_sink=0, key_normalize=False,
+                                   key_quantize_over_token=False, value_quantize_over_token=True,
+                                   key_quantize_mode="asymmetric", value_quantize_mode="symmetric"),
+        "hybrid_v": dict(k_bits=3, v_bits=2, key_flush_size=1, value_flush_size=32, key_group_size=32,
+                         value_group_size=32, key_w_recent=96, value_w_recent=96, key_w_sink=32,
+                         value_w_sink=32, key_normalize=True, key_quantize_over_token=False,
+                         value_quantize_over_token=True, key_quantize_mode="symmetric",
+                         value_quantize_mode="hybrid"),
+        "k_only": dict(k_bits=4, v_bits=16, key_flush_size=1, key_group_size=64, key_w_recent=16,
+                       key_w_sink=2, key_normalize=False, key_quantize_mode="asymmetric"),
+    }
+    trace = {}
+    B, H, D = 1, 2, 64
+    prefill, steps = 150, 70
+    for name, kw in presets.items():
+        cfg = Cfg()
+        for k, v in kw.items():
+            setattr(cfg, k, v)
+        layer = Layer(cfg, 0)
+        seed = sum(map(ord, name))
+        kx = synth.kv_tensor(B, H, prefill + steps, D, seed=seed, n_out=2, factor=8.0)
+        vx = synth.kv_tensor(B, H, prefill + steps, D, seed=seed + 1, n_out=2, factor=8.0)
+        trace[f"{name}_seed"] = np.array([seed, B, H, D, prefill, steps])
+        kt, vt = torch.from_numpy(kx), torch.from_numpy(vx)
+        K, V = layer.update(kt[:, :, :prefill].clone(), vt[:, :, :prefill].clone())
+        trace[f"{name}_step0_sha256"] = digest(np.concatenate([f16(K).ravel(), f16(V).ravel()]))
+        for s in range(steps):
+            K, V = layer.update(kt[:, :, prefill + s:prefill + s + 1].clone(),
+                                vt[:, :, prefill + s:prefill + s + 1].clone())
+            if s == steps - 1:
+                trace[f"{name}_step{s + 1}_k"] = f16(K)
+                trace[f"{name}_step{s + 1}_v"] = f16(V)
+            trace[f"{name}_step{s + 1}_sha256"] = digest(np.concatenate([f16(K).ravel(), f16(V).ravel()]))
+            trace[f"{name}_len{s + 1}"] = np.array([K.shape[-2], V.shape[-2],
+                                                    layer.keys_recent.shape[-2], layer.values_recent.shape[-2]])
+    np.savez_compressed(os.path.join(HERE, "cache_golden.npz"), **trace)
+    print("wrote", os.path.join(HERE, "quant_golden.npz"), os.path.join(HERE, "cache_golden.npz"))
+
+
+if __name__ == "__main__":
+    main(sys.argv[1] if len(sys.argv) > 1 else "/root/reference")

@@ -1,0 +1,172 @@
+"""C-ABI checks that run without a GPU: the library loads, exports every
+function include/innerq_abi.h declares, and rejects bad arguments on the host
+before any launch (each case below has exactly one invalid argument, so no
+call here ever reaches a kernel launch)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from innerq_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "innerq_abi.h")
+FAKE = ctypes.c_void_p(0x1000)  # never dereferenced: validation fails first
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(iq_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.lib()
+    names = declared_functions()
+    assert "iq_qk_gemv" in names and "iq_av_gemv" in names and "iq_quantize_k" in names
+    for n in names:
+        assert hasattr(lib, n), n
+    assert set(names) <= set(_lib.SIGNATURES), set(names) - set(_lib.SIGNATURES)
+
+
+def test_version_and_strerror():
+    lib = _lib.lib()
+    assert lib.iq_abi_version() == 1
+    assert lib.iq_strerror(0) == b"ok"
+    assert b"bits" in lib.iq_strerror(-2)
+    assert lib.iq_strerror(12345) == b"unknown status"
+
+
+def _store_bytes(fn, *args):
+    cb, mb = ctypes.c_int64(), ctypes.c_int64()
+    st = getattr(_lib.lib(), fn)(*args, ctypes.byref(cb), ctypes.byref(mb))
+    return st, cb.value, mb.value
+
+
+def test_store_sizes():
+    st, cb, mb = _store_bytes("iq_k_store_bytes", 8, 8, 32768, 128, 32, 4, 0)
+    assert st == 0 and cb == 8 * 8 * 32768 * 64 and mb == 8 * 8 * 32768 * 4 * 4
+    st, cb, mb = _store_bytes("iq_v_store_bytes", 8, 8, 32768, 128, 64, 2, 1)
+    assert st == 0 and cb == 8 * 8 * 32768 * 32 and mb == 8 * 8 * 512 * 128 * 2
+    assert _store_bytes("iq_k_store_bytes", 1, 1, 100, 128, 32, 4, 0)[0] == -5   # t_cap % 64
+    assert _store_bytes("iq_k_store_bytes", 1, 1, 64, 128, 32, 5, 0)[0] == -2    # bits
+    assert _store_bytes("iq_k_store_bytes", 1, 1, 64, 96, 64, 4, 0)[0] == -3     # D % G
+    assert _store_bytes("iq_v_store_bytes", 1, 1, 48, 128, 32, 4, 0)[0] == -3    # t_cap % G
+    assert _store_bytes("iq_v_store_bytes", 1, 1, 64, 128, 32, 4, 2)[0] == -7    # mode
+
+
+def qk_args(**kw):
+    a = dict(q=FAKE, sqb=1024, sqh=128, norm=None, kc=FAKE, km=FAKE, t_cap=1024, B=1, Hq=32, Hkv=8, t0=0,
+             T=512, D=128, G=32, bits=4, mode=0, scale=1.0, out=FAKE, sob=1, soh=1, stream=None)
+    a.update(kw)
+    return list(a.values())
+
+
+@pytest.mark.parametrize("kw,err", [
+    (dict(q=None), -1), (dict(kc=None), -1), (dict(out=None), -1),
+    (dict(bits=5), -2), (dict(bits=1), -2), (dict(G=48), -3), (dict(G=256), -3),
+    (dict(mode=3), -7), (dict(D=96), -4), (dict(Hkv=5), -4), (dict(Hq=48), -4),
+    (dict(T=-1), -4), (dict(t0=32), -5), (dict(t_cap=1000), -5), (dict(T=1100), -8),
+    (dict(kc=ctypes.c_void_p(0x1004)), -5),
+])
+def test_qk_rejects(kw, err):
+    assert _lib.lib().iq_qk_gemv(*qk_args(**kw)) == err
+
+
+def av_args(**kw):
+    a = dict(p=FAKE, spb=1, sph=1, vc=FAKE, vm=FAKE, t_cap=1024, B=1, Hq=32, Hkv=8, t0=0, T=512, D=128, G=32,
+             bits=4, mode=0, out32=FAKE, out16=None, sob=1, soh=1, acc=0, ws=None, wsb=0, stream=None)
+    a.update(kw)
+    return list(a.values())
+
+
+@pytest.mark.parametrize("kw,err", [
+    (dict(p=None), -1), (dict(vm=None), -1), (dict(out32=None), -1), (dict(out32=None, acc=1, out16=FAKE), -1),
+    (dict(bits=0), -2), (dict(G=16), -3), (dict(T=500), -3), (dict(t0=16), -3), (dict(mode=-1), -7),
+    (dict(D=256), -4), (dict(Hq=12), -4), (dict(T=2048), -8), (dict(vc=ctypes.c_void_p(0x1008)), -5),
+    (dict(ws=None, wsb=0), -6), (dict(ws=FAKE, wsb=16), -6),
+])
+def test_av_rejects(kw, err):
+    assert _lib.lib().iq_av_gemv(*av_args(**kw)) == err
+
+
+def test_workspace_queries():
+    lib = _lib.lib()
+    n = lib.iq_av_workspace_bytes(8, 32, 32768, 128, 32)
+    assert n > 0 and n % (8 * 32 * 128 * 4) == 0
+    assert lib.iq_av_workspace_bytes(8, 32, 32768, 96, 32) == 0
+    assert lib.iq_decode_workspace_bytes(8, 32, 32768, 128) >= 8 * 32 * 32768 * 6
+    assert lib.iq_decode_workspace_bytes(0, 32, 32768, 128) == 0
+
+
+def quant_k_args(**kw):
+    a = dict(x=FAKE, sxb=0, sxh=0, sxt=128, norm=None, B=1, H=1, n=4, D=128, G=32, bits=4, mode=0, kc=FAKE,
+             km=FAKE, t_cap=64, t_off=0, c32=None, s16=None, z16=None, sg16=None, stream=None)
+    a.update(kw)
+    return list(a.values())
+
+
+@pytest.mark.parametrize("kw,err", [
+    (dict(x=None), -1), (dict(kc=None), -1), (dict(bits=8), -2), (dict(G=64, D=96), -3), (dict(G=33), -3),
+    (dict(mode=2), -7), (dict(n=-1), -4), (dict(t_off=62), -8), (dict(t_cap=100), -5),
+    (dict(x=ctypes.c_void_p(0x1002)), -5), (dict(sxt=100), -5), (dict(mode=1, z16=FAKE), -7),
+    (dict(mode=0, sg16=FAKE), -7),
+])
+def test_quantize_k_rejects(kw, err):
+    assert _lib.lib().iq_quantize_k(*quant_k_args(**kw)) == err
+
+
+def quant_v_args(**kw):
+    a = dict(x=FAKE, sxb=0, sxh=0, sxt=128, B=1, H=1, n=64, D=128, G=32, bits=4, mode=0, vc=FAKE, vm=FAKE,
+             t_cap=64, t_off=0, c32=None, s16=None, z16=None, sg16=None, stream=None)
+    a.update(kw)
+    return list(a.values())
+
+
+@pytest.mark.parametrize("kw,err", [
+    (dict(x=None), -1), (dict(vm=None), -1), (dict(bits=1), -2), (dict(n=48), -3), (dict(t_off=32), -8),
+    (dict(t_off=16), -5), (dict(t_cap=48), -5), (dict(mode=7), -7),
+])
+def test_quantize_v_rejects(kw, err):
+    assert _lib.lib().iq_quantize_v(*quant_v_args(**kw)) == err
+
+
+def test_decode_rejects():
+    lib = _lib.lib()
+    seg = (_lib.iq_segment * 3)()
+    seg[0].n, seg[1].n, seg[2].n = 10, 0, 0
+    vseg = (_lib.iq_segment * 3)()
+    vseg[0].n = 10
+    # dense segments without pointers
+    assert lib.iq_decode_attention(FAKE, 1, 1, None, seg, vseg, 1, 32, 8, 10, 128, 1.0, FAKE, 1, 1, None, 0,
+                                   None) == -1
+    seg[0].dense = 0x1000
+    vseg[0].dense = 0x1000
+    # token counts disagree
+    assert lib.iq_decode_attention(FAKE, 1, 1, None, seg, vseg, 1, 32, 8, 11, 128, 1.0, FAKE, 1, 1, None, 0,
+                                   None) == -4
+    # no workspace
+    assert lib.iq_decode_attention(FAKE, 1, 1, None, seg, vseg, 1, 32, 8, 10, 128, 1.0, FAKE, 1, 1, None, 0,
+                                   None) == -6
+    # quantized K segment with bad bits
+    seg[1].n, seg[0].n = 5, 5
+    seg[1].codes, seg[1].meta, seg[1].t_cap, seg[1].bits, seg[1].group, seg[1].mode = 0x1000, 0x1000, 64, 7, 32, 0
+    assert lib.iq_decode_attention(FAKE, 1, 1, None, seg, vseg, 1, 32, 8, 10, 128, 1.0, FAKE, 1, 1, FAKE, 1 << 30,
+                                   None) == -2
+
+
+def test_dequant_rejects():
+    lib = _lib.lib()
+    assert lib.iq_dequant_k(FAKE, FAKE, 64, None, 1, 1, 0, 65, 128, 32, 4, 0, FAKE, None, 1, 1, 1, None) == -8
+    assert lib.iq_dequant_k(FAKE, FAKE, 64, None, 1, 1, 0, 64, 128, 32, 4, 0, None, None, 1, 1, 1, None) == -1
+    assert lib.iq_dequant_v(FAKE, FAKE, 64, 1, 1, 0, 40, 128, 32, 4, 0, FAKE, None, 1, 1, 1, None) == -3
+    assert lib.iq_dequant_dense(FAKE, FAKE, FAKE, 1, 40, 1, 32, 0, 0, FAKE, None) == -3
+    assert lib.iq_dequant_dense(FAKE, FAKE, FAKE, 1, 64, 1, 32, 0, 2, FAKE, None) == -4
+
+
+def test_cpu_tensor_raises_no_fallback():
+    import torch
+    from innerq_amd import ops
+    with pytest.raises(TypeError, match="no CPU path"):
+        ops.quantize_dense(torch.zeros(2, 64, dtype=torch.float16), 32, 4, "asymmetric", "channel")

@@ -1,0 +1,326 @@
+"""GPU parity of the HIP kernels (through the C ABI) against the CPU oracle.
+
+Bars: packed bytes, codes, scales and zero points bit-exact; dense dequantized
+values bit-exact (fp16, up to the sign of zero for sym); QK^T logits and
+attn.V outputs within 1e-3 of the float64 dequantize-then-matmul oracle in
+the max-relative metric  max|got-ref| / max|ref|.
+"""
+import numpy as np
+import pytest
+import torch
+
+from innerq_amd import ops, synth
+from oracle import attn_ref as A
+from oracle import quant_ref as Q
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+TOL = 1e-3
+MODES = ["asymmetric", "symmetric"]
+
+
+def f16t(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def oracle_q(x, bits, G, mode, axis):
+    fn = getattr(Q, f"quantize_{axis}dim_{'asym' if mode == 'asymmetric' else 'sym'}")
+    return fn(x, G, bits)
+
+
+def oracle_deq(c, s, z, G, mode, axis):
+    fn = getattr(Q, f"dequantize_{axis}dim_{'asym' if mode == 'asymmetric' else 'sym'}")
+    return fn(c, s, z, G)
+
+
+def special_input(B, H, T, D, seed):
+    x = synth.kv_tensor(B, H, T, D, seed=seed, n_out=3, factor=10.0).astype(np.float32)
+    x[0, 0, 3, :] = 0.5                          # constant channel-dim groups
+    x[0, 0, :32, 5] = -2.0                       # a constant token-dim group
+    x[0, H - 1, 7, :32] = np.arange(32) % 4 - 2  # ties
+    x[0, H - 1, 8, :] = 0.0
+    return x.astype(np.float16)
+
+
+# ----------------------------------------------------------------------------
+# quantize-on-append (A1, A2, A5)
+# ----------------------------------------------------------------------------
+@pytest.mark.parametrize("axis", ["channel", "token"])
+@pytest.mark.parametrize("mode", MODES)
+@pytest.mark.parametrize("bits", [2, 3, 4])
+@pytest.mark.parametrize("G", [32, 64, 128])
+def test_quantize_dense_bit_exact(axis, mode, bits, G):
+    x = special_input(2, 3, 128, 128, seed=bits * 10 + G)
+    c, s, z = ops.quantize_dense(f16t(x), G, bits, mode, axis)
+    rc, rs, rz = oracle_q(x, bits, G, mode, axis)
+    np.testing.assert_array_equal(c.cpu().numpy(), rc)
+    np.testing.assert_array_equal(s.cpu().numpy().view(np.uint16), rs.view(np.uint16))
+    np.testing.assert_array_equal(z.cpu().numpy().view(np.uint16), rz.view(np.uint16))
+
+
+def test_quantize_dense_matches_reference_golden(quant_golden):
+    g = quant_golden
+    x = g["x"].view(np.float16)
+    for axis in ("channel", "token"):
+        for mode, tag in (("asymmetric", "asym"), ("symmetric", "sym")):
+            for bits in (2, 3, 4):
+                for G in (32, 64):
+                    c, s, z = ops.quantize_dense(f16t(x), G, bits, mode, axis)
+                    key = f"{axis}_{tag}_b{bits}_g{G}"
+                    cc = c.cpu().numpy()
+                    cc = np.where(cc == -2147483648, -128, cc).astype(np.int8)
+                    np.testing.assert_array_equal(cc, g[key + "_codes"], err_msg=key)
+                    np.testing.assert_array_equal(s.cpu().numpy().view(np.uint16), g[key + "_scale"], err_msg=key)
+                    np.testing.assert_array_equal(z.cpu().numpy().view(np.uint16),
+                                                  g[key + ("_zero" if tag == "asym" else "_signs")], err_msg=key)
+
+
+@pytest.mark.parametrize("mode", MODES)
+@pytest.mark.parametrize("bits", [2, 3, 4])
+@pytest.mark.parametrize("G", [32, 64])
+def test_k_store_append_bit_exact(mode, bits, G):
+    """quantize-on-append in pieces (prefill, single tokens, a burst) == oracle store bytes"""
+    B, H, T, D = 2, 2, 200, 128
+    x = special_input(B, H, T, D, seed=bits + G)
+    st = ops.PackedStore("channel", B, H, D, G, bits, mode, DEV)
+    xt = f16t(x)
+    for a, b in ((0, 130), (130, 131), (131, 132), (132, 200)):
+        st.append(xt[:, :, a:b])
+    assert st.length == T
+    c, s, z = oracle_q(x, bits, G, mode, "channel")
+    cw, meta = Q.build_k_store(c, s, z, bits, G, mode, tcap=st.t_cap)
+    nblk = -(-T // 64)
+    got_c = st.codes.cpu().numpy().view(np.uint32).reshape(cw.shape)
+    got_m = st.meta.cpu().numpy().view(np.uint16).reshape(meta.shape)
+    # rows past T in the last block are unspecified
+    gc, rc = Q.k_store_to_codes(got_c, got_m, T, bits, G, mode), Q.k_store_to_codes(cw, meta, T, bits, G, mode)
+    np.testing.assert_array_equal(gc[0], rc[0])
+    np.testing.assert_array_equal(gc[1].view(np.uint16), rc[1].view(np.uint16))
+    if mode == "asymmetric":
+        np.testing.assert_array_equal(gc[2].view(np.uint16), rc[2].view(np.uint16))
+    np.testing.assert_array_equal(got_c[:, :, :nblk - 1], cw[:, :, :nblk - 1])
+
+
+@pytest.mark.parametrize("mode", MODES)
+@pytest.mark.parametrize("bits", [2, 3, 4])
+@pytest.mark.parametrize("G", [32, 64])
+def test_v_store_append_bit_exact(mode, bits, G):
+    B, H, T, D = 2, 2, 4 * G, 128
+    x = special_input(B, H, T, D, seed=3 * bits + G)
+    st = ops.PackedStore("token", B, H, D, G, bits, mode, DEV)
+    xt = f16t(x)
+    st.append(xt[:, :, :G])
+    st.append(xt[:, :, G:4 * G])
+    c, s, z = oracle_q(x, bits, G, mode, "token")
+    cw, meta = Q.build_v_store(c, s, z, bits, G, mode, tcap=st.t_cap)
+    np.testing.assert_array_equal(st.codes.cpu().numpy().view(np.uint32).reshape(cw.shape)[:, :, :T // G],
+                                  cw[:, :, :T // G])
+    np.testing.assert_array_equal(st.meta.cpu().numpy().view(np.uint16).reshape(meta.shape)[:, :, :T // G],
+                                  meta[:, :, :T // G])
+
+
+# ----------------------------------------------------------------------------
+# dense read path (A3, A4, A10)
+# ----------------------------------------------------------------------------
+@pytest.mark.parametrize("axis", ["channel", "token"])
+@pytest.mark.parametrize("mode", MODES)
+@pytest.mark.parametrize("bits", [2, 3, 4])
+def test_store_dequant_bit_exact(axis, mode, bits):
+    B, H, T, D, G = 1, 3, 192, 128, 32
+    x = special_input(B, H, T, D, seed=40 + bits)
+    st = ops.PackedStore(axis, B, H, D, G, bits, mode, DEV)
+    st.append(f16t(x))
+    c, s, z = oracle_q(x, bits, G, mode, axis)
+    ref = oracle_deq(c, s, z, G, mode, axis)
+    got32 = st.dequant(dtype=torch.float32).cpu().numpy()
+    np.testing.assert_array_equal(got32, ref)  # value equality (+0 == -0)
+    got16 = st.dequant().cpu().numpy()
+    np.testing.assert_array_equal(got16, ref.astype(np.float16))
+    # a strided sub-range
+    out = torch.zeros(B, H, 300, D, dtype=torch.float16, device=DEV)
+    st.dequant(64, 96, out=out[:, :, 10:106])
+    np.testing.assert_array_equal(out[:, :, 10:106].cpu().numpy(), ref[:, :, 64:160].astype(np.float16))
+
+
+@pytest.mark.parametrize("axis", ["channel", "token"])
+@pytest.mark.parametrize("mode", MODES)
+def test_dequantize_dense_api(axis, mode):
+    x = special_input(1, 2, 64, 128, seed=77)
+    c, s, z = oracle_q(x, 4, 32, mode, axis)
+    ref = oracle_deq(c, s, z, 32, mode, axis)
+    got = ops.dequantize_dense(torch.from_numpy(c).to(DEV), f16t(s), f16t(z), 32, mode, axis).cpu().numpy()
+    np.testing.assert_array_equal(got, ref)
+
+
+def test_key_normalized_store_dequant():
+    B, H, T, D, G = 1, 2, 128, 128, 32
+    x = special_input(B, H, T, D, seed=5)
+    norm = np.sqrt(np.abs(x).max(axis=-2, keepdims=True).astype(np.float32)).astype(np.float16)
+    xn = (x.astype(np.float32) / norm.astype(np.float32)).astype(np.float16)
+    st = ops.PackedStore("channel", B, H, D, G, 3, "symmetric", DEV)
+    st.append(f16t(x), norm=f16t(norm))
+    c, s, sg = Q.quantize_channeldim_sym(xn, G, 3)
+    ref = Q.dequantize_channeldim_sym(c, s, sg, G) * norm.astype(np.float32)
+    got = st.dequant(norm=f16t(norm), dtype=torch.float32).cpu().numpy()
+    np.testing.assert_array_equal(got, ref)
+
+
+# ----------------------------------------------------------------------------
+# GEMVs (A6, A8)
+# ----------------------------------------------------------------------------
+def build_k(B, Hkv, T, D, G, bits, mode, seed):
+    x = synth.kv_tensor(B, Hkv, T, D, seed=seed, n_out=4, factor=10.0)
+    st = ops.PackedStore("channel", B, Hkv, D, G, bits, mode, DEV)
+    st.append(f16t(x))
+    c, s, z = oracle_q(x, bits, G, mode, "channel")
+    return st, oracle_deq(c, s, z, G, mode, "channel")
+
+
+def build_v(B, Hkv, T, D, G, bits, mode, seed):
+    x = synth.kv_tensor(B, Hkv, T, D, seed=seed, n_out=4, factor=10.0)
+    st = ops.PackedStore("token", B, Hkv, D, G, bits, mode, DEV)
+    st.append(f16t(x))
+    c, s, z = oracle_q(x, bits, G, mode, "token")
+    return st, oracle_deq(c, s, z, G, mode, "token")
+
+
+@pytest.mark.parametrize("mode", MODES)
+@pytest.mark.parametrize("bits", [2, 3, 4])
+@pytest.mark.parametrize("G", [32, 64, 128])
+@pytest.mark.parametrize("nrep", [1, 4])
+def test_qk_gemv_parity(mode, bits, G, nrep):
+    B, Hkv, T, D = 2, 2, 333, 128
+    st, kdeq = build_k(B, Hkv, T, D, G, bits, mode, seed=bits * 7 + G + nrep)
+    q = synth.normal((B, Hkv * nrep, D), seed=99 + G).astype(np.float16)
+    scale = D ** -0.5
+    got = ops.qk_gemv(f16t(q), st, scale).cpu().numpy()
+    ref = A.qk_logits(q, kdeq, scale)
+    assert A.rel_err(got, ref) < TOL
+
+
+@pytest.mark.parametrize("nrep", [2, 8])
+@pytest.mark.parametrize("D", [64, 128])
+def test_qk_gemv_shapes(nrep, D):
+    B, Hkv, T = 3, 1, 64 * 5 + 17
+    st, kdeq = build_k(B, Hkv, T, D, 32, 4, "asymmetric", seed=nrep + D)
+    q = synth.normal((B, Hkv * nrep, D), seed=3).astype(np.float16)
+    got = ops.qk_gemv(f16t(q), st, 1.0).cpu().numpy()
+    assert A.rel_err(got, A.qk_logits(q, kdeq, 1.0)) < TOL
+    # sub-range starting at a block boundary, written into a strided output
+    out = torch.full((B, Hkv * nrep, 400), 7.0, device=DEV)
+    ops.qk_gemv(f16t(q), st, 1.0, t0=128, T=T - 128, out=out[:, :, 5:5 + T - 128])
+    o = out.cpu().numpy()
+    assert A.rel_err(o[:, :, 5:5 + T - 128], A.qk_logits(q, kdeq[:, :, 128:], 1.0)) < TOL
+    assert np.all(o[:, :, :5] == 7.0) and np.all(o[:, :, 5 + T - 128:] == 7.0)
+
+
+def test_qk_gemv_key_norm_folded():
+    B, Hkv, T, D, G = 1, 2, 256, 128, 32
+    x = synth.kv_tensor(B, Hkv, T, D, seed=11, n_out=4, factor=8.0)
+    norm = np.sqrt(np.abs(x).max(axis=-2, keepdims=True).astype(np.float32)).astype(np.float16)
+    st = ops.PackedStore("channel", B, Hkv, D, G, 3, "symmetric", DEV)
+    st.append(f16t(x), norm=f16t(norm))
+    xn = (x.astype(np.float32) / norm.astype(np.float32)).astype(np.float16)
+    c, s, sg = Q.quantize_channeldim_sym(xn, G, 3)
+    kdeq = Q.dequantize_channeldim_sym(c, s, sg, G) * norm.astype(np.float32)
+    q = synth.normal((B, Hkv * 4, D), seed=12).astype(np.float16)
+    got = ops.qk_gemv(f16t(q), st, D ** -0.5, norm=f16t(norm)).cpu().numpy()
+    assert A.rel_err(got, A.qk_logits(q, kdeq, D ** -0.5)) < TOL
+
+
+def peaked_p(B, Hq, T, seed, std=2.0):
+    logits = synth.normal((B, Hq, T), seed=seed, std=std).astype(np.float64)
+    return A.softmax(logits).astype(np.float16)
+
+
+@pytest.mark.parametrize("mode", MODES)
+@pytest.mark.parametrize("bits", [2, 3, 4])
+@pytest.mark.parametrize("G", [32, 64, 128])
+@pytest.mark.parametrize("nrep", [1, 4])
+def test_av_gemv_parity(mode, bits, G, nrep):
+    B, Hkv, D = 2, 2, 128
+    T = 6 * G
+    st, vdeq = build_v(B, Hkv, T, D, G, bits, mode, seed=bits * 5 + G + nrep)
+    p = peaked_p(B, Hkv * nrep, T, seed=G + bits)
+    got = ops.av_gemv(f16t(p), st).cpu().numpy().astype(np.float64)
+    ref = A.av_out(p, vdeq)
+    assert A.rel_err(got, ref) < TOL
+
+
+@pytest.mark.parametrize("nrep", [2, 8])
+@pytest.mark.parametrize("D", [64, 128])
+def test_av_gemv_shapes_and_accumulate(nrep, D):
+    B, Hkv, G = 2, 1, 32
+    T = 3000 - 3000 % G
+    st, vdeq = build_v(B, Hkv, T, D, G, 4, "asymmetric", seed=nrep * D)
+    p = peaked_p(B, Hkv * nrep, T, seed=4)
+    o32 = torch.ones(B, Hkv * nrep, D, device=DEV)
+    o16 = torch.empty(B, Hkv * nrep, D, dtype=torch.float16, device=DEV)
+    ops.av_gemv(f16t(p), st, t0=G, T=T - 2 * G, out=o16, out32=o32, accumulate=True)
+    ref = A.av_out(p[:, :, G:T - G], vdeq[:, :, G:T - G]) + 1.0
+    assert A.rel_err(o32.cpu().numpy(), ref) < TOL
+    assert A.rel_err(o16.cpu().numpy().astype(np.float64), ref) < 2e-3
+
+
+def test_av_gemv_linearity():
+    """p -> p.V is linear: AV(p1 + p2) == AV(p1) + AV(p2) (size-independent property)"""
+    B, Hkv, T, D, G = 1, 2, 4096, 128, 64
+    st, _ = build_v(B, Hkv, T, D, G, 2, "asymmetric", seed=8)
+    p1 = peaked_p(B, Hkv * 4, T, seed=1).astype(np.float32) / 2
+    p2 = peaked_p(B, Hkv * 4, T, seed=2).astype(np.float32) / 2
+    a = ops.av_gemv(f16t(p1.astype(np.float16)), st, out32=torch.empty(B, 8, D, device=DEV)).cpu().numpy()
+    b = ops.av_gemv(f16t(p2.astype(np.float16)), st, out32=torch.empty(B, 8, D, device=DEV)).cpu().numpy()
+    c = ops.av_gemv(f16t((p1.astype(np.float16).astype(np.float32) + p2.astype(np.float16).astype(np.float32))
+                         .astype(np.float16)), st, out32=torch.empty(B, 8, D, device=DEV)).cpu().numpy()
+    assert A.rel_err(c, a + b) < 2e-3
+
+
+# ----------------------------------------------------------------------------
+# decode step (A9 + segments)
+# ----------------------------------------------------------------------------
+@pytest.mark.parametrize("kb,vb,kmode,vmode", [(4, 4, "asymmetric", "asymmetric"), (3, 3, "symmetric", "symmetric"),
+                                               (2, 4, "asymmetric", "symmetric")])
+def test_decode_attention_segments(kb, vb, kmode, vmode):
+    B, Hkv, nrep, D, G = 2, 2, 4, 128, 32
+    ks, kq, kr = 32, 640 - 32 - 96, 96        # K: flush 1 keeps the recent window full
+    vs, vq, vr = 32, 640 - 32 - 64, 64        # V: flush 32 drains it
+    T = ks + kq + kr
+    kx = synth.kv_tensor(B, Hkv, T, D, seed=21, n_out=4, factor=8.0)
+    vx = synth.kv_tensor(B, Hkv, T, D, seed=22, n_out=4, factor=8.0)
+    kst = ops.PackedStore("channel", B, Hkv, D, G, kb, kmode, DEV)
+    kst.append(f16t(kx[:, :, ks:ks + kq]))
+    vst = ops.PackedStore("token", B, Hkv, D, G, vb, vmode, DEV)
+    vst.append(f16t(vx[:, :, vs:vs + vq]))
+    q = synth.normal((B, Hkv * nrep, D), seed=23).astype(np.float16)
+    kxt, vxt = f16t(kx), f16t(vx)
+    got = ops.decode_attention(f16t(q), kxt[:, :, :ks], kst, kxt[:, :, ks + kq:], vxt[:, :, :vs], vst,
+                               vxt[:, :, vs + vq:], D ** -0.5).cpu().numpy().astype(np.float64)
+    c, s, z = oracle_q(kx[:, :, ks:ks + kq], kb, G, kmode, "channel")
+    kd = np.concatenate([kx[:, :, :ks].astype(np.float32), oracle_deq(c, s, z, G, kmode, "channel"),
+                         kx[:, :, ks + kq:].astype(np.float32)], axis=2)
+    c, s, z = oracle_q(vx[:, :, vs:vs + vq], vb, G, vmode, "token")
+    vd = np.concatenate([vx[:, :, :vs].astype(np.float32), oracle_deq(c, s, z, G, vmode, "token"),
+                         vx[:, :, vs + vq:].astype(np.float32)], axis=2)
+    ref = A.decode_attention(q, kd, vd, D ** -0.5, p_dtype=None)
+    assert A.rel_err(got, ref) < TOL
+
+
+def test_decode_attention_all_quantized_and_all_dense():
+    B, Hkv, nrep, D, G, T = 1, 2, 4, 128, 32, 512
+    kx = synth.kv_tensor(B, Hkv, T, D, seed=31)
+    vx = synth.kv_tensor(B, Hkv, T, D, seed=32)
+    q = synth.normal((B, Hkv * nrep, D), seed=33).astype(np.float16)
+    kst = ops.PackedStore("channel", B, Hkv, D, G, 4, "asymmetric", DEV)
+    vst = ops.PackedStore("token", B, Hkv, D, G, 4, "asymmetric", DEV)
+    kst.append(f16t(kx))
+    vst.append(f16t(vx))
+    got = ops.decode_attention(f16t(q), None, kst, None, None, vst, None, D ** -0.5).cpu().numpy()
+    c, s, z = Q.quantize_channeldim_asym(kx, G, 4)
+    kd = Q.dequantize_channeldim_asym(c, s, z, G)
+    c, s, z = Q.quantize_tokendim_asym(vx, G, 4)
+    vd = Q.dequantize_tokendim_asym(c, s, z, G)
+    assert A.rel_err(got.astype(np.float64), A.decode_attention(q, kd, vd, D ** -0.5, None)) < TOL
+    # fp16 only (no quantized segments): exactly the eager attention over fp16 K/V
+    got = ops.decode_attention(f16t(q), f16t(kx), None, None, f16t(vx), None, None, D ** -0.5).cpu().numpy()
+    ref = A.decode_attention(q, kx.astype(np.float32), vx.astype(np.float32), D ** -0.5, None)
+    assert A.rel_err(got.astype(np.float64), ref) < TOL

@@ -1,0 +1,94 @@
+"""Pin the cache state-machine oracle (oracle/cache_ref.py) against traces of the
+live reference InnerqDynamicLayer (tests/golden/cache_golden.npz)."""
+import hashlib
+
+import numpy as np
+import pytest
+
+from innerq_amd import synth
+from oracle import cache_ref
+
+PRESETS = {
+    "innerq_base": dict(k_bits=3, v_bits=3, key_flush_size=1, value_flush_size=32, key_group_size=32,
+                        value_group_size=32, key_w_recent=96, value_w_recent=96, key_w_sink=32,
+                        value_w_sink=32, key_normalize=True, key_quantize_over_token=False,
+                        value_quantize_over_token=True, key_quantize_mode="symmetric",
+                        value_quantize_mode="symmetric"),
+    "asym4_nosink": dict(k_bits=4, v_bits=4, key_flush_size=1, value_flush_size=32, key_group_size=32,
+                         value_group_size=32, key_w_recent=32, value_w_recent=64, key_w_sink=0,
+                         value_w_sink=0, key_normalize=False, key_quantize_over_token=False,
+                         value_quantize_over_token=True, key_quantize_mode="asymmetric",
+                         value_quantize_mode="asymmetric"),
+    "mixed_k2v4_flush32": dict(k_bits=2, v_bits=4, key_flush_size=32, value_flush_size=64,
+                               key_group_size=32, value_group_size=32, key_w_recent=40, value_w_recent=70,
+                               key_w_sink=4, value_w_sink=0, key_normalize=False,
+                               key_quantize_over_token=False, value_quantize_over_token=True,
+                               key_quantize_mode="asymmetric", value_quantize_mode="symmetric"),
+    "hybrid_v": dict(k_bits=3, v_bits=2, key_flush_size=1, value_flush_size=32, key_group_size=32,
+                     value_group_size=32, key_w_recent=96, value_w_recent=96, key_w_sink=32,
+                     value_w_sink=32, key_normalize=True, key_quantize_over_token=False,
+                     value_quantize_over_token=True, key_quantize_mode="symmetric",
+                     value_quantize_mode="hybrid"),
+    "k_only": dict(k_bits=4, v_bits=16, key_flush_size=1, key_group_size=64, key_w_recent=16,
+                   key_w_sink=2, key_normalize=False, key_quantize_mode="asymmetric"),
+}
+
+
+class Cfg:
+    def __init__(self, **kw):
+        self.__dict__.update(kw)
+
+
+def _sha(k, v):
+    b = np.concatenate([k.view(np.uint16).ravel(), v.view(np.uint16).ravel()])
+    return np.frombuffer(hashlib.sha256(b.tobytes()).digest(), dtype=np.uint8)
+
+
+def golden_inputs(g, name):
+    seed, B, H, D, prefill, steps = (int(x) for x in g[f"{name}_seed"])
+    kx = synth.kv_tensor(B, H, prefill + steps, D, seed=seed, n_out=2, factor=8.0)
+    vx = synth.kv_tensor(B, H, prefill + steps, D, seed=seed + 1, n_out=2, factor=8.0)
+    return kx, vx, prefill, steps
+
+
+@pytest.mark.parametrize("name", list(PRESETS))
+def test_cache_oracle_matches_reference_trace(cache_golden, name):
+    g = cache_golden
+    kx, vx, prefill, steps = golden_inputs(g, name)
+    layer = cache_ref.CacheLayerRef(Cfg(**PRESETS[name]))
+    K, V = layer.update(kx[:, :, :prefill], vx[:, :, :prefill])
+    np.testing.assert_array_equal(_sha(K, V), g[f"{name}_step0_sha256"])
+    for s in range(steps):
+        K, V = layer.update(kx[:, :, prefill + s:prefill + s + 1], vx[:, :, prefill + s:prefill + s + 1])
+        if s == steps - 1:
+            np.testing.assert_array_equal(K.view(np.uint16), g[f"{name}_step{s + 1}_k"])
+            np.testing.assert_array_equal(V.view(np.uint16), g[f"{name}_step{s + 1}_v"])
+        np.testing.assert_array_equal(_sha(K, V), g[f"{name}_step{s + 1}_sha256"], err_msg=f"step {s + 1}")
+        lens = g[f"{name}_len{s + 1}"]
+        assert (K.shape[-2], V.shape[-2], layer.keys_recent.shape[-2], layer.values_recent.shape[-2]) == tuple(lens)
+
+
+@pytest.mark.parametrize("name", list(PRESETS))
+def test_length_schedule_matches_reference_trace(cache_golden, name):
+    """the length-only simulator reproduces the reference's recent-window lengths (incl. the V drain)"""
+    p = PRESETS[name]
+    g = cache_golden
+    _, _, prefill, steps = golden_inputs(g, name)
+    ks = cache_cache = cache_ref.schedule(prefill, steps, p.get("key_w_sink", 0), p.get("key_w_recent", 32),
+                                          p.get("key_flush_size", 32), p.get("k_bits", 16) < 16,
+                                          p.get("key_quantize_over_token", False))
+    vs = cache_ref.schedule(prefill, steps, p.get("value_w_sink", 0), p.get("value_w_recent", 32),
+                            p.get("value_flush_size", 32), p.get("v_bits", 16) < 16,
+                            p.get("value_quantize_over_token", True))
+    for s in range(1, steps + 1):
+        lens = g[f"{name}_len{s}"]
+        assert ks[s][2] == lens[2] and vs[s][2] == lens[3]
+        assert sum(ks[s]) == lens[0] and sum(vs[s]) == lens[1]
+
+
+def test_value_recent_window_drains():
+    """V with flush 32 drains its recent window 96 -> 65 -> 34 -> 3 (cache.py:296-307)"""
+    sched = cache_ref.schedule(500, 100, 32, 96, 32, True, True)
+    nr = [x[2] for x in sched]
+    assert nr[0] == 84  # (468 - r) % 32 == 0 -> r = 84
+    assert min(nr[1:]) < 32 and max(nr[1:]) <= 96
