@@ -1,0 +1,256 @@
+"""Headline benchmark: decode QK^T + attn.V on packed 4-bit KV at 32k context (one MI355X).
+
+Workload H (BASELINE.json metric, configs[4] shape with 4-bit K and V, one
+layer, every token quantized): B=8, 32 query heads over 8 KV heads (GQA 4),
+head_dim 128, T=32768, asym groups of 32 (K along head_dim, V along tokens).
+A step is one decode-attention call of the product path (QK^T GEMV, fp32
+softmax -> fp16, attn.V GEMV with its split-T combine) for one new query
+token per sequence.  Inputs are resident in HBM; the packed caches rotate
+over --copies independent copies (>= 1 GiB) so every step reads cold data
+past the 256 MiB Infinity Cache.
+
+value = algorithmic packed-code + metadata bytes of both GEMVs / step time.
+roofline = the dominant GEMV kernel alone, timed with HIP events on the
+stream it runs on.  cpu_baseline = the reference's torch CPU path
+(dequantize int32 codes -> fp16 -> eager attention) on a sample of the same
+workload, timed on host cores (oracle/timing.py).
+
+    python bench.py [--gpus 1] [--steps 100] [--warmup 10]
+    python bench.py --config {H,1,2,3,4}    other BASELINE configs (not the headline line)
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, HERE)
+
+METRIC = "decode QK^T+attn·V µs/step and HBM GB/s (% of peak) at 32k ctx, 4-bit"
+PEAK_GBS = 8000.0
+
+
+def gemv_bytes(B, Hkv, T, D, G, bits, mode, axis):
+    m = 4 if mode == "asymmetric" else 2
+    groups = T * (D // G) if axis == "channel" else (T // G) * D
+    return B * Hkv * (T * D * bits // 8 + groups * m)
+
+
+def make_store(axis, B, Hkv, T, D, G, bits, mode, seed, dev, n_out=4, factor=10.0):
+    import torch
+    from innerq_amd import ops
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    x = torch.randn(B, Hkv, T, D, generator=gen, device=dev, dtype=torch.float32)
+    ch = torch.randperm(D, generator=torch.Generator().manual_seed(seed))[:n_out].to(dev)
+    x[..., ch] *= factor
+    x = x.to(torch.float16)
+    st = ops.PackedStore(axis, B, Hkv, D, G, bits, mode, dev, t_cap=T)
+    st.append(x)
+    del x
+    return st
+
+
+def time_loop(fn, n, warmup):
+    import torch
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for i in range(n):
+        fn(i)
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / n * 1e3  # us per call
+
+
+def cpu_baseline(B, Hq, Hkv, T, D, G, bk, bv, step_bytes, budget_s=12.0):
+    import torch
+    from oracle import timing
+    threads = min(16, os.cpu_count() or 1)
+    sample_b = 1
+    sec, reps = timing.time_reference(sample_b, Hq, Hkv, T, D, G, bk, bv, threads, min_seconds=budget_s)
+    step_s = sec * (B / sample_b)
+    return {"value": round(step_bytes / step_s / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "us_per_step": round(step_s * 1e6, 1),
+            "sample": f"{reps} reference steps of 1 of the {B} sequences (Hq={Hq}, Hkv={Hkv}, T={T}, D={D}, "
+                      f"int32 codes -> fp32 dequant -> fp16 -> eager attention, torch CPU, {threads} threads), "
+                      f"scaled x{B // sample_b}",
+            "cpu": _cpu_model(), "torch_threads": threads}
+
+
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def traffic_from_profiles(kernel):
+    path = os.path.join(HERE, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get(kernel)
+    except (OSError, ValueError):
+        return None
+
+
+def bench_headline(args):
+    import torch
+    from innerq_amd import ops
+    dev = torch.device("cuda:0")
+    B, Hq, Hkv, D, T, G, bits, mode = 8, 32, 8, 128, 32768, 32, 4, "asymmetric"
+    scale = D ** -0.5
+    ks = [make_store("channel", B, Hkv, T, D, G, bits, mode, 100 + c, dev) for c in range(args.copies)]
+    vs = [make_store("token", B, Hkv, T, D, G, bits, mode, 200 + c, dev) for c in range(args.copies)]
+    q = torch.randn(B, Hq, D, device=dev, dtype=torch.float16)
+    out = torch.empty(B, Hq, D, device=dev, dtype=torch.float16)
+    C = args.copies
+
+    def step(i):
+        ops.decode_attention(q, None, ks[i % C], None, None, vs[i % C], None, scale, out=out)
+
+    us_step = time_loop(step, args.steps, args.warmup)
+
+    logits = torch.empty(B, Hq, T, device=dev, dtype=torch.float32)
+    p = torch.softmax(torch.randn(B, Hq, T, device=dev) * 2.0, dim=-1).to(torch.float16)
+    o32 = torch.empty(B, Hq, D, device=dev, dtype=torch.float32)
+    us_qk = time_loop(lambda i: ops.qk_gemv(q, ks[i % C], scale, out=logits), args.steps, args.warmup)
+    us_av = time_loop(lambda i: ops.av_gemv(p, vs[i % C], out32=o32), args.steps, args.warmup)
+
+    qk_b = gemv_bytes(B, Hkv, T, D, G, bits, mode, "channel")
+    av_b = gemv_bytes(B, Hkv, T, D, G, bits, mode, "token")
+    step_b = qk_b + av_b
+    value = step_b / (us_step * 1e-6) / 1e9
+    dom, dom_us, dom_b = ("qk_kernel", us_qk, qk_b) if us_qk >= us_av else ("av_kernel+av_combine", us_av, av_b)
+    ach = dom_b / (dom_us * 1e-6) / 1e9
+    line = {
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(us_step / 1e3, 5), "us_per_step": round(us_step, 2),
+        "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "frac_of_hbm_peak": round(value / PEAK_GBS, 4),
+        "dtype": "u4 codes, f16 operands, f32 accumulate", "data": "synthetic (seeded torch.randn K/V, 4 outlier "
+                                                                      "channels x10, quantized by the product path)",
+        "config": {"workload": "H: one-layer decode attention, B=8, Hq=32, Hkv=8, D=128, T=32768 all quantized, "
+                               "4-bit K (groups along head_dim) and V (groups along tokens), asym, G=32",
+                   "global_batch": B, "seq_len": T, "parallelism": "single GPU", "copies_rotated": C,
+                   "algorithmic_bytes_per_step": step_b},
+        "kernels_us": {"qk_gemv": round(us_qk, 2), "av_gemv_incl_combine": round(us_av, 2),
+                       "qk_GBs": round(qk_b / us_qk / 1e3, 1), "av_GBs": round(av_b / us_av / 1e3, 1)},
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(ach, 1), "peak": PEAK_GBS, "unit": "GB/s",
+                     "frac": round(ach / PEAK_GBS, 4), "traffic": traffic_from_profiles(dom),
+                     "algorithmic_bytes": dom_b},
+    }
+    if not args.no_cpu:
+        line["cpu_baseline"] = cpu_baseline(B, Hq, Hkv, T, D, G, bits, bits, step_b)
+    print(json.dumps(line), flush=True)
+
+
+def bench_config(args):
+    """Non-headline BASELINE configs, one JSON line each (used for DESIGN.md tables)."""
+    import torch
+    from innerq_amd import ops
+    dev = torch.device("cuda:0")
+    C = args.copies
+    cfg = args.config
+    res = {"config": cfg}
+    if cfg == "1":
+        B, Hq, Hkv, D, T, G = 1, 32, 8, 128, 8192, 32
+        ks = [make_store("channel", B, Hkv, T, D, G, 4, "asymmetric", 10 + c, dev) for c in range(C)]
+        q = torch.randn(B, Hq, D, device=dev, dtype=torch.float16)
+        lg = torch.empty(B, Hq, T, device=dev)
+        us = time_loop(lambda i: ops.qk_gemv(q, ks[i % C], D ** -0.5, out=lg), args.steps, args.warmup)
+        b = gemv_bytes(B, Hkv, T, D, G, 4, "asymmetric", "channel")
+        res.update(us=us, GBs=b / us / 1e3, bytes=b)
+    elif cfg == "2":
+        B, Hq, Hkv, D, T, G = 8, 32, 8, 128, 32768, 64
+        for mode in ("asymmetric", "symmetric"):
+            vs = [make_store("token", B, Hkv, T, D, G, 2, mode, 20 + c, dev) for c in range(C)]
+            p = torch.softmax(torch.randn(B, Hq, T, device=dev) * 2.0, dim=-1).to(torch.float16)
+            out = torch.empty(B, Hq, D, device=dev, dtype=torch.float16)
+            us = time_loop(lambda i: ops.av_gemv(p, vs[i % C], out=out), args.steps, args.warmup)
+            b = gemv_bytes(B, Hkv, T, D, G, 2, mode, "token")
+            res[mode] = dict(us=us, GBs=b / us / 1e3, bytes=b)
+            del vs
+    elif cfg == "3":
+        B, Hq, Hkv, D, T, G, R = 16, 32, 8, 128, 16384, 32, 128
+        Tq = T - R
+        ks = [make_store("channel", B, Hkv, Tq, D, G, 3, "symmetric", 30 + c, dev) for c in range(C)]
+        vs = [make_store("token", B, Hkv, Tq, D, G, 3, "symmetric", 40 + c, dev) for c in range(C)]
+        kr = torch.randn(B, Hkv, R, D, device=dev, dtype=torch.float16)
+        vr = torch.randn(B, Hkv, R, D, device=dev, dtype=torch.float16)
+        q = torch.randn(B, Hq, D, device=dev, dtype=torch.float16)
+        knew = torch.randn(B, Hkv, 1, D, device=dev, dtype=torch.float16)
+        out = torch.empty(B, Hq, D, device=dev, dtype=torch.float16)
+        ap = [make_store("channel", B, Hkv, 64, D, G, 3, "symmetric", 50, dev) for _ in range(1)][0]
+
+        def step(i):
+            ops.decode_attention(q, None, ks[i % C], kr, None, vs[i % C], vr, D ** -0.5, out=out)
+            ap.length = 0
+            ap.append(knew)  # quantize-on-append of one token per sequence (K, flush 1)
+
+        us = time_loop(step, args.steps, args.warmup)
+        b = 2 * gemv_bytes(B, Hkv, Tq, D, G, 3, "symmetric", "channel")
+        res.update(us=us, GBs=b / us / 1e3, bytes=b)
+    elif cfg == "4":
+        B, Hq, Hkv, D, T, G, R, L = 8, 32, 8, 128, 32768, 32, 128, 32
+        Tq = T - R
+        ks = [make_store("channel", B, Hkv, Tq, D, G, 2, "asymmetric", 60 + l, dev) for l in range(L)]
+        vs = [make_store("token", B, Hkv, Tq, D, G, 4, "asymmetric", 100 + l, dev) for l in range(L)]
+        kr = torch.randn(B, Hkv, R, D, device=dev, dtype=torch.float16)
+        vr = torch.randn(B, Hkv, R, D, device=dev, dtype=torch.float16)
+        q = torch.randn(B, Hq, D, device=dev, dtype=torch.float16)
+        out = torch.empty(B, Hq, D, device=dev, dtype=torch.float16)
+
+        def step(i):
+            for l in range(L):
+                ops.decode_attention(q, None, ks[l], kr, None, vs[l], vr, D ** -0.5, out=out)
+
+        us = time_loop(step, max(1, args.steps // 10), 2)
+        b = L * (gemv_bytes(B, Hkv, Tq, D, G, 2, "asymmetric", "channel")
+                 + gemv_bytes(B, Hkv, Tq - Tq % G, D, G, 4, "asymmetric", "token"))
+        res.update(us=us, us_per_layer=us / L, GBs=b / us / 1e3, bytes=b)
+    print(json.dumps(res), flush=True)
+
+
+def calib_copy(args):
+    """A plain device copy of known size, for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE."""
+    import torch
+    n = 256 << 20
+    src = torch.empty(n, dtype=torch.uint8, device="cuda:0").fill_(1)
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"calib_copy_bytes": n}), flush=True)
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--copies", type=int, default=4)
+    ap.add_argument("--config", default="H")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calib-copy", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one MI355X: this build runs on one GPU only (no collectives); "
+              f"--gpus {args.gpus} is not supported", file=sys.stderr)
+        sys.exit(2)
+    if args.calib_copy:
+        calib_copy(args)
+    elif args.config == "H":
+        bench_headline(args)
+    else:
+        bench_config(args)
+
+
+if __name__ == "__main__":
+    main()

@@ -256,7 +256,7 @@ def test_av_gemv_shapes_and_accumulate(nrep, D):
     p = peaked_p(B, Hkv * nrep, T, seed=4)
     o32 = torch.ones(B, Hkv * nrep, D, device=DEV)
     o16 = torch.empty(B, Hkv * nrep, D, dtype=torch.float16, device=DEV)
-    ops.av_gemv(f16t(p), st, t0=G, T=T - 2 * G, out=o16, out32=o32, accumulate=True)
+    ops.av_gemv(f16t(p[:, :, G:T - G]), st, t0=G, T=T - 2 * G, out=o16, out32=o32, accumulate=True)
     ref = A.av_out(p[:, :, G:T - G], vdeq[:, :, G:T - G]) + 1.0
     assert A.rel_err(o32.cpu().numpy(), ref) < TOL
     assert A.rel_err(o16.cpu().numpy().astype(np.float64), ref) < 2e-3
