@@ -129,13 +129,18 @@ int iq_dequant_dense(const int32_t* codes, const void* scale16, const void* zs16
  * q fp16 [B,Hq,D] (strides sq_b, sq_h; D contiguous); out fp32 with strides
  * so_b, so_h (token index contiguous).  Replaces matmul(q, repeat_kv(K_deq)^T)
  * * scaling (TF/models/llama/modeling_llama.py:201-204) over the quantized
- * segment, without materializing K_deq. */
+ * segment, without materializing K_deq.  workspace: iq_qk_workspace_bytes(). */
 int iq_qk_gemv(const void* q, int64_t sq_b, int64_t sq_h, const void* norm,
                const uint32_t* k_codes, const uint16_t* k_meta, int64_t t_cap,
                int B, int Hq, int Hkv, int t0, int T, int D, int group, int bits, int mode, float scale,
-               float* out, int64_t so_b, int64_t so_h, void* stream);
+               float* out, int64_t so_b, int64_t so_h, void* workspace, size_t workspace_bytes, void* stream);
 
-/* Workspace for iq_av_gemv: fp32 split-T partials. */
+/* Workspace for iq_qk_gemv: the query operand records (query pairs in the
+ * unpack plan's order plus per-group sums), 16-byte aligned. */
+size_t iq_qk_workspace_bytes(int B, int Hq, int D);
+
+/* Workspace for iq_av_gemv: probability operand records plus fp32 split-T
+ * partials, 16-byte aligned. */
 size_t iq_av_workspace_bytes(int B, int Hq, int T, int D, int group);
 
 /* Decode attn.V GEMV over a packed V store: for store tokens [t0, t0+T)

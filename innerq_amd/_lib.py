@@ -59,7 +59,8 @@ SIGNATURES = {
     "iq_dequant_k": (I, [P, P, L, P, I, I, I, I, I, I, I, I, P, P, L, L, L, P]),
     "iq_dequant_v": (I, [P, P, L, I, I, I, I, I, I, I, I, P, P, L, L, L, P]),
     "iq_dequant_dense": (I, [P, P, P, L, L, L, I, I, I, P, P]),
-    "iq_qk_gemv": (I, [P, L, L, P, P, P, L, I, I, I, I, I, I, I, I, I, F, P, L, L, P]),
+    "iq_qk_gemv": (I, [P, L, L, P, P, P, L, I, I, I, I, I, I, I, I, I, F, P, L, L, P, S, P]),
+    "iq_qk_workspace_bytes": (S, [I, I, I]),
     "iq_av_workspace_bytes": (S, [I, I, I, I, I]),
     "iq_av_gemv": (I, [P, L, L, P, P, L, I, I, I, I, I, I, I, I, I, P, P, L, L, I, P, S, P]),
     "iq_decode_workspace_bytes": (S, [I, I, I, I]),

@@ -1,0 +1,316 @@
+// Decode attn.V GEMV over a packed V store (gfx950).
+//
+// out[b, h, d] = sum_g ( s[g,d] * sum_{t in g} p[h,t] c[t,d] + z[g,d] * sum_{t in g} p[h,t] )
+//
+// Mapping: a workgroup of four waves owns a contiguous range of token groups
+// of one (batch, KV head) (split-T); wave w takes every fourth group of the
+// range, two groups per step with the next two prefetched.  Lane = head_dim
+// column (two columns at D=128), so a wave reads a group's D*G*b/8 code bytes
+// contiguously.  The probabilities come as operand records (pairs in plan
+// order, per-group bias sums and plain sums; iq_gemv.h) through scalar loads.
+// The four waves' partial sums are reduced in LDS in a fixed order, each
+// workgroup writes one fp32 partial per split, and a second kernel sums the
+// splits in split order: no atomics, deterministic results.
+#include "iq_gemv.h"
+
+using namespace iq;
+
+namespace {
+
+// one thread per (b, kvh, g, h): probability pairs in plan order + sums
+template <int BITS, int G, int NREP>
+__global__ __launch_bounds__(256) void av_record_kernel(const uint16_t* __restrict__ p, int64_t spb, int64_t sph,
+                                                        int B, int Hkv, int ngroups, uint32_t* __restrict__ rec) {
+  constexpr int NP = G / 2;
+  constexpr int RD = rec_dwords<G, NREP>();
+  constexpr PairTable<BITS, NP> PT{};
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= int64_t(B) * Hkv * ngroups * NREP) return;
+  const int h = int(i % NREP);
+  const int64_t g = (i / NREP) % ngroups;
+  const int64_t bh = i / (int64_t(NREP) * ngroups);
+  const int b = int(bh / Hkv), kvh = int(bh % Hkv);
+  const uint16_t* pr = p + b * spb + (kvh * NREP + h) * sph + g * G;
+  uint32_t* r = rec + (bh * ngroups + g) * RD;
+  float beta = 0.f, sum = 0.f;
+  for (int k = 0; k < NP; ++k) {
+    const uint16_t ua = pr[PT.a[k]], uc = pr[PT.c[k]];
+    const float xa = h2f(ua), xc = h2f(uc);
+    r[h * NP + k] = uint32_t(ua) | (uint32_t(uc) << 16);
+    beta += xa * PT.ba[k] + xc * PT.bc[k];
+    sum += xa + xc;
+  }
+  r[NP * NREP + h] = __float_as_uint(beta);
+  r[NP * NREP + NREP + h] = __float_as_uint(sum);
+}
+
+struct AVArgs {
+  const uint32_t* rec;   // records of the range's groups, [B*Hkv][ngroups]
+  const uint32_t* vc;
+  const uint16_t* vm;
+  int64_t cap_groups;
+  int Hkv, g0, ngroups, gpw;
+  float* part;           // [nsplit][B*Hq][D]
+};
+
+template <int BITS, int G, int D, int NREP, bool SYM>
+__global__ __launch_bounds__(WG) void av_kernel(AVArgs a) {
+  constexpr int W = G * BITS / 32;
+  constexpr int NP = G / 2;
+  constexpr int M = SYM ? 1 : 2;
+  constexpr int DPL = D / 64;
+  constexpr int RD = rec_dwords<G, NREP>();
+  constexpr int NB = 2;  // groups per step
+  __shared__ float red[NWAVES - 1][NREP][D];
+
+  const int bh = blockIdx.y;
+  const int split = blockIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int d0 = lane * DPL;
+  const int gl0 = split * a.gpw;
+  const int ng = min(a.gpw, a.ngroups - gl0);
+  const int cnt = ng > wave ? (ng - wave + NWAVES - 1) / NWAVES : 0;
+  const int64_t gbase = int64_t(bh) * a.cap_groups + a.g0 + gl0;
+  const cptr_u32 recb = (cptr_u32)(a.rec) + (int64_t(bh) * a.ngroups + gl0) * RD;
+
+  float acc[NREP][DPL];
+#pragma unroll
+  for (int h = 0; h < NREP; ++h)
+#pragma unroll
+    for (int e = 0; e < DPL; ++e) acc[h][e] = 0.f;
+
+  uint32_t w[NB][DPL][W];
+  uint32_t m[NB][DPL];
+  auto load = [&](int i0) {
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      if (i0 + u < cnt) {
+        const int64_t unit = (gbase + wave + NWAVES * (i0 + u)) * D + d0;
+        load_words<DPL * W>(a.vc + unit * W, &w[u][0][0]);
+        if constexpr (SYM) {
+          if constexpr (DPL == 2) {
+            const uint32_t mm = *reinterpret_cast<const uint32_t*>(a.vm + unit);
+            m[u][0] = mm & 0xffffu;
+            m[u][1] = mm >> 16;
+          } else {
+            m[u][0] = a.vm[unit];
+          }
+        } else {
+          if constexpr (DPL == 2) {
+            const uint2 mm = *reinterpret_cast<const uint2*>(a.vm + unit * 2);
+            m[u][0] = mm.x;
+            m[u][1] = mm.y;
+          } else {
+            m[u][0] = reinterpret_cast<const uint32_t*>(a.vm)[unit];
+          }
+        }
+      }
+    }
+  };
+  if (cnt > 0) load(0);
+  for (int i = 0; i < cnt; i += NB) {
+    uint32_t cw[NB][DPL][W];
+    uint32_t cm[NB][DPL];
+#pragma unroll
+    for (int u = 0; u < NB; ++u)
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) {
+        cm[u][e] = m[u][e];
+#pragma unroll
+        for (int x = 0; x < W; ++x) cw[u][e][x] = w[u][e][x];
+      }
+    if (i + NB < cnt) load(i + NB);  // prefetch the next step
+#pragma unroll
+    for (int u = 0; u < NB; ++u) {
+      if (i + u < cnt) {
+        const cptr_u32 rec = recb + (wave + NWAVES * (i + u)) * RD;
+        if constexpr (SYM) {
+#pragma unroll
+          for (int e = 0; e < DPL; ++e) to_offset_binary<BITS>(cw[u][e], W);
+        }
+        float dv[DPL][NREP];
+#pragma unroll
+        for (int h = 0; h < NREP; ++h) {
+          const float beta = rec_f32(rec, NP * NREP + h);
+#pragma unroll
+          for (int e = 0; e < DPL; ++e) dv[e][h] = -beta;
+        }
+        group_dot_rec<BITS, G, NREP, DPL>(cw[u], rec, dv);
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) {
+          const float s = h2f(uint16_t(cm[u][e] & 0xffffu));
+          const float z = SYM ? -float(1 << (BITS - 1)) * s : h2f(uint16_t(cm[u][e] >> 16));
+#pragma unroll
+          for (int h = 0; h < NREP; ++h) {
+            const float ps = rec_f32(rec, NP * NREP + NREP + h);
+            acc[h][e] = fmaf(s, dv[e][h], fmaf(z, ps, acc[h][e]));
+          }
+        }
+      }
+    }
+  }
+  if (wave > 0) {
+#pragma unroll
+    for (int h = 0; h < NREP; ++h)
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) red[wave - 1][h][d0 + e] = acc[h][e];
+  }
+  __syncthreads();
+  if (wave == 0) {
+    float* dst = a.part + (int64_t(split) * gridDim.y * NREP + int64_t(bh) * NREP) * D;
+#pragma unroll
+    for (int h = 0; h < NREP; ++h)
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) {
+        float v = acc[h][e];
+#pragma unroll
+        for (int r = 0; r < NWAVES - 1; ++r) v += red[r][h][d0 + e];
+        dst[h * D + d0 + e] = v;
+      }
+  }
+}
+
+__global__ __launch_bounds__(256) void av_combine_kernel(const float* __restrict__ part, int nsplit, int Hq, int D,
+                                                         int64_t rows, detail::OutPair o, int accumulate) {
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= rows * D) return;
+  const int64_t bq = i / D;
+  const int d = int(i % D);
+  float v = 0.f;
+  for (int s = 0; s < nsplit; ++s) v += part[(int64_t(s) * rows + bq) * D + d];
+  const int64_t off32 = (bq / Hq) * o.s32b + (bq % Hq) * o.s32h + d;
+  if (accumulate) v += o.out32[off32];
+  if (o.out32) o.out32[off32] = v;
+  if (o.out16) o.out16[(bq / Hq) * o.s16b + (bq % Hq) * o.s16h + d] = __half_as_ushort(__float2half_rn(v));
+}
+
+// groups per workgroup for a range of ngroups groups: about four workgroups
+// per CU over the whole launch, at least two groups per wave
+int groups_per_wg(int B, int Hkv, int ngroups) {
+  const int64_t target = int64_t(detail::num_cus()) * 4;
+  const int64_t bhs = std::max<int64_t>(1, int64_t(B) * Hkv);
+  const int64_t splits = std::max<int64_t>(1, target / bhs);
+  int gpw = int(ceil_div(ngroups, splits));
+  gpw = std::max(gpw, std::min(ngroups, 2 * NWAVES));
+  gpw = int(ceil_div(gpw, NWAVES) * NWAVES);
+  return std::max(gpw, 1);
+}
+
+int check_av(const void* p, const uint32_t* v_codes, const uint16_t* v_meta, int64_t t_cap, int B, int Hq, int Hkv,
+             int t0, int T, int D, int group, int bits, int mode) {
+  IQ_CHECK(p && v_codes && v_meta, IQ_ERR_NULL);
+  if (int e = check_common(bits, group, mode)) return e;
+  IQ_CHECK(B >= 0 && T >= 0 && t0 >= 0 && Hkv > 0 && Hq > 0, IQ_ERR_SHAPE);
+  IQ_CHECK(d_ok(D) && Hq % Hkv == 0 && nrep_ok(Hq / Hkv), IQ_ERR_SHAPE);
+  IQ_CHECK(T % group == 0 && t0 % group == 0 && t_cap % group == 0, IQ_ERR_GROUP);
+  IQ_CHECK(int64_t(t0) + T <= t_cap, IQ_ERR_RANGE);
+  IQ_CHECK(aligned(v_codes, 16) && aligned(v_meta, 8), IQ_ERR_ALIGN);
+  return IQ_OK;
+}
+
+}  // namespace
+
+namespace iq::detail {
+
+int av_splits(int B, int Hkv, int T, int group) {
+  const int ng = T / group;
+  if (ng <= 0) return 0;
+  return int(ceil_div(ng, groups_per_wg(B, Hkv, ng)));
+}
+
+size_t av_record_bytes(int B, int Hq, int T, int group) {
+  return ((size_t(B) * Hq * (T / group) * (group / 2 + 2) * 4) + 255) & ~size_t(255);
+}
+
+size_t av_part_bytes(int B, int Hq, int T, int D, int group) {
+  // Bound on the split count of any range of at most T tokens and any Hkv:
+  // groups_per_wg() gives gpw >= ceil(ng / S) with S <= 4*CUs/B (Hkv = 1), and
+  // gpw >= min(ng, 8), so nsplit <= min(S, ceil(ng / 8)) (and >= 1).
+  const int64_t ng = T / group;
+  const int64_t s_max = std::max<int64_t>(1, int64_t(num_cus()) * 4 / std::max(B, 1));
+  const int64_t bound = std::max<int64_t>(1, std::min<int64_t>(s_max, ceil_div(ng, 2 * NWAVES)));
+  return ((size_t(bound) * B * Hq * D * 4) + 255) & ~size_t(255);
+}
+
+int av_record_launch(const void* p, int64_t sp_b, int64_t sp_h, int B, int Hq, int Hkv, int T, int group, int bits,
+                     uint32_t* rec, hipStream_t stream) {
+  const int ng = T / group;
+  const int64_t n = int64_t(B) * Hq * ng;
+  if (n == 0) return IQ_OK;
+  return dispatch_rec(bits, group, Hq / Hkv, [&]<int BITS, int G, int R>() {
+    av_record_kernel<BITS, G, R><<<dim3(unsigned(ceil_div(n, 256))), 256, 0, stream>>>(
+        (const uint16_t*)p, sp_b, sp_h, B, Hkv, ng, rec);
+    return launch_status();
+  });
+}
+
+int av_launch_gpw(const uint32_t* rec, const uint32_t* v_codes, const uint16_t* v_meta, int64_t t_cap, int B, int Hq,
+                  int Hkv, int t0, int T, int D, int group, int bits, int mode, float* part, int gpw,
+                  hipStream_t stream) {
+  const int ng = T / group;
+  const int nsplit = int(ceil_div(ng, gpw));
+  AVArgs a{rec, v_codes, v_meta, t_cap / group, Hkv, t0 / group, ng, gpw, part};
+  return dispatch_shape(bits, group, D, Hq / Hkv, mode == IQ_MODE_SYM, [&]<int BITS, int G, int DD, int R, bool S>() {
+    av_kernel<BITS, G, DD, R, S><<<dim3(nsplit, B * Hkv), WG, 0, stream>>>(a);
+    return launch_status();
+  });
+}
+
+int av_main_launch(const uint32_t* rec, const uint32_t* v_codes, const uint16_t* v_meta, int64_t t_cap, int B,
+                   int Hq, int Hkv, int t0, int T, int D, int group, int bits, int mode, float* part,
+                   hipStream_t stream) {
+  return av_launch_gpw(rec, v_codes, v_meta, t_cap, B, Hq, Hkv, t0, T, D, group, bits, mode, part,
+                       groups_per_wg(B, Hkv, T / group), stream);
+}
+
+// attn.V over the flash-decoding splits: one workgroup per QK^T split
+int av_flash_launch(const uint32_t* rec, const uint32_t* v_codes, const uint16_t* v_meta, int64_t t_cap, int B,
+                    int Hq, int Hkv, int t0, int T, int D, int group, int bits, int mode, float* part,
+                    hipStream_t stream) {
+  return av_launch_gpw(rec, v_codes, v_meta, t_cap, B, Hq, Hkv, t0, T, D, group, bits, mode, part,
+                       flash_split_tokens() / group, stream);
+}
+
+int av_combine_launch(const float* part, int nsplit, int B, int Hq, int D, const OutPair& o, int accumulate,
+                      hipStream_t stream) {
+  const int64_t rows = int64_t(B) * Hq;
+  if (rows == 0) return IQ_OK;
+  av_combine_kernel<<<dim3(unsigned(ceil_div(rows * D, 256))), 256, 0, stream>>>(part, nsplit, Hq, D, rows, o,
+                                                                                accumulate);
+  return launch_status();
+}
+
+}  // namespace iq::detail
+
+extern "C" {
+
+size_t iq_av_workspace_bytes(int B, int Hq, int T, int D, int group) {
+  if (B <= 0 || Hq <= 0 || T <= 0 || !group_ok(group) || !d_ok(D) || T % group) return 0;
+  return detail::av_record_bytes(B, Hq, T, group) + detail::av_part_bytes(B, Hq, T, D, group);
+}
+
+int iq_av_gemv(const void* p, int64_t sp_b, int64_t sp_h, const uint32_t* v_codes, const uint16_t* v_meta,
+               int64_t t_cap, int B, int Hq, int Hkv, int t0, int T, int D, int group, int bits, int mode,
+               float* out32, void* out16, int64_t so_b, int64_t so_h, int accumulate, void* workspace,
+               size_t workspace_bytes, void* stream) {
+  if (int e = check_av(p, v_codes, v_meta, t_cap, B, Hq, Hkv, t0, T, D, group, bits, mode)) return e;
+  IQ_CHECK(out32 || out16, IQ_ERR_NULL);
+  IQ_CHECK(!accumulate || out32, IQ_ERR_NULL);
+  IQ_CHECK(aligned(p, 2), IQ_ERR_ALIGN);
+  hipStream_t st = (hipStream_t)stream;
+  const detail::OutPair o{out32, so_b, so_h, (uint16_t*)out16, so_b, so_h};
+  if (B == 0) return IQ_OK;
+  if (T == 0) return accumulate ? detail::av_combine_launch(nullptr, 0, B, Hq, D, o, 1, st) : IQ_ERR_SHAPE;
+  const size_t rb = detail::av_record_bytes(B, Hq, T, group);
+  IQ_CHECK(workspace && workspace_bytes >= rb + detail::av_part_bytes(B, Hq, T, D, group), IQ_ERR_WORKSPACE);
+  IQ_CHECK(aligned(workspace, 16), IQ_ERR_ALIGN);
+  uint32_t* rec = (uint32_t*)workspace;
+  float* part = (float*)((char*)workspace + rb);
+  if (int e = detail::av_record_launch(p, sp_b, sp_h, B, Hq, Hkv, T, group, bits, rec, st)) return e;
+  if (int e = detail::av_main_launch(rec, v_codes, v_meta, t_cap, B, Hq, Hkv, t0, T, D, group, bits, mode, part, st))
+    return e;
+  return detail::av_combine_launch(part, detail::av_splits(B, Hkv, T, group), B, Hq, D, o, accumulate, st);
+}
+
+}  // extern "C"

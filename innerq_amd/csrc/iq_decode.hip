@@ -1,0 +1,295 @@
+// One decode step of attention over [sink | packed | recent] K and V (gfx950),
+// flash-decoding style.
+//
+// The token axis is cut into
+//   * the fused range: tokens packed in both the K and the V store (the
+//     middle segment of cache.py:235-276 for both), in splits of
+//     flash_split_tokens() tokens.  QK^T runs with its flash epilogue (per
+//     split max m, sum l and fp16 probabilities written as attn.V operand
+//     records), then attn.V writes one unnormalized partial output per split;
+//   * the dense tokens: everything else (fp16 sinks and recent windows, plus
+//     packed tokens of only one of K/V, which are dequantized element by
+//     element).  One workgroup per (batch, query head) runs an online softmax
+//     over them and contributes one extra split.
+// A combine kernel rescales the splits by exp(m_s - max m) and divides by the
+// total sum: softmax(q K^T * scale) V in fp32, written as fp16
+// (TF/models/llama/modeling_llama.py:201-210).  The probabilities that meet V
+// are rounded to fp16 as the reference rounds its softmax output.
+#include "iq_gemv.h"
+
+using namespace iq;
+
+namespace {
+
+constexpr int DCHUNK = 256;  // dense tokens per online-softmax step
+
+struct Seg {
+  const uint16_t* dense;
+  int64_t sb, sh, st;
+  int n, start;  // token count, first token of the segment in the step
+  const uint32_t* codes;
+  const uint16_t* meta;
+  int64_t t_cap;
+  int t0, bits, group, sym;
+};
+
+__device__ __forceinline__ uint32_t field(const uint32_t* w, int bits, int i) {
+  const int bit = bits * i, wi = bit >> 5, o = bit & 31;
+  uint32_t f = w[wi] >> o;
+  if (o + bits > 32) f |= w[wi + 1] << (32 - o);
+  return f & ((1u << bits) - 1u);
+}
+
+__device__ __forceinline__ float deq(uint32_t f, int bits, int sym, const uint16_t* meta, int64_t unit) {
+  if (sym) {
+    const int c = (f >> (bits - 1)) ? int(f) - (1 << bits) : int(f);
+    return __fmul_rn(float(c), h2f(meta[unit]));
+  }
+  const uint32_t sz = reinterpret_cast<const uint32_t*>(meta)[unit];
+  return __fadd_rn(__fmul_rn(float(f), h2f(uint16_t(sz & 0xffffu))), h2f(uint16_t(sz >> 16)));
+}
+
+// element (token t of the step, column d) of a K (channel-grouped store) or V
+// (token-grouped store) segment list
+__device__ float seg_elem(const Seg* s, bool is_k, int64_t b, int64_t kvh, int64_t Hkv, int D, int t, int d,
+                          const uint16_t* norm) {
+#pragma unroll
+  for (int i = 0; i < 3; ++i) {
+    const Seg& g = s[i];
+    if (t < g.start || t >= g.start + g.n) continue;
+    const int tl = t - g.start;
+    if (g.dense) return h2f(g.dense[b * g.sb + kvh * g.sh + tl * g.st + d]);
+    const int st = g.t0 + tl;
+    const int64_t bh = b * Hkv + kvh;
+    const int W = g.group * g.bits / 32;
+    if (is_k) {
+      const int ng = D / g.group;
+      const int64_t unit = ((bh * (g.t_cap / TOKEN_BLOCK) + st / TOKEN_BLOCK) * ng + d / g.group) * TOKEN_BLOCK +
+                           st % TOKEN_BLOCK;
+      float v = deq(field(g.codes + unit * W, g.bits, d % g.group), g.bits, g.sym, g.meta, unit);
+      if (norm) v = __fmul_rn(v, h2f(norm[bh * D + d]));
+      return v;
+    }
+    const int64_t unit = (bh * (g.t_cap / g.group) + st / g.group) * D + d;
+    return deq(field(g.codes + unit * W, g.bits, st % g.group), g.bits, g.sym, g.meta, unit);
+  }
+  return 0.f;
+}
+
+struct DenseArgs {
+  const uint16_t* q;
+  int64_t sqb, sqh;
+  const uint16_t* norm;
+  Seg k[3], v[3];
+  int lo0, hi0, lo1, hi1;  // dense tokens: [lo0, hi0) and [lo1, hi1)
+  int Hq, Hkv, D;
+  float scale;
+  float* ml;  // row block of the extra split: [rows][2]
+  float* o;   // [rows][D]
+};
+
+// One workgroup per (b, hq): online softmax over the dense tokens.
+__global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs a) {
+  __shared__ float qs[128];
+  __shared__ float lg[DCHUNK];
+  __shared__ int tok[DCHUNK];
+  __shared__ float red[4];
+  const int row = blockIdx.x;
+  const int hq = row % a.Hq, b = row / a.Hq;
+  const int kvh = hq / (a.Hq / a.Hkv);
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  if (tid < a.D) qs[tid] = h2f(a.q[b * a.sqb + hq * a.sqh + tid]);
+  const int n0 = a.hi0 - a.lo0, n = n0 + (a.hi1 - a.lo1);
+  float m = -INFINITY, l = 0.f, o = 0.f;  // o: column tid (tid < D)
+  __syncthreads();
+  for (int c0 = 0; c0 < n; c0 += DCHUNK) {
+    const int i = c0 + tid;
+    float x = -INFINITY;
+    int t = -1;
+    if (i < n) {
+      t = i < n0 ? a.lo0 + i : a.lo1 + (i - n0);
+      float s = 0.f;
+      for (int d = 0; d < a.D; ++d) s = fmaf(qs[d], seg_elem(a.k, true, b, kvh, a.Hkv, a.D, t, d, a.norm), s);
+      x = s * a.scale;
+    }
+    float cm = wave_max(x);
+    if (lane == 0) red[wave] = cm;
+    __syncthreads();
+    cm = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    __syncthreads();
+    const float mn = fmaxf(m, cm);
+    const float p = (x == -INFINITY) ? 0.f : __expf(x - mn);
+    lg[tid] = __half2float(__float2half_rn(p));  // the probability that meets V is fp16
+    tok[tid] = t;
+    float cs = wave_sum(p);
+    if (lane == 0) red[wave] = cs;
+    __syncthreads();
+    cs = (red[0] + red[1]) + (red[2] + red[3]);
+    const float alpha = (m == -INFINITY) ? 0.f : __expf(m - mn);
+    l = l * alpha + cs;
+    if (tid < a.D) {
+      float acc = o * alpha;
+      const int cnt = min(DCHUNK, n - c0);
+      for (int j = 0; j < cnt; ++j)
+        acc = fmaf(lg[j], seg_elem(a.v, false, b, kvh, a.Hkv, a.D, tok[j], tid, nullptr), acc);
+      o = acc;
+    }
+    m = mn;
+    __syncthreads();
+  }
+  if (tid == 0) {
+    a.ml[row * 2] = m;
+    a.ml[row * 2 + 1] = l;
+  }
+  if (tid < a.D) a.o[int64_t(row) * a.D + tid] = o;
+}
+
+// out[bq, d] = sum_s e^{m_s - M} o_s[bq, d] / sum_s e^{m_s - M} l_s
+__global__ __launch_bounds__(256) void flash_combine_kernel(const float* __restrict__ ml, const float* __restrict__ part,
+                                                            int nsplit, int64_t rows, int Hq, int D,
+                                                            uint16_t* __restrict__ out, int64_t sob, int64_t soh) {
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= rows * D) return;
+  const int64_t bq = i / D;
+  const int d = int(i % D);
+  float M = -INFINITY;
+  for (int s = 0; s < nsplit; ++s) M = fmaxf(M, ml[(int64_t(s) * rows + bq) * 2]);
+  float L = 0.f, acc = 0.f;
+  for (int s = 0; s < nsplit; ++s) {
+    const float ms = ml[(int64_t(s) * rows + bq) * 2];
+    if (ms == -INFINITY) continue;
+    const float w = __expf(ms - M);
+    L = fmaf(w, ml[(int64_t(s) * rows + bq) * 2 + 1], L);
+    acc = fmaf(w, part[(int64_t(s) * rows + bq) * D + d], acc);
+  }
+  out[(bq / Hq) * sob + (bq % Hq) * soh + d] = __half_as_ushort(__float2half_rn(acc / L));
+}
+
+size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
+
+int nsplit_max(int T) { return int(ceil_div(T, detail::flash_split_tokens())); }
+
+Seg to_seg(const iq_segment& s, int start) {
+  Seg g{};
+  g.dense = (const uint16_t*)s.dense;
+  g.sb = s.s_b; g.sh = s.s_h; g.st = s.s_t;
+  g.n = s.n; g.start = start;
+  g.codes = s.codes; g.meta = s.meta; g.t_cap = s.t_cap; g.t0 = s.t0;
+  g.bits = s.bits; g.group = s.group; g.sym = s.mode == IQ_MODE_SYM;
+  if (s.n && s.codes) g.dense = nullptr;
+  return g;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t iq_decode_workspace_bytes(int B, int Hq, int T, int D) {
+  if (B <= 0 || Hq <= 0 || T <= 0 || !d_ok(D)) return 0;
+  const size_t rows = size_t(B) * Hq;
+  size_t vrec = 0;
+  for (int g : {32, 64, 128}) vrec = std::max(vrec, size_t(B) * Hq * (T / g) * (g / 2 + 2) * 4);
+  const size_t ns = size_t(nsplit_max(T)) + 1;
+  return detail::qk_record_bytes(B, Hq, D) + align256(vrec) + align256(ns * rows * 2 * 4) +
+         align256(ns * rows * D * 4);
+}
+
+int iq_decode_attention(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, const iq_segment* k,
+                        const iq_segment* v, int B, int Hq, int Hkv, int T, int D, float scale, void* out,
+                        int64_t so_b, int64_t so_h, void* workspace, size_t workspace_bytes, void* stream) {
+  IQ_CHECK(q && k && v && out, IQ_ERR_NULL);
+  IQ_CHECK(B >= 0 && T > 0 && Hkv > 0 && Hq > 0, IQ_ERR_SHAPE);
+  IQ_CHECK(d_ok(D) && Hq % Hkv == 0 && nrep_ok(Hq / Hkv), IQ_ERR_SHAPE);
+  for (int s = 0; s < 3; ++s) IQ_CHECK(k[s].n >= 0 && v[s].n >= 0, IQ_ERR_SHAPE);
+  IQ_CHECK(k[0].n + k[1].n + k[2].n == T && v[0].n + v[1].n + v[2].n == T, IQ_ERR_SHAPE);
+  for (int s : {0, 2}) {
+    IQ_CHECK(k[s].n == 0 || k[s].dense, IQ_ERR_NULL);
+    IQ_CHECK(v[s].n == 0 || v[s].dense, IQ_ERR_NULL);
+  }
+  if (k[1].n) {
+    const iq_segment& g = k[1];
+    IQ_CHECK(g.codes && g.meta, IQ_ERR_NULL);
+    if (int e = check_common(g.bits, g.group, g.mode)) return e;
+    IQ_CHECK(D % g.group == 0, IQ_ERR_GROUP);
+    IQ_CHECK(g.t_cap % TOKEN_BLOCK == 0 && g.t0 % TOKEN_BLOCK == 0 && g.t0 >= 0, IQ_ERR_ALIGN);
+    IQ_CHECK(int64_t(g.t0) + g.n <= g.t_cap, IQ_ERR_RANGE);
+    IQ_CHECK(aligned(g.codes, 16) && aligned(g.meta, 4), IQ_ERR_ALIGN);
+  }
+  if (v[1].n) {
+    const iq_segment& g = v[1];
+    IQ_CHECK(g.codes && g.meta, IQ_ERR_NULL);
+    if (int e = check_common(g.bits, g.group, g.mode)) return e;
+    IQ_CHECK(g.n % g.group == 0 && g.t0 % g.group == 0 && g.t0 >= 0 && g.t_cap % g.group == 0, IQ_ERR_GROUP);
+    IQ_CHECK(int64_t(g.t0) + g.n <= g.t_cap, IQ_ERR_RANGE);
+    IQ_CHECK(aligned(g.codes, 16) && aligned(g.meta, 8), IQ_ERR_ALIGN);
+  }
+  IQ_CHECK(workspace && workspace_bytes >= iq_decode_workspace_bytes(B, Hq, T, D), IQ_ERR_WORKSPACE);
+  IQ_CHECK(aligned(workspace, 256), IQ_ERR_ALIGN);
+  if (B == 0) return IQ_OK;
+
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t rows = int64_t(B) * Hq;
+  char* ws = (char*)workspace;
+  uint32_t* qrec = (uint32_t*)ws;
+  ws += detail::qk_record_bytes(B, Hq, D);
+  size_t vrec_bytes = 0;
+  for (int g : {32, 64, 128}) vrec_bytes = std::max(vrec_bytes, size_t(B) * Hq * (T / g) * (g / 2 + 2) * 4);
+  uint32_t* vrec = (uint32_t*)ws;
+  ws += align256(vrec_bytes);
+  const size_t ns_cap = size_t(nsplit_max(T)) + 1;
+  float* ml = (float*)ws;
+  ws += align256(ns_cap * rows * 2 * 4);
+  float* part = (float*)ws;
+
+  // fused range: packed in both K and V, aligned to K blocks and V groups
+  const int ks = k[0].n, vs = v[0].n;
+  const int lo = std::max(ks, vs), hi = std::min(ks + k[1].n, vs + v[1].n);
+  int a0 = -1, c = 0;
+  if (k[1].n && v[1].n && hi > lo) {
+    const int vg = v[1].group;
+    for (int t = lo; t < std::min(hi, lo + TOKEN_BLOCK * vg); ++t)
+      if ((k[1].t0 + t - ks) % TOKEN_BLOCK == 0 && (v[1].t0 + t - vs) % vg == 0) {
+        a0 = t;
+        break;
+      }
+    if (a0 >= 0) {
+      c = hi - a0;
+      c -= c % vg;
+      if (detail::flash_split_tokens() % vg) c = 0;
+    }
+  }
+  if (c <= 0) { a0 = 0; c = 0; }
+  const int nsf = c ? int(ceil_div(c, detail::flash_split_tokens())) : 0;
+
+  if (c) {
+    const iq_segment& kg = k[1];
+    const iq_segment& vg = v[1];
+    if (int e = detail::qk_record_launch(q, sq_b, sq_h, norm, B, Hq, Hkv, D, kg.group, kg.bits, qrec, st)) return e;
+    const detail::FlashOut f{ml, vrec, vg.bits, vg.group};
+    if (int e = detail::qk_flash_launch(qrec, kg.codes, kg.meta, kg.t_cap, B, Hq, Hkv, kg.t0 + (a0 - ks), c, D,
+                                        kg.group, kg.bits, kg.mode, scale, f, st))
+      return e;
+    if (int e = detail::av_flash_launch(vrec, vg.codes, vg.meta, vg.t_cap, B, Hq, Hkv, vg.t0 + (a0 - vs), c, D,
+                                        vg.group, vg.bits, vg.mode, part, st))
+      return e;
+  }
+  // dense tokens -> extra split nsf
+  DenseArgs da{};
+  da.q = (const uint16_t*)q; da.sqb = sq_b; da.sqh = sq_h; da.norm = (const uint16_t*)norm;
+  int start = 0;
+  for (int s = 0; s < 3; ++s) { da.k[s] = to_seg(k[s], start); start += k[s].n; }
+  start = 0;
+  for (int s = 0; s < 3; ++s) { da.v[s] = to_seg(v[s], start); start += v[s].n; }
+  da.lo0 = 0; da.hi0 = c ? a0 : T;
+  da.lo1 = c ? a0 + c : T; da.hi1 = T;
+  da.Hq = Hq; da.Hkv = Hkv; da.D = D; da.scale = scale;
+  da.ml = ml + int64_t(nsf) * rows * 2;
+  da.o = part + int64_t(nsf) * rows * D;
+  dense_attn_kernel<<<dim3(unsigned(rows)), 256, 0, st>>>(da);
+  if (int e = launch_status()) return e;
+  flash_combine_kernel<<<dim3(unsigned(ceil_div(rows * D, 256))), 256, 0, st>>>(ml, part, nsf + 1, rows, Hq, D,
+                                                                                 (uint16_t*)out, so_b, so_h);
+  return launch_status();
+}
+
+}  // extern "C"

@@ -225,8 +225,10 @@ def qk_gemv(q: torch.Tensor, k: PackedStore, scale: float, norm: Optional[torch.
     assert out.stride(-1) == 1 and out.dtype == torch.float32
     if norm is not None:
         norm = norm.reshape(k.B, k.H, D).contiguous()
+    ws = _workspace(q.device, _lib.lib().iq_qk_workspace_bytes(B, Hq, D))
     call("iq_qk_gemv", _p(q), q.stride(0), q.stride(1), _p(norm), _p(k.codes), _p(k.meta), k.t_cap, B, Hq, k.H, t0,
-         T, D, k.group, k.bits, k.mode, float(scale), _p(out), out.stride(0), out.stride(1), _stream(q.device))
+         T, D, k.group, k.bits, k.mode, float(scale), _p(out), out.stride(0), out.stride(1), _p(ws), ws.numel(),
+         _stream(q.device))
     return out
 
 

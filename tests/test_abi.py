@@ -58,7 +58,8 @@ def test_store_sizes():
 
 def qk_args(**kw):
     a = dict(q=FAKE, sqb=1024, sqh=128, norm=None, kc=FAKE, km=FAKE, t_cap=1024, B=1, Hq=32, Hkv=8, t0=0,
-             T=512, D=128, G=32, bits=4, mode=0, scale=1.0, out=FAKE, sob=1, soh=1, stream=None)
+             T=512, D=128, G=32, bits=4, mode=0, scale=1.0, out=FAKE, sob=1, soh=1, ws=FAKE, wsb=1 << 20,
+             stream=None)
     a.update(kw)
     return list(a.values())
 
@@ -68,7 +69,8 @@ def qk_args(**kw):
     (dict(bits=5), -2), (dict(bits=1), -2), (dict(G=48), -3), (dict(G=256), -3),
     (dict(mode=3), -7), (dict(D=96), -4), (dict(Hkv=5), -4), (dict(Hq=48), -4),
     (dict(T=-1), -4), (dict(t0=32), -5), (dict(t_cap=1000), -5), (dict(T=1100), -8),
-    (dict(kc=ctypes.c_void_p(0x1004)), -5),
+    (dict(kc=ctypes.c_void_p(0x1004)), -5), (dict(ws=None), -6), (dict(wsb=64), -6),
+    (dict(ws=ctypes.c_void_p(0x1008)), -5),
 ])
 def test_qk_rejects(kw, err):
     assert _lib.lib().iq_qk_gemv(*qk_args(**kw)) == err
@@ -94,9 +96,10 @@ def test_av_rejects(kw, err):
 def test_workspace_queries():
     lib = _lib.lib()
     n = lib.iq_av_workspace_bytes(8, 32, 32768, 128, 32)
-    assert n > 0 and n % (8 * 32 * 128 * 4) == 0
+    assert n >= 8 * 32 * 32768 * 2 + 8 * 32 * 128 * 4
+    assert lib.iq_qk_workspace_bytes(8, 32, 128) >= 8 * 32 * (64 + 8) * 4
     assert lib.iq_av_workspace_bytes(8, 32, 32768, 96, 32) == 0
-    assert lib.iq_decode_workspace_bytes(8, 32, 32768, 128) >= 8 * 32 * 32768 * 6
+    assert lib.iq_decode_workspace_bytes(8, 32, 32768, 128) >= 8 * 32 * 32768 * 2  # fp16 probability records
     assert lib.iq_decode_workspace_bytes(0, 32, 32768, 128) == 0
 
 

@@ -324,3 +324,70 @@ def test_decode_attention_all_quantized_and_all_dense():
     got = ops.decode_attention(f16t(q), f16t(kx), None, None, f16t(vx), None, None, D ** -0.5).cpu().numpy()
     ref = A.decode_attention(q, kx.astype(np.float32), vx.astype(np.float32), D ** -0.5, None)
     assert A.rel_err(got.astype(np.float64), ref) < TOL
+
+
+def _decode_case(B, Hkv, nrep, D, kseg, vseg, kfmt, vfmt, seed, norm=False):
+    """kseg/vseg = (sink, packed, recent) token counts; fmt = (bits, group, mode)."""
+    T = sum(kseg)
+    assert sum(vseg) == T
+    kx = synth.kv_tensor(B, Hkv, T, D, seed=seed, n_out=4, factor=8.0)
+    vx = synth.kv_tensor(B, Hkv, T, D, seed=seed + 1, n_out=4, factor=8.0)
+    q = synth.normal((B, Hkv * nrep, D), seed=seed + 2).astype(np.float16)
+    ks, kq, kr = kseg
+    vs, vq, vr = vseg
+    kb, kg, km = kfmt
+    vb, vg, vm = vfmt
+    nrm = None
+    kpart = kx[:, :, ks:ks + kq]
+    if norm:
+        nrm = np.sqrt(np.abs(kpart).max(axis=-2, keepdims=True).astype(np.float32)).astype(np.float16)
+    kst = ops.PackedStore("channel", B, Hkv, D, kg, kb, km, DEV)
+    kst.append(f16t(kpart), norm=None if nrm is None else f16t(nrm))
+    vst = ops.PackedStore("token", B, Hkv, D, vg, vb, vm, DEV)
+    vst.append(f16t(vx[:, :, vs:vs + vq]))
+    kxt, vxt = f16t(kx), f16t(vx)
+    got = ops.decode_attention(f16t(q), kxt[:, :, :ks] if ks else None, kst if kq else None,
+                               kxt[:, :, ks + kq:] if kr else None, vxt[:, :, :vs] if vs else None,
+                               vst if vq else None, vxt[:, :, vs + vq:] if vr else None, D ** -0.5,
+                               norm=None if nrm is None else f16t(nrm)).cpu().numpy().astype(np.float64)
+    kin = kpart if nrm is None else (kpart.astype(np.float32) / nrm.astype(np.float32)).astype(np.float16)
+    c, s, z = oracle_q(kin, kb, kg, km, "channel")
+    kd = oracle_deq(c, s, z, kg, km, "channel")
+    if nrm is not None:
+        kd = kd * nrm.astype(np.float32)
+    kd = np.concatenate([kx[:, :, :ks].astype(np.float32), kd, kx[:, :, ks + kq:].astype(np.float32)], axis=2)
+    c, s, z = oracle_q(vx[:, :, vs:vs + vq], vb, vg, vm, "token")
+    vd = np.concatenate([vx[:, :, :vs].astype(np.float32), oracle_deq(c, s, z, vg, vm, "token"),
+                         vx[:, :, vs + vq:].astype(np.float32)], axis=2)
+    ref = A.decode_attention(q, kd, vd, D ** -0.5, p_dtype=None)
+    return A.rel_err(got, ref)
+
+
+@pytest.mark.parametrize("kseg,vseg", [
+    ((4, 64 * 20, 100), (0, 32 * 41, 72)),      # different sinks, V drained, fused range shifted
+    ((32, 64 * 9, 96), (32, 32 * 19, 64)),      # innerq preset shape, partial last split
+    ((0, 64 * 3, 7), (0, 32 * 4, 71)),          # K packed past V's packed range
+    ((3, 0, 200), (3, 64, 136)),                # no packed K: everything dense
+])
+def test_decode_attention_fused_and_dense_ranges(kseg, vseg):
+    err = _decode_case(2, 2, 4, 128, kseg, vseg, (4, 32, "asymmetric"), (4, 32, "asymmetric"), seed=sum(kseg))
+    assert err < TOL
+
+
+@pytest.mark.parametrize("kfmt,vfmt", [((3, 32, "symmetric"), (3, 32, "symmetric")),
+                                       ((2, 64, "asymmetric"), (4, 64, "symmetric")),
+                                       ((4, 128, "asymmetric"), (2, 128, "asymmetric"))])
+def test_decode_attention_formats_and_norm(kfmt, vfmt):
+    G = max(kfmt[1], vfmt[1])
+    kseg = (32, 64 * 24, 96)
+    vq = (64 * 24 + 96) // G * G - G
+    vseg = (32, vq, 64 * 24 + 96 - vq)
+    err = _decode_case(1, 2, 4, 128, kseg, vseg, kfmt, vfmt, seed=5, norm=True)
+    assert err < TOL
+
+
+@pytest.mark.parametrize("nrep,D", [(1, 128), (8, 64), (2, 128)])
+def test_decode_attention_gqa_shapes(nrep, D):
+    err = _decode_case(2, 2, nrep, D, (0, 64 * 17, 128), (0, 32 * 34, 128), (4, 32, "asymmetric"),
+                       (4, 32, "asymmetric"), seed=nrep * D)
+    assert err < TOL
