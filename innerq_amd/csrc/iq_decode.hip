@@ -145,24 +145,46 @@ __global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs a) {
 }
 
 // out[bq, d] = sum_s e^{m_s - M} o_s[bq, d] / sum_s e^{m_s - M} l_s
+// One workgroup per row bq: the split weights are computed once into LDS, then
+// each column's partials are summed with independent (unrolled) loads.
+constexpr int MAXSPLIT = 1024;
 __global__ __launch_bounds__(256) void flash_combine_kernel(const float* __restrict__ ml, const float* __restrict__ part,
                                                             int nsplit, int64_t rows, int Hq, int D,
                                                             uint16_t* __restrict__ out, int64_t sob, int64_t soh) {
-  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
-  if (i >= rows * D) return;
-  const int64_t bq = i / D;
-  const int d = int(i % D);
-  float M = -INFINITY;
-  for (int s = 0; s < nsplit; ++s) M = fmaxf(M, ml[(int64_t(s) * rows + bq) * 2]);
-  float L = 0.f, acc = 0.f;
-  for (int s = 0; s < nsplit; ++s) {
+  __shared__ float wgt[MAXSPLIT];
+  __shared__ float red[4];
+  const int64_t bq = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  float mx = -INFINITY;
+  for (int s = tid; s < nsplit; s += 256) mx = fmaxf(mx, ml[(int64_t(s) * rows + bq) * 2]);
+  mx = wave_max(mx);
+  if (lane == 0) red[wave] = mx;
+  __syncthreads();
+  const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  __syncthreads();
+  float L = 0.f;
+  for (int s = tid; s < nsplit; s += 256) {
     const float ms = ml[(int64_t(s) * rows + bq) * 2];
-    if (ms == -INFINITY) continue;
-    const float w = __expf(ms - M);
+    const float w = ms == -INFINITY ? 0.f : __expf(ms - M);
+    wgt[s] = w;
     L = fmaf(w, ml[(int64_t(s) * rows + bq) * 2 + 1], L);
-    acc = fmaf(w, part[(int64_t(s) * rows + bq) * D + d], acc);
   }
-  out[(bq / Hq) * sob + (bq % Hq) * soh + d] = __half_as_ushort(__float2half_rn(acc / L));
+  L = wave_sum(L);
+  if (lane == 0) red[wave] = L;
+  __syncthreads();
+  L = (red[0] + red[1]) + (red[2] + red[3]);
+  for (int d = tid; d < D; d += 256) {
+    const float* pc = part + bq * D + d;
+    float acc[4] = {0.f, 0.f, 0.f, 0.f};
+    int s = 0;
+    for (; s + 4 <= nsplit; s += 4) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) acc[u] = fmaf(wgt[s + u], pc[int64_t(s + u) * rows * D], acc[u]);
+    }
+    for (; s < nsplit; ++s) acc[0] = fmaf(wgt[s], pc[int64_t(s) * rows * D], acc[0]);
+    const float v = ((acc[0] + acc[1]) + (acc[2] + acc[3])) / L;
+    out[(bq / Hq) * sob + (bq % Hq) * soh + d] = __half_as_ushort(__float2half_rn(v));
+  }
 }
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
@@ -285,10 +307,15 @@ int iq_decode_attention(const void* q, int64_t sq_b, int64_t sq_h, const void* n
   da.Hq = Hq; da.Hkv = Hkv; da.D = D; da.scale = scale;
   da.ml = ml + int64_t(nsf) * rows * 2;
   da.o = part + int64_t(nsf) * rows * D;
-  dense_attn_kernel<<<dim3(unsigned(rows)), 256, 0, st>>>(da);
-  if (int e = launch_status()) return e;
-  flash_combine_kernel<<<dim3(unsigned(ceil_div(rows * D, 256))), 256, 0, st>>>(ml, part, nsf + 1, rows, Hq, D,
-                                                                                 (uint16_t*)out, so_b, so_h);
+  const int n_dense = (da.hi0 - da.lo0) + (da.hi1 - da.lo1);
+  if (n_dense > 0) {
+    dense_attn_kernel<<<dim3(unsigned(rows)), 256, 0, st>>>(da);
+    if (int e = launch_status()) return e;
+  }
+  const int nsplit = nsf + (n_dense > 0 ? 1 : 0);
+  IQ_CHECK(nsplit <= MAXSPLIT, IQ_ERR_SHAPE);
+  flash_combine_kernel<<<dim3(unsigned(rows)), 256, 0, st>>>(ml, part, nsplit, rows, Hq, D, (uint16_t*)out, so_b,
+                                                              so_h);
   return launch_status();
 }
 

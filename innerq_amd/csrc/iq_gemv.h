@@ -133,7 +133,9 @@ __device__ __forceinline__ void chunk_dot(const uint32_t (&w)[NB][W], cptr_u32 r
       ...);
 #pragma unroll
   for (int h = 0; h < NREP; ++h) {
-    const cptr_u32 r = launder(rec + h * NP + K0, dv[0][h == 0 ? 0 : h - 1]);
+    // head h's pairs may load once head h-2 is done: two heads of operands
+    // (32 SGPRs) in flight, so the scalar-load latency overlaps head h-1's dots
+    const cptr_u32 r = launder(rec + h * NP + K0, dv[0][h < 2 ? 0 : h - 2]);
     (
         [&] {
           const h2_t op = __builtin_bit_cast(h2_t, r[K]);

@@ -106,26 +106,23 @@ __global__ __launch_bounds__(WG) void qk_kernel(QKArgs a) {
   if (wblk >= a.nblk && !a.flash) return;  // the flash epilogue needs every wave at its barriers
   const int nb = max(0, min(BPW, a.nblk - wblk));
 
-  const int64_t blkbase = int64_t(bh) * a.cap_blocks + a.blk0 + wblk;
+  const int64_t blkbase = int64_t(bh) * a.cap_blocks + a.blk0;
   const uint32_t* kcb = a.kc + blkbase * (NG * TOKEN_BLOCK * W);
   const uint16_t* kmb = a.km + blkbase * (NG * TOKEN_BLOCK * M);
 
   // words of group g for the wave's blocks; the next group's are prefetched
   uint32_t w[BPW][W];
   uint32_t m[BPW];
+  // Blocks past the end of the range (tail waves) re-read the range's last
+  // block: in-bounds loads whose results are masked out, and no branches.
   auto load = [&](int g) {
 #pragma unroll
     for (int j = 0; j < BPW; ++j) {
-      if (j < nb) {
-        const int64_t unit = (int64_t(j) * NG + g) * TOKEN_BLOCK + lane;
-        load_words<W>(kcb + unit * W, w[j]);
-        if constexpr (SYM) m[j] = kmb[unit];
-        else m[j] = reinterpret_cast<const uint32_t*>(kmb)[unit];
-      } else {
-#pragma unroll
-        for (int x = 0; x < W; ++x) w[j][x] = 0u;
-        m[j] = 0u;
-      }
+      const int blk = min(wblk + j, a.nblk - 1);
+      const int64_t unit = (int64_t(blk) * NG + g) * TOKEN_BLOCK + lane;
+      load_words<W>(kcb + unit * W, w[j]);
+      if constexpr (SYM) m[j] = kmb[unit];
+      else m[j] = reinterpret_cast<const uint32_t*>(kmb)[unit];
     }
   };
   load(0);
