@@ -5,9 +5,12 @@
 // Mapping: a workgroup of four waves owns a contiguous range of token groups
 // of one (batch, KV head) (split-T); wave w takes every fourth group of the
 // range, two groups per step with the next two prefetched.  Lane = head_dim
-// column (two columns at D=128), so a wave reads a group's D*G*b/8 code bytes
-// contiguously.  The probabilities come as operand records (pairs in plan
-// order, per-group bias sums and plain sums; iq_gemv.h) through scalar loads.
+// column d = lane + 64 e (two columns at D=128), so each wave load covers 64
+// consecutive (group, column) units.  The dot products run on the matrix
+// cores: eight v_mfma_f32_4x4x4f16 per group and column set, B = four unpacked
+// codes of the lane's column, A = four probabilities of head 4q + lane%4 from
+// the probability operand record (iq_gemv.h); the VALU unpacks codes and
+// applies scale and zero point.
 // The four waves' partial sums are reduced in LDS in a fixed order, each
 // workgroup writes one fp32 partial per split, and a second kernel sums the
 // splits in split order: no atomics, deterministic results.
@@ -67,7 +70,6 @@ __global__ __launch_bounds__(WG) void av_kernel(AVArgs a) {
   const int split = blockIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
-  const int d0 = lane * DPL;
   const int gl0 = split * a.gpw;
   const int ng = min(a.gpw, a.ngroups - gl0);
   const int cnt = ng > wave ? (ng - wave + NWAVES - 1) / NWAVES : 0;
@@ -82,28 +84,17 @@ __global__ __launch_bounds__(WG) void av_kernel(AVArgs a) {
 
   uint32_t w[NB][DPL][W];
   uint32_t m[NB][DPL];
+  // column d = lane + 64 e: every wave load is 64 consecutive (group, d) units
   auto load = [&](int i0) {
 #pragma unroll
     for (int u = 0; u < NB; ++u) {
       if (i0 + u < cnt) {
-        const int64_t unit = (gbase + wave + NWAVES * (i0 + u)) * D + d0;
-        load_words<DPL * W>(a.vc + unit * W, &w[u][0][0]);
-        if constexpr (SYM) {
-          if constexpr (DPL == 2) {
-            const uint32_t mm = *reinterpret_cast<const uint32_t*>(a.vm + unit);
-            m[u][0] = mm & 0xffffu;
-            m[u][1] = mm >> 16;
-          } else {
-            m[u][0] = a.vm[unit];
-          }
-        } else {
-          if constexpr (DPL == 2) {
-            const uint2 mm = *reinterpret_cast<const uint2*>(a.vm + unit * 2);
-            m[u][0] = mm.x;
-            m[u][1] = mm.y;
-          } else {
-            m[u][0] = reinterpret_cast<const uint32_t*>(a.vm)[unit];
-          }
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) {
+          const int64_t unit = (gbase + wave + NWAVES * (i0 + u)) * D + lane + 64 * e;
+          load_words<W>(a.vc + unit * W, w[u][e]);
+          if constexpr (SYM) m[u][e] = a.vm[unit];
+          else m[u][e] = reinterpret_cast<const uint32_t*>(a.vm)[unit];
         }
       }
     }
@@ -129,14 +120,14 @@ __global__ __launch_bounds__(WG) void av_kernel(AVArgs a) {
 #pragma unroll
           for (int e = 0; e < DPL; ++e) to_offset_binary<BITS>(cw[u][e], W);
         }
-        float dv[DPL][NREP];
+        constexpr int NQ = (NREP + 3) / 4;
+        f4_t dv[DPL][NQ];
 #pragma unroll
-        for (int h = 0; h < NREP; ++h) {
-          const float beta = rec_f32(rec, NP * NREP + h);
+        for (int e = 0; e < DPL; ++e)
 #pragma unroll
-          for (int e = 0; e < DPL; ++e) dv[e][h] = -beta;
-        }
-        group_dot_rec<BITS, G, NREP, DPL>(cw[u], rec, dv);
+          for (int q = 0; q < NQ; ++q) dv[e][q] = f4_t{0.f, 0.f, 0.f, 0.f};
+        group_mfma<BITS, G, NREP, DPL>(cw[u], a.rec + (int64_t(bh) * a.ngroups + gl0 + wave + NWAVES * (i + u)) * RD,
+                                       lane & 3, dv);
 #pragma unroll
         for (int e = 0; e < DPL; ++e) {
           const float s = h2f(uint16_t(cm[u][e] & 0xffffu));
@@ -144,7 +135,7 @@ __global__ __launch_bounds__(WG) void av_kernel(AVArgs a) {
 #pragma unroll
           for (int h = 0; h < NREP; ++h) {
             const float ps = rec_f32(rec, NP * NREP + NREP + h);
-            acc[h][e] = fmaf(s, dv[e][h], fmaf(z, ps, acc[h][e]));
+            acc[h][e] = fmaf(s, dv[e][h / 4][h % 4], fmaf(z, ps, acc[h][e]));
           }
         }
       }
@@ -154,7 +145,7 @@ __global__ __launch_bounds__(WG) void av_kernel(AVArgs a) {
 #pragma unroll
     for (int h = 0; h < NREP; ++h)
 #pragma unroll
-      for (int e = 0; e < DPL; ++e) red[wave - 1][h][d0 + e] = acc[h][e];
+      for (int e = 0; e < DPL; ++e) red[wave - 1][h][lane + 64 * e] = acc[h][e];
   }
   __syncthreads();
   if (wave == 0) {
@@ -165,8 +156,8 @@ __global__ __launch_bounds__(WG) void av_kernel(AVArgs a) {
       for (int e = 0; e < DPL; ++e) {
         float v = acc[h][e];
 #pragma unroll
-        for (int r = 0; r < NWAVES - 1; ++r) v += red[r][h][d0 + e];
-        dst[h * D + d0 + e] = v;
+        for (int r = 0; r < NWAVES - 1; ++r) v += red[r][h][lane + 64 * e];
+        dst[h * D + lane + 64 * e] = v;
       }
   }
 }

@@ -90,14 +90,22 @@ __device__ __forceinline__ uint32_t window(const uint32_t* w) {
   }
 }
 
+// A constant held in a VGPR and opaque to constant folding.  The asm is not
+// volatile, so identical constants are CSE'd and hoisted out of loops.
+__device__ __forceinline__ uint32_t vgpr_const(uint32_t c) {
+  asm("" : "+v"(c));
+  return c;
+}
+
 // (x & m) | c in one v_and_or_b32.  gfx9 VOP3 has no literal operand, so the
-// mask and the exponent pattern are passed in VGPRs (materialized once per
-// kernel); written with VALU inline asm because the compiler otherwise
-// splits it into v_and_b32 + v_or_b32 with literals.
+// mask and the exponent pattern live in VGPRs (materialized once per kernel);
+// with literal operands the compiler would split it into v_and_b32 +
+// v_or_b32.  The instruction itself must come from the compiler, not from
+// inline asm: its result feeds MFMA source operands, and the required VALU
+// write -> MFMA read wait states are only inserted for instructions the
+// compiler's hazard recognizer can see.
 __device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t c) {
-  uint32_t r;
-  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(m), "v"(c));
-  return r;
+  return (x & vgpr_const(m)) | vgpr_const(c);
 }
 
 template <int BITS, int K>
@@ -105,6 +113,13 @@ __device__ __forceinline__ h2_t extract_pair(const uint32_t* w) {
   constexpr int S = Plan<BITS>::S[K];
   const uint32_t x = and_or(window<BITS, S>(w), mask_of<BITS>(K), magic_of<BITS>(K));
   return __builtin_bit_cast(h2_t, x);
+}
+
+// The pair's two codes as exact fp16 integers (bias removed).
+template <int BITS, int K>
+__device__ __forceinline__ h2_t extract_codes(const uint32_t* w) {
+  constexpr h2_t bias = {_Float16(bias_a<BITS>(K)), _Float16(bias_c<BITS>(K))};
+  return extract_pair<BITS, K>(w) - bias;
 }
 
 __device__ __forceinline__ float dot2(h2_t a, h2_t b, float c) {

@@ -170,6 +170,93 @@ __device__ __forceinline__ void group_dot_rec(const uint32_t (&w)[NB][G * BITS /
 
 __device__ __forceinline__ float rec_f32(cptr_u32 rec, int i) { return __builtin_bit_cast(float, rec[i]); }
 
+// ---------------------------------------------------------------------------
+// Matrix-core group dot (v_mfma_f32_4x4x4_16b_f16).
+//
+// The instruction runs 16 independent 4x4x4 products; block b = lane / 4,
+// and lane 4b+i supplies row i of A and column i of B (the four fp16 of its
+// operand, k = element index) and receives column i of D, rows 0..3 in its
+// four result registers (verified on gfx950 with lane-coded operands).  With
+// B = four unpacked codes of the lane's own token / column and A = the
+// operand pairs of head 4q + (lane & 3), one instruction gives every lane the
+// dot products of four heads over four codes: 8 instructions cover a 32-code
+// group, and the VALU only unpacks codes and applies scale / zero point.
+//
+// The B operand is the code pair itself, not the biased magic-number pair:
+// with a bias of up to 1024 per code, partial sums reach ~1e4 and cancel
+// back to ~1, and the MFMA's fp32 accumulation loses ~1e-3 of the result at
+// G = 128.  Subtracting the bias pair first (one v_pk_add_f16, exact because
+// both operands are integers below 2048) keeps every partial sum small.
+// ---------------------------------------------------------------------------
+typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
+typedef float f4_t __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ f4_t mfma4(h4_t a, h4_t b, f4_t c) {
+  return __builtin_amdgcn_mfma_f32_4x4x4f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ h4_t cat_h2(h2_t lo, h2_t hi) { return __builtin_shufflevector(lo, hi, 0, 1, 2, 3); }
+
+template <int BITS, int W, int NREP, int NB, int K0, int... K>
+__device__ __forceinline__ void mfma_chunk(const uint32_t (&w)[NB][W], const uint32_t* __restrict__ rec, int NP,
+                                           int hl, f4_t (&dv)[NB][(NREP + 3) / 4],
+                                           std::integer_sequence<int, K...>) {
+  constexpr int NPS = Plan<BITS>::NPAIR;
+  constexpr int SBW = Plan<BITS>::WORDS;
+  constexpr int CH = sizeof...(K);
+  constexpr int NQ = (NREP + 3) / 4;
+  // A rows: pairs [K0, K0+CH) of head 4q + hl (heads past NREP read as zero)
+  uint32_t av[NQ][CH];
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    const int h = 4 * q + hl;
+    if constexpr (NREP % 4 == 0) {
+      load_words<CH>(rec + h * NP + K0, av[q]);
+    } else {
+      load_words<CH>(rec + min(h, NREP - 1) * NP + K0, av[q]);
+#pragma unroll
+      for (int k = 0; k < CH; ++k) av[q][k] = h < NREP ? av[q][k] : 0u;
+    }
+  }
+  h2_t x[NB][CH];
+  (
+      [&] {
+#pragma unroll
+        for (int j = 0; j < NB; ++j) x[j][K] = extract_codes<BITS, (K0 + K) % NPS>(&w[j][((K0 + K) / NPS) * SBW]);
+      }(),
+      ...);
+#pragma unroll
+  for (int st = 0; st < CH / 2; ++st) {
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const h4_t a4 = cat_h2(__builtin_bit_cast(h2_t, av[q][2 * st]), __builtin_bit_cast(h2_t, av[q][2 * st + 1]));
+#pragma unroll
+      for (int j = 0; j < NB; ++j) dv[j][q] = mfma4(a4, cat_h2(x[j][2 * st], x[j][2 * st + 1]), dv[j][q]);
+    }
+  }
+}
+
+template <int BITS, int G, int NREP, int NB, int C, int NCH>
+__device__ __forceinline__ void mfma_chunks(const uint32_t (&w)[NB][G * BITS / 32], const uint32_t* __restrict__ rec,
+                                            int hl, f4_t (&dv)[NB][(NREP + 3) / 4]) {
+  if constexpr (C < NCH) {
+    constexpr int CH = (G / 2) / NCH;
+    mfma_chunk<BITS, G * BITS / 32, NREP, NB, C * CH>(w, rec, G / 2, hl, dv, std::make_integer_sequence<int, CH>{});
+    mfma_chunks<BITS, G, NREP, NB, C + 1, NCH>(w, rec, hl, dv);
+  }
+}
+
+// dv[j][q][i] += sum over the group's pairs of opnd(head 4q+i) . codes(set j)
+// (unbiased codes: no -beta start value),
+// rec = this group's operand record (vector-loaded per lane: row = hl).
+template <int BITS, int G, int NREP, int NB>
+__device__ __forceinline__ void group_mfma(const uint32_t (&w)[NB][G * BITS / 32], const uint32_t* __restrict__ rec,
+                                           int hl, f4_t (&dv)[NB][(NREP + 3) / 4]) {
+  constexpr int NP = G / 2;
+  constexpr int NCH = NP <= 16 ? 1 : NP / 16;
+  mfma_chunks<BITS, G, NREP, NB, 0, NCH>(w, rec, hl, dv);
+}
+
 // ---- host-side launchers shared between translation units -----------------
 namespace detail {
 int qk_record_launch(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, int B, int Hq, int Hkv, int D,

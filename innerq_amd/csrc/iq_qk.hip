@@ -8,9 +8,11 @@
 // K store keeps a block's 64 tokens contiguous per group, so every load is a
 // 1 KiB coalesced wave access for 4-bit G=32) while group g+1's are in
 // flight.  The n_rep query heads sharing the KV head use the same unpacked
-// pairs, with the query pairs coming from the scalar register file (operand
-// records, iq_gemv.h).  A workgroup (four waves) covers one split of
-// 4*QK_BPW*64 tokens.
+// codes: each group is eight v_mfma_f32_4x4x4f16 per four heads, B = four
+// unpacked codes of the lane's token, A = four query values of head
+// 4q + lane%4 from the query operand record (iq_gemv.h), so the VALU only
+// unpacks codes and applies scale and zero point.  A workgroup (four waves)
+// covers one split of 4*QK_BPW*64 tokens.
 //
 // Epilogue, chosen per launch:
 //   logits  write scale * logit (fp32) for every token;
@@ -152,14 +154,13 @@ __global__ __launch_bounds__(WG) void qk_kernel(QKArgs a) {
 #pragma unroll
       for (int j = 0; j < BPW; ++j) to_offset_binary<BITS>(cw[j], W);
     }
-    float dv[BPW][NREP];
+    constexpr int NQ = (NREP + 3) / 4;
+    f4_t dv[BPW][NQ];
 #pragma unroll
-    for (int h = 0; h < NREP; ++h) {
-      const float beta = rec_f32(rec, NP * NREP + h);
+    for (int j = 0; j < BPW; ++j)
 #pragma unroll
-      for (int j = 0; j < BPW; ++j) dv[j][h] = -beta;
-    }
-    group_dot_rec<BITS, G, NREP, BPW>(cw, rec, dv);
+      for (int q = 0; q < NQ; ++q) dv[j][q] = f4_t{0.f, 0.f, 0.f, 0.f};
+    group_mfma<BITS, G, NREP, BPW>(cw, a.rec + (int64_t(bh) * NG + g) * RD, lane & 3, dv);
 #pragma unroll
     for (int j = 0; j < BPW; ++j) {
       const float s = h2f(uint16_t(cm[j] & 0xffffu));
@@ -167,7 +168,7 @@ __global__ __launch_bounds__(WG) void qk_kernel(QKArgs a) {
 #pragma unroll
       for (int h = 0; h < NREP; ++h) {
         const float qs = rec_f32(rec, NP * NREP + NREP + h);
-        acc[j][h] = fmaf(s, dv[j][h], fmaf(z, qs, acc[j][h]));
+        acc[j][h] = fmaf(s, dv[j][h / 4][h % 4], fmaf(z, qs, acc[j][h]));
       }
     }
   }
