@@ -20,7 +20,7 @@ using namespace iq;
 
 namespace {
 
-// one thread per (b, kvh, g, h): probability pairs in plan order + sums
+// one thread per (b, kvh, g, h): probability pairs in plan order and their sum
 template <int BITS, int G, int NREP>
 __global__ __launch_bounds__(256) void av_record_kernel(const uint16_t* __restrict__ p, int64_t spb, int64_t sph,
                                                         int B, int Hkv, int ngroups, uint32_t* __restrict__ rec) {
@@ -35,16 +35,13 @@ __global__ __launch_bounds__(256) void av_record_kernel(const uint16_t* __restri
   const int b = int(bh / Hkv), kvh = int(bh % Hkv);
   const uint16_t* pr = p + b * spb + (kvh * NREP + h) * sph + g * G;
   uint32_t* r = rec + (bh * ngroups + g) * RD;
-  float beta = 0.f, sum = 0.f;
+  float sum = 0.f;
   for (int k = 0; k < NP; ++k) {
     const uint16_t ua = pr[PT.a[k]], uc = pr[PT.c[k]];
-    const float xa = h2f(ua), xc = h2f(uc);
     r[h * NP + k] = uint32_t(ua) | (uint32_t(uc) << 16);
-    beta += xa * PT.ba[k] + xc * PT.bc[k];
-    sum += xa + xc;
+    sum += h2f(ua) + h2f(uc);
   }
-  r[NP * NREP + h] = __float_as_uint(beta);
-  r[NP * NREP + NREP + h] = __float_as_uint(sum);
+  r[NP * NREP + h] = __float_as_uint(sum);
 }
 
 struct AVArgs {
@@ -120,12 +117,7 @@ __global__ __launch_bounds__(WG) void av_kernel(AVArgs a) {
 #pragma unroll
           for (int e = 0; e < DPL; ++e) to_offset_binary<BITS>(cw[u][e], W);
         }
-        constexpr int NQ = (NREP + 3) / 4;
-        f4_t dv[DPL][NQ];
-#pragma unroll
-        for (int e = 0; e < DPL; ++e)
-#pragma unroll
-          for (int q = 0; q < NQ; ++q) dv[e][q] = f4_t{0.f, 0.f, 0.f, 0.f};
+        f4_t dv[DPL][(NREP + 3) / 4];
         group_mfma<BITS, G, NREP, DPL>(cw[u], a.rec + (int64_t(bh) * a.ngroups + gl0 + wave + NWAVES * (i + u)) * RD,
                                        lane & 3, dv);
 #pragma unroll
@@ -134,7 +126,7 @@ __global__ __launch_bounds__(WG) void av_kernel(AVArgs a) {
           const float z = SYM ? -float(1 << (BITS - 1)) * s : h2f(uint16_t(cm[u][e] >> 16));
 #pragma unroll
           for (int h = 0; h < NREP; ++h) {
-            const float ps = rec_f32(rec, NP * NREP + NREP + h);
+            const float ps = rec_f32(rec, NP * NREP + h);
             acc[h][e] = fmaf(s, dv[e][h / 4][h % 4], fmaf(z, ps, acc[h][e]));
           }
         }
@@ -211,7 +203,7 @@ int av_splits(int B, int Hkv, int T, int group) {
 }
 
 size_t av_record_bytes(int B, int Hq, int T, int group) {
-  return ((size_t(B) * Hq * (T / group) * (group / 2 + 2) * 4) + 255) & ~size_t(255);
+  return (rec_bytes_bound(int64_t(B) * Hq, T / group, group) + 255) & ~size_t(255);
 }
 
 size_t av_part_bytes(int B, int Hq, int T, int D, int group) {

@@ -4,9 +4,11 @@
 // The token axis is cut into
 //   * the fused range: tokens packed in both the K and the V store (the
 //     middle segment of cache.py:235-276 for both), in splits of
-//     flash_split_tokens() tokens.  QK^T runs with its flash epilogue (per
-//     split max m, sum l and fp16 probabilities written as attn.V operand
-//     records), then attn.V writes one unnormalized partial output per split;
+//     flash_split_tokens() tokens.  When K and V share bit width and group
+//     size, one kernel per split runs QK^T, the split softmax and attn.V
+//     (iq_flash.hip).  Otherwise QK^T runs with its flash epilogue (per split
+//     max m, sum l and fp16 probabilities written as attn.V operand records),
+//     then attn.V writes one unnormalized partial output per split;
 //   * the dense tokens: everything else (fp16 sinks and recent windows, plus
 //     packed tokens of only one of K/V, which are dequantized element by
 //     element).  One workgroup per (batch, query head) runs an online softmax
@@ -210,7 +212,7 @@ size_t iq_decode_workspace_bytes(int B, int Hq, int T, int D) {
   if (B <= 0 || Hq <= 0 || T <= 0 || !d_ok(D)) return 0;
   const size_t rows = size_t(B) * Hq;
   size_t vrec = 0;
-  for (int g : {32, 64, 128}) vrec = std::max(vrec, size_t(B) * Hq * (T / g) * (g / 2 + 2) * 4);
+  for (int g : {32, 64, 128}) vrec = std::max(vrec, rec_bytes_bound(int64_t(B) * Hq, T / g, g));
   const size_t ns = size_t(nsplit_max(T)) + 1;
   return detail::qk_record_bytes(B, Hq, D) + align256(vrec) + align256(ns * rows * 2 * 4) +
          align256(ns * rows * D * 4);
@@ -255,7 +257,7 @@ int iq_decode_attention(const void* q, int64_t sq_b, int64_t sq_h, const void* n
   uint32_t* qrec = (uint32_t*)ws;
   ws += detail::qk_record_bytes(B, Hq, D);
   size_t vrec_bytes = 0;
-  for (int g : {32, 64, 128}) vrec_bytes = std::max(vrec_bytes, size_t(B) * Hq * (T / g) * (g / 2 + 2) * 4);
+  for (int g : {32, 64, 128}) vrec_bytes = std::max(vrec_bytes, rec_bytes_bound(int64_t(B) * Hq, T / g, g));
   uint32_t* vrec = (uint32_t*)ws;
   ws += align256(vrec_bytes);
   const size_t ns_cap = size_t(nsplit_max(T)) + 1;
@@ -283,12 +285,19 @@ int iq_decode_attention(const void* q, int64_t sq_b, int64_t sq_h, const void* n
   if (c <= 0) { a0 = 0; c = 0; }
   const int nsf = c ? int(ceil_div(c, detail::flash_split_tokens())) : 0;
 
-  if (c) {
+  if (c && k[1].bits == v[1].bits && k[1].group == v[1].group) {
+    const iq_segment& kg = k[1];
+    const iq_segment& vg = v[1];
+    const detail::FusedStore fk{kg.codes, kg.meta, kg.t_cap, kg.t0 + (a0 - ks), kg.bits, kg.group, kg.mode};
+    const detail::FusedStore fv{vg.codes, vg.meta, vg.t_cap, vg.t0 + (a0 - vs), vg.bits, vg.group, vg.mode};
+    if (int e = detail::flash_fused_launch(q, sq_b, sq_h, norm, fk, fv, B, Hq, Hkv, c, D, scale, ml, part, st))
+      return e;
+  } else if (c) {
     const iq_segment& kg = k[1];
     const iq_segment& vg = v[1];
     if (int e = detail::qk_record_launch(q, sq_b, sq_h, norm, B, Hq, Hkv, D, kg.group, kg.bits, qrec, st)) return e;
     const detail::FlashOut f{ml, vrec, vg.bits, vg.group};
-    if (int e = detail::qk_flash_launch(qrec, kg.codes, kg.meta, kg.t_cap, B, Hq, Hkv, kg.t0 + (a0 - ks), c, D,
+    if (int e = detail::qk_flash_launch(qrec, norm != nullptr, kg.codes, kg.meta, kg.t_cap, B, Hq, Hkv, kg.t0 + (a0 - ks), c, D,
                                         kg.group, kg.bits, kg.mode, scale, f, st))
       return e;
     if (int e = detail::av_flash_launch(vrec, vg.codes, vg.meta, vg.t_cap, B, Hq, Hkv, vg.t0 + (a0 - vs), c, D,

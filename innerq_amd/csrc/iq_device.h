@@ -10,12 +10,10 @@
 // A window of the group's bit string (a word, a shifted word, or an alignbit
 // of two words) is masked and OR-ed with an fp16 exponent pattern in one
 // v_and_or_b32, which yields two fp16 values {bias_a + c_a, bias_b + c_b}
-// exactly (field LSB weight 1, bias 2^(10-p) for a field at in-half bit p).
-// One v_dot2_f32_f16 then multiplies the pair with the matching pair of the
-// fp16 operand (q for QK^T, p for attn.V) and accumulates in fp32.  The bias
-// contribution sum(operand * bias) is a per-(group, head) constant and is
-// subtracted by starting the accumulation at -beta.  Sym codes are turned
-// into offset binary with one XOR per word (u = signed + 2^(b-1)), so
+// exactly (field LSB weight 1, bias 2^(10-p) for a field at in-half bit p);
+// one v_pk_add_f16 removes the biases, leaving the two codes as exact fp16
+// integers for the matrix cores.  Sym codes are turned into offset binary
+// with one XOR per word (u = signed + 2^(b-1)), so
 // sum(q*signed) = sum(q*u) - 2^(b-1)*sum(q), folded into the zero term.
 //
 // Plans (windows counted as extra VALU ops, aligned words are free):
@@ -120,10 +118,6 @@ template <int BITS, int K>
 __device__ __forceinline__ h2_t extract_codes(const uint32_t* w) {
   constexpr h2_t bias = {_Float16(bias_a<BITS>(K)), _Float16(bias_c<BITS>(K))};
   return extract_pair<BITS, K>(w) - bias;
-}
-
-__device__ __forceinline__ float dot2(h2_t a, h2_t b, float c) {
-  return __builtin_amdgcn_fdot2(a, b, c, false);
 }
 
 __device__ __forceinline__ h2_t h2_from_halves(__half a, __half b) {

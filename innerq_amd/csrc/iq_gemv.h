@@ -1,24 +1,45 @@
 // Shared pieces of the decode GEMV kernels (gfx950).
 //
-// Operand records.  Both GEMVs multiply unpacked code pairs by pairs of an
-// fp16 operand that is the same for every lane of a wave: the query (QK^T,
-// lane = token) or the attention probabilities (attn.V, lane = head_dim
-// column).  That operand is laid out once per (batch, KV head, group) as a
-// record
+// Operand records.  Both GEMVs multiply unpacked codes by an fp16 operand
+// that is shared by every lane of a wave: the query (QK^T, lane = token) or
+// the attention probabilities (attn.V, lane = head_dim column).  That operand
+// is laid out once per (batch, KV head, group) as a record
 //     pairs [n_rep][G/2]  uint32 = {x[a_k], x[c_k]} in the unpack plan's pair order
-//     beta  [n_rep]       f32    = sum_k x[a_k]*bias_a(k) + x[c_k]*bias_c(k)
 //     osum  [n_rep]       f32    = sum_i x[i]
-// and read with scalar loads (s_load_dwordx16) into SGPRs, so that every
-// v_dot2_f32_f16 takes its operand pair straight from the scalar register
-// file: no LDS traffic and no VGPRs for the operand.  A head's pairs are
-// contiguous, so a chunk of 16 pairs of one head is one s_load_dwordx16 and
-// only that chunk is live in SGPRs.
+// A head's pairs are contiguous, so the matrix-core A operand of a 16-pair
+// chunk is four 16-byte loads per lane (from global memory or LDS), and osum
+// (needed for the zero-point term) is a scalar load.
+//
+// Matrix-core group dot (v_mfma_f32_4x4x4_16b_f16).  The instruction runs 16
+// independent 4x4x4 products; block b = lane / 4, and lane 4b+i supplies row
+// i of A and column i of B (the four fp16 of its operand, k = element index)
+// and receives column i of D, rows 0..3 in its four result registers
+// (verified on gfx950 with lane-coded operands).  With B = four unpacked codes
+// of the lane's own token / column and A = the operand pairs of head
+// 4q + (lane & 3), one instruction gives every lane the dot products of four
+// heads over four codes: 8 instructions cover a 32-code group, and the VALU
+// only unpacks codes and applies scale and zero point.
+//
+// The B operand is the code pair itself, not the biased magic-number pair:
+// with a bias of up to 1024 per code, partial sums reach ~1e4 and cancel back
+// to ~1, and the MFMA's fp32 accumulation loses ~1e-3 of the result at
+// G = 128.  Subtracting the bias pair first (one v_pk_add_f16, exact because
+// both operands are integers below 2048) keeps every partial sum small.
 #pragma once
 
 #include <utility>
 
 #include "iq_common.h"
 #include "iq_device.h"
+
+// 64-token K blocks per wave in a flash-decoding split (split = 4 waves x
+// this x 64 tokens) and code pairs unpacked per matrix-core chunk.
+#ifndef IQ_FLASH_BPW
+#define IQ_FLASH_BPW 2
+#endif
+#ifndef IQ_MFMA_CH
+#define IQ_MFMA_CH 8
+#endif
 
 namespace iq {
 
@@ -27,15 +48,22 @@ typedef const __attribute__((address_space(4))) uint32_t* cptr_u32;
 constexpr int NWAVES = 4;
 constexpr int WG = NWAVES * 64;
 
+// record stride: padded to 4 dwords so every head's pairs start 16-byte aligned
+__host__ __device__ constexpr int rec_dwords_rt(int G, int nrep) { return (nrep * (G / 2 + 1) + 3) & ~3; }
+
 template <int G, int NREP>
 __host__ __device__ constexpr int rec_dwords() {
-  return NREP * (G / 2 + 2);
+  return rec_dwords_rt(G, NREP);
 }
 
-__host__ __device__ constexpr int rec_dwords_rt(int G, int nrep) { return nrep * (G / 2 + 2); }
+// bound on the record bytes of n_heads query heads (n_heads / n_rep records of
+// n_rep heads each) over n_groups groups of G: at most G/2 + 4 dwords per head
+__host__ __device__ constexpr size_t rec_bytes_bound(int64_t n_heads, int64_t n_groups, int G) {
+  return size_t(n_heads) * size_t(n_groups) * size_t(G / 2 + 4) * 4;
+}
 
-template <int N>
-__device__ __forceinline__ void load_words(const uint32_t* __restrict__ p, uint32_t* w) {
+template <int N, typename P>
+__device__ __forceinline__ void load_words(P p, uint32_t* w) {
   if constexpr (N % 4 == 0) {
 #pragma unroll
     for (int j = 0; j < N; j += 4) {
@@ -67,31 +95,26 @@ __host__ __device__ constexpr int pair_code_c(int k) {
 template <int BITS, int NP>
 struct PairTable {
   int a[NP], c[NP];
-  float ba[NP], bc[NP];
-  constexpr PairTable() : a(), c(), ba(), bc() {
+  constexpr PairTable() : a(), c() {
     for (int k = 0; k < NP; ++k) {
       a[k] = pair_code_a<BITS>(k);
       c[k] = pair_code_c<BITS>(k);
-      ba[k] = bias_a<BITS>(k % Plan<BITS>::NPAIR);
-      bc[k] = bias_c<BITS>(k % Plan<BITS>::NPAIR);
     }
   }
 };
 
 // Pair k (any k < 64, any group size) of the unpack plan for runtime bits:
-// code indices a, c inside the group and the fp16 biases of the two halves.
+// the code indices a, c of its two halves inside the group.
 template <int BITS>
-__device__ __forceinline__ void plan_pair_t(int k, int& a, int& c, float& ba, float& bc) {
+__device__ __forceinline__ void plan_pair_t(int k, int& a, int& c) {
   constexpr PairTable<BITS, 64> PT{};
   a = PT.a[k];
   c = PT.c[k];
-  ba = PT.ba[k];
-  bc = PT.bc[k];
 }
-__device__ __forceinline__ void plan_pair(int bits, int k, int& a, int& c, float& ba, float& bc) {
-  if (bits == 2) plan_pair_t<2>(k, a, c, ba, bc);
-  else if (bits == 3) plan_pair_t<3>(k, a, c, ba, bc);
-  else plan_pair_t<4>(k, a, c, ba, bc);
+__device__ __forceinline__ void plan_pair(int bits, int k, int& a, int& c) {
+  if (bits == 2) plan_pair_t<2>(k, a, c);
+  else if (bits == 3) plan_pair_t<3>(k, a, c);
+  else plan_pair_t<4>(k, a, c);
 }
 
 template <int BITS>
@@ -101,93 +124,8 @@ __device__ __forceinline__ void to_offset_binary(uint32_t* w, int nw) {
   for (int j = 0; j < nw; ++j) w[j] ^= Plan<BITS>::SIGN[j % SBW];
 }
 
-// The value of p, unknown to the optimizer until `after` has been computed.
-// Constant-address loads count as invariant, so without this the compiler
-// hoists every group's / chunk's scalar loads to the top of the kernel and
-// spills SGPRs; tying the base pointer to the previous chunk's accumulator
-// keeps at most one chunk of operand SGPRs live.
-__device__ __forceinline__ cptr_u32 launder(cptr_u32 p, float after) {
-  asm volatile("" : "+s"(p) : "v"(after));
-  return p;
-}
-
-template <int OFF, int... I>
-constexpr std::integer_sequence<int, (OFF + I)...> offset_seq(std::integer_sequence<int, I...>) {
-  return {};
-}
-
-// Extract pairs [K0, K0+CH) of NB code-word sets into VGPRs, then for each
-// head read that head's CH operand pairs (one scalar load) and accumulate.
-template <int BITS, int W, int NREP, int NB, int NP, int K0, int... K>
-__device__ __forceinline__ void chunk_dot(const uint32_t (&w)[NB][W], cptr_u32 rec, float (&dv)[NB][NREP],
-                                          std::integer_sequence<int, K...>) {
-  constexpr int NPS = Plan<BITS>::NPAIR;
-  constexpr int SBW = Plan<BITS>::WORDS;
-  constexpr int CH = sizeof...(K);
-  h2_t x[CH][NB];
-  (
-      [&] {
-#pragma unroll
-        for (int j = 0; j < NB; ++j) x[K][j] = extract_pair<BITS, (K0 + K) % NPS>(&w[j][((K0 + K) / NPS) * SBW]);
-      }(),
-      ...);
-#pragma unroll
-  for (int h = 0; h < NREP; ++h) {
-    // head h's pairs may load once head h-2 is done: two heads of operands
-    // (32 SGPRs) in flight, so the scalar-load latency overlaps head h-1's dots
-    const cptr_u32 r = launder(rec + h * NP + K0, dv[0][h < 2 ? 0 : h - 2]);
-    (
-        [&] {
-          const h2_t op = __builtin_bit_cast(h2_t, r[K]);
-#pragma unroll
-          for (int j = 0; j < NB; ++j) dv[j][h] = dot2(op, x[K][j], dv[j][h]);
-        }(),
-        ...);
-  }
-}
-
-template <int BITS, int G, int NREP, int NB, int C, int NCH>
-__device__ __forceinline__ void chunks_from(const uint32_t (&w)[NB][G * BITS / 32], cptr_u32 rec,
-                                           float (&dv)[NB][NREP]) {
-  if constexpr (C < NCH) {
-    constexpr int NP = G / 2;
-    constexpr int CH = NP / NCH;
-    chunk_dot<BITS, G * BITS / 32, NREP, NB, NP, C * CH>(w, rec, dv, std::make_integer_sequence<int, CH>{});
-    chunks_from<BITS, G, NREP, NB, C + 1, NCH>(w, rec, dv);
-  }
-}
-
-// One group: NB code-word sets (tokens for QK^T, columns for attn.V) against
-// one operand record.  dv must be pre-initialized (to -beta).  Pairs are
-// handled 16 at a time so the extracted pairs stay within 16*NB VGPRs.
-template <int BITS, int G, int NREP, int NB>
-__device__ __forceinline__ void group_dot_rec(const uint32_t (&w)[NB][G * BITS / 32], cptr_u32 rec,
-                                              float (&dv)[NB][NREP]) {
-  constexpr int NP = G / 2;
-  constexpr int NCH = NP <= 16 ? 1 : NP / 16;
-  chunks_from<BITS, G, NREP, NB, 0, NCH>(w, rec, dv);
-}
-
 __device__ __forceinline__ float rec_f32(cptr_u32 rec, int i) { return __builtin_bit_cast(float, rec[i]); }
 
-// ---------------------------------------------------------------------------
-// Matrix-core group dot (v_mfma_f32_4x4x4_16b_f16).
-//
-// The instruction runs 16 independent 4x4x4 products; block b = lane / 4,
-// and lane 4b+i supplies row i of A and column i of B (the four fp16 of its
-// operand, k = element index) and receives column i of D, rows 0..3 in its
-// four result registers (verified on gfx950 with lane-coded operands).  With
-// B = four unpacked codes of the lane's own token / column and A = the
-// operand pairs of head 4q + (lane & 3), one instruction gives every lane the
-// dot products of four heads over four codes: 8 instructions cover a 32-code
-// group, and the VALU only unpacks codes and applies scale / zero point.
-//
-// The B operand is the code pair itself, not the biased magic-number pair:
-// with a bias of up to 1024 per code, partial sums reach ~1e4 and cancel
-// back to ~1, and the MFMA's fp32 accumulation loses ~1e-3 of the result at
-// G = 128.  Subtracting the bias pair first (one v_pk_add_f16, exact because
-// both operands are integers below 2048) keeps every partial sum small.
-// ---------------------------------------------------------------------------
 typedef _Float16 h4_t __attribute__((ext_vector_type(4)));
 typedef float f4_t __attribute__((ext_vector_type(4)));
 
@@ -197,15 +135,15 @@ __device__ __forceinline__ f4_t mfma4(h4_t a, h4_t b, f4_t c) {
 
 __device__ __forceinline__ h4_t cat_h2(h2_t lo, h2_t hi) { return __builtin_shufflevector(lo, hi, 0, 1, 2, 3); }
 
-template <int BITS, int W, int NREP, int NB, int K0, int... K>
-__device__ __forceinline__ void mfma_chunk(const uint32_t (&w)[NB][W], const uint32_t* __restrict__ rec, int NP,
-                                           int hl, f4_t (&dv)[NB][(NREP + 3) / 4],
-                                           std::integer_sequence<int, K...>) {
+// Pairs [K0, K0+CH) of one group: A rows from the record (head 4q + hl; heads
+// past NREP read as zero), B from the NB code-word sets.
+template <int BITS, int W, int NREP, int NB, int K0, typename P, int... K>
+__device__ __forceinline__ void mfma_chunk(const uint32_t (&w)[NB][W], P rec, int NP, int hl,
+                                           f4_t (&dv)[NB][(NREP + 3) / 4], std::integer_sequence<int, K...>) {
   constexpr int NPS = Plan<BITS>::NPAIR;
   constexpr int SBW = Plan<BITS>::WORDS;
   constexpr int CH = sizeof...(K);
   constexpr int NQ = (NREP + 3) / 4;
-  // A rows: pairs [K0, K0+CH) of head 4q + hl (heads past NREP read as zero)
   uint32_t av[NQ][CH];
 #pragma unroll
   for (int q = 0; q < NQ; ++q) {
@@ -236,9 +174,9 @@ __device__ __forceinline__ void mfma_chunk(const uint32_t (&w)[NB][W], const uin
   }
 }
 
-template <int BITS, int G, int NREP, int NB, int C, int NCH>
-__device__ __forceinline__ void mfma_chunks(const uint32_t (&w)[NB][G * BITS / 32], const uint32_t* __restrict__ rec,
-                                            int hl, f4_t (&dv)[NB][(NREP + 3) / 4]) {
+template <int BITS, int G, int NREP, int NB, int C, int NCH, typename P>
+__device__ __forceinline__ void mfma_chunks(const uint32_t (&w)[NB][G * BITS / 32], P rec, int hl,
+                                            f4_t (&dv)[NB][(NREP + 3) / 4]) {
   if constexpr (C < NCH) {
     constexpr int CH = (G / 2) / NCH;
     mfma_chunk<BITS, G * BITS / 32, NREP, NB, C * CH>(w, rec, G / 2, hl, dv, std::make_integer_sequence<int, CH>{});
@@ -246,23 +184,88 @@ __device__ __forceinline__ void mfma_chunks(const uint32_t (&w)[NB][G * BITS / 3
   }
 }
 
-// dv[j][q][i] += sum over the group's pairs of opnd(head 4q+i) . codes(set j)
-// (unbiased codes: no -beta start value),
-// rec = this group's operand record (vector-loaded per lane: row = hl).
-template <int BITS, int G, int NREP, int NB>
-__device__ __forceinline__ void group_mfma(const uint32_t (&w)[NB][G * BITS / 32], const uint32_t* __restrict__ rec,
-                                           int hl, f4_t (&dv)[NB][(NREP + 3) / 4]) {
+// Query operand record (QK^T) of one group:
+//     pairs [2*n_rep][G/2]  rows h < n_rep: fp16 query pairs, or with key
+//                           normalization the high parts hi = fp16(q*n);
+//                           rows n_rep + h: the low parts lo = fp16(q*n - hi)
+//                           (key normalization only)
+//     osum  [n_rep]  f32    sum_i q_i (times n_i)
+// q*n is exact in fp32 and hi + lo holds it to 2^-22, so folding the key
+// normalization into the query costs no precision (rounding q*n to one fp16
+// moves the logits by ~1e-4 relative, which exp() turns into ~1e-3 of the
+// attention output).
+template <int G, int NREP>
+__host__ __device__ constexpr int qrec_dwords() {
+  return (NREP * (G + 1) + 3) & ~3;
+}
+template <int G, int NREP>
+__host__ __device__ constexpr int qrec_osum() {
+  return NREP * G;
+}
+
+// pair (ia, ic) of query row qrow (and norm row nrow, or null): writes the hi
+// pair to *hi and, with a norm, the lo pair to *lo; adds the pair to sum.
+__device__ __forceinline__ void qrec_pair(const uint16_t* qrow, const uint16_t* nrow, int ia, int ic, uint32_t* hi,
+                                          uint32_t* lo, float& sum) {
+  if (!nrow) {
+    const uint16_t ua = qrow[ia], uc = qrow[ic];
+    *hi = uint32_t(ua) | (uint32_t(uc) << 16);
+    sum += h2f(ua) + h2f(uc);
+    return;
+  }
+  const float qa = h2f(qrow[ia]) * h2f(nrow[ia]), qc = h2f(qrow[ic]) * h2f(nrow[ic]);  // exact
+  const uint16_t ha = __half_as_ushort(__float2half_rn(qa)), hc = __half_as_ushort(__float2half_rn(qc));
+  *hi = uint32_t(ha) | (uint32_t(hc) << 16);
+  *lo = uint32_t(__half_as_ushort(__float2half_rn(qa - h2f(ha)))) |
+        (uint32_t(__half_as_ushort(__float2half_rn(qc - h2f(hc)))) << 16);
+  sum += qa + qc;
+}
+
+// dv[j][q][i] = sum over the group's pairs of opnd(head 4q+i) . codes(set j),
+// rec = this group's operand record (global memory or LDS; each lane loads
+// the row of head 4q + hl).  Pairs go IQ_MFMA_CH at a time so the extracted
+// codes stay within IQ_MFMA_CH*NB VGPRs.
+template <int BITS, int G, int NREP, int NB, typename P>
+__device__ __forceinline__ void group_mfma(const uint32_t (&w)[NB][G * BITS / 32], P rec, int hl,
+                                           f4_t (&dv)[NB][(NREP + 3) / 4]) {
   constexpr int NP = G / 2;
-  constexpr int NCH = NP <= 16 ? 1 : NP / 16;
+  constexpr int NCH = NP <= IQ_MFMA_CH ? 1 : NP / IQ_MFMA_CH;
+#pragma unroll
+  for (int j = 0; j < NB; ++j)
+#pragma unroll
+    for (int q = 0; q < (NREP + 3) / 4; ++q) dv[j][q] = f4_t{0.f, 0.f, 0.f, 0.f};
   mfma_chunks<BITS, G, NREP, NB, 0, NCH>(w, rec, hl, dv);
+}
+
+// Query dot products of NB code sets: d[j][h] = sum_i q'[h,i] c_j[i] over the
+// group, from the hi rows or, when split, hi + lo rows of the query record.
+template <int BITS, int G, int NREP, int NB, typename P>
+__device__ __forceinline__ void qk_group_dot(const uint32_t (&w)[NB][G * BITS / 32], P rec, int hl, bool split,
+                                             float (&d)[NB][NREP]) {
+  if (split) {
+    f4_t dv[NB][(2 * NREP + 3) / 4];
+    group_mfma<BITS, G, 2 * NREP, NB>(w, rec, hl, dv);
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+      for (int h = 0; h < NREP; ++h) d[j][h] = dv[j][h / 4][h % 4] + dv[j][(NREP + h) / 4][(NREP + h) % 4];
+  } else {
+    f4_t dv[NB][(NREP + 3) / 4];
+    group_mfma<BITS, G, NREP, NB>(w, rec, hl, dv);
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+      for (int h = 0; h < NREP; ++h) d[j][h] = dv[j][h / 4][h % 4];
+  }
 }
 
 // ---- host-side launchers shared between translation units -----------------
 namespace detail {
 int qk_record_launch(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, int B, int Hq, int Hkv, int D,
                      int group, int bits, uint32_t* rec, hipStream_t stream);
-int qk_main_launch(const uint32_t* rec, const uint32_t* k_codes, const uint16_t* k_meta, int64_t t_cap, int B,
-                   int Hq, int Hkv, int t0, int T, int D, int group, int bits, int mode, float scale, float* out,
+// split: the records carry hi/lo query rows (built with a key normalization)
+int qk_main_launch(const uint32_t* rec, int split, const uint32_t* k_codes, const uint16_t* k_meta, int64_t t_cap,
+                   int B, int Hq, int Hkv, int t0, int T, int D, int group, int bits, int mode, float scale, float* out,
                    int64_t so_b, int64_t so_h, hipStream_t stream);
 // Flash-decoding split size (tokens per QK^T workgroup) and the QK^T launch
 // that, instead of logits, writes per-split softmax statistics (m, l) and the
@@ -273,8 +276,8 @@ struct FlashOut {
   uint32_t* vrec;     // attn.V operand records [B*Hkv][T/vgroup]
   int vbits, vgroup;  // V store format (records follow its unpack plan)
 };
-int qk_flash_launch(const uint32_t* rec, const uint32_t* k_codes, const uint16_t* k_meta, int64_t t_cap, int B,
-                    int Hq, int Hkv, int t0, int T, int D, int group, int bits, int mode, float scale,
+int qk_flash_launch(const uint32_t* rec, int split, const uint32_t* k_codes, const uint16_t* k_meta, int64_t t_cap,
+                    int B, int Hq, int Hkv, int t0, int T, int D, int group, int bits, int mode, float scale,
                     const FlashOut& f, hipStream_t stream);
 int av_flash_launch(const uint32_t* rec, const uint32_t* v_codes, const uint16_t* v_meta, int64_t t_cap, int B,
                     int Hq, int Hkv, int t0, int T, int D, int group, int bits, int mode, float* part,
@@ -293,6 +296,19 @@ int av_main_launch(const uint32_t* rec, const uint32_t* v_codes, const uint16_t*
                    hipStream_t stream);
 int av_combine_launch(const float* part, int nsplit, int B, int Hq, int D, const OutPair& o, int accumulate,
                       hipStream_t stream);
+// The fused flash-decoding split kernel (QK^T + split softmax + attn.V in one
+// workgroup) for K and V stores of the same bit width and group size; writes
+// the same split statistics and partials as the unfused path.
+struct FusedStore {
+  const uint32_t* codes;
+  const uint16_t* meta;
+  int64_t t_cap;
+  int t0;  // first store token of the range
+  int bits, group, mode;
+};
+int flash_fused_launch(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, const FusedStore& k,
+                       const FusedStore& v, int B, int Hq, int Hkv, int T, int D, float scale, float* ml,
+                       float* part, hipStream_t stream);
 size_t qk_record_bytes(int B, int Hq, int D);
 size_t av_record_bytes(int B, int Hq, int T, int group);
 size_t av_part_bytes(int B, int Hq, int T, int D, int group);

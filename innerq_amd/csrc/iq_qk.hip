@@ -25,22 +25,19 @@
 
 using namespace iq;
 
-#ifndef IQ_QK_BPW
-#define IQ_QK_BPW 2
-#endif
-
 namespace {
 
-constexpr int QK_BPW = IQ_QK_BPW;
+constexpr int QK_BPW = IQ_FLASH_BPW;
 constexpr int SPLIT = NWAVES * QK_BPW * TOKEN_BLOCK;  // tokens per workgroup
 
-// one thread per (b, kvh, g, h): query pairs in plan order, bias sum and plain sum
+// one thread per (b, kvh, g, h): query pairs in plan order (hi/lo with a key
+// normalization folded in, cache.py:128-133) and their sum
 template <int BITS, int G, int NREP>
 __global__ __launch_bounds__(256) void qk_record_kernel(const uint16_t* __restrict__ q, int64_t sqb, int64_t sqh,
                                                         const uint16_t* __restrict__ norm, int B, int Hkv, int D,
                                                         uint32_t* __restrict__ rec) {
   constexpr int NP = G / 2;
-  constexpr int RD = rec_dwords<G, NREP>();
+  constexpr int RD = qrec_dwords<G, NREP>();
   constexpr PairTable<BITS, NP> PT{};
   const int ng = D / G;
   const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -52,21 +49,10 @@ __global__ __launch_bounds__(256) void qk_record_kernel(const uint16_t* __restri
   const uint16_t* qr = q + b * sqb + (kvh * NREP + h) * sqh + g * G;
   const uint16_t* nr = norm ? norm + bh * D + g * G : nullptr;
   uint32_t* r = rec + (bh * ng + g) * RD;
-  float beta = 0.f, sum = 0.f;
+  float sum = 0.f;
 #pragma unroll
-  for (int k = 0; k < NP; ++k) {
-    float qa = h2f(qr[PT.a[k]]), qc = h2f(qr[PT.c[k]]);
-    if (nr) {  // fold the key normalization factor into the query (cache.py:132)
-      qa = round_f16(qa * h2f(nr[PT.a[k]]));
-      qc = round_f16(qc * h2f(nr[PT.c[k]]));
-    }
-    r[h * NP + k] = uint32_t(__half_as_ushort(__float2half_rn(qa))) |
-                    (uint32_t(__half_as_ushort(__float2half_rn(qc))) << 16);
-    beta += qa * PT.ba[k] + qc * PT.bc[k];
-    sum += qa + qc;
-  }
-  r[NP * NREP + h] = __float_as_uint(beta);
-  r[NP * NREP + NREP + h] = __float_as_uint(sum);
+  for (int k = 0; k < NP; ++k) qrec_pair(qr, nr, PT.a[k], PT.c[k], &r[h * NP + k], &r[(NREP + h) * NP + k], sum);
+  r[qrec_osum<G, NREP>() + h] = __float_as_uint(sum);
 }
 
 struct QKArgs {
@@ -76,6 +62,7 @@ struct QKArgs {
   int64_t cap_blocks;
   int Hkv, blk0, T, nblk;
   float scale;
+  int split;   // hi/lo query rows
   float* out;  // logits epilogue
   int64_t sob, soh;
   int flash;   // flash epilogue
@@ -96,7 +83,7 @@ __global__ __launch_bounds__(WG) void qk_kernel(QKArgs a) {
   constexpr int W = G * BITS / 32;
   constexpr int NP = G / 2;
   constexpr int M = SYM ? 1 : 2;
-  constexpr int RD = rec_dwords<G, NREP>();
+  constexpr int RD = qrec_dwords<G, NREP>();
   constexpr int BPW = QK_BPW;
   __shared__ FlashSmem<NREP> sm;
 
@@ -154,21 +141,16 @@ __global__ __launch_bounds__(WG) void qk_kernel(QKArgs a) {
 #pragma unroll
       for (int j = 0; j < BPW; ++j) to_offset_binary<BITS>(cw[j], W);
     }
-    constexpr int NQ = (NREP + 3) / 4;
-    f4_t dv[BPW][NQ];
-#pragma unroll
-    for (int j = 0; j < BPW; ++j)
-#pragma unroll
-      for (int q = 0; q < NQ; ++q) dv[j][q] = f4_t{0.f, 0.f, 0.f, 0.f};
-    group_mfma<BITS, G, NREP, BPW>(cw, a.rec + (int64_t(bh) * NG + g) * RD, lane & 3, dv);
+    float d[BPW][NREP];
+    qk_group_dot<BITS, G, NREP, BPW>(cw, a.rec + (int64_t(bh) * NG + g) * RD, lane & 3, a.split, d);
 #pragma unroll
     for (int j = 0; j < BPW; ++j) {
       const float s = h2f(uint16_t(cm[j] & 0xffffu));
       const float z = SYM ? -float(1 << (BITS - 1)) * s : h2f(uint16_t(cm[j] >> 16));
 #pragma unroll
       for (int h = 0; h < NREP; ++h) {
-        const float qs = rec_f32(rec, NP * NREP + NREP + h);
-        acc[j][h] = fmaf(s, dv[j][h / 4][h % 4], fmaf(z, qs, acc[j][h]));
+        const float qs = rec_f32(rec, qrec_osum<G, NREP>() + h);
+        acc[j][h] = fmaf(s, d[j][h], fmaf(z, qs, acc[j][h]));
       }
     }
   }
@@ -227,7 +209,7 @@ __global__ __launch_bounds__(WG) void qk_kernel(QKArgs a) {
     dst[1] = (sm.l[0][h] + sm.l[1][h]) + (sm.l[2][h] + sm.l[3][h]);
   }
   // records: one thread per (V group of this split, head)
-  const int vg = a.f.vgroup, vnp = vg / 2, vrd = NREP * (vnp + 2);
+  const int vg = a.f.vgroup, vnp = vg / 2, vrd = rec_dwords_rt(vg, NREP);
   const int gps = SPLIT / vg;
   for (int i = threadIdx.x; i < gps * NREP; i += WG) {
     const int gl = i / NREP, h = i % NREP;
@@ -235,19 +217,15 @@ __global__ __launch_bounds__(WG) void qk_kernel(QKArgs a) {
     if (gabs >= a.ngv) continue;
     uint32_t* r = a.f.vrec + (int64_t(bh) * a.ngv + gabs) * vrd;
     const uint16_t* pp = &sm.p[h][gl * vg];
-    float beta = 0.f, sum = 0.f;
+    float sum = 0.f;
     for (int k = 0; k < vnp; ++k) {
       int ia, ic;
-      float ba, bc;
-      plan_pair(a.f.vbits, k, ia, ic, ba, bc);
+      plan_pair(a.f.vbits, k, ia, ic);
       const uint16_t ua = pp[ia], uc = pp[ic];
       r[h * vnp + k] = uint32_t(ua) | (uint32_t(uc) << 16);
-      const float fa = h2f(ua), fc = h2f(uc);
-      beta += fa * ba + fc * bc;
-      sum += fa + fc;
+      sum += h2f(ua) + h2f(uc);
     }
-    r[vnp * NREP + h] = __float_as_uint(beta);
-    r[vnp * NREP + NREP + h] = __float_as_uint(sum);
+    r[vnp * NREP + h] = __float_as_uint(sum);
   }
 }
 
@@ -291,10 +269,11 @@ int num_cus() {
 int flash_split_tokens() { return SPLIT; }
 
 size_t qk_record_bytes(int B, int Hq, int D) {
-  // largest record set over the supported groups: n_rep*(G/2+2) dwords per group, D/G groups
+  // largest record set over the supported groups: D/G records per n_rep query
+  // heads, at most G + 1 dwords per head and 3 of padding per record
   size_t best = 0;
   for (int g : {32, 64, 128})
-    if (D % g == 0) best = std::max(best, size_t(B) * Hq * (D / g) * (g / 2 + 2) * 4);
+    if (D % g == 0) best = std::max(best, size_t(B) * Hq * (D / g) * size_t(g + 4) * 4);
   return (best + 255) & ~size_t(255);
 }
 
@@ -309,24 +288,24 @@ int qk_record_launch(const void* q, int64_t sq_b, int64_t sq_h, const void* norm
   });
 }
 
-int qk_main_launch(const uint32_t* rec, const uint32_t* k_codes, const uint16_t* k_meta, int64_t t_cap, int B,
-                   int Hq, int Hkv, int t0, int T, int D, int group, int bits, int mode, float scale, float* out,
+int qk_main_launch(const uint32_t* rec, int split, const uint32_t* k_codes, const uint16_t* k_meta, int64_t t_cap,
+                   int B, int Hq, int Hkv, int t0, int T, int D, int group, int bits, int mode, float scale, float* out,
                    int64_t so_b, int64_t so_h, hipStream_t stream) {
   if (B == 0 || T == 0) return IQ_OK;
   QKArgs a{};
-  a.rec = rec; a.kc = k_codes; a.km = k_meta; a.cap_blocks = t_cap / TOKEN_BLOCK; a.Hkv = Hkv;
+  a.rec = rec; a.split = split; a.kc = k_codes; a.km = k_meta; a.cap_blocks = t_cap / TOKEN_BLOCK; a.Hkv = Hkv;
   a.blk0 = t0 / TOKEN_BLOCK; a.T = T; a.nblk = int(ceil_div(T, TOKEN_BLOCK)); a.scale = scale;
   a.out = out; a.sob = so_b; a.soh = so_h; a.flash = 0;
   return launch(a, B, Hq, Hkv, D, group, bits, mode, stream);
 }
 
-int qk_flash_launch(const uint32_t* rec, const uint32_t* k_codes, const uint16_t* k_meta, int64_t t_cap, int B,
-                    int Hq, int Hkv, int t0, int T, int D, int group, int bits, int mode, float scale,
+int qk_flash_launch(const uint32_t* rec, int split, const uint32_t* k_codes, const uint16_t* k_meta, int64_t t_cap,
+                    int B, int Hq, int Hkv, int t0, int T, int D, int group, int bits, int mode, float scale,
                     const FlashOut& f, hipStream_t stream) {
   if (B == 0 || T == 0) return IQ_OK;
   if (SPLIT % f.vgroup || T % f.vgroup) return IQ_ERR_GROUP;
   QKArgs a{};
-  a.rec = rec; a.kc = k_codes; a.km = k_meta; a.cap_blocks = t_cap / TOKEN_BLOCK; a.Hkv = Hkv;
+  a.rec = rec; a.split = split; a.kc = k_codes; a.km = k_meta; a.cap_blocks = t_cap / TOKEN_BLOCK; a.Hkv = Hkv;
   a.blk0 = t0 / TOKEN_BLOCK; a.T = T; a.nblk = int(ceil_div(T, TOKEN_BLOCK)); a.scale = scale;
   a.flash = 1; a.f = f; a.ngv = T / f.vgroup;
   return launch(a, B, Hq, Hkv, D, group, bits, mode, stream);
@@ -351,7 +330,7 @@ int iq_qk_gemv(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, cons
   hipStream_t st = (hipStream_t)stream;
   uint32_t* rec = (uint32_t*)workspace;
   if (int e = detail::qk_record_launch(q, sq_b, sq_h, norm, B, Hq, Hkv, D, group, bits, rec, st)) return e;
-  return detail::qk_main_launch(rec, k_codes, k_meta, t_cap, B, Hq, Hkv, t0, T, D, group, bits, mode, scale, out,
+  return detail::qk_main_launch(rec, norm != nullptr, k_codes, k_meta, t_cap, B, Hq, Hkv, t0, T, D, group, bits, mode, scale, out,
                                 so_b, so_h, st);
 }
 

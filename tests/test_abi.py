@@ -97,7 +97,8 @@ def test_workspace_queries():
     lib = _lib.lib()
     n = lib.iq_av_workspace_bytes(8, 32, 32768, 128, 32)
     assert n >= 8 * 32 * 32768 * 2 + 8 * 32 * 128 * 4
-    assert lib.iq_qk_workspace_bytes(8, 32, 128) >= 8 * 32 * (64 + 8) * 4
+    # per query head: D/2 query pairs + one fp32 sum per group (4 groups at G=32)
+    assert lib.iq_qk_workspace_bytes(8, 32, 128) >= 8 * 32 * (64 + 4) * 4
     assert lib.iq_av_workspace_bytes(8, 32, 32768, 96, 32) == 0
     assert lib.iq_decode_workspace_bytes(8, 32, 32768, 128) >= 8 * 32 * 32768 * 2  # fp16 probability records
     assert lib.iq_decode_workspace_bytes(0, 32, 32768, 128) == 0

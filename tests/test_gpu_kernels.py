@@ -214,8 +214,12 @@ def test_qk_gemv_shapes(nrep, D):
     assert np.all(o[:, :, :5] == 7.0) and np.all(o[:, :, 5 + T - 128:] == 7.0)
 
 
-def test_qk_gemv_key_norm_folded():
-    B, Hkv, T, D, G = 1, 2, 256, 128, 32
+# The normalization is folded into the query as hi/lo fp16 rows (n_rep query
+# heads become 2*n_rep matrix-core rows): every n_rep exercises another row
+# layout (n_rep 1, 2: one 4-row block; 4: two blocks; 8: four).
+@pytest.mark.parametrize("nrep,G", [(1, 32), (2, 128), (4, 32), (8, 64)])
+def test_qk_gemv_key_norm_folded(nrep, G):
+    B, Hkv, T, D = 1, 2, 256, 128
     x = synth.kv_tensor(B, Hkv, T, D, seed=11, n_out=4, factor=8.0)
     norm = np.sqrt(np.abs(x).max(axis=-2, keepdims=True).astype(np.float32)).astype(np.float16)
     st = ops.PackedStore("channel", B, Hkv, D, G, 3, "symmetric", DEV)
@@ -223,7 +227,7 @@ def test_qk_gemv_key_norm_folded():
     xn = (x.astype(np.float32) / norm.astype(np.float32)).astype(np.float16)
     c, s, sg = Q.quantize_channeldim_sym(xn, G, 3)
     kdeq = Q.dequantize_channeldim_sym(c, s, sg, G) * norm.astype(np.float32)
-    q = synth.normal((B, Hkv * 4, D), seed=12).astype(np.float16)
+    q = synth.normal((B, Hkv * nrep, D), seed=12).astype(np.float16)
     got = ops.qk_gemv(f16t(q), st, D ** -0.5, norm=f16t(norm)).cpu().numpy()
     assert A.rel_err(got, A.qk_logits(q, kdeq, D ** -0.5)) < TOL
 
@@ -390,4 +394,23 @@ def test_decode_attention_formats_and_norm(kfmt, vfmt):
 def test_decode_attention_gqa_shapes(nrep, D):
     err = _decode_case(2, 2, nrep, D, (0, 64 * 17, 128), (0, 32 * 34, 128), (4, 32, "asymmetric"),
                        (4, 32, "asymmetric"), seed=nrep * D)
+    assert err < TOL
+
+
+# K and V of one bit width and group size take the fused split kernel (one
+# workgroup runs QK^T, the split softmax and attn.V); sym/asym may differ.
+@pytest.mark.parametrize("fmt,nrep,D", [
+    ((2, 32, "asymmetric", "asymmetric"), 4, 128),
+    ((2, 64, "symmetric", "asymmetric"), 8, 128),
+    ((3, 64, "asymmetric", "symmetric"), 2, 64),
+    ((3, 128, "asymmetric", "asymmetric"), 1, 128),
+    ((4, 64, "asymmetric", "symmetric"), 4, 64),
+    ((4, 128, "symmetric", "symmetric"), 4, 128),
+])
+def test_decode_attention_fused_formats(fmt, nrep, D):
+    bits, G, km, vm = fmt
+    kseg = (16, 64 * 21, 80)
+    vq = (64 * 21 + 80) // G * G - G
+    vseg = (16, vq, 64 * 21 + 80 - vq)
+    err = _decode_case(2, 2, nrep, D, kseg, vseg, (bits, G, km), (bits, G, vm), seed=bits * G + nrep, norm=True)
     assert err < TOL
