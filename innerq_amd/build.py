@@ -30,6 +30,9 @@ HIPCC_FLAGS = [
     "-std=c++20",
     "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # matrix-core results in VGPRs: the GEMV epilogues read every MFMA result
+    # with VALU instructions, which AGPR results would need copied out first
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wall",
     "-Wno-unused-function",
     "-Wno-unused-variable",

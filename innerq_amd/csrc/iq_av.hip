@@ -96,6 +96,7 @@ __global__ __launch_bounds__(WG) void av_kernel(AVArgs a) {
       }
     }
   };
+  const PlanRegs<BITS> pr;
   if (cnt > 0) load(0);
   for (int i = 0; i < cnt; i += NB) {
     uint32_t cw[NB][DPL][W];
@@ -119,7 +120,7 @@ __global__ __launch_bounds__(WG) void av_kernel(AVArgs a) {
         }
         f4_t dv[DPL][(NREP + 3) / 4];
         group_mfma<BITS, G, NREP, DPL>(cw[u], a.rec + (int64_t(bh) * a.ngroups + gl0 + wave + NWAVES * (i + u)) * RD,
-                                       lane & 3, dv);
+                                       lane & 3, pr, dv);
 #pragma unroll
         for (int e = 0; e < DPL; ++e) {
           const float s = h2f(uint16_t(cm[u][e] & 0xffffu));

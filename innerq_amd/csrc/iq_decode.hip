@@ -147,22 +147,25 @@ __global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs a) {
 }
 
 // out[bq, d] = sum_s e^{m_s - M} o_s[bq, d] / sum_s e^{m_s - M} l_s
-// One workgroup per row bq: the split weights are computed once into LDS, then
-// each column's partials are summed with independent (unrolled) loads.
+// One workgroup per row bq.  The split weights go to LDS once; then thread t
+// takes column quad t % (D/4) and every NSL-th split starting at t / (D/4),
+// with all of its 16-byte partial loads independent (in flight together), and
+// the NSL slices are summed in LDS in slice order.
 constexpr int MAXSPLIT = 1024;
 __global__ __launch_bounds__(256) void flash_combine_kernel(const float* __restrict__ ml, const float* __restrict__ part,
                                                             int nsplit, int64_t rows, int Hq, int D,
                                                             uint16_t* __restrict__ out, int64_t sob, int64_t soh) {
   __shared__ float wgt[MAXSPLIT];
-  __shared__ float red[4];
+  __shared__ float4 red[256];
+  __shared__ float rs[4];
   const int64_t bq = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   float mx = -INFINITY;
   for (int s = tid; s < nsplit; s += 256) mx = fmaxf(mx, ml[(int64_t(s) * rows + bq) * 2]);
   mx = wave_max(mx);
-  if (lane == 0) red[wave] = mx;
+  if (lane == 0) rs[wave] = mx;
   __syncthreads();
-  const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const float M = fmaxf(fmaxf(rs[0], rs[1]), fmaxf(rs[2], rs[3]));
   __syncthreads();
   float L = 0.f;
   for (int s = tid; s < nsplit; s += 256) {
@@ -172,20 +175,47 @@ __global__ __launch_bounds__(256) void flash_combine_kernel(const float* __restr
     L = fmaf(w, ml[(int64_t(s) * rows + bq) * 2 + 1], L);
   }
   L = wave_sum(L);
-  if (lane == 0) red[wave] = L;
+  if (lane == 0) rs[wave] = L;
   __syncthreads();
-  L = (red[0] + red[1]) + (red[2] + red[3]);
-  for (int d = tid; d < D; d += 256) {
-    const float* pc = part + bq * D + d;
-    float acc[4] = {0.f, 0.f, 0.f, 0.f};
-    int s = 0;
-    for (; s + 4 <= nsplit; s += 4) {
+  L = (rs[0] + rs[1]) + (rs[2] + rs[3]);
+  const int nq = D / 4;           // column quads
+  const int nsl = 256 / nq;       // split slices (8 at D = 128, 16 at D = 64)
+  const int cq = tid % nq, sl = tid / nq;
+  const float4* pc = reinterpret_cast<const float4*>(part + bq * D) + cq;
+  const int64_t sstride = rows * D / 4;  // float4 per split
+  float4 acc = {0.f, 0.f, 0.f, 0.f};
+  constexpr int U = 8;
+  int s = sl;
+  for (; s + (U - 1) * nsl < nsplit; s += U * nsl) {
+    float4 v[U];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) acc[u] = fmaf(wgt[s + u], pc[int64_t(s + u) * rows * D], acc[u]);
+    for (int u = 0; u < U; ++u) v[u] = pc[int64_t(s + u * nsl) * sstride];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const float w = wgt[s + u * nsl];
+      acc.x = fmaf(w, v[u].x, acc.x); acc.y = fmaf(w, v[u].y, acc.y);
+      acc.z = fmaf(w, v[u].z, acc.z); acc.w = fmaf(w, v[u].w, acc.w);
     }
-    for (; s < nsplit; ++s) acc[0] = fmaf(wgt[s], pc[int64_t(s) * rows * D], acc[0]);
-    const float v = ((acc[0] + acc[1]) + (acc[2] + acc[3])) / L;
-    out[(bq / Hq) * sob + (bq % Hq) * soh + d] = __half_as_ushort(__float2half_rn(v));
+  }
+  for (; s < nsplit; s += nsl) {
+    const float4 v = pc[int64_t(s) * sstride];
+    const float w = wgt[s];
+    acc.x = fmaf(w, v.x, acc.x); acc.y = fmaf(w, v.y, acc.y);
+    acc.z = fmaf(w, v.z, acc.z); acc.w = fmaf(w, v.w, acc.w);
+  }
+  red[tid] = acc;
+  __syncthreads();
+  if (tid < nq) {
+    float4 t = red[tid];
+    for (int r = 1; r < nsl; ++r) {
+      const float4 u = red[r * nq + tid];
+      t.x += u.x; t.y += u.y; t.z += u.z; t.w += u.w;
+    }
+    uint16_t* o = out + (bq / Hq) * sob + (bq % Hq) * soh + 4 * tid;
+    o[0] = __half_as_ushort(__float2half_rn(t.x / L));
+    o[1] = __half_as_ushort(__float2half_rn(t.y / L));
+    o[2] = __half_as_ushort(__float2half_rn(t.z / L));
+    o[3] = __half_as_ushort(__float2half_rn(t.w / L));
   }
 }
 
@@ -285,7 +315,8 @@ int iq_decode_attention(const void* q, int64_t sq_b, int64_t sq_h, const void* n
   if (c <= 0) { a0 = 0; c = 0; }
   const int nsf = c ? int(ceil_div(c, detail::flash_split_tokens())) : 0;
 
-  if (c && k[1].bits == v[1].bits && k[1].group == v[1].group) {
+  if (c && k[1].bits == v[1].bits && k[1].group == v[1].group &&
+      detail::flash_fused_supported(q, sq_b, sq_h, norm)) {
     const iq_segment& kg = k[1];
     const iq_segment& vg = v[1];
     const detail::FusedStore fk{kg.codes, kg.meta, kg.t_cap, kg.t0 + (a0 - ks), kg.bits, kg.group, kg.mode};

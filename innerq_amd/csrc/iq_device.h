@@ -95,29 +95,65 @@ __device__ __forceinline__ uint32_t vgpr_const(uint32_t c) {
   return c;
 }
 
-// (x & m) | c in one v_and_or_b32.  gfx9 VOP3 has no literal operand, so the
-// mask and the exponent pattern live in VGPRs (materialized once per kernel);
-// with literal operands the compiler would split it into v_and_b32 +
-// v_or_b32.  The instruction itself must come from the compiler, not from
-// inline asm: its result feeds MFMA source operands, and the required VALU
-// write -> MFMA read wait states are only inserted for instructions the
-// compiler's hazard recognizer can see.
-__device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t c) {
-  return (x & vgpr_const(m)) | vgpr_const(c);
-}
+// (x & m) | c is one v_and_or_b32.  gfx9 VOP3 has no literal operand, so the
+// mask and the exponent pattern live in VGPRs (PlanRegs, materialized once
+// per kernel); with literal operands the compiler would split it into
+// v_and_b32 + v_or_b32.  The instruction itself must come from the compiler,
+// not from inline asm: its result feeds MFMA source operands, and the
+// required VALU write -> MFMA read wait states are only inserted for
+// instructions the compiler's hazard recognizer can see.
+
+// The distinct (mask, exponent pattern) pairs of a plan (4 for 4-bit, 5 for
+// 2- and 3-bit) and which one each code pair uses.
+template <int BITS>
+struct PlanConsts {
+  static constexpr int N = Plan<BITS>::NPAIR;
+  int idx[N] = {};
+  int nd = 0;
+  uint32_t mask[N] = {}, magic[N] = {};
+  constexpr PlanConsts() {
+    for (int k = 0; k < N; ++k) {
+      const uint32_t m = mask_of<BITS>(k), c = magic_of<BITS>(k);
+      int j = 0;
+      while (j < nd && !(mask[j] == m && magic[j] == c)) ++j;
+      if (j == nd) {
+        mask[nd] = m;
+        magic[nd] = c;
+        ++nd;
+      }
+      idx[k] = j;
+    }
+  }
+};
+
+// A plan's constants held in VGPRs, materialized once per kernel (the VGPR
+// operands of v_and_or_b32).
+template <int BITS>
+struct PlanRegs {
+  static constexpr PlanConsts<BITS> PC{};
+  uint32_t m[PC.nd], c[PC.nd];
+  __device__ __forceinline__ PlanRegs() {
+#pragma unroll
+    for (int j = 0; j < PC.nd; ++j) {
+      m[j] = vgpr_const(PC.mask[j]);
+      c[j] = vgpr_const(PC.magic[j]);
+    }
+  }
+};
 
 template <int BITS, int K>
-__device__ __forceinline__ h2_t extract_pair(const uint32_t* w) {
+__device__ __forceinline__ h2_t extract_pair(const uint32_t* w, const PlanRegs<BITS>& pr) {
   constexpr int S = Plan<BITS>::S[K];
-  const uint32_t x = and_or(window<BITS, S>(w), mask_of<BITS>(K), magic_of<BITS>(K));
+  constexpr int J = PlanRegs<BITS>::PC.idx[K];
+  const uint32_t x = (window<BITS, S>(w) & pr.m[J]) | pr.c[J];  // one v_and_or_b32
   return __builtin_bit_cast(h2_t, x);
 }
 
 // The pair's two codes as exact fp16 integers (bias removed).
 template <int BITS, int K>
-__device__ __forceinline__ h2_t extract_codes(const uint32_t* w) {
+__device__ __forceinline__ h2_t extract_codes(const uint32_t* w, const PlanRegs<BITS>& pr) {
   constexpr h2_t bias = {_Float16(bias_a<BITS>(K)), _Float16(bias_c<BITS>(K))};
-  return extract_pair<BITS, K>(w) - bias;
+  return extract_pair<BITS, K>(w, pr) - bias;
 }
 
 __device__ __forceinline__ h2_t h2_from_halves(__half a, __half b) {
@@ -137,8 +173,75 @@ __device__ __forceinline__ float round_f16(float x) {
 }
 
 // ---------------------------------------------------------------------------
-// wave64 reductions (DPP/permute through the compiler's shuffle lowering)
+// wave64 reductions
 // ---------------------------------------------------------------------------
+// Wave reductions with six DPP steps (no LDS traffic): pairs (quad_perm
+// 1,0,3,2), quads (2,3,0,1), 8 lanes (row_half_mirror), rows of 16
+// (row_mirror), then row_bcast:15 and row_bcast:31 fold rows 0-1 and 2-3 so
+// that lane 63 holds the result, which is returned to every lane.  Every step
+// runs on all four rows (rows without a broadcast source read 0); only lane
+// 63 is meaningful after the broadcasts, and every lane it depends on has a
+// source.  N independent reductions advance together, so the operands of
+// each DPP step are ready without wait states, and each step is one DPP VALU
+// instruction.
+template <int CTRL, int N>
+__device__ __forceinline__ void sum_step(float (&v)[N]) {
+#pragma unroll
+  for (int i = 0; i < N; ++i)
+    v[i] += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v[i]), CTRL, 0xf, 0xf,
+                                                                  true));
+}
+template <int CTRL, int N>
+__device__ __forceinline__ void max_step(int (&v)[N]) {
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = max(v[i], __builtin_amdgcn_update_dpp(0, v[i], CTRL, 0xf, 0xf, true));
+}
+
+// float <-> int with the same order (for non-NaN values): negative floats
+// have their magnitude bits reversed.  The map is its own inverse.
+__device__ __forceinline__ int f2ord(float f) {
+  const int i = __builtin_bit_cast(int, f);
+  return i ^ ((i >> 31) & 0x7fffffff);
+}
+__device__ __forceinline__ float ord2f(int i) { return __builtin_bit_cast(float, i ^ ((i >> 31) & 0x7fffffff)); }
+
+template <int N>
+__device__ __forceinline__ void wave_sum_dpp(float (&v)[N]) {
+  sum_step<0xb1>(v);
+  sum_step<0x4e>(v);
+  sum_step<0x141>(v);
+  sum_step<0x140>(v);
+  sum_step<0x142>(v);
+  sum_step<0x143>(v);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v[i]), 63));
+}
+// max of non-NaN values (-inf allowed)
+template <int N>
+__device__ __forceinline__ void wave_max_dpp(float (&v)[N]) {
+  int o[N];
+#pragma unroll
+  for (int i = 0; i < N; ++i) o[i] = f2ord(v[i]);
+  max_step<0xb1>(o);
+  max_step<0x4e>(o);
+  max_step<0x141>(o);
+  max_step<0x140>(o);
+  max_step<0x142>(o);
+  max_step<0x143>(o);
+#pragma unroll
+  for (int i = 0; i < N; ++i) v[i] = ord2f(__builtin_amdgcn_readlane(o[i], 63));
+}
+
+// Orders one wave's LDS accesses around a point where lanes read what other
+// lanes of the same wave wrote: a wave's LDS instructions execute in order,
+// so only the compiler has to be kept from moving them.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// wave64 reductions through the compiler's shuffle lowering
 __device__ __forceinline__ float wave_max(float v) {
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));

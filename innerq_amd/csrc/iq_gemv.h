@@ -139,7 +139,8 @@ __device__ __forceinline__ h4_t cat_h2(h2_t lo, h2_t hi) { return __builtin_shuf
 // past NREP read as zero), B from the NB code-word sets.
 template <int BITS, int W, int NREP, int NB, int K0, typename P, int... K>
 __device__ __forceinline__ void mfma_chunk(const uint32_t (&w)[NB][W], P rec, int NP, int hl,
-                                           f4_t (&dv)[NB][(NREP + 3) / 4], std::integer_sequence<int, K...>) {
+                                           const PlanRegs<BITS>& pr, f4_t (&dv)[NB][(NREP + 3) / 4],
+                                           std::integer_sequence<int, K...>) {
   constexpr int NPS = Plan<BITS>::NPAIR;
   constexpr int SBW = Plan<BITS>::WORDS;
   constexpr int CH = sizeof...(K);
@@ -160,7 +161,7 @@ __device__ __forceinline__ void mfma_chunk(const uint32_t (&w)[NB][W], P rec, in
   (
       [&] {
 #pragma unroll
-        for (int j = 0; j < NB; ++j) x[j][K] = extract_codes<BITS, (K0 + K) % NPS>(&w[j][((K0 + K) / NPS) * SBW]);
+        for (int j = 0; j < NB; ++j) x[j][K] = extract_codes<BITS, (K0 + K) % NPS>(&w[j][((K0 + K) / NPS) * SBW], pr);
       }(),
       ...);
 #pragma unroll
@@ -176,11 +177,12 @@ __device__ __forceinline__ void mfma_chunk(const uint32_t (&w)[NB][W], P rec, in
 
 template <int BITS, int G, int NREP, int NB, int C, int NCH, typename P>
 __device__ __forceinline__ void mfma_chunks(const uint32_t (&w)[NB][G * BITS / 32], P rec, int hl,
-                                            f4_t (&dv)[NB][(NREP + 3) / 4]) {
+                                            const PlanRegs<BITS>& pr, f4_t (&dv)[NB][(NREP + 3) / 4]) {
   if constexpr (C < NCH) {
     constexpr int CH = (G / 2) / NCH;
-    mfma_chunk<BITS, G * BITS / 32, NREP, NB, C * CH>(w, rec, G / 2, hl, dv, std::make_integer_sequence<int, CH>{});
-    mfma_chunks<BITS, G, NREP, NB, C + 1, NCH>(w, rec, hl, dv);
+    mfma_chunk<BITS, G * BITS / 32, NREP, NB, C * CH>(w, rec, G / 2, hl, pr, dv,
+                                                      std::make_integer_sequence<int, CH>{});
+    mfma_chunks<BITS, G, NREP, NB, C + 1, NCH>(w, rec, hl, pr, dv);
   }
 }
 
@@ -205,20 +207,25 @@ __host__ __device__ constexpr int qrec_osum() {
 
 // pair (ia, ic) of query row qrow (and norm row nrow, or null): writes the hi
 // pair to *hi and, with a norm, the lo pair to *lo; adds the pair to sum.
-__device__ __forceinline__ void qrec_pair(const uint16_t* qrow, const uint16_t* nrow, int ia, int ic, uint32_t* hi,
-                                          uint32_t* lo, float& sum) {
-  if (!nrow) {
-    const uint16_t ua = qrow[ia], uc = qrow[ic];
+// the same from already loaded fp16 values (na, nc ignored without a norm)
+__device__ __forceinline__ void qrec_pair_vals(uint16_t ua, uint16_t uc, uint16_t na, uint16_t nc, bool norm,
+                                               uint32_t* hi, uint32_t* lo, float& sum) {
+  if (!norm) {
     *hi = uint32_t(ua) | (uint32_t(uc) << 16);
     sum += h2f(ua) + h2f(uc);
     return;
   }
-  const float qa = h2f(qrow[ia]) * h2f(nrow[ia]), qc = h2f(qrow[ic]) * h2f(nrow[ic]);  // exact
+  const float qa = h2f(ua) * h2f(na), qc = h2f(uc) * h2f(nc);  // exact
   const uint16_t ha = __half_as_ushort(__float2half_rn(qa)), hc = __half_as_ushort(__float2half_rn(qc));
   *hi = uint32_t(ha) | (uint32_t(hc) << 16);
   *lo = uint32_t(__half_as_ushort(__float2half_rn(qa - h2f(ha)))) |
         (uint32_t(__half_as_ushort(__float2half_rn(qc - h2f(hc)))) << 16);
   sum += qa + qc;
+}
+__device__ __forceinline__ void qrec_pair(const uint16_t* qrow, const uint16_t* nrow, int ia, int ic, uint32_t* hi,
+                                          uint32_t* lo, float& sum) {
+  qrec_pair_vals(qrow[ia], qrow[ic], nrow ? nrow[ia] : uint16_t(0), nrow ? nrow[ic] : uint16_t(0), nrow != nullptr,
+                 hi, lo, sum);
 }
 
 // dv[j][q][i] = sum over the group's pairs of opnd(head 4q+i) . codes(set j),
@@ -227,31 +234,31 @@ __device__ __forceinline__ void qrec_pair(const uint16_t* qrow, const uint16_t* 
 // codes stay within IQ_MFMA_CH*NB VGPRs.
 template <int BITS, int G, int NREP, int NB, typename P>
 __device__ __forceinline__ void group_mfma(const uint32_t (&w)[NB][G * BITS / 32], P rec, int hl,
-                                           f4_t (&dv)[NB][(NREP + 3) / 4]) {
+                                           const PlanRegs<BITS>& pr, f4_t (&dv)[NB][(NREP + 3) / 4]) {
   constexpr int NP = G / 2;
   constexpr int NCH = NP <= IQ_MFMA_CH ? 1 : NP / IQ_MFMA_CH;
 #pragma unroll
   for (int j = 0; j < NB; ++j)
 #pragma unroll
     for (int q = 0; q < (NREP + 3) / 4; ++q) dv[j][q] = f4_t{0.f, 0.f, 0.f, 0.f};
-  mfma_chunks<BITS, G, NREP, NB, 0, NCH>(w, rec, hl, dv);
+  mfma_chunks<BITS, G, NREP, NB, 0, NCH>(w, rec, hl, pr, dv);
 }
 
 // Query dot products of NB code sets: d[j][h] = sum_i q'[h,i] c_j[i] over the
 // group, from the hi rows or, when split, hi + lo rows of the query record.
 template <int BITS, int G, int NREP, int NB, typename P>
 __device__ __forceinline__ void qk_group_dot(const uint32_t (&w)[NB][G * BITS / 32], P rec, int hl, bool split,
-                                             float (&d)[NB][NREP]) {
+                                             const PlanRegs<BITS>& pr, float (&d)[NB][NREP]) {
   if (split) {
     f4_t dv[NB][(2 * NREP + 3) / 4];
-    group_mfma<BITS, G, 2 * NREP, NB>(w, rec, hl, dv);
+    group_mfma<BITS, G, 2 * NREP, NB>(w, rec, hl, pr, dv);
 #pragma unroll
     for (int j = 0; j < NB; ++j)
 #pragma unroll
       for (int h = 0; h < NREP; ++h) d[j][h] = dv[j][h / 4][h % 4] + dv[j][(NREP + h) / 4][(NREP + h) % 4];
   } else {
     f4_t dv[NB][(NREP + 3) / 4];
-    group_mfma<BITS, G, NREP, NB>(w, rec, hl, dv);
+    group_mfma<BITS, G, NREP, NB>(w, rec, hl, pr, dv);
 #pragma unroll
     for (int j = 0; j < NB; ++j)
 #pragma unroll
@@ -306,6 +313,7 @@ struct FusedStore {
   int t0;  // first store token of the range
   int bits, group, mode;
 };
+bool flash_fused_supported(const void* q, int64_t sq_b, int64_t sq_h, const void* norm);
 int flash_fused_launch(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, const FusedStore& k,
                        const FusedStore& v, int B, int Hq, int Hkv, int T, int D, float scale, float* ml,
                        float* part, hipStream_t stream);

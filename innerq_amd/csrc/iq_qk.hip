@@ -123,6 +123,7 @@ __global__ __launch_bounds__(WG) void qk_kernel(QKArgs a) {
 #pragma unroll
     for (int h = 0; h < NREP; ++h) acc[j][h] = 0.f;
 
+  const PlanRegs<BITS> pr;
   // A runtime loop: each group's operand records are loaded inside its own
   // iteration, so at most one chunk of them occupies SGPRs.
 #pragma unroll 1
@@ -142,7 +143,7 @@ __global__ __launch_bounds__(WG) void qk_kernel(QKArgs a) {
       for (int j = 0; j < BPW; ++j) to_offset_binary<BITS>(cw[j], W);
     }
     float d[BPW][NREP];
-    qk_group_dot<BITS, G, NREP, BPW>(cw, a.rec + (int64_t(bh) * NG + g) * RD, lane & 3, a.split, d);
+    qk_group_dot<BITS, G, NREP, BPW>(cw, a.rec + (int64_t(bh) * NG + g) * RD, lane & 3, a.split, pr, d);
 #pragma unroll
     for (int j = 0; j < BPW; ++j) {
       const float s = h2f(uint16_t(cm[j] & 0xffffu));
