@@ -15,7 +15,9 @@
  *    caller passes any workspace, sized by the matching *_workspace_bytes().
  *  - Every entry point validates its arguments on the host before any launch
  *    and returns 0 (IQ_OK) or a negative IQ_ERR_* code; iq_strerror() names it.
- *  - bits in {2,3,4}; group in {32,64,128}; head_dim D in {64,128};
+ *  - bits in {2,3,4} (packed-store quantize / dequantize / unpack entry
+ *    points also take 1 with IQ_MODE_ASYM: the asym half of 2-bit hybrid
+ *    quantization, quant.py:136); group in {32,64,128}; head_dim D in {64,128};
  *    query heads per KV head (Hq/Hkv) in {1,2,4,8}; mode IQ_MODE_ASYM or
  *    IQ_MODE_SYM (quant.py:43-56 'asymmetric' / 'symmetric').
  *
@@ -46,7 +48,7 @@ extern "C" {
 enum iq_status {
   IQ_OK = 0,
   IQ_ERR_NULL = -1,       /* a required pointer is NULL */
-  IQ_ERR_BITS = -2,       /* bits not in {2,3,4} */
+  IQ_ERR_BITS = -2,       /* bits not in {2,3,4} (1 allowed for asym packed stores) */
   IQ_ERR_GROUP = -3,      /* group not in {32,64,128} or does not divide the grouped axis */
   IQ_ERR_SHAPE = -4,      /* a size is negative / zero where not allowed / unsupported head_dim or GQA ratio */
   IQ_ERR_ALIGN = -5,      /* pointer or stride not aligned as the kernel needs */
@@ -121,6 +123,41 @@ int iq_dequant_v(const uint32_t* v_codes, const uint16_t* v_meta, int64_t t_cap,
  * callers holding reference-format codes. */
 int iq_dequant_dense(const int32_t* codes, const void* scale16, const void* zs16, int64_t outer, int64_t n,
                      int64_t inner, int group, int mode, int out_f16, void* out, void* stream);
+
+/* Reference-format tensors of store tokens [t0, t0+T): int32 codes [B,H,T,D]
+ * (sym: magnitudes), fp16 scale and fp16 zero point (asym) or fp16 sign
+ * tensor [B,H,T,D] (sym; 0 where the code is 0, whose sign the packed form
+ * does not keep), all contiguous.  K: scale/zero [B,H,T,D/G]; V (t0, T
+ * multiples of group): scale/zero [B,H,T/G,D].  Backs the state attributes
+ * keys_q / keys_scale_factor / keys_zp_sign (and values_*) of
+ * cache.py:190-210 for callers that read them. */
+int iq_unpack_k(const uint32_t* k_codes, const uint16_t* k_meta, int64_t t_cap, int B, int H, int t0, int T, int D,
+                int group, int bits, int mode, int32_t* codes_i32, void* scale16, void* zs16, void* stream);
+int iq_unpack_v(const uint32_t* v_codes, const uint16_t* v_meta, int64_t t_cap, int B, int H, int t0, int T, int D,
+                int group, int bits, int mode, int32_t* codes_i32, void* scale16, void* zs16, void* stream);
+
+/* Key normalization factor out16[b,h,d] = fp16(sqrt(max_t |k[b,h,t,d]|)) over
+ * T tokens of k (fp16, element strides sk_b, sk_h, sk_t; D contiguous).
+ * Replaces key_states.abs().max(dim=-2).values.sqrt() (cache.py:121-126). */
+int iq_key_norm_factor(const void* k, int64_t sk_b, int64_t sk_h, int64_t sk_t, int B, int H, int T, int D,
+                       void* out16, void* stream);
+
+/* Hybrid quantization (quant.py:133-176): per group, mask = L1 error of the
+ * asym dequantization > L1 error of the sym one, i.e. use the sym codes.
+ * x16: the quantizer's fp16 input [BH,T,D] (divided by norm16 [BH,D] in fp16
+ * first when non-NULL, as the quantizer does); deq_a, deq_s: fp32 [BH,T,D]
+ * dequantizations of the asym (bits-1) and sym (bits) codes.  axis 0: groups
+ * along D, mask uint8 [BH,T,D/G]; axis 1: groups along T, mask [BH,T/G,D].
+ * Error sums are accumulated in fp64 (the reference sums fp32 in torch's
+ * reduction order; exact ties may resolve differently). */
+int iq_hybrid_mask(const void* x16, const void* norm16, const float* deq_a, const float* deq_s, int64_t BH, int T,
+                   int D, int group, int axis, uint8_t* mask, void* stream);
+
+/* out = mask ? deq_s : deq_a elementwise over [BH,T,D] (mask as produced by
+ * iq_hybrid_mask), written as fp32 (out_f16 = 0) or fp16 (out_f16 = 1).
+ * Replaces the torch.where of dequantize_hybrid (quant.py:153-176). */
+int iq_hybrid_select(const float* deq_a, const float* deq_s, const uint8_t* mask, int64_t BH, int T, int D, int group,
+                     int axis, int out_f16, void* out, void* stream);
 
 /* Decode QK^T GEMV over a packed K store: for store tokens [t0, t0+T),
  *   out[b, h, t] = scale * sum_g ( s_g * sum_{i in g} q'[b,h,i] c[t,i] + z_g * sum_{i in g} q'[b,h,i] )

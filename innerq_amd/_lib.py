@@ -59,6 +59,11 @@ SIGNATURES = {
     "iq_dequant_k": (I, [P, P, L, P, I, I, I, I, I, I, I, I, P, P, L, L, L, P]),
     "iq_dequant_v": (I, [P, P, L, I, I, I, I, I, I, I, I, P, P, L, L, L, P]),
     "iq_dequant_dense": (I, [P, P, P, L, L, L, I, I, I, P, P]),
+    "iq_unpack_k": (I, [P, P, L, I, I, I, I, I, I, I, I, P, P, P, P]),
+    "iq_unpack_v": (I, [P, P, L, I, I, I, I, I, I, I, I, P, P, P, P]),
+    "iq_key_norm_factor": (I, [P, L, L, L, I, I, I, I, P, P]),
+    "iq_hybrid_mask": (I, [P, P, P, P, L, I, I, I, I, P, P]),
+    "iq_hybrid_select": (I, [P, P, P, L, I, I, I, I, I, P, P]),
     "iq_qk_gemv": (I, [P, L, L, P, P, P, L, I, I, I, I, I, I, I, I, I, F, P, L, L, P, S, P]),
     "iq_qk_workspace_bytes": (S, [I, I, I]),
     "iq_av_workspace_bytes": (S, [I, I, I, I, I]),

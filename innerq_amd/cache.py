@@ -1,0 +1,442 @@
+"""Drop-in for the reference's ``innerq.cache`` (src/innerq/cache.py) on MI355X.
+
+``InnerqDynamicLayer``, ``InnerqDynamicSlidingWindowLayer`` and
+``DynamicCache`` keep the reference's configuration attributes, state machine
+(sinks, recent windows, flush of the oldest tokens, key normalization) and
+``update()`` contract: the first call returns its inputs, later calls return
+the dense fp16 K and V of [sink | dequantized | recent] (cache.py:235-281,
+382-396), bit-identical to the reference's.
+
+What differs is the storage: quantized tokens are kept packed (2/3/4-bit
+codes + fp16 scale/zero) in ``ops.PackedStore`` and quantized on append by the
+gfx950 kernels, instead of int32 code tensors grown with torch.cat.  The
+reference's state attributes ``keys_q`` / ``keys_scale_factor`` /
+``keys_zp_sign`` (and ``values_*``) are read-only views unpacked on access.
+
+Two methods serve the fused decode path, which the reference does not have:
+``append(k, v)`` advances the state without materializing K and V, and
+``attend(q, scaling)`` runs softmax(q K^T * scaling) V over [sink | packed |
+recent] in one gfx950 decode kernel chain (ops.decode_attention).
+"""
+from __future__ import annotations
+
+from collections.abc import Iterable
+from typing import Any, Optional
+
+import torch
+from transformers.cache_utils import Cache, CacheLayerMixin
+
+from . import ops
+from .quant import QMode
+
+
+class _Quantized:
+    """The packed tokens of one role (K or V) of a layer.
+
+    axis 'channel' groups along head_dim (quant.py:75-77), 'token' along tokens
+    (quant.py:79-81).  Hybrid keeps an asym store (bits-1), a sym store (bits)
+    and the per-group choice (quant.py:133-176).
+    """
+
+    def __init__(self, axis: str, like: torch.Tensor, group: int, bits: int, mode: QMode):
+        B, H, _, D = like.shape
+        self.axis, self.group, self.bits, self.mode = axis, group, bits, mode
+        dev = like.device
+        if mode == QMode.HYBRID:
+            self.zp = ops.PackedStore(axis, B, H, D, group, bits - 1, "asymmetric", dev)
+            self.nozp = ops.PackedStore(axis, B, H, D, group, bits, "symmetric", dev)
+            self.mask: Optional[torch.Tensor] = None
+            self.store = None
+        else:
+            self.store = ops.PackedStore(axis, B, H, D, group, bits, mode.value, dev)
+
+    @property
+    def length(self) -> int:
+        return (self.store or self.zp).length
+
+    def append(self, x: torch.Tensor, norm: Optional[torch.Tensor]) -> None:
+        """Quantize x [B,H,n,D] (divided by norm in fp16 first, keys only) and append it."""
+        if norm is not None and self.axis != "channel":
+            raise NotImplementedError("key normalization is supported for keys grouped along head_dim")
+        if self.mode != QMode.HYBRID:
+            self.store.append(x, norm=norm)
+            return
+        t0, n = self.zp.length, x.shape[2]
+        self.zp.append(x, norm=norm)
+        self.nozp.append(x, norm=norm)
+        da = self.zp.dequant(t0, n, dtype=torch.float32)
+        ds = self.nozp.dequant(t0, n, dtype=torch.float32)
+        mask = ops.hybrid_mask(x.contiguous(), da, ds, self.group, self.axis, norm=norm)
+        self.mask = mask if self.mask is None else torch.cat([self.mask, mask], dim=2)
+
+    def dequant_into(self, out: torch.Tensor, norm: Optional[torch.Tensor]) -> None:
+        """Dense values (times norm) of every packed token, written into the fp16 view ``out``."""
+        if self.mode != QMode.HYBRID:
+            self.store.dequant(0, self.length, out=out, norm=norm)
+            return
+        da = self.zp.dequant(dtype=torch.float32, norm=norm)
+        ds = self.nozp.dequant(dtype=torch.float32, norm=norm)
+        out.copy_(ops.hybrid_select(da, ds, self.mask, self.group, self.axis, dtype=out.dtype))
+
+    def reference_tensors(self):
+        """(codes, scale, zero|signs) as quant.py returns them (dicts for hybrid)."""
+        if self.mode != QMode.HYBRID:
+            return ops.unpack_store(self.store)
+        cz, sz, zz = ops.unpack_store(self.zp)
+        cs, ss, gs = ops.unpack_store(self.nozp)
+        return {'zp': cz, 'nozp': cs}, {'zp': sz, 'nozp': ss, 'mask': self.mask}, {'zp': zz, 'nozp': gs}
+
+
+class InnerqDynamicLayer(CacheLayerMixin):
+    """cache.py:60-419 with packed quantized storage."""
+    is_sliding = False
+
+    def __init__(self, config, layer_idx):
+        self.parse_config(config)
+        self.layer_idx = layer_idx
+        self.cumulative_length = 0
+        super().__init__()
+
+    def parse_config(self, config):
+        """The reference's 15 configuration attributes and defaults (cache.py:71-91)."""
+        self.key_bits = getattr(config, 'k_bits', 16)
+        self.value_bits = getattr(config, 'v_bits', 16)
+        self.key_quantize = False if self.key_bits >= 16 else True
+        self.value_quantize = False if self.value_bits >= 16 else True
+
+        self.key_group_size = getattr(config, 'key_group_size', 32)
+        self.value_group_size = getattr(config, 'value_group_size', 32)
+        self.key_w_recent = getattr(config, 'key_w_recent', 32)
+        self.value_w_recent = getattr(config, 'value_w_recent', 32)
+        self.key_w_sink = getattr(config, 'key_w_sink', 0)
+        self.value_w_sink = getattr(config, 'value_w_sink', 0)
+        self.key_flush_size = getattr(config, 'key_flush_size', 32)
+        self.value_flush_size = getattr(config, 'value_flush_size', 32)
+        self.key_normalize = getattr(config, 'key_normalize', False)
+        self.key_normalization_factor = None
+
+        self.key_quantize_over_token = getattr(config, 'key_quantize_over_token', False)
+        self.value_quantize_over_token = getattr(config, 'value_quantize_over_token', True)
+
+        self.key_quantize_mode = QMode.from_str(getattr(config, 'key_quantize_mode', 'symmetric'))
+        self.value_quantize_mode = QMode.from_str(getattr(config, 'value_quantize_mode', 'symmetric'))
+        self._kq: Optional[_Quantized] = None
+        self._vq: Optional[_Quantized] = None
+
+    # ---- reference state attributes (read-only views of the packed stores) ----
+    def _ref(self, q: Optional[_Quantized], i: int):
+        return None if q is None or q.length == 0 else q.reference_tensors()[i]
+
+    @property
+    def keys_q(self):
+        return self._ref(self._kq, 0)
+
+    @property
+    def keys_scale_factor(self):
+        return self._ref(self._kq, 1)
+
+    @property
+    def keys_zp_sign(self):
+        return self._ref(self._kq, 2)
+
+    @property
+    def values_q(self):
+        return self._ref(self._vq, 0)
+
+    @property
+    def values_scale_factor(self):
+        return self._ref(self._vq, 1)
+
+    @property
+    def values_zp_sign(self):
+        return self._ref(self._vq, 2)
+
+    # ---- prefill (cache.py:121-233) ----
+    def normalize_keys(self, key_states: torch.Tensor) -> Optional[torch.Tensor]:
+        """The key normalization factor for these keys (computed once, cache.py:121-126);
+        the division itself happens in the quantize kernel."""
+        if not self.key_normalize:
+            return None
+        if self.key_normalization_factor is None:
+            self.key_normalization_factor = ops.key_norm_factor(key_states)
+        return self.key_normalization_factor
+
+    def initialize_keys_sink(self, key_states: torch.Tensor) -> torch.Tensor:
+        viable_w_sink_key = min(self.key_w_sink, key_states.shape[-2])
+        if self.key_quantize:
+            self.keys_sink = key_states[:, :, :viable_w_sink_key]
+            key_states = key_states[:, :, viable_w_sink_key:]
+        else:
+            shape = list(key_states.shape)
+            shape[-2] = 0
+            self.keys_sink = torch.zeros(shape, dtype=self.dtype, device=self.device)
+        return key_states
+
+    def initialize_values_sink(self, value_states: torch.Tensor) -> torch.Tensor:
+        viable_w_sink_value = min(self.value_w_sink, value_states.shape[-2])
+        if self.value_quantize:
+            self.values_sink = value_states[:, :, :viable_w_sink_value]
+            value_states = value_states[:, :, viable_w_sink_value:]
+        else:
+            shape = list(value_states.shape)
+            shape[-2] = 0
+            self.values_sink = torch.zeros(shape, dtype=self.dtype, device=self.device)
+        return value_states
+
+    def initialize_keys_recent(self, key_states: torch.Tensor) -> torch.Tensor:
+        if self.key_quantize:
+            viable_recent_size_key = min(self.key_w_recent, key_states.shape[-2])
+            if self.key_quantize_over_token:
+                while (key_states.shape[-2] - viable_recent_size_key) % self.key_flush_size != 0:
+                    viable_recent_size_key -= 1
+        else:
+            viable_recent_size_key = key_states.shape[-2]
+        nq = key_states.shape[-2] - viable_recent_size_key
+        self.keys_recent = key_states[:, :, nq:, :].contiguous()
+        return key_states[:, :, :nq, :].contiguous()
+
+    def initialize_values_recent(self, value_states: torch.Tensor) -> torch.Tensor:
+        if self.value_quantize:
+            viable_recent_size_value = min(self.value_w_recent, value_states.shape[-2])
+            if self.value_quantize_over_token:
+                while (value_states.shape[-2] - viable_recent_size_value) % self.value_flush_size != 0:
+                    viable_recent_size_value -= 1
+        else:
+            viable_recent_size_value = value_states.shape[-2]
+        nq = value_states.shape[-2] - viable_recent_size_value
+        self.values_recent = value_states[:, :, nq:, :].contiguous()
+        return value_states[:, :, :nq, :].contiguous()
+
+    def _quantize_keys(self, key_states: torch.Tensor) -> None:
+        if key_states.numel() == 0:
+            return
+        norm = self.normalize_keys(key_states)
+        if self._kq is None:
+            axis = "token" if self.key_quantize_over_token else "channel"
+            self._kq = _Quantized(axis, key_states, self.key_group_size, self.key_bits, self.key_quantize_mode)
+        self._kq.append(key_states, norm)
+
+    def _quantize_values(self, value_states: torch.Tensor) -> None:
+        if value_states.numel() == 0:
+            return
+        if self._vq is None:
+            axis = "token" if self.value_quantize_over_token else "channel"
+            self._vq = _Quantized(axis, value_states, self.value_group_size, self.value_bits,
+                                  self.value_quantize_mode)
+        self._vq.append(value_states, None)
+
+    def initialize_keys_q(self, key_states: torch.Tensor) -> None:
+        if self.key_quantize:
+            self._quantize_keys(key_states)
+
+    def initialize_values_q(self, value_states: torch.Tensor) -> None:
+        if self.value_quantize:
+            self._quantize_values(value_states)
+
+    def lazy_initialization(self, key_states: torch.Tensor, value_states: torch.Tensor) -> None:
+        ops.require_device(key_states, "key_states")
+        ops.require_device(value_states, "value_states")
+        self.dtype, self.device = key_states.dtype, key_states.device
+        key_states = self.initialize_keys_sink(key_states)
+        value_states = self.initialize_values_sink(value_states)
+        key_states = self.initialize_keys_recent(key_states)
+        value_states = self.initialize_values_recent(value_states)
+        self.initialize_keys_q(key_states)
+        self.initialize_values_q(value_states)
+        self.is_initialized = True
+
+    # ---- decode (cache.py:283-396) ----
+    def update_keys_recent(self, key_states: torch.Tensor) -> torch.Tensor:
+        self.keys_recent = torch.cat([self.keys_recent, key_states], dim=-2)
+        n = self.key_flush_size if self.key_quantize and self.keys_recent.shape[-2] >= self.key_flush_size else 0
+        key_states = self.keys_recent[:, :, :n]
+        self.keys_recent = self.keys_recent[:, :, n:]
+        return key_states
+
+    def update_values_recent(self, value_states: torch.Tensor) -> torch.Tensor:
+        self.values_recent = torch.cat([self.values_recent, value_states], dim=-2)
+        n = (self.value_flush_size
+             if self.value_quantize and self.values_recent.shape[-2] >= self.value_flush_size else 0)
+        value_states = self.values_recent[:, :, :n]
+        self.values_recent = self.values_recent[:, :, n:]
+        return value_states
+
+    def add_to_cache(self, key_states: torch.Tensor, value_states: torch.Tensor) -> None:
+        key_states = self.update_keys_recent(key_states)
+        value_states = self.update_values_recent(value_states)
+        if key_states.numel() != 0:
+            self._quantize_keys(key_states)
+        if value_states.numel() != 0:
+            self._quantize_values(value_states)
+
+    def _dense(self, sink, q: Optional[_Quantized], recent, norm, dtype) -> torch.Tensor:
+        """[sink | dequantized (times norm) | recent] in dtype: one rounding of the
+        fp32 dequantized values, as the reference's cat + .to(dtype)."""
+        ns, nq, nr = sink.shape[-2], (q.length if q is not None else 0), recent.shape[-2]
+        B, H, _, D = recent.shape
+        out = torch.empty(B, H, ns + nq + nr, D, dtype=dtype, device=self.device)
+        if ns:
+            out[:, :, :ns].copy_(sink)
+        if nq:
+            q.dequant_into(out[:, :, ns:ns + nq], norm)
+        if nr:
+            out[:, :, ns + nq:].copy_(recent)
+        return out
+
+    def _deq_dtype(self, q: Optional[_Quantized]):
+        # cache.py:235-281: fp32 once a dequantized segment joins the cat
+        return torch.float32 if q is not None and q.length else self.dtype
+
+    def get_keys_deq(self) -> torch.Tensor:
+        return self._dense(self.keys_sink, self._kq, self.keys_recent, self.key_normalization_factor,
+                           self._deq_dtype(self._kq))
+
+    def get_values_deq(self) -> torch.Tensor:
+        return self._dense(self.values_sink, self._vq, self.values_recent, None, self._deq_dtype(self._vq))
+
+    def get_deq_tensors(self) -> tuple[torch.Tensor, torch.Tensor]:
+        # written in self.dtype directly: the same values as get_*_deq().to(self.dtype)
+        return (self._dense(self.keys_sink, self._kq, self.keys_recent, self.key_normalization_factor, self.dtype),
+                self._dense(self.values_sink, self._vq, self.values_recent, None, self.dtype))
+
+    def update(
+        self,
+        key_states: torch.Tensor,
+        value_states: torch.Tensor,
+        cache_kwargs: dict[str, Any] | None = None,
+    ) -> tuple[torch.Tensor, torch.Tensor]:
+        self.cumulative_length += key_states.shape[-2]
+        if not self.is_initialized:
+            self.lazy_initialization(key_states, value_states)
+            return key_states, value_states
+        self.add_to_cache(key_states, value_states)
+        return self.get_deq_tensors()
+
+    def append(self, key_states: torch.Tensor, value_states: torch.Tensor) -> None:
+        """update() without materializing K and V (for attend())."""
+        self.cumulative_length += key_states.shape[-2]
+        if not self.is_initialized:
+            self.lazy_initialization(key_states, value_states)
+        else:
+            self.add_to_cache(key_states, value_states)
+
+    def attend(self, query_states: torch.Tensor, scaling: float) -> torch.Tensor:
+        """Decode attention of one new token per sequence over this layer's cache:
+        softmax(q K^T * scaling, fp32) -> fp16 -> @ V (TF/models/llama/modeling_llama.py:201-210),
+        with K and V read packed.  query_states [B, Hq, 1, D] fp16 -> [B, Hq, 1, D] fp16."""
+        if query_states.dim() != 4 or query_states.shape[2] != 1:
+            raise ValueError("attend() takes one query token per sequence: [B, Hq, 1, D]")
+        if not self.is_initialized:
+            raise RuntimeError("attend() needs a prefilled cache")
+        for q, name, want in ((self._kq, "keys", "channel"), (self._vq, "values", "token")):
+            if q is not None and (q.mode == QMode.HYBRID or q.axis != want):
+                raise NotImplementedError(f"fused decode reads {name} grouped along the "
+                                          f"{'head_dim' if want == 'channel' else 'token'} axis, asym or sym")
+        q = query_states[:, :, 0]
+        out = ops.decode_attention(
+            q, self.keys_sink if self.keys_sink.shape[-2] else None, self._kq.store if self._kq else None,
+            self.keys_recent if self.keys_recent.shape[-2] else None,
+            self.values_sink if self.values_sink.shape[-2] else None, self._vq.store if self._vq else None,
+            self.values_recent if self.values_recent.shape[-2] else None, scaling,
+            norm=self.key_normalization_factor if self._kq is not None else None)
+        return out[:, :, None]
+
+    def get_mask_sizes(self, query_length) -> tuple[int, int]:
+        """(kv_length, kv_offset); takes the query length (transformers >= 5.15) or
+        the cache_position tensor (cache.py:398-402)."""
+        if isinstance(query_length, torch.Tensor):
+            query_length = query_length.shape[0]
+        return self.get_seq_length() + query_length, 0
+
+    def get_seq_length(self) -> int:
+        return self.cumulative_length
+
+    def get_max_length(self) -> int:
+        return -1
+
+    def get_max_cache_shape(self) -> int:
+        return -1
+
+    def crop(self, max_length: int) -> None:
+        raise ValueError('This function is not implementable for quantized cache. '
+                         'It leads to the loss of accuracy on the recent tokens')
+
+    def batch_repeat_interleave(self, repeats: int) -> None:
+        raise Exception('This function is not implemented yet.')
+
+    def batch_select_indices(self, indices: torch.Tensor) -> None:
+        raise Exception('This function is not implemented yet.')
+
+
+class InnerqDynamicSlidingWindowLayer(InnerqDynamicLayer):
+    """cache.py:421-461."""
+    is_sliding = True
+
+    def __init__(self, config, layer_idx: int, sliding_window: int):
+        super().__init__(config, layer_idx)
+        self.sliding_window = sliding_window
+        self.cumulative_length = 0
+        self._sliding_window_tensor = torch.tensor(self.sliding_window, dtype=torch.long)
+
+    def lazy_initialization(self, key_states: torch.Tensor, value_states: torch.Tensor) -> None:
+        super().lazy_initialization(key_states, value_states)
+        self._sliding_window_tensor = self._sliding_window_tensor.to(self.device)
+
+    def update(self, key_states, value_states, cache_kwargs=None):
+        full_key_states, full_value_states = super().update(key_states, value_states, cache_kwargs)
+        if self.cumulative_length - key_states.shape[-2] > self.sliding_window:
+            # the reference indexes a single token here (cache.py:443-444); kept as is
+            full_key_states = full_key_states[:, :, -self.sliding_window, :]
+            full_value_states = full_value_states[:, :, -self.sliding_window, :]
+        return full_key_states, full_value_states
+
+    def get_mask_sizes(self, query_length) -> tuple[int, int]:
+        if isinstance(query_length, torch.Tensor):
+            query_length = query_length.shape[0]
+        is_full = self.cumulative_length >= self.sliding_window
+        kv_offset = max(self.cumulative_length - self.sliding_window + 1, 0)
+        if is_full:
+            kv_length = self.sliding_window - 1 + query_length
+        else:
+            kv_length = self.cumulative_length + query_length
+        return kv_length, kv_offset
+
+    def get_max_length(self) -> int:
+        return self.sliding_window
+
+    def get_max_cache_shape(self) -> int:
+        return self.sliding_window
+
+
+class DynamicCache(Cache):
+    """cache.py:463-496: one InnerqDynamic(SlidingWindow)Layer per decoder layer."""
+
+    def __init__(
+        self,
+        ddp_cache_data: Iterable[tuple[torch.Tensor | None, ...]] | None = None,
+        config=None,
+        offloading: bool = False,
+        offload_only_non_sliding: bool = False,
+    ):
+        layers = []
+        if config is not None:
+            decoder_config = config.get_text_config(decoder=True)
+            sliding_window = getattr(decoder_config, "sliding_window", None) or getattr(
+                decoder_config, "attention_chunk_size", None)
+            layer_types = getattr(decoder_config, "layer_types", None)
+            if layer_types is None:
+                layer_types = ["sliding_attention" if sliding_window is not None else "full_attention"
+                               for _ in range(decoder_config.num_hidden_layers)]
+            if hasattr(decoder_config, "num_kv_shared_layers"):
+                layer_types = layer_types[: -decoder_config.num_kv_shared_layers]
+            for layer_idx, layer_type in enumerate(layer_types):
+                if layer_type in ("sliding_attention", "chunked_attention"):
+                    layers.append(InnerqDynamicSlidingWindowLayer(config=config, layer_idx=layer_idx,
+                                                                  sliding_window=sliding_window))
+                else:
+                    layers.append(InnerqDynamicLayer(config=config, layer_idx=layer_idx))
+        super().__init__(layers=layers, offloading=offloading, offload_only_non_sliding=offload_only_non_sliding)
+
+    def __iter__(self):
+        for layer in self.layers:
+            yield layer.keys, layer.values, getattr(layer, "_sliding_window_tensor", None)

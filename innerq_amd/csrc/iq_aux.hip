@@ -1,0 +1,138 @@
+// Cache-side helpers of the drop-in layer (gfx950): the key normalization
+// factor and the hybrid (asym / sym per group) selection.  Both run once per
+// prefill or flush, never in the decode GEMVs.
+#include "iq_common.h"
+#include "iq_device.h"
+
+using namespace iq;
+
+namespace {
+
+// out[bh, d] = fp16(sqrt(max_t |k[bh, t, d]|)): cache.py:121-126 computes
+// key_states.abs().max(dim=-2).values.sqrt() in fp16, i.e. the correctly
+// rounded fp32 square root of an fp16 value, rounded to fp16.
+__global__ __launch_bounds__(256) void key_norm_kernel(const uint16_t* __restrict__ k, int64_t skb, int64_t skh,
+                                                       int64_t skt, int H, int T, int D, int64_t n,
+                                                       uint16_t* __restrict__ out) {
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  const int d = int(i % D);
+  const int64_t bh = i / D;
+  const uint16_t* p = k + (bh / H) * skb + (bh % H) * skh + d;
+  float mx = 0.f;
+  for (int t = 0; t < T; ++t) mx = fmaxf(mx, fabsf(h2f(p[int64_t(t) * skt])));
+  out[i] = __half_as_ushort(__float2half_rn(__fsqrt_rn(mx)));
+}
+
+// Hybrid selection mask (quant.py:133-151): per group, the L1 error of the
+// asym dequantization exceeds that of the sym one.  x fp16 [BH, T, D] (the
+// quantizer's input; divided by norm [BH, D] in fp16 first when given, as
+// the quantizer does), deq_a / deq_s fp32 [BH, T, D] contiguous.  Groups along D
+// (axis 0, mask [BH, T, D/G]) or along T (axis 1, mask [BH, T/G, D]).  The
+// differences are fp32 like the reference's; the sums are accumulated in
+// fp64, which the oracle uses and which reproduced the reference's traces.
+__global__ __launch_bounds__(256) void hybrid_mask_kernel(const uint16_t* __restrict__ x,
+                                                          const uint16_t* __restrict__ norm,
+                                                          const float* __restrict__ da, const float* __restrict__ ds,
+                                                          int T, int D, int group, int axis, int64_t n,
+                                                          uint8_t* __restrict__ mask) {
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (i >= n) return;
+  int64_t bh, e0, step;
+  int dcol;  // a column of the group (for the norm)
+  if (axis == 0) {
+    const int ng = D / group;
+    const int64_t row = i / ng;  // bh * T + t
+    const int g = int(i % ng);
+    bh = row / T;
+    e0 = row * D + int64_t(g) * group;
+    step = 1;
+    dcol = g * group;
+  } else {
+    const int d = int(i % D);
+    const int64_t r = i / D;  // bh * (T / G) + gi
+    const int ngT = T / group;
+    bh = r / ngT;
+    e0 = (bh * T + (r % ngT) * group) * D + d;
+    step = D;
+    dcol = d;
+  }
+  double ea = 0.0, es = 0.0;
+  for (int j = 0; j < group; ++j) {
+    const int64_t e = e0 + j * step;
+    float v = h2f(x[e]);
+    if (norm) v = round_f16(v / h2f(norm[bh * D + dcol + (axis == 0 ? j : 0)]));
+    ea += double(fabsf(__fsub_rn(da[e], v)));
+    es += double(fabsf(__fsub_rn(ds[e], v)));
+  }
+  mask[i] = ea > es ? 1 : 0;
+}
+
+// out = mask ? deq_s : deq_a (quant.py:153-176 dequantize_hybrid), fp32 or fp16.
+__global__ __launch_bounds__(256) void hybrid_select_kernel(const float* __restrict__ da,
+                                                            const float* __restrict__ ds,
+                                                            const uint8_t* __restrict__ mask, int T, int D,
+                                                            int group, int axis, int64_t n, int out_f16,
+                                                            void* __restrict__ out) {
+  const int64_t e = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (e >= n) return;
+  const int d = int(e % D);
+  const int64_t row = e / D;  // bh * T + t
+  int64_t mi;
+  if (axis == 0) {
+    mi = row * (D / group) + d / group;
+  } else {
+    const int64_t bh = row / T;
+    const int t = int(row % T);
+    mi = (bh * (T / group) + t / group) * D + d;
+  }
+  const float v = mask[mi] ? ds[e] : da[e];
+  if (out_f16) static_cast<uint16_t*>(out)[e] = __half_as_ushort(__float2half_rn(v));
+  else static_cast<float*>(out)[e] = v;
+}
+
+int check_hybrid(int64_t BH, int T, int D, int group, int axis) {
+  IQ_CHECK(BH >= 0 && T >= 0 && D > 0, IQ_ERR_SHAPE);
+  IQ_CHECK(group > 0 && (axis == 0 || axis == 1), IQ_ERR_SHAPE);
+  IQ_CHECK(axis == 0 ? D % group == 0 : T % group == 0, IQ_ERR_GROUP);
+  return IQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int iq_key_norm_factor(const void* k, int64_t sk_b, int64_t sk_h, int64_t sk_t, int B, int H, int T, int D,
+                       void* out16, void* stream) {
+  IQ_CHECK(k && out16, IQ_ERR_NULL);
+  IQ_CHECK(B >= 0 && H >= 0 && T > 0 && D > 0, IQ_ERR_SHAPE);
+  const int64_t n = int64_t(B) * H * D;
+  if (n == 0) return IQ_OK;
+  key_norm_kernel<<<dim3(unsigned(ceil_div(n, 256))), 256, 0, (hipStream_t)stream>>>(
+      (const uint16_t*)k, sk_b, sk_h, sk_t, H, T, D, n, (uint16_t*)out16);
+  return launch_status();
+}
+
+int iq_hybrid_mask(const void* x16, const void* norm16, const float* deq_a, const float* deq_s, int64_t BH, int T,
+                   int D, int group, int axis, uint8_t* mask, void* stream) {
+  IQ_CHECK(x16 && deq_a && deq_s && mask, IQ_ERR_NULL);
+  if (int e = check_hybrid(BH, T, D, group, axis)) return e;
+  const int64_t n = axis == 0 ? BH * T * (D / group) : BH * (T / group) * D;
+  if (n == 0) return IQ_OK;
+  hybrid_mask_kernel<<<dim3(unsigned(ceil_div(n, 256))), 256, 0, (hipStream_t)stream>>>(
+      (const uint16_t*)x16, (const uint16_t*)norm16, deq_a, deq_s, T, D, group, axis, n, mask);
+  return launch_status();
+}
+
+int iq_hybrid_select(const float* deq_a, const float* deq_s, const uint8_t* mask, int64_t BH, int T, int D, int group,
+                     int axis, int out_f16, void* out, void* stream) {
+  IQ_CHECK(deq_a && deq_s && mask && out, IQ_ERR_NULL);
+  if (int e = check_hybrid(BH, T, D, group, axis)) return e;
+  const int64_t n = BH * T * int64_t(D);
+  if (n == 0) return IQ_OK;
+  hybrid_select_kernel<<<dim3(unsigned(ceil_div(n, 256))), 256, 0, (hipStream_t)stream>>>(
+      deq_a, deq_s, mask, T, D, group, axis, n, out_f16 ? 1 : 0, out);
+  return launch_status();
+}
+
+}  // extern "C"

@@ -29,6 +29,16 @@ inline int check_common(int bits, int group, int mode) {
   return IQ_OK;
 }
 
+// Packed stores also hold 1-bit asym codes: the asym half of 2-bit hybrid
+// quantization (quant.py:136).  The GEMVs take 2-4 bits only.
+inline int check_store(int bits, int group, int mode) {
+  IQ_CHECK(bits_ok(bits) || bits == 1, IQ_ERR_BITS);
+  IQ_CHECK(group_ok(group), IQ_ERR_GROUP);
+  IQ_CHECK(mode_ok(mode), IQ_ERR_MODE);
+  IQ_CHECK(bits != 1 || mode == IQ_MODE_ASYM, IQ_ERR_BITS);
+  return IQ_OK;
+}
+
 inline int launch_status() {
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? IQ_OK : IQ_ERR_HIP;
@@ -46,6 +56,18 @@ int dispatch_bits_group(int bits, int group, F&& f) {
   IQ_CASE(4, 32) IQ_CASE(4, 64) IQ_CASE(4, 128)
 #undef IQ_CASE
   return IQ_ERR_BITS;
+}
+
+// dispatch_bits_group plus 1-bit (packed-store kernels only)
+template <typename F>
+int dispatch_store_bits_group(int bits, int group, F&& f) {
+  if (bits == 1) {
+    if (group == 32) return f.template operator()<1, 32>();
+    if (group == 64) return f.template operator()<1, 64>();
+    if (group == 128) return f.template operator()<1, 128>();
+    return IQ_ERR_GROUP;
+  }
+  return dispatch_bits_group(bits, group, f);
 }
 
 }  // namespace iq

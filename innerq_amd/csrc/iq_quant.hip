@@ -376,6 +376,89 @@ __global__ __launch_bounds__(256) void dequant_dense_kernel(const int32_t* __res
   }
 }
 
+
+// ---- packed store -> reference-format tensors (cache state attributes) -----
+// codes: quant.py's int32 codes (sym: magnitudes); scale16 / zero16 as the
+// quantizer returns them; signs16 (sym): the sign of the stored code (0 for a
+// zero code, whose sign the packed form does not keep).
+struct UnpackOut {
+  int32_t* codes;
+  uint16_t* scale;
+  uint16_t* zs;
+};
+
+__device__ __forceinline__ void unpack_meta(const uint16_t* meta, int64_t unit, bool sym, uint16_t& s, uint16_t& z) {
+  if (sym) {
+    s = meta[unit];
+    z = 0;
+  } else {
+    const uint32_t sz = reinterpret_cast<const uint32_t*>(meta)[unit];
+    s = uint16_t(sz & 0xffffu);
+    z = uint16_t(sz >> 16);
+  }
+}
+
+__device__ __forceinline__ uint16_t sign16(int32_t c) { return c > 0 ? 0x3c00u : (c < 0 ? 0xbc00u : 0u); }
+
+template <int BITS, int G>
+__global__ __launch_bounds__(256) void unpack_k_kernel(const uint32_t* __restrict__ kc, const uint16_t* __restrict__ km,
+                                                       int64_t cap_blocks, int B, int H, int t0, int T, int D, int sym,
+                                                       UnpackOut o) {
+  constexpr int W = G * BITS / 32;
+  const int ng = D / G;
+  const int64_t gid = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (gid >= int64_t(B) * H * T * ng) return;
+  const int g = int(gid % ng);
+  const int64_t row = gid / ng;  // (b*H + h)*T + t
+  const int64_t bh = row / T;
+  const int64_t tt = int64_t(t0) + row % T;
+  const int64_t unit = ((bh * cap_blocks + tt / TOKEN_BLOCK) * ng + g) * TOKEN_BLOCK + tt % TOKEN_BLOCK;
+  uint32_t w[W];
+#pragma unroll
+  for (int j = 0; j < W; ++j) w[j] = kc[unit * W + j];
+  int32_t c[G];
+  unpack_fields<BITS, G>(w, sym != 0, c);
+  uint16_t s, z;
+  unpack_meta(km, unit, sym != 0, s, z);
+  o.scale[row * ng + g] = s;
+  if (!sym) o.zs[row * ng + g] = z;
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    const int64_t e = row * D + g * G + i;
+    o.codes[e] = c[i] < 0 ? -c[i] : c[i];
+    if (sym) o.zs[e] = sign16(c[i]);
+  }
+}
+
+template <int BITS, int G>
+__global__ __launch_bounds__(256) void unpack_v_kernel(const uint32_t* __restrict__ vc, const uint16_t* __restrict__ vm,
+                                                       int64_t cap_groups, int B, int H, int g0, int ngT, int D,
+                                                       int sym, UnpackOut o) {
+  constexpr int W = G * BITS / 32;
+  const int64_t gid = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (gid >= int64_t(B) * H * ngT * D) return;
+  const int d = int(gid % D);
+  const int64_t r = gid / D;  // (b*H + h)*ngT + gi
+  const int gi = int(r % ngT);
+  const int64_t bh = r / ngT;
+  const int64_t unit = (bh * cap_groups + g0 + gi) * D + d;
+  uint32_t w[W];
+#pragma unroll
+  for (int j = 0; j < W; ++j) w[j] = vc[unit * W + j];
+  int32_t c[G];
+  unpack_fields<BITS, G>(w, sym != 0, c);
+  uint16_t s, z;
+  unpack_meta(vm, unit, sym != 0, s, z);
+  o.scale[r * D + d] = s;
+  if (!sym) o.zs[r * D + d] = z;
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    const int64_t e = ((bh * ngT + gi) * G + i) * D + d;
+    o.codes[e] = c[i] < 0 ? -c[i] : c[i];
+    if (sym) o.zs[e] = sign16(c[i]);
+  }
+}
+
 }  // namespace
 
 // =============================================================================
@@ -389,7 +472,7 @@ const char* iq_strerror(int status) {
   switch (status) {
     case IQ_OK: return "ok";
     case IQ_ERR_NULL: return "null pointer argument";
-    case IQ_ERR_BITS: return "bits must be 2, 3 or 4";
+    case IQ_ERR_BITS: return "bits must be 2, 3 or 4 (packed stores: also 1 with asym)";
     case IQ_ERR_GROUP: return "group must be 32, 64 or 128 and divide the grouped axis";
     case IQ_ERR_SHAPE: return "unsupported or invalid shape";
     case IQ_ERR_ALIGN: return "pointer or stride misaligned";
@@ -404,7 +487,7 @@ const char* iq_strerror(int status) {
 int iq_k_store_bytes(int64_t B, int64_t H, int64_t t_cap, int64_t D, int group, int bits, int mode,
                      int64_t* codes_bytes, int64_t* meta_bytes) {
   IQ_CHECK(codes_bytes && meta_bytes, IQ_ERR_NULL);
-  if (int e = check_common(bits, group, mode)) return e;
+  if (int e = check_store(bits, group, mode)) return e;
   IQ_CHECK(B >= 0 && H >= 0 && t_cap >= 0 && D > 0, IQ_ERR_SHAPE);
   IQ_CHECK(D % group == 0, IQ_ERR_GROUP);
   IQ_CHECK(t_cap % TOKEN_BLOCK == 0, IQ_ERR_ALIGN);
@@ -416,7 +499,7 @@ int iq_k_store_bytes(int64_t B, int64_t H, int64_t t_cap, int64_t D, int group, 
 int iq_v_store_bytes(int64_t B, int64_t H, int64_t t_cap, int64_t D, int group, int bits, int mode,
                      int64_t* codes_bytes, int64_t* meta_bytes) {
   IQ_CHECK(codes_bytes && meta_bytes, IQ_ERR_NULL);
-  if (int e = check_common(bits, group, mode)) return e;
+  if (int e = check_store(bits, group, mode)) return e;
   IQ_CHECK(B >= 0 && H >= 0 && t_cap >= 0 && D > 0, IQ_ERR_SHAPE);
   IQ_CHECK(t_cap % group == 0, IQ_ERR_GROUP);
   *codes_bytes = B * H * t_cap * D * bits / 8;
@@ -429,7 +512,7 @@ int iq_quantize_k(const void* x, int64_t sx_b, int64_t sx_h, int64_t sx_t, const
                   int64_t t_cap, int64_t t_off, int32_t* codes_i32, void* scale16, void* zero16, void* signs16,
                   void* stream) {
   IQ_CHECK(x, IQ_ERR_NULL);
-  if (int e = check_common(bits, group, mode)) return e;
+  if (int e = check_store(bits, group, mode)) return e;
   IQ_CHECK(B >= 0 && H >= 0 && n >= 0 && D > 0, IQ_ERR_SHAPE);
   IQ_CHECK(D % group == 0, IQ_ERR_GROUP);
   IQ_CHECK(aligned(x, 16) && sx_b % 8 == 0 && sx_h % 8 == 0 && sx_t % 8 == 0, IQ_ERR_ALIGN);
@@ -446,7 +529,7 @@ int iq_quantize_k(const void* x, int64_t sx_b, int64_t sx_h, int64_t sx_t, const
   QuantOut o{k_codes, k_meta, t_cap / TOKEN_BLOCK, t_off, codes_i32, (uint16_t*)scale16, (uint16_t*)zero16,
              (uint16_t*)signs16};
   const int sym = mode == IQ_MODE_SYM;
-  return dispatch_bits_group(bits, group, [&]<int BITS, int G>() {
+  return dispatch_store_bits_group(bits, group, [&]<int BITS, int G>() {
     quant_k_kernel<BITS, G><<<dim3(unsigned(ceil_div(total, 256))), 256, 0, (hipStream_t)stream>>>(
         (const uint16_t*)x, sx_b, sx_h, sx_t, (const uint16_t*)norm, B, H, n, D, sym, o);
     return launch_status();
@@ -457,7 +540,7 @@ int iq_quantize_v(const void* x, int64_t sx_b, int64_t sx_h, int64_t sx_t, int B
                   int group, int bits, int mode, uint32_t* v_codes, uint16_t* v_meta, int64_t t_cap,
                   int64_t t_off, int32_t* codes_i32, void* scale16, void* zero16, void* signs16, void* stream) {
   IQ_CHECK(x, IQ_ERR_NULL);
-  if (int e = check_common(bits, group, mode)) return e;
+  if (int e = check_store(bits, group, mode)) return e;
   IQ_CHECK(B >= 0 && H >= 0 && n >= 0 && D > 0, IQ_ERR_SHAPE);
   IQ_CHECK(n % group == 0, IQ_ERR_GROUP);
   IQ_CHECK(aligned(x, 2), IQ_ERR_ALIGN);
@@ -474,7 +557,7 @@ int iq_quantize_v(const void* x, int64_t sx_b, int64_t sx_h, int64_t sx_t, int B
   QuantOut o{v_codes, v_meta, t_cap / group, t_off, codes_i32, (uint16_t*)scale16, (uint16_t*)zero16,
              (uint16_t*)signs16};
   const int sym = mode == IQ_MODE_SYM;
-  return dispatch_bits_group(bits, group, [&]<int BITS, int G>() {
+  return dispatch_store_bits_group(bits, group, [&]<int BITS, int G>() {
     quant_v_kernel<BITS, G><<<dim3(unsigned(ceil_div(total, 256))), 256, 0, (hipStream_t)stream>>>(
         (const uint16_t*)x, sx_b, sx_h, sx_t, B, H, n, D, sym, o);
     return launch_status();
@@ -486,7 +569,7 @@ int iq_dequant_k(const uint32_t* k_codes, const uint16_t* k_meta, int64_t t_cap,
                  int64_t so_h, int64_t so_t, void* stream) {
   IQ_CHECK(k_codes && k_meta, IQ_ERR_NULL);
   IQ_CHECK(out16 || out32, IQ_ERR_NULL);
-  if (int e = check_common(bits, group, mode)) return e;
+  if (int e = check_store(bits, group, mode)) return e;
   IQ_CHECK(B >= 0 && H >= 0 && T >= 0 && t0 >= 0 && D > 0, IQ_ERR_SHAPE);
   IQ_CHECK(D % group == 0, IQ_ERR_GROUP);
   IQ_CHECK(t_cap % TOKEN_BLOCK == 0, IQ_ERR_ALIGN);
@@ -495,7 +578,7 @@ int iq_dequant_k(const uint32_t* k_codes, const uint16_t* k_meta, int64_t t_cap,
   if (total == 0) return IQ_OK;
   DeqOut o{(uint16_t*)out16, out32, so_b, so_h, so_t};
   const int sym = mode == IQ_MODE_SYM;
-  return dispatch_bits_group(bits, group, [&]<int BITS, int G>() {
+  return dispatch_store_bits_group(bits, group, [&]<int BITS, int G>() {
     dequant_k_kernel<BITS, G><<<dim3(unsigned(ceil_div(total, 256))), 256, 0, (hipStream_t)stream>>>(
         k_codes, k_meta, t_cap / TOKEN_BLOCK, (const uint16_t*)norm, B, H, t0, T, D, sym, o);
     return launch_status();
@@ -507,7 +590,7 @@ int iq_dequant_v(const uint32_t* v_codes, const uint16_t* v_meta, int64_t t_cap,
                  int64_t so_t, void* stream) {
   IQ_CHECK(v_codes && v_meta, IQ_ERR_NULL);
   IQ_CHECK(out16 || out32, IQ_ERR_NULL);
-  if (int e = check_common(bits, group, mode)) return e;
+  if (int e = check_store(bits, group, mode)) return e;
   IQ_CHECK(B >= 0 && H >= 0 && T >= 0 && t0 >= 0 && D > 0, IQ_ERR_SHAPE);
   IQ_CHECK(T % group == 0 && t0 % group == 0 && t_cap % group == 0, IQ_ERR_GROUP);
   IQ_CHECK(int64_t(t0) + T <= t_cap, IQ_ERR_RANGE);
@@ -515,7 +598,7 @@ int iq_dequant_v(const uint32_t* v_codes, const uint16_t* v_meta, int64_t t_cap,
   if (total == 0) return IQ_OK;
   DeqOut o{(uint16_t*)out16, out32, so_b, so_h, so_t};
   const int sym = mode == IQ_MODE_SYM;
-  return dispatch_bits_group(bits, group, [&]<int BITS, int G>() {
+  return dispatch_store_bits_group(bits, group, [&]<int BITS, int G>() {
     dequant_v_kernel<BITS, G><<<dim3(unsigned(ceil_div(total, 256))), 256, 0, (hipStream_t)stream>>>(
         v_codes, v_meta, t_cap / G, B, H, t0 / G, T / G, D, sym, o);
     return launch_status();
@@ -534,6 +617,41 @@ int iq_dequant_dense(const int32_t* codes, const void* scale16, const void* zs16
       codes, (const uint16_t*)scale16, (const uint16_t*)zs16, outer, n, inner, group, mode == IQ_MODE_SYM, out_f16,
       out);
   return launch_status();
+}
+
+int iq_unpack_k(const uint32_t* k_codes, const uint16_t* k_meta, int64_t t_cap, int B, int H, int t0, int T, int D,
+                int group, int bits, int mode, int32_t* codes_i32, void* scale16, void* zs16, void* stream) {
+  IQ_CHECK(k_codes && k_meta && codes_i32 && scale16 && zs16, IQ_ERR_NULL);
+  if (int e = check_store(bits, group, mode)) return e;
+  IQ_CHECK(B >= 0 && H >= 0 && T >= 0 && t0 >= 0 && D > 0, IQ_ERR_SHAPE);
+  IQ_CHECK(D % group == 0, IQ_ERR_GROUP);
+  IQ_CHECK(t_cap % TOKEN_BLOCK == 0, IQ_ERR_ALIGN);
+  IQ_CHECK(int64_t(t0) + T <= t_cap, IQ_ERR_RANGE);
+  const int64_t total = int64_t(B) * H * T * (D / group);
+  if (total == 0) return IQ_OK;
+  const UnpackOut o{codes_i32, (uint16_t*)scale16, (uint16_t*)zs16};
+  return dispatch_store_bits_group(bits, group, [&]<int BITS, int G>() {
+    unpack_k_kernel<BITS, G><<<dim3(unsigned(ceil_div(total, 256))), 256, 0, (hipStream_t)stream>>>(
+        k_codes, k_meta, t_cap / TOKEN_BLOCK, B, H, t0, T, D, mode == IQ_MODE_SYM, o);
+    return launch_status();
+  });
+}
+
+int iq_unpack_v(const uint32_t* v_codes, const uint16_t* v_meta, int64_t t_cap, int B, int H, int t0, int T, int D,
+                int group, int bits, int mode, int32_t* codes_i32, void* scale16, void* zs16, void* stream) {
+  IQ_CHECK(v_codes && v_meta && codes_i32 && scale16 && zs16, IQ_ERR_NULL);
+  if (int e = check_store(bits, group, mode)) return e;
+  IQ_CHECK(B >= 0 && H >= 0 && T >= 0 && t0 >= 0 && D > 0, IQ_ERR_SHAPE);
+  IQ_CHECK(T % group == 0 && t0 % group == 0 && t_cap % group == 0, IQ_ERR_GROUP);
+  IQ_CHECK(int64_t(t0) + T <= t_cap, IQ_ERR_RANGE);
+  const int64_t total = int64_t(B) * H * (T / group) * D;
+  if (total == 0) return IQ_OK;
+  const UnpackOut o{codes_i32, (uint16_t*)scale16, (uint16_t*)zs16};
+  return dispatch_store_bits_group(bits, group, [&]<int BITS, int G>() {
+    unpack_v_kernel<BITS, G><<<dim3(unsigned(ceil_div(total, 256))), 256, 0, (hipStream_t)stream>>>(
+        v_codes, v_meta, t_cap / G, B, H, t0 / G, T / G, D, mode == IQ_MODE_SYM, o);
+    return launch_status();
+  });
 }
 
 }  // extern "C"

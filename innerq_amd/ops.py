@@ -303,3 +303,65 @@ def decode_attention(q: torch.Tensor, k_sink: Optional[torch.Tensor], k_store: O
     call("iq_decode_attention", _p(q), q.stride(0), q.stride(1), _p(norm), ks, vs, B, Hq, Hkv, T, D, float(scale),
          _p(out), out.stride(0), out.stride(1), _p(ws), ws.numel(), _stream(q.device))
     return out
+
+
+# --- cache-side helpers --------------------------------------------------------
+def unpack_store(store: PackedStore, t0: int = 0, T: Optional[int] = None):
+    """Reference-format (codes int32, scale fp16, zero | signs fp16) of store tokens [t0, t0+T)."""
+    T = store.length - t0 if T is None else T
+    B, H, D, G = store.B, store.H, store.D, store.group
+    dev = store.device
+    codes = torch.empty(B, H, T, D, dtype=torch.int32, device=dev)
+    red = (B, H, T, D // G) if store.axis == "channel" else (B, H, T // G, D)
+    scale = torch.empty(red, dtype=torch.float16, device=dev)
+    zs = torch.empty(red if store.mode == IQ_MODE_ASYM else (B, H, T, D), dtype=torch.float16, device=dev)
+    fn = "iq_unpack_k" if store.axis == "channel" else "iq_unpack_v"
+    call(fn, _p(store.codes), _p(store.meta), store.t_cap, B, H, t0, T, D, G, store.bits, store.mode, _p(codes),
+         _p(scale), _p(zs), _stream(dev))
+    return codes, scale, zs
+
+
+def key_norm_factor(k: torch.Tensor) -> torch.Tensor:
+    """fp16 sqrt(max_t |k|) of k [B,H,T,D] as [B,H,1,D] (cache.py:121-126)."""
+    require_device(k, "key_states")
+    if k.stride(-1) != 1:
+        k = k.contiguous()
+    B, H, T, D = k.shape
+    out = torch.empty(B, H, 1, D, dtype=torch.float16, device=k.device)
+    call("iq_key_norm_factor", _p(k), k.stride(0), k.stride(1), k.stride(2), B, H, T, D, _p(out), _stream(k.device))
+    return out
+
+
+def hybrid_mask(x: torch.Tensor, deq_a: torch.Tensor, deq_s: torch.Tensor, group: int, axis: str,
+                norm: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Per-group choice of the sym quantization (quant.py:133-151) over [BH,T,D]-viewable tensors."""
+    require_device(x, "tensor")
+    require_device(deq_a, "deq_zp", torch.float32)
+    require_device(deq_s, "deq_nozp", torch.float32)
+    *lead, T, D = x.shape
+    BH = int(torch.tensor(lead).prod()) if lead else 1
+    ax = 0 if axis == "channel" else 1
+    shape = tuple(lead) + ((T, D // group) if ax == 0 else (T // group, D))
+    mask = torch.empty(shape, dtype=torch.bool, device=x.device)
+    if norm is not None:
+        require_device(norm, "norm")
+        norm = norm.reshape(BH, D).contiguous()
+    call("iq_hybrid_mask", _p(x.contiguous()), _p(norm), _p(deq_a.contiguous()), _p(deq_s.contiguous()), BH, T, D,
+         group, ax, _p(mask), _stream(x.device))
+    return mask
+
+
+def hybrid_select(deq_a: torch.Tensor, deq_s: torch.Tensor, mask: torch.Tensor, group: int, axis: str,
+                  dtype=torch.float32) -> torch.Tensor:
+    """mask ? deq_s : deq_a over [BH,T,D]-viewable fp32 tensors (quant.py:153-176)."""
+    require_device(deq_a, "deq_zp", torch.float32)
+    require_device(deq_s, "deq_nozp", torch.float32)
+    require_device(mask, "mask", torch.bool)
+    *lead, T, D = deq_a.shape
+    BH = int(torch.tensor(lead).prod()) if lead else 1
+    if dtype not in (torch.float32, torch.float16):
+        raise TypeError("op_dtype must be torch.float32 or torch.float16")
+    out = torch.empty(deq_a.shape, dtype=dtype, device=deq_a.device)
+    call("iq_hybrid_select", _p(deq_a.contiguous()), _p(deq_s.contiguous()), _p(mask.contiguous()), BH, T, D, group,
+         0 if axis == "channel" else 1, 1 if dtype == torch.float16 else 0, _p(out), _stream(deq_a.device))
+    return out

@@ -129,7 +129,7 @@ def quant_v_args(**kw):
 
 
 @pytest.mark.parametrize("kw,err", [
-    (dict(x=None), -1), (dict(vm=None), -1), (dict(bits=1), -2), (dict(n=48), -3), (dict(t_off=32), -8),
+    (dict(x=None), -1), (dict(vm=None), -1), (dict(bits=1, mode=1), -2), (dict(n=48), -3), (dict(t_off=32), -8),
     (dict(t_off=16), -5), (dict(t_cap=48), -5), (dict(mode=7), -7),
 ])
 def test_quantize_v_rejects(kw, err):

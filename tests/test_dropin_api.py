@@ -1,0 +1,88 @@
+"""The drop-in API surface (innerq_amd.quant / innerq_amd.cache) without a GPU:
+names, configuration parsing, error behaviour and the no-CPU-path rule."""
+import pytest
+import torch
+
+from innerq_amd import cache as C
+from innerq_amd import quant as IQ
+
+
+class Cfg:
+    def __init__(self, **kw):
+        self.__dict__.update(kw)
+
+
+def test_qmode_matches_reference():
+    assert IQ.QMode.from_str(" Asymmetric ") is IQ.QMode.ASYM
+    assert IQ.QMode.from_str("symmetric") is IQ.QMode.SYM
+    assert IQ.QMode.from_str("HYBRID") is IQ.QMode.HYBRID
+    with pytest.raises(ValueError):
+        IQ.QMode.from_str("int4")
+
+
+def test_quant_api_names():
+    for axis in ("channeldim", "tokendim"):
+        for mode in ("asym", "sym"):
+            assert callable(getattr(IQ, f"quantize_{axis}_{mode}"))
+            assert callable(getattr(IQ, f"dequantize_{axis}_{mode}"))
+    assert callable(IQ.quantize_hybrid(IQ.quantize_channeldim_asym, IQ.quantize_channeldim_sym,
+                                       IQ.dequantize_channeldim_asym, IQ.dequantize_channeldim_sym))
+    assert callable(IQ.dequantize_hybrid(IQ.dequantize_tokendim_asym, IQ.dequantize_tokendim_sym))
+
+
+def test_no_cpu_path():
+    x = torch.zeros(1, 2, 64, 64, dtype=torch.float16)
+    with pytest.raises(TypeError):
+        IQ.quantize_channeldim_asym(x, 32, 4)
+    layer = C.InnerqDynamicLayer(Cfg(k_bits=4, v_bits=4), 0)
+    with pytest.raises(TypeError):
+        layer.update(x, x)
+
+
+def test_config_defaults_match_reference():
+    l = C.InnerqDynamicLayer(Cfg(), 3)
+    assert (l.key_bits, l.value_bits, l.key_quantize, l.value_quantize) == (16, 16, False, False)
+    assert (l.key_group_size, l.value_group_size, l.key_w_recent, l.value_w_recent) == (32, 32, 32, 32)
+    assert (l.key_w_sink, l.value_w_sink, l.key_flush_size, l.value_flush_size) == (0, 0, 32, 32)
+    assert (l.key_normalize, l.key_normalization_factor) == (False, None)
+    assert (l.key_quantize_over_token, l.value_quantize_over_token) == (False, True)
+    assert l.key_quantize_mode is IQ.QMode.SYM and l.value_quantize_mode is IQ.QMode.SYM
+    assert (l.layer_idx, l.cumulative_length, l.is_initialized) == (3, 0, False)
+    assert l.keys_q is None and l.values_scale_factor is None
+
+
+def test_layer_queries_and_errors():
+    l = C.InnerqDynamicLayer(Cfg(k_bits=2, v_bits=2), 0)
+    l.cumulative_length = 10
+    assert l.get_mask_sizes(torch.arange(3)) == (13, 0)   # cache_position (cache.py:398-402)
+    assert l.get_mask_sizes(3) == (13, 0)                  # query_length (transformers 5.15)
+    assert l.get_seq_length() == 10 and l.get_max_cache_shape() == -1 and l.get_max_length() == -1
+    with pytest.raises(ValueError):
+        l.crop(4)
+    with pytest.raises(Exception):
+        l.batch_repeat_interleave(2)
+    with pytest.raises(Exception):
+        l.batch_select_indices(torch.tensor([0]))
+
+
+def test_sliding_window_layer_queries():
+    l = C.InnerqDynamicSlidingWindowLayer(Cfg(k_bits=4), 0, sliding_window=8)
+    assert l.is_sliding and l.get_max_cache_shape() == 8
+    l.cumulative_length = 5
+    assert l.get_mask_sizes(1) == (6, 0)
+    l.cumulative_length = 20
+    assert l.get_mask_sizes(torch.arange(1)) == (8, 13)
+
+
+def test_dynamic_cache_layer_types():
+    from transformers import LlamaConfig, MistralConfig
+    cfg = LlamaConfig(num_hidden_layers=4, num_attention_heads=4, num_key_value_heads=2, hidden_size=64,
+                      intermediate_size=32, vocab_size=16)
+    cfg.k_bits = 3
+    cache = C.DynamicCache(config=cfg)
+    assert len(cache.layers) == 4 and not any(l.is_sliding for l in cache.layers)
+    assert all(l.key_bits == 3 for l in cache.layers)
+    mcfg = MistralConfig(num_hidden_layers=2, num_attention_heads=4, num_key_value_heads=2, hidden_size=64,
+                         intermediate_size=32, vocab_size=16, sliding_window=16)
+    cache = C.DynamicCache(config=mcfg)
+    assert all(isinstance(l, C.InnerqDynamicSlidingWindowLayer) and l.sliding_window == 16 for l in cache.layers)

@@ -1,0 +1,188 @@
+"""GPU parity of the drop-in API (innerq_amd.quant / innerq_amd.cache) against
+the live reference's golden fixtures (tests/golden/*.npz).
+
+quant: codes, scales, zero points, signs, dequantized values and hybrid masks
+bit-exact.  cache: the fp16 K and V that update() returns at every step of the
+reference traces bit-exact (SHA-256 per step), and the recent-window lengths
+equal.  attend(): the fused decode attention over the packed cache within 1e-3
+(max-relative) of float64 attention over update()'s dense K and V.
+"""
+import hashlib
+
+import numpy as np
+import pytest
+import torch
+
+from innerq_amd import cache as C
+from innerq_amd import quant as IQ
+from innerq_amd import synth
+from oracle import attn_ref as A
+from oracle import quant_ref as Q
+from tests.test_oracle_cache import PRESETS, Cfg, golden_inputs
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def _sha(a):
+    return np.frombuffer(hashlib.sha256(np.ascontiguousarray(a).tobytes()).digest(), dtype=np.uint8)
+
+
+def _codes8(c):
+    c = np.where(c == Q.INT32_MIN, -128, c)
+    return c.astype(np.int8)
+
+
+def _x(g):
+    return torch.from_numpy(g["x"].view(np.float16).copy()).to(DEV)
+
+
+@pytest.mark.parametrize("axis", ["channel", "token"])
+@pytest.mark.parametrize("mode", ["asym", "sym"])
+@pytest.mark.parametrize("bits", [2, 3, 4])
+@pytest.mark.parametrize("G", [32, 64])
+def test_quantize_api_matches_reference(quant_golden, axis, mode, bits, G):
+    g = quant_golden
+    c, s, z = getattr(IQ, f"quantize_{axis}dim_{mode}")(_x(g), G, bits)
+    assert c.dtype == torch.int32 and s.dtype == torch.float16 and z.dtype == torch.float16
+    key = f"{axis}_{mode}_b{bits}_g{G}"
+    np.testing.assert_array_equal(_codes8(c.cpu().numpy()), g[key + "_codes"])
+    np.testing.assert_array_equal(s.cpu().numpy().view(np.uint16), g[key + "_scale"])
+    np.testing.assert_array_equal(z.cpu().numpy().view(np.uint16), g[key + ("_zero" if mode == "asym" else "_signs")])
+
+
+@pytest.mark.parametrize("axis", ["channel", "token"])
+def test_dequantize_api_matches_reference(quant_golden, axis):
+    g = quant_golden
+    x = _x(g)
+    c, s, z = getattr(IQ, f"quantize_{axis}dim_asym")(x, 32, 4)
+    d = getattr(IQ, f"dequantize_{axis}dim_asym")(c, s, z, 32)
+    assert d.dtype == torch.float32
+    np.testing.assert_array_equal(_sha(d.cpu().numpy()), g[f"{axis}_asym_b4_g32_deq_sha256"])
+    c, s, sg = getattr(IQ, f"quantize_{axis}dim_sym")(x, 32, 3)
+    d = getattr(IQ, f"dequantize_{axis}dim_sym")(c, s, sg, 32)
+    np.testing.assert_array_equal(_sha(d.cpu().numpy()), g[f"{axis}_sym_b3_g32_deq_sha256"])
+
+
+@pytest.mark.parametrize("axis", ["channel", "token"])
+@pytest.mark.parametrize("bits", [3, 4])
+def test_hybrid_api_matches_reference(quant_golden, axis, bits):
+    g = quant_golden
+    qa, qs = getattr(IQ, f"quantize_{axis}dim_asym"), getattr(IQ, f"quantize_{axis}dim_sym")
+    da, ds = getattr(IQ, f"dequantize_{axis}dim_asym"), getattr(IQ, f"dequantize_{axis}dim_sym")
+    c, s, z = IQ.quantize_hybrid(qa, qs, da, ds)(_x(g), 32, bits)
+    key = f"{axis}_hybrid_b{bits}_g32"
+    assert set(c) == {"zp", "nozp"} and set(s) == {"zp", "nozp", "mask"} and set(z) == {"zp", "nozp"}
+    np.testing.assert_array_equal(s["mask"].cpu().numpy(), g[key + "_mask"])
+    d = IQ.dequantize_hybrid(da, ds)(c, s, z, 32)
+    np.testing.assert_array_equal(_sha(d.cpu().numpy()), g[key + "_deq_sha256"])
+
+
+def test_quant_api_errors():
+    x = torch.zeros(1, 2, 64, 96, dtype=torch.float16, device=DEV)
+    with pytest.raises(AssertionError):        # 96 % 64 != 0, as quant.py:61
+        IQ.quantize_channeldim_asym(x, 64, 4)
+    with pytest.raises(ValueError):
+        IQ.quantize_channeldim_asym(x, 32, 5)
+    with pytest.raises(TypeError):
+        IQ.quantize_channeldim_asym(x.float(), 32, 4)
+
+
+def _sha16(k, v):
+    return _sha(np.concatenate([k.view(np.uint16).ravel(), v.view(np.uint16).ravel()]))
+
+
+def _np(t):
+    return t.cpu().numpy()
+
+
+@pytest.mark.parametrize("name", list(PRESETS))
+def test_cache_update_matches_reference_trace(cache_golden, name):
+    """update() returns the reference's K and V at every step: equal values to the
+    oracle's (pinned bit-exact to the reference traces) and to the reference's
+    last-step arrays.  Values, not bits: the packed sym format does not keep the
+    sign of a zero code, so the reference's -0.0 comes back as +0.0."""
+    from oracle import cache_ref
+    g = cache_golden
+    kx, vx, prefill, steps = golden_inputs(g, name)
+    kt, vt = torch.from_numpy(kx).to(DEV), torch.from_numpy(vx).to(DEV)
+    layer = C.InnerqDynamicLayer(Cfg(**PRESETS[name]), 0)
+    ref = cache_ref.CacheLayerRef(Cfg(**PRESETS[name]))
+    K, V = layer.update(kt[:, :, :prefill].clone(), vt[:, :, :prefill].clone())
+    Kr, Vr = ref.update(kx[:, :, :prefill], vx[:, :, :prefill])
+    np.testing.assert_array_equal(_sha16(_np(K), _np(V)), g[f"{name}_step0_sha256"])
+    for s in range(steps):
+        K, V = layer.update(kt[:, :, prefill + s:prefill + s + 1].clone(), vt[:, :, prefill + s:prefill + s + 1].clone())
+        Kr, Vr = ref.update(kx[:, :, prefill + s:prefill + s + 1], vx[:, :, prefill + s:prefill + s + 1])
+        k, v = _np(K), _np(V)
+        assert k.dtype == np.float16 and v.dtype == np.float16
+        np.testing.assert_array_equal(k, Kr, err_msg=f"K step {s + 1}")
+        np.testing.assert_array_equal(v, Vr, err_msg=f"V step {s + 1}")
+        if s == steps - 1:
+            np.testing.assert_array_equal(k, g[f"{name}_step{s + 1}_k"].view(np.float16))
+            np.testing.assert_array_equal(v, g[f"{name}_step{s + 1}_v"].view(np.float16))
+        assert (k.shape[-2], v.shape[-2], layer.keys_recent.shape[-2], layer.values_recent.shape[-2]) == \
+            tuple(g[f"{name}_len{s + 1}"])
+    assert layer.get_seq_length() == prefill + steps
+
+
+@pytest.mark.parametrize("name", [n for n in PRESETS if PRESETS[n].get("value_quantize_mode") != "hybrid"])
+@pytest.mark.parametrize("nrep", [1, 4])
+def test_cache_attend_matches_dense_attention(cache_golden, name, nrep):
+    """append() + attend() (fused, packed) within 1e-3 of float64 attention over the
+    fp32 dequantize-then-matmul K and V (get_keys_deq / get_values_deq, cache.py:235-271)."""
+    g = cache_golden
+    kx, vx, prefill, steps = golden_inputs(g, name)
+    kt, vt = torch.from_numpy(kx).to(DEV), torch.from_numpy(vx).to(DEV)
+    layer = C.InnerqDynamicLayer(Cfg(**PRESETS[name]), 0)
+    layer.append(kt[:, :, :prefill].clone(), vt[:, :, :prefill].clone())
+    B, H, _, D = kx.shape
+    for s in range(steps):
+        layer.append(kt[:, :, prefill + s:prefill + s + 1].clone(), vt[:, :, prefill + s:prefill + s + 1].clone())
+        if s % 23 == 5 or s == steps - 1:
+            q = synth.normal((B, H * nrep, D), seed=s + 7 * nrep).astype(np.float16)
+            out = layer.attend(torch.from_numpy(q).to(DEV)[:, :, None], D ** -0.5)
+            assert out.shape == (B, H * nrep, 1, D) and out.dtype == torch.float16
+            K, V = layer.get_keys_deq(), layer.get_values_deq()
+            ref = A.decode_attention(q, _np(K.float()), _np(V.float()), D ** -0.5, None)
+            assert A.rel_err(_np(out[:, :, 0]).astype(np.float64), ref) < 1e-3, f"step {s + 1}"
+
+
+def test_cache_state_views_match_quantizer():
+    """keys_q / keys_scale_factor / keys_zp_sign and values_* unpack to quant.py's tensors."""
+    cfg = Cfg(k_bits=4, v_bits=3, key_flush_size=1, value_flush_size=64, key_group_size=32, value_group_size=64,
+              key_w_recent=8, value_w_recent=64, key_quantize_mode="asymmetric", value_quantize_mode="symmetric")
+    kx = synth.kv_tensor(1, 2, 200, 64, seed=3, n_out=2, factor=8.0)
+    vx = synth.kv_tensor(1, 2, 200, 64, seed=4, n_out=2, factor=8.0)
+    layer = C.InnerqDynamicLayer(cfg, 0)
+    layer.update(torch.from_numpy(kx).to(DEV), torch.from_numpy(vx).to(DEV))
+    nk = layer.keys_q.shape[2]
+    nv = layer.values_q.shape[2]
+    assert nk == 200 - 8 and nv == 192  # V keeps 8 recent: (200 - 8) % 64 == 0
+    c, s, z = Q.quantize_channeldim_asym(kx[:, :, :nk], 32, 4)
+    np.testing.assert_array_equal(_np(layer.keys_q), c)
+    np.testing.assert_array_equal(_np(layer.keys_scale_factor).view(np.uint16), s.view(np.uint16))
+    np.testing.assert_array_equal(_np(layer.keys_zp_sign).view(np.uint16), z.view(np.uint16))
+    c, s, sg = Q.quantize_tokendim_sym(vx[:, :, :nv], 64, 3)
+    np.testing.assert_array_equal(_np(layer.values_q), c)
+    np.testing.assert_array_equal(_np(layer.values_scale_factor).view(np.uint16), s.view(np.uint16))
+    got = _np(layer.values_zp_sign)
+    nz = c != 0   # the packed form keeps the sign of non-zero codes only
+    np.testing.assert_array_equal(got[nz], sg[nz])
+    assert np.all(got[~nz] == 0)
+
+
+def test_dynamic_cache_from_llama_config():
+    from transformers import LlamaConfig
+    cfg = LlamaConfig(num_hidden_layers=3, num_attention_heads=8, num_key_value_heads=2, hidden_size=512,
+                      intermediate_size=64, vocab_size=32)
+    for k, v in PRESETS["asym4_nosink"].items():
+        setattr(cfg, k, v)
+    cache = C.DynamicCache(config=cfg)
+    assert len(cache.layers) == 3 and all(isinstance(l, C.InnerqDynamicLayer) for l in cache.layers)
+    k = torch.randn(1, 2, 100, 64, dtype=torch.float16, device=DEV)
+    v = torch.randn(1, 2, 100, 64, dtype=torch.float16, device=DEV)
+    K, V = cache.update(k, v, 1)
+    assert K is k and V is v
+    K, V = cache.update(k[:, :, :1], v[:, :, :1], 1)
+    assert K.shape == (1, 2, 101, 64) and cache.get_seq_length(1) == 101
