@@ -10,10 +10,13 @@ over --copies independent copies (>= 1 GiB) so every step reads cold data
 past the 256 MiB Infinity Cache.
 
 value = algorithmic packed-code + metadata bytes of both GEMVs / step time.
-roofline = the dominant GEMV kernel alone, timed with HIP events on the
-stream it runs on.  cpu_baseline = the reference's torch CPU path
-(dequantize int32 codes -> fp16 -> eager attention) on a sample of the same
-workload, timed on host cores (oracle/timing.py).
+roofline = the dominant kernel (the fused flash-decoding split kernel, which
+reads every packed byte) alone: the split stage of the step timed with HIP
+events on the stream it runs on; traffic = its HBM bytes from rocprofv3
+FETCH_SIZE / WRITE_SIZE (profiles/traffic.json).  cpu_baseline = the
+reference's torch CPU path (dequantize int32 codes -> fp16 -> eager
+attention) on a sample of the same workload, timed on host cores
+(oracle/timing.py).
 
     python bench.py [--gpus 1] [--steps 100] [--warmup 10]
     python bench.py --config {H,1,2,3,4}    other BASELINE configs (not the headline line)
@@ -92,11 +95,13 @@ def _cpu_model():
 
 
 def traffic_from_profiles(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 counter summary
+    (FETCH_SIZE and WRITE_SIZE passes scaled by a plain-copy calibration), or None."""
     path = os.path.join(HERE, "profiles", "traffic.json")
     try:
         with open(path) as f:
-            return json.load(f).get(kernel)
-    except (OSError, ValueError):
+            return json.load(f).get(kernel, {}).get("bytes")
+    except (OSError, ValueError, AttributeError):
         return None
 
 
@@ -116,19 +121,18 @@ def bench_headline(args):
         ops.decode_attention(q, None, ks[i % C], None, None, vs[i % C], None, scale, out=out)
 
     us_step = time_loop(step, args.steps, args.warmup)
-
-    logits = torch.empty(B, Hq, T, device=dev, dtype=torch.float32)
-    p = torch.softmax(torch.randn(B, Hq, T, device=dev) * 2.0, dim=-1).to(torch.float16)
-    o32 = torch.empty(B, Hq, D, device=dev, dtype=torch.float32)
-    us_qk = time_loop(lambda i: ops.qk_gemv(q, ks[i % C], scale, out=logits), args.steps, args.warmup)
-    us_av = time_loop(lambda i: ops.av_gemv(p, vs[i % C], out32=o32), args.steps, args.warmup)
+    # the split stage alone: one launch of the fused split kernel here (K and V share
+    # their format and every token is packed); the rest of the step is the combine of
+    # its 64 splits (too short to time alone from the host: see the rocprofv3 summary)
+    nsplit = ops.decode_attention_splits(q, None, ks[0], None, None, vs[0], None, scale)
+    us_split = time_loop(lambda i: ops.decode_attention_splits(q, None, ks[i % C], None, None, vs[i % C], None,
+                                                               scale), args.steps, args.warmup)
 
     qk_b = gemv_bytes(B, Hkv, T, D, G, bits, mode, "channel")
     av_b = gemv_bytes(B, Hkv, T, D, G, bits, mode, "token")
     step_b = qk_b + av_b
     value = step_b / (us_step * 1e-6) / 1e9
-    dom, dom_us, dom_b = ("qk_kernel", us_qk, qk_b) if us_qk >= us_av else ("av_kernel+av_combine", us_av, av_b)
-    ach = dom_b / (dom_us * 1e-6) / 1e9
+    ach = step_b / (us_split * 1e-6) / 1e9
     line = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
         "warmup": args.warmup, "ms_per_step": round(us_step / 1e3, 5), "us_per_step": round(us_step, 2),
@@ -140,12 +144,19 @@ def bench_headline(args):
                                "4-bit K (groups along head_dim) and V (groups along tokens), asym, G=32",
                    "global_batch": B, "seq_len": T, "parallelism": "single GPU", "copies_rotated": C,
                    "algorithmic_bytes_per_step": step_b},
-        "kernels_us": {"qk_gemv": round(us_qk, 2), "av_gemv_incl_combine": round(us_av, 2),
-                       "qk_GBs": round(qk_b / us_qk / 1e3, 1), "av_GBs": round(av_b / us_av / 1e3, 1)},
-        "roofline": {"bound": "hbm", "kernel": dom, "achieved": round(ach, 1), "peak": PEAK_GBS, "unit": "GB/s",
-                     "frac": round(ach / PEAK_GBS, 4), "traffic": traffic_from_profiles(dom),
-                     "algorithmic_bytes": dom_b},
+        "kernels_us": {"flash_fused_kernel": round(us_split, 2), "splits": nsplit},
+        "roofline": {"bound": "hbm", "kernel": "flash_fused_kernel", "achieved": round(ach, 1), "peak": PEAK_GBS,
+                     "unit": "GB/s", "frac": round(ach / PEAK_GBS, 4),
+                     "traffic": traffic_from_profiles("flash_fused_kernel"), "algorithmic_bytes": step_b},
     }
+    if args.gemvs:
+        logits = torch.empty(B, Hq, T, device=dev, dtype=torch.float32)
+        p = torch.softmax(torch.randn(B, Hq, T, device=dev) * 2.0, dim=-1).to(torch.float16)
+        o32 = torch.empty(B, Hq, D, device=dev, dtype=torch.float32)
+        us_qk = time_loop(lambda i: ops.qk_gemv(q, ks[i % C], scale, out=logits), args.steps, args.warmup)
+        us_av = time_loop(lambda i: ops.av_gemv(p, vs[i % C], out32=o32), args.steps, args.warmup)
+        line["kernels_us"].update(qk_gemv=round(us_qk, 2), av_gemv_incl_records_combine=round(us_av, 2),
+                                  qk_GBs=round(qk_b / us_qk / 1e3, 1), av_GBs=round(av_b / us_av / 1e3, 1))
     if not args.no_cpu:
         line["cpu_baseline"] = cpu_baseline(B, Hq, Hkv, T, D, G, bits, bits, step_b)
     print(json.dumps(line), flush=True)
@@ -239,6 +250,7 @@ def main():
     ap.add_argument("--config", default="H")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--calib-copy", action="store_true")
+    ap.add_argument("--gemvs", action="store_true", help="also time the standalone QK^T and attn.V GEMV API calls")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: this build runs on one GPU only (no collectives); "

@@ -226,6 +226,20 @@ int iq_decode_attention(const void* q, int64_t sq_b, int64_t sq_h, const void* n
                         void* out, int64_t so_b, int64_t so_h,
                         void* workspace, size_t workspace_bytes, void* stream);
 
+/* The two stages of iq_decode_attention, for callers that schedule them
+ * separately (e.g. to time or overlap the split stage).  _splits validates as
+ * iq_decode_attention, launches every kernel up to the per-split softmax
+ * statistics and unnormalized partial outputs (kept in the workspace) and
+ * stores their count in *nsplit (host memory, known at return).  _combine
+ * merges nsplit splits from the same workspace into out (fp16 [B,Hq,D],
+ * strides so_b, so_h); T and D are those of the _splits call.  Flash-decoding
+ * split + combine, atomic-free. */
+int iq_decode_attention_splits(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, const iq_segment* k,
+                               const iq_segment* v, int B, int Hq, int Hkv, int T, int D, float scale,
+                               void* workspace, size_t workspace_bytes, int* nsplit, void* stream);
+int iq_decode_attention_combine(int nsplit, int B, int Hq, int T, int D, void* out, int64_t so_b, int64_t so_h,
+                                void* workspace, size_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -71,6 +71,9 @@ SIGNATURES = {
     "iq_decode_workspace_bytes": (S, [I, I, I, I]),
     "iq_decode_attention": (I, [P, L, L, P, ctypes.POINTER(iq_segment), ctypes.POINTER(iq_segment),
                                 I, I, I, I, I, F, P, L, L, P, S, P]),
+    "iq_decode_attention_splits": (I, [P, L, L, P, ctypes.POINTER(iq_segment), ctypes.POINTER(iq_segment),
+                                       I, I, I, I, I, F, P, S, ctypes.POINTER(I), P]),
+    "iq_decode_attention_combine": (I, [I, I, I, I, I, P, L, L, P, S, P]),
 }
 
 _lib = None

@@ -236,24 +236,38 @@ Seg to_seg(const iq_segment& s, int start) {
 
 }  // namespace
 
-extern "C" {
+namespace {
 
-size_t iq_decode_workspace_bytes(int B, int Hq, int T, int D) {
-  if (B <= 0 || Hq <= 0 || T <= 0 || !d_ok(D)) return 0;
+struct Workspace {
+  uint32_t* qrec;  // query operand records (unfused path)
+  uint32_t* vrec;  // probability operand records (unfused path)
+  float* ml;       // [nsplit][B*Hq][2] split (max, sum)
+  float* part;     // [nsplit][B*Hq][D] unnormalized split outputs
+};
+
+Workspace carve(void* workspace, int B, int Hq, int T, int D) {
   const size_t rows = size_t(B) * Hq;
-  size_t vrec = 0;
-  for (int g : {32, 64, 128}) vrec = std::max(vrec, rec_bytes_bound(int64_t(B) * Hq, T / g, g));
-  const size_t ns = size_t(nsplit_max(T)) + 1;
-  return detail::qk_record_bytes(B, Hq, D) + align256(vrec) + align256(ns * rows * 2 * 4) +
-         align256(ns * rows * D * 4);
+  char* ws = (char*)workspace;
+  Workspace w{};
+  w.qrec = (uint32_t*)ws;
+  ws += detail::qk_record_bytes(B, Hq, D);
+  size_t vrec_bytes = 0;
+  for (int g : {32, 64, 128}) vrec_bytes = std::max(vrec_bytes, rec_bytes_bound(int64_t(B) * Hq, T / g, g));
+  w.vrec = (uint32_t*)ws;
+  ws += align256(vrec_bytes);
+  const size_t ns_cap = size_t(nsplit_max(T)) + 1;
+  w.ml = (float*)ws;
+  ws += align256(ns_cap * rows * 2 * 4);
+  w.part = (float*)ws;
+  return w;
 }
 
-int iq_decode_attention(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, const iq_segment* k,
-                        const iq_segment* v, int B, int Hq, int Hkv, int T, int D, float scale, void* out,
-                        int64_t so_b, int64_t so_h, void* workspace, size_t workspace_bytes, void* stream) {
-  IQ_CHECK(q && k && v && out, IQ_ERR_NULL);
+int check_decode(const void* q, const iq_segment* k, const iq_segment* v, int B, int Hq, int Hkv, int T, int D,
+                 const void* workspace, size_t workspace_bytes) {
+  IQ_CHECK(q && k && v, IQ_ERR_NULL);
   IQ_CHECK(B >= 0 && T > 0 && Hkv > 0 && Hq > 0, IQ_ERR_SHAPE);
   IQ_CHECK(d_ok(D) && Hq % Hkv == 0 && nrep_ok(Hq / Hkv), IQ_ERR_SHAPE);
+  IQ_CHECK(nsplit_max(T) + 1 <= MAXSPLIT, IQ_ERR_SHAPE);
   for (int s = 0; s < 3; ++s) IQ_CHECK(k[s].n >= 0 && v[s].n >= 0, IQ_ERR_SHAPE);
   IQ_CHECK(k[0].n + k[1].n + k[2].n == T && v[0].n + v[1].n + v[2].n == T, IQ_ERR_SHAPE);
   for (int s : {0, 2}) {
@@ -279,22 +293,14 @@ int iq_decode_attention(const void* q, int64_t sq_b, int64_t sq_h, const void* n
   }
   IQ_CHECK(workspace && workspace_bytes >= iq_decode_workspace_bytes(B, Hq, T, D), IQ_ERR_WORKSPACE);
   IQ_CHECK(aligned(workspace, 256), IQ_ERR_ALIGN);
-  if (B == 0) return IQ_OK;
+  return IQ_OK;
+}
 
-  hipStream_t st = (hipStream_t)stream;
+// Launches everything up to the split statistics and partials; *nsplit = their count.
+int launch_splits(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, const iq_segment* k,
+                  const iq_segment* v, int B, int Hq, int Hkv, int T, int D, float scale, const Workspace& w,
+                  int* nsplit, hipStream_t st) {
   const int64_t rows = int64_t(B) * Hq;
-  char* ws = (char*)workspace;
-  uint32_t* qrec = (uint32_t*)ws;
-  ws += detail::qk_record_bytes(B, Hq, D);
-  size_t vrec_bytes = 0;
-  for (int g : {32, 64, 128}) vrec_bytes = std::max(vrec_bytes, rec_bytes_bound(int64_t(B) * Hq, T / g, g));
-  uint32_t* vrec = (uint32_t*)ws;
-  ws += align256(vrec_bytes);
-  const size_t ns_cap = size_t(nsplit_max(T)) + 1;
-  float* ml = (float*)ws;
-  ws += align256(ns_cap * rows * 2 * 4);
-  float* part = (float*)ws;
-
   // fused range: packed in both K and V, aligned to K blocks and V groups
   const int ks = k[0].n, vs = v[0].n;
   const int lo = std::max(ks, vs), hi = std::min(ks + k[1].n, vs + v[1].n);
@@ -321,18 +327,19 @@ int iq_decode_attention(const void* q, int64_t sq_b, int64_t sq_h, const void* n
     const iq_segment& vg = v[1];
     const detail::FusedStore fk{kg.codes, kg.meta, kg.t_cap, kg.t0 + (a0 - ks), kg.bits, kg.group, kg.mode};
     const detail::FusedStore fv{vg.codes, vg.meta, vg.t_cap, vg.t0 + (a0 - vs), vg.bits, vg.group, vg.mode};
-    if (int e = detail::flash_fused_launch(q, sq_b, sq_h, norm, fk, fv, B, Hq, Hkv, c, D, scale, ml, part, st))
+    if (int e = detail::flash_fused_launch(q, sq_b, sq_h, norm, fk, fv, B, Hq, Hkv, c, D, scale, w.ml, w.part, st))
       return e;
   } else if (c) {
     const iq_segment& kg = k[1];
     const iq_segment& vg = v[1];
-    if (int e = detail::qk_record_launch(q, sq_b, sq_h, norm, B, Hq, Hkv, D, kg.group, kg.bits, qrec, st)) return e;
-    const detail::FlashOut f{ml, vrec, vg.bits, vg.group};
-    if (int e = detail::qk_flash_launch(qrec, norm != nullptr, kg.codes, kg.meta, kg.t_cap, B, Hq, Hkv, kg.t0 + (a0 - ks), c, D,
-                                        kg.group, kg.bits, kg.mode, scale, f, st))
+    if (int e = detail::qk_record_launch(q, sq_b, sq_h, norm, B, Hq, Hkv, D, kg.group, kg.bits, w.qrec, st))
       return e;
-    if (int e = detail::av_flash_launch(vrec, vg.codes, vg.meta, vg.t_cap, B, Hq, Hkv, vg.t0 + (a0 - vs), c, D,
-                                        vg.group, vg.bits, vg.mode, part, st))
+    const detail::FlashOut f{w.ml, w.vrec, vg.bits, vg.group};
+    if (int e = detail::qk_flash_launch(w.qrec, norm != nullptr, kg.codes, kg.meta, kg.t_cap, B, Hq, Hkv,
+                                        kg.t0 + (a0 - ks), c, D, kg.group, kg.bits, kg.mode, scale, f, st))
+      return e;
+    if (int e = detail::av_flash_launch(w.vrec, vg.codes, vg.meta, vg.t_cap, B, Hq, Hkv, vg.t0 + (a0 - vs), c, D,
+                                        vg.group, vg.bits, vg.mode, w.part, st))
       return e;
   }
   // dense tokens -> extra split nsf
@@ -345,18 +352,72 @@ int iq_decode_attention(const void* q, int64_t sq_b, int64_t sq_h, const void* n
   da.lo0 = 0; da.hi0 = c ? a0 : T;
   da.lo1 = c ? a0 + c : T; da.hi1 = T;
   da.Hq = Hq; da.Hkv = Hkv; da.D = D; da.scale = scale;
-  da.ml = ml + int64_t(nsf) * rows * 2;
-  da.o = part + int64_t(nsf) * rows * D;
+  da.ml = w.ml + int64_t(nsf) * rows * 2;
+  da.o = w.part + int64_t(nsf) * rows * D;
   const int n_dense = (da.hi0 - da.lo0) + (da.hi1 - da.lo1);
   if (n_dense > 0) {
     dense_attn_kernel<<<dim3(unsigned(rows)), 256, 0, st>>>(da);
     if (int e = launch_status()) return e;
   }
-  const int nsplit = nsf + (n_dense > 0 ? 1 : 0);
-  IQ_CHECK(nsplit <= MAXSPLIT, IQ_ERR_SHAPE);
-  flash_combine_kernel<<<dim3(unsigned(rows)), 256, 0, st>>>(ml, part, nsplit, rows, Hq, D, (uint16_t*)out, so_b,
-                                                              so_h);
+  *nsplit = nsf + (n_dense > 0 ? 1 : 0);
+  return IQ_OK;
+}
+
+int launch_combine(const Workspace& w, int nsplit, int B, int Hq, int D, void* out, int64_t so_b, int64_t so_h,
+                   hipStream_t st) {
+  const int64_t rows = int64_t(B) * Hq;
+  flash_combine_kernel<<<dim3(unsigned(rows)), 256, 0, st>>>(w.ml, w.part, nsplit, rows, Hq, D, (uint16_t*)out,
+                                                              so_b, so_h);
   return launch_status();
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t iq_decode_workspace_bytes(int B, int Hq, int T, int D) {
+  if (B <= 0 || Hq <= 0 || T <= 0 || !d_ok(D)) return 0;
+  const size_t rows = size_t(B) * Hq;
+  size_t vrec = 0;
+  for (int g : {32, 64, 128}) vrec = std::max(vrec, rec_bytes_bound(int64_t(B) * Hq, T / g, g));
+  const size_t ns = size_t(nsplit_max(T)) + 1;
+  return detail::qk_record_bytes(B, Hq, D) + align256(vrec) + align256(ns * rows * 2 * 4) +
+         align256(ns * rows * D * 4);
+}
+
+int iq_decode_attention_splits(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, const iq_segment* k,
+                               const iq_segment* v, int B, int Hq, int Hkv, int T, int D, float scale,
+                               void* workspace, size_t workspace_bytes, int* nsplit, void* stream) {
+  IQ_CHECK(nsplit, IQ_ERR_NULL);
+  if (int e = check_decode(q, k, v, B, Hq, Hkv, T, D, workspace, workspace_bytes)) return e;
+  *nsplit = 0;
+  if (B == 0) return IQ_OK;
+  return launch_splits(q, sq_b, sq_h, norm, k, v, B, Hq, Hkv, T, D, scale, carve(workspace, B, Hq, T, D), nsplit,
+                       (hipStream_t)stream);
+}
+
+int iq_decode_attention_combine(int nsplit, int B, int Hq, int T, int D, void* out, int64_t so_b, int64_t so_h,
+                                void* workspace, size_t workspace_bytes, void* stream) {
+  IQ_CHECK(out && workspace, IQ_ERR_NULL);
+  IQ_CHECK(B >= 0 && Hq > 0 && T > 0 && d_ok(D), IQ_ERR_SHAPE);
+  IQ_CHECK(nsplit >= 1 && nsplit <= nsplit_max(T) + 1 && nsplit <= MAXSPLIT, IQ_ERR_SHAPE);
+  IQ_CHECK(workspace_bytes >= iq_decode_workspace_bytes(B, Hq, T, D), IQ_ERR_WORKSPACE);
+  IQ_CHECK(aligned(workspace, 256), IQ_ERR_ALIGN);
+  if (B == 0) return IQ_OK;
+  return launch_combine(carve(workspace, B, Hq, T, D), nsplit, B, Hq, D, out, so_b, so_h, (hipStream_t)stream);
+}
+
+int iq_decode_attention(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, const iq_segment* k,
+                        const iq_segment* v, int B, int Hq, int Hkv, int T, int D, float scale, void* out,
+                        int64_t so_b, int64_t so_h, void* workspace, size_t workspace_bytes, void* stream) {
+  IQ_CHECK(out, IQ_ERR_NULL);
+  if (int e = check_decode(q, k, v, B, Hq, Hkv, T, D, workspace, workspace_bytes)) return e;
+  if (B == 0) return IQ_OK;
+  const Workspace w = carve(workspace, B, Hq, T, D);
+  int nsplit = 0;
+  if (int e = launch_splits(q, sq_b, sq_h, norm, k, v, B, Hq, Hkv, T, D, scale, w, &nsplit, (hipStream_t)stream))
+    return e;
+  return launch_combine(w, nsplit, B, Hq, D, out, so_b, so_h, (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -271,11 +271,7 @@ def _segment(dense: Optional[torch.Tensor], store: Optional[PackedStore], n: int
     return s
 
 
-def decode_attention(q: torch.Tensor, k_sink: Optional[torch.Tensor], k_store: Optional[PackedStore],
-                     k_recent: Optional[torch.Tensor], v_sink: Optional[torch.Tensor],
-                     v_store: Optional[PackedStore], v_recent: Optional[torch.Tensor], scale: float,
-                     norm: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """One decode step of attention for q [B,Hq,D] over [sink | packed | recent] K and V."""
+def _decode_args(q, k_sink, k_store, k_recent, v_sink, v_store, v_recent, norm):
     require_device(q, "q")
     B, Hq, D = q.shape
     if q.stride(-1) != 1:
@@ -294,14 +290,46 @@ def decode_attention(q: torch.Tensor, k_sink: Optional[torch.Tensor], k_store: O
                                _segment(k_recent, None, kn[2]))
     vs = (_lib.iq_segment * 3)(_segment(v_sink, None, vn[0]), _segment(None, v_store, vn[1]),
                                _segment(v_recent, None, vn[2]))
-    if out is None:
-        out = torch.empty(B, Hq, D, dtype=torch.float16, device=q.device)
     if norm is not None:
         norm = norm.reshape(B, Hkv, D).contiguous()
-    nbytes = _lib.lib().iq_decode_workspace_bytes(B, Hq, T, D)
-    ws = _workspace(q.device, nbytes)
+    ws = _workspace(q.device, _lib.lib().iq_decode_workspace_bytes(B, Hq, T, D))
+    return q, B, Hq, Hkv, T, D, ks, vs, norm, ws
+
+
+def decode_attention(q: torch.Tensor, k_sink: Optional[torch.Tensor], k_store: Optional[PackedStore],
+                     k_recent: Optional[torch.Tensor], v_sink: Optional[torch.Tensor],
+                     v_store: Optional[PackedStore], v_recent: Optional[torch.Tensor], scale: float,
+                     norm: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """One decode step of attention for q [B,Hq,D] over [sink | packed | recent] K and V."""
+    q, B, Hq, Hkv, T, D, ks, vs, norm, ws = _decode_args(q, k_sink, k_store, k_recent, v_sink, v_store, v_recent,
+                                                         norm)
+    if out is None:
+        out = torch.empty(B, Hq, D, dtype=torch.float16, device=q.device)
     call("iq_decode_attention", _p(q), q.stride(0), q.stride(1), _p(norm), ks, vs, B, Hq, Hkv, T, D, float(scale),
          _p(out), out.stride(0), out.stride(1), _p(ws), ws.numel(), _stream(q.device))
+    return out
+
+
+def decode_attention_splits(q, k_sink, k_store, k_recent, v_sink, v_store, v_recent, scale, norm=None) -> int:
+    """The split stage of decode_attention (statistics + partials in the device's
+    decode workspace); returns the split count for decode_attention_combine."""
+    q, B, Hq, Hkv, T, D, ks, vs, norm, ws = _decode_args(q, k_sink, k_store, k_recent, v_sink, v_store, v_recent,
+                                                         norm)
+    ns = ctypes.c_int(0)
+    call("iq_decode_attention_splits", _p(q), q.stride(0), q.stride(1), _p(norm), ks, vs, B, Hq, Hkv, T, D,
+         float(scale), _p(ws), ws.numel(), ctypes.byref(ns), _stream(q.device))
+    return ns.value
+
+
+def decode_attention_combine(nsplit: int, B: int, Hq: int, T: int, D: int, device,
+                             out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """The combine stage: merges the splits left in the device's decode workspace."""
+    device = torch.device(device)
+    if out is None:
+        out = torch.empty(B, Hq, D, dtype=torch.float16, device=device)
+    ws = _workspace(device, _lib.lib().iq_decode_workspace_bytes(B, Hq, T, D))
+    call("iq_decode_attention_combine", nsplit, B, Hq, T, D, _p(out), out.stride(0), out.stride(1), _p(ws),
+         ws.numel(), _stream(device))
     return out
 
 

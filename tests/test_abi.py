@@ -174,3 +174,21 @@ def test_cpu_tensor_raises_no_fallback():
     from innerq_amd import ops
     with pytest.raises(TypeError, match="no CPU path"):
         ops.quantize_dense(torch.zeros(2, 64, dtype=torch.float16), 32, 4, "asymmetric", "channel")
+
+
+def test_decode_stage_rejects():
+    lib = _lib.lib()
+    ns = ctypes.c_int(-7)
+    seg = (_lib.iq_segment * 3)()
+    seg[2].n = 64
+    seg[2].dense = FAKE
+    # a NULL split-count pointer, then a bad shape: rejected before any launch
+    assert lib.iq_decode_attention_splits(FAKE, 1024, 128, None, seg, seg, 1, 32, 8, 64, 128, 1.0, FAKE, 1 << 30,
+                                          None, None) == -1
+    assert lib.iq_decode_attention_splits(FAKE, 1024, 128, None, seg, seg, 1, 32, 8, 64, 96, 1.0, FAKE, 1 << 30,
+                                          ctypes.byref(ns), None) == -4
+    assert ns.value == -7
+    assert lib.iq_decode_attention_combine(0, 1, 32, 64, 128, FAKE, 4096, 128, FAKE, 1 << 30, None) == -4
+    assert lib.iq_decode_attention_combine(3, 1, 32, 64, 128, FAKE, 4096, 128, FAKE, 1 << 30, None) == -4
+    assert lib.iq_decode_attention_combine(1, 1, 32, 64, 128, None, 4096, 128, FAKE, 1 << 30, None) == -1
+    assert lib.iq_decode_attention_combine(1, 1, 32, 64, 128, FAKE, 4096, 128, FAKE, 64, None) == -6

@@ -414,3 +414,25 @@ def test_decode_attention_fused_formats(fmt, nrep, D):
     vseg = (16, vq, 64 * 21 + 80 - vq)
     err = _decode_case(2, 2, nrep, D, kseg, vseg, (bits, G, km), (bits, G, vm), seed=bits * G + nrep, norm=True)
     assert err < TOL
+
+
+@pytest.mark.parametrize("fused", [True, False])
+def test_decode_stages_equal_decode_attention(fused):
+    """iq_decode_attention_splits + _combine give decode_attention's output bit for bit
+    (fused split kernel: K and V of one format; unfused: different bit widths)."""
+    B, Hkv, nrep, D = 2, 2, 4, 128
+    kb, vb = (4, 4) if fused else (2, 4)
+    T = 64 * 12 + 40
+    kx = synth.kv_tensor(B, Hkv, T, D, seed=61)
+    vx = synth.kv_tensor(B, Hkv, T, D, seed=62)
+    kst = ops.PackedStore("channel", B, Hkv, D, 32, kb, "asymmetric", DEV)
+    vst = ops.PackedStore("token", B, Hkv, D, 32, vb, "asymmetric", DEV)
+    kst.append(f16t(kx[:, :, :768]))
+    vst.append(f16t(vx[:, :, :768]))
+    kr, vr = f16t(kx[:, :, 768:]), f16t(vx[:, :, 768:])
+    q = f16t(synth.normal((B, Hkv * nrep, D), seed=63).astype(np.float16))
+    ref = ops.decode_attention(q, None, kst, kr, None, vst, vr, D ** -0.5).cpu().numpy()
+    ns = ops.decode_attention_splits(q, None, kst, kr, None, vst, vr, D ** -0.5)
+    assert ns == 2 + 1  # two 512-token splits of the packed range + the dense tail
+    got = ops.decode_attention_combine(ns, B, Hkv * nrep, T, D, DEV).cpu().numpy()
+    np.testing.assert_array_equal(got.view(np.uint16), ref.view(np.uint16))
