@@ -86,3 +86,17 @@ def test_dynamic_cache_layer_types():
                          intermediate_size=32, vocab_size=16, sliding_window=16)
     cache = C.DynamicCache(config=mcfg)
     assert all(isinstance(l, C.InnerqDynamicSlidingWindowLayer) and l.sliding_window == 16 for l in cache.layers)
+
+
+def test_model_hooks_install_the_drop_in_cache():
+    from transformers import LlamaConfig
+    from innerq_amd.models import InnerqLlamaForCausalLM
+    cfg = LlamaConfig(num_hidden_layers=2, num_attention_heads=4, num_key_value_heads=2, hidden_size=64,
+                      intermediate_size=32, vocab_size=16)
+    cfg.k_bits, cfg.v_bits = 4, 2
+    model = InnerqLlamaForCausalLM(cfg)
+    kw = {}
+    model._prepare_cache_for_generation(None, kw, None, 1, 0)
+    cache = kw["past_key_values"]
+    assert isinstance(cache, C.DynamicCache) and len(cache.layers) == 2
+    assert cache.layers[0].key_bits == 4 and cache.layers[1].value_bits == 2
