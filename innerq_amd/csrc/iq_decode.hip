@@ -147,17 +147,21 @@ __global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs a) {
 }
 
 // out[bq, d] = sum_s e^{m_s - M} o_s[bq, d] / sum_s e^{m_s - M} l_s
-// One workgroup per row bq.  The split weights go to LDS once; then thread t
-// takes column quad t % (D/4) and every NSL-th split starting at t / (D/4),
-// with all of its 16-byte partial loads independent (in flight together), and
-// the NSL slices are summed in LDS in slice order.
+// One workgroup per row bq.  The splits with a nonzero weight are listed in
+// LDS in split order (a split slot with m = -inf carries no tokens: the fused
+// kernel leaves such slots' partials unwritten, so they must not be read);
+// then thread t takes column quad t % (D/4) and every NSL-th listed split
+// starting at t / (D/4), with all of its 16-byte partial loads independent (in
+// flight together), and the NSL slices are summed in LDS in slice order.
 constexpr int MAXSPLIT = 1024;
 __global__ __launch_bounds__(256) void flash_combine_kernel(const float* __restrict__ ml, const float* __restrict__ part,
                                                             int nsplit, int64_t rows, int Hq, int D,
                                                             uint16_t* __restrict__ out, int64_t sob, int64_t soh) {
   __shared__ float wgt[MAXSPLIT];
+  __shared__ int sidx[MAXSPLIT];
   __shared__ float4 red[256];
   __shared__ float rs[4];
+  __shared__ int cnt[4];
   const int64_t bq = blockIdx.x;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   float mx = -INFINITY;
@@ -168,11 +172,27 @@ __global__ __launch_bounds__(256) void flash_combine_kernel(const float* __restr
   const float M = fmaxf(fmaxf(rs[0], rs[1]), fmaxf(rs[2], rs[3]));
   __syncthreads();
   float L = 0.f;
-  for (int s = tid; s < nsplit; s += 256) {
-    const float ms = ml[(int64_t(s) * rows + bq) * 2];
-    const float w = ms == -INFINITY ? 0.f : __expf(ms - M);
-    wgt[s] = w;
-    L = fmaf(w, ml[(int64_t(s) * rows + bq) * 2 + 1], L);
+  int nnz = 0;
+  for (int s0 = 0; s0 < nsplit; s0 += 256) {
+    const int s = s0 + tid;
+    float w = 0.f;
+    if (s < nsplit) {
+      const float ms = ml[(int64_t(s) * rows + bq) * 2];
+      w = ms == -INFINITY ? 0.f : __expf(ms - M);
+      if (w != 0.f) L = fmaf(w, ml[(int64_t(s) * rows + bq) * 2 + 1], L);
+    }
+    const unsigned long long bal = __ballot(w != 0.f);
+    if (lane == 0) cnt[wave] = __popcll(bal);
+    __syncthreads();
+    int off = nnz;
+    for (int x = 0; x < wave; ++x) off += cnt[x];
+    if (w != 0.f) {
+      const int k = off + __popcll(bal & ((1ull << lane) - 1ull));
+      sidx[k] = s;
+      wgt[k] = w;
+    }
+    nnz += (cnt[0] + cnt[1]) + (cnt[2] + cnt[3]);
+    __syncthreads();
   }
   L = wave_sum(L);
   if (lane == 0) rs[wave] = L;
@@ -185,21 +205,21 @@ __global__ __launch_bounds__(256) void flash_combine_kernel(const float* __restr
   const int64_t sstride = rows * D / 4;  // float4 per split
   float4 acc = {0.f, 0.f, 0.f, 0.f};
   constexpr int U = 8;
-  int s = sl;
-  for (; s + (U - 1) * nsl < nsplit; s += U * nsl) {
+  int k = sl;
+  for (; k + (U - 1) * nsl < nnz; k += U * nsl) {
     float4 v[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) v[u] = pc[int64_t(s + u * nsl) * sstride];
+    for (int u = 0; u < U; ++u) v[u] = pc[int64_t(sidx[k + u * nsl]) * sstride];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      const float w = wgt[s + u * nsl];
+      const float w = wgt[k + u * nsl];
       acc.x = fmaf(w, v[u].x, acc.x); acc.y = fmaf(w, v[u].y, acc.y);
       acc.z = fmaf(w, v[u].z, acc.z); acc.w = fmaf(w, v[u].w, acc.w);
     }
   }
-  for (; s < nsplit; s += nsl) {
-    const float4 v = pc[int64_t(s) * sstride];
-    const float w = wgt[s];
+  for (; k < nnz; k += nsl) {
+    const float4 v = pc[int64_t(sidx[k]) * sstride];
+    const float w = wgt[k];
     acc.x = fmaf(w, v.x, acc.x); acc.y = fmaf(w, v.y, acc.y);
     acc.z = fmaf(w, v.z, acc.z); acc.w = fmaf(w, v.w, acc.w);
   }
@@ -321,12 +341,12 @@ int launch_splits(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, c
   if (c <= 0) { a0 = 0; c = 0; }
   const int nsf = c ? int(ceil_div(c, detail::flash_split_tokens())) : 0;
 
+  const detail::FusedStore fk{k[1].codes, k[1].meta, k[1].t_cap, k[1].t0 + (a0 - ks), k[1].bits, k[1].group,
+                              k[1].mode};
+  const detail::FusedStore fv{v[1].codes, v[1].meta, v[1].t_cap, v[1].t0 + (a0 - vs), v[1].bits, v[1].group,
+                              v[1].mode};
   if (c && k[1].bits == v[1].bits && k[1].group == v[1].group &&
-      detail::flash_fused_supported(q, sq_b, sq_h, norm)) {
-    const iq_segment& kg = k[1];
-    const iq_segment& vg = v[1];
-    const detail::FusedStore fk{kg.codes, kg.meta, kg.t_cap, kg.t0 + (a0 - ks), kg.bits, kg.group, kg.mode};
-    const detail::FusedStore fv{vg.codes, vg.meta, vg.t_cap, vg.t0 + (a0 - vs), vg.bits, vg.group, vg.mode};
+      detail::flash_fused_supported(q, sq_b, sq_h, norm, fk, fv, Hq, Hkv, D)) {
     if (int e = detail::flash_fused_launch(q, sq_b, sq_h, norm, fk, fv, B, Hq, Hkv, c, D, scale, w.ml, w.part, st))
       return e;
   } else if (c) {

@@ -10,18 +10,24 @@
 // A window of the group's bit string (a word, a shifted word, or an alignbit
 // of two words) is masked and OR-ed with an fp16 exponent pattern in one
 // v_and_or_b32, which yields two fp16 values {bias_a + c_a, bias_b + c_b}
-// exactly (field LSB weight 1, bias 2^(10-p) for a field at in-half bit p);
-// one v_pk_add_f16 removes the biases, leaving the two codes as exact fp16
-// integers for the matrix cores.  Sym codes are turned into offset binary
+// exactly (field LSB weight 1, bias 2^(10-p) for a field at in-half bit p).
+// The fused decode kernel feeds these biased pairs to the matrix cores as
+// they are and starts each accumulation from -sum(operand * bias) (exact
+// powers of two, summed once per operand record), so the bias costs no VALU;
+// the unfused kernels remove it with one v_pk_add_f16 per pair (exact: both
+// operands are integers below 2048).  The plans keep every field at p >= 10 -
+// b - 4 or so, i.e. bias / code unit <= 256 (4-bit), 64 (2-bit), 128 (3-bit):
+// the fp32 partial sums stay within ~2^8 of the result, a relative error of a
+// few 1e-6 per 128-code dot product.  Sym codes are turned into offset binary
 // with one XOR per word (u = signed + 2^(b-1)), so
 // sum(q*signed) = sum(q*u) - 2^(b-1)*sum(q), folded into the zero term.
 //
-// Plans (windows counted as extra VALU ops, aligned words are free):
-//   4-bit, per word (8 codes):   s=0 {(0,4),(1,5)}, s=8 {(2,6),(3,7)}
-//   2-bit, per word (16 codes):  s=0 {(i,i+8) i<5},  s=10 {(i,i+8) 5<=i<8}
-//   3-bit, per 3 words (32 codes): distance-5 pairs in two 10-code blocks,
-//          distance-6 pairs for the last 12 codes; windows
-//          s in {-1, 8, 29, 38, 60, 66, 72}.
+// Plans (found by exhaustive search for the fewest windows under that bias
+// bound; S = window start bit, word-aligned windows are free):
+//   4-bit, per word (8 codes):   pairs (i, i+4); S = -6, 0, 6, 6  (2 shifts)
+//   2-bit, per word (16 codes):  pairs (i, i+8); S = -6,-6, 0,0,0, 6,6,6
+//   3-bit, per 3 words (32 codes): 16 pairs over 11 windows, 8 of them
+//          shifts or alignbits (24 VALU per 32 codes).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -41,23 +47,23 @@ template <int BITS> struct Plan;
 
 template <> struct Plan<4> {
   static constexpr int WORDS = 1, CODES = 8, NPAIR = 4;
-  static constexpr int S[NPAIR] = {0, 0, 8, 8};
+  static constexpr int S[NPAIR] = {-6, 0, 6, 6};
   static constexpr int A[NPAIR] = {0, 1, 2, 3};
   static constexpr int C[NPAIR] = {4, 5, 6, 7};
   static constexpr uint32_t SIGN[WORDS] = {0x88888888u};
 };
 template <> struct Plan<2> {
   static constexpr int WORDS = 1, CODES = 16, NPAIR = 8;
-  static constexpr int S[NPAIR] = {0, 0, 0, 0, 0, 10, 10, 10};
+  static constexpr int S[NPAIR] = {-6, -6, 0, 0, 0, 6, 6, 6};
   static constexpr int A[NPAIR] = {0, 1, 2, 3, 4, 5, 6, 7};
   static constexpr int C[NPAIR] = {8, 9, 10, 11, 12, 13, 14, 15};
   static constexpr uint32_t SIGN[WORDS] = {0xAAAAAAAAu};
 };
 template <> struct Plan<3> {
   static constexpr int WORDS = 3, CODES = 32, NPAIR = 16;
-  static constexpr int S[NPAIR] = {-1, -1, -1, 8, 8, 29, 29, 29, 38, 38, 60, 60, 66, 66, 72, 72};
-  static constexpr int A[NPAIR] = {0, 1, 2, 3, 4, 10, 11, 12, 13, 14, 20, 21, 22, 23, 24, 25};
-  static constexpr int C[NPAIR] = {5, 6, 7, 8, 9, 15, 16, 17, 18, 19, 26, 27, 28, 29, 30, 31};
+  static constexpr int S[NPAIR] = {-4, -4, 0, 5, 5, 26, 26, 32, 32, 35, 53, 58, 61, 64, 71, 71};
+  static constexpr int A[NPAIR] = {0, 1, 2, 3, 4, 10, 11, 12, 13, 14, 20, 21, 22, 23, 25, 26};
+  static constexpr int C[NPAIR] = {5, 6, 7, 8, 9, 15, 16, 17, 18, 19, 24, 27, 28, 29, 30, 31};
   static constexpr uint32_t SIGN[WORDS] = {0x24924924u, 0x49249249u, 0x92492492u};
 };
 
@@ -71,6 +77,26 @@ template <int BITS> __host__ __device__ constexpr uint32_t magic_of(int k) {
 }
 template <int BITS> __host__ __device__ constexpr float bias_a(int k) { return float(1 << (10 - pa_of<BITS>(k))); }
 template <int BITS> __host__ __device__ constexpr float bias_c(int k) { return float(1 << (10 - pc_of<BITS>(k))); }
+
+// A plan is valid when its pairs cover every code of the super-block once,
+// every field lies inside its half's 10-bit mantissa at p >= 2 (bias <= 256
+// code units), and every window is one the window() helper can form.
+template <int BITS>
+constexpr bool plan_valid() {
+  using P = Plan<BITS>;
+  int seen[P::CODES] = {};
+  for (int k = 0; k < P::NPAIR; ++k) {
+    const int pa = pa_of<BITS>(k), pc = pc_of<BITS>(k);
+    if (pa < 2 || pa > 10 - BITS || pc < 2 || pc > 10 - BITS) return false;
+    if (P::S[k] < -9 || P::S[k] >= 32 * P::WORDS) return false;
+    ++seen[P::A[k]];
+    ++seen[P::C[k]];
+  }
+  for (int i = 0; i < P::CODES; ++i)
+    if (seen[i] != 1) return false;
+  return P::CODES * BITS == 32 * P::WORDS;
+}
+static_assert(plan_valid<2>() && plan_valid<3>() && plan_valid<4>(), "pair plans");
 
 // window of the super-block's bit string starting at bit S (S may be -1..-9:
 // a left shift of word 0; windows past the end are zero-filled).

@@ -1,115 +1,75 @@
-// Fused flash-decoding split (gfx950): QK^T, softmax and attn.V of one
-// (batch, KV head) over FSPLIT consecutive tokens in one workgroup, for K and
-// V stores that share bit width and group size.
+// Fused flash-decoding split kernel (gfx950): QK^T, softmax and attn.V of one
+// (batch, KV head) over a split of FSPLIT consecutive tokens, for K and V
+// stores that share bit width and group size.  The combine kernel
+// (iq_decode.hip) merges the splits' partial outputs.
 //
-// Each of the four waves owns a sub-split of FBPW*64 consecutive tokens
-// (lane = token for QK^T) and runs the whole pipeline on it alone; the waves
-// meet only at the start (query records) and at the end (merge):
-//   start  query operand records of the D/G head_dim groups, built in LDS
-//          while every wave's first K group is in flight (a key
-//          normalization, which the reference applies to the dequantized
+// Persistent and software pipelined.  The grid holds as many workgroups as fit
+// on the device; workgroup w processes splits w, w + grid, ...  A wave owns
+// WTOK consecutive tokens of the split (lane = token for QK^T) and streams its
+// packed data straight into VGPRs with raw buffer loads.  At the top of each
+// split it issues, oldest first:
+//   V codes and {scale, zero} of its tokens (lane = head_dim column),
+//   K codes and {scale, zero} of the NEXT split (kept in flight across the
+//   whole split), and the q (and key-norm) values of the next split's records;
+// then runs, on data loaded one split earlier:
+//   QK^T   per head_dim group eight v_mfma_f32_4x4x4f16 per 32 codes and four
+//          query heads (iq_gemv.h), A = query records in LDS;
+//   softmax  max per head over the wave (DPP), p = exp2(logit*scale*log2e -
+//          m); each lane writes its fp16 p straight into its slot of the
+//          wave's attn.V operand records (the inverse of the unpack plan); the
+//          per-V-group sums of p (zero-point term, and the wave's l) by DPP;
+//   attn.V lane = column d = lane + 64 e over the wave's V groups;
+//   merge  m = max over the waves, outputs rescaled by exp2(m_w - m) and
+//          summed in LDS; the split's (m, l) and unnormalized output go to the
+//          split statistics and partials;
+//   records  the next split's query records from the prefetched q values (a
+//          key normalization, which the reference applies to the dequantized
 //          keys, cache.py:128-133 and 249, is folded into q as hi/lo fp16
-//          parts of q*n);
-//   QK^T   the wave walks the head_dim groups with the next group's code words
-//          and {scale, zero} prefetched, eight v_mfma_f32_4x4x4f16 per 32
-//          codes and four query heads (iq_gemv.h); its V groups' loads are
-//          issued when the last K group has arrived;
-//   softmax  max m_w over the sub-split per head (DPP reduction), p =
-//          exp(logit - m_w); each lane writes its fp16 p straight into its
-//          slot of the wave's attn.V operand records (the inverse of the
-//          unpack plan), and the wave sums l_w = sum p (fp32);
-//   attn.V lane = head_dim column d = lane + 64 e over the wave's V groups
-//          (G divides the sub-split);
-//   merge  m = max_w m_w; each wave's output is rescaled by exp(m_w - m) and
-//          the four are summed in LDS in wave order; the split's (m, l) and
-//          unnormalized output go to the split statistics and partials.
-// The probabilities never leave LDS, nothing is exchanged between waves in
-// the middle of the pipeline (so the waves of a CU drift apart and one's
-// arithmetic overlaps another's loads), and one launch replaces the
-// query-record, QK^T and attn.V launches of the unfused path.  A combine
-// kernel (iq_decode.hip) merges the splits.
+//          parts of q*n).
+// The memory system always has the next split's K of every resident wave in
+// flight, so load latency overlaps the arithmetic of the current split instead
+// of opening each workgroup's life.
 //
 // The store formats follow the unfused kernels: K codes [B,H,t_cap/64,D/G,64,W],
 // V codes [B,H,t_cap/G,D,W]; sym or asym per store is a runtime flag (a
 // uniform branch), so the kernel is instantiated per (bits, G, D, n_rep) only.
+#include <algorithm>
+
 #include "iq_gemv.h"
 
 using namespace iq;
 
 namespace {
 
-constexpr int FBPW = IQ_FLASH_BPW;                   // 64-token K blocks per wave
-constexpr int WTOK = FBPW * TOKEN_BLOCK;             // tokens per wave (sub-split)
-constexpr int FSPLIT = NWAVES * WTOK;                // tokens per workgroup
+constexpr int FSPLIT = NWAVES * IQ_FLASH_BPW * TOKEN_BLOCK;  // tokens per split (= flash_split_tokens())
 
-// V units loaded into each K group's slots as soon as QK^T has read them (1),
-// or all after QK^T (0).
-#ifndef IQ_FLASH_VSTREAM
-#define IQ_FLASH_VSTREAM 0
-#endif
-
-// Fully unrolled group loops (1) or runtime loops (0).
-#ifndef IQ_FLASH_UNROLL
-#define IQ_FLASH_UNROLL 0
-#endif
-#if IQ_FLASH_UNROLL
-#define IQ_GROUP_LOOP _Pragma("unroll")
-#else
-#define IQ_GROUP_LOOP _Pragma("unroll 1")
-#endif
 
 // Pair k of a group's unpack plan: code index of its first and second half.
 template <int BITS>
-__host__ __device__ constexpr int plan_a(int k) {
-  if constexpr (BITS == 4) {
-    return 8 * (k >> 2) + (k & 3);
-  } else if constexpr (BITS == 2) {
-    return 16 * (k >> 3) + (k & 7);
-  } else {
-    const int kk = k & 15;
-    return 32 * (k >> 4) + (kk < 5 ? kk : kk < 10 ? kk + 5 : kk + 10);
-  }
-}
+__host__ __device__ constexpr int plan_a(int k) { return pair_code_a<BITS>(k); }
 template <int BITS>
-__host__ __device__ constexpr int plan_c(int k) {
-  if constexpr (BITS == 4) return plan_a<4>(k) + 4;
-  else if constexpr (BITS == 2) return plan_a<2>(k) + 8;
-  else return plan_a<3>(k) + ((k & 15) < 10 ? 5 : 6);
-}
-template <int BITS>
-constexpr bool plan_formula_ok() {
-  for (int k = 0; k < 64; ++k)
-    if (plan_a<BITS>(k) != pair_code_a<BITS>(k) || plan_c<BITS>(k) != pair_code_c<BITS>(k)) return false;
-  return true;
-}
-static_assert(plan_formula_ok<2>() && plan_formula_ok<3>() && plan_formula_ok<4>(), "plan formula");
+__host__ __device__ constexpr int plan_c(int k) { return pair_code_c<BITS>(k); }
 
-// Inverse of the plan: code i of a group sits in pair k, half hi (0: low).
+// Inverse of the plan: code i of a group sits in pair k, half hi (0: low),
+// with bias 2^(10 - p) (p = the field's bit position in its half).
 template <int BITS>
-__host__ __device__ constexpr void plan_inv(int i, int& k, int& hi) {
-  if constexpr (BITS == 4) {
-    const int r = i & 7;
-    k = 4 * (i >> 3) + (r & 3);
-    hi = r >> 2;
-  } else if constexpr (BITS == 2) {
-    const int r = i & 15;
-    k = 8 * (i >> 4) + (r & 7);
-    hi = r >> 3;
-  } else {
-    const int r = i & 31, sb = 16 * (i >> 5);
-    if (r < 5) { k = sb + r; hi = 0; }
-    else if (r < 10) { k = sb + r - 5; hi = 1; }
-    else if (r < 15) { k = sb + r - 5; hi = 0; }
-    else if (r < 20) { k = sb + r - 10; hi = 1; }
-    else if (r < 26) { k = sb + r - 10; hi = 0; }
-    else { k = sb + r - 16; hi = 1; }
+__host__ __device__ constexpr void plan_inv(int i, int& k, int& hi, float& bias) {
+  using P = Plan<BITS>;
+  const int sb = i / P::CODES, r = i % P::CODES;
+  k = 0;
+  hi = 0;
+  bias = 0.f;
+  for (int x = 0; x < P::NPAIR; ++x) {
+    if (P::A[x] == r) { k = sb * P::NPAIR + x; hi = 0; bias = bias_a<BITS>(x); }
+    if (P::C[x] == r) { k = sb * P::NPAIR + x; hi = 1; bias = bias_c<BITS>(x); }
   }
 }
 template <int BITS>
 constexpr bool plan_inv_ok() {
   for (int i = 0; i < 128; ++i) {
     int k = 0, hi = 0;
-    plan_inv<BITS>(i, k, hi);
+    float b = 0.f;
+    plan_inv<BITS>(i, k, hi, b);
     if ((hi ? plan_c<BITS>(k) : plan_a<BITS>(k)) != i) return false;
   }
   return true;
@@ -128,382 +88,499 @@ struct FusedArgs {
   const uint16_t* vm;
   int64_t v_cap_groups;
   int vg0, vsym;
-  int Hkv, T;  // T: tokens of the range, a multiple of G
-  float scale;
-  float* ml;    // [nsplit][B*Hq][2]
-  float* part;  // [nsplit][B*Hq][D]
+  int Hkv, T;          // T: tokens of the range, a multiple of G
+  int nsplit, nitems;  // splits per (batch, KV head); nsplit * B * Hkv
+  uint32_t k_code_bytes, k_meta_bytes, v_code_bytes, v_meta_bytes, q_bytes, norm_bytes;
+  float scale_log2;    // scale * log2(e)
+  float* ml;           // [nsplit][B*Hq][2]
+  float* part;         // [nsplit][B*Hq][D]
 };
 
-// Staging of packed data in LDS.  A "unit" is the data of 64 lanes for one
-// (K block, head_dim group) or one (V group, 64-column set): 64 x W code words
-// in chunks of CW words per lane ([chunk][lane][CW] words, one direct
-// global->LDS load per chunk) followed by 256 bytes of {scale, zero} (asym:
-// one dword per lane; sym: the 128 bytes of 64 fp16 scales, loaded as 32
-// dwords).  Each wave stages its own units in a private region: all of its K
-// units at kernel start, then, once its QK^T is done, its V units in the same
-// place.  Loads land in LDS without occupying VGPRs, so a wave has every byte
-// of its sub-split in flight at once.
-template <int W>
-struct Stage {
-  static constexpr int CW = W % 4 == 0 ? 4 : 1;  // words per lane per load (16- or 4-byte loads)
-  static constexpr int NCHK = W / CW;
-  static constexpr int META = W * 256;              // byte offset of the meta block
-  static constexpr int UNIT = (W + 1) * 256;        // bytes per unit
-};
-
-// Records use the padded stride rec_dwords(): each head's pairs start 16-byte
-// aligned, as the 16-byte LDS reads of the matrix-core operand require.
-template <int BITS, int G, int D, int NREP>
-struct FusedSmem {
-  static constexpr int W = G * BITS / 32;
-  static constexpr int NUNITS = (D / G) * FBPW;  // = (WTOK / G) * (D / 64)
-  static constexpr int QDW = NREP * D / 2;                 // query dwords (fp16 pairs)
-  static constexpr int QDW_PAD = (QDW + 63) / 64 * 64;     // whole 64-lane loads
-  alignas(16) uint32_t qrec[D / G][qrec_dwords<G, NREP>()];
-  alignas(16) uint32_t vrec[NWAVES][WTOK / G][rec_dwords<G, NREP>()];
-  alignas(16) uint32_t qraw[QDW_PAD];  // q rows of the n_rep heads, [h][D] fp16
-  alignas(16) uint32_t nraw[64];       // key normalization row, D fp16
-  union alignas(16) {
-    unsigned char stage[NWAVES][NUNITS * Stage<W>::UNIT];  // until attn.V ends
-    float red[NWAVES - 1][NREP][D];                         // merge
-  };
-  float m[NWAVES][NREP];
-  float l[NWAVES][NREP];
-};
-
-// Direct global->LDS load of BYTES per lane (4 or 16); lane i's data lands
-// at lds + i * BYTES.
-template <int BYTES>
-__device__ __forceinline__ void dma_t(const void* src, void* lds) {
-  auto* l = (__attribute__((address_space(3))) void*)lds;
-  if constexpr (BYTES == 16) __builtin_amdgcn_global_load_lds(src, l, 16, 0, 0);
-  else if constexpr (BYTES == 4) __builtin_amdgcn_global_load_lds(src, l, 4, 0, 0);
-  else static_assert(BYTES == 4, "direct LDS loads of 4 or 16 bytes per lane");
+// waves per SIMD the register allocation aims at: three (<= 168 VGPRs) for
+// 64-token waves and up to 4 query heads per KV head, fewer where the operand
+// and accumulator registers need more (8 heads, or hi/lo query rows with 4)
+template <int G, int NREP, bool QS>
+constexpr int fused_waves_per_simd() {
+  return G > TOKEN_BLOCK ? 1 : (NREP > 4 || (QS && NREP == 4)) ? 2 : 3;
 }
 
-// The compiler does not order LDS reads after direct LDS loads: every read
-// of a stage region is preceded by an explicit wait for the loads.
-__device__ __forceinline__ void wait_vm_all() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
-__device__ __forceinline__ void wait_lgkm_all() { asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory"); }
+// Workgroup shape: one workgroup per CU, filling every SIMD to the register
+// allocation's occupancy; a wave processes blocks of WTOK consecutive tokens
+// (lane = token for QK^T), so that a V group of G tokens lies inside a block.
+template <int G, int NREP, bool QS>
+struct FusedShape {
+  static constexpr int WTOK = G > TOKEN_BLOCK ? G : TOKEN_BLOCK;
+  static constexpr int FBPW = WTOK / TOKEN_BLOCK;                // 64-token K blocks per wave block
+  static constexpr int NW = 4 * fused_waves_per_simd<G, NREP, QS>();  // waves per workgroup
+  static constexpr int NT = NW * 64;
+  static constexpr int VPW = WTOK / G;                           // V groups per wave block
+  static_assert(FSPLIT % WTOK == 0, "a split holds whole wave blocks");
+};
 
-// Workgroup barrier for data exchanged through LDS only.  __syncthreads()
-// would also wait for every outstanding global load, direct LDS loads
-// included, i.e. for the wave's whole stage stream; the stage regions are
-// wave-private, so only the LDS writes need to be complete.
+template <int BITS, int G, int D, int NREP, bool QS>
+struct FusedSmem {
+  using FS = FusedShape<G, NREP, QS>;
+  alignas(16) uint32_t qrec[D / G][qrec_dwords<G, NREP>()];         // query records of the current split
+  alignas(16) uint32_t vrec[FS::NW][FS::VPW][rec_dwords<G, NREP>()];  // per wave: fp16 p pairs
+  alignas(16) float red[FS::NW][NREP][D];                            // merge of the waves' outputs
+  float m[FS::NW][NREP];
+  float l[FS::NW][NREP];
+  int next_block;  // the current run's next unclaimed wave block
+};
+
+// ---- raw buffer loads -------------------------------------------------------
+// Each split reads its (batch, KV head) slice of a store through a buffer
+// resource: a byte offset per lane (VGPR) plus a uniform offset (SGPR).  A
+// resource with zero records turns every load into a zero fill that moves no
+// data; the prefetch of "the next split" after a workgroup's last one uses
+// that, so every iteration issues the same loads and the compiler's memory
+// counter waits stay exact.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, int(bytes), 0x00020000);
+}
+template <int N>
+__device__ __forceinline__ void bload_words(rsrc_t r, uint32_t voff, uint32_t soff, uint32_t (&w)[N]) {
+#pragma unroll
+  for (int c = 0; c < N / 4; ++c) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff + 16 * c, soff, 0);
+    w[4 * c] = v[0]; w[4 * c + 1] = v[1]; w[4 * c + 2] = v[2]; w[4 * c + 3] = v[3];
+  }
+  constexpr int R = N % 4, C0 = N - N % 4;
+  if constexpr (R == 3) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b96(r, voff + 4 * C0, soff, 0);
+    w[C0] = v[0]; w[C0 + 1] = v[1]; w[C0 + 2] = v[2];
+  } else if constexpr (R == 2) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, voff + 4 * C0, soff, 0);
+    w[C0] = v[0]; w[C0 + 1] = v[1];
+  } else if constexpr (R == 1) {
+    w[C0] = __builtin_amdgcn_raw_buffer_load_b32(r, voff + 4 * C0, soff, 0);
+  }
+}
+__device__ __forceinline__ uint32_t bload_u32(rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+}
+__device__ __forceinline__ uint16_t bload_u16(rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);
+}
+
+// {scale, zero} of a lane's token (K) or column (V) from its meta dword: asym
+// meta is one {scale, zero} dword per lane; sym meta is one fp16 scale per
+// lane, read as the dword holding the scales of lanes 2i and 2i + 1.
+__device__ __forceinline__ uint32_t meta_voff(int lane, int sym) { return sym ? uint32_t(lane & ~1) * 2 : uint32_t(lane) * 4; }
+template <int BITS>
+__device__ __forceinline__ void meta_sz(uint32_t mw, int lane, int sym, float& s, float& z) {
+  if (sym) {
+    s = h2f(uint16_t((lane & 1) ? (mw >> 16) : (mw & 0xffffu)));
+    z = -float(1 << (BITS - 1)) * s;  // offset-binary codes: signed = u - 2^(b-1)
+  } else {
+    s = h2f(uint16_t(mw & 0xffffu));
+    z = h2f(uint16_t(mw >> 16));
+  }
+}
+
+// Workgroup barrier for data exchanged through LDS.  __syncthreads() would
+// also wait for every outstanding global load, i.e. for the next split's
+// prefetch; only the LDS writes need to be complete.
 __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
 }
 
-// issue the loads of one unit: codes at src (this lane's first word) and meta
-template <int W>
-__device__ __forceinline__ void stage_unit(unsigned char* unit, const uint32_t* codes, const uint16_t* meta_unit0,
-                                           int lane, int sym) {
-  using S = Stage<W>;
+// sum over aligned segments of N lanes (every lane gets its segment's sum)
+template <int N>
+__device__ __forceinline__ float seg_sum(float v) {
 #pragma unroll
-  for (int c = 0; c < S::NCHK; ++c) dma_t<S::CW * 4>(codes + c * S::CW, unit + c * 64 * S::CW * 4);
-  // asym: one {scale, zero} dword per lane; sym: 64 fp16 scales = 32 dwords,
-  // lanes 32-63 re-load them into the unused upper half of the meta block
-  const uint32_t* m32 = reinterpret_cast<const uint32_t*>(meta_unit0);
-  dma_t<4>(m32 + (sym ? (lane & 31) : lane), unit + S::META);
+  for (int o = 1; o < N; o <<= 1) v += __shfl_xor(v, o, 64);
+  return v;
 }
 
-// read back this lane's words and meta of one unit
-template <int W>
-__device__ __forceinline__ void read_unit(const unsigned char* unit, int lane, int sym, uint32_t (&w)[W],
-                                          uint32_t& meta) {
-  using S = Stage<W>;
-#pragma unroll
-  for (int c = 0; c < S::NCHK; ++c) {
-    const uint32_t* p = reinterpret_cast<const uint32_t*>(unit + (c * 64 + lane) * S::CW * 4);
-    if constexpr (S::CW == 4) {
-      const uint4 u = *reinterpret_cast<const uint4*>(p);
-      w[4 * c] = u.x; w[4 * c + 1] = u.y; w[4 * c + 2] = u.z; w[4 * c + 3] = u.w;
-    } else {
-#pragma unroll
-      for (int x = 0; x < S::CW; ++x) w[c * S::CW + x] = p[x];
-    }
-  }
-  if (sym) meta = reinterpret_cast<const uint16_t*>(unit + S::META)[lane];
-  else meta = reinterpret_cast<const uint32_t*>(unit + S::META)[lane];
-}
-
-template <int BITS, int G, int D, int NREP>
-__global__ __launch_bounds__(WG) void flash_fused_kernel(FusedArgs a) {
+template <int BITS, int G, int D, int NREP, bool QS>
+__global__ __launch_bounds__((FusedShape<G, NREP, QS>::NT), (fused_waves_per_simd<G, NREP, QS>())) void flash_fused_kernel(FusedArgs a) {
+  using FS = FusedShape<G, NREP, QS>;
+  constexpr int NW = FS::NW, NT = FS::NT, WTOK = FS::WTOK, FBPW = FS::FBPW, VPW = FS::VPW;
+  constexpr int BPS = FSPLIT / WTOK;  // wave blocks per split
   constexpr int NG = D / G;
   constexpr int W = G * BITS / 32;
   constexpr int NP = G / 2;
-  constexpr int VPW = WTOK / G;  // V groups per wave
-  constexpr int RD = rec_dwords<G, NREP>();
   constexpr int DPL = D / 64;
-  constexpr int UB = Stage<W>::UNIT;
-  constexpr float ZS = -float(1 << (BITS - 1));
-  static_assert(WTOK % G == 0, "a V group lies inside one wave's tokens");
-  __shared__ FusedSmem<BITS, G, D, NREP> sm;
+  constexpr int NPAIRS = NG * NREP * NP;  // query pairs of a split's records
+  constexpr int NPT = (NPAIRS + NT - 1) / NT;
+  constexpr int QOS = qrec_osum<G, NREP>();
+  constexpr int QNB = qrec_nbsum<G, NREP>();
+  constexpr int NQ = (NREP + 3) / 4;
+  __shared__ FusedSmem<BITS, G, D, NREP, QS> sm;
 
-  const int bh = blockIdx.y;
-  const int split = blockIdx.x;
-  const int b = bh / a.Hkv, kvh = bh % a.Hkv;
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lane = tid & 63;
   const int hl = lane & 3;
-  const int wt0 = (split * NWAVES + wave) * WTOK;  // first token of the wave's sub-split
-  unsigned char* stage = sm.stage[wave];
+  constexpr bool qsplit = QS;  // key normalization: hi/lo query rows
+  const int kms = a.ksym ? 2 : 4, vms = a.vsym ? 2 : 4;  // meta bytes per token / column
+  const uint32_t kmv = meta_voff(lane, a.ksym), vmv = meta_voff(lane, a.vsym);
+  const int64_t rows = int64_t(a.nitems / a.nsplit) * NREP;
 
-  // ---- q rows (and the norm row) into LDS, issued ahead of the K stream ----
-  // Direct LDS loads complete in order with the stage loads issued after
-  // them; a wait for "all but the K loads" then covers exactly these.
-  using SM = FusedSmem<BITS, G, D, NREP>;
-  constexpr int QLOADS = SM::QDW_PAD / 64;  // 64-dword loads over the workgroup
-  constexpr int QLPW = (QLOADS + NWAVES - 1) / NWAVES;
-  const bool qsplit = a.norm != nullptr;
-  {
-    const uint16_t* qb = a.q + b * a.sqb + int64_t(kvh * NREP) * a.sqh;
-#pragma unroll
-    for (int r = 0; r < QLPW; ++r) {
-      const int c = min(wave + NWAVES * r, QLOADS - 1);  // waves past the loads repeat the last one
-      const int i = min(c * 64 + lane, SM::QDW - 1);      // dword: head i / (D/2), pair i % (D/2)
-      const int h = i / (D / 2), dd = i % (D / 2);
-      dma_t<4>(qb + h * a.sqh + 2 * dd, &sm.qraw[c * 64]);
-    }
-    const uint16_t* nb = a.norm ? a.norm + int64_t(bh) * D : qb;  // the q row itself when unused
-    dma_t<4>(nb + 2 * min(lane, D / 2 - 1), &sm.nraw[0]);
-  }
-  // ---- every K unit of the wave into its stage region ----
-  // blocks past the range (tail waves) re-read its last block: in-bounds
-  // loads whose tokens are masked out
-  {
-    const int nblk = (a.T + TOKEN_BLOCK - 1) / TOKEN_BLOCK;
-    const int64_t kbase = int64_t(bh) * a.k_cap_blocks + a.kblk0;
-    const uint32_t* kcb = a.kc + kbase * (NG * TOKEN_BLOCK * W);
-    const uint16_t* kmb = a.km + kbase * (NG * TOKEN_BLOCK * (a.ksym ? 1 : 2));
+  struct KRegs { uint32_t w[NG][FBPW][W]; uint32_t m[NG][FBPW]; };
+  struct VRegs { uint32_t w[VPW][DPL][W]; uint32_t m[VPW][DPL]; };
+  struct QRegs { uint16_t a[NPT], c[NPT], na[NPT], nc[NPT]; };
+
+  // ---- loads of wave block blk (tokens [blk*WTOK, +WTOK) of the range) of
+  // (batch, KV head) bh into registers; real = false: zero fill ----
+  auto load_k = [&](int bh, int blk, bool real, KRegs& k) {
+    const int64_t blk0 = int64_t(bh) * a.k_cap_blocks + a.kblk0;
+    const rsrc_t rc = make_rsrc(a.kc + blk0 * (NG * TOKEN_BLOCK * W), real ? a.k_code_bytes : 0u);
+    const rsrc_t rm = make_rsrc(a.km + blk0 * (NG * TOKEN_BLOCK * (kms / 2)), real ? a.k_meta_bytes : 0u);
+    const int b0 = blk * FBPW;
 #pragma unroll
     for (int g = 0; g < NG; ++g)
 #pragma unroll
       for (int j = 0; j < FBPW; ++j) {
-        const int blk = min(wt0 / TOKEN_BLOCK + j, nblk - 1);
-        const int64_t unit0 = (int64_t(blk) * NG + g) * TOKEN_BLOCK;
-        stage_unit<W>(stage + (g * FBPW + j) * UB, kcb + (unit0 + lane) * W,
-                      kmb + unit0 * (a.ksym ? 1 : 2), lane, a.ksym);
+        const uint32_t u = uint32_t((b0 + j) * NG + g) * TOKEN_BLOCK;  // first token slot of the unit
+        bload_words<W>(rc, uint32_t(lane) * (W * 4), u * (W * 4), k.w[g][j]);
+        k.m[g][j] = bload_u32(rm, kmv, u * kms);
       }
-  }
-
-  // ---- query records (the only workgroup-wide step before the merge) ----
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(NG * FBPW * (Stage<W>::NCHK + 1)) : "memory");
-  lds_barrier();
-  {
-    const uint16_t* qh = reinterpret_cast<const uint16_t*>(sm.qraw);
-    const uint16_t* nh = reinterpret_cast<const uint16_t*>(sm.nraw);
-    for (int i = tid; i < NG * NREP * NP; i += WG) {
-      const int k = i % NP, h = (i / NP) % NREP, g = i / (NP * NREP);
-      const int ia = g * G + plan_a<BITS>(k), ic = g * G + plan_c<BITS>(k);
-      float unused = 0.f;
-      qrec_pair_vals(qh[h * D + ia], qh[h * D + ic], nh[ia], nh[ic], qsplit, &sm.qrec[g][h * NP + k],
-                     &sm.qrec[g][(NREP + h) * NP + k], unused);
-    }
-    lds_barrier();
-    if (tid < NG * NREP) {
-      const int g = tid / NREP, h = tid % NREP;
-      float s = 0.f;
-      for (int k = 0; k < NP; ++k) {
-        const uint32_t u = sm.qrec[g][h * NP + k];
-        s += h2f(uint16_t(u & 0xffffu)) + h2f(uint16_t(u >> 16));
-        if (qsplit) {
-          const uint32_t v = sm.qrec[g][(NREP + h) * NP + k];
-          s += h2f(uint16_t(v & 0xffffu)) + h2f(uint16_t(v >> 16));
-        }
-      }
-      sm.qrec[g][qrec_osum<G, NREP>() + h] = __float_as_uint(s);
-    }
-    lds_barrier();
-  }
-
-  // ---- QK^T over the wave's tokens, from the stage; V streams in behind ----
-  // Group g's K units occupy slots [g*FBPW, (g+1)*FBPW); once they are read,
-  // the V units of the same slots are loaded there (slot = V group * DPL +
-  // column set).  Every wave loads every V unit (groups past the range
-  // re-read the range's last group), so the load counts are compile-time:
-  // before group g, the outstanding loads are the K loads of groups > g plus
-  // the V loads of groups < g, NG - 1 groups' worth in all.
-  constexpr int KPG = FBPW * (Stage<W>::NCHK + 1);  // loads per group of slots
-  const int vg_last = a.T / G - 1;                  // T is a multiple of G
-  const int64_t vbase = int64_t(bh) * a.v_cap_groups + a.vg0;
-  auto stage_v = [&](int slot0) {
-#pragma unroll
-    for (int j = 0; j < FBPW; ++j) {
-      const int slot = slot0 + j, u = slot / DPL, e = slot % DPL;
-      const int64_t unit0 = (vbase + min(wt0 / G + u, vg_last)) * D + 64 * e;
-      stage_unit<W>(stage + slot * UB, a.vc + (unit0 + lane) * W, a.vm + unit0 * (a.vsym ? 1 : 2), lane, a.vsym);
-    }
   };
-  const PlanRegs<BITS> pr;
-  float acc[FBPW][NREP];
+  auto load_v = [&](int bh, int blk, bool real, VRegs& v) {
+    const int64_t g0 = int64_t(bh) * a.v_cap_groups + a.vg0;
+    const rsrc_t rc = make_rsrc(a.vc + g0 * (D * W), real ? a.v_code_bytes : 0u);
+    const rsrc_t rm = make_rsrc(a.vm + g0 * (D * (vms / 2)), real ? a.v_meta_bytes : 0u);
+    const int vgw = blk * WTOK / G;  // the block's first V group
 #pragma unroll
-  for (int j = 0; j < FBPW; ++j)
-#pragma unroll
-    for (int h = 0; h < NREP; ++h) acc[j][h] = 0.f;
-  IQ_GROUP_LOOP
-  for (int g = 0; g < NG; ++g) {
-#if IQ_FLASH_VSTREAM
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(KPG * (NG - 1)) : "memory");
-#else
-    if (g == 0) wait_vm_all();
-#endif
-    uint32_t cw[FBPW][W], cm[FBPW];
-#pragma unroll
-    for (int j = 0; j < FBPW; ++j) read_unit<W>(stage + (g * FBPW + j) * UB, lane, a.ksym, cw[j], cm[j]);
-#if IQ_FLASH_VSTREAM
-    wait_lgkm_all();
-    stage_v(g * FBPW);
-#endif
-    if (a.ksym) {
-#pragma unroll
-      for (int j = 0; j < FBPW; ++j) to_offset_binary<BITS>(cw[j], W);
-    }
-    float d[FBPW][NREP];
-    qk_group_dot<BITS, G, NREP, FBPW>(cw, &sm.qrec[g][0], hl, qsplit, pr, d);
-#pragma unroll
-    for (int j = 0; j < FBPW; ++j) {
-      const float s = h2f(uint16_t(cm[j] & 0xffffu));
-      const float z = a.ksym ? ZS * s : h2f(uint16_t(cm[j] >> 16));
-#pragma unroll
-      for (int h = 0; h < NREP; ++h) {
-        const float qs = __uint_as_float(sm.qrec[g][qrec_osum<G, NREP>() + h]);
-        acc[j][h] = fmaf(s, d[j][h], fmaf(z, qs, acc[j][h]));
-      }
-    }
-  }
-#if !IQ_FLASH_VSTREAM
-  wait_lgkm_all();
-  for (int g = 0; g < NG; ++g) stage_v(g * FBPW);
-#endif
-  const int vcnt = max(0, min(VPW, (a.T - wt0) / G));  // the wave's V groups inside the range
-
-  // ---- softmax over the wave's tokens; fp16 p straight into the V records ----
-  uint32_t (&vrec)[VPW][RD] = sm.vrec[wave];
-  float mw[NREP], lw[NREP];
-#pragma unroll
-  for (int j = 0; j < FBPW; ++j) {
-    const bool live = wt0 + j * TOKEN_BLOCK + lane < a.T;
-#pragma unroll
-    for (int h = 0; h < NREP; ++h) acc[j][h] = live ? acc[j][h] * a.scale : -INFINITY;
-  }
-#pragma unroll
-  for (int h = 0; h < NREP; ++h) {
-    mw[h] = acc[0][h];
-#pragma unroll
-    for (int j = 1; j < FBPW; ++j) mw[h] = fmaxf(mw[h], acc[j][h]);
-  }
-  wave_max_dpp(mw);
-#pragma unroll
-  for (int h = 0; h < NREP; ++h) {
-    lw[h] = 0.f;
-#pragma unroll
-    for (int j = 0; j < FBPW; ++j) {
-      const float p = acc[j][h] == -INFINITY ? 0.f : __expf(acc[j][h] - mw[h]);
-      lw[h] += p;
-      const int tl = j * TOKEN_BLOCK + lane;  // token within the wave
-      int k = 0, hi = 0;
-      plan_inv<BITS>(tl % G, k, hi);
-      reinterpret_cast<uint16_t*>(&vrec[tl / G][h * NP + k])[hi] = __half_as_ushort(__float2half_rn(p));
-    }
-  }
-  wave_sum_dpp(lw);
-  wave_lds_sync();
-  // per (V group, head): sum of the fp16 probabilities (zero-point term)
-  if (lane < VPW * NREP) {
-    const int u = lane / NREP, h = lane % NREP;
-    float s = 0.f;
-#pragma unroll
-    for (int k = 0; k < NP; k += 4) {
-      const uint4 w4 = *reinterpret_cast<const uint4*>(&vrec[u][h * NP + k]);
-      const uint32_t ww[4] = {w4.x, w4.y, w4.z, w4.w};
-#pragma unroll
-      for (int y = 0; y < 4; ++y) s += h2f(uint16_t(ww[y] & 0xffffu)) + h2f(uint16_t(ww[y] >> 16));
-    }
-    vrec[u][NP * NREP + h] = __float_as_uint(s);
-  }
-  wave_lds_sync();
-
-  // ---- attn.V over the wave's V groups, from the stage ----
-  wait_vm_all();
-  float o[NREP][DPL];
-#pragma unroll
-  for (int h = 0; h < NREP; ++h)
-#pragma unroll
-    for (int e = 0; e < DPL; ++e) o[h][e] = 0.f;
-  IQ_GROUP_LOOP
-  for (int u = 0; u < VPW; ++u) {
-    if (u >= vcnt) break;
-    uint32_t cw[DPL][W], cm[DPL];
-#pragma unroll
-    for (int e = 0; e < DPL; ++e) read_unit<W>(stage + (u * DPL + e) * UB, lane, a.vsym, cw[e], cm[e]);
-    if (a.vsym) {
-#pragma unroll
-      for (int e = 0; e < DPL; ++e) to_offset_binary<BITS>(cw[e], W);
-    }
-    f4_t dv[DPL][(NREP + 3) / 4];
-    group_mfma<BITS, G, NREP, DPL>(cw, &vrec[u][0], hl, pr, dv);
-#pragma unroll
-    for (int e = 0; e < DPL; ++e) {
-      const float s = h2f(uint16_t(cm[e] & 0xffffu));
-      const float z = a.vsym ? ZS * s : h2f(uint16_t(cm[e] >> 16));
-#pragma unroll
-      for (int h = 0; h < NREP; ++h) {
-        const float ps = __uint_as_float(vrec[u][NP * NREP + h]);
-        o[h][e] = fmaf(s, dv[e][h / 4][h % 4], fmaf(z, ps, o[h][e]));
-      }
-    }
-  }
-
-  // ---- merge the four waves ----
-  if (lane == 0) {
-#pragma unroll
-    for (int h = 0; h < NREP; ++h) {
-      sm.m[wave][h] = mw[h];
-      sm.l[wave][h] = lw[h];
-    }
-  }
-  lds_barrier();  // also: every wave is done with its stage (red aliases it)
-  float mt[NREP];
-#pragma unroll
-  for (int h = 0; h < NREP; ++h) {
-    mt[h] = fmaxf(fmaxf(sm.m[0][h], sm.m[1][h]), fmaxf(sm.m[2][h], sm.m[3][h]));
-    const float sc = mw[h] == -INFINITY ? 0.f : __expf(mw[h] - mt[h]);
-#pragma unroll
-    for (int e = 0; e < DPL; ++e) o[h][e] *= sc;
-  }
-  if (wave > 0) {
-#pragma unroll
-    for (int h = 0; h < NREP; ++h)
-#pragma unroll
-      for (int e = 0; e < DPL; ++e) sm.red[wave - 1][h][lane + 64 * e] = o[h][e];
-  }
-  lds_barrier();
-  const int64_t rows = int64_t(gridDim.y) * NREP;
-  if (wave == 0) {
-    float* dst = a.part + (int64_t(split) * rows + int64_t(bh) * NREP) * D;
-#pragma unroll
-    for (int h = 0; h < NREP; ++h)
+    for (int u = 0; u < VPW; ++u)
 #pragma unroll
       for (int e = 0; e < DPL; ++e) {
-        float v = o[h][e];
-#pragma unroll
-        for (int r = 0; r < NWAVES - 1; ++r) v += sm.red[r][h][lane + 64 * e];
-        dst[h * D + lane + 64 * e] = v;
+        const uint32_t c0 = uint32_t((vgw + u) * D + 64 * e);  // first column slot of the unit
+        bload_words<W>(rc, uint32_t(lane) * (W * 4), c0 * (W * 4), v.w[u][e]);
+        v.m[u][e] = bload_u32(rm, vmv, c0 * vms);
       }
-    if (lane < NREP) {  // split statistics of head `lane`
-      const int h = lane;
-      const float m = fmaxf(fmaxf(sm.m[0][h], sm.m[1][h]), fmaxf(sm.m[2][h], sm.m[3][h]));
-      float l = 0.f;
+  };
+  auto load_q = [&](int bh, bool real, QRegs& qq) {
+    const int b = bh / a.Hkv, kvh = bh - b * a.Hkv;
+    const rsrc_t rq = make_rsrc(a.q + b * a.sqb + int64_t(kvh * NREP) * a.sqh, real ? a.q_bytes : 0u);
+    const rsrc_t rn = make_rsrc(a.norm ? a.norm + int64_t(bh) * D : a.q, real ? a.norm_bytes : 0u);
 #pragma unroll
-      for (int w = 0; w < NWAVES; ++w) l += sm.m[w][h] == -INFINITY ? 0.f : sm.l[w][h] * __expf(sm.m[w][h] - m);
-      float* ml = a.ml + (int64_t(split) * rows + int64_t(bh) * NREP + h) * 2;
-      ml[0] = m;
-      ml[1] = l;
+    for (int r = 0; r < NPT; ++r) {
+      const int i = min(tid + r * NT, NPAIRS - 1);
+      const int k = i % NP, h = (i / NP) % NREP, g = i / (NP * NREP);
+      const int ia = g * G + plan_a<BITS>(k), ic = g * G + plan_c<BITS>(k);
+      qq.a[r] = bload_u16(rq, uint32_t(h * a.sqh + ia) * 2, 0);
+      qq.c[r] = bload_u16(rq, uint32_t(h * a.sqh + ic) * 2, 0);
+      qq.na[r] = bload_u16(rn, uint32_t(ia) * 2, 0);
+      qq.nc[r] = bload_u16(rn, uint32_t(ic) * 2, 0);
     }
+  };
+  // query records of a split from its loaded q (and norm) values; osum by
+  // shuffles inside the NP lanes of each (group, head)
+  auto build_records = [&](const QRegs& qq) {
+#pragma unroll
+    for (int r = 0; r < NPT; ++r) {
+      const int i0 = tid + r * NT;
+      const int i = min(i0, NPAIRS - 1);
+      const int k = i % NP, h = (i / NP) % NREP, g = i / (NP * NREP);
+      uint32_t hi = 0, lo = 0;
+      float s = 0.f;
+      qrec_pair_vals(qq.a[r], qq.c[r], qq.na[r], qq.nc[r], qsplit, &hi, &lo, s);
+      // -sum(x * bias) of the hi and lo rows (exact products: the biases are powers of two)
+      const float ba = bias_a<BITS>(k % Plan<BITS>::NPAIR), bc = bias_c<BITS>(k % Plan<BITS>::NPAIR);
+      float bh = -(h2f(uint16_t(hi & 0xffffu)) * ba + h2f(uint16_t(hi >> 16)) * bc);
+      float bl = -(h2f(uint16_t(lo & 0xffffu)) * ba + h2f(uint16_t(lo >> 16)) * bc);
+      s = seg_sum<NP>(s);
+      bh = seg_sum<NP>(bh);
+      bl = seg_sum<NP>(bl);
+      if (i0 < NPAIRS) {
+        sm.qrec[g][h * NP + k] = hi;
+        if (qsplit) sm.qrec[g][(NREP + h) * NP + k] = lo;
+        if (k == 0) {
+          sm.qrec[g][QOS + h] = __float_as_uint(s);
+          sm.qrec[g][QNB + h] = __float_as_uint(bh);
+          sm.qrec[g][QNB + NREP + h] = __float_as_uint(bl);
+        }
+      }
+    }
+  };
+
+  const PlanRegs<BITS> pr;
+  // ---- work: this workgroup's splits [i0, i1) of the (batch, KV head)-major
+  // split list (contiguous, equal shares: one workgroup per CU), processed as
+  // runs, the maximal pieces of one (batch, KV head).  Inside a run the waves
+  // claim wave blocks from a counter in LDS (the first two per wave are
+  // fixed), so they all finish the run within about one block of each other
+  // whatever the issue arbitration favours. ----
+  const int i0 = int(int64_t(blockIdx.x) * a.nitems / gridDim.x);
+  const int i1 = int(int64_t(blockIdx.x + 1) * a.nitems / gridDim.x);
+  if (i0 >= i1) return;  // uniform over the workgroup, before any barrier
+  struct Run {
+    int bh, split0, nsplit, nb;  // (batch, KV head), first split, splits, wave blocks
+  };
+  auto run_at = [&](int s0) {
+    Run r;
+    r.bh = s0 / a.nsplit;
+    r.split0 = s0 - r.bh * a.nsplit;
+    r.nsplit = min(i1, (r.bh + 1) * a.nsplit) - s0;
+    r.nb = r.nsplit * BPS;
+    return r;
+  };
+  // wave block (within the (batch, KV head)) of run-relative index idx
+  auto block_of = [&](const Run& r, int idx) { return r.split0 * BPS + idx; };
+
+  // running softmax state of the wave over the current run (log2 domain)
+  float m_run[NREP], l_run[NREP], o_run[NREP][DPL];
+  auto reset_run = [&]() {
+#pragma unroll
+    for (int h = 0; h < NREP; ++h) {
+      m_run[h] = -INFINITY;
+      l_run[h] = 0.f;
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) o_run[h][e] = 0.f;
+    }
+  };
+  // merge the waves' run states and write the run's partial into the slot of
+  // its first split (every wave is past its last QK^T of the run afterwards)
+  auto flush_run = [&](int bh, int split0) {
+    if (lane == 0) {
+#pragma unroll
+      for (int h = 0; h < NREP; ++h) {
+        sm.m[wave][h] = m_run[h];
+        sm.l[wave][h] = l_run[h];
+      }
+    }
+    lds_barrier();
+#pragma unroll
+    for (int h = 0; h < NREP; ++h) {
+      float mt = sm.m[0][h];
+#pragma unroll
+      for (int w = 1; w < NW; ++w) mt = fmaxf(mt, sm.m[w][h]);
+      const float sc = m_run[h] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run[h] - mt);
+#pragma unroll
+      for (int e = 0; e < DPL; ++e) sm.red[wave][h][lane + 64 * e] = o_run[h][e] * sc;
+    }
+    float mls = 0.f, lls = 0.f;  // run statistics of head tid (m in natural-log units)
+    if (tid < NREP) {
+      const int h = tid;
+      float mt = sm.m[0][h];
+#pragma unroll
+      for (int w = 1; w < NW; ++w) mt = fmaxf(mt, sm.m[w][h]);
+#pragma unroll
+      for (int w = 0; w < NW; ++w) lls += sm.m[w][h] == -INFINITY ? 0.f : sm.l[w][h] * __builtin_amdgcn_exp2f(sm.m[w][h] - mt);
+      mls = mt * 0.69314718055994531f;
+    }
+    // every read of the statistics is done: a wave that runs ahead into its
+    // next run may overwrite them after this barrier
+    lds_barrier();
+    float* dst = a.part + (int64_t(split0) * rows + int64_t(bh) * NREP) * D;
+#pragma unroll
+    for (int r = tid; r < NREP * D; r += NT) {
+      const int h = r / D, dd = r % D;
+      float val = 0.f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) val += sm.red[w][h][dd];
+      dst[r] = val;
+    }
+    if (tid < NREP) {
+      float* ml = a.ml + (int64_t(split0) * rows + int64_t(bh) * NREP + tid) * 2;
+      ml[0] = mls;
+      ml[1] = lls;
+    }
+  };
+
+  // the lane's tokens' slots in the attn.V operand records and their code biases
+  int tk[FBPW], thi[FBPW];
+  float tb[FBPW];
+#pragma unroll
+  for (int j = 0; j < FBPW; ++j) plan_inv<BITS>((j * TOKEN_BLOCK + lane) % G, tk[j], thi[j], tb[j]);
+
+  Run run = run_at(i0);
+  int rs2 = i0 + run.nsplit;                // first split of the next run (i1: none)
+  Run run2 = run_at(min(rs2, i1 - 1));
+  int cur = wave < run.nb ? wave : -1;           // the wave's current block (index in the run)
+  int nxt = NW + wave < run.nb ? NW + wave : -1;  // the block whose data it loads next
+  QRegs qq;
+  VRegs v;
+  // ---- one wave block: K in kc and V in v (loaded during the previous
+  // block); loads the next block's K into kn at the top and its V into v
+  // after attn.V; the wave's last block of a run ends in the run merge ----
+  auto step = [&](KRegs& kc, KRegs& kn) -> bool {
+    const bool have = cur >= 0;
+    const bool ends = nxt < 0;  // the wave's last block of the run
+    const bool nrun = rs2 < i1;
+    // the block loaded during this one: nxt, or the wave's first block of the next run
+    const int lbh = ends ? run2.bh : run.bh;
+    const int lblk = ends ? block_of(run2, wave) : block_of(run, max(nxt, 0));
+    const bool lreal = ends ? nrun && wave < run2.nb : true;
+    load_k(lbh, lblk, lreal, kn);  // in flight through this whole block
+    int nn = 0;
+    if (!ends && lane == 0) nn = atomicAdd(&sm.next_block, 1);
+    if (have) {
+      const int wt0 = block_of(run, cur) * WTOK;  // first token of the block
+      // ---- QK^T over the wave's tokens, from registers ----
+      float acc[FBPW][NREP];
+#pragma unroll
+      for (int j = 0; j < FBPW; ++j)
+#pragma unroll
+        for (int h = 0; h < NREP; ++h) acc[j][h] = 0.f;
+#pragma unroll
+      for (int g = 0; g < NG; ++g) {
+        if (a.ksym) {
+#pragma unroll
+          for (int j = 0; j < FBPW; ++j) to_offset_binary<BITS>(kc.w[g][j], W);
+        }
+        float d[FBPW][NREP];
+        qk_group_dot_biased<BITS, G, NREP, FBPW>(kc.w[g], &sm.qrec[g][0], hl, qsplit, pr, d);
+#pragma unroll
+        for (int j = 0; j < FBPW; ++j) {
+          float s, z;
+          meta_sz<BITS>(kc.m[g][j], lane, a.ksym, s, z);
+#pragma unroll
+          for (int h = 0; h < NREP; ++h) {
+            const float qs = __uint_as_float(sm.qrec[g][QOS + h]);
+            acc[j][h] = fmaf(s, d[j][h], fmaf(z, qs, acc[j][h]));
+          }
+        }
+      }
+
+      // ---- softmax against the running max (log2 domain); fp16 p straight
+      // into the V records ----
+      auto& vrec = sm.vrec[wave];
+      float mw[NREP], ps[VPW][NREP], alpha[NREP];
+#pragma unroll
+      for (int j = 0; j < FBPW; ++j) {
+        const bool live = wt0 + j * TOKEN_BLOCK + lane < a.T;
+#pragma unroll
+        for (int h = 0; h < NREP; ++h) acc[j][h] = live ? acc[j][h] * a.scale_log2 : -INFINITY;
+      }
+#pragma unroll
+      for (int h = 0; h < NREP; ++h) {
+        mw[h] = acc[0][h];
+#pragma unroll
+        for (int j = 1; j < FBPW; ++j) mw[h] = fmaxf(mw[h], acc[j][h]);
+      }
+      wave_max_dpp(mw);
+#pragma unroll
+      for (int h = 0; h < NREP; ++h) {
+        const float mn = fmaxf(m_run[h], mw[h]);
+        alpha[h] = m_run[h] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run[h] - mn);
+        m_run[h] = mn;
+      }
+      // x[h]: p; x[NREP + h]: -p * bias (the attn.V accumulators' seed)
+      float x[2 * NREP], pb[VPW][NREP];
+#pragma unroll
+      for (int h = 0; h < NREP; ++h) {
+        x[h] = 0.f;
+        x[NREP + h] = 0.f;
+#pragma unroll
+        for (int j = 0; j < FBPW; ++j) {
+          const float p = acc[j][h] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(acc[j][h] - m_run[h]);
+          const uint16_t p16 = __half_as_ushort(__float2half_rn(p));
+          const int tl = j * TOKEN_BLOCK + lane;  // token within the wave
+          reinterpret_cast<uint16_t*>(&vrec[tl / G][h * NP + tk[j]])[thi[j]] = p16;
+          const float pf = h2f(p16);  // the zero-point term uses the fp16 p the matrix cores see
+          x[h] += pf;
+          x[NREP + h] = fmaf(-pf, tb[j], x[NREP + h]);
+        }
+      }
+      // per (V group, head): sums over the group's tokens
+      if constexpr (G == 32) {  // two groups per wave: lanes 0-31 and 32-63
+        sum_step<0xb1>(x);
+        sum_step<0x4e>(x);
+        sum_step<0x141>(x);
+        sum_step<0x140>(x);
+#pragma unroll
+        for (int h = 0; h < 2 * NREP; ++h) {
+          x[h] += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x[h]), 0x142, 0xa,
+                                                                        0xf, false));
+          const float s0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x[h]), 31));
+          const float s1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x[h]), 63));
+          if (h < NREP) { ps[0][h] = s0; ps[1][h] = s1; }
+          else { pb[0][h - NREP] = s0; pb[1][h - NREP] = s1; }
+        }
+      } else {
+        static_assert(VPW == 1, "one V group per wave for G >= 64");
+        wave_sum_dpp(x);
+#pragma unroll
+        for (int h = 0; h < NREP; ++h) {
+          ps[0][h] = x[h];
+          pb[0][h] = x[NREP + h];
+        }
+      }
+#pragma unroll
+      for (int h = 0; h < NREP; ++h) {
+        float lsum = 0.f;
+#pragma unroll
+        for (int u = 0; u < VPW; ++u) lsum += ps[u][h];
+        l_run[h] = fmaf(l_run[h], alpha[h], lsum);
+#pragma unroll
+        for (int e = 0; e < DPL; ++e) o_run[h][e] *= alpha[h];
+      }
+      wave_lds_sync();
+
+      // ---- attn.V over the wave's V groups, from registers ----
+      const int vcnt = max(0, min(VPW, (a.T - wt0) / G));  // the wave's V groups inside the range
+#pragma unroll
+      for (int u = 0; u < VPW; ++u) {
+        if (u < vcnt) {
+          if (a.vsym) {
+#pragma unroll
+            for (int e = 0; e < DPL; ++e) to_offset_binary<BITS>(v.w[u][e], W);
+          }
+          f4_t init[NQ], dv[DPL][NQ];
+#pragma unroll
+          for (int q = 0; q < NQ; ++q)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) init[q][i] = 4 * q + i < NREP ? pb[u][4 * q + i] : 0.f;
+          group_mfma_biased<BITS, G, NREP, DPL>(v.w[u], &vrec[u][0], hl, pr, init, dv);
+#pragma unroll
+          for (int e = 0; e < DPL; ++e) {
+            float s, z;
+            meta_sz<BITS>(v.m[u][e], lane, a.vsym, s, z);
+#pragma unroll
+            for (int h = 0; h < NREP; ++h)
+              o_run[h][e] = fmaf(s, dv[e][h / 4][h % 4], fmaf(z, ps[u][h], o_run[h][e]));
+          }
+        }
+      }
+    }
+    load_v(lbh, lblk, lreal, v);  // streams in during the next block's QK^T
+    if (!ends) {
+      nn = __builtin_amdgcn_readlane(nn, 0);
+      cur = nxt;
+      nxt = nn < run.nb ? nn : -1;
+      return true;
+    }
+    // ---- run end: merge the waves; empty statistics in the run's other
+    // split slots (the combine skips them) ----
+    flush_run(run.bh, run.split0);
+    if (wave == 0 && lane < NREP) {
+      for (int sp = run.split0 + 1; sp < run.split0 + run.nsplit; ++sp) {
+        float* ml = a.ml + (int64_t(sp) * rows + int64_t(run.bh) * NREP + lane) * 2;
+        ml[0] = -INFINITY;
+        ml[1] = 0.f;
+      }
+    }
+    if (!nrun) return false;
+    reset_run();
+    run = run2;
+    rs2 += run.nsplit;
+    run2 = run_at(min(rs2, i1 - 1));
+    build_records(qq);  // the new (batch, KV head)'s query records
+    if (tid == 0) sm.next_block = 2 * NW;
+    lds_barrier();
+    load_q(run2.bh, rs2 < i1, qq);  // the run after: in flight through this one
+    cur = wave < run.nb ? wave : -1;
+    nxt = NW + wave < run.nb ? NW + wave : -1;
+    return true;
+  };
+
+  KRegs ka, kb;
+  reset_run();
+  load_k(run.bh, block_of(run, max(cur, 0)), cur >= 0, ka);
+  load_v(run.bh, block_of(run, max(cur, 0)), cur >= 0, v);
+  load_q(run.bh, true, qq);
+  build_records(qq);
+  if (tid == 0) sm.next_block = 2 * NW;
+  lds_barrier();
+  load_q(run2.bh, rs2 < i1, qq);
+  while (step(ka, kb) && step(kb, ka)) {
   }
 }
 
@@ -511,9 +588,16 @@ __global__ __launch_bounds__(WG) void flash_fused_kernel(FusedArgs a) {
 
 namespace iq::detail {
 
-// q rows (and the norm row) are read as fp16 pairs: 4-byte aligned rows
-bool flash_fused_supported(const void* q, int64_t sq_b, int64_t sq_h, const void* norm) {
-  return aligned(q, 4) && sq_b % 2 == 0 && sq_h % 2 == 0 && (!norm || aligned(norm, 4));
+// the buffer offsets of a split are 32-bit: every (batch, KV head) slice of
+// the stores and the q rows of one KV head must stay below 2 GiB
+bool flash_fused_supported(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, const FusedStore& k,
+                           const FusedStore& v, int Hq, int Hkv, int D) {
+  (void)q; (void)sq_b; (void)norm;
+  const int64_t lim = int64_t(1) << 31;
+  const int nrep = Hkv > 0 ? Hq / Hkv : 1;
+  return sq_h >= 0 && (int64_t(nrep - 1) * sq_h + D) * 2 < lim && k.t_cap * D * k.bits / 8 < lim &&
+         k.t_cap * D * 4 / std::max(k.group, 1) < lim && v.t_cap * D * v.bits / 8 < lim &&
+         v.t_cap * D * 4 / std::max(v.group, 1) < lim;
 }
 
 int flash_fused_launch(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, const FusedStore& k,
@@ -523,17 +607,39 @@ int flash_fused_launch(const void* q, int64_t sq_b, int64_t sq_h, const void* no
   if (k.bits != v.bits || k.group != v.group) return IQ_ERR_GROUP;
   if (T % k.group || FSPLIT != flash_split_tokens()) return IQ_ERR_GROUP;
   if (k.t0 % TOKEN_BLOCK || v.t0 % v.group) return IQ_ERR_ALIGN;
-  if (!flash_fused_supported(q, sq_b, sq_h, norm)) return IQ_ERR_ALIGN;
+  if (!flash_fused_supported(q, sq_b, sq_h, norm, k, v, Hq, Hkv, D)) return IQ_ERR_SHAPE;
   FusedArgs a{};
   a.q = (const uint16_t*)q; a.sqb = sq_b; a.sqh = sq_h; a.norm = (const uint16_t*)norm;
   a.kc = k.codes; a.km = k.meta; a.k_cap_blocks = k.t_cap / TOKEN_BLOCK; a.kblk0 = k.t0 / TOKEN_BLOCK;
   a.ksym = k.mode == IQ_MODE_SYM;
   a.vc = v.codes; a.vm = v.meta; a.v_cap_groups = v.t_cap / v.group; a.vg0 = v.t0 / v.group;
   a.vsym = v.mode == IQ_MODE_SYM;
-  a.Hkv = Hkv; a.T = T; a.scale = scale; a.ml = ml; a.part = part;
-  const int nsplit = int(ceil_div(T, FSPLIT));
+  a.Hkv = Hkv; a.T = T;
+  a.nsplit = int(ceil_div(T, FSPLIT));
+  a.nitems = a.nsplit * B * Hkv;
+  const int64_t nblk = ceil_div(T, TOKEN_BLOCK);
+  a.k_code_bytes = uint32_t(nblk * TOKEN_BLOCK * D * k.bits / 8);
+  a.k_meta_bytes = uint32_t(nblk * TOKEN_BLOCK * (D / k.group) * (a.ksym ? 2 : 4));
+  a.v_code_bytes = uint32_t(int64_t(T) * D * v.bits / 8);
+  a.v_meta_bytes = uint32_t(int64_t(T / v.group) * D * (a.vsym ? 2 : 4));
+  a.q_bytes = uint32_t((int64_t(Hq / Hkv - 1) * sq_h + D) * 2);
+  a.norm_bytes = norm ? uint32_t(D * 2) : 0u;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  a.ml = ml; a.part = part;
   return dispatch_shape(k.bits, k.group, D, Hq / Hkv, 0, [&]<int BITS, int G, int DD, int R, bool S>() {
-    flash_fused_kernel<BITS, G, DD, R><<<dim3(nsplit, B * Hkv), WG, 0, stream>>>(a);
+    auto* kern = norm ? flash_fused_kernel<BITS, G, DD, R, true> : flash_fused_kernel<BITS, G, DD, R, false>;
+    const int nt = norm ? FusedShape<G, R, true>::NT : FusedShape<G, R, false>::NT;
+    // persistent grid: one workgroup per CU (as many as fit at once)
+    static int per_cu[2] = {0, 0};
+    int& pc = per_cu[norm ? 1 : 0];
+    if (pc == 0) {
+      int n = 0;
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, nt, 0) != hipSuccess || n <= 0) n = 1;
+      pc = n;
+    }
+    const int per_cu_n = pc;
+    const int grid = int(std::min<int64_t>(a.nitems, int64_t(per_cu_n) * num_cus()));
+    kern<<<dim3(grid), nt, 0, stream>>>(a);
     return launch_status();
   });
 }

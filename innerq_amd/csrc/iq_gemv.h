@@ -20,11 +20,11 @@
 // heads over four codes: 8 instructions cover a 32-code group, and the VALU
 // only unpacks codes and applies scale and zero point.
 //
-// The B operand is the code pair itself, not the biased magic-number pair:
-// with a bias of up to 1024 per code, partial sums reach ~1e4 and cancel back
-// to ~1, and the MFMA's fp32 accumulation loses ~1e-3 of the result at
-// G = 128.  Subtracting the bias pair first (one v_pk_add_f16, exact because
-// both operands are integers below 2048) keeps every partial sum small.
+// The B operand is either the code pair itself (unfused kernels: the bias
+// pair is subtracted with one v_pk_add_f16) or the biased magic-number pair
+// (fused kernel: each accumulation starts from -sum(opnd * bias) instead of
+// 0, taken from the operand record).  The pair plans keep the biases within
+// 2^8 code units (iq_device.h), so the fp32 partial sums stay small.
 #pragma once
 
 #include <utility>
@@ -35,7 +35,7 @@
 // 64-token K blocks per wave in a flash-decoding split (split = 4 waves x
 // this x 64 tokens) and code pairs unpacked per matrix-core chunk.
 #ifndef IQ_FLASH_BPW
-#define IQ_FLASH_BPW 2
+#define IQ_FLASH_BPW 1
 #endif
 #ifndef IQ_MFMA_CH
 #define IQ_MFMA_CH 8
@@ -137,7 +137,7 @@ __device__ __forceinline__ h4_t cat_h2(h2_t lo, h2_t hi) { return __builtin_shuf
 
 // Pairs [K0, K0+CH) of one group: A rows from the record (head 4q + hl; heads
 // past NREP read as zero), B from the NB code-word sets.
-template <int BITS, int W, int NREP, int NB, int K0, typename P, int... K>
+template <int BITS, int W, int NREP, int NB, int K0, bool BIASED, typename P, int... K>
 __device__ __forceinline__ void mfma_chunk(const uint32_t (&w)[NB][W], P rec, int NP, int hl,
                                            const PlanRegs<BITS>& pr, f4_t (&dv)[NB][(NREP + 3) / 4],
                                            std::integer_sequence<int, K...>) {
@@ -161,7 +161,10 @@ __device__ __forceinline__ void mfma_chunk(const uint32_t (&w)[NB][W], P rec, in
   (
       [&] {
 #pragma unroll
-        for (int j = 0; j < NB; ++j) x[j][K] = extract_codes<BITS, (K0 + K) % NPS>(&w[j][((K0 + K) / NPS) * SBW], pr);
+        for (int j = 0; j < NB; ++j) {
+          if constexpr (BIASED) x[j][K] = extract_pair<BITS, (K0 + K) % NPS>(&w[j][((K0 + K) / NPS) * SBW], pr);
+          else x[j][K] = extract_codes<BITS, (K0 + K) % NPS>(&w[j][((K0 + K) / NPS) * SBW], pr);
+        }
       }(),
       ...);
 #pragma unroll
@@ -175,14 +178,14 @@ __device__ __forceinline__ void mfma_chunk(const uint32_t (&w)[NB][W], P rec, in
   }
 }
 
-template <int BITS, int G, int NREP, int NB, int C, int NCH, typename P>
+template <int BITS, int G, int NREP, int NB, int C, int NCH, bool BIASED, typename P>
 __device__ __forceinline__ void mfma_chunks(const uint32_t (&w)[NB][G * BITS / 32], P rec, int hl,
                                             const PlanRegs<BITS>& pr, f4_t (&dv)[NB][(NREP + 3) / 4]) {
   if constexpr (C < NCH) {
     constexpr int CH = (G / 2) / NCH;
-    mfma_chunk<BITS, G * BITS / 32, NREP, NB, C * CH>(w, rec, G / 2, hl, pr, dv,
-                                                      std::make_integer_sequence<int, CH>{});
-    mfma_chunks<BITS, G, NREP, NB, C + 1, NCH>(w, rec, hl, pr, dv);
+    mfma_chunk<BITS, G * BITS / 32, NREP, NB, C * CH, BIASED>(w, rec, G / 2, hl, pr, dv,
+                                                              std::make_integer_sequence<int, CH>{});
+    mfma_chunks<BITS, G, NREP, NB, C + 1, NCH, BIASED>(w, rec, hl, pr, dv);
   }
 }
 
@@ -192,17 +195,25 @@ __device__ __forceinline__ void mfma_chunks(const uint32_t (&w)[NB][G * BITS / 3
 //                           rows n_rep + h: the low parts lo = fp16(q*n - hi)
 //                           (key normalization only)
 //     osum  [n_rep]  f32    sum_i q_i (times n_i)
+//     nbsum [2*n_rep] f32   -sum_i x[i] * bias(i) of every row (hi and lo),
+//                           16-byte aligned: the initial accumulators of the
+//                           fused kernel's biased matrix-core products (built
+//                           by the fused kernel only)
 // q*n is exact in fp32 and hi + lo holds it to 2^-22, so folding the key
 // normalization into the query costs no precision (rounding q*n to one fp16
 // moves the logits by ~1e-4 relative, which exp() turns into ~1e-3 of the
 // attention output).
 template <int G, int NREP>
-__host__ __device__ constexpr int qrec_dwords() {
-  return (NREP * (G + 1) + 3) & ~3;
-}
-template <int G, int NREP>
 __host__ __device__ constexpr int qrec_osum() {
   return NREP * G;
+}
+template <int G, int NREP>
+__host__ __device__ constexpr int qrec_nbsum() {
+  return (NREP * G + NREP + 3) & ~3;
+}
+template <int G, int NREP>
+__host__ __device__ constexpr int qrec_dwords() {
+  return (qrec_nbsum<G, NREP>() + 2 * NREP + 3) & ~3;
 }
 
 // pair (ia, ic) of query row qrow (and norm row nrow, or null): writes the hi
@@ -241,7 +252,23 @@ __device__ __forceinline__ void group_mfma(const uint32_t (&w)[NB][G * BITS / 32
   for (int j = 0; j < NB; ++j)
 #pragma unroll
     for (int q = 0; q < (NREP + 3) / 4; ++q) dv[j][q] = f4_t{0.f, 0.f, 0.f, 0.f};
-  mfma_chunks<BITS, G, NREP, NB, 0, NCH>(w, rec, hl, pr, dv);
+  mfma_chunks<BITS, G, NREP, NB, 0, NCH, false>(w, rec, hl, pr, dv);
+}
+
+// The same over biased code pairs: dv[j][q] starts at init[q] (rows 4q..4q+3:
+// -sum(opnd * bias) of the record's rows), which removes the biases exactly
+// in the accumulation.
+template <int BITS, int G, int NREP, int NB, typename P>
+__device__ __forceinline__ void group_mfma_biased(const uint32_t (&w)[NB][G * BITS / 32], P rec, int hl,
+                                                  const PlanRegs<BITS>& pr, const f4_t (&init)[(NREP + 3) / 4],
+                                                  f4_t (&dv)[NB][(NREP + 3) / 4]) {
+  constexpr int NP = G / 2;
+  constexpr int NCH = NP <= IQ_MFMA_CH ? 1 : NP / IQ_MFMA_CH;
+#pragma unroll
+  for (int j = 0; j < NB; ++j)
+#pragma unroll
+    for (int q = 0; q < (NREP + 3) / 4; ++q) dv[j][q] = init[q];
+  mfma_chunks<BITS, G, NREP, NB, 0, NCH, true>(w, rec, hl, pr, dv);
 }
 
 // Query dot products of NB code sets: d[j][h] = sum_i q'[h,i] c_j[i] over the
@@ -259,6 +286,35 @@ __device__ __forceinline__ void qk_group_dot(const uint32_t (&w)[NB][G * BITS / 
   } else {
     f4_t dv[NB][(NREP + 3) / 4];
     group_mfma<BITS, G, NREP, NB>(w, rec, hl, pr, dv);
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+      for (int h = 0; h < NREP; ++h) d[j][h] = dv[j][h / 4][h % 4];
+  }
+}
+
+// qk_group_dot over biased code pairs; rec is a query record in LDS (its
+// nbsum rows seed the accumulators)
+template <int BITS, int G, int NREP, int NB>
+__device__ __forceinline__ void qk_group_dot_biased(const uint32_t (&w)[NB][G * BITS / 32], const uint32_t* rec, int hl,
+                                                    bool split, const PlanRegs<BITS>& pr, float (&d)[NB][NREP]) {
+  const f4_t* nb = reinterpret_cast<const f4_t*>(rec + qrec_nbsum<G, NREP>());
+  if (split) {
+    constexpr int NQ = (2 * NREP + 3) / 4;
+    f4_t init[NQ], dv[NB][NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) init[q] = nb[q];
+    group_mfma_biased<BITS, G, 2 * NREP, NB>(w, rec, hl, pr, init, dv);
+#pragma unroll
+    for (int j = 0; j < NB; ++j)
+#pragma unroll
+      for (int h = 0; h < NREP; ++h) d[j][h] = dv[j][h / 4][h % 4] + dv[j][(NREP + h) / 4][(NREP + h) % 4];
+  } else {
+    constexpr int NQ = (NREP + 3) / 4;
+    f4_t init[NQ], dv[NB][NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) init[q] = nb[q];
+    group_mfma_biased<BITS, G, NREP, NB>(w, rec, hl, pr, init, dv);
 #pragma unroll
     for (int j = 0; j < NB; ++j)
 #pragma unroll
@@ -313,7 +369,9 @@ struct FusedStore {
   int t0;  // first store token of the range
   int bits, group, mode;
 };
-bool flash_fused_supported(const void* q, int64_t sq_b, int64_t sq_h, const void* norm);
+// the fused kernel reads each (batch, KV head) slice through 32-bit buffer offsets
+bool flash_fused_supported(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, const FusedStore& k,
+                           const FusedStore& v, int Hq, int Hkv, int D);
 int flash_fused_launch(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, const FusedStore& k,
                        const FusedStore& v, int B, int Hq, int Hkv, int T, int D, float scale, float* ml,
                        float* part, hipStream_t stream);

@@ -271,10 +271,11 @@ int flash_split_tokens() { return SPLIT; }
 
 size_t qk_record_bytes(int B, int Hq, int D) {
   // largest record set over the supported groups: D/G records per n_rep query
-  // heads, at most G + 1 dwords per head and 3 of padding per record
+  // heads, at most G + 3 dwords per head (pairs, osum, nbsum) and 9 of
+  // alignment padding per record
   size_t best = 0;
   for (int g : {32, 64, 128})
-    if (D % g == 0) best = std::max(best, size_t(B) * Hq * (D / g) * size_t(g + 4) * 4);
+    if (D % g == 0) best = std::max(best, size_t(B) * Hq * (D / g) * size_t(g + 12) * 4);
   return (best + 255) & ~size_t(255);
 }
 

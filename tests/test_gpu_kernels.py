@@ -433,6 +433,6 @@ def test_decode_stages_equal_decode_attention(fused):
     q = f16t(synth.normal((B, Hkv * nrep, D), seed=63).astype(np.float16))
     ref = ops.decode_attention(q, None, kst, kr, None, vst, vr, D ** -0.5).cpu().numpy()
     ns = ops.decode_attention_splits(q, None, kst, kr, None, vst, vr, D ** -0.5)
-    assert ns == 2 + 1  # two 512-token splits of the packed range + the dense tail
+    assert ns == 3 + 1  # three 256-token splits of the packed range + the dense tail
     got = ops.decode_attention_combine(ns, B, Hkv * nrep, T, D, DEV).cpu().numpy()
     np.testing.assert_array_equal(got.view(np.uint16), ref.view(np.uint16))
