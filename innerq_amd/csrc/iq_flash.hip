@@ -1,38 +1,42 @@
-// Fused flash-decoding split kernel (gfx950): QK^T, softmax and attn.V of one
-// (batch, KV head) over a split of FSPLIT consecutive tokens, for K and V
-// stores that share bit width and group size.  The combine kernel
-// (iq_decode.hip) merges the splits' partial outputs.
+// Fused flash-decoding kernel (gfx950): QK^T, softmax and attn.V over the
+// packed range of every (batch, KV head), for K and V stores that share bit
+// width and group size.  Its output is one partial (m, l, unnormalized o) per
+// run in the split slots of the decode workspace; the combine kernel
+// (iq_decode.hip) merges the slots.
 //
-// Persistent and software pipelined.  The grid holds as many workgroups as fit
-// on the device; workgroup w processes splits w, w + grid, ...  A wave owns
-// WTOK consecutive tokens of the split (lane = token for QK^T) and streams its
-// packed data straight into VGPRs with raw buffer loads.  At the top of each
-// split it issues, oldest first:
-//   V codes and {scale, zero} of its tokens (lane = head_dim column),
-//   K codes and {scale, zero} of the NEXT split (kept in flight across the
-//   whole split), and the q (and key-norm) values of the next split's records;
-// then runs, on data loaded one split earlier:
+// Persistent and software pipelined.  One workgroup per CU (as many waves as
+// the register allocation allows per SIMD) takes an equal contiguous share of
+// the (batch, KV head)-major list of FSPLIT-token splits and processes it as
+// runs, the maximal pieces of one (batch, KV head).  Inside a run the waves
+// claim wave blocks of WTOK tokens (lane = token for QK^T) from a counter in
+// LDS, so they finish the run together, and each wave keeps a running
+// softmax state (m, l, o) over its blocks.  A wave streams its packed data
+// straight into VGPRs with raw buffer loads:
+//   at the top of a block: K codes and {scale, zero} of its NEXT block (kept
+//          in flight through the whole block);
+//   after attn.V: V codes and {scale, zero} of the next block (lane = head_dim
+//          column);
+// and computes on data loaded one block earlier:
 //   QK^T   per head_dim group eight v_mfma_f32_4x4x4f16 per 32 codes and four
-//          query heads (iq_gemv.h), A = query records in LDS;
-//   softmax  max per head over the wave (DPP), p = exp2(logit*scale*log2e -
-//          m); each lane writes its fp16 p straight into its slot of the
-//          wave's attn.V operand records (the inverse of the unpack plan); the
-//          per-V-group sums of p (zero-point term, and the wave's l) by DPP;
-//   attn.V lane = column d = lane + 64 e over the wave's V groups;
-//   merge  m = max over the waves, outputs rescaled by exp2(m_w - m) and
-//          summed in LDS; the split's (m, l) and unnormalized output go to the
-//          split statistics and partials;
-//   records  the next split's query records from the prefetched q values (a
-//          key normalization, which the reference applies to the dequantized
-//          keys, cache.py:128-133 and 249, is folded into q as hi/lo fp16
-//          parts of q*n).
-// The memory system always has the next split's K of every resident wave in
-// flight, so load latency overlaps the arithmetic of the current split instead
-// of opening each workgroup's life.
+//          query heads (iq_gemv.h): B = biased code pairs, A = the run's query
+//          records in LDS, accumulators seeded with -sum(q * bias);
+//   softmax  against the wave's running max (log2 domain, DPP reductions);
+//          each lane writes its fp16 p straight into its slot of the wave's
+//          attn.V operand record (the inverse of the unpack plan); the
+//          per-V-group sums of p (zero-point term, l) and of -p * bias (seed
+//          of attn.V) by DPP;
+//   attn.V lane = column d = lane + 64 e over the block's V groups.
+// At the end of a run the waves merge (rescale by exp2(m_w - m), sum in LDS)
+// and write the run's partial into the slot of its first split; its other
+// split slots get empty statistics.  The next run's query records come from
+// q values prefetched during the run (a key normalization, which the
+// reference applies to the dequantized keys, cache.py:128-133 and 249, is
+// folded into q as hi/lo fp16 parts of q*n).
 //
 // The store formats follow the unfused kernels: K codes [B,H,t_cap/64,D/G,64,W],
 // V codes [B,H,t_cap/G,D,W]; sym or asym per store is a runtime flag (a
-// uniform branch), so the kernel is instantiated per (bits, G, D, n_rep) only.
+// uniform branch), so the kernel is instantiated per (bits, G, D, n_rep,
+// hi/lo query rows) only.
 #include <algorithm>
 
 #include "iq_gemv.h"
@@ -129,12 +133,11 @@ struct FusedSmem {
 };
 
 // ---- raw buffer loads -------------------------------------------------------
-// Each split reads its (batch, KV head) slice of a store through a buffer
+// A block reads its (batch, KV head) slice of a store through a buffer
 // resource: a byte offset per lane (VGPR) plus a uniform offset (SGPR).  A
 // resource with zero records turns every load into a zero fill that moves no
-// data; the prefetch of "the next split" after a workgroup's last one uses
-// that, so every iteration issues the same loads and the compiler's memory
-// counter waits stay exact.
+// data; the prefetch past a wave's last block uses that, so every iteration
+// issues the same loads and the compiler's memory counter waits stay exact.
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, int(bytes), 0x00020000);
