@@ -147,96 +147,94 @@ __global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs a) {
 }
 
 // out[bq, d] = sum_s e^{m_s - M} o_s[bq, d] / sum_s e^{m_s - M} l_s
-// One workgroup per row bq.  The splits with a nonzero weight are listed in
-// LDS in split order (a split slot with m = -inf carries no tokens: the fused
-// kernel leaves such slots' partials unwritten, so they must not be read);
-// then thread t takes column quad t % (D/4) and every NSL-th listed split
-// starting at t / (D/4), with all of its 16-byte partial loads independent (in
-// flight together), and the NSL slices are summed in LDS in slice order.
-constexpr int MAXSPLIT = 1024;
-__global__ __launch_bounds__(256) void flash_combine_kernel(const float* __restrict__ ml, const float* __restrict__ part,
-                                                            int nsplit, int64_t rows, int Hq, int D,
-                                                            uint16_t* __restrict__ out, int64_t sob, int64_t soh) {
-  __shared__ float wgt[MAXSPLIT];
-  __shared__ int sidx[MAXSPLIT];
-  __shared__ float4 red[256];
-  __shared__ float rs[4];
-  __shared__ int cnt[4];
+// One wave per row bq, lane = head_dim columns DPL*lane .. DPL*lane+DPL-1.  A
+// split slot with m = -inf carries no tokens and its partial may be unwritten:
+// it is never used.  The fused kernel puts the partials of a (batch, KV head)
+// into its first split slots and the dense tokens take the last one, so one
+// round of loads - every slot's (m, l) and, unconditionally, the partials of
+// the first CSPEC slots and of the last - finds the usual layout whole; a slot
+// is used only if its weight is nonzero (a select: an unwritten partial cannot
+// reach the sum).  Nonempty slots outside that set (the unfused path writes
+// every slot) are listed in LDS and read in a second round, CSPEC loads in
+// flight at a time.
+constexpr int MAXSPLIT = 1024;  // split slots of one step, at most
+constexpr int CSPEC = 8;
+template <int DPL, int E>
+__global__ __launch_bounds__(64) void flash_combine_kernel(const float* __restrict__ ml, const float* __restrict__ part,
+                                                           int nsplit, int64_t rows, int Hq,
+                                                           uint16_t* __restrict__ out, int64_t sob, int64_t soh) {
+  using Vec = float __attribute__((ext_vector_type(DPL)));
+  constexpr int D = 64 * DPL;
+  __shared__ int sidx[64 * E];
+  __shared__ float swgt[64 * E];
   const int64_t bq = blockIdx.x;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  float mx = -INFINITY;
-  for (int s = tid; s < nsplit; s += 256) mx = fmaxf(mx, ml[(int64_t(s) * rows + bq) * 2]);
-  mx = wave_max(mx);
-  if (lane == 0) rs[wave] = mx;
-  __syncthreads();
-  const float M = fmaxf(fmaxf(rs[0], rs[1]), fmaxf(rs[2], rs[3]));
-  __syncthreads();
-  float L = 0.f;
-  int nnz = 0;
-  for (int s0 = 0; s0 < nsplit; s0 += 256) {
-    const int s = s0 + tid;
-    float w = 0.f;
-    if (s < nsplit) {
-      const float ms = ml[(int64_t(s) * rows + bq) * 2];
-      w = ms == -INFINITY ? 0.f : __expf(ms - M);
-      if (w != 0.f) L = fmaf(w, ml[(int64_t(s) * rows + bq) * 2 + 1], L);
-    }
-    const unsigned long long bal = __ballot(w != 0.f);
-    if (lane == 0) cnt[wave] = __popcll(bal);
-    __syncthreads();
-    int off = nnz;
-    for (int x = 0; x < wave; ++x) off += cnt[x];
-    if (w != 0.f) {
-      const int k = off + __popcll(bal & ((1ull << lane) - 1ull));
-      sidx[k] = s;
-      wgt[k] = w;
-    }
-    nnz += (cnt[0] + cnt[1]) + (cnt[2] + cnt[3]);
-    __syncthreads();
+  const int lane = threadIdx.x;
+  const float2* st = reinterpret_cast<const float2*>(ml) + bq;       // slot s: st[s * rows]
+  const Vec* pr = reinterpret_cast<const Vec*>(part + bq * D) + lane;  // slot s: pr[s * rows * 64]
+  const int64_t pstride = rows * 64;
+  const int last = nsplit - 1;
+  // ---- one round: statistics of every slot, partials of the likely ones
+  // (indices clamped to the last slot, so that every load is issued
+  // unconditionally and all are in flight together) ----
+  float2 sl[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) sl[e] = st[int64_t(min(e * 64 + lane, last)) * rows];
+  Vec pv[CSPEC + 1];
+#pragma unroll
+  for (int j = 0; j < CSPEC; ++j) pv[j] = pr[int64_t(min(j, last)) * pstride];
+  pv[CSPEC] = pr[int64_t(last) * pstride];
+  const float m_last = st[int64_t(last) * rows].x;
+  const bool last_apart = last >= CSPEC;
+#pragma unroll
+  for (int e = 0; e < E; ++e)
+    if (e * 64 + lane > last) sl[e] = make_float2(-INFINITY, 0.f);
+  float M = -INFINITY;
+#pragma unroll
+  for (int e = 0; e < E; ++e) M = fmaxf(M, sl[e].x);
+  M = wave_max(M);
+  float L = 0.f, w[E];
+#pragma unroll
+  for (int e = 0; e < E; ++e) {
+    w[e] = sl[e].x == -INFINITY ? 0.f : __expf(sl[e].x - M);
+    L = fmaf(w[e], sl[e].y, L);
   }
   L = wave_sum(L);
-  if (lane == 0) rs[wave] = L;
-  __syncthreads();
-  L = (rs[0] + rs[1]) + (rs[2] + rs[3]);
-  const int nq = D / 4;           // column quads
-  const int nsl = 256 / nq;       // split slices (8 at D = 128, 16 at D = 64)
-  const int cq = tid % nq, sl = tid / nq;
-  const float4* pc = reinterpret_cast<const float4*>(part + bq * D) + cq;
-  const int64_t sstride = rows * D / 4;  // float4 per split
-  float4 acc = {0.f, 0.f, 0.f, 0.f};
-  constexpr int U = 8;
-  int k = sl;
-  for (; k + (U - 1) * nsl < nnz; k += U * nsl) {
-    float4 v[U];
+  Vec acc = 0.f;
 #pragma unroll
-    for (int u = 0; u < U; ++u) v[u] = pc[int64_t(sidx[k + u * nsl]) * sstride];
+  for (int j = 0; j < CSPEC; ++j) {
+    const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w[0]), j));  // slot j: lane j
+    if (wj != 0.f) acc += wj * pv[j];
+  }
+  if (last_apart && m_last != -INFINITY) acc += __expf(m_last - M) * pv[CSPEC];
+  // ---- the rest: nonempty slots in [CSPEC, last) ----
+  int n = 0;
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const float w = wgt[k + u * nsl];
-      acc.x = fmaf(w, v[u].x, acc.x); acc.y = fmaf(w, v[u].y, acc.y);
-      acc.z = fmaf(w, v[u].z, acc.z); acc.w = fmaf(w, v[u].w, acc.w);
+  for (int e = 0; e < E; ++e) {
+    if (e * 64 >= nsplit) break;
+    const int s = e * 64 + lane;
+    const bool take = w[e] != 0.f && s >= CSPEC && s < last;
+    const unsigned long long bal = __ballot(take);
+    if (take) {
+      const int k = n + __popcll(bal & ((1ull << lane) - 1ull));
+      sidx[k] = s;
+      swgt[k] = w[e];
+    }
+    n += __popcll(bal);
+  }
+  if (n) {
+    __syncthreads();
+    for (int k0 = 0; k0 < n; k0 += CSPEC) {
+      Vec v[CSPEC];
+#pragma unroll
+      for (int u = 0; u < CSPEC; ++u) v[u] = pr[int64_t(sidx[min(k0 + u, n - 1)]) * pstride];
+#pragma unroll
+      for (int u = 0; u < CSPEC; ++u)
+        if (k0 + u < n) acc += swgt[k0 + u] * v[u];
     }
   }
-  for (; k < nnz; k += nsl) {
-    const float4 v = pc[int64_t(sidx[k]) * sstride];
-    const float w = wgt[k];
-    acc.x = fmaf(w, v.x, acc.x); acc.y = fmaf(w, v.y, acc.y);
-    acc.z = fmaf(w, v.z, acc.z); acc.w = fmaf(w, v.w, acc.w);
-  }
-  red[tid] = acc;
-  __syncthreads();
-  if (tid < nq) {
-    float4 t = red[tid];
-    for (int r = 1; r < nsl; ++r) {
-      const float4 u = red[r * nq + tid];
-      t.x += u.x; t.y += u.y; t.z += u.z; t.w += u.w;
-    }
-    uint16_t* o = out + (bq / Hq) * sob + (bq % Hq) * soh + 4 * tid;
-    o[0] = __half_as_ushort(__float2half_rn(t.x / L));
-    o[1] = __half_as_ushort(__float2half_rn(t.y / L));
-    o[2] = __half_as_ushort(__float2half_rn(t.z / L));
-    o[3] = __half_as_ushort(__float2half_rn(t.w / L));
-  }
+  uint16_t* o = out + (bq / Hq) * sob + (bq % Hq) * soh + DPL * lane;
+#pragma unroll
+  for (int i = 0; i < DPL; ++i) o[i] = __half_as_ushort(__float2half_rn(acc[i] / L));
 }
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
@@ -386,8 +384,21 @@ int launch_splits(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, c
 int launch_combine(const Workspace& w, int nsplit, int B, int Hq, int D, void* out, int64_t so_b, int64_t so_h,
                    hipStream_t st) {
   const int64_t rows = int64_t(B) * Hq;
-  flash_combine_kernel<<<dim3(unsigned(rows)), 256, 0, st>>>(w.ml, w.part, nsplit, rows, Hq, D, (uint16_t*)out,
-                                                              so_b, so_h);
+  // statistics registers per lane: the smallest power of two with 64 E >= nsplit
+  auto go = [&]<int DPL, int E>() {
+    flash_combine_kernel<DPL, E><<<dim3(unsigned(rows)), 64, 0, st>>>(w.ml, w.part, nsplit, rows, Hq,
+                                                                      (uint16_t*)out, so_b, so_h);
+  };
+  auto by_e = [&]<int DPL>() {
+    if (nsplit <= 64) go.template operator()<DPL, 1>();
+    else if (nsplit <= 128) go.template operator()<DPL, 2>();
+    else if (nsplit <= 256) go.template operator()<DPL, 4>();
+    else if (nsplit <= 512) go.template operator()<DPL, 8>();
+    else go.template operator()<DPL, 16>();
+  };
+  static_assert(MAXSPLIT == 64 * 16, "combine variants");
+  if (D == 128) by_e.template operator()<2>();
+  else by_e.template operator()<1>();
   return launch_status();
 }
 

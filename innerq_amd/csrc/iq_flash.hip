@@ -326,6 +326,21 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS>::NT), (fused_waves_per_sim
   };
   // wave block (within the (batch, KV head)) of run-relative index idx
   auto block_of = [&](const Run& r, int idx) { return r.split0 * BPS + idx; };
+  // the workgroup whose share holds global split s: max c with c*nitems/grid <= s
+  auto share_of = [&](int s) {
+    return int(((int64_t(s) + 1) * gridDim.x + a.nitems - 1) / a.nitems) - 1;
+  };
+  // The runs of one (batch, KV head) come from the consecutive shares
+  // share_of(first split) .. share_of(last split), one run each: run k of them
+  // writes its partial into split slot k, so the nr partials of a (batch, KV
+  // head) fill slots [0, nr) and the combine finds them without a search; the
+  // slots [nr, nsplit) carry empty statistics, each written by the run whose
+  // splits hold it.
+  auto run_slots = [&](const Run& r, int& slot, int& nr) {
+    const int c0 = share_of(r.bh * a.nsplit);
+    slot = int(blockIdx.x) - c0;
+    nr = share_of((r.bh + 1) * a.nsplit - 1) - c0 + 1;
+  };
 
   // running softmax state of the wave over the current run (log2 domain)
   float m_run[NREP], l_run[NREP], o_run[NREP][DPL];
@@ -338,9 +353,9 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS>::NT), (fused_waves_per_sim
       for (int e = 0; e < DPL; ++e) o_run[h][e] = 0.f;
     }
   };
-  // merge the waves' run states and write the run's partial into the slot of
-  // its first split (every wave is past its last QK^T of the run afterwards)
-  auto flush_run = [&](int bh, int split0) {
+  // merge the waves' run states and write the run's partial into split slot
+  // `slot` (every wave is past its last QK^T of the run afterwards)
+  auto flush_run = [&](int bh, int slot) {
     if (lane == 0) {
 #pragma unroll
       for (int h = 0; h < NREP; ++h) {
@@ -371,7 +386,7 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS>::NT), (fused_waves_per_sim
     // every read of the statistics is done: a wave that runs ahead into its
     // next run may overwrite them after this barrier
     lds_barrier();
-    float* dst = a.part + (int64_t(split0) * rows + int64_t(bh) * NREP) * D;
+    float* dst = a.part + (int64_t(slot) * rows + int64_t(bh) * NREP) * D;
 #pragma unroll
     for (int r = tid; r < NREP * D; r += NT) {
       const int h = r / D, dd = r % D;
@@ -381,7 +396,7 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS>::NT), (fused_waves_per_sim
       dst[r] = val;
     }
     if (tid < NREP) {
-      float* ml = a.ml + (int64_t(split0) * rows + int64_t(bh) * NREP + tid) * 2;
+      float* ml = a.ml + (int64_t(slot) * rows + int64_t(bh) * NREP + tid) * 2;
       ml[0] = mls;
       ml[1] = lls;
     }
@@ -550,11 +565,14 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS>::NT), (fused_waves_per_sim
       nxt = nn < run.nb ? nn : -1;
       return true;
     }
-    // ---- run end: merge the waves; empty statistics in the run's other
-    // split slots (the combine skips them) ----
-    flush_run(run.bh, run.split0);
+    // ---- run end: merge the waves; empty statistics in the slots past the
+    // (batch, KV head)'s partials that lie among this run's splits (the
+    // combine skips them) ----
+    int slot, nr;
+    run_slots(run, slot, nr);
+    flush_run(run.bh, slot);
     if (wave == 0 && lane < NREP) {
-      for (int sp = run.split0 + 1; sp < run.split0 + run.nsplit; ++sp) {
+      for (int sp = max(run.split0, nr); sp < run.split0 + run.nsplit; ++sp) {
         float* ml = a.ml + (int64_t(sp) * rows + int64_t(run.bh) * NREP + lane) * 2;
         ml[0] = -INFINITY;
         ml[1] = 0.f;
