@@ -23,12 +23,15 @@ using namespace iq;
 
 namespace {
 
-constexpr int DCHUNK = 256;  // dense tokens per online-softmax step
+constexpr int DT = 64;        // dense tokens per chunk
+constexpr int NSD_MAX = 4;    // split slots of the dense tokens, at most
+constexpr int DSLICE = 32;    // dense tokens per split slot, at least
 
 struct Seg {
   const uint16_t* dense;
   int64_t sb, sh, st;
   int n, start;  // token count, first token of the segment in the step
+  int vec;       // dense rows 16-byte aligned (base and strides): vector loads
   const uint32_t* codes;
   const uint16_t* meta;
   int64_t t_cap;
@@ -51,31 +54,59 @@ __device__ __forceinline__ float deq(uint32_t f, int bits, int sym, const uint16
   return __fadd_rn(__fmul_rn(float(f), h2f(uint16_t(sz & 0xffffu))), h2f(uint16_t(sz >> 16)));
 }
 
-// element (token t of the step, column d) of a K (channel-grouped store) or V
-// (token-grouped store) segment list
-__device__ float seg_elem(const Seg* s, bool is_k, int64_t b, int64_t kvh, int64_t Hkv, int D, int t, int d,
-                          const uint16_t* norm) {
+// element (segment-local token tl, column d) of a packed K (channel-grouped)
+// or V (token-grouped) segment, dequantized as the reference does
+__device__ float packed_elem(const Seg& g, bool is_k, int64_t bh, int D, int tl, int d, const uint16_t* norm) {
+  const int st = g.t0 + tl;
+  const int W = g.group * g.bits / 32;
+  if (is_k) {
+    const int ng = D / g.group;
+    const int64_t unit = ((bh * (g.t_cap / TOKEN_BLOCK) + st / TOKEN_BLOCK) * ng + d / g.group) * TOKEN_BLOCK +
+                         st % TOKEN_BLOCK;
+    float v = deq(field(g.codes + unit * W, g.bits, d % g.group), g.bits, g.sym, g.meta, unit);
+    if (norm) v = __fmul_rn(v, h2f(norm[bh * D + d]));
+    return v;
+  }
+  const int64_t unit = (bh * (g.t_cap / g.group) + st / g.group) * D + d;
+  return deq(field(g.codes + unit * W, g.bits, st % g.group), g.bits, g.sym, g.meta, unit);
+}
+
+// fp16 elements [d0, d0 + N) of token t's row (a K or V segment list), as N/2
+// dwords; a token outside every segment gives zeros.  Dense rows load as
+// 16-byte vectors where aligned; packed rows (tokens packed in only one of K
+// and V) are dequantized element by element.
+template <int N>
+__device__ __forceinline__ void gather_row(const Seg* s, bool is_k, int64_t b, int64_t kvh, int64_t Hkv, int D, int t,
+                                           int d0, const uint16_t* norm, uint32_t (&out)[N / 2]) {
+#pragma unroll
+  for (int i = 0; i < N / 2; ++i) out[i] = 0u;
 #pragma unroll
   for (int i = 0; i < 3; ++i) {
     const Seg& g = s[i];
     if (t < g.start || t >= g.start + g.n) continue;
     const int tl = t - g.start;
-    if (g.dense) return h2f(g.dense[b * g.sb + kvh * g.sh + tl * g.st + d]);
-    const int st = g.t0 + tl;
-    const int64_t bh = b * Hkv + kvh;
-    const int W = g.group * g.bits / 32;
-    if (is_k) {
-      const int ng = D / g.group;
-      const int64_t unit = ((bh * (g.t_cap / TOKEN_BLOCK) + st / TOKEN_BLOCK) * ng + d / g.group) * TOKEN_BLOCK +
-                           st % TOKEN_BLOCK;
-      float v = deq(field(g.codes + unit * W, g.bits, d % g.group), g.bits, g.sym, g.meta, unit);
-      if (norm) v = __fmul_rn(v, h2f(norm[bh * D + d]));
-      return v;
+    if (g.dense) {
+      const uint16_t* row = g.dense + b * g.sb + kvh * g.sh + int64_t(tl) * g.st + d0;
+      if (g.vec) {
+#pragma unroll
+        for (int c = 0; c < N / 8; ++c) {
+          const uint4 x = reinterpret_cast<const uint4*>(row)[c];
+          out[4 * c] = x.x; out[4 * c + 1] = x.y; out[4 * c + 2] = x.z; out[4 * c + 3] = x.w;
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < N / 2; ++j) out[j] = uint32_t(row[2 * j]) | (uint32_t(row[2 * j + 1]) << 16);
+      }
+    } else {
+      const int64_t bh = b * Hkv + kvh;
+      for (int j = 0; j < N / 2; ++j) {
+        const float x0 = packed_elem(g, is_k, bh, D, tl, d0 + 2 * j, norm);
+        const float x1 = packed_elem(g, is_k, bh, D, tl, d0 + 2 * j + 1, norm);
+        out[j] = uint32_t(__half_as_ushort(__float2half_rn(x0))) | (uint32_t(__half_as_ushort(__float2half_rn(x1))) << 16);
+      }
     }
-    const int64_t unit = (bh * (g.t_cap / g.group) + st / g.group) * D + d;
-    return deq(field(g.codes + unit * W, g.bits, st % g.group), g.bits, g.sym, g.meta, unit);
+    return;
   }
-  return 0.f;
 }
 
 struct DenseArgs {
@@ -84,81 +115,157 @@ struct DenseArgs {
   const uint16_t* norm;
   Seg k[3], v[3];
   int lo0, hi0, lo1, hi1;  // dense tokens: [lo0, hi0) and [lo1, hi1)
-  int Hq, Hkv, D;
+  int Hq, Hkv;
   float scale;
-  float* ml;  // row block of the extra split: [rows][2]
-  float* o;   // [rows][D]
+  float* ml;  // the dense split slots' statistics: slot s at ml + s * rows * 2
+  float* o;   // and partial outputs: slot s at o + s * rows * D
 };
 
-// One workgroup per (b, hq): online softmax over the dense tokens.
+// Online softmax over the dense tokens (fp16 sinks and recent windows, and
+// tokens packed in only one of K and V).  Workgroup (s, b * Hkv + kvh) takes
+// slice s of the dense tokens for the NREP query heads of KV head kvh, in
+// chunks of DT tokens: the chunk's K and V rows are gathered as fp16 into
+// LDS (the next chunk's rows are loaded into registers meanwhile), wave w
+// computes the logits of heads w, w + 4, ... with lane = token and keeps their
+// running (m, l), and thread (head, column pair) accumulates the output.  The
+// probability that meets V is rounded to fp16, as the reference rounds its
+// softmax output; logits, sums and outputs are fp32.
+template <int D, int NREP>
 __global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs a) {
-  __shared__ float qs[128];
-  __shared__ float lg[DCHUNK];
-  __shared__ int tok[DCHUNK];
-  __shared__ float red[4];
-  const int row = blockIdx.x;
-  const int hq = row % a.Hq, b = row / a.Hq;
-  const int kvh = hq / (a.Hq / a.Hkv);
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  if (tid < a.D) qs[tid] = h2f(a.q[b * a.sqb + hq * a.sqh + tid]);
+  constexpr int KS = D / 2 + 1;               // K tile row stride in dwords (odd: no bank conflicts)
+  constexpr int HPW = (NREP + 3) / 4;         // heads per wave
+  constexpr int NPR = D / 2;                  // column pairs per head
+  constexpr int OPT = (NREP * NPR + 255) / 256;  // (head, pair) items per thread
+  constexpr int RE = D / 4;                   // row elements per gathering thread
+  __shared__ uint32_t kt[DT][KS];
+  __shared__ uint32_t vt[DT][D / 2];
+  __shared__ float qs[NREP][D];
+  __shared__ float ps[NREP][DT];
+  __shared__ float al[NREP];
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int bh = blockIdx.y, b = bh / a.Hkv, kvh = bh % a.Hkv;
   const int n0 = a.hi0 - a.lo0, n = n0 + (a.hi1 - a.lo1);
-  float m = -INFINITY, l = 0.f, o = 0.f;  // o: column tid (tid < D)
-  __syncthreads();
-  for (int c0 = 0; c0 < n; c0 += DCHUNK) {
-    const int i = c0 + tid;
-    float x = -INFINITY;
-    int t = -1;
-    if (i < n) {
-      t = i < n0 ? a.lo0 + i : a.lo1 + (i - n0);
-      float s = 0.f;
-      for (int d = 0; d < a.D; ++d) s = fmaf(qs[d], seg_elem(a.k, true, b, kvh, a.Hkv, a.D, t, d, a.norm), s);
-      x = s * a.scale;
+  const int i0 = int(int64_t(blockIdx.x) * n / gridDim.x), i1 = int(int64_t(blockIdx.x + 1) * n / gridDim.x);
+  const int64_t rows = int64_t(gridDim.y) * NREP;
+  for (int i = tid; i < NREP * D; i += 256)
+    qs[i / D][i % D] = h2f(a.q[b * a.sqb + (kvh * NREP + i / D) * a.sqh + i % D]);
+
+  // gathering: thread = (row tid / 4, quarter tid % 4 of the row)
+  const int gr = tid >> 2, gq = tid & 3;
+  uint32_t kr[RE / 2], vr[RE / 2];
+  auto gather = [&](int c0) {
+    const int i = c0 + gr;
+    const int t = i < i1 ? (i < n0 ? a.lo0 + i : a.lo1 + (i - n0)) : -1;
+    gather_row<RE>(a.k, true, b, kvh, a.Hkv, D, t, gq * RE, a.norm, kr);
+    gather_row<RE>(a.v, false, b, kvh, a.Hkv, D, t, gq * RE, nullptr, vr);
+  };
+  float m[HPW], l[HPW];
+#pragma unroll
+  for (int hh = 0; hh < HPW; ++hh) { m[hh] = -INFINITY; l[hh] = 0.f; }
+  float o[OPT][2];
+#pragma unroll
+  for (int it = 0; it < OPT; ++it) o[it][0] = o[it][1] = 0.f;
+
+  if (i0 < i1) gather(i0);
+  for (int c0 = i0; c0 < i1; c0 += DT) {
+#pragma unroll
+    for (int j = 0; j < RE / 2; ++j) {
+      kt[gr][gq * (RE / 2) + j] = kr[j];
+      vt[gr][gq * (RE / 2) + j] = vr[j];
     }
-    float cm = wave_max(x);
-    if (lane == 0) red[wave] = cm;
     __syncthreads();
-    cm = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    __syncthreads();
-    const float mn = fmaxf(m, cm);
-    const float p = (x == -INFINITY) ? 0.f : __expf(x - mn);
-    lg[tid] = __half2float(__float2half_rn(p));  // the probability that meets V is fp16
-    tok[tid] = t;
-    float cs = wave_sum(p);
-    if (lane == 0) red[wave] = cs;
-    __syncthreads();
-    cs = (red[0] + red[1]) + (red[2] + red[3]);
-    const float alpha = (m == -INFINITY) ? 0.f : __expf(m - mn);
-    l = l * alpha + cs;
-    if (tid < a.D) {
-      float acc = o * alpha;
-      const int cnt = min(DCHUNK, n - c0);
-      for (int j = 0; j < cnt; ++j)
-        acc = fmaf(lg[j], seg_elem(a.v, false, b, kvh, a.Hkv, a.D, tok[j], tid, nullptr), acc);
-      o = acc;
+    if (c0 + DT < i1) gather(c0 + DT);  // in flight through this chunk
+    // ---- logits and running softmax: wave w, heads w + 4 hh, lane = token ----
+    float dot[HPW];
+#pragma unroll
+    for (int hh = 0; hh < HPW; ++hh) dot[hh] = 0.f;
+#pragma unroll 8
+    for (int i = 0; i < D / 2; ++i) {
+      const uint32_t k2 = kt[lane][i];
+      const float k0 = h2f(uint16_t(k2 & 0xffffu)), k1 = h2f(uint16_t(k2 >> 16));
+#pragma unroll
+      for (int hh = 0; hh < HPW; ++hh) {
+        const int h = wave + 4 * hh;
+        if (h < NREP) dot[hh] = fmaf(qs[h][2 * i + 1], k1, fmaf(qs[h][2 * i], k0, dot[hh]));
+      }
     }
-    m = mn;
+    const bool live = c0 + lane < i1;
+#pragma unroll
+    for (int hh = 0; hh < HPW; ++hh) {
+      const int h = wave + 4 * hh;
+      if (h < NREP) {
+        const float x = live ? dot[hh] * a.scale : -INFINITY;
+        const float mn = fmaxf(m[hh], wave_max(x));
+        const float p = x == -INFINITY ? 0.f : __expf(x - mn);
+        ps[h][lane] = __half2float(__float2half_rn(p));
+        const float cs = wave_sum(p);
+        const float alpha = m[hh] == -INFINITY ? 0.f : __expf(m[hh] - mn);
+        l[hh] = fmaf(l[hh], alpha, cs);
+        m[hh] = mn;
+        if (lane == 0) al[h] = alpha;
+      }
+    }
+    __syncthreads();
+    // ---- attn.V: thread = (head, column pair) ----
+    const int cnt = min(DT, i1 - c0);
+#pragma unroll
+    for (int it = 0; it < OPT; ++it) {
+      const int idx = tid + 256 * it;
+      if (idx < NREP * NPR) {
+        const int h = idx / NPR, dp = idx % NPR;
+        float o0 = o[it][0] * al[h], o1 = o[it][1] * al[h];
+        for (int j = 0; j < cnt; ++j) {
+          const float p = ps[h][j];
+          const uint32_t v2 = vt[j][dp];
+          o0 = fmaf(p, h2f(uint16_t(v2 & 0xffffu)), o0);
+          o1 = fmaf(p, h2f(uint16_t(v2 >> 16)), o1);
+        }
+        o[it][0] = o0;
+        o[it][1] = o1;
+      }
+    }
     __syncthreads();
   }
-  if (tid == 0) {
-    a.ml[row * 2] = m;
-    a.ml[row * 2 + 1] = l;
+  // ---- this slice's statistics and unnormalized output (an empty slice:
+  // m = -inf, which the combine skips) ----
+  float* mls = a.ml + int64_t(blockIdx.x) * rows * 2;
+  float* os = a.o + int64_t(blockIdx.x) * rows * D;
+  const int64_t row0 = int64_t(b) * a.Hq + int64_t(kvh) * NREP;
+#pragma unroll
+  for (int hh = 0; hh < HPW; ++hh) {
+    const int h = wave + 4 * hh;
+    if (h < NREP && lane == 0) {
+      mls[(row0 + h) * 2] = m[hh];
+      mls[(row0 + h) * 2 + 1] = l[hh];
+    }
   }
-  if (tid < a.D) a.o[int64_t(row) * a.D + tid] = o;
+#pragma unroll
+  for (int it = 0; it < OPT; ++it) {
+    const int idx = tid + 256 * it;
+    if (idx < NREP * NPR) {
+      const int h = idx / NPR, dp = idx % NPR;
+      float* dst = os + (row0 + h) * D + 2 * dp;
+      dst[0] = o[it][0];
+      dst[1] = o[it][1];
+    }
+  }
 }
 
 // out[bq, d] = sum_s e^{m_s - M} o_s[bq, d] / sum_s e^{m_s - M} l_s
 // One wave per row bq, lane = head_dim columns DPL*lane .. DPL*lane+DPL-1.  A
 // split slot with m = -inf carries no tokens and its partial may be unwritten:
 // it is never used.  The fused kernel puts the partials of a (batch, KV head)
-// into its first split slots and the dense tokens take the last one, so one
-// round of loads - every slot's (m, l) and, unconditionally, the partials of
-// the first CSPEC slots and of the last - finds the usual layout whole; a slot
-// is used only if its weight is nonzero (a select: an unwritten partial cannot
-// reach the sum).  Nonempty slots outside that set (the unfused path writes
-// every slot) are listed in LDS and read in a second round, CSPEC loads in
-// flight at a time.
+// into its first split slots and the dense tokens take the last NSD_MAX at
+// most, so one round of loads - every slot's (m, l) and, unconditionally, the
+// partials of the first CSPEC slots and of the last CTAIL - finds the usual
+// layout whole; a slot is used only if its weight is nonzero (a select: an
+// unwritten partial cannot reach the sum).  Nonempty slots outside those sets
+// (the unfused path writes every slot) are listed in LDS and read in a second
+// round, CSPEC loads in flight at a time.
 constexpr int MAXSPLIT = 1024;  // split slots of one step, at most
 constexpr int CSPEC = 8;
+constexpr int CTAIL = NSD_MAX;
 template <int DPL, int E>
 __global__ __launch_bounds__(64) void flash_combine_kernel(const float* __restrict__ ml, const float* __restrict__ part,
                                                            int nsplit, int64_t rows, int Hq,
@@ -179,12 +286,17 @@ __global__ __launch_bounds__(64) void flash_combine_kernel(const float* __restri
   float2 sl[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) sl[e] = st[int64_t(min(e * 64 + lane, last)) * rows];
-  Vec pv[CSPEC + 1];
+  Vec pv[CSPEC], pt[CTAIL];
 #pragma unroll
   for (int j = 0; j < CSPEC; ++j) pv[j] = pr[int64_t(min(j, last)) * pstride];
-  pv[CSPEC] = pr[int64_t(last) * pstride];
-  const float m_last = st[int64_t(last) * rows].x;
-  const bool last_apart = last >= CSPEC;
+  const int tail0 = max(nsplit - CTAIL, CSPEC);  // first tail slot not among the first CSPEC
+  float mt[CTAIL];
+#pragma unroll
+  for (int k = 0; k < CTAIL; ++k) {
+    const int s = min(tail0 + k, last);
+    pt[k] = pr[int64_t(s) * pstride];
+    mt[k] = st[int64_t(s) * rows].x;
+  }
 #pragma unroll
   for (int e = 0; e < E; ++e)
     if (e * 64 + lane > last) sl[e] = make_float2(-INFINITY, 0.f);
@@ -205,14 +317,16 @@ __global__ __launch_bounds__(64) void flash_combine_kernel(const float* __restri
     const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w[0]), j));  // slot j: lane j
     if (wj != 0.f) acc += wj * pv[j];
   }
-  if (last_apart && m_last != -INFINITY) acc += __expf(m_last - M) * pv[CSPEC];
-  // ---- the rest: nonempty slots in [CSPEC, last) ----
+#pragma unroll
+  for (int k = 0; k < CTAIL; ++k)
+    if (tail0 + k <= last && mt[k] != -INFINITY) acc += __expf(mt[k] - M) * pt[k];
+  // ---- the rest: nonempty slots in [CSPEC, tail0) ----
   int n = 0;
 #pragma unroll
   for (int e = 0; e < E; ++e) {
     if (e * 64 >= nsplit) break;
     const int s = e * 64 + lane;
-    const bool take = w[e] != 0.f && s >= CSPEC && s < last;
+    const bool take = w[e] != 0.f && s >= CSPEC && s < tail0;
     const unsigned long long bal = __ballot(take);
     if (take) {
       const int k = n + __popcll(bal & ((1ull << lane) - 1ull));
@@ -249,6 +363,7 @@ Seg to_seg(const iq_segment& s, int start) {
   g.codes = s.codes; g.meta = s.meta; g.t_cap = s.t_cap; g.t0 = s.t0;
   g.bits = s.bits; g.group = s.group; g.sym = s.mode == IQ_MODE_SYM;
   if (s.n && s.codes) g.dense = nullptr;
+  g.vec = g.dense && aligned(g.dense, 16) && s.s_b % 8 == 0 && s.s_h % 8 == 0 && s.s_t % 8 == 0;
   return g;
 }
 
@@ -273,7 +388,7 @@ Workspace carve(void* workspace, int B, int Hq, int T, int D) {
   for (int g : {32, 64, 128}) vrec_bytes = std::max(vrec_bytes, rec_bytes_bound(int64_t(B) * Hq, T / g, g));
   w.vrec = (uint32_t*)ws;
   ws += align256(vrec_bytes);
-  const size_t ns_cap = size_t(nsplit_max(T)) + 1;
+  const size_t ns_cap = size_t(nsplit_max(T)) + NSD_MAX;
   w.ml = (float*)ws;
   ws += align256(ns_cap * rows * 2 * 4);
   w.part = (float*)ws;
@@ -285,7 +400,7 @@ int check_decode(const void* q, const iq_segment* k, const iq_segment* v, int B,
   IQ_CHECK(q && k && v, IQ_ERR_NULL);
   IQ_CHECK(B >= 0 && T > 0 && Hkv > 0 && Hq > 0, IQ_ERR_SHAPE);
   IQ_CHECK(d_ok(D) && Hq % Hkv == 0 && nrep_ok(Hq / Hkv), IQ_ERR_SHAPE);
-  IQ_CHECK(nsplit_max(T) + 1 <= MAXSPLIT, IQ_ERR_SHAPE);
+  IQ_CHECK(nsplit_max(T) + NSD_MAX <= MAXSPLIT, IQ_ERR_SHAPE);
   for (int s = 0; s < 3; ++s) IQ_CHECK(k[s].n >= 0 && v[s].n >= 0, IQ_ERR_SHAPE);
   IQ_CHECK(k[0].n + k[1].n + k[2].n == T && v[0].n + v[1].n + v[2].n == T, IQ_ERR_SHAPE);
   for (int s : {0, 2}) {
@@ -360,7 +475,8 @@ int launch_splits(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, c
                                         vg.group, vg.bits, vg.mode, w.part, st))
       return e;
   }
-  // dense tokens -> extra split nsf
+  // dense tokens -> split slots nsf, nsf + 1, ...: enough workgroups to
+  // spread over the CUs, at least DSLICE tokens each
   DenseArgs da{};
   da.q = (const uint16_t*)q; da.sqb = sq_b; da.sqh = sq_h; da.norm = (const uint16_t*)norm;
   int start = 0;
@@ -369,15 +485,29 @@ int launch_splits(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, c
   for (int s = 0; s < 3; ++s) { da.v[s] = to_seg(v[s], start); start += v[s].n; }
   da.lo0 = 0; da.hi0 = c ? a0 : T;
   da.lo1 = c ? a0 + c : T; da.hi1 = T;
-  da.Hq = Hq; da.Hkv = Hkv; da.D = D; da.scale = scale;
+  da.Hq = Hq; da.Hkv = Hkv; da.scale = scale;
   da.ml = w.ml + int64_t(nsf) * rows * 2;
   da.o = w.part + int64_t(nsf) * rows * D;
   const int n_dense = (da.hi0 - da.lo0) + (da.hi1 - da.lo1);
+  int nsd = 0;
   if (n_dense > 0) {
-    dense_attn_kernel<<<dim3(unsigned(rows)), 256, 0, st>>>(da);
+    const int64_t bhs = int64_t(B) * Hkv;
+    nsd = int(std::min<int64_t>({NSD_MAX, ceil_div(n_dense, DSLICE), std::max<int64_t>(1, ceil_div(detail::num_cus(), bhs))}));
+    const dim3 grid{unsigned(nsd), unsigned(bhs), 1u};
+    auto go = [&]<int DD, int R>() { dense_attn_kernel<DD, R><<<grid, 256, 0, st>>>(da); };
+    auto by_r = [&]<int DD>() {
+      switch (Hq / Hkv) {
+        case 1: go.template operator()<DD, 1>(); break;
+        case 2: go.template operator()<DD, 2>(); break;
+        case 4: go.template operator()<DD, 4>(); break;
+        default: go.template operator()<DD, 8>(); break;
+      }
+    };
+    if (D == 128) by_r.template operator()<128>();
+    else by_r.template operator()<64>();
     if (int e = launch_status()) return e;
   }
-  *nsplit = nsf + (n_dense > 0 ? 1 : 0);
+  *nsplit = nsf + nsd;
   return IQ_OK;
 }
 
@@ -411,7 +541,7 @@ size_t iq_decode_workspace_bytes(int B, int Hq, int T, int D) {
   const size_t rows = size_t(B) * Hq;
   size_t vrec = 0;
   for (int g : {32, 64, 128}) vrec = std::max(vrec, rec_bytes_bound(int64_t(B) * Hq, T / g, g));
-  const size_t ns = size_t(nsplit_max(T)) + 1;
+  const size_t ns = size_t(nsplit_max(T)) + NSD_MAX;
   return detail::qk_record_bytes(B, Hq, D) + align256(vrec) + align256(ns * rows * 2 * 4) +
          align256(ns * rows * D * 4);
 }
@@ -431,7 +561,7 @@ int iq_decode_attention_combine(int nsplit, int B, int Hq, int T, int D, void* o
                                 void* workspace, size_t workspace_bytes, void* stream) {
   IQ_CHECK(out && workspace, IQ_ERR_NULL);
   IQ_CHECK(B >= 0 && Hq > 0 && T > 0 && d_ok(D), IQ_ERR_SHAPE);
-  IQ_CHECK(nsplit >= 1 && nsplit <= nsplit_max(T) + 1 && nsplit <= MAXSPLIT, IQ_ERR_SHAPE);
+  IQ_CHECK(nsplit >= 1 && nsplit <= nsplit_max(T) + NSD_MAX && nsplit <= MAXSPLIT, IQ_ERR_SHAPE);
   IQ_CHECK(workspace_bytes >= iq_decode_workspace_bytes(B, Hq, T, D), IQ_ERR_WORKSPACE);
   IQ_CHECK(aligned(workspace, 256), IQ_ERR_ALIGN);
   if (B == 0) return IQ_OK;

@@ -189,6 +189,7 @@ def test_decode_stage_rejects():
                                           ctypes.byref(ns), None) == -4
     assert ns.value == -7
     assert lib.iq_decode_attention_combine(0, 1, 32, 64, 128, FAKE, 4096, 128, FAKE, 1 << 30, None) == -4
-    assert lib.iq_decode_attention_combine(3, 1, 32, 64, 128, FAKE, 4096, 128, FAKE, 1 << 30, None) == -4
+    # T = 64: one 256-token split of packed tokens + at most four slices of dense tokens
+    assert lib.iq_decode_attention_combine(6, 1, 32, 64, 128, FAKE, 4096, 128, FAKE, 1 << 30, None) == -4
     assert lib.iq_decode_attention_combine(1, 1, 32, 64, 128, None, 4096, 128, FAKE, 1 << 30, None) == -1
     assert lib.iq_decode_attention_combine(1, 1, 32, 64, 128, FAKE, 4096, 128, FAKE, 64, None) == -6

@@ -397,6 +397,37 @@ def test_decode_attention_gqa_shapes(nrep, D):
     assert err < TOL
 
 
+@pytest.mark.parametrize("nrep,D,R", [(8, 64, 72), (1, 128, 200), (4, 128, 1000)])
+def test_decode_attention_dense_window_unaligned(nrep, D, R):
+    """Recent windows given as views whose rows are not 16-byte aligned (odd token
+    stride, base two bytes in): the dense gather's element-wise path; R = 1000 runs
+    several 64-token chunks per dense slice."""
+    B, Hkv, G = 2, 2, 32
+    Tq = 64 * 6
+    T = Tq + R
+    kx = synth.kv_tensor(B, Hkv, T, D, seed=71 + R, n_out=4, factor=8.0)
+    vx = synth.kv_tensor(B, Hkv, T, D, seed=72 + R, n_out=4, factor=8.0)
+    q = synth.normal((B, Hkv * nrep, D), seed=73).astype(np.float16)
+    kst = ops.PackedStore("channel", B, Hkv, D, G, 4, "asymmetric", DEV)
+    vst = ops.PackedStore("token", B, Hkv, D, G, 4, "asymmetric", DEV)
+    kst.append(f16t(kx[:, :, :Tq]))
+    vst.append(f16t(vx[:, :, :Tq]))
+
+    def unaligned(x):
+        buf = torch.zeros(B, Hkv, R, D + 1, dtype=torch.float16, device=DEV)
+        buf[..., 1:] = f16t(x)
+        return buf[..., 1:]
+
+    kr, vr = unaligned(kx[:, :, Tq:]), unaligned(vx[:, :, Tq:])
+    assert kr.stride(2) % 8 and kr.data_ptr() % 16
+    got = ops.decode_attention(f16t(q), None, kst, kr, None, vst, vr, D ** -0.5).cpu().numpy().astype(np.float64)
+    c, s, z = oracle_q(kx[:, :, :Tq], 4, G, "asymmetric", "channel")
+    kd = np.concatenate([oracle_deq(c, s, z, G, "asymmetric", "channel"), kx[:, :, Tq:].astype(np.float32)], axis=2)
+    c, s, z = oracle_q(vx[:, :, :Tq], 4, G, "asymmetric", "token")
+    vd = np.concatenate([oracle_deq(c, s, z, G, "asymmetric", "token"), vx[:, :, Tq:].astype(np.float32)], axis=2)
+    assert A.rel_err(got, A.decode_attention(q, kd, vd, D ** -0.5, p_dtype=None)) < TOL
+
+
 # K and V of one bit width and group size take the fused split kernel (one
 # workgroup runs QK^T, the split softmax and attn.V); sym/asym may differ.
 @pytest.mark.parametrize("fmt,nrep,D", [
@@ -433,6 +464,6 @@ def test_decode_stages_equal_decode_attention(fused):
     q = f16t(synth.normal((B, Hkv * nrep, D), seed=63).astype(np.float16))
     ref = ops.decode_attention(q, None, kst, kr, None, vst, vr, D ** -0.5).cpu().numpy()
     ns = ops.decode_attention_splits(q, None, kst, kr, None, vst, vr, D ** -0.5)
-    assert ns == 3 + 1  # three 256-token splits of the packed range + the dense tail
+    assert ns == 3 + 2  # three 256-token splits of the packed range + the 40 dense tokens in two slices
     got = ops.decode_attention_combine(ns, B, Hkv * nrep, T, D, DEV).cpu().numpy()
     np.testing.assert_array_equal(got.view(np.uint16), ref.view(np.uint16))
