@@ -4,15 +4,17 @@
 // The token axis is cut into
 //   * the fused range: tokens packed in both the K and the V store (the
 //     middle segment of cache.py:235-276 for both), in splits of
-//     flash_split_tokens() tokens.  When K and V share bit width and group
-//     size, one kernel per split runs QK^T, the split softmax and attn.V
-//     (iq_flash.hip).  Otherwise QK^T runs with its flash epilogue (per split
-//     max m, sum l and fp16 probabilities written as attn.V operand records),
-//     then attn.V writes one unnormalized partial output per split;
+//     flash_split_tokens() tokens.  When K and V share their group size (bit
+//     widths may differ), one persistent kernel runs QK^T, the softmax and
+//     attn.V over every split (iq_flash.h) and writes one partial per run of
+//     splits.  Otherwise QK^T runs with its flash epilogue (per split max m,
+//     sum l and fp16 probabilities written as attn.V operand records), then
+//     attn.V writes one unnormalized partial output per split;
 //   * the dense tokens: everything else (fp16 sinks and recent windows, plus
 //     packed tokens of only one of K/V, which are dequantized element by
-//     element).  One workgroup per (batch, query head) runs an online softmax
-//     over them and contributes one extra split.
+//     element), in up to NSD_MAX slices, each an extra split: one workgroup
+//     per (slice, batch, KV head) runs an online softmax over its tokens for
+//     the KV head's query heads.
 // A combine kernel rescales the splits by exp(m_s - max m) and divides by the
 // total sum: softmax(q K^T * scale) V in fp32, written as fp16
 // (TF/models/llama/modeling_llama.py:201-210).  The probabilities that meet V
@@ -458,8 +460,7 @@ int launch_splits(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, c
                               k[1].mode};
   const detail::FusedStore fv{v[1].codes, v[1].meta, v[1].t_cap, v[1].t0 + (a0 - vs), v[1].bits, v[1].group,
                               v[1].mode};
-  if (c && k[1].bits == v[1].bits && k[1].group == v[1].group &&
-      detail::flash_fused_supported(q, sq_b, sq_h, norm, fk, fv, Hq, Hkv, D)) {
+  if (c && k[1].group == v[1].group && detail::flash_fused_supported(q, sq_b, sq_h, norm, fk, fv, Hq, Hkv, D)) {
     if (int e = detail::flash_fused_launch(q, sq_b, sq_h, norm, fk, fv, B, Hq, Hkv, c, D, scale, w.ml, w.part, st))
       return e;
   } else if (c) {

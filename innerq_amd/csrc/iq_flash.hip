@@ -1,42 +1,5 @@
-// Fused flash-decoding kernel (gfx950): QK^T, softmax and attn.V over the
-// packed range of every (batch, KV head), for K and V stores that share bit
-// width and group size.  Its output is one partial (m, l, unnormalized o) per
-// run in the split slots of the decode workspace; the combine kernel
-// (iq_decode.hip) merges the slots.
-//
-// Persistent and software pipelined.  One workgroup per CU (as many waves as
-// the register allocation allows per SIMD) takes an equal contiguous share of
-// the (batch, KV head)-major list of FSPLIT-token splits and processes it as
-// runs, the maximal pieces of one (batch, KV head).  Inside a run the waves
-// claim wave blocks of WTOK tokens (lane = token for QK^T) from a counter in
-// LDS, so they finish the run together, and each wave keeps a running
-// softmax state (m, l, o) over its blocks.  A wave streams its packed data
-// straight into VGPRs with raw buffer loads:
-//   at the top of a block: K codes and {scale, zero} of its NEXT block (kept
-//          in flight through the whole block);
-//   after attn.V: V codes and {scale, zero} of the next block (lane = head_dim
-//          column);
-// and computes on data loaded one block earlier:
-//   QK^T   per head_dim group eight v_mfma_f32_4x4x4f16 per 32 codes and four
-//          query heads (iq_gemv.h): B = biased code pairs, A = the run's query
-//          records in LDS, accumulators seeded with -sum(q * bias);
-//   softmax  against the wave's running max (log2 domain, DPP reductions);
-//          each lane writes its fp16 p straight into its slot of the wave's
-//          attn.V operand record (the inverse of the unpack plan); the
-//          per-V-group sums of p (zero-point term, l) and of -p * bias (seed
-//          of attn.V) by DPP;
-//   attn.V lane = column d = lane + 64 e over the block's V groups.
-// At the end of a run the waves merge (rescale by exp2(m_w - m), sum in LDS)
-// and write the run's partial into the slot of its first split; its other
-// split slots get empty statistics.  The next run's query records come from
-// q values prefetched during the run (a key normalization, which the
-// reference applies to the dequantized keys, cache.py:128-133 and 249, is
-// folded into q as hi/lo fp16 parts of q*n).
-//
-// The store formats follow the unfused kernels: K codes [B,H,t_cap/64,D/G,64,W],
-// V codes [B,H,t_cap/G,D,W]; sym or asym per store is a runtime flag (a
-// uniform branch), so the kernel is instantiated per (bits, G, D, n_rep,
-// hi/lo query rows) only.
+// Host entry of the fused flash-decoding kernel (iq_flash.h): argument
+// checks, the kernel's argument block, and the launch for the K bit width.
 #include <algorithm>
 
 #include "iq_gemv.h"
@@ -44,567 +7,7 @@
 using namespace iq;
 
 namespace {
-
 constexpr int FSPLIT = NWAVES * IQ_FLASH_BPW * TOKEN_BLOCK;  // tokens per split (= flash_split_tokens())
-
-
-// Pair k of a group's unpack plan: code index of its first and second half.
-template <int BITS>
-__host__ __device__ constexpr int plan_a(int k) { return pair_code_a<BITS>(k); }
-template <int BITS>
-__host__ __device__ constexpr int plan_c(int k) { return pair_code_c<BITS>(k); }
-
-// Inverse of the plan: code i of a group sits in pair k, half hi (0: low),
-// with bias 2^(10 - p) (p = the field's bit position in its half).
-template <int BITS>
-__host__ __device__ constexpr void plan_inv(int i, int& k, int& hi, float& bias) {
-  using P = Plan<BITS>;
-  const int sb = i / P::CODES, r = i % P::CODES;
-  k = 0;
-  hi = 0;
-  bias = 0.f;
-  for (int x = 0; x < P::NPAIR; ++x) {
-    if (P::A[x] == r) { k = sb * P::NPAIR + x; hi = 0; bias = bias_a<BITS>(x); }
-    if (P::C[x] == r) { k = sb * P::NPAIR + x; hi = 1; bias = bias_c<BITS>(x); }
-  }
-}
-template <int BITS>
-constexpr bool plan_inv_ok() {
-  for (int i = 0; i < 128; ++i) {
-    int k = 0, hi = 0;
-    float b = 0.f;
-    plan_inv<BITS>(i, k, hi, b);
-    if ((hi ? plan_c<BITS>(k) : plan_a<BITS>(k)) != i) return false;
-  }
-  return true;
-}
-static_assert(plan_inv_ok<2>() && plan_inv_ok<3>() && plan_inv_ok<4>(), "plan inverse");
-
-struct FusedArgs {
-  const uint16_t* q;
-  int64_t sqb, sqh;
-  const uint16_t* norm;  // [B*Hkv][D] or null
-  const uint32_t* kc;
-  const uint16_t* km;
-  int64_t k_cap_blocks;
-  int kblk0, ksym;
-  const uint32_t* vc;
-  const uint16_t* vm;
-  int64_t v_cap_groups;
-  int vg0, vsym;
-  int Hkv, T;          // T: tokens of the range, a multiple of G
-  int nsplit, nitems;  // splits per (batch, KV head); nsplit * B * Hkv
-  uint32_t k_code_bytes, k_meta_bytes, v_code_bytes, v_meta_bytes, q_bytes, norm_bytes;
-  float scale_log2;    // scale * log2(e)
-  float* ml;           // [nsplit][B*Hq][2]
-  float* part;         // [nsplit][B*Hq][D]
-};
-
-// waves per SIMD the register allocation aims at: three (<= 168 VGPRs) for
-// 64-token waves and up to 4 query heads per KV head, fewer where the operand
-// and accumulator registers need more (8 heads, or hi/lo query rows with 4)
-template <int G, int NREP, bool QS>
-constexpr int fused_waves_per_simd() {
-  return G > TOKEN_BLOCK ? 1 : (NREP > 4 || (QS && NREP == 4)) ? 2 : 3;
-}
-
-// Workgroup shape: one workgroup per CU, filling every SIMD to the register
-// allocation's occupancy; a wave processes blocks of WTOK consecutive tokens
-// (lane = token for QK^T), so that a V group of G tokens lies inside a block.
-template <int G, int NREP, bool QS>
-struct FusedShape {
-  static constexpr int WTOK = G > TOKEN_BLOCK ? G : TOKEN_BLOCK;
-  static constexpr int FBPW = WTOK / TOKEN_BLOCK;                // 64-token K blocks per wave block
-  static constexpr int NW = 4 * fused_waves_per_simd<G, NREP, QS>();  // waves per workgroup
-  static constexpr int NT = NW * 64;
-  static constexpr int VPW = WTOK / G;                           // V groups per wave block
-  static_assert(FSPLIT % WTOK == 0, "a split holds whole wave blocks");
-};
-
-template <int BITS, int G, int D, int NREP, bool QS>
-struct FusedSmem {
-  using FS = FusedShape<G, NREP, QS>;
-  alignas(16) uint32_t qrec[D / G][qrec_dwords<G, NREP>()];         // query records of the current split
-  alignas(16) uint32_t vrec[FS::NW][FS::VPW][rec_dwords<G, NREP>()];  // per wave: fp16 p pairs
-  alignas(16) float red[FS::NW][NREP][D];                            // merge of the waves' outputs
-  float m[FS::NW][NREP];
-  float l[FS::NW][NREP];
-  int next_block;  // the current run's next unclaimed wave block
-};
-
-// ---- raw buffer loads -------------------------------------------------------
-// A block reads its (batch, KV head) slice of a store through a buffer
-// resource: a byte offset per lane (VGPR) plus a uniform offset (SGPR).  A
-// resource with zero records turns every load into a zero fill that moves no
-// data; the prefetch past a wave's last block uses that, so every iteration
-// issues the same loads and the compiler's memory counter waits stay exact.
-typedef __amdgpu_buffer_rsrc_t rsrc_t;
-__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, int(bytes), 0x00020000);
-}
-template <int N>
-__device__ __forceinline__ void bload_words(rsrc_t r, uint32_t voff, uint32_t soff, uint32_t (&w)[N]) {
-#pragma unroll
-  for (int c = 0; c < N / 4; ++c) {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff + 16 * c, soff, 0);
-    w[4 * c] = v[0]; w[4 * c + 1] = v[1]; w[4 * c + 2] = v[2]; w[4 * c + 3] = v[3];
-  }
-  constexpr int R = N % 4, C0 = N - N % 4;
-  if constexpr (R == 3) {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b96(r, voff + 4 * C0, soff, 0);
-    w[C0] = v[0]; w[C0 + 1] = v[1]; w[C0 + 2] = v[2];
-  } else if constexpr (R == 2) {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, voff + 4 * C0, soff, 0);
-    w[C0] = v[0]; w[C0 + 1] = v[1];
-  } else if constexpr (R == 1) {
-    w[C0] = __builtin_amdgcn_raw_buffer_load_b32(r, voff + 4 * C0, soff, 0);
-  }
-}
-__device__ __forceinline__ uint32_t bload_u32(rsrc_t r, uint32_t voff, uint32_t soff) {
-  return __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
-}
-__device__ __forceinline__ uint16_t bload_u16(rsrc_t r, uint32_t voff, uint32_t soff) {
-  return __builtin_amdgcn_raw_buffer_load_b16(r, voff, soff, 0);
-}
-
-// {scale, zero} of a lane's token (K) or column (V) from its meta dword: asym
-// meta is one {scale, zero} dword per lane; sym meta is one fp16 scale per
-// lane, read as the dword holding the scales of lanes 2i and 2i + 1.
-__device__ __forceinline__ uint32_t meta_voff(int lane, int sym) { return sym ? uint32_t(lane & ~1) * 2 : uint32_t(lane) * 4; }
-template <int BITS>
-__device__ __forceinline__ void meta_sz(uint32_t mw, int lane, int sym, float& s, float& z) {
-  if (sym) {
-    s = h2f(uint16_t((lane & 1) ? (mw >> 16) : (mw & 0xffffu)));
-    z = -float(1 << (BITS - 1)) * s;  // offset-binary codes: signed = u - 2^(b-1)
-  } else {
-    s = h2f(uint16_t(mw & 0xffffu));
-    z = h2f(uint16_t(mw >> 16));
-  }
-}
-
-// Workgroup barrier for data exchanged through LDS.  __syncthreads() would
-// also wait for every outstanding global load, i.e. for the next split's
-// prefetch; only the LDS writes need to be complete.
-__device__ __forceinline__ void lds_barrier() {
-  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-
-// sum over aligned segments of N lanes (every lane gets its segment's sum)
-template <int N>
-__device__ __forceinline__ float seg_sum(float v) {
-#pragma unroll
-  for (int o = 1; o < N; o <<= 1) v += __shfl_xor(v, o, 64);
-  return v;
-}
-
-template <int BITS, int G, int D, int NREP, bool QS>
-__global__ __launch_bounds__((FusedShape<G, NREP, QS>::NT), (fused_waves_per_simd<G, NREP, QS>())) void flash_fused_kernel(FusedArgs a) {
-  using FS = FusedShape<G, NREP, QS>;
-  constexpr int NW = FS::NW, NT = FS::NT, WTOK = FS::WTOK, FBPW = FS::FBPW, VPW = FS::VPW;
-  constexpr int BPS = FSPLIT / WTOK;  // wave blocks per split
-  constexpr int NG = D / G;
-  constexpr int W = G * BITS / 32;
-  constexpr int NP = G / 2;
-  constexpr int DPL = D / 64;
-  constexpr int NPAIRS = NG * NREP * NP;  // query pairs of a split's records
-  constexpr int NPT = (NPAIRS + NT - 1) / NT;
-  constexpr int QOS = qrec_osum<G, NREP>();
-  constexpr int QNB = qrec_nbsum<G, NREP>();
-  constexpr int NQ = (NREP + 3) / 4;
-  __shared__ FusedSmem<BITS, G, D, NREP, QS> sm;
-
-  const int tid = threadIdx.x;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int lane = tid & 63;
-  const int hl = lane & 3;
-  constexpr bool qsplit = QS;  // key normalization: hi/lo query rows
-  const int kms = a.ksym ? 2 : 4, vms = a.vsym ? 2 : 4;  // meta bytes per token / column
-  const uint32_t kmv = meta_voff(lane, a.ksym), vmv = meta_voff(lane, a.vsym);
-  const int64_t rows = int64_t(a.nitems / a.nsplit) * NREP;
-
-  struct KRegs { uint32_t w[NG][FBPW][W]; uint32_t m[NG][FBPW]; };
-  struct VRegs { uint32_t w[VPW][DPL][W]; uint32_t m[VPW][DPL]; };
-  struct QRegs { uint16_t a[NPT], c[NPT], na[NPT], nc[NPT]; };
-
-  // ---- loads of wave block blk (tokens [blk*WTOK, +WTOK) of the range) of
-  // (batch, KV head) bh into registers; real = false: zero fill ----
-  auto load_k = [&](int bh, int blk, bool real, KRegs& k) {
-    const int64_t blk0 = int64_t(bh) * a.k_cap_blocks + a.kblk0;
-    const rsrc_t rc = make_rsrc(a.kc + blk0 * (NG * TOKEN_BLOCK * W), real ? a.k_code_bytes : 0u);
-    const rsrc_t rm = make_rsrc(a.km + blk0 * (NG * TOKEN_BLOCK * (kms / 2)), real ? a.k_meta_bytes : 0u);
-    const int b0 = blk * FBPW;
-#pragma unroll
-    for (int g = 0; g < NG; ++g)
-#pragma unroll
-      for (int j = 0; j < FBPW; ++j) {
-        const uint32_t u = uint32_t((b0 + j) * NG + g) * TOKEN_BLOCK;  // first token slot of the unit
-        bload_words<W>(rc, uint32_t(lane) * (W * 4), u * (W * 4), k.w[g][j]);
-        k.m[g][j] = bload_u32(rm, kmv, u * kms);
-      }
-  };
-  auto load_v = [&](int bh, int blk, bool real, VRegs& v) {
-    const int64_t g0 = int64_t(bh) * a.v_cap_groups + a.vg0;
-    const rsrc_t rc = make_rsrc(a.vc + g0 * (D * W), real ? a.v_code_bytes : 0u);
-    const rsrc_t rm = make_rsrc(a.vm + g0 * (D * (vms / 2)), real ? a.v_meta_bytes : 0u);
-    const int vgw = blk * WTOK / G;  // the block's first V group
-#pragma unroll
-    for (int u = 0; u < VPW; ++u)
-#pragma unroll
-      for (int e = 0; e < DPL; ++e) {
-        const uint32_t c0 = uint32_t((vgw + u) * D + 64 * e);  // first column slot of the unit
-        bload_words<W>(rc, uint32_t(lane) * (W * 4), c0 * (W * 4), v.w[u][e]);
-        v.m[u][e] = bload_u32(rm, vmv, c0 * vms);
-      }
-  };
-  auto load_q = [&](int bh, bool real, QRegs& qq) {
-    const int b = bh / a.Hkv, kvh = bh - b * a.Hkv;
-    const rsrc_t rq = make_rsrc(a.q + b * a.sqb + int64_t(kvh * NREP) * a.sqh, real ? a.q_bytes : 0u);
-    const rsrc_t rn = make_rsrc(a.norm ? a.norm + int64_t(bh) * D : a.q, real ? a.norm_bytes : 0u);
-#pragma unroll
-    for (int r = 0; r < NPT; ++r) {
-      const int i = min(tid + r * NT, NPAIRS - 1);
-      const int k = i % NP, h = (i / NP) % NREP, g = i / (NP * NREP);
-      const int ia = g * G + plan_a<BITS>(k), ic = g * G + plan_c<BITS>(k);
-      qq.a[r] = bload_u16(rq, uint32_t(h * a.sqh + ia) * 2, 0);
-      qq.c[r] = bload_u16(rq, uint32_t(h * a.sqh + ic) * 2, 0);
-      qq.na[r] = bload_u16(rn, uint32_t(ia) * 2, 0);
-      qq.nc[r] = bload_u16(rn, uint32_t(ic) * 2, 0);
-    }
-  };
-  // query records of a split from its loaded q (and norm) values; osum by
-  // shuffles inside the NP lanes of each (group, head)
-  auto build_records = [&](const QRegs& qq) {
-#pragma unroll
-    for (int r = 0; r < NPT; ++r) {
-      const int i0 = tid + r * NT;
-      const int i = min(i0, NPAIRS - 1);
-      const int k = i % NP, h = (i / NP) % NREP, g = i / (NP * NREP);
-      uint32_t hi = 0, lo = 0;
-      float s = 0.f;
-      qrec_pair_vals(qq.a[r], qq.c[r], qq.na[r], qq.nc[r], qsplit, &hi, &lo, s);
-      // -sum(x * bias) of the hi and lo rows (exact products: the biases are powers of two)
-      const float ba = bias_a<BITS>(k % Plan<BITS>::NPAIR), bc = bias_c<BITS>(k % Plan<BITS>::NPAIR);
-      float bh = -(h2f(uint16_t(hi & 0xffffu)) * ba + h2f(uint16_t(hi >> 16)) * bc);
-      float bl = -(h2f(uint16_t(lo & 0xffffu)) * ba + h2f(uint16_t(lo >> 16)) * bc);
-      s = seg_sum<NP>(s);
-      bh = seg_sum<NP>(bh);
-      bl = seg_sum<NP>(bl);
-      if (i0 < NPAIRS) {
-        sm.qrec[g][h * NP + k] = hi;
-        if (qsplit) sm.qrec[g][(NREP + h) * NP + k] = lo;
-        if (k == 0) {
-          sm.qrec[g][QOS + h] = __float_as_uint(s);
-          sm.qrec[g][QNB + h] = __float_as_uint(bh);
-          sm.qrec[g][QNB + NREP + h] = __float_as_uint(bl);
-        }
-      }
-    }
-  };
-
-  const PlanRegs<BITS> pr;
-  // ---- work: this workgroup's splits [i0, i1) of the (batch, KV head)-major
-  // split list (contiguous, equal shares: one workgroup per CU), processed as
-  // runs, the maximal pieces of one (batch, KV head).  Inside a run the waves
-  // claim wave blocks from a counter in LDS (the first two per wave are
-  // fixed), so they all finish the run within about one block of each other
-  // whatever the issue arbitration favours. ----
-  const int i0 = int(int64_t(blockIdx.x) * a.nitems / gridDim.x);
-  const int i1 = int(int64_t(blockIdx.x + 1) * a.nitems / gridDim.x);
-  if (i0 >= i1) return;  // uniform over the workgroup, before any barrier
-  struct Run {
-    int bh, split0, nsplit, nb;  // (batch, KV head), first split, splits, wave blocks
-  };
-  auto run_at = [&](int s0) {
-    Run r;
-    r.bh = s0 / a.nsplit;
-    r.split0 = s0 - r.bh * a.nsplit;
-    r.nsplit = min(i1, (r.bh + 1) * a.nsplit) - s0;
-    r.nb = r.nsplit * BPS;
-    return r;
-  };
-  // wave block (within the (batch, KV head)) of run-relative index idx
-  auto block_of = [&](const Run& r, int idx) { return r.split0 * BPS + idx; };
-  // the workgroup whose share holds global split s: max c with c*nitems/grid <= s
-  auto share_of = [&](int s) {
-    return int(((int64_t(s) + 1) * gridDim.x + a.nitems - 1) / a.nitems) - 1;
-  };
-  // The runs of one (batch, KV head) come from the consecutive shares
-  // share_of(first split) .. share_of(last split), one run each: run k of them
-  // writes its partial into split slot k, so the nr partials of a (batch, KV
-  // head) fill slots [0, nr) and the combine finds them without a search; the
-  // slots [nr, nsplit) carry empty statistics, each written by the run whose
-  // splits hold it.
-  auto run_slots = [&](const Run& r, int& slot, int& nr) {
-    const int c0 = share_of(r.bh * a.nsplit);
-    slot = int(blockIdx.x) - c0;
-    nr = share_of((r.bh + 1) * a.nsplit - 1) - c0 + 1;
-  };
-
-  // running softmax state of the wave over the current run (log2 domain)
-  float m_run[NREP], l_run[NREP], o_run[NREP][DPL];
-  auto reset_run = [&]() {
-#pragma unroll
-    for (int h = 0; h < NREP; ++h) {
-      m_run[h] = -INFINITY;
-      l_run[h] = 0.f;
-#pragma unroll
-      for (int e = 0; e < DPL; ++e) o_run[h][e] = 0.f;
-    }
-  };
-  // merge the waves' run states and write the run's partial into split slot
-  // `slot` (every wave is past its last QK^T of the run afterwards)
-  auto flush_run = [&](int bh, int slot) {
-    if (lane == 0) {
-#pragma unroll
-      for (int h = 0; h < NREP; ++h) {
-        sm.m[wave][h] = m_run[h];
-        sm.l[wave][h] = l_run[h];
-      }
-    }
-    lds_barrier();
-#pragma unroll
-    for (int h = 0; h < NREP; ++h) {
-      float mt = sm.m[0][h];
-#pragma unroll
-      for (int w = 1; w < NW; ++w) mt = fmaxf(mt, sm.m[w][h]);
-      const float sc = m_run[h] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run[h] - mt);
-#pragma unroll
-      for (int e = 0; e < DPL; ++e) sm.red[wave][h][lane + 64 * e] = o_run[h][e] * sc;
-    }
-    float mls = 0.f, lls = 0.f;  // run statistics of head tid (m in natural-log units)
-    if (tid < NREP) {
-      const int h = tid;
-      float mt = sm.m[0][h];
-#pragma unroll
-      for (int w = 1; w < NW; ++w) mt = fmaxf(mt, sm.m[w][h]);
-#pragma unroll
-      for (int w = 0; w < NW; ++w) lls += sm.m[w][h] == -INFINITY ? 0.f : sm.l[w][h] * __builtin_amdgcn_exp2f(sm.m[w][h] - mt);
-      mls = mt * 0.69314718055994531f;
-    }
-    // every read of the statistics is done: a wave that runs ahead into its
-    // next run may overwrite them after this barrier
-    lds_barrier();
-    float* dst = a.part + (int64_t(slot) * rows + int64_t(bh) * NREP) * D;
-#pragma unroll
-    for (int r = tid; r < NREP * D; r += NT) {
-      const int h = r / D, dd = r % D;
-      float val = 0.f;
-#pragma unroll
-      for (int w = 0; w < NW; ++w) val += sm.red[w][h][dd];
-      dst[r] = val;
-    }
-    if (tid < NREP) {
-      float* ml = a.ml + (int64_t(slot) * rows + int64_t(bh) * NREP + tid) * 2;
-      ml[0] = mls;
-      ml[1] = lls;
-    }
-  };
-
-  // the lane's tokens' slots in the attn.V operand records and their code biases
-  int tk[FBPW], thi[FBPW];
-  float tb[FBPW];
-#pragma unroll
-  for (int j = 0; j < FBPW; ++j) plan_inv<BITS>((j * TOKEN_BLOCK + lane) % G, tk[j], thi[j], tb[j]);
-
-  Run run = run_at(i0);
-  int rs2 = i0 + run.nsplit;                // first split of the next run (i1: none)
-  Run run2 = run_at(min(rs2, i1 - 1));
-  int cur = wave < run.nb ? wave : -1;           // the wave's current block (index in the run)
-  int nxt = NW + wave < run.nb ? NW + wave : -1;  // the block whose data it loads next
-  QRegs qq;
-  VRegs v;
-  // ---- one wave block: K in kc and V in v (loaded during the previous
-  // block); loads the next block's K into kn at the top and its V into v
-  // after attn.V; the wave's last block of a run ends in the run merge ----
-  auto step = [&](KRegs& kc, KRegs& kn) -> bool {
-    const bool have = cur >= 0;
-    const bool ends = nxt < 0;  // the wave's last block of the run
-    const bool nrun = rs2 < i1;
-    // the block loaded during this one: nxt, or the wave's first block of the next run
-    const int lbh = ends ? run2.bh : run.bh;
-    const int lblk = ends ? block_of(run2, wave) : block_of(run, max(nxt, 0));
-    const bool lreal = ends ? nrun && wave < run2.nb : true;
-    load_k(lbh, lblk, lreal, kn);  // in flight through this whole block
-    int nn = 0;
-    if (!ends && lane == 0) nn = atomicAdd(&sm.next_block, 1);
-    if (have) {
-      const int wt0 = block_of(run, cur) * WTOK;  // first token of the block
-      // ---- QK^T over the wave's tokens, from registers ----
-      float acc[FBPW][NREP];
-#pragma unroll
-      for (int j = 0; j < FBPW; ++j)
-#pragma unroll
-        for (int h = 0; h < NREP; ++h) acc[j][h] = 0.f;
-#pragma unroll
-      for (int g = 0; g < NG; ++g) {
-        if (a.ksym) {
-#pragma unroll
-          for (int j = 0; j < FBPW; ++j) to_offset_binary<BITS>(kc.w[g][j], W);
-        }
-        float d[FBPW][NREP];
-        qk_group_dot_biased<BITS, G, NREP, FBPW>(kc.w[g], &sm.qrec[g][0], hl, qsplit, pr, d);
-#pragma unroll
-        for (int j = 0; j < FBPW; ++j) {
-          float s, z;
-          meta_sz<BITS>(kc.m[g][j], lane, a.ksym, s, z);
-#pragma unroll
-          for (int h = 0; h < NREP; ++h) {
-            const float qs = __uint_as_float(sm.qrec[g][QOS + h]);
-            acc[j][h] = fmaf(s, d[j][h], fmaf(z, qs, acc[j][h]));
-          }
-        }
-      }
-
-      // ---- softmax against the running max (log2 domain); fp16 p straight
-      // into the V records ----
-      auto& vrec = sm.vrec[wave];
-      float mw[NREP], ps[VPW][NREP], alpha[NREP];
-#pragma unroll
-      for (int j = 0; j < FBPW; ++j) {
-        const bool live = wt0 + j * TOKEN_BLOCK + lane < a.T;
-#pragma unroll
-        for (int h = 0; h < NREP; ++h) acc[j][h] = live ? acc[j][h] * a.scale_log2 : -INFINITY;
-      }
-#pragma unroll
-      for (int h = 0; h < NREP; ++h) {
-        mw[h] = acc[0][h];
-#pragma unroll
-        for (int j = 1; j < FBPW; ++j) mw[h] = fmaxf(mw[h], acc[j][h]);
-      }
-      wave_max_dpp(mw);
-#pragma unroll
-      for (int h = 0; h < NREP; ++h) {
-        const float mn = fmaxf(m_run[h], mw[h]);
-        alpha[h] = m_run[h] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run[h] - mn);
-        m_run[h] = mn;
-      }
-      // x[h]: p; x[NREP + h]: -p * bias (the attn.V accumulators' seed)
-      float x[2 * NREP], pb[VPW][NREP];
-#pragma unroll
-      for (int h = 0; h < NREP; ++h) {
-        x[h] = 0.f;
-        x[NREP + h] = 0.f;
-#pragma unroll
-        for (int j = 0; j < FBPW; ++j) {
-          const float p = acc[j][h] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(acc[j][h] - m_run[h]);
-          const uint16_t p16 = __half_as_ushort(__float2half_rn(p));
-          const int tl = j * TOKEN_BLOCK + lane;  // token within the wave
-          reinterpret_cast<uint16_t*>(&vrec[tl / G][h * NP + tk[j]])[thi[j]] = p16;
-          const float pf = h2f(p16);  // the zero-point term uses the fp16 p the matrix cores see
-          x[h] += pf;
-          x[NREP + h] = fmaf(-pf, tb[j], x[NREP + h]);
-        }
-      }
-      // per (V group, head): sums over the group's tokens
-      if constexpr (G == 32) {  // two groups per wave: lanes 0-31 and 32-63
-        sum_step<0xb1>(x);
-        sum_step<0x4e>(x);
-        sum_step<0x141>(x);
-        sum_step<0x140>(x);
-#pragma unroll
-        for (int h = 0; h < 2 * NREP; ++h) {
-          x[h] += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x[h]), 0x142, 0xa,
-                                                                        0xf, false));
-          const float s0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x[h]), 31));
-          const float s1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x[h]), 63));
-          if (h < NREP) { ps[0][h] = s0; ps[1][h] = s1; }
-          else { pb[0][h - NREP] = s0; pb[1][h - NREP] = s1; }
-        }
-      } else {
-        static_assert(VPW == 1, "one V group per wave for G >= 64");
-        wave_sum_dpp(x);
-#pragma unroll
-        for (int h = 0; h < NREP; ++h) {
-          ps[0][h] = x[h];
-          pb[0][h] = x[NREP + h];
-        }
-      }
-#pragma unroll
-      for (int h = 0; h < NREP; ++h) {
-        float lsum = 0.f;
-#pragma unroll
-        for (int u = 0; u < VPW; ++u) lsum += ps[u][h];
-        l_run[h] = fmaf(l_run[h], alpha[h], lsum);
-#pragma unroll
-        for (int e = 0; e < DPL; ++e) o_run[h][e] *= alpha[h];
-      }
-      wave_lds_sync();
-
-      // ---- attn.V over the wave's V groups, from registers ----
-      const int vcnt = max(0, min(VPW, (a.T - wt0) / G));  // the wave's V groups inside the range
-#pragma unroll
-      for (int u = 0; u < VPW; ++u) {
-        if (u < vcnt) {
-          if (a.vsym) {
-#pragma unroll
-            for (int e = 0; e < DPL; ++e) to_offset_binary<BITS>(v.w[u][e], W);
-          }
-          f4_t init[NQ], dv[DPL][NQ];
-#pragma unroll
-          for (int q = 0; q < NQ; ++q)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) init[q][i] = 4 * q + i < NREP ? pb[u][4 * q + i] : 0.f;
-          group_mfma_biased<BITS, G, NREP, DPL>(v.w[u], &vrec[u][0], hl, pr, init, dv);
-#pragma unroll
-          for (int e = 0; e < DPL; ++e) {
-            float s, z;
-            meta_sz<BITS>(v.m[u][e], lane, a.vsym, s, z);
-#pragma unroll
-            for (int h = 0; h < NREP; ++h)
-              o_run[h][e] = fmaf(s, dv[e][h / 4][h % 4], fmaf(z, ps[u][h], o_run[h][e]));
-          }
-        }
-      }
-    }
-    load_v(lbh, lblk, lreal, v);  // streams in during the next block's QK^T
-    if (!ends) {
-      nn = __builtin_amdgcn_readlane(nn, 0);
-      cur = nxt;
-      nxt = nn < run.nb ? nn : -1;
-      return true;
-    }
-    // ---- run end: merge the waves; empty statistics in the slots past the
-    // (batch, KV head)'s partials that lie among this run's splits (the
-    // combine skips them) ----
-    int slot, nr;
-    run_slots(run, slot, nr);
-    flush_run(run.bh, slot);
-    if (wave == 0 && lane < NREP) {
-      for (int sp = max(run.split0, nr); sp < run.split0 + run.nsplit; ++sp) {
-        float* ml = a.ml + (int64_t(sp) * rows + int64_t(run.bh) * NREP + lane) * 2;
-        ml[0] = -INFINITY;
-        ml[1] = 0.f;
-      }
-    }
-    if (!nrun) return false;
-    reset_run();
-    run = run2;
-    rs2 += run.nsplit;
-    run2 = run_at(min(rs2, i1 - 1));
-    build_records(qq);  // the new (batch, KV head)'s query records
-    if (tid == 0) sm.next_block = 2 * NW;
-    lds_barrier();
-    load_q(run2.bh, rs2 < i1, qq);  // the run after: in flight through this one
-    cur = wave < run.nb ? wave : -1;
-    nxt = NW + wave < run.nb ? NW + wave : -1;
-    return true;
-  };
-
-  KRegs ka, kb;
-  reset_run();
-  load_k(run.bh, block_of(run, max(cur, 0)), cur >= 0, ka);
-  load_v(run.bh, block_of(run, max(cur, 0)), cur >= 0, v);
-  load_q(run.bh, true, qq);
-  build_records(qq);
-  if (tid == 0) sm.next_block = 2 * NW;
-  lds_barrier();
-  load_q(run2.bh, rs2 < i1, qq);
-  while (step(ka, kb) && step(kb, ka)) {
-  }
-}
-
 }  // namespace
 
 namespace iq::detail {
@@ -625,7 +28,7 @@ int flash_fused_launch(const void* q, int64_t sq_b, int64_t sq_h, const void* no
                        const FusedStore& v, int B, int Hq, int Hkv, int T, int D, float scale, float* ml,
                        float* part, hipStream_t stream) {
   if (B == 0 || T == 0) return IQ_OK;
-  if (k.bits != v.bits || k.group != v.group) return IQ_ERR_GROUP;
+  if (k.group != v.group) return IQ_ERR_GROUP;
   if (T % k.group || FSPLIT != flash_split_tokens()) return IQ_ERR_GROUP;
   if (k.t0 % TOKEN_BLOCK || v.t0 % v.group) return IQ_ERR_ALIGN;
   if (!flash_fused_supported(q, sq_b, sq_h, norm, k, v, Hq, Hkv, D)) return IQ_ERR_SHAPE;
@@ -647,22 +50,12 @@ int flash_fused_launch(const void* q, int64_t sq_b, int64_t sq_h, const void* no
   a.norm_bytes = norm ? uint32_t(D * 2) : 0u;
   a.scale_log2 = scale * 1.4426950408889634f;
   a.ml = ml; a.part = part;
-  return dispatch_shape(k.bits, k.group, D, Hq / Hkv, 0, [&]<int BITS, int G, int DD, int R, bool S>() {
-    auto* kern = norm ? flash_fused_kernel<BITS, G, DD, R, true> : flash_fused_kernel<BITS, G, DD, R, false>;
-    const int nt = norm ? FusedShape<G, R, true>::NT : FusedShape<G, R, false>::NT;
-    // persistent grid: one workgroup per CU (as many as fit at once)
-    static int per_cu[2] = {0, 0};
-    int& pc = per_cu[norm ? 1 : 0];
-    if (pc == 0) {
-      int n = 0;
-      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, nt, 0) != hipSuccess || n <= 0) n = 1;
-      pc = n;
-    }
-    const int per_cu_n = pc;
-    const int grid = int(std::min<int64_t>(a.nitems, int64_t(per_cu_n) * num_cus()));
-    kern<<<dim3(grid), nt, 0, stream>>>(a);
-    return launch_status();
-  });
+  switch (k.bits) {
+    case 2: return flash_fused_launch_k2(a, v.bits, k.group, D, Hq / Hkv, norm != nullptr, stream);
+    case 3: return flash_fused_launch_k3(a, v.bits, k.group, D, Hq / Hkv, norm != nullptr, stream);
+    case 4: return flash_fused_launch_k4(a, v.bits, k.group, D, Hq / Hkv, norm != nullptr, stream);
+    default: return IQ_ERR_BITS;
+  }
 }
 
 }  // namespace iq::detail

@@ -1,0 +1,11 @@
+// Instantiations of the fused flash-decoding kernel for 2-bit K (every V bit
+// width, group size, head_dim and query heads per KV head).
+#include "iq_flash.h"
+
+namespace iq::detail {
+
+int flash_fused_launch_k2(const FusedArgs& a, int vbits, int group, int D, int nrep, bool norm, hipStream_t stream) {
+  return fused_launch_kb<2>(a, vbits, group, D, nrep, norm, stream);
+}
+
+}  // namespace iq::detail

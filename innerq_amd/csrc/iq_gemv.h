@@ -359,9 +359,9 @@ int av_main_launch(const uint32_t* rec, const uint32_t* v_codes, const uint16_t*
                    hipStream_t stream);
 int av_combine_launch(const float* part, int nsplit, int B, int Hq, int D, const OutPair& o, int accumulate,
                       hipStream_t stream);
-// The fused flash-decoding split kernel (QK^T + split softmax + attn.V in one
-// workgroup) for K and V stores of the same bit width and group size; writes
-// the same split statistics and partials as the unfused path.
+// The fused flash-decoding kernel (QK^T + softmax + attn.V, persistent) for
+// K and V stores of the same group size (any bit widths); writes split
+// statistics and partials that the same combine merges as the unfused path's.
 struct FusedStore {
   const uint32_t* codes;
   const uint16_t* meta;
@@ -375,6 +375,30 @@ bool flash_fused_supported(const void* q, int64_t sq_b, int64_t sq_h, const void
 int flash_fused_launch(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, const FusedStore& k,
                        const FusedStore& v, int B, int Hq, int Hkv, int T, int D, float scale, float* ml,
                        float* part, hipStream_t stream);
+// the fused kernel's arguments (filled by flash_fused_launch)
+struct FusedArgs {
+  const uint16_t* q;
+  int64_t sqb, sqh;
+  const uint16_t* norm;  // [B*Hkv][D] or null
+  const uint32_t* kc;
+  const uint16_t* km;
+  int64_t k_cap_blocks;
+  int kblk0, ksym;
+  const uint32_t* vc;
+  const uint16_t* vm;
+  int64_t v_cap_groups;
+  int vg0, vsym;
+  int Hkv, T;          // T: tokens of the range, a multiple of G
+  int nsplit, nitems;  // splits per (batch, KV head); nsplit * B * Hkv
+  uint32_t k_code_bytes, k_meta_bytes, v_code_bytes, v_meta_bytes, q_bytes, norm_bytes;
+  float scale_log2;    // scale * log2(e)
+  float* ml;           // [nsplit][B*Hq][2]
+  float* part;         // [nsplit][B*Hq][D]
+};
+// its launch per K bit width (iq_flash_k{2,3,4}.hip)
+int flash_fused_launch_k2(const FusedArgs& a, int vbits, int group, int D, int nrep, bool norm, hipStream_t stream);
+int flash_fused_launch_k3(const FusedArgs& a, int vbits, int group, int D, int nrep, bool norm, hipStream_t stream);
+int flash_fused_launch_k4(const FusedArgs& a, int vbits, int group, int D, int nrep, bool norm, hipStream_t stream);
 size_t qk_record_bytes(int B, int Hq, int D);
 size_t av_record_bytes(int B, int Hq, int T, int group);
 size_t av_part_bytes(int B, int Hq, int T, int D, int group);

@@ -380,7 +380,10 @@ def test_decode_attention_fused_and_dense_ranges(kseg, vseg):
 
 @pytest.mark.parametrize("kfmt,vfmt", [((3, 32, "symmetric"), (3, 32, "symmetric")),
                                        ((2, 64, "asymmetric"), (4, 64, "symmetric")),
-                                       ((4, 128, "asymmetric"), (2, 128, "asymmetric"))])
+                                       ((4, 128, "asymmetric"), (2, 128, "asymmetric")),
+                                       # different group sizes: the unfused QK^T / attn.V kernels
+                                       ((4, 32, "asymmetric"), (4, 64, "symmetric")),
+                                       ((2, 128, "symmetric"), (3, 32, "asymmetric"))])
 def test_decode_attention_formats_and_norm(kfmt, vfmt):
     G = max(kfmt[1], vfmt[1])
     kseg = (32, 64 * 24, 96)
@@ -431,33 +434,41 @@ def test_decode_attention_dense_window_unaligned(nrep, D, R):
 # K and V of one bit width and group size take the fused split kernel (one
 # workgroup runs QK^T, the split softmax and attn.V); sym/asym may differ.
 @pytest.mark.parametrize("fmt,nrep,D", [
-    ((2, 32, "asymmetric", "asymmetric"), 4, 128),
-    ((2, 64, "symmetric", "asymmetric"), 8, 128),
-    ((3, 64, "asymmetric", "symmetric"), 2, 64),
-    ((3, 128, "asymmetric", "asymmetric"), 1, 128),
-    ((4, 64, "asymmetric", "symmetric"), 4, 64),
-    ((4, 128, "symmetric", "symmetric"), 4, 128),
+    ((2, 2, 32, "asymmetric", "asymmetric"), 4, 128),
+    ((2, 2, 64, "symmetric", "asymmetric"), 8, 128),
+    ((3, 3, 64, "asymmetric", "symmetric"), 2, 64),
+    ((3, 3, 128, "asymmetric", "asymmetric"), 1, 128),
+    ((4, 4, 64, "asymmetric", "symmetric"), 4, 64),
+    ((4, 4, 128, "symmetric", "symmetric"), 4, 128),
+    # K and V of different bit widths (one group size)
+    ((2, 4, 32, "asymmetric", "asymmetric"), 4, 128),
+    ((4, 2, 32, "symmetric", "asymmetric"), 8, 128),
+    ((3, 4, 64, "asymmetric", "symmetric"), 4, 64),
+    ((2, 3, 128, "symmetric", "symmetric"), 2, 128),
+    ((4, 3, 32, "asymmetric", "asymmetric"), 1, 64),
 ])
 def test_decode_attention_fused_formats(fmt, nrep, D):
-    bits, G, km, vm = fmt
+    kbits, vbits, G, km, vm = fmt
     kseg = (16, 64 * 21, 80)
     vq = (64 * 21 + 80) // G * G - G
     vseg = (16, vq, 64 * 21 + 80 - vq)
-    err = _decode_case(2, 2, nrep, D, kseg, vseg, (bits, G, km), (bits, G, vm), seed=bits * G + nrep, norm=True)
+    err = _decode_case(2, 2, nrep, D, kseg, vseg, (kbits, G, km), (vbits, G, vm), seed=kbits * G + nrep + vbits,
+                       norm=True)
     assert err < TOL
 
 
 @pytest.mark.parametrize("fused", [True, False])
 def test_decode_stages_equal_decode_attention(fused):
     """iq_decode_attention_splits + _combine give decode_attention's output bit for bit
-    (fused split kernel: K and V of one format; unfused: different bit widths)."""
+    (fused kernel: K and V of one group size, here of different bit widths;
+    unfused: different group sizes)."""
     B, Hkv, nrep, D = 2, 2, 4, 128
-    kb, vb = (4, 4) if fused else (2, 4)
+    kg, vg = (32, 32) if fused else (32, 64)
     T = 64 * 12 + 40
     kx = synth.kv_tensor(B, Hkv, T, D, seed=61)
     vx = synth.kv_tensor(B, Hkv, T, D, seed=62)
-    kst = ops.PackedStore("channel", B, Hkv, D, 32, kb, "asymmetric", DEV)
-    vst = ops.PackedStore("token", B, Hkv, D, 32, vb, "asymmetric", DEV)
+    kst = ops.PackedStore("channel", B, Hkv, D, kg, 2, "asymmetric", DEV)
+    vst = ops.PackedStore("token", B, Hkv, D, vg, 4, "asymmetric", DEV)
     kst.append(f16t(kx[:, :, :768]))
     vst.append(f16t(vx[:, :, :768]))
     kr, vr = f16t(kx[:, :, 768:]), f16t(vx[:, :, 768:])
