@@ -14,7 +14,14 @@
 // The four waves' partial sums are reduced in LDS in a fixed order, each
 // workgroup writes one fp32 partial per split, and a second kernel sums the
 // splits in split order: no atomics, deterministic results.
-#include "iq_gemv.h"
+//
+// iq_av_gemv takes this path only where the persistent kernel cannot run (a
+// slice beyond 32-bit buffer offsets).  Its main path is the fused decode
+// kernel in attn.V-only mode (iq_flash.h): one workgroup per CU streams V
+// and the probabilities of its share of the token range (read straight into
+// the operand records, no record kernel), one partial per run, then the same
+// combine over each (batch, KV head)'s run slots.
+#include "iq_flash.h"
 
 using namespace iq;
 
@@ -156,13 +163,20 @@ __global__ __launch_bounds__(WG) void av_kernel(AVArgs a) {
 }
 
 __global__ __launch_bounds__(256) void av_combine_kernel(const float* __restrict__ part, int nsplit, int Hq, int D,
-                                                         int64_t rows, detail::OutPair o, int accumulate) {
+                                                         int64_t rows, detail::OutPair o, int accumulate, int grid,
+                                                         int nrep) {
   const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= rows * D) return;
   const int64_t bq = i / D;
   const int d = int(i % D);
+  int n = nsplit;
+  if (grid > 0) {  // the runs of the (batch, KV head) in the persistent kernel's shares
+    const int64_t bh = bq / nrep, nitems = rows / nrep * nsplit;
+    auto share_of = [&](int64_t s) { return (s + 1) * grid / nitems + ((s + 1) * grid % nitems ? 1 : 0) - 1; };
+    n = int(share_of((bh + 1) * nsplit - 1) - share_of(bh * nsplit) + 1);
+  }
   float v = 0.f;
-  for (int s = 0; s < nsplit; ++s) v += part[(int64_t(s) * rows + bq) * D + d];
+  for (int s = 0; s < n; ++s) v += part[(int64_t(s) * rows + bq) * D + d];
   const int64_t off32 = (bq / Hq) * o.s32b + (bq % Hq) * o.s32h + d;
   if (accumulate) v += o.out32[off32];
   if (o.out32) o.out32[off32] = v;
@@ -210,10 +224,11 @@ size_t av_record_bytes(int B, int Hq, int T, int group) {
 size_t av_part_bytes(int B, int Hq, int T, int D, int group) {
   // Bound on the split count of any range of at most T tokens and any Hkv:
   // groups_per_wg() gives gpw >= ceil(ng / S) with S <= 4*CUs/B (Hkv = 1), and
-  // gpw >= min(ng, 8), so nsplit <= min(S, ceil(ng / 8)) (and >= 1).
+  // gpw >= min(ng, 8), so nsplit <= min(S, ceil(ng / 8)) (and >= 1).  The
+  // persistent kernel writes at most one slot per FSPLIT tokens.
   const int64_t ng = T / group;
   const int64_t s_max = std::max<int64_t>(1, int64_t(num_cus()) * 4 / std::max(B, 1));
-  const int64_t bound = std::max<int64_t>(1, std::min<int64_t>(s_max, ceil_div(ng, 2 * NWAVES)));
+  const int64_t bound = std::max<int64_t>({1, std::min<int64_t>(s_max, ceil_div(ng, 2 * NWAVES)), ceil_div(T, FSPLIT)});
   return ((size_t(bound) * B * Hq * D * 4) + 255) & ~size_t(255);
 }
 
@@ -257,12 +272,50 @@ int av_flash_launch(const uint32_t* rec, const uint32_t* v_codes, const uint16_t
 }
 
 int av_combine_launch(const float* part, int nsplit, int B, int Hq, int D, const OutPair& o, int accumulate,
-                      hipStream_t stream) {
+                      hipStream_t stream, int grid, int nrep) {
   const int64_t rows = int64_t(B) * Hq;
   if (rows == 0) return IQ_OK;
   av_combine_kernel<<<dim3(unsigned(ceil_div(rows * D, 256))), 256, 0, stream>>>(part, nsplit, Hq, D, rows, o,
-                                                                                accumulate);
+                                                                                accumulate, grid, nrep);
   return launch_status();
+}
+
+// attn.V over the persistent fused kernel in attn.V-only mode; *grid = its
+// workgroup count (0: the slices exceed its 32-bit buffer offsets, nothing
+// launched)
+int av_fused_launch(const void* p, int64_t sp_b, int64_t sp_h, const uint32_t* v_codes, const uint16_t* v_meta,
+                    int64_t t_cap, int B, int Hq, int Hkv, int t0, int T, int D, int group, int bits, int mode,
+                    float* part, int* grid, hipStream_t stream) {
+  *grid = 0;
+  const int nrep = Hq / Hkv;
+  const int64_t lim = int64_t(1) << 31;
+  if (sp_h < 0 || (int64_t(nrep - 1) * sp_h + T) * 2 >= lim || t_cap * D * bits / 8 >= lim ||
+      t_cap * D * 4 / group >= lim)
+    return IQ_OK;
+  FusedArgs a{};
+  a.q = (const uint16_t*)p; a.sqb = sp_b; a.sqh = sp_h;
+  a.vc = v_codes; a.vm = v_meta; a.v_cap_groups = t_cap / group; a.vg0 = t0 / group;
+  a.vsym = mode == IQ_MODE_SYM;
+  a.Hkv = Hkv; a.T = T;
+  a.nsplit = int(ceil_div(T, FSPLIT));
+  a.nitems = a.nsplit * B * Hkv;
+  a.v_code_bytes = uint32_t(int64_t(T) * D * bits / 8);
+  a.v_meta_bytes = uint32_t(int64_t(T / group) * D * (a.vsym ? 2 : 4));
+  a.q_bytes = uint32_t((int64_t(nrep - 1) * sp_h + T) * 2);
+  a.part = part;
+  return dispatch_shape(bits, group, D, nrep, 0, [&]<int VB, int G, int DD, int R, bool S>() {
+    auto* kern = flash_fused_kernel<VB, VB, G, DD, R, false, true>;
+    const int nt = FusedShape<G, R, false>::NT;
+    static int per_cu = 0;  // workgroups per CU at once
+    if (per_cu == 0) {
+      int n = 0;
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, nt, 0) != hipSuccess || n <= 0) n = 1;
+      per_cu = n;
+    }
+    *grid = int(std::min<int64_t>(a.nitems, int64_t(per_cu) * num_cus()));
+    kern<<<dim3(*grid), nt, 0, stream>>>(a);
+    return launch_status();
+  });
 }
 
 }  // namespace iq::detail
@@ -291,6 +344,12 @@ int iq_av_gemv(const void* p, int64_t sp_b, int64_t sp_h, const uint32_t* v_code
   IQ_CHECK(aligned(workspace, 16), IQ_ERR_ALIGN);
   uint32_t* rec = (uint32_t*)workspace;
   float* part = (float*)((char*)workspace + rb);
+  int grid = 0;
+  if (int e = detail::av_fused_launch(p, sp_b, sp_h, v_codes, v_meta, t_cap, B, Hq, Hkv, t0, T, D, group, bits, mode,
+                                      part, &grid, st))
+    return e;
+  if (grid > 0)
+    return detail::av_combine_launch(part, int(ceil_div(T, FSPLIT)), B, Hq, D, o, accumulate, st, grid, Hq / Hkv);
   if (int e = detail::av_record_launch(p, sp_b, sp_h, B, Hq, Hkv, T, group, bits, rec, st)) return e;
   if (int e = detail::av_main_launch(rec, v_codes, v_meta, t_cap, B, Hq, Hkv, t0, T, D, group, bits, mode, part, st))
     return e;

@@ -43,6 +43,7 @@
 // n_rep, hi/lo query rows) only.
 #pragma once
 #include <algorithm>
+#include <type_traits>
 
 #include "iq_gemv.h"
 
@@ -186,7 +187,12 @@ __device__ __forceinline__ float seg_sum(float v) {
   return v;
 }
 
-template <int KB, int VB, int G, int D, int NREP, bool QS>
+// AVO (attn.V only, the standalone GEMV of iq_av.hip): no K, no softmax; the
+// fp16 probabilities p [B, Hq, T] come in through the q fields of the
+// arguments (q, sqb, sqh, q_bytes), are loaded one block ahead in place of K
+// and written into the attn.V operand records as they are; the runs' partials
+// are plain sums (no statistics are written).
+template <int KB, int VB, int G, int D, int NREP, bool QS, bool AVO = false>
 __global__ __launch_bounds__((FusedShape<G, NREP, QS>::NT), (fused_waves_per_simd<G, NREP, QS>())) void flash_fused_kernel(FusedArgs a) {
   using FS = FusedShape<G, NREP, QS>;
   constexpr int NW = FS::NW, NT = FS::NT, WTOK = FS::WTOK, FBPW = FS::FBPW, VPW = FS::VPW;
@@ -214,6 +220,8 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS>::NT), (fused_waves_per_sim
   struct KRegs { uint32_t w[NG][FBPW][KW]; uint32_t m[NG][FBPW]; };
   struct VRegs { uint32_t w[VPW][DPL][VW]; uint32_t m[VPW][DPL]; };
   struct QRegs { uint16_t a[NPT], c[NPT], na[NPT], nc[NPT]; };
+  struct PRegs { uint32_t p[FBPW][NREP]; };  // attn.V only: a block's fp16 probabilities
+  using XRegs = std::conditional_t<AVO, PRegs, KRegs>;  // what is loaded one block ahead
 
   // ---- loads of wave block blk (tokens [blk*WTOK, +WTOK) of the range) of
   // (batch, KV head) bh into registers; real = false: zero fill ----
@@ -244,6 +252,20 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS>::NT), (fused_waves_per_sim
         bload_words<VW>(rc, uint32_t(lane) * (VW * 4), c0 * (VW * 4), v.w[u][e]);
         v.m[u][e] = bload_u32(rm, vmv, c0 * vms);
       }
+  };
+  // attn.V only: the probabilities of block blk, lane = token, one row per head
+  auto load_p = [&](int bh, int blk, bool real, PRegs& pp) {
+    const int b = bh / a.Hkv, kvh = bh - b * a.Hkv;
+    const rsrc_t rp = make_rsrc(a.q + b * a.sqb + int64_t(kvh * NREP) * a.sqh, real ? a.q_bytes : 0u);
+#pragma unroll
+    for (int j = 0; j < FBPW; ++j)
+#pragma unroll
+      for (int h = 0; h < NREP; ++h)
+        pp.p[j][h] = bload_u16(rp, uint32_t(h * a.sqh + blk * WTOK + j * TOKEN_BLOCK + lane) * 2, 0);
+  };
+  auto load_x = [&](int bh, int blk, bool real, XRegs& x) {
+    if constexpr (AVO) load_p(bh, blk, real, x);
+    else load_k(bh, blk, real, x);
   };
   auto load_q = [&](int bh, bool real, QRegs& qq) {
     const int b = bh / a.Hkv, kvh = bh - b * a.Hkv;
@@ -357,7 +379,7 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS>::NT), (fused_waves_per_sim
       float mt = sm.m[0][h];
 #pragma unroll
       for (int w = 1; w < NW; ++w) mt = fmaxf(mt, sm.m[w][h]);
-      const float sc = m_run[h] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run[h] - mt);
+      const float sc = AVO ? 1.f : m_run[h] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run[h] - mt);
 #pragma unroll
       for (int e = 0; e < DPL; ++e) sm.red[wave][h][lane + 64 * e] = o_run[h][e] * sc;
     }
@@ -383,7 +405,7 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS>::NT), (fused_waves_per_sim
       for (int w = 0; w < NW; ++w) val += sm.red[w][h][dd];
       dst[r] = val;
     }
-    if (tid < NREP) {
+    if (!AVO && tid < NREP) {
       float* ml = a.ml + (int64_t(slot) * rows + int64_t(bh) * NREP + tid) * 2;
       ml[0] = mls;
       ml[1] = lls;
@@ -406,7 +428,7 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS>::NT), (fused_waves_per_sim
   // ---- one wave block: K in kc and V in v (loaded during the previous
   // block); loads the next block's K into kn at the top and its V into v
   // after attn.V; the wave's last block of a run ends in the run merge ----
-  auto step = [&](KRegs& kc, KRegs& kn) -> bool {
+  auto step = [&](XRegs& kc, XRegs& kn) -> bool {
     const bool have = cur >= 0;
     const bool ends = nxt < 0;  // the wave's last block of the run
     const bool nrun = rs2 < i1;
@@ -414,7 +436,7 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS>::NT), (fused_waves_per_sim
     const int lbh = ends ? run2.bh : run.bh;
     const int lblk = ends ? block_of(run2, wave) : block_of(run, max(nxt, 0));
     const bool lreal = ends ? nrun && wave < run2.nb : true;
-    load_k(lbh, lblk, lreal, kn);  // in flight through this whole block
+    load_x(lbh, lblk, lreal, kn);  // in flight through this whole block
     int nn = 0;
     if (!ends && lane == 0) nn = atomicAdd(&sm.next_block, 1);
     if (have) {
@@ -425,22 +447,24 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS>::NT), (fused_waves_per_sim
       for (int j = 0; j < FBPW; ++j)
 #pragma unroll
         for (int h = 0; h < NREP; ++h) acc[j][h] = 0.f;
+      if constexpr (!AVO) {
 #pragma unroll
-      for (int g = 0; g < NG; ++g) {
-        if (a.ksym) {
+        for (int g = 0; g < NG; ++g) {
+          if (a.ksym) {
 #pragma unroll
-          for (int j = 0; j < FBPW; ++j) to_offset_binary<KB>(kc.w[g][j], KW);
-        }
-        float d[FBPW][NREP];
-        qk_group_dot_biased<KB, G, NREP, FBPW>(kc.w[g], &sm.qrec[g][0], hl, qsplit, prk, d);
+            for (int j = 0; j < FBPW; ++j) to_offset_binary<KB>(kc.w[g][j], KW);
+          }
+          float d[FBPW][NREP];
+          qk_group_dot_biased<KB, G, NREP, FBPW>(kc.w[g], &sm.qrec[g][0], hl, qsplit, prk, d);
 #pragma unroll
-        for (int j = 0; j < FBPW; ++j) {
-          float s, z;
-          meta_sz<KB>(kc.m[g][j], lane, a.ksym, s, z);
+          for (int j = 0; j < FBPW; ++j) {
+            float s, z;
+            meta_sz<KB>(kc.m[g][j], lane, a.ksym, s, z);
 #pragma unroll
-          for (int h = 0; h < NREP; ++h) {
-            const float qs = __uint_as_float(sm.qrec[g][QOS + h]);
-            acc[j][h] = fmaf(s, d[j][h], fmaf(z, qs, acc[j][h]));
+            for (int h = 0; h < NREP; ++h) {
+              const float qs = __uint_as_float(sm.qrec[g][QOS + h]);
+              acc[j][h] = fmaf(s, d[j][h], fmaf(z, qs, acc[j][h]));
+            }
           }
         }
       }
@@ -449,24 +473,26 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS>::NT), (fused_waves_per_sim
       // into the V records ----
       auto& vrec = sm.vrec[wave];
       float mw[NREP], ps[VPW][NREP], alpha[NREP];
+      if constexpr (!AVO) {
 #pragma unroll
-      for (int j = 0; j < FBPW; ++j) {
-        const bool live = wt0 + j * TOKEN_BLOCK + lane < a.T;
+        for (int j = 0; j < FBPW; ++j) {
+          const bool live = wt0 + j * TOKEN_BLOCK + lane < a.T;
 #pragma unroll
-        for (int h = 0; h < NREP; ++h) acc[j][h] = live ? acc[j][h] * a.scale_log2 : -INFINITY;
-      }
+          for (int h = 0; h < NREP; ++h) acc[j][h] = live ? acc[j][h] * a.scale_log2 : -INFINITY;
+        }
 #pragma unroll
-      for (int h = 0; h < NREP; ++h) {
-        mw[h] = acc[0][h];
+        for (int h = 0; h < NREP; ++h) {
+          mw[h] = acc[0][h];
 #pragma unroll
-        for (int j = 1; j < FBPW; ++j) mw[h] = fmaxf(mw[h], acc[j][h]);
-      }
-      wave_max_dpp(mw);
+          for (int j = 1; j < FBPW; ++j) mw[h] = fmaxf(mw[h], acc[j][h]);
+        }
+        wave_max_dpp(mw);
 #pragma unroll
-      for (int h = 0; h < NREP; ++h) {
-        const float mn = fmaxf(m_run[h], mw[h]);
-        alpha[h] = m_run[h] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run[h] - mn);
-        m_run[h] = mn;
+        for (int h = 0; h < NREP; ++h) {
+          const float mn = fmaxf(m_run[h], mw[h]);
+          alpha[h] = m_run[h] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run[h] - mn);
+          m_run[h] = mn;
+        }
       }
       // x[h]: p; x[NREP + h]: -p * bias (the attn.V accumulators' seed)
       float x[2 * NREP], pb[VPW][NREP];
@@ -476,8 +502,13 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS>::NT), (fused_waves_per_sim
         x[NREP + h] = 0.f;
 #pragma unroll
         for (int j = 0; j < FBPW; ++j) {
-          const float p = acc[j][h] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(acc[j][h] - m_run[h]);
-          const uint16_t p16 = __half_as_ushort(__float2half_rn(p));
+          uint16_t p16;
+          if constexpr (AVO) {
+            p16 = uint16_t(kc.p[j][h]);  // the given probability, as it is
+          } else {
+            const float p = acc[j][h] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(acc[j][h] - m_run[h]);
+            p16 = __half_as_ushort(__float2half_rn(p));
+          }
           const int tl = j * TOKEN_BLOCK + lane;  // token within the wave
           reinterpret_cast<uint16_t*>(&vrec[tl / G][h * NP + tk[j]])[thi[j]] = p16;
           const float pf = h2f(p16);  // the zero-point term uses the fp16 p the matrix cores see
@@ -509,14 +540,16 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS>::NT), (fused_waves_per_sim
           pb[0][h] = x[NREP + h];
         }
       }
+      if constexpr (!AVO) {
 #pragma unroll
-      for (int h = 0; h < NREP; ++h) {
-        float lsum = 0.f;
+        for (int h = 0; h < NREP; ++h) {
+          float lsum = 0.f;
 #pragma unroll
-        for (int u = 0; u < VPW; ++u) lsum += ps[u][h];
-        l_run[h] = fmaf(l_run[h], alpha[h], lsum);
+          for (int u = 0; u < VPW; ++u) lsum += ps[u][h];
+          l_run[h] = fmaf(l_run[h], alpha[h], lsum);
 #pragma unroll
-        for (int e = 0; e < DPL; ++e) o_run[h][e] *= alpha[h];
+          for (int e = 0; e < DPL; ++e) o_run[h][e] *= alpha[h];
+        }
       }
       wave_lds_sync();
 
@@ -559,7 +592,7 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS>::NT), (fused_waves_per_sim
     int slot, nr;
     run_slots(run, slot, nr);
     flush_run(run.bh, slot);
-    if (wave == 0 && lane < NREP) {
+    if (!AVO && wave == 0 && lane < NREP) {
       for (int sp = max(run.split0, nr); sp < run.split0 + run.nsplit; ++sp) {
         float* ml = a.ml + (int64_t(sp) * rows + int64_t(run.bh) * NREP + lane) * 2;
         ml[0] = -INFINITY;
@@ -571,24 +604,26 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS>::NT), (fused_waves_per_sim
     run = run2;
     rs2 += run.nsplit;
     run2 = run_at(min(rs2, i1 - 1));
-    build_records(qq);  // the new (batch, KV head)'s query records
+    if constexpr (!AVO) build_records(qq);  // the new (batch, KV head)'s query records
     if (tid == 0) sm.next_block = 2 * NW;
     lds_barrier();
-    load_q(run2.bh, rs2 < i1, qq);  // the run after: in flight through this one
+    if constexpr (!AVO) load_q(run2.bh, rs2 < i1, qq);  // the run after: in flight through this one
     cur = wave < run.nb ? wave : -1;
     nxt = NW + wave < run.nb ? NW + wave : -1;
     return true;
   };
 
-  KRegs ka, kb;
+  XRegs ka, kb;
   reset_run();
-  load_k(run.bh, block_of(run, max(cur, 0)), cur >= 0, ka);
+  load_x(run.bh, block_of(run, max(cur, 0)), cur >= 0, ka);
   load_v(run.bh, block_of(run, max(cur, 0)), cur >= 0, v);
-  load_q(run.bh, true, qq);
-  build_records(qq);
+  if constexpr (!AVO) {
+    load_q(run.bh, true, qq);
+    build_records(qq);
+  }
   if (tid == 0) sm.next_block = 2 * NW;
   lds_barrier();
-  load_q(run2.bh, rs2 < i1, qq);
+  if constexpr (!AVO) load_q(run2.bh, rs2 < i1, qq);
   while (step(ka, kb) && step(kb, ka)) {
   }
 }

@@ -357,8 +357,11 @@ int av_splits(int B, int Hkv, int T, int group);
 int av_main_launch(const uint32_t* rec, const uint32_t* v_codes, const uint16_t* v_meta, int64_t t_cap, int B,
                    int Hq, int Hkv, int t0, int T, int D, int group, int bits, int mode, float* part,
                    hipStream_t stream);
+// grid > 0: the partials of the persistent kernel's runs (slots [0, runs of
+// the (batch, KV head)) of nsplit per (batch, KV head), a grid of `grid`
+// workgroups); grid = 0: every one of the nsplit slots
 int av_combine_launch(const float* part, int nsplit, int B, int Hq, int D, const OutPair& o, int accumulate,
-                      hipStream_t stream);
+                      hipStream_t stream, int grid = 0, int nrep = 1);
 // The fused flash-decoding kernel (QK^T + softmax + attn.V, persistent) for
 // K and V stores of the same group size (any bit widths); writes split
 // statistics and partials that the same combine merges as the unfused path's.

@@ -266,6 +266,24 @@ def test_av_gemv_shapes_and_accumulate(nrep, D):
     assert A.rel_err(o16.cpu().numpy().astype(np.float64), ref) < 2e-3
 
 
+@pytest.mark.parametrize("bits,G,mode", [(2, 64, "asymmetric"), (4, 32, "symmetric")])
+def test_av_gemv_many_runs(bits, G, mode):
+    """A long range over many (batch, KV head)s: the persistent kernel's shares cut the
+    heads into several runs each, whose partials the combine sums.  Reference: fp32
+    p @ V over V unpacked by the library (unpack is bit-exact to the oracle elsewhere)."""
+    B, Hkv, nrep, D, T = 2, 4, 4, 128, 16384
+    gen = torch.Generator(device=DEV).manual_seed(bits * G)
+    x = torch.randn(B, Hkv, T, D, generator=gen, device=DEV).to(torch.float16)
+    st = ops.PackedStore("token", B, Hkv, D, G, bits, mode, DEV, t_cap=T)
+    st.append(x)
+    vd = ops.dequantize_dense(*ops.unpack_store(st), G, mode, "token")
+    p = torch.softmax(torch.randn(B, Hkv * nrep, T, generator=gen, device=DEV) * 2.0, dim=-1).to(torch.float16)
+    got = ops.av_gemv(p, st, out32=torch.empty(B, Hkv * nrep, D, device=DEV))
+    ref = torch.matmul(p.float().view(B, Hkv, nrep, T), vd).view(B, Hkv * nrep, D)
+    err = ((got - ref).abs().max() / ref.abs().max()).item()
+    assert err < TOL
+
+
 def test_av_gemv_linearity():
     """p -> p.V is linear: AV(p1 + p2) == AV(p1) + AV(p2) (size-independent property)"""
     B, Hkv, T, D, G = 1, 2, 4096, 128, 64
