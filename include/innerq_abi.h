@@ -29,8 +29,8 @@
  *     codes  uint32 [B, H, t_cap/G, D, G*bits/32]
  *     meta   uint16 [B, H, t_cap/G, D, M]
  *  Inside a group, code i occupies bits [bits*i, bits*i+bits) LSB first
- *  (speedtest/benchmark_quantization.cu:25-84); asym stores the code, sym the
- *  two's complement of sign*magnitude.
+ *  (speedtest/benchmark_quantization.cu:25-84); asym stores the code, sym
+ *  sign*magnitude + 2^(bits-1) (offset binary, benchmark_quantization.cu:128).
  */
 #ifndef INNERQ_ABI_H
 #define INNERQ_ABI_H

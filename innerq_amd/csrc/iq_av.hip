@@ -121,10 +121,6 @@ __global__ __launch_bounds__(WG) void av_kernel(AVArgs a) {
     for (int u = 0; u < NB; ++u) {
       if (i + u < cnt) {
         const cptr_u32 rec = recb + (wave + NWAVES * (i + u)) * RD;
-        if constexpr (SYM) {
-#pragma unroll
-          for (int e = 0; e < DPL; ++e) to_offset_binary<BITS>(cw[u][e], W);
-        }
         f4_t dv[DPL][(NREP + 3) / 4];
         group_mfma<BITS, G, NREP, DPL>(cw[u], a.rec + (int64_t(bh) * a.ngroups + gl0 + wave + NWAVES * (i + u)) * RD,
                                        lane & 3, pr, dv);

@@ -49,7 +49,7 @@ __device__ __forceinline__ uint32_t field(const uint32_t* w, int bits, int i) {
 
 __device__ __forceinline__ float deq(uint32_t f, int bits, int sym, const uint16_t* meta, int64_t unit) {
   if (sym) {
-    const int c = (f >> (bits - 1)) ? int(f) - (1 << bits) : int(f);
+    const int c = int(f) - (1 << (bits - 1));  // offset binary
     return __fmul_rn(float(c), h2f(meta[unit]));
   }
   const uint32_t sz = reinterpret_cast<const uint32_t*>(meta)[unit];

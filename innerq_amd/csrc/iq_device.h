@@ -4,7 +4,8 @@
 // code i sits at bits [b*i, b*i+b) of a little-endian bit string stored as
 // G*b/32 32-bit words, LSB first (the convention of the reference's speedtest
 // kernels, speedtest/benchmark_quantization.cu:25-84).  Asym codes are the
-// unsigned field; sym codes are the b-bit two's complement of sign*magnitude.
+// unsigned field; sym codes are offset binary, u = sign*magnitude + 2^(b-1)
+// (the speedtest's sym packing, benchmark_quantization.cu:128 and 161).
 //
 // In-register unpack ("pair plans").  A GEMV never converts codes one by one.
 // A window of the group's bit string (a word, a shifted word, or an alignbit
@@ -18,9 +19,9 @@
 // operands are integers below 2048).  The plans keep every field at p >= 10 -
 // b - 4 or so, i.e. bias / code unit <= 256 (4-bit), 64 (2-bit), 128 (3-bit):
 // the fp32 partial sums stay within ~2^8 of the result, a relative error of a
-// few 1e-6 per 128-code dot product.  Sym codes are turned into offset binary
-// with one XOR per word (u = signed + 2^(b-1)), so
-// sum(q*signed) = sum(q*u) - 2^(b-1)*sum(q), folded into the zero term.
+// few 1e-6 per 128-code dot product.  Sym codes are offset binary
+// (u = signed + 2^(b-1)), so sum(q*signed) = sum(q*u) - 2^(b-1)*sum(q),
+// folded into the zero term: sym and asym unpack alike.
 //
 // Plans (found by exhaustive search for the fewest windows under that bias
 // bound; S = window start bit, word-aligned windows are free):
@@ -50,21 +51,18 @@ template <> struct Plan<4> {
   static constexpr int S[NPAIR] = {-6, 0, 6, 6};
   static constexpr int A[NPAIR] = {0, 1, 2, 3};
   static constexpr int C[NPAIR] = {4, 5, 6, 7};
-  static constexpr uint32_t SIGN[WORDS] = {0x88888888u};
 };
 template <> struct Plan<2> {
   static constexpr int WORDS = 1, CODES = 16, NPAIR = 8;
   static constexpr int S[NPAIR] = {-6, -6, 0, 0, 0, 6, 6, 6};
   static constexpr int A[NPAIR] = {0, 1, 2, 3, 4, 5, 6, 7};
   static constexpr int C[NPAIR] = {8, 9, 10, 11, 12, 13, 14, 15};
-  static constexpr uint32_t SIGN[WORDS] = {0xAAAAAAAAu};
 };
 template <> struct Plan<3> {
   static constexpr int WORDS = 3, CODES = 32, NPAIR = 16;
   static constexpr int S[NPAIR] = {-4, -4, 0, 5, 5, 26, 26, 32, 32, 35, 53, 58, 61, 64, 71, 71};
   static constexpr int A[NPAIR] = {0, 1, 2, 3, 4, 10, 11, 12, 13, 14, 20, 21, 22, 23, 25, 26};
   static constexpr int C[NPAIR] = {5, 6, 7, 8, 9, 15, 16, 17, 18, 19, 24, 27, 28, 29, 30, 31};
-  static constexpr uint32_t SIGN[WORDS] = {0x24924924u, 0x49249249u, 0x92492492u};
 };
 
 template <int BITS> __host__ __device__ constexpr int pa_of(int k) { return BITS * Plan<BITS>::A[k] - Plan<BITS>::S[k]; }

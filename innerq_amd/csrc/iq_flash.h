@@ -450,10 +450,6 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS>::NT), (fused_waves_per_sim
       if constexpr (!AVO) {
 #pragma unroll
         for (int g = 0; g < NG; ++g) {
-          if (a.ksym) {
-#pragma unroll
-            for (int j = 0; j < FBPW; ++j) to_offset_binary<KB>(kc.w[g][j], KW);
-          }
           float d[FBPW][NREP];
           qk_group_dot_biased<KB, G, NREP, FBPW>(kc.w[g], &sm.qrec[g][0], hl, qsplit, prk, d);
 #pragma unroll
@@ -473,25 +469,39 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS>::NT), (fused_waves_per_sim
       // into the V records ----
       auto& vrec = sm.vrec[wave];
       float mw[NREP], ps[VPW][NREP], alpha[NREP];
+      bool rescale = false;  // the running max moved: the run state is rescaled by alpha
       if constexpr (!AVO) {
+        // Lazy running max: the reference max only has to bound the block's
+        // logits, so it is raised (a wave reduction and a rescale) only when
+        // one exceeds it by more than LAZY_MAX (log2 units): p <= 2^LAZY_MAX,
+        // well inside fp16, and softmax does not depend on the reference.
+        constexpr float LAZY_MAX = 8.f;
+        bool need = false;
 #pragma unroll
         for (int j = 0; j < FBPW; ++j) {
           const bool live = wt0 + j * TOKEN_BLOCK + lane < a.T;
 #pragma unroll
-          for (int h = 0; h < NREP; ++h) acc[j][h] = live ? acc[j][h] * a.scale_log2 : -INFINITY;
+          for (int h = 0; h < NREP; ++h) {
+            acc[j][h] = live ? acc[j][h] * a.scale_log2 : -INFINITY;
+            need |= !(acc[j][h] <= m_run[h] + LAZY_MAX);
+          }
         }
+        rescale = __builtin_amdgcn_ballot_w64(need) != 0;
+        if (rescale) {
+          asm volatile("");  // a real branch: keeps the compiler from flattening it into selects
 #pragma unroll
-        for (int h = 0; h < NREP; ++h) {
-          mw[h] = acc[0][h];
+          for (int h = 0; h < NREP; ++h) {
+            mw[h] = acc[0][h];
 #pragma unroll
-          for (int j = 1; j < FBPW; ++j) mw[h] = fmaxf(mw[h], acc[j][h]);
-        }
-        wave_max_dpp(mw);
+            for (int j = 1; j < FBPW; ++j) mw[h] = fmaxf(mw[h], acc[j][h]);
+          }
+          wave_max_dpp(mw);
 #pragma unroll
-        for (int h = 0; h < NREP; ++h) {
-          const float mn = fmaxf(m_run[h], mw[h]);
-          alpha[h] = m_run[h] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run[h] - mn);
-          m_run[h] = mn;
+          for (int h = 0; h < NREP; ++h) {
+            const float mn = fmaxf(m_run[h], mw[h]);
+            alpha[h] = m_run[h] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run[h] - mn);
+            m_run[h] = mn;
+          }
         }
       }
       // x[h]: p; x[NREP + h]: -p * bias (the attn.V accumulators' seed)
@@ -546,9 +556,14 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS>::NT), (fused_waves_per_sim
           float lsum = 0.f;
 #pragma unroll
           for (int u = 0; u < VPW; ++u) lsum += ps[u][h];
-          l_run[h] = fmaf(l_run[h], alpha[h], lsum);
+          if (rescale) {
+            asm volatile("");
+            l_run[h] = fmaf(l_run[h], alpha[h], lsum);
 #pragma unroll
-          for (int e = 0; e < DPL; ++e) o_run[h][e] *= alpha[h];
+            for (int e = 0; e < DPL; ++e) o_run[h][e] *= alpha[h];
+          } else {
+            l_run[h] += lsum;
+          }
         }
       }
       wave_lds_sync();
@@ -558,10 +573,6 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS>::NT), (fused_waves_per_sim
 #pragma unroll
       for (int u = 0; u < VPW; ++u) {
         if (u < vcnt) {
-          if (a.vsym) {
-#pragma unroll
-            for (int e = 0; e < DPL; ++e) to_offset_binary<VB>(v.w[u][e], VW);
-          }
           f4_t init[NQ], dv[DPL][NQ];
 #pragma unroll
           for (int q = 0; q < NQ; ++q)

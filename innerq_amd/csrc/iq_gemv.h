@@ -117,12 +117,6 @@ __device__ __forceinline__ void plan_pair(int bits, int k, int& a, int& c) {
   else plan_pair_t<4>(k, a, c);
 }
 
-template <int BITS>
-__device__ __forceinline__ void to_offset_binary(uint32_t* w, int nw) {
-  constexpr int SBW = Plan<BITS>::WORDS;
-#pragma unroll
-  for (int j = 0; j < nw; ++j) w[j] ^= Plan<BITS>::SIGN[j % SBW];
-}
 
 __device__ __forceinline__ float rec_f32(cptr_u32 rec, int i) { return __builtin_bit_cast(float, rec[i]); }
 

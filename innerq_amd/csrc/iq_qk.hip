@@ -138,10 +138,6 @@ __global__ __launch_bounds__(WG) void qk_kernel(QKArgs a) {
     }
     if (g + 1 < NG) load(g + 1);
     const cptr_u32 rec = recb + g * RD;
-    if constexpr (SYM) {
-#pragma unroll
-      for (int j = 0; j < BPW; ++j) to_offset_binary<BITS>(cw[j], W);
-    }
     float d[BPW][NREP];
     qk_group_dot<BITS, G, NREP, BPW>(cw, a.rec + (int64_t(bh) * NG + g) * RD, lane & 3, a.split, pr, d);
 #pragma unroll

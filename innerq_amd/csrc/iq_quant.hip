@@ -89,7 +89,7 @@ __device__ __forceinline__ void quantize_group(const float* v, bool sym, uint32_
       const float sg = v[i] > 0.f ? 1.f : (v[i] < 0.f ? -1.f : 0.f);  // torch.sign
       codes[i] = c;
       const int32_t sc = (c == I32_MIN) ? 0 : (sg > 0.f ? c : (sg < 0.f ? -c : 0));
-      fields[i] = uint32_t(sc) & FMASK;
+      fields[i] = uint32_t(sc + (1 << (BITS - 1))) & FMASK;  // offset binary
       sgn[i] = sg;
     }
     s_out = s;
@@ -124,7 +124,7 @@ __device__ __forceinline__ void unpack_fields(const uint32_t* w, bool sym, int32
     if (o + BITS > 32) f |= w[wi + 1] << (32 - o);
     f &= FMASK;
     int32_t v = int32_t(f);
-    if (sym && (f >> (BITS - 1))) v -= (1 << BITS);
+    if (sym) v -= (1 << (BITS - 1));  // offset binary
     c[i] = v;
   }
 }

@@ -28,8 +28,9 @@ unpack): within one quantization group, code i occupies bits [b*i, b*i+b) of
 a little-endian bit string split into 32-bit words, LSB first.  A group of G
 codes is G*b/32 words; 3-bit groups of 32 codes are 3 words and codes 10 and
 21 straddle word boundaries.  Asym codes are stored as their low b bits
-(INT32_MIN -> 0); sym codes are stored as the b-bit two's complement of
-``sign * magnitude``.
+(INT32_MIN -> 0); sym codes are stored as offset binary,
+``sign * magnitude + 2^(b-1)`` (the speedtest's sym packing,
+benchmark_quantization.cu:128 and 161).
 
 Packed HBM store layouts (this build's, written by the HIP kernels):
 
@@ -222,11 +223,11 @@ dequantize_tokendim_hybrid = dequantize_hybrid(dequantize_tokendim_asym, dequant
 # ----------------------------------------------------------------------------
 
 def stored_codes(codes, bits, signs=None):
-    """Value written into the b-bit field: asym -> low b bits; sym -> two's
-    complement of sign*magnitude (signs given)."""
+    """Value written into the b-bit field: asym -> low b bits; sym (signs
+    given) -> sign*magnitude + 2^(b-1), offset binary."""
     c = np.asarray(codes).astype(np.int64)
     if signs is not None:
-        c = c * np.asarray(signs).astype(np.int64)
+        c = c * np.asarray(signs).astype(np.int64) + (1 << (bits - 1))
     return (c & ((1 << bits) - 1)).astype(np.uint32)
 
 
@@ -248,7 +249,7 @@ def pack_groups(fields, bits):
 
 
 def unpack_groups(words, bits, G, signed=False):
-    """Inverse of ``pack_groups``; ``signed`` sign-extends two's complement fields."""
+    """Inverse of ``pack_groups``; ``signed`` decodes offset-binary fields (u - 2^(b-1))."""
     words = np.asarray(words, dtype=np.uint64)
     out = np.zeros(words.shape[:-1] + (G,), dtype=np.int64)
     mask = (1 << bits) - 1
@@ -260,7 +261,7 @@ def unpack_groups(words, bits, G, signed=False):
             v = v | (words[..., w + 1] << np.uint64(32 - o))
         v = (v & np.uint64(mask)).astype(np.int64)
         if signed:
-            v = np.where(v >= (1 << (bits - 1)), v - (1 << bits), v)
+            v = v - (1 << (bits - 1))
         out[..., i] = v
     return out.astype(np.int32)
 

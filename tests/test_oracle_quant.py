@@ -152,12 +152,15 @@ def test_pack_3bit_straddle_positions():
     f[0, 21] = 0b011
     w = Q.pack_groups(f, 3)[0]
     assert w[0] == (0b01 << 30) and w[1] == (0b1 | (0b1 << 31)) and w[2] == 0b01
-    # sym: two's complement sign extension
+    # sym: offset binary (u = signed + 4 at 3 bits), straddling fields included
     f = np.zeros((1, 32), np.int64)
     f[0, 10] = -3
-    f[0, 21] = -4
-    w = Q.pack_groups((f & 7).astype(np.uint32), 3)
-    np.testing.assert_array_equal(Q.unpack_groups(w, 3, 32, signed=True)[0], f[0])
+    f[0, 21] = 3
+    wp = Q.pack_groups((f + 4).astype(np.uint32), 3)
+    w = wp[0]
+    assert w[0] >> 30 == 0b01 and w[1] & 1 == 0 and (w[1] >> 31, w[2] & 3) == (1, 0b11)
+    np.testing.assert_array_equal(Q.unpack_groups(wp, 3, 32, signed=True)[0], f[0])
+    np.testing.assert_array_equal(Q.stored_codes(np.abs(f), 3, np.sign(f)), (f + 4).astype(np.uint32))
 
 
 @pytest.mark.parametrize("mode", ["asymmetric", "symmetric"])
