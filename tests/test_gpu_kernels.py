@@ -449,6 +449,60 @@ def test_decode_attention_dense_window_unaligned(nrep, D, R):
     assert A.rel_err(got, A.decode_attention(q, kd, vd, D ** -0.5, p_dtype=None)) < TOL
 
 
+def _decode_inputs(B, Hkv, nrep, D, Tq, R, bits, seed):
+    gen = torch.Generator(device=DEV).manual_seed(seed)
+    k = torch.randn(B, Hkv, Tq + R, D, generator=gen, device=DEV).to(torch.float16)
+    v = torch.randn(B, Hkv, Tq + R, D, generator=gen, device=DEV).to(torch.float16)
+    q = torch.randn(B, Hkv * nrep, D, generator=gen, device=DEV).to(torch.float16)
+    kst = ops.PackedStore("channel", B, Hkv, D, 32, bits, "asymmetric", DEV, t_cap=Tq)
+    vst = ops.PackedStore("token", B, Hkv, D, 32, bits, "asymmetric", DEV, t_cap=Tq)
+    kst.append(k[:, :, :Tq])
+    vst.append(v[:, :, :Tq])
+    kd = torch.cat([ops.dequantize_dense(*ops.unpack_store(kst), 32, "asymmetric", "channel"),
+                    k[:, :, Tq:].float()], dim=2)
+    vd = torch.cat([ops.dequantize_dense(*ops.unpack_store(vst), 32, "asymmetric", "token"),
+                    v[:, :, Tq:].float()], dim=2)
+    lg = torch.matmul(q.float().view(B, Hkv, nrep, D), kd.transpose(-1, -2).contiguous()) * D ** -0.5
+    ref = torch.matmul(torch.softmax(lg, dim=-1), vd).view(B, Hkv * nrep, D)
+    return q, kst, vst, k[:, :, Tq:], v[:, :, Tq:], ref
+
+
+def test_decode_attention_long_range_repeated():
+    """A long range over 8 (batch, KV head)s (several workgroups per head, a dense
+    window), three calls in a row on one workspace.  Reference: fp32 attention over
+    K/V dequantized by the library (unpack is bit-exact to the oracle elsewhere)."""
+    q, kst, vst, kr, vr, ref = _decode_inputs(2, 4, 4, 128, 16384, 64, 4, seed=91)
+    for _ in range(3):
+        got = ops.decode_attention(q, None, kst, kr, None, vst, vr, 128 ** -0.5)
+        torch.cuda.synchronize()
+        assert ((got.float() - ref).abs().max() / ref.abs().max()).item() < TOL
+
+
+def test_decode_attention_graph_replay():
+    """The decode step captured in a HIP graph and replayed several times (eager
+    work between replays): every replay equals the eager result."""
+    q, kst, vst, kr, vr, ref = _decode_inputs(2, 4, 4, 128, 8192, 64, 4, seed=92)
+    side = torch.cuda.Stream()
+    out = torch.empty(2, 16, 128, dtype=torch.float16, device=DEV)
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):  # warm-up on the capture stream: its workspace exists before capture
+        ops.decode_attention(q, None, kst, kr, None, vst, vr, 128 ** -0.5, out=out)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    eager = out.clone()
+    assert ((eager.float() - ref).abs().max() / ref.abs().max()).item() < TOL
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=side):
+        ops.decode_attention(q, None, kst, kr, None, vst, vr, 128 ** -0.5, out=out)
+    for _ in range(3):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert ((out.float() - eager.float()).abs().max() / eager.float().abs().max()).item() < 1e-5
+        ops.decode_attention(q, None, kst, kr, None, vst, vr, 128 ** -0.5)  # eager work between replays
+        torch.cuda.synchronize()
+
+
 # K and V of one bit width and group size take the fused split kernel (one
 # workgroup runs QK^T, the split softmax and attn.V); sym/asym may differ.
 @pytest.mark.parametrize("fmt,nrep,D", [
