@@ -193,19 +193,31 @@ __global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs a) {
       }
     }
     const bool live = c0 + lane < i1;
+    if (wave < 4) {  // DPP reductions over the wave's heads at once
+      float x[HPW], mx[HPW], cs[HPW];
 #pragma unroll
-    for (int hh = 0; hh < HPW; ++hh) {
-      const int h = wave + 4 * hh;
-      if (h < NREP) {
-        const float x = live ? dot[hh] * a.scale : -INFINITY;
-        const float mn = fmaxf(m[hh], wave_max(x));
-        const float p = x == -INFINITY ? 0.f : __expf(x - mn);
-        ps[h][lane] = __half2float(__float2half_rn(p));
-        const float cs = wave_sum(p);
-        const float alpha = m[hh] == -INFINITY ? 0.f : __expf(m[hh] - mn);
-        l[hh] = fmaf(l[hh], alpha, cs);
-        m[hh] = mn;
-        if (lane == 0) al[h] = alpha;
+      for (int hh = 0; hh < HPW; ++hh) {
+        x[hh] = live && wave + 4 * hh < NREP ? dot[hh] * a.scale : -INFINITY;
+        mx[hh] = x[hh];
+      }
+      wave_max_dpp(mx);
+#pragma unroll
+      for (int hh = 0; hh < HPW; ++hh) {
+        mx[hh] = fmaxf(m[hh], mx[hh]);
+        cs[hh] = x[hh] == -INFINITY ? 0.f : __expf(x[hh] - mx[hh]);
+        x[hh] = cs[hh];
+      }
+      wave_sum_dpp(cs);
+#pragma unroll
+      for (int hh = 0; hh < HPW; ++hh) {
+        const int h = wave + 4 * hh;
+        if (h < NREP) {
+          ps[h][lane] = __half2float(__float2half_rn(x[hh]));
+          const float alpha = m[hh] == -INFINITY ? 0.f : __expf(m[hh] - mx[hh]);
+          l[hh] = fmaf(l[hh], alpha, cs[hh]);
+          m[hh] = mx[hh];
+          if (lane == 0) al[h] = alpha;
+        }
       }
     }
     __syncthreads();
@@ -302,17 +314,19 @@ __global__ __launch_bounds__(64) void flash_combine_kernel(const float* __restri
 #pragma unroll
   for (int e = 0; e < E; ++e)
     if (e * 64 + lane > last) sl[e] = make_float2(-INFINITY, 0.f);
-  float M = -INFINITY;
+  float Mv[1] = {-INFINITY};
 #pragma unroll
-  for (int e = 0; e < E; ++e) M = fmaxf(M, sl[e].x);
-  M = wave_max(M);
-  float L = 0.f, w[E];
+  for (int e = 0; e < E; ++e) Mv[0] = fmaxf(Mv[0], sl[e].x);
+  wave_max_dpp(Mv);
+  const float M = Mv[0];
+  float Lv[1] = {0.f}, w[E];
 #pragma unroll
   for (int e = 0; e < E; ++e) {
     w[e] = sl[e].x == -INFINITY ? 0.f : __expf(sl[e].x - M);
-    L = fmaf(w[e], sl[e].y, L);
+    Lv[0] = fmaf(w[e], sl[e].y, Lv[0]);
   }
-  L = wave_sum(L);
+  wave_sum_dpp(Lv);
+  const float L = Lv[0];
   Vec acc = 0.f;
 #pragma unroll
   for (int j = 0; j < CSPEC; ++j) {
