@@ -69,6 +69,32 @@ def time_loop(fn, n, warmup):
     return e0.elapsed_time(e1) / n * 1e3  # us per call
 
 
+def time_graph(fn, reps, n):
+    """GPU time per call: `reps` calls captured in one HIP graph and replayed n
+    times, so the Python/ctypes launch cost of each call is not in the timing."""
+    import torch
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):  # warm-up on the capture stream: its workspace exists before capture
+        for i in range(reps):
+            fn(i)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=side):
+        for i in range(reps):
+            fn(i)
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(n):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / (n * reps) * 1e3
+
+
 def cpu_baseline(B, Hq, Hkv, T, D, G, bk, bv, step_bytes, budget_s=12.0):
     import torch
     from oracle import timing
@@ -163,7 +189,9 @@ def bench_headline(args):
 
 
 def bench_config(args):
-    """Non-headline BASELINE configs, one JSON line each (used for DESIGN.md tables)."""
+    """Non-headline BASELINE configs, one JSON line each: us = per call through the
+    Python API (host launch cost included), us_graph = the same calls replayed from
+    a captured HIP graph (GPU time)."""
     import torch
     from innerq_amd import ops
     dev = torch.device("cuda:0")
@@ -175,18 +203,22 @@ def bench_config(args):
         ks = [make_store("channel", B, Hkv, T, D, G, 4, "asymmetric", 10 + c, dev) for c in range(C)]
         q = torch.randn(B, Hq, D, device=dev, dtype=torch.float16)
         lg = torch.empty(B, Hq, T, device=dev)
-        us = time_loop(lambda i: ops.qk_gemv(q, ks[i % C], D ** -0.5, out=lg), args.steps, args.warmup)
+        fn = lambda i: ops.qk_gemv(q, ks[i % C], D ** -0.5, out=lg)
+        us = time_loop(fn, args.steps, args.warmup)
+        ug = time_graph(fn, 4 * C, max(1, args.steps // 4))
         b = gemv_bytes(B, Hkv, T, D, G, 4, "asymmetric", "channel")
-        res.update(us=us, GBs=b / us / 1e3, bytes=b)
+        res.update(us=us, GBs=b / us / 1e3, us_graph=ug, GBs_graph=b / ug / 1e3, bytes=b)
     elif cfg == "2":
         B, Hq, Hkv, D, T, G = 8, 32, 8, 128, 32768, 64
         for mode in ("asymmetric", "symmetric"):
             vs = [make_store("token", B, Hkv, T, D, G, 2, mode, 20 + c, dev) for c in range(C)]
             p = torch.softmax(torch.randn(B, Hq, T, device=dev) * 2.0, dim=-1).to(torch.float16)
             out = torch.empty(B, Hq, D, device=dev, dtype=torch.float16)
-            us = time_loop(lambda i: ops.av_gemv(p, vs[i % C], out=out), args.steps, args.warmup)
+            fn = lambda i: ops.av_gemv(p, vs[i % C], out=out)
+            us = time_loop(fn, args.steps, args.warmup)
+            ug = time_graph(fn, C, max(1, args.steps // 4))
             b = gemv_bytes(B, Hkv, T, D, G, 2, mode, "token")
-            res[mode] = dict(us=us, GBs=b / us / 1e3, bytes=b)
+            res[mode] = dict(us=us, GBs=b / us / 1e3, us_graph=ug, GBs_graph=b / ug / 1e3, bytes=b)
             del vs
     elif cfg == "3":
         B, Hq, Hkv, D, T, G, R = 16, 32, 8, 128, 16384, 32, 128
@@ -206,8 +238,9 @@ def bench_config(args):
             ap.append(knew)  # quantize-on-append of one token per sequence (K, flush 1)
 
         us = time_loop(step, args.steps, args.warmup)
+        ug = time_graph(step, C, max(1, args.steps // 4))
         b = 2 * gemv_bytes(B, Hkv, Tq, D, G, 3, "symmetric", "channel")
-        res.update(us=us, GBs=b / us / 1e3, bytes=b)
+        res.update(us=us, GBs=b / us / 1e3, us_graph=ug, GBs_graph=b / ug / 1e3, bytes=b)
     elif cfg == "4":
         B, Hq, Hkv, D, T, G, R, L = 8, 32, 8, 128, 32768, 32, 128, 32
         Tq = T - R
@@ -223,9 +256,11 @@ def bench_config(args):
                 ops.decode_attention(q, None, ks[l], kr, None, vs[l], vr, D ** -0.5, out=out)
 
         us = time_loop(step, max(1, args.steps // 10), 2)
+        ug = time_graph(step, 1, max(1, args.steps // 10))
         b = L * (gemv_bytes(B, Hkv, Tq, D, G, 2, "asymmetric", "channel")
                  + gemv_bytes(B, Hkv, Tq - Tq % G, D, G, 4, "asymmetric", "token"))
-        res.update(us=us, us_per_layer=us / L, GBs=b / us / 1e3, bytes=b)
+        res.update(us=us, us_per_layer=us / L, GBs=b / us / 1e3, us_graph=ug, us_per_layer_graph=ug / L,
+                   GBs_graph=b / ug / 1e3, bytes=b)
     print(json.dumps(res), flush=True)
 
 
