@@ -192,7 +192,11 @@ __device__ __forceinline__ float seg_sum(float v) {
 // arguments (q, sqb, sqh, q_bytes), are loaded one block ahead in place of K
 // and written into the attn.V operand records as they are; the runs' partials
 // are plain sums (no statistics are written).
-template <int KB, int VB, int G, int D, int NREP, bool QS, bool AVO = false>
+// QKO (QK^T only, the standalone logits GEMV of iq_qk.hip): no V, no
+// softmax; each block's scaled logits (scale_log2 holds the plain scale) go to
+// the fp32 output at part (element strides sob, soh per batch and query head,
+// 1 per token).
+template <int KB, int VB, int G, int D, int NREP, bool QS, bool AVO = false, bool QKO = false>
 __global__ __launch_bounds__((FusedShape<G, NREP, QS>::NT), (fused_waves_per_simd<G, NREP, QS>())) void flash_fused_kernel(FusedArgs a) {
   using FS = FusedShape<G, NREP, QS>;
   constexpr int NW = FS::NW, NT = FS::NT, WTOK = FS::WTOK, FBPW = FS::FBPW, VPW = FS::VPW;
@@ -465,6 +469,19 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS>::NT), (fused_waves_per_sim
         }
       }
 
+      if constexpr (QKO) {
+        // ---- the block's logits, lane = token ----
+        const int b = run.bh / a.Hkv, kvh = run.bh - b * a.Hkv;
+        float* o = a.part + b * a.sob + int64_t(kvh * NREP) * a.soh;
+#pragma unroll
+        for (int j = 0; j < FBPW; ++j) {
+          const int t = wt0 + j * TOKEN_BLOCK + lane;
+          if (t < a.T) {
+#pragma unroll
+            for (int h = 0; h < NREP; ++h) o[h * a.soh + t] = acc[j][h] * a.scale_log2;
+          }
+        }
+      } else {
       // ---- softmax against the running max (log2 domain); fp16 p straight
       // into the V records ----
       auto& vrec = sm.vrec[wave];
@@ -589,8 +606,9 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS>::NT), (fused_waves_per_sim
           }
         }
       }
+      }
     }
-    load_v(lbh, lblk, lreal, v);  // streams in during the next block's QK^T
+    if constexpr (!QKO) load_v(lbh, lblk, lreal, v);  // streams in during the next block's QK^T
     if (!ends) {
       nn = __builtin_amdgcn_readlane(nn, 0);
       cur = nxt;
@@ -602,8 +620,9 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS>::NT), (fused_waves_per_sim
     // combine skips them) ----
     int slot, nr;
     run_slots(run, slot, nr);
-    flush_run(run.bh, slot);
-    if (!AVO && wave == 0 && lane < NREP) {
+    if constexpr (QKO) lds_barrier();  // every wave is past its last QK^T of the run
+    else flush_run(run.bh, slot);
+    if (!AVO && !QKO && wave == 0 && lane < NREP) {
       for (int sp = max(run.split0, nr); sp < run.split0 + run.nsplit; ++sp) {
         float* ml = a.ml + (int64_t(sp) * rows + int64_t(run.bh) * NREP + lane) * 2;
         ml[0] = -INFINITY;
@@ -627,7 +646,7 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS>::NT), (fused_waves_per_sim
   XRegs ka, kb;
   reset_run();
   load_x(run.bh, block_of(run, max(cur, 0)), cur >= 0, ka);
-  load_v(run.bh, block_of(run, max(cur, 0)), cur >= 0, v);
+  if constexpr (!QKO) load_v(run.bh, block_of(run, max(cur, 0)), cur >= 0, v);
   if constexpr (!AVO) {
     load_q(run.bh, true, qq);
     build_records(qq);

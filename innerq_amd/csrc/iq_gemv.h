@@ -391,6 +391,7 @@ struct FusedArgs {
   float scale_log2;    // scale * log2(e)
   float* ml;           // [nsplit][B*Hq][2]
   float* part;         // [nsplit][B*Hq][D]
+  int64_t sob, soh;    // QK^T only: strides of the logits output (part)
 };
 // its launch per K bit width (iq_flash_k{2,3,4}.hip)
 int flash_fused_launch_k2(const FusedArgs& a, int vbits, int group, int D, int nrep, bool norm, hipStream_t stream);

@@ -21,7 +21,7 @@
 //           the probabilities exp(logit - m), rounded to fp16, are written
 //           straight into attn.V operand records for the V store's unpack
 //           plan, so no logits or probabilities round-trip through HBM.
-#include "iq_gemv.h"
+#include "iq_flash.h"
 
 using namespace iq;
 
@@ -311,6 +311,54 @@ int qk_flash_launch(const uint32_t* rec, int split, const uint32_t* k_codes, con
 
 }  // namespace iq::detail
 
+namespace {
+
+// QK^T through the persistent fused kernel in QK^T-only mode (query records
+// built in LDS by each workgroup, no record kernel); returns 1 if launched, 0
+// if a slice exceeds its 32-bit buffer offsets
+int qk_fused_launch(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, const uint32_t* k_codes,
+                    const uint16_t* k_meta, int64_t t_cap, int B, int Hq, int Hkv, int t0, int T, int D, int group,
+                    int bits, int mode, float scale, float* out, int64_t so_b, int64_t so_h, hipStream_t stream,
+                    int* status) {
+  const int nrep = Hq / Hkv;
+  const int64_t lim = int64_t(1) << 31;
+  if (sq_h < 0 || (int64_t(nrep - 1) * sq_h + D) * 2 >= lim || t_cap * D * bits / 8 >= lim ||
+      t_cap * D * 4 / group >= lim)
+    return 0;
+  detail::FusedArgs a{};
+  a.q = (const uint16_t*)q; a.sqb = sq_b; a.sqh = sq_h; a.norm = (const uint16_t*)norm;
+  a.kc = k_codes; a.km = k_meta; a.k_cap_blocks = t_cap / TOKEN_BLOCK; a.kblk0 = t0 / TOKEN_BLOCK;
+  a.ksym = mode == IQ_MODE_SYM;
+  a.Hkv = Hkv; a.T = T;
+  a.nsplit = int(ceil_div(T, FSPLIT));
+  a.nitems = a.nsplit * B * Hkv;
+  const int64_t nblk = ceil_div(T, TOKEN_BLOCK);
+  a.k_code_bytes = uint32_t(nblk * TOKEN_BLOCK * D * bits / 8);
+  a.k_meta_bytes = uint32_t(nblk * TOKEN_BLOCK * (D / group) * (a.ksym ? 2 : 4));
+  a.q_bytes = uint32_t((int64_t(nrep - 1) * sq_h + D) * 2);
+  a.norm_bytes = norm ? uint32_t(D * 2) : 0u;
+  a.scale_log2 = scale;  // QK^T only: the plain scale of the logits
+  a.part = out; a.sob = so_b; a.soh = so_h;
+  *status = dispatch_shape(bits, group, D, nrep, 0, [&]<int KB, int G, int DD, int R, bool S>() {
+    auto* kern = norm ? flash_fused_kernel<KB, KB, G, DD, R, true, false, true>
+                      : flash_fused_kernel<KB, KB, G, DD, R, false, false, true>;
+    const int nt = norm ? FusedShape<G, R, true>::NT : FusedShape<G, R, false>::NT;
+    static int per_cu[2] = {0, 0};  // workgroups per CU at once
+    int& pc = per_cu[norm ? 1 : 0];
+    if (pc == 0) {
+      int n = 0;
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, nt, 0) != hipSuccess || n <= 0) n = 1;
+      pc = n;
+    }
+    const int grid = int(std::min<int64_t>(a.nitems, int64_t(pc) * detail::num_cus()));
+    kern<<<dim3(grid), nt, 0, stream>>>(a);
+    return launch_status();
+  });
+  return 1;
+}
+
+}  // namespace
+
 extern "C" {
 
 size_t iq_qk_workspace_bytes(int B, int Hq, int D) {
@@ -326,6 +374,11 @@ int iq_qk_gemv(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, cons
   IQ_CHECK(workspace && workspace_bytes >= detail::qk_record_bytes(B, Hq, D), IQ_ERR_WORKSPACE);
   IQ_CHECK(aligned(workspace, 16), IQ_ERR_ALIGN);
   hipStream_t st = (hipStream_t)stream;
+  if (B == 0 || T == 0) return IQ_OK;
+  int status = IQ_OK;
+  if (qk_fused_launch(q, sq_b, sq_h, norm, k_codes, k_meta, t_cap, B, Hq, Hkv, t0, T, D, group, bits, mode, scale, out,
+                      so_b, so_h, st, &status))
+    return status;
   uint32_t* rec = (uint32_t*)workspace;
   if (int e = detail::qk_record_launch(q, sq_b, sq_h, norm, B, Hq, Hkv, D, group, bits, rec, st)) return e;
   return detail::qk_main_launch(rec, norm != nullptr, k_codes, k_meta, t_cap, B, Hq, Hkv, t0, T, D, group, bits, mode, scale, out,
