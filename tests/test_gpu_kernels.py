@@ -232,6 +232,27 @@ def test_qk_gemv_key_norm_folded(nrep, G):
     assert A.rel_err(got, A.qk_logits(q, kdeq, D ** -0.5)) < TOL
 
 
+@pytest.mark.parametrize("bits,G,mode,norm", [(4, 32, "asymmetric", False), (2, 64, "symmetric", True),
+                                              (3, 128, "asymmetric", False)])
+def test_qk_gemv_many_runs(bits, G, mode, norm):
+    """A long range over several (batch, KV head)s: the persistent kernel's shares
+    cut every head into several runs, each building its own query records.
+    Reference: fp32 q . K over the store's own dequantization (dequant is
+    bit-exact to the oracle in the tests above) times the normalization."""
+    B, Hkv, nrep, D, T = 2, 4, 4, 128, 16384 + 64 * 5 + 9
+    gen = torch.Generator(device=DEV).manual_seed(bits * G + norm)
+    x = torch.randn(B, Hkv, T, D, generator=gen, device=DEV).to(torch.float16)
+    nrm = (torch.rand(B, Hkv, 1, D, generator=gen, device=DEV) + 0.5).to(torch.float16) if norm else None
+    st = ops.PackedStore("channel", B, Hkv, D, G, bits, mode, DEV, t_cap=T)
+    st.append(x, norm=nrm)
+    kd = st.dequant(norm=nrm, dtype=torch.float32)
+    q = torch.randn(B, Hkv * nrep, D, generator=gen, device=DEV).to(torch.float16)
+    got = ops.qk_gemv(q, st, D ** -0.5, norm=nrm)
+    ref = torch.matmul(q.float().view(B, Hkv, nrep, D), kd.transpose(-1, -2).contiguous())
+    ref = ref.view(B, Hkv * nrep, T) * D ** -0.5
+    assert A.rel_err(got.cpu().numpy(), ref.cpu().numpy()) < TOL
+
+
 def peaked_p(B, Hq, T, seed, std=2.0):
     logits = synth.normal((B, Hq, T), seed=seed, std=std).astype(np.float64)
     return A.softmax(logits).astype(np.float16)
