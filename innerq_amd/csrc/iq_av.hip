@@ -301,7 +301,7 @@ int av_fused_launch(const void* p, int64_t sp_b, int64_t sp_h, const uint32_t* v
   a.part = part;
   return dispatch_shape(bits, group, D, nrep, 0, [&]<int VB, int G, int DD, int R, bool S>() {
     auto* kern = flash_fused_kernel<VB, VB, G, DD, R, false, true>;
-    const int nt = FusedShape<G, R, false>::NT;
+    const int nt = FusedShape<G, R, false, true>::NT;
     static int per_cu = 0;  // workgroups per CU at once
     if (per_cu == 0) {
       int n = 0;

@@ -76,8 +76,9 @@ __device__ float packed_elem(const Seg& g, bool is_k, int64_t bh, int D, int tl,
 // fp16 elements [d0, d0 + N) of token t's row (a K or V segment list), as N/2
 // dwords; a token outside every segment gives zeros.  Dense rows load as
 // 16-byte vectors where aligned; packed rows (tokens packed in only one of K
-// and V) are dequantized element by element.
-template <int N>
+// and V) are dequantized element by element.  PK = false: the caller has no
+// packed segment (their code is left out: a short kernel fetches less code).
+template <int N, bool PK>
 __device__ __forceinline__ void gather_row(const Seg* s, bool is_k, int64_t b, int64_t kvh, int64_t Hkv, int D, int t,
                                            int d0, const uint16_t* norm, uint32_t (&out)[N / 2]) {
 #pragma unroll
@@ -99,7 +100,7 @@ __device__ __forceinline__ void gather_row(const Seg* s, bool is_k, int64_t b, i
 #pragma unroll
         for (int j = 0; j < N / 2; ++j) out[j] = uint32_t(row[2 * j]) | (uint32_t(row[2 * j + 1]) << 16);
       }
-    } else {
+    } else if constexpr (PK) {
       const int64_t bh = b * Hkv + kvh;
       for (int j = 0; j < N / 2; ++j) {
         const float x0 = packed_elem(g, is_k, bh, D, tl, d0 + 2 * j, norm);
@@ -132,7 +133,7 @@ struct DenseArgs {
 // running (m, l), and thread (head, column pair) accumulates the output.  The
 // probability that meets V is rounded to fp16, as the reference rounds its
 // softmax output; logits, sums and outputs are fp32.
-template <int D, int NREP>
+template <int D, int NREP, bool PK>
 __global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs a) {
   constexpr int KS = D / 2 + 1;               // K tile row stride in dwords (odd: no bank conflicts)
   constexpr int HPW = (NREP + 3) / 4;         // heads per wave
@@ -150,8 +151,6 @@ __global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs a) {
   const int n0 = a.hi0 - a.lo0, n = n0 + (a.hi1 - a.lo1);
   const int i0 = int(int64_t(blockIdx.x) * n / gridDim.x), i1 = int(int64_t(blockIdx.x + 1) * n / gridDim.x);
   const int64_t rows = int64_t(gridDim.y) * NREP;
-  for (int i = tid; i < NREP * D; i += 256)
-    qs[i / D][i % D] = h2f(a.q[b * a.sqb + (kvh * NREP + i / D) * a.sqh + i % D]);
 
   // gathering: thread = (row tid / 4, quarter tid % 4 of the row)
   const int gr = tid >> 2, gq = tid & 3;
@@ -159,9 +158,13 @@ __global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs a) {
   auto gather = [&](int c0) {
     const int i = c0 + gr;
     const int t = i < i1 ? (i < n0 ? a.lo0 + i : a.lo1 + (i - n0)) : -1;
-    gather_row<RE>(a.k, true, b, kvh, a.Hkv, D, t, gq * RE, a.norm, kr);
-    gather_row<RE>(a.v, false, b, kvh, a.Hkv, D, t, gq * RE, nullptr, vr);
+    gather_row<RE, PK>(a.k, true, b, kvh, a.Hkv, D, t, gq * RE, a.norm, kr);
+    gather_row<RE, PK>(a.v, false, b, kvh, a.Hkv, D, t, gq * RE, nullptr, vr);
   };
+  // the first chunk's rows and the query are loaded together (one round trip)
+  if (i0 < i1) gather(i0);
+  for (int i = tid; i < NREP * D; i += 256)
+    qs[i / D][i % D] = h2f(a.q[b * a.sqb + (kvh * NREP + i / D) * a.sqh + i % D]);
   float m[HPW], l[HPW];
 #pragma unroll
   for (int hh = 0; hh < HPW; ++hh) { m[hh] = -INFINITY; l[hh] = 0.f; }
@@ -169,7 +172,6 @@ __global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs a) {
 #pragma unroll
   for (int it = 0; it < OPT; ++it) o[it][0] = o[it][1] = 0.f;
 
-  if (i0 < i1) gather(i0);
   for (int c0 = i0; c0 < i1; c0 += DT) {
 #pragma unroll
     for (int j = 0; j < RE / 2; ++j) {
@@ -509,7 +511,18 @@ int launch_splits(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, c
     const int64_t bhs = int64_t(B) * Hkv;
     nsd = int(std::min<int64_t>({NSD_MAX, ceil_div(n_dense, DSLICE), std::max<int64_t>(1, ceil_div(detail::num_cus(), bhs))}));
     const dim3 grid{unsigned(nsd), unsigned(bhs), 1u};
-    auto go = [&]<int DD, int R>() { dense_attn_kernel<DD, R><<<grid, 256, 0, st>>>(da); };
+    // any packed segment (tokens packed in only one of K and V) needs the
+    // general gather; a dense-only step takes the short kernel
+    auto packed_in_range = [&](const Seg& g) {
+      auto meets = [&](int lo, int hi) { return lo < hi && g.start < hi && lo < g.start + g.n; };
+      return g.n > 0 && !g.dense && (meets(da.lo0, da.hi0) || meets(da.lo1, da.hi1));
+    };
+    bool pk = false;
+    for (int s = 0; s < 3; ++s) pk |= packed_in_range(da.k[s]) || packed_in_range(da.v[s]);
+    auto go = [&]<int DD, int R>() {
+      if (pk) dense_attn_kernel<DD, R, true><<<grid, 256, 0, st>>>(da);
+      else dense_attn_kernel<DD, R, false><<<grid, 256, 0, st>>>(da);
+    };
     auto by_r = [&]<int DD>() {
       switch (Hq / Hkv) {
         case 1: go.template operator()<DD, 1>(); break;

@@ -88,30 +88,34 @@ static_assert(plan_inv_ok<2>() && plan_inv_ok<3>() && plan_inv_ok<4>(), "plan in
 
 using detail::FusedArgs;
 
-// waves per SIMD the register allocation aims at: three (<= 168 VGPRs) for
-// 64-token waves and up to 4 query heads per KV head, fewer where the operand
-// and accumulator registers need more (8 heads, or hi/lo query rows with 4)
-template <int G, int NREP, bool QS>
+// waves per SIMD: one for G-token waves (G > 64); for 64-token waves two,
+// and three in attn.V-only mode (AVO).  Three fit the registers of up to 4
+// query heads per KV head, but measured slower for the decode step (~1.5 us
+// at the headline): each wave keeps one block's loads in flight, and the
+// memory system streams the cache faster with fewer requests in flight per
+// CU (the same trend as load-only probes).  The lighter attn.V-only waves
+// measured ~1 us faster with three.
+template <int G, int NREP, bool QS, bool AVO = false>
 constexpr int fused_waves_per_simd() {
-  return G > TOKEN_BLOCK ? 1 : (NREP > 4 || (QS && NREP == 4)) ? 2 : 3;
+  return G > TOKEN_BLOCK ? 1 : AVO && NREP <= 4 && !QS ? 3 : 2;
 }
 
 // Workgroup shape: one workgroup per CU, filling every SIMD to the register
 // allocation's occupancy; a wave processes blocks of WTOK consecutive tokens
 // (lane = token for QK^T), so that a V group of G tokens lies inside a block.
-template <int G, int NREP, bool QS>
+template <int G, int NREP, bool QS, bool AVO = false>
 struct FusedShape {
   static constexpr int WTOK = G > TOKEN_BLOCK ? G : TOKEN_BLOCK;
   static constexpr int FBPW = WTOK / TOKEN_BLOCK;                // 64-token K blocks per wave block
-  static constexpr int NW = 4 * fused_waves_per_simd<G, NREP, QS>();  // waves per workgroup
+  static constexpr int NW = 4 * fused_waves_per_simd<G, NREP, QS, AVO>();  // waves per workgroup
   static constexpr int NT = NW * 64;
   static constexpr int VPW = WTOK / G;                           // V groups per wave block
   static_assert(FSPLIT % WTOK == 0, "a split holds whole wave blocks");
 };
 
-template <int G, int D, int NREP, bool QS>
+template <int G, int D, int NREP, bool QS, bool AVO>
 struct FusedSmem {
-  using FS = FusedShape<G, NREP, QS>;
+  using FS = FusedShape<G, NREP, QS, AVO>;
   alignas(16) uint32_t qrec[D / G][qrec_dwords<G, NREP>()];         // query records of the current split
   alignas(16) uint32_t vrec[FS::NW][FS::VPW][rec_dwords<G, NREP>()];  // per wave: fp16 p pairs
   alignas(16) float red[FS::NW][NREP][D];                            // merge of the waves' outputs
@@ -197,8 +201,8 @@ __device__ __forceinline__ float seg_sum(float v) {
 // the fp32 output at part (element strides sob, soh per batch and query head,
 // 1 per token).
 template <int KB, int VB, int G, int D, int NREP, bool QS, bool AVO = false, bool QKO = false>
-__global__ __launch_bounds__((FusedShape<G, NREP, QS>::NT), (fused_waves_per_simd<G, NREP, QS>())) void flash_fused_kernel(FusedArgs a) {
-  using FS = FusedShape<G, NREP, QS>;
+__global__ __launch_bounds__((FusedShape<G, NREP, QS, AVO>::NT), (fused_waves_per_simd<G, NREP, QS, AVO>())) void flash_fused_kernel(FusedArgs a) {
+  using FS = FusedShape<G, NREP, QS, AVO>;
   constexpr int NW = FS::NW, NT = FS::NT, WTOK = FS::WTOK, FBPW = FS::FBPW, VPW = FS::VPW;
   constexpr int BPS = FSPLIT / WTOK;  // wave blocks per split
   constexpr int NG = D / G;
@@ -210,7 +214,7 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS>::NT), (fused_waves_per_sim
   constexpr int QOS = qrec_osum<G, NREP>();
   constexpr int QNB = qrec_nbsum<G, NREP>();
   constexpr int NQ = (NREP + 3) / 4;
-  __shared__ FusedSmem<G, D, NREP, QS> sm;
+  __shared__ FusedSmem<G, D, NREP, QS, AVO> sm;
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -634,10 +638,16 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS>::NT), (fused_waves_per_sim
     run = run2;
     rs2 += run.nsplit;
     run2 = run_at(min(rs2, i1 - 1));
-    if constexpr (!AVO) build_records(qq);  // the new (batch, KV head)'s query records
+    // the new (batch, KV head)'s query records.  The query is loaded here and
+    // not prefetched during the previous run: registers with loads pending
+    // across the block loop made the compiler wait for every outstanding load
+    // at the loop's back edge
+    if constexpr (!AVO) {
+      load_q(run.bh, true, qq);
+      build_records(qq);
+    }
     if (tid == 0) sm.next_block = 2 * NW;
     lds_barrier();
-    if constexpr (!AVO) load_q(run2.bh, rs2 < i1, qq);  // the run after: in flight through this one
     cur = wave < run.nb ? wave : -1;
     nxt = NW + wave < run.nb ? NW + wave : -1;
     return true;
@@ -653,7 +663,6 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS>::NT), (fused_waves_per_sim
   }
   if (tid == 0) sm.next_block = 2 * NW;
   lds_barrier();
-  if constexpr (!AVO) load_q(run2.bh, rs2 < i1, qq);
   while (step(ka, kb) && step(kb, ka)) {
   }
 }
