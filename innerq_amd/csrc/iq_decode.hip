@@ -83,32 +83,45 @@ __device__ __forceinline__ void gather_row(const Seg* s, bool is_k, int64_t b, i
                                            int d0, const uint16_t* norm, uint32_t (&out)[N / 2]) {
 #pragma unroll
   for (int i = 0; i < N / 2; ++i) out[i] = 0u;
+  // The lane's segment, chosen by value: every segment's fields are read with
+  // a constant index (uniform, scalar loads of the kernel arguments) and the
+  // lane selects its row pointer; a per-lane pointer to the segment would turn
+  // every field into a dependent load through memory.
+  const uint16_t* row = nullptr;
+  bool vec = false;
+  int pseg = -1, ptl = 0;  // packed segment of the lane and its local token
 #pragma unroll
   for (int i = 0; i < 3; ++i) {
-    const Seg& g = s[i];
-    if (t < g.start || t >= g.start + g.n) continue;
-    const int tl = t - g.start;
-    if (g.dense) {
-      const uint16_t* row = g.dense + b * g.sb + kvh * g.sh + int64_t(tl) * g.st + d0;
-      if (g.vec) {
+    const bool in = t >= s[i].start && t < s[i].start + s[i].n;
+    if (in && s[i].dense) {
+      row = s[i].dense + b * s[i].sb + kvh * s[i].sh + int64_t(t - s[i].start) * s[i].st + d0;
+      vec = s[i].vec != 0;
+    } else if (in) {
+      pseg = i;
+      ptl = t - s[i].start;
+    }
+  }
+  if (row) {
+    if (vec) {
 #pragma unroll
-        for (int c = 0; c < N / 8; ++c) {
-          const uint4 x = reinterpret_cast<const uint4*>(row)[c];
-          out[4 * c] = x.x; out[4 * c + 1] = x.y; out[4 * c + 2] = x.z; out[4 * c + 3] = x.w;
-        }
-      } else {
-#pragma unroll
-        for (int j = 0; j < N / 2; ++j) out[j] = uint32_t(row[2 * j]) | (uint32_t(row[2 * j + 1]) << 16);
+      for (int c = 0; c < N / 8; ++c) {
+        const uint4 x = reinterpret_cast<const uint4*>(row)[c];
+        out[4 * c] = x.x; out[4 * c + 1] = x.y; out[4 * c + 2] = x.z; out[4 * c + 3] = x.w;
       }
-    } else if constexpr (PK) {
+    } else {
+#pragma unroll
+      for (int j = 0; j < N / 2; ++j) out[j] = uint32_t(row[2 * j]) | (uint32_t(row[2 * j + 1]) << 16);
+    }
+  } else if constexpr (PK) {
+    if (pseg >= 0) {
+      const Seg& g = s[pseg];
       const int64_t bh = b * Hkv + kvh;
       for (int j = 0; j < N / 2; ++j) {
-        const float x0 = packed_elem(g, is_k, bh, D, tl, d0 + 2 * j, norm);
-        const float x1 = packed_elem(g, is_k, bh, D, tl, d0 + 2 * j + 1, norm);
+        const float x0 = packed_elem(g, is_k, bh, D, ptl, d0 + 2 * j, norm);
+        const float x1 = packed_elem(g, is_k, bh, D, ptl, d0 + 2 * j + 1, norm);
         out[j] = uint32_t(__half_as_ushort(__float2half_rn(x0))) | (uint32_t(__half_as_ushort(__float2half_rn(x1))) << 16);
       }
     }
-    return;
   }
 }
 
@@ -184,14 +197,17 @@ __global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs a) {
     float dot[HPW];
 #pragma unroll
     for (int hh = 0; hh < HPW; ++hh) dot[hh] = 0.f;
+    // no per-iteration guard on the head (a wave-uniform branch in the loop
+    // serialized it on LDS latency): heads past NREP read the last head's
+    // query and their logits are dropped below
 #pragma unroll 8
     for (int i = 0; i < D / 2; ++i) {
       const uint32_t k2 = kt[lane][i];
       const float k0 = h2f(uint16_t(k2 & 0xffffu)), k1 = h2f(uint16_t(k2 >> 16));
 #pragma unroll
       for (int hh = 0; hh < HPW; ++hh) {
-        const int h = wave + 4 * hh;
-        if (h < NREP) dot[hh] = fmaf(qs[h][2 * i + 1], k1, fmaf(qs[h][2 * i], k0, dot[hh]));
+        const int h = min(wave + 4 * hh, NREP - 1);
+        dot[hh] = fmaf(qs[h][2 * i + 1], k1, fmaf(qs[h][2 * i], k0, dot[hh]));
       }
     }
     const bool live = c0 + lane < i1;
