@@ -89,15 +89,16 @@ static_assert(plan_inv_ok<2>() && plan_inv_ok<3>() && plan_inv_ok<4>(), "plan in
 using detail::FusedArgs;
 
 // waves per SIMD: one for G-token waves (G > 64); for 64-token waves two,
-// and three in attn.V-only mode (AVO).  Three fit the registers of up to 4
+// and four in attn.V-only mode (AVO).  Three fit the registers of up to 4
 // query heads per KV head, but measured slower for the decode step (~1.5 us
-// at the headline): each wave keeps one block's loads in flight, and the
-// memory system streams the cache faster with fewer requests in flight per
-// CU (the same trend as load-only probes).  The lighter attn.V-only waves
-// measured ~1 us faster with three.
+// at the headline): each wave keeps one block's loads in flight (10 KB at
+// 4-bit), and the memory system streams the cache faster with fewer requests
+// in flight per CU (the same trend as load-only probes).  An attn.V-only
+// block is 3 KB (2-bit, G = 64) and its waves need <= 104 VGPRs: four per
+// SIMD measured ~0.6 us faster than three, three ~1 us faster than two.
 template <int G, int NREP, bool QS, bool AVO = false>
 constexpr int fused_waves_per_simd() {
-  return G > TOKEN_BLOCK ? 1 : AVO && NREP <= 4 && !QS ? 3 : 2;
+  return G > TOKEN_BLOCK ? 1 : AVO && NREP <= 4 && !QS ? 4 : 2;
 }
 
 // Workgroup shape: one workgroup per CU, filling every SIMD to the register
