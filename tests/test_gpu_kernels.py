@@ -499,6 +499,36 @@ def test_decode_attention_long_range_repeated():
         assert ((got.float() - ref).abs().max() / ref.abs().max()).item() < TOL
 
 
+@pytest.mark.parametrize("kbits,vbits,R", [(4, 4, 0), (2, 4, 128)])
+def test_decode_attention_full_size(kbits, vbits, R):
+    """The benchmark's shapes at full size: B=8, 32 query / 8 KV heads, D=128,
+    32768 tokens, asym G=32; 4-bit K and V all packed (the headline step) and
+    2-bit K / 4-bit V with a 128-token fp16 window (one layer of config 4).
+    Reference: fp32 attention over K/V dequantized by the library (unpack is
+    bit-exact to the oracle elsewhere), query heads grouped per KV head."""
+    B, Hkv, nrep, D, T = 8, 8, 4, 128, 32768
+    Tq = T - R
+    gen = torch.Generator(device=DEV).manual_seed(kbits * 10 + vbits + R)
+    k = torch.randn(B, Hkv, T, D, generator=gen, device=DEV).to(torch.float16)
+    v = torch.randn(B, Hkv, T, D, generator=gen, device=DEV).to(torch.float16)
+    k[..., :4] *= 10  # outlier channels, as in the benchmark's data
+    q = torch.randn(B, Hkv * nrep, D, generator=gen, device=DEV).to(torch.float16)
+    kst = ops.PackedStore("channel", B, Hkv, D, 32, kbits, "asymmetric", DEV, t_cap=Tq)
+    vst = ops.PackedStore("token", B, Hkv, D, 32, vbits, "asymmetric", DEV, t_cap=Tq)
+    kst.append(k[:, :, :Tq])
+    vst.append(v[:, :, :Tq])
+    kr = k[:, :, Tq:] if R else None
+    vr = v[:, :, Tq:] if R else None
+    got = ops.decode_attention(q, None, kst, kr, None, vst, vr, D ** -0.5).float()
+    kd = torch.cat([kst.dequant(dtype=torch.float32), k[:, :, Tq:].float()], dim=2)
+    del k
+    lg = torch.matmul(q.float().view(B, Hkv, nrep, D), kd.transpose(-1, -2).contiguous()) * D ** -0.5
+    del kd
+    vd = torch.cat([vst.dequant(dtype=torch.float32), v[:, :, Tq:].float()], dim=2)
+    ref = torch.matmul(torch.softmax(lg, dim=-1), vd).view(B, Hkv * nrep, D)
+    assert ((got - ref).abs().max() / ref.abs().max()).item() < TOL
+
+
 def test_decode_attention_graph_replay():
     """The decode step captured in a HIP graph and replayed several times (eager
     work between replays): every replay equals the eager result."""
