@@ -1,0 +1,56 @@
+"""The fused decode step inside transformers' models.
+
+Registers the attention implementation ``"innerq_fused"``
+(``AttentionInterface``, with sdpa's mask construction).  A model loaded with
+``attn_implementation="innerq_fused"`` whose generation cache is the drop-in
+``DynamicCache`` (``InnerqLlamaForCausalLM`` builds it) decodes each new token
+with ``InnerqDynamicLayer.attend()``: QK^T, softmax and attn.V over the packed
+K and V (``iq_decode_attention``), with no dense K/V in between.  The
+reference instead dequantizes the whole cache in ``update()`` and runs the
+model's attention over it (src/innerq/cache.py:242-270,
+TF/models/llama/modeling_llama.py:201-210); prefill, padded batches and
+layouts the fused kernels do not take keep that path.
+"""
+from __future__ import annotations
+
+import torch
+from transformers import AttentionInterface
+from transformers.integrations.sdpa_attention import sdpa_attention_forward
+from transformers.masking_utils import AttentionMaskInterface, sdpa_mask
+
+from .cache import FUSED_ATTENTION
+
+
+def _masks_tokens(attention_mask) -> bool:
+    if attention_mask is None:
+        return False
+    if attention_mask.dtype == torch.bool:
+        return not bool(attention_mask.all())
+    return bool((attention_mask < 0).any())
+
+
+def innerq_fused_attention(module, query, key, value, attention_mask, dropout: float = 0.0, scaling=None,
+                           **kwargs):
+    """transformers attention function: query [B, Hq, q_len, D]; returns
+    ([B, q_len, Hq, D], None).  A key tensor tagged by DynamicCache.update
+    (fused-decode mode, one new token) is served by its layer's attend();
+    anything else by sdpa over the given (or, for a tagged step that attend()
+    cannot take, the layer's dequantized) K and V."""
+    layer = getattr(key, "_innerq_layer", None)
+    if layer is None:
+        return sdpa_attention_forward(module, query, key, value, attention_mask, dropout=dropout, scaling=scaling,
+                                      **kwargs)
+    if scaling is None:
+        scaling = query.shape[-1] ** -0.5
+    nrep = query.shape[1] // key.shape[1]
+    if (_masks_tokens(attention_mask) or dropout or query.dtype != torch.float16 or query.shape[-1] not in (64, 128)
+            or nrep not in (1, 2, 4, 8) or query.shape[1] != nrep * key.shape[1]):
+        k, v = layer.get_deq_tensors()
+        return sdpa_attention_forward(module, query, k, v, attention_mask, dropout=dropout, scaling=scaling,
+                                      **kwargs)
+    out = layer.attend(query, scaling)  # [B, Hq, 1, D]
+    return out.transpose(1, 2).contiguous(), None
+
+
+AttentionInterface.register(FUSED_ATTENTION, innerq_fused_attention)
+AttentionMaskInterface.register(FUSED_ATTENTION, sdpa_mask)

@@ -29,6 +29,9 @@ from transformers.cache_utils import Cache, CacheLayerMixin
 from . import ops
 from .quant import QMode
 
+# attn_implementation name of the fused decode path (innerq_amd.attention)
+FUSED_ATTENTION = "innerq_fused"
+
 
 class _Quantized:
     """The packed tokens of one role (K or V) of a layer.
@@ -320,6 +323,15 @@ class InnerqDynamicLayer(CacheLayerMixin):
         else:
             self.add_to_cache(key_states, value_states)
 
+    def fused_decode_ready(self, key_states: torch.Tensor) -> bool:
+        """Whether attend() can serve this step: one new token per sequence, a
+        prefilled full-attention layer, K grouped along head_dim and V along
+        tokens (asym or sym)."""
+        if self.is_sliding or not self.is_initialized or key_states.shape[-2] != 1:
+            return False
+        return all(q is None or (q.mode != QMode.HYBRID and q.axis == want)
+                   for q, want in ((self._kq, "channel"), (self._vq, "token")))
+
     def attend(self, query_states: torch.Tensor, scaling: float) -> torch.Tensor:
         """Decode attention of one new token per sequence over this layer's cache:
         softmax(q K^T * scaling, fp32) -> fp16 -> @ V (TF/models/llama/modeling_llama.py:201-210),
@@ -436,6 +448,22 @@ class DynamicCache(Cache):
                 else:
                     layers.append(InnerqDynamicLayer(config=config, layer_idx=layer_idx))
         super().__init__(layers=layers, offloading=offloading, offload_only_non_sliding=offload_only_non_sliding)
+        # a model running the fused attention (attn_implementation "innerq_fused")
+        # decodes over the packed stores without materializing K and V
+        self.fused_decode = config is not None and getattr(config, "_attn_implementation", None) == FUSED_ATTENTION
+
+    def update(self, key_states: torch.Tensor, value_states: torch.Tensor, layer_idx: int, *args, **kwargs):
+        """Cache.update.  In fused-decode mode a one-token step that the layer's
+        attend() can serve is appended without materializing K and V; the
+        returned key tensor carries the layer (``_innerq_layer``) for the
+        fused attention function, which reads the packed cache through it."""
+        if self.fused_decode and layer_idx < len(self.layers):
+            layer = self.layers[layer_idx]
+            if layer.fused_decode_ready(key_states):
+                layer.append(key_states, value_states)
+                key_states._innerq_layer = layer
+                return key_states, value_states
+        return super().update(key_states, value_states, layer_idx, *args, **kwargs)
 
     def __iter__(self):
         for layer in self.layers:

@@ -100,3 +100,41 @@ def test_model_hooks_install_the_drop_in_cache():
     cache = kw["past_key_values"]
     assert isinstance(cache, C.DynamicCache) and len(cache.layers) == 2
     assert cache.layers[0].key_bits == 4 and cache.layers[1].value_bits == 2
+
+
+def test_fused_attention_registered():
+    """Importing innerq_amd.models registers the "innerq_fused" attention (and
+    sdpa's mask construction for it); a cache built from a config that selects
+    it decodes in fused mode."""
+    from transformers import AttentionInterface, LlamaConfig
+    from transformers.masking_utils import ALL_MASK_ATTENTION_FUNCTIONS
+    import innerq_amd.models  # noqa: F401
+    from innerq_amd.attention import innerq_fused_attention
+    assert AttentionInterface._global_mapping[C.FUSED_ATTENTION] is innerq_fused_attention
+    assert C.FUSED_ATTENTION in ALL_MASK_ATTENTION_FUNCTIONS._global_mapping
+    cfg = LlamaConfig(num_hidden_layers=2, num_attention_heads=4, num_key_value_heads=2, hidden_size=256,
+                      intermediate_size=32, vocab_size=16)
+    cfg._attn_implementation = C.FUSED_ATTENTION
+    assert C.DynamicCache(config=cfg).fused_decode
+    cfg._attn_implementation = "sdpa"
+    assert not C.DynamicCache(config=cfg).fused_decode
+    assert not C.DynamicCache().fused_decode
+
+
+def test_fused_attention_untagged_keys_take_sdpa():
+    """Keys that no fused-mode cache tagged (prefill, other caches) go to sdpa."""
+    import torch
+    from transformers.integrations.sdpa_attention import sdpa_attention_forward
+    from innerq_amd.attention import innerq_fused_attention
+
+    class M(torch.nn.Module):
+        is_causal = True
+        num_key_value_groups = 2
+
+    g = torch.Generator().manual_seed(0)
+    q = torch.randn(1, 4, 5, 16, generator=g)
+    k = torch.randn(1, 2, 5, 16, generator=g)
+    v = torch.randn(1, 2, 5, 16, generator=g)
+    a, _ = innerq_fused_attention(M(), q, k, v, None, scaling=0.25)
+    b, _ = sdpa_attention_forward(M(), q, k, v, None, scaling=0.25)
+    assert torch.equal(a, b)

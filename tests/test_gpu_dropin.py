@@ -186,3 +186,77 @@ def test_dynamic_cache_from_llama_config():
     assert K is k and V is v
     K, V = cache.update(k[:, :, :1], v[:, :, :1], 1)
     assert K.shape == (1, 2, 101, 64) and cache.get_seq_length(1) == 101
+
+
+def _tiny_llama(preset):
+    from transformers import LlamaConfig
+    from innerq_amd.models import InnerqLlamaForCausalLM
+    cfg = LlamaConfig(num_hidden_layers=2, num_attention_heads=8, num_key_value_heads=2, hidden_size=512,
+                      intermediate_size=256, vocab_size=64, max_position_embeddings=512)
+    for k, v in PRESETS[preset].items():
+        setattr(cfg, k, v)
+    torch.manual_seed(0)
+    return InnerqLlamaForCausalLM(cfg).to(device=DEV, dtype=torch.float16).eval()
+
+
+def _count_attend(monkeypatch):
+    calls = [0]
+    orig = C.InnerqDynamicLayer.attend
+
+    def attend(self, *a, **kw):
+        calls[0] += 1
+        return orig(self, *a, **kw)
+
+    monkeypatch.setattr(C.InnerqDynamicLayer, "attend", attend)
+    return calls
+
+
+@pytest.mark.parametrize("preset", ["innerq_base", "mixed_k2v4_flush32", "hybrid_v"])
+def test_fused_attention_in_llama_matches_reference_path(preset, monkeypatch):
+    """A random 2-layer Llama (8 query / 2 KV heads, head_dim 64) on the drop-in
+    cache, teacher-forced through 40 decode steps after a 200-token prefill:
+    logits with attn_implementation="innerq_fused" (attend() over the packed
+    cache; hybrid V falls back to the dequantized cache) against the
+    reference's path (update() dequantizes the cache, eager attention), same
+    weights and tokens."""
+    model = _tiny_llama(preset)
+    gen = torch.Generator(device=DEV).manual_seed(7)
+    ids = torch.randint(0, 64, (2, 200), generator=gen, device=DEV)
+    dec = torch.randint(0, 64, (2, 40), generator=gen, device=DEV)
+    logits = {}
+    calls = _count_attend(monkeypatch)
+    for attn in ("eager", "innerq_fused"):
+        model.config._attn_implementation = attn
+        cache = C.DynamicCache(config=model.config)
+        assert cache.fused_decode == (attn == "innerq_fused")
+        steps = []
+        with torch.no_grad():
+            model(ids, past_key_values=cache, use_cache=True)
+            for t in range(dec.shape[1]):
+                steps.append(model(dec[:, t:t + 1], past_key_values=cache, use_cache=True).logits[:, -1].float())
+        assert cache.get_seq_length() == 240
+        logits[attn] = torch.stack(steps)
+    ref, got = logits["eager"], logits["innerq_fused"]
+    assert ((got - ref).abs().max() / ref.abs().max()).item() < 2e-2
+    # every decode step of both layers went through attend(), except for hybrid V
+    assert calls[0] == (0 if preset == "hybrid_v" else 2 * dec.shape[1])
+
+
+def test_fused_attention_generate(monkeypatch):
+    """generate() on the hooked model with attn_implementation="innerq_fused":
+    the hook's cache decodes in fused mode; the step scores match those of the
+    reference's path for a short greedy continuation."""
+    model = _tiny_llama("asym4_nosink")
+    ids = torch.randint(0, 64, (1, 150), generator=torch.Generator(device=DEV).manual_seed(3), device=DEV)
+    outs = {}
+    calls = _count_attend(monkeypatch)
+    for attn in ("eager", "innerq_fused"):
+        model.config._attn_implementation = attn
+        with torch.no_grad():
+            outs[attn] = model.generate(ids, max_new_tokens=6, do_sample=False, output_scores=True,
+                                        return_dict_in_generate=True)
+        assert outs[attn].sequences.shape == (1, 156)
+    ref = torch.stack(outs["eager"].scores).float()
+    got = torch.stack(outs["innerq_fused"].scores).float()
+    assert ((got - ref).abs().max() / ref.abs().max()).item() < 2e-2
+    assert calls[0] == 2 * 5  # the 5 decode steps after the prefill, both layers
