@@ -96,6 +96,68 @@ class PackedStore:
         groups = n * (self.D // self.group) if self.axis == "channel" else (n // self.group) * self.D
         return self.B * self.H * (n * self.D * self.bits // 8 + groups * m)
 
+    # --- wire / on-disk format ------------------------------------------------
+    # A safetensors blob: tensors "codes" int32 [B*H, U, words per unit] and
+    # "meta" int16 [B*H, U, halves per unit] holding the first U = ceil(length /
+    # unit) units of every (batch, head) exactly as they lie in HBM (unit = a
+    # 64-token block for axis 'channel', a G-token group for 'token'; the word
+    # and half order inside a unit is the store layout), plus string metadata:
+    # format "innerq-packed-store", version, axis, B, H, D, group, bits, mode
+    # ("asymmetric" | "symmetric"), length, unit.  Codes are LSB-first fields of
+    # little-endian u32 words; sym fields are offset binary.
+    WIRE_FORMAT, WIRE_VERSION = "innerq-packed-store", "1"
+
+    def to_bytes(self) -> bytes:
+        """The store's valid units in the wire format (see above)."""
+        from safetensors.torch import save
+        bh, u = self.B * self.H, self.unit
+        used = -(-self.length // u)
+        nu = self.t_cap // u
+        codes = self.codes.view(bh, nu, -1)[:, :used].contiguous().cpu() if nu else \
+            torch.empty(bh, 0, 0, dtype=torch.int32)
+        meta = self.meta.view(bh, nu, -1)[:, :used].contiguous().cpu() if nu else \
+            torch.empty(bh, 0, 0, dtype=torch.int16)
+        md = {"format": self.WIRE_FORMAT, "version": self.WIRE_VERSION, "axis": self.axis, "B": self.B,
+              "H": self.H, "D": self.D, "group": self.group, "bits": self.bits,
+              "mode": "symmetric" if self.mode == IQ_MODE_SYM else "asymmetric", "length": self.length, "unit": u}
+        return save({"codes": codes, "meta": meta}, metadata={k: str(v) for k, v in md.items()})
+
+    @classmethod
+    def from_bytes(cls, blob: bytes, device, t_cap: int = 0) -> "PackedStore":
+        """A store on ``device`` holding what to_bytes() wrote (capacity at least
+        ``t_cap`` tokens).  Raises ValueError on a foreign or inconsistent blob."""
+        import json
+        import struct
+        from safetensors.torch import load
+        n = struct.unpack("<Q", blob[:8])[0]
+        md = json.loads(blob[8:8 + n].decode("utf-8")).get("__metadata__", {})
+        if md.get("format") != cls.WIRE_FORMAT or md.get("version") != cls.WIRE_VERSION:
+            raise ValueError(f"not an {cls.WIRE_FORMAT} v{cls.WIRE_VERSION} blob: {md.get('format')!r} "
+                             f"v{md.get('version')!r}")
+        t = load(blob)
+        B, H, D, group, bits, length = (int(md[k]) for k in ("B", "H", "D", "group", "bits", "length"))
+        st = cls(md["axis"], B, H, D, group, bits, md["mode"], device, t_cap=max(t_cap, length))
+        u = st.unit
+        used, nu = -(-length // u), st.t_cap // u
+        if int(md["unit"]) != u:
+            raise ValueError("unit does not match the axis and group")
+        cv, mv = st.codes.view(B * H, nu, -1), st.meta.view(B * H, nu, -1)
+        if tuple(t["codes"].shape) != (B * H, used, cv.shape[2]) or tuple(t["meta"].shape) != (B * H, used, mv.shape[2]):
+            raise ValueError("codes / meta shapes do not match the store header")
+        cv[:, :used].copy_(t["codes"])
+        mv[:, :used].copy_(t["meta"])
+        st.length = length
+        return st
+
+    def save(self, path: str) -> None:
+        with open(path, "wb") as f:
+            f.write(self.to_bytes())
+
+    @classmethod
+    def load(cls, path: str, device, t_cap: int = 0) -> "PackedStore":
+        with open(path, "rb") as f:
+            return cls.from_bytes(f.read(), device, t_cap)
+
     # --- writes -------------------------------------------------------------
     def append(self, x: torch.Tensor, norm: Optional[torch.Tensor] = None) -> None:
         """Quantize x [B,H,n,D] fp16 and append it (quantize-on-append)."""

@@ -253,6 +253,27 @@ def test_qk_gemv_many_runs(bits, G, mode, norm):
     assert A.rel_err(got.cpu().numpy(), ref.cpu().numpy()) < TOL
 
 
+@pytest.mark.parametrize("axis,bits,mode,n0,n1", [("channel", 4, "asymmetric", 150, 50),
+                                                  ("token", 3, "symmetric", 128, 64)])
+def test_store_wire_round_trip(axis, bits, mode, n0, n1):
+    """A store written to the wire format and read back onto the device (a
+    partial last K block included) dequantizes bit for bit like the original,
+    decodes the same, and keeps appending like it."""
+    B, H, D, G = 2, 2, 128, 32
+    x = torch.randn(B, H, n0 + n1, D, generator=torch.Generator(device=DEV).manual_seed(bits), device=DEV).half()
+    st = ops.PackedStore(axis, B, H, D, G, bits, mode, DEV)
+    st.append(x[:, :, :n0])
+    back = ops.PackedStore.from_bytes(st.to_bytes(), DEV)
+    assert back.length == n0
+    assert torch.equal(back.dequant(dtype=torch.float32), st.dequant(dtype=torch.float32))
+    st.append(x[:, :, n0:])
+    back.append(x[:, :, n0:])
+    assert torch.equal(back.dequant(dtype=torch.float32), st.dequant(dtype=torch.float32))
+    if axis == "channel":
+        q = torch.randn(B, 4 * H, D, device=DEV).half()
+        assert torch.equal(ops.qk_gemv(q, back, 0.1), ops.qk_gemv(q, st, 0.1))
+
+
 def peaked_p(B, Hq, T, seed, std=2.0):
     logits = synth.normal((B, Hq, T), seed=seed, std=std).astype(np.float64)
     return A.softmax(logits).astype(np.float16)

@@ -1,0 +1,76 @@
+"""The packed store's wire / on-disk format (PackedStore.to_bytes / from_bytes,
+save / load) on the host: a round trip keeps every valid unit bit for bit,
+foreign or inconsistent blobs are refused.  No kernel runs here; the GPU
+tests check that a loaded store decodes and keeps appending like the
+original."""
+import json
+import struct
+
+import pytest
+import torch
+
+from innerq_amd import ops
+
+
+def _filled(axis, bits, mode, length, t_cap, seed):
+    g = torch.Generator().manual_seed(seed)
+    st = ops.PackedStore(axis, 2, 3, 128, 32, bits, mode, "cpu", t_cap=t_cap)
+    st.codes.copy_(torch.randint(-2**31, 2**31 - 1, st.codes.shape, dtype=torch.int32, generator=g))
+    st.meta.copy_(torch.randint(-2**15, 2**15 - 1, st.meta.shape, dtype=torch.int16, generator=g))
+    st.length = length
+    return st
+
+
+def _units(st):
+    u = st.unit
+    used = -(-st.length // u)
+    nu = st.t_cap // u
+    bh = st.B * st.H
+    return st.codes.view(bh, nu, -1)[:, :used], st.meta.view(bh, nu, -1)[:, :used]
+
+
+@pytest.mark.parametrize("axis,bits,mode,length", [("channel", 4, "asymmetric", 150), ("channel", 3, "symmetric", 64),
+                                                   ("token", 2, "asymmetric", 96), ("token", 4, "symmetric", 0)])
+def test_round_trip(axis, bits, mode, length, tmp_path):
+    st = _filled(axis, bits, mode, length, 200, seed=bits + length)
+    p = tmp_path / "store.safetensors"
+    st.save(str(p))
+    back = ops.PackedStore.load(str(p), "cpu", t_cap=500)
+    assert (back.axis, back.B, back.H, back.D, back.group, back.bits, back.mode, back.length) == \
+        (st.axis, st.B, st.H, st.D, st.group, st.bits, st.mode, st.length)
+    assert back.t_cap >= 500
+    for a, b in zip(_units(st), _units(back)):
+        assert torch.equal(a, b)
+    # only the valid units travel: the blob is the packed bytes plus a small header
+    hdr = struct.unpack("<Q", st.to_bytes()[:8])[0]
+    used = -(-length // st.unit)
+    body = st.B * st.H * used * (st.codes.numel() // (st.B * st.H * (st.t_cap // st.unit)) * 4 +
+                                 st.meta.numel() // (st.B * st.H * (st.t_cap // st.unit)) * 2)
+    assert len(st.to_bytes()) == 8 + hdr + body
+
+
+def test_header_fields():
+    st = _filled("channel", 4, "asymmetric", 70, 128, seed=1)
+    blob = st.to_bytes()
+    n = struct.unpack("<Q", blob[:8])[0]
+    md = json.loads(blob[8:8 + n])["__metadata__"]
+    assert md == {"format": "innerq-packed-store", "version": "1", "axis": "channel", "B": "2", "H": "3",
+                  "D": "128", "group": "32", "bits": "4", "mode": "asymmetric", "length": "70", "unit": "64"}
+
+
+def test_foreign_and_inconsistent_blobs_are_refused():
+    from safetensors.torch import save
+    st = _filled("token", 4, "asymmetric", 64, 64, seed=2)
+    blob = st.to_bytes()
+    with pytest.raises(ValueError):
+        ops.PackedStore.from_bytes(save({"x": torch.zeros(1)}, metadata={"format": "other"}), "cpu")
+    n = struct.unpack("<Q", blob[:8])[0]
+    md = json.loads(blob[8:8 + n])["__metadata__"]
+    from safetensors.torch import load
+    t = load(blob)
+    bad = dict(md, length="96")  # more tokens than the units hold
+    with pytest.raises(ValueError):
+        ops.PackedStore.from_bytes(save(t, metadata=bad), "cpu")
+    bad = dict(md, version="2")
+    with pytest.raises(ValueError):
+        ops.PackedStore.from_bytes(save(t, metadata=bad), "cpu")
