@@ -55,6 +55,28 @@ def make_store(axis, B, Hkv, T, D, G, bits, mode, seed, dev, n_out=4, factor=10.
     return st
 
 
+def clock_warmup(dev, ms: float = 40.0) -> None:
+    """Bring the GPU out of its idle power state before anything is timed: plain
+    256 MiB device copies for about ``ms`` milliseconds.  Without it the first
+    ~200 decode steps after an idle period run up to ~15% slower while the
+    clocks ramp (measured per launch with HIP events: 67.7 -> 60.1 us for the
+    fused kernel over the first 13 ms of back-to-back steps), so a short
+    warm-up of the workload itself would time the ramp."""
+    import torch
+    src = torch.empty(256 << 20, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(2000):  # bounded: ~70 us per copy, stops at ``ms``
+        for _ in range(20):
+            dst.copy_(src)
+        e1.record()
+        e1.synchronize()
+        if e0.elapsed_time(e1) >= ms:
+            break
+    del src, dst
+
+
 def time_loop(fn, n, warmup):
     import torch
     for i in range(warmup):
@@ -146,6 +168,7 @@ def bench_headline(args):
     def step(i):
         ops.decode_attention(q, None, ks[i % C], None, None, vs[i % C], None, scale, out=out)
 
+    clock_warmup(dev)
     us_step = time_loop(step, args.steps, args.warmup)
     # the split stage alone: one launch of the fused split kernel here (K and V share
     # their format and every token is packed); the rest of the step is the combine of
@@ -204,6 +227,7 @@ def bench_config(args):
         q = torch.randn(B, Hq, D, device=dev, dtype=torch.float16)
         lg = torch.empty(B, Hq, T, device=dev)
         fn = lambda i: ops.qk_gemv(q, ks[i % C], D ** -0.5, out=lg)
+        clock_warmup(dev)
         us = time_loop(fn, args.steps, args.warmup)
         ug = time_graph(fn, 4 * C, max(1, args.steps // 4))
         b = gemv_bytes(B, Hkv, T, D, G, 4, "asymmetric", "channel")
@@ -215,6 +239,7 @@ def bench_config(args):
             p = torch.softmax(torch.randn(B, Hq, T, device=dev) * 2.0, dim=-1).to(torch.float16)
             out = torch.empty(B, Hq, D, device=dev, dtype=torch.float16)
             fn = lambda i: ops.av_gemv(p, vs[i % C], out=out)
+            clock_warmup(dev)
             us = time_loop(fn, args.steps, args.warmup)
             ug = time_graph(fn, C, max(1, args.steps // 4))
             b = gemv_bytes(B, Hkv, T, D, G, 2, mode, "token")
@@ -237,6 +262,8 @@ def bench_config(args):
             ap.length = 0
             ap.append(knew)  # quantize-on-append of one token per sequence (K, flush 1)
 
+        clock_warmup(dev)
+
         us = time_loop(step, args.steps, args.warmup)
         ug = time_graph(step, C, max(1, args.steps // 4))
         b = 2 * gemv_bytes(B, Hkv, Tq, D, G, 3, "symmetric", "channel")
@@ -254,6 +281,8 @@ def bench_config(args):
         def step(i):
             for l in range(L):
                 ops.decode_attention(q, None, ks[l], kr, None, vs[l], vr, D ** -0.5, out=out)
+
+        clock_warmup(dev)
 
         us = time_loop(step, max(1, args.steps // 10), 2)
         ug = time_graph(step, 1, max(1, args.steps // 10))
