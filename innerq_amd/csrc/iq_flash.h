@@ -138,6 +138,7 @@ struct FusedSmem {
 // of it changed nothing).  The query, reused by every workgroup of a head,
 // keeps the default policy.
 constexpr int STREAM = 2;  // cache policy bits of a streaming load: nt
+constexpr unsigned XCDS = 8;  // accelerator complex dies of an MI355X
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, int(bytes), 0x00020000);
@@ -337,8 +338,14 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS, AVO>::NT), (fused_waves_pe
   // claim wave blocks from a counter in LDS (the first two per wave are
   // fixed), so they all finish the run within about one block of each other
   // whatever the issue arbitration favours. ----
-  const int i0 = int(int64_t(blockIdx.x) * a.nitems / gridDim.x);
-  const int i1 = int(int64_t(blockIdx.x + 1) * a.nitems / gridDim.x);
+  // Share sh of the list for workgroup b: workgroups are dealt to the XCDs
+  // round robin (b runs on XCD b % 8), so sh = (b % 8) * (grid / 8) + b / 8
+  // gives each XCD one contiguous eighth of the list (its own heads, whole)
+  // instead of every eighth share: -1 us per headline step (A/B, five rounds).
+  const int sh = gridDim.x % XCDS == 0 ? int(blockIdx.x % XCDS) * int(gridDim.x / XCDS) + int(blockIdx.x / XCDS)
+                                       : int(blockIdx.x);
+  const int i0 = int(int64_t(sh) * a.nitems / gridDim.x);
+  const int i1 = int(int64_t(sh + 1) * a.nitems / gridDim.x);
   if (i0 >= i1) return;  // uniform over the workgroup, before any barrier
   struct Run {
     int bh, split0, nsplit, nb;  // (batch, KV head), first split, splits, wave blocks
@@ -353,7 +360,7 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS, AVO>::NT), (fused_waves_pe
   };
   // wave block (within the (batch, KV head)) of run-relative index idx
   auto block_of = [&](const Run& r, int idx) { return r.split0 * BPS + idx; };
-  // the workgroup whose share holds global split s: max c with c*nitems/grid <= s
+  // the share holding global split s: max c with c*nitems/grid <= s
   auto share_of = [&](int s) {
     return int(((int64_t(s) + 1) * gridDim.x + a.nitems - 1) / a.nitems) - 1;
   };
@@ -365,7 +372,7 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS, AVO>::NT), (fused_waves_pe
   // splits hold it.
   auto run_slots = [&](const Run& r, int& slot, int& nr) {
     const int c0 = share_of(r.bh * a.nsplit);
-    slot = int(blockIdx.x) - c0;
+    slot = sh - c0;
     nr = share_of((r.bh + 1) * a.nsplit - 1) - c0 + 1;
   };
 
