@@ -8,9 +8,10 @@
 // iq_flash_k{2,3,4}.hip instantiate it (one translation unit per K width, so
 // the instantiations compile in parallel) and iq_flash.hip holds the entry.
 //
-// Persistent and software pipelined.  One workgroup per CU (as many waves as
-// the register allocation allows per SIMD) takes an equal contiguous share of
-// the (batch, KV head)-major list of FSPLIT-token splits and processes it as
+// Persistent and software pipelined.  One workgroup per CU (waves per SIMD:
+// fused_waves_per_simd) takes an equal contiguous share of the (batch, KV
+// head)-major list of FSPLIT-token splits (each XCD one contiguous eighth of
+// the list), loaded with the non-temporal cache policy, and processes it as
 // runs, the maximal pieces of one (batch, KV head).  Inside a run the waves
 // claim wave blocks of WTOK tokens (lane = token for QK^T) from a counter in
 // LDS, so they finish the run together, and each wave keeps a running
@@ -32,10 +33,10 @@
 //   attn.V lane = column d = lane + 64 e over the block's V groups.
 // At the end of a run the waves merge (rescale by exp2(m_w - m), sum in LDS)
 // and write the run's partial into split slot k for the k-th run of its
-// (batch, KV head); the slots past the last run's get empty statistics.  The next run's query records come from
-// q values prefetched during the run (a key normalization, which the
-// reference applies to the dequantized keys, cache.py:128-133 and 249, is
-// folded into q as hi/lo fp16 parts of q*n).
+// (batch, KV head); the slots past the last run's get empty statistics.  Each
+// run starts by building its query records from q loaded at that point (a key
+// normalization, which the reference applies to the dequantized keys,
+// cache.py:128-133 and 249, is folded into q as hi/lo fp16 parts of q*n).
 //
 // The store formats follow the unfused kernels: K codes [B,H,t_cap/64,D/G,64,W],
 // V codes [B,H,t_cap/G,D,W]; sym or asym per store is a runtime flag (a
