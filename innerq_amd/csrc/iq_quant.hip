@@ -130,7 +130,7 @@ __device__ __forceinline__ void unpack_fields(const uint32_t* w, bool sym, int32
 }
 
 // ---- K: groups along head_dim, one thread per (b, h, t, g) ----------------
-template <int BITS, int G>
+template <int BITS, int G, bool DENSE>
 __global__ __launch_bounds__(256) void quant_k_kernel(const uint16_t* __restrict__ x, int64_t sxb, int64_t sxh,
                                                       int64_t sxt, const uint16_t* __restrict__ norm, int B,
                                                       int H, int n, int D, int sym, QuantOut o) {
@@ -187,22 +187,24 @@ __global__ __launch_bounds__(256) void quant_k_kernel(const uint16_t* __restrict
       reinterpret_cast<uint32_t*>(o.meta)[unit] = sz;
     }
   }
-  const int64_t row_el = (bh * n + t) * D + g * G;
-  if (o.codes_i32) {
+  if constexpr (DENSE) {  // the reference-format outputs (quant.py API)
+    const int64_t row_el = (bh * n + t) * D + g * G;
+    if (o.codes_i32) {
 #pragma unroll
-    for (int i = 0; i < G; ++i) o.codes_i32[row_el + i] = c[i];
-  }
-  if (o.signs16) {
+      for (int i = 0; i < G; ++i) o.codes_i32[row_el + i] = c[i];
+    }
+    if (o.signs16) {
 #pragma unroll
-    for (int i = 0; i < G; ++i) o.signs16[row_el + i] = __half_as_ushort(__float2half_rn(sg[i]));
+      for (int i = 0; i < G; ++i) o.signs16[row_el + i] = __half_as_ushort(__float2half_rn(sg[i]));
+    }
+    const int64_t red = (bh * n + t) * ng + g;
+    if (o.scale16) o.scale16[red] = __half_as_ushort(__float2half_rn(s));
+    if (o.zero16) o.zero16[red] = __half_as_ushort(__float2half_rn(z));
   }
-  const int64_t red = (bh * n + t) * ng + g;
-  if (o.scale16) o.scale16[red] = __half_as_ushort(__float2half_rn(s));
-  if (o.zero16) o.zero16[red] = __half_as_ushort(__float2half_rn(z));
 }
 
 // ---- V: groups along tokens, one thread per (b, h, token-group, d) --------
-template <int BITS, int G>
+template <int BITS, int G, bool DENSE>
 __global__ __launch_bounds__(256) void quant_v_kernel(const uint16_t* __restrict__ x, int64_t sxb, int64_t sxh,
                                                       int64_t sxt, int B, int H, int n, int D, int sym,
                                                       QuantOut o) {
@@ -245,17 +247,19 @@ __global__ __launch_bounds__(256) void quant_v_kernel(const uint16_t* __restrict
       reinterpret_cast<uint32_t*>(o.meta)[unit] = sz;
     }
   }
-  if (o.codes_i32 || o.signs16) {
+  if constexpr (DENSE) {  // the reference-format outputs (quant.py API)
+    if (o.codes_i32 || o.signs16) {
 #pragma unroll
-    for (int i = 0; i < G; ++i) {
-      const int64_t el = (bh * n + int64_t(gi) * G + i) * D + d;
-      if (o.codes_i32) o.codes_i32[el] = c[i];
-      if (o.signs16) o.signs16[el] = __half_as_ushort(__float2half_rn(sg[i]));
+      for (int i = 0; i < G; ++i) {
+        const int64_t el = (bh * n + int64_t(gi) * G + i) * D + d;
+        if (o.codes_i32) o.codes_i32[el] = c[i];
+        if (o.signs16) o.signs16[el] = __half_as_ushort(__float2half_rn(sg[i]));
+      }
     }
+    const int64_t red = (bh * ngn + gi) * D + d;
+    if (o.scale16) o.scale16[red] = __half_as_ushort(__float2half_rn(s));
+    if (o.zero16) o.zero16[red] = __half_as_ushort(__float2half_rn(z));
   }
-  const int64_t red = (bh * ngn + gi) * D + d;
-  if (o.scale16) o.scale16[red] = __half_as_ushort(__float2half_rn(s));
-  if (o.zero16) o.zero16[red] = __half_as_ushort(__float2half_rn(z));
 }
 
 // ---- dequantization (dense read path) --------------------------------------
@@ -530,7 +534,10 @@ int iq_quantize_k(const void* x, int64_t sx_b, int64_t sx_h, int64_t sx_t, const
              (uint16_t*)signs16};
   const int sym = mode == IQ_MODE_SYM;
   return dispatch_store_bits_group(bits, group, [&]<int BITS, int G>() {
-    quant_k_kernel<BITS, G><<<dim3(unsigned(ceil_div(total, 256))), 256, 0, (hipStream_t)stream>>>(
+    // the store-only append (no reference-format outputs) drops their registers
+    auto* kern = (codes_i32 || scale16 || zero16 || signs16) ? quant_k_kernel<BITS, G, true>
+                                                              : quant_k_kernel<BITS, G, false>;
+    kern<<<dim3(unsigned(ceil_div(total, 256))), 256, 0, (hipStream_t)stream>>>(
         (const uint16_t*)x, sx_b, sx_h, sx_t, (const uint16_t*)norm, B, H, n, D, sym, o);
     return launch_status();
   });
@@ -558,7 +565,9 @@ int iq_quantize_v(const void* x, int64_t sx_b, int64_t sx_h, int64_t sx_t, int B
              (uint16_t*)signs16};
   const int sym = mode == IQ_MODE_SYM;
   return dispatch_store_bits_group(bits, group, [&]<int BITS, int G>() {
-    quant_v_kernel<BITS, G><<<dim3(unsigned(ceil_div(total, 256))), 256, 0, (hipStream_t)stream>>>(
+    auto* kern = (codes_i32 || scale16 || zero16 || signs16) ? quant_v_kernel<BITS, G, true>
+                                                              : quant_v_kernel<BITS, G, false>;
+    kern<<<dim3(unsigned(ceil_div(total, 256))), 256, 0, (hipStream_t)stream>>>(
         (const uint16_t*)x, sx_b, sx_h, sx_t, B, H, n, D, sym, o);
     return launch_status();
   });
