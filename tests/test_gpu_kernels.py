@@ -550,6 +550,16 @@ def test_decode_attention_full_size(kbits, vbits, R):
     assert ((got - ref).abs().max() / ref.abs().max()).item() < TOL
 
 
+@pytest.mark.parametrize("B,Hkv,nrep,T", [(10, 10, 1, 768 + 40), (3, 8, 2, 4096 + 40)])
+def test_decode_attention_shares_straddle_heads(B, Hkv, nrep, T):
+    """More splits than workgroups, not a multiple of them: shares of one or two
+    splits cross (batch, KV head) boundaries (two runs in one workgroup), dealt
+    to the XCDs in contiguous eighths of the list."""
+    q, kst, vst, kr, vr, ref = _decode_inputs(B, Hkv, nrep, 64, T - 40, 40, 4, seed=B * Hkv + T)
+    got = ops.decode_attention(q, None, kst, kr, None, vst, vr, 64 ** -0.5)
+    assert ((got.float() - ref).abs().max() / ref.abs().max()).item() < TOL
+
+
 def test_decode_attention_graph_replay():
     """The decode step captured in a HIP graph and replayed several times (eager
     work between replays): every replay equals the eager result."""
