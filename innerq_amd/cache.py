@@ -344,6 +344,7 @@ class InnerqDynamicLayer(CacheLayerMixin):
             if q is not None and (q.mode == QMode.HYBRID or q.axis != want):
                 raise NotImplementedError(f"fused decode reads {name} grouped along the "
                                           f"{'head_dim' if want == 'channel' else 'token'} axis, asym or sym")
+        self._fused_pending = False
         q = query_states[:, :, 0]
         out = ops.decode_attention(
             q, self.keys_sink if self.keys_sink.shape[-2] else None, self._kq.store if self._kq else None,
@@ -459,9 +460,15 @@ class DynamicCache(Cache):
         fused attention function, which reads the packed cache through it."""
         if self.fused_decode and layer_idx < len(self.layers):
             layer = self.layers[layer_idx]
+            if getattr(layer, "_fused_pending", False):
+                # the previous tagged step never reached attend(): an attention
+                # other than "innerq_fused" read only the new token's K/V
+                raise RuntimeError("a fused-decode DynamicCache needs attn_implementation='innerq_fused'; "
+                                   "build a new cache after switching the attention implementation")
             if layer.fused_decode_ready(key_states):
                 layer.append(key_states, value_states)
                 key_states._innerq_layer = layer
+                layer._fused_pending = True
                 return key_states, value_states
         return super().update(key_states, value_states, layer_idx, *args, **kwargs)
 

@@ -260,3 +260,19 @@ def test_fused_attention_generate(monkeypatch):
     got = torch.stack(outs["innerq_fused"].scores).float()
     assert ((got - ref).abs().max() / ref.abs().max()).item() < 2e-2
     assert calls[0] == 2 * 5  # the 5 decode steps after the prefill, both layers
+
+
+def test_fused_cache_with_another_attention_fails_loudly():
+    """A fused-decode cache driven by a model whose attention is no longer
+    "innerq_fused" would feed that attention the new token alone: the next
+    step raises instead of returning wrong logits silently."""
+    model = _tiny_llama("asym4_nosink")
+    ids = torch.randint(0, 64, (1, 150), generator=torch.Generator(device=DEV).manual_seed(5), device=DEV)
+    model.config._attn_implementation = "innerq_fused"
+    cache = C.DynamicCache(config=model.config)
+    model.config._attn_implementation = "sdpa"  # no mask for one query token: nothing else would notice
+    with torch.no_grad():
+        model(ids, past_key_values=cache, use_cache=True)
+        model(ids[:, :1], past_key_values=cache, use_cache=True)  # tagged step read by sdpa
+        with pytest.raises(RuntimeError, match="innerq_fused"):
+            model(ids[:, :1], past_key_values=cache, use_cache=True)
