@@ -31,8 +31,14 @@ Pinning (what checks each function; see tests/test_oracle_*.py):
   * pack / unpack: bijection brute-forced over every code value at every lane
     position, 3-bit word-straddling codes 10 and 21 checked explicitly.
   * quantize_hybrid / dequantize_hybrid: golden vectors from the live reference.
-  * attn_ref: factored-sum formulation vs dequantize-then-matmul, float64 brute
-    force loops on tiny shapes, closed-form cases (constant codes).
+  * attn_ref (tests/test_oracle_attn.py): softmax(qk_logits), av_out and
+    decode_attention against transformers' own eager attention (repeat_kv +
+    eager_attention_forward) on KV heads with distinct data; float64 index
+    loops on tiny shapes with the GQA map kv = h // n_rep written out; the
+    factored group sums (qk_factored / av_factored) over quantized codes
+    against dequantize-then-matmul; each check rejects a planted mistake
+    (h % Hkv head map, missing 1/sqrt(D), softmax over the wrong axis,
+    dropped zero-point term).
   * cache_ref: golden traces of the live reference cache (token-index
     bookkeeping) and a length-only schedule simulator.
 """
