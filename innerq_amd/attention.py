@@ -21,12 +21,25 @@ from transformers.masking_utils import AttentionMaskInterface, sdpa_mask
 from .cache import FUSED_ATTENTION
 
 
+# (mask tensor, answer) of the last mask inspected: every layer of one forward
+# pass receives the same mask object, so the device-to-host read that the
+# answer needs happens once per decode step, not once per layer
+_last_mask: list = [None, False]
+
+
 def _masks_tokens(attention_mask) -> bool:
+    """Whether the mask hides any cache token (padding): the fused kernels attend
+    to every token."""
     if attention_mask is None:
         return False
+    if attention_mask is _last_mask[0]:
+        return _last_mask[1]
     if attention_mask.dtype == torch.bool:
-        return not bool(attention_mask.all())
-    return bool((attention_mask < 0).any())
+        ans = not bool(attention_mask.all())
+    else:
+        ans = bool((attention_mask < 0).any())
+    _last_mask[0], _last_mask[1] = attention_mask, ans
+    return ans
 
 
 def innerq_fused_attention(module, query, key, value, attention_mask, dropout: float = 0.0, scaling=None,
@@ -45,7 +58,6 @@ def innerq_fused_attention(module, query, key, value, attention_mask, dropout: f
     nrep = query.shape[1] // key.shape[1]
     if (_masks_tokens(attention_mask) or dropout or query.dtype != torch.float16 or query.shape[-1] not in (64, 128)
             or nrep not in (1, 2, 4, 8) or query.shape[1] != nrep * key.shape[1]):
-        layer._fused_pending = False
         k, v = layer.get_deq_tensors()
         return sdpa_attention_forward(module, query, k, v, attention_mask, dropout=dropout, scaling=scaling,
                                       **kwargs)

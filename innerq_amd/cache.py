@@ -344,7 +344,6 @@ class InnerqDynamicLayer(CacheLayerMixin):
             if q is not None and (q.mode == QMode.HYBRID or q.axis != want):
                 raise NotImplementedError(f"fused decode reads {name} grouped along the "
                                           f"{'head_dim' if want == 'channel' else 'token'} axis, asym or sym")
-        self._fused_pending = False
         q = query_states[:, :, 0]
         out = ops.decode_attention(
             q, self.keys_sink if self.keys_sink.shape[-2] else None, self._kq.store if self._kq else None,
@@ -449,26 +448,31 @@ class DynamicCache(Cache):
                 else:
                     layers.append(InnerqDynamicLayer(config=config, layer_idx=layer_idx))
         super().__init__(layers=layers, offloading=offloading, offload_only_non_sliding=offload_only_non_sliding)
-        # a model running the fused attention (attn_implementation "innerq_fused")
-        # decodes over the packed stores without materializing K and V
-        self.fused_decode = config is not None and getattr(config, "_attn_implementation", None) == FUSED_ATTENTION
+        # the model's config, read again on every update(): the model may switch
+        # its attention implementation while this cache lives
+        self._config = config
+
+    @property
+    def fused_decode(self) -> bool:
+        """Whether the model currently runs the fused attention (attn_implementation
+        "innerq_fused"), which decodes over the packed stores without
+        materializing K and V."""
+        return self._config is not None and getattr(self._config, "_attn_implementation", None) == FUSED_ATTENTION
 
     def update(self, key_states: torch.Tensor, value_states: torch.Tensor, layer_idx: int, *args, **kwargs):
-        """Cache.update.  In fused-decode mode a one-token step that the layer's
-        attend() can serve is appended without materializing K and V; the
-        returned key tensor carries the layer (``_innerq_layer``) for the
-        fused attention function, which reads the packed cache through it."""
-        if self.fused_decode and layer_idx < len(self.layers):
+        """Cache.update.  While the model runs the fused attention, a one-token
+        step that the layer's attend() can serve is appended without
+        materializing K and V; the returned key tensor carries the layer
+        (``_innerq_layer``) for the fused attention function, which reads the
+        packed cache through it.  Under any other attention implementation,
+        checked on every call, update() returns the dense K and V as the
+        reference does: append() and update() advance the same state, so the
+        two kinds of step can follow each other in either order."""
+        if layer_idx < len(self.layers) and self.fused_decode:
             layer = self.layers[layer_idx]
-            if getattr(layer, "_fused_pending", False):
-                # the previous tagged step never reached attend(): an attention
-                # other than "innerq_fused" read only the new token's K/V
-                raise RuntimeError("a fused-decode DynamicCache needs attn_implementation='innerq_fused'; "
-                                   "build a new cache after switching the attention implementation")
             if layer.fused_decode_ready(key_states):
                 layer.append(key_states, value_states)
                 key_states._innerq_layer = layer
-                layer._fused_pending = True
                 return key_states, value_states
         return super().update(key_states, value_states, layer_idx, *args, **kwargs)
 

@@ -41,6 +41,111 @@ def mode_id(mode) -> int:
     return MODES[m]
 
 
+def _shape_error(msg: str):
+    raise ValueError(msg)
+
+
+def check_store(store, role: str, axis: str, B: int, H: Optional[int], D: int) -> None:
+    """``store`` (a PackedStore, or anything with its attributes) holds [B, H, *, D]
+    grouped along ``axis``; H = None accepts any head count."""
+    if store.axis != axis:
+        _shape_error(f"{role}: store grouped along the {store.axis} axis, this call reads a "
+                     f"{'head_dim' if axis == 'channel' else 'token'}-grouped store")
+    if store.B != B or store.D != D or (H is not None and store.H != H):
+        _shape_error(f"{role}: store holds [B={store.B}, H={store.H}, D={store.D}], the call has "
+                     f"[B={B}, H={H if H is not None else store.H}, D={D}]")
+
+
+def check_range(store, role: str, t0: int, T: int) -> None:
+    if t0 < 0 or T < 0 or t0 + T > store.length:
+        _shape_error(f"{role}: tokens [{t0}, {t0 + T}) are not inside the store's {store.length} tokens")
+
+
+def check_gqa(Hq: int, Hkv: int) -> None:
+    if Hkv <= 0 or Hq % Hkv:
+        _shape_error(f"{Hq} query heads do not divide over {Hkv} KV heads")
+
+
+def check_out(shape, want, role: str = "out") -> None:
+    if tuple(shape) != tuple(want):
+        _shape_error(f"{role} has shape {tuple(shape)}, expected {tuple(want)}")
+
+
+def check_norm(norm_numel: Optional[int], B: int, Hkv: int, D: int) -> None:
+    if norm_numel is not None and norm_numel != B * Hkv * D:
+        _shape_error(f"key normalization factor has {norm_numel} values, expected B*Hkv*D = {B * Hkv * D}")
+
+
+def check_qk_shapes(q_shape, store, t0: int, T: int, out_shape=None, norm_numel=None) -> None:
+    """Shapes of a QK^T GEMV call (host only): q [B,Hq,D] over store tokens
+    [t0, t0+T) of a head_dim-grouped store [B,Hkv,*,D]; out [B,Hq,T]."""
+    if len(q_shape) != 3:
+        _shape_error(f"q must be [B, Hq, D], got {tuple(q_shape)}")
+    B, Hq, D = q_shape
+    check_store(store, "K", "channel", B, None, D)
+    check_gqa(Hq, store.H)
+    check_range(store, "K", t0, T)
+    check_norm(norm_numel, B, store.H, D)
+    if out_shape is not None:
+        check_out(out_shape, (B, Hq, T))
+
+
+def check_av_shapes(p_shape, store, t0: int, T: int, out_shapes=()) -> None:
+    """Shapes of an attn.V GEMV call (host only): p [B,Hq,>=T] (p[..., i] weighs
+    store token t0+i) over a token-grouped store [B,Hkv,*,D]; outputs [B,Hq,D]."""
+    if len(p_shape) != 3:
+        _shape_error(f"p must be [B, Hq, T], got {tuple(p_shape)}")
+    B, Hq, Tp = p_shape
+    check_store(store, "V", "token", B, None, store.D)
+    check_gqa(Hq, store.H)
+    check_range(store, "V", t0, T)
+    if Tp < T:
+        _shape_error(f"p holds {Tp} tokens, the call reads {T}")
+    for s in out_shapes:
+        check_out(s, (B, Hq, store.D))
+
+
+def check_decode_shapes(q_shape, k_sink, k_store, k_recent, v_sink, v_store, v_recent, norm_numel=None,
+                        out_shape=None) -> tuple:
+    """Shapes of a decode-attention call (host only).  Dense segments are shapes
+    [B,Hkv,n,D] or None; stores are PackedStores (or anything with their
+    attributes) or None.  Returns (B, Hq, Hkv, T, D)."""
+    if len(q_shape) != 3:
+        _shape_error(f"q must be [B, Hq, D], got {tuple(q_shape)}")
+    B, Hq, D = q_shape
+    Hkv = None
+    for st in (k_store, v_store):
+        if st is not None:
+            Hkv = st.H
+            break
+    for name, seg in (("k_sink", k_sink), ("k_recent", k_recent), ("v_sink", v_sink), ("v_recent", v_recent)):
+        if seg is None:
+            continue
+        if len(seg) != 4:
+            _shape_error(f"{name} must be [B, Hkv, n, D], got {tuple(seg)}")
+        Hkv = seg[1] if Hkv is None else Hkv
+        if (seg[0], seg[1], seg[3]) != (B, Hkv, D):
+            _shape_error(f"{name} has shape {tuple(seg)}, expected [B={B}, Hkv={Hkv}, n, D={D}]")
+    if Hkv is None:
+        _shape_error("decode attention needs at least one K/V segment")
+    if k_store is not None:
+        check_store(k_store, "K", "channel", B, Hkv, D)
+    if v_store is not None:
+        check_store(v_store, "V", "token", B, Hkv, D)
+    check_gqa(Hq, Hkv)
+    check_norm(norm_numel, B, Hkv, D)
+
+    def n_of(seg):
+        return 0 if seg is None else seg[2]
+    T = n_of(k_sink) + (k_store.length if k_store is not None else 0) + n_of(k_recent)
+    Tv = n_of(v_sink) + (v_store.length if v_store is not None else 0) + n_of(v_recent)
+    if T != Tv:
+        _shape_error(f"K has {T} tokens but V has {Tv}")
+    if out_shape is not None:
+        check_out(out_shape, (B, Hq, D))
+    return B, Hq, Hkv, T, D
+
+
 class PackedStore:
     """Packed codes + fp16 metadata of one quantized K or V segment.
 
@@ -83,10 +188,16 @@ class PackedStore:
         cb, mb = self._bytes(new_cap)
         codes = torch.empty(cb // 4, dtype=torch.int32, device=self.device)
         meta = torch.empty(mb // 2, dtype=torch.int16, device=self.device)
-        if self.t_cap:
-            ou, nu = self.t_cap // u, new_cap // u
-            codes.view(self.B * self.H, nu, -1)[:, :ou].copy_(self.codes.view(self.B * self.H, ou, -1))
-            meta.view(self.B * self.H, nu, -1)[:, :ou].copy_(self.meta.view(self.B * self.H, ou, -1))
+        # new capacity starts zeroed: the rows of a partly filled 64-token K block
+        # past ``length`` are never written by a quantize, and to_bytes() ships the
+        # whole block, so they must not carry stale device memory
+        ou, nu, bh = self.t_cap // u, new_cap // u, self.B * self.H
+        cv, mv = codes.view(bh, nu, -1), meta.view(bh, nu, -1)
+        if ou:
+            cv[:, :ou].copy_(self.codes.view(bh, ou, -1))
+            mv[:, :ou].copy_(self.meta.view(bh, ou, -1))
+        cv[:, ou:].zero_()
+        mv[:, ou:].zero_()
         self.codes, self.meta, self.t_cap = codes, meta, new_cap
 
     def nbytes(self, n_tokens: Optional[int] = None) -> int:
@@ -107,9 +218,28 @@ class PackedStore:
     # little-endian u32 words; sym fields are offset binary.
     WIRE_FORMAT, WIRE_VERSION = "innerq-packed-store", "1"
 
+    @staticmethod
+    def _safetensors(tensors: dict, metadata: dict) -> bytes:
+        """A safetensors container (8-byte little-endian header size, JSON header,
+        raw little-endian data) with its JSON keys sorted, so equal stores give
+        byte-identical blobs (safetensors' own writer orders the metadata map
+        differently from call to call)."""
+        import json
+        import struct
+        dt = {torch.int32: "I32", torch.int16: "I16"}
+        header, off, bufs = {"__metadata__": dict(sorted(metadata.items()))}, 0, []
+        for name in sorted(tensors):
+            t = tensors[name].contiguous()
+            b = t.numpy().tobytes()
+            header[name] = {"dtype": dt[t.dtype], "shape": list(t.shape), "data_offsets": [off, off + len(b)]}
+            off += len(b)
+            bufs.append(b)
+        h = json.dumps(header, sort_keys=True, separators=(",", ":")).encode()
+        h += b" " * (-len(h) % 8)
+        return struct.pack("<Q", len(h)) + h + b"".join(bufs)
+
     def to_bytes(self) -> bytes:
         """The store's valid units in the wire format (see above)."""
-        from safetensors.torch import save
         bh, u = self.B * self.H, self.unit
         used = -(-self.length // u)
         nu = self.t_cap // u
@@ -120,7 +250,7 @@ class PackedStore:
         md = {"format": self.WIRE_FORMAT, "version": self.WIRE_VERSION, "axis": self.axis, "B": self.B,
               "H": self.H, "D": self.D, "group": self.group, "bits": self.bits,
               "mode": "symmetric" if self.mode == IQ_MODE_SYM else "asymmetric", "length": self.length, "unit": u}
-        return save({"codes": codes, "meta": meta}, metadata={k: str(v) for k, v in md.items()})
+        return self._safetensors({"codes": codes, "meta": meta}, {k: str(v) for k, v in md.items()})
 
     @classmethod
     def from_bytes(cls, blob: bytes, device, t_cap: int = 0) -> "PackedStore":
@@ -162,8 +292,12 @@ class PackedStore:
     def append(self, x: torch.Tensor, norm: Optional[torch.Tensor] = None) -> None:
         """Quantize x [B,H,n,D] fp16 and append it (quantize-on-append)."""
         require_device(x, "x")
+        if x.dim() != 4 or (x.shape[0], x.shape[1], x.shape[3]) != (self.B, self.H, self.D):
+            _shape_error(f"append: x has shape {tuple(x.shape)}, the store holds [B={self.B}, H={self.H}, n, "
+                         f"D={self.D}]")
         B, H, n, D = x.shape
-        assert (B, H, D) == (self.B, self.H, self.D), "store shape mismatch"
+        if self.axis == "token" and n % self.group:
+            _shape_error(f"append: a token-grouped store takes whole groups of {self.group} tokens, got {n}")
         if n == 0:
             return
         self.reserve(self.length + n)
@@ -189,9 +323,12 @@ class PackedStore:
                 norm: Optional[torch.Tensor] = None, dtype=torch.float16) -> torch.Tensor:
         """Dense [B,H,T,D] values of tokens [t0, t0+T) (fp16 or fp32); ``out`` may be a strided view."""
         T = self.length - t0 if T is None else T
+        check_range(self, "dequant", t0, T)
         if out is None:
             out = torch.empty(self.B, self.H, T, self.D, dtype=dtype, device=self.device)
-        assert out.shape == (self.B, self.H, T, self.D) and out.stride(-1) == 1
+        check_out(out.shape, (self.B, self.H, T, self.D))
+        if out.stride(-1) != 1:
+            _shape_error("dequant output must have a contiguous last dimension")
         o16 = _p(out) if out.dtype == torch.float16 else None
         o32 = _p(out) if out.dtype == torch.float32 else None
         if o16 is None and o32 is None:
@@ -203,7 +340,8 @@ class PackedStore:
             call("iq_dequant_k", _p(self.codes), _p(self.meta), self.t_cap, _p(norm), self.B, self.H, t0, T, self.D,
                  self.group, self.bits, self.mode, o16, o32, st[0], st[1], st[2], _stream(out.device))
         else:
-            assert norm is None
+            if norm is not None:
+                raise ValueError("a key normalization factor applies to head_dim-grouped (K) stores only")
             call("iq_dequant_v", _p(self.codes), _p(self.meta), self.t_cap, self.B, self.H, t0, T, self.D,
                  self.group, self.bits, self.mode, o16, o32, st[0], st[1], st[2], _stream(out.device))
         return out
@@ -277,14 +415,17 @@ def qk_gemv(q: torch.Tensor, k: PackedStore, scale: float, norm: Optional[torch.
             T: Optional[int] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """logits [B,Hq,T] fp32 = scale * q . K[t0:t0+T] over a channel-grouped store."""
     require_device(q, "q")
-    assert k.axis == "channel"
-    B, Hq, D = q.shape
     T = k.length - t0 if T is None else T
+    check_qk_shapes(q.shape, k, t0, T, None if out is None else out.shape,
+                    None if norm is None else norm.numel())
+    B, Hq, D = q.shape
     if q.stride(-1) != 1:
         q = q.contiguous()
     if out is None:
         out = torch.empty(B, Hq, T, dtype=torch.float32, device=q.device)
-    assert out.stride(-1) == 1 and out.dtype == torch.float32
+    require_device(out, "out", torch.float32)
+    if out.stride(-1) != 1:
+        _shape_error("logits output must have a contiguous token dimension")
     if norm is not None:
         norm = norm.reshape(k.B, k.H, D).contiguous()
     ws = _workspace(q.device, _lib.lib().iq_qk_workspace_bytes(B, Hq, D))
@@ -299,16 +440,22 @@ def av_gemv(p: torch.Tensor, v: PackedStore, t0: int = 0, T: Optional[int] = Non
             accumulate: bool = False) -> torch.Tensor:
     """out [B,Hq,D] = p . V[t0:t0+T] over a token-grouped store (fp16 and/or fp32 outputs)."""
     require_device(p, "p")
-    assert v.axis == "token"
-    B, Hq, Tp = p.shape
     T = v.length - t0 if T is None else T
+    check_av_shapes(p.shape, v, t0, T, [o.shape for o in (out, out32) if o is not None])
+    B, Hq, Tp = p.shape
     if p.stride(-1) != 1:
         p = p.contiguous()
     if out is None and out32 is None:
         out = torch.empty(B, Hq, v.D, dtype=torch.float16, device=p.device)
+    if out is not None:
+        require_device(out, "out")
+    if out32 is not None:
+        require_device(out32, "out32", torch.float32)
     ref = out if out is not None else out32
-    if out is not None and out32 is not None:
-        assert out.stride() == out32.stride()
+    if out is not None and out32 is not None and out.stride() != out32.stride():
+        _shape_error("out and out32 must have the same strides")
+    if ref.stride(-1) != 1:
+        _shape_error("attn.V output must have a contiguous head_dim")
     nbytes = _lib.lib().iq_av_workspace_bytes(B, Hq, T, v.D, v.group)
     ws = _workspace(p.device, nbytes)
     call("iq_av_gemv", _p(p), p.stride(0), p.stride(1), _p(v.codes), _p(v.meta), v.t_cap, B, Hq, v.H, t0, T, v.D,
@@ -327,15 +474,26 @@ def _segment(dense: Optional[torch.Tensor], store: Optional[PackedStore], n: int
         s.bits, s.group, s.mode = store.bits, store.group, store.mode
     else:
         require_device(dense, "segment")
-        assert dense.stride(-1) == 1
+        if dense.stride(-1) != 1:
+            _shape_error("a dense K/V segment must have a contiguous head_dim")
         s.dense = dense.data_ptr()
         s.s_b, s.s_h, s.s_t = dense.stride(0), dense.stride(1), dense.stride(2)
     return s
 
 
-def _decode_args(q, k_sink, k_store, k_recent, v_sink, v_store, v_recent, norm):
+def _decode_args(q, k_sink, k_store, k_recent, v_sink, v_store, v_recent, norm, out=None):
     require_device(q, "q")
-    B, Hq, D = q.shape
+
+    def shp(t):
+        return None if t is None else tuple(t.shape)
+
+    B, Hq, Hkv, T, D = check_decode_shapes(shp(q), shp(k_sink), k_store, shp(k_recent), shp(v_sink), v_store,
+                                           shp(v_recent), None if norm is None else norm.numel(),
+                                           None if out is None else tuple(out.shape))
+    if out is not None:
+        require_device(out, "out")
+        if out.stride(-1) != 1:
+            _shape_error("decode output must have a contiguous head_dim")
     if q.stride(-1) != 1:
         q = q.contiguous()
 
@@ -344,10 +502,6 @@ def _decode_args(q, k_sink, k_store, k_recent, v_sink, v_store, v_recent, norm):
 
     kn = [n_of(k_sink), k_store.length if k_store is not None else 0, n_of(k_recent)]
     vn = [n_of(v_sink), v_store.length if v_store is not None else 0, n_of(v_recent)]
-    T = sum(kn)
-    if sum(vn) != T:
-        raise ValueError(f"K has {T} tokens but V has {sum(vn)}")
-    Hkv = (k_store.H if k_store is not None else (k_sink if k_sink is not None else k_recent).shape[1])
     ks = (_lib.iq_segment * 3)(_segment(k_sink, None, kn[0]), _segment(None, k_store, kn[1]),
                                _segment(k_recent, None, kn[2]))
     vs = (_lib.iq_segment * 3)(_segment(v_sink, None, vn[0]), _segment(None, v_store, vn[1]),
@@ -364,7 +518,7 @@ def decode_attention(q: torch.Tensor, k_sink: Optional[torch.Tensor], k_store: O
                      norm: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """One decode step of attention for q [B,Hq,D] over [sink | packed | recent] K and V."""
     q, B, Hq, Hkv, T, D, ks, vs, norm, ws = _decode_args(q, k_sink, k_store, k_recent, v_sink, v_store, v_recent,
-                                                         norm)
+                                                         norm, out)
     if out is None:
         out = torch.empty(B, Hq, D, dtype=torch.float16, device=q.device)
     call("iq_decode_attention", _p(q), q.stride(0), q.stride(1), _p(norm), ks, vs, B, Hq, Hkv, T, D, float(scale),
@@ -389,6 +543,8 @@ def decode_attention_combine(nsplit: int, B: int, Hq: int, T: int, D: int, devic
     device = torch.device(device)
     if out is None:
         out = torch.empty(B, Hq, D, dtype=torch.float16, device=device)
+    require_device(out, "out")
+    check_out(out.shape, (B, Hq, D))
     ws = _workspace(device, _lib.lib().iq_decode_workspace_bytes(B, Hq, T, D))
     call("iq_decode_attention_combine", nsplit, B, Hq, T, D, _p(out), out.stride(0), out.stride(1), _p(ws),
          ws.numel(), _stream(device))
@@ -399,6 +555,7 @@ def decode_attention_combine(nsplit: int, B: int, Hq: int, T: int, D: int, devic
 def unpack_store(store: PackedStore, t0: int = 0, T: Optional[int] = None):
     """Reference-format (codes int32, scale fp16, zero | signs fp16) of store tokens [t0, t0+T)."""
     T = store.length - t0 if T is None else T
+    check_range(store, "unpack", t0, T)
     B, H, D, G = store.B, store.H, store.D, store.group
     dev = store.device
     codes = torch.empty(B, H, T, D, dtype=torch.int32, device=dev)

@@ -262,17 +262,32 @@ def test_fused_attention_generate(monkeypatch):
     assert calls[0] == 2 * 5  # the 5 decode steps after the prefill, both layers
 
 
-def test_fused_cache_with_another_attention_fails_loudly():
-    """A fused-decode cache driven by a model whose attention is no longer
-    "innerq_fused" would feed that attention the new token alone: the next
-    step raises instead of returning wrong logits silently."""
+def test_fused_cache_follows_an_attention_switch():
+    """A cache built while the model ran "innerq_fused" stays correct when the
+    model switches attention mid-generation: update() reads the model's
+    current attn_implementation on every call, so a step under sdpa gets the
+    dense K and V (the reference's behaviour, from the very first such step)
+    and a step under innerq_fused attends over the packed cache.  Every step's
+    logits match a cache that only ever ran the reference's path."""
     model = _tiny_llama("asym4_nosink")
-    ids = torch.randint(0, 64, (1, 150), generator=torch.Generator(device=DEV).manual_seed(5), device=DEV)
-    model.config._attn_implementation = "innerq_fused"
-    cache = C.DynamicCache(config=model.config)
-    model.config._attn_implementation = "sdpa"  # no mask for one query token: nothing else would notice
-    with torch.no_grad():
-        model(ids, past_key_values=cache, use_cache=True)
-        model(ids[:, :1], past_key_values=cache, use_cache=True)  # tagged step read by sdpa
-        with pytest.raises(RuntimeError, match="innerq_fused"):
-            model(ids[:, :1], past_key_values=cache, use_cache=True)
+    gen = torch.Generator(device=DEV).manual_seed(5)
+    ids = torch.randint(0, 64, (1, 150), generator=gen, device=DEV)
+    dec = torch.randint(0, 64, (1, 8), generator=gen, device=DEV)
+    plan = ["sdpa", "sdpa", "innerq_fused", "sdpa", "innerq_fused", "innerq_fused", "sdpa", "innerq_fused"]
+    logits = {}
+    for run in ("reference", "switching"):
+        model.config._attn_implementation = "eager" if run == "reference" else "innerq_fused"
+        cache = C.DynamicCache(config=model.config)
+        steps = []
+        with torch.no_grad():
+            model(ids, past_key_values=cache, use_cache=True)
+            for t, attn in enumerate(plan):
+                if run == "switching":
+                    model.config._attn_implementation = attn
+                    assert cache.fused_decode == (attn == "innerq_fused")
+                steps.append(model(dec[:, t:t + 1], past_key_values=cache, use_cache=True).logits[:, -1].float())
+        assert cache.get_seq_length() == 150 + len(plan)
+        logits[run] = torch.stack(steps)
+    ref, got = logits["reference"], logits["switching"]
+    err = ((got - ref).abs().amax(dim=(1, 2)) / ref.abs().amax(dim=(1, 2)))
+    assert err.max().item() < 2e-2, err.tolist()
