@@ -240,6 +240,22 @@ int iq_decode_attention_splits(const void* q, int64_t sq_b, int64_t sq_h, const 
 int iq_decode_attention_combine(int nsplit, int B, int Hq, int T, int D, void* out, int64_t so_b, int64_t so_h,
                                 void* workspace, size_t workspace_bytes, void* stream);
 
+/* iq_decode_attention without the workspace argument, for callers that
+ * cannot allocate device memory (code under HIP graph capture, serving loops
+ * and harnesses that forbid hipMalloc).  It has no counterpart in the
+ * reference.  Arguments, results and errors are those of iq_decode_attention;
+ * the workspace is a library-owned device array of
+ * iq_decode_noalloc_max_bytes() bytes (64 MiB) per GPU, held until the process
+ * ends, and a call whose iq_decode_workspace_bytes(B, Hq, T, D) exceeds it
+ * returns IQ_ERR_WORKSPACE before any launch.  The call allocates nothing.
+ * Every call on one GPU uses the same array: calls that overlap on one GPU
+ * (concurrent streams, threads) race and must be serialized by the caller. */
+size_t iq_decode_noalloc_max_bytes(void);
+int iq_decode_attention_noalloc(const void* q, int64_t sq_b, int64_t sq_h, const void* norm,
+                                const iq_segment* k, const iq_segment* v,
+                                int B, int Hq, int Hkv, int T, int D, float scale,
+                                void* out, int64_t so_b, int64_t so_h, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -74,6 +74,9 @@ SIGNATURES = {
     "iq_decode_attention_splits": (I, [P, L, L, P, ctypes.POINTER(iq_segment), ctypes.POINTER(iq_segment),
                                        I, I, I, I, I, F, P, S, ctypes.POINTER(I), P]),
     "iq_decode_attention_combine": (I, [I, I, I, I, I, P, L, L, P, S, P]),
+    "iq_decode_noalloc_max_bytes": (S, []),
+    "iq_decode_attention_noalloc": (I, [P, L, L, P, ctypes.POINTER(iq_segment), ctypes.POINTER(iq_segment),
+                                        I, I, I, I, I, F, P, L, L, P]),
 }
 
 _lib = None

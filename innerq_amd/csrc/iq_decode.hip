@@ -19,6 +19,8 @@
 // total sum: softmax(q K^T * scale) V in fp32, written as fp16
 // (TF/models/llama/modeling_llama.py:201-210).  The probabilities that meet V
 // are rounded to fp16 as the reference rounds its softmax output.
+#include <mutex>
+
 #include "iq_gemv.h"
 
 using namespace iq;
@@ -576,9 +578,60 @@ int launch_combine(const Workspace& w, int nsplit, int B, int Hq, int D, void* o
   return launch_status();
 }
 
+// ---- scratch of the no-allocation entry point ----
+// The decode workspace (records, split statistics, partials) of
+// iq_decode_attention_noalloc lives in this file-scope device array: each GPU
+// the library runs on holds its own copy, at its own address, until the
+// process ends.  Nothing in it has to start at zero: every split slot the
+// combine reads is written by the split stage of the same call.  Calls that
+// overlap on one GPU share the array and race.
+constexpr size_t SCRATCH_BYTES = size_t(64) << 20;
+static __device__ __align__(256) unsigned char scratch[SCRATCH_BYTES];
+
+constexpr int MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[MAX_DEVICES] = {};
+
+// The device address of `scratch` on the current device, looked up once per
+// device with that device current (the array's name is a host-side stand-in,
+// never a device address).
+int scratch_address(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) return IQ_ERR_HIP;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    if (hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)) != hipSuccess || !p) return IQ_ERR_HIP;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return IQ_OK;
+}
+
 }  // namespace
 
 extern "C" {
+
+size_t iq_decode_noalloc_max_bytes(void) { return SCRATCH_BYTES; }
+
+int iq_decode_attention_noalloc(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, const iq_segment* k,
+                                const iq_segment* v, int B, int Hq, int Hkv, int T, int D, float scale, void* out,
+                                int64_t so_b, int64_t so_h, void* stream) {
+  IQ_CHECK(out, IQ_ERR_NULL);
+  // every check of iq_decode_attention, host only, with the scratch's size as
+  // the workspace size: a call whose workspace would exceed SCRATCH_BYTES
+  // returns IQ_ERR_WORKSPACE before any HIP call (the stand-in pointer is only
+  // tested for being non-null and aligned, never used)
+  if (int e = check_decode(q, k, v, B, Hq, Hkv, T, D, reinterpret_cast<void*>(256), SCRATCH_BYTES)) return e;
+  if (B == 0) return IQ_OK;
+  void* ws = nullptr;
+  if (int e = scratch_address(&ws)) return e;
+  const Workspace w = carve(ws, B, Hq, T, D);
+  int nsplit = 0;
+  if (int e = launch_splits(q, sq_b, sq_h, norm, k, v, B, Hq, Hkv, T, D, scale, w, &nsplit, (hipStream_t)stream))
+    return e;
+  return launch_combine(w, nsplit, B, Hq, D, out, so_b, so_h, (hipStream_t)stream);
+}
 
 size_t iq_decode_workspace_bytes(int B, int Hq, int T, int D) {
   if (B <= 0 || Hq <= 0 || T <= 0 || !d_ok(D)) return 0;

@@ -193,3 +193,25 @@ def test_decode_stage_rejects():
     assert lib.iq_decode_attention_combine(6, 1, 32, 64, 128, FAKE, 4096, 128, FAKE, 1 << 30, None) == -4
     assert lib.iq_decode_attention_combine(1, 1, 32, 64, 128, None, 4096, 128, FAKE, 1 << 30, None) == -1
     assert lib.iq_decode_attention_combine(1, 1, 32, 64, 128, FAKE, 4096, 128, FAKE, 64, None) == -6
+
+
+def test_decode_noalloc_limits():
+    """The no-allocation decode entry point: its scratch size, and a call whose
+    workspace would exceed it refused with IQ_ERR_WORKSPACE before any HIP call
+    (the FAKE pointers are never dereferenced); a bad shape is refused first."""
+    lib = _lib.lib()
+    assert lib.iq_decode_noalloc_max_bytes() == 64 << 20
+    k = (_lib.iq_segment * 3)()
+    v = (_lib.iq_segment * 3)()
+    T = 131072
+    for s, grp in ((k, 32), (v, 32)):
+        s[1].n, s[1].codes, s[1].meta, s[1].t_cap, s[1].t0 = T, 0x1000, 0x1000, T, 0
+        s[1].bits, s[1].group, s[1].mode = 4, grp, 0
+    need = lib.iq_decode_workspace_bytes(64, 32, T, 128)
+    assert need > 64 << 20
+    assert lib.iq_decode_attention_noalloc(FAKE, 4096, 128, None, k, v, 64, 32, 8, T, 128, 1.0, FAKE, 4096, 128,
+                                           None) == -6
+    assert lib.iq_decode_attention_noalloc(FAKE, 4096, 128, None, k, v, 64, 32, 8, T, 96, 1.0, FAKE, 4096, 128,
+                                           None) == -4
+    assert lib.iq_decode_attention_noalloc(FAKE, 4096, 128, None, k, v, 64, 32, 8, T, 128, 1.0, None, 4096, 128,
+                                           None) == -1
