@@ -210,6 +210,7 @@ typedef struct iq_segment {
   int bits, group, mode;
 } iq_segment;
 
+/* Workspace of the decode entry points (no initialization needed). */
 size_t iq_decode_workspace_bytes(int B, int Hq, int T, int D);
 
 /* Full decode attention for one layer and one new query token per sequence:

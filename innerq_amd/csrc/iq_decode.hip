@@ -408,6 +408,7 @@ Seg to_seg(const iq_segment& s, int start) {
 namespace {
 
 struct Workspace {
+  unsigned long long* tickets;  // [B*Hq] {tag, count} run tickets of the in-kernel merge
   uint32_t* qrec;  // query operand records (unfused path)
   uint32_t* vrec;  // probability operand records (unfused path)
   float* ml;       // [nsplit][B*Hq][2] split (max, sum)
@@ -418,6 +419,8 @@ Workspace carve(void* workspace, int B, int Hq, int T, int D) {
   const size_t rows = size_t(B) * Hq;
   char* ws = (char*)workspace;
   Workspace w{};
+  w.tickets = (unsigned long long*)ws;
+  ws += align256(rows * sizeof(unsigned long long));
   w.qrec = (uint32_t*)ws;
   ws += detail::qk_record_bytes(B, Hq, D);
   size_t vrec_bytes = 0;
@@ -465,10 +468,15 @@ int check_decode(const void* q, const iq_segment* k, const iq_segment* v, int B,
   return IQ_OK;
 }
 
-// Launches everything up to the split statistics and partials; *nsplit = their count.
+// Launches everything up to the split statistics and partials; *nsplit = their
+// count.  With `out` (fp16, strides so_b, so_h) the fused kernel merges them
+// into out itself when it covers the packed range (*merged = true; the dense
+// slices run first so that their slots are complete); otherwise, or without
+// `out`, the combine kernel merges them.
 int launch_splits(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, const iq_segment* k,
                   const iq_segment* v, int B, int Hq, int Hkv, int T, int D, float scale, const Workspace& w,
-                  int* nsplit, hipStream_t st) {
+                  int* nsplit, void* out, int64_t so_b, int64_t so_h, bool* merged, hipStream_t st) {
+  *merged = false;
   const int64_t rows = int64_t(B) * Hq;
   // fused range: packed in both K and V, aligned to K blocks and V groups
   const int ks = k[0].n, vs = v[0].n;
@@ -494,22 +502,9 @@ int launch_splits(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, c
                               k[1].mode};
   const detail::FusedStore fv{v[1].codes, v[1].meta, v[1].t_cap, v[1].t0 + (a0 - vs), v[1].bits, v[1].group,
                               v[1].mode};
-  if (c && k[1].group == v[1].group && detail::flash_fused_supported(q, sq_b, sq_h, norm, fk, fv, Hq, Hkv, D)) {
-    if (int e = detail::flash_fused_launch(q, sq_b, sq_h, norm, fk, fv, B, Hq, Hkv, c, D, scale, w.ml, w.part, st))
-      return e;
-  } else if (c) {
-    const iq_segment& kg = k[1];
-    const iq_segment& vg = v[1];
-    if (int e = detail::qk_record_launch(q, sq_b, sq_h, norm, B, Hq, Hkv, D, kg.group, kg.bits, w.qrec, st))
-      return e;
-    const detail::FlashOut f{w.ml, w.vrec, vg.bits, vg.group};
-    if (int e = detail::qk_flash_launch(w.qrec, norm != nullptr, kg.codes, kg.meta, kg.t_cap, B, Hq, Hkv,
-                                        kg.t0 + (a0 - ks), c, D, kg.group, kg.bits, kg.mode, scale, f, st))
-      return e;
-    if (int e = detail::av_flash_launch(w.vrec, vg.codes, vg.meta, vg.t_cap, B, Hq, Hkv, vg.t0 + (a0 - vs), c, D,
-                                        vg.group, vg.bits, vg.mode, w.part, st))
-      return e;
-  }
+  const bool fused =
+      c && k[1].group == v[1].group && detail::flash_fused_supported(q, sq_b, sq_h, norm, fk, fv, Hq, Hkv, D);
+
   // dense tokens -> split slots nsf, nsf + 1, ...: enough workgroups to
   // spread over the CUs, at least DSLICE tokens each
   DenseArgs da{};
@@ -553,6 +548,26 @@ int launch_splits(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, c
     else by_r.template operator()<64>();
     if (int e = launch_status()) return e;
   }
+
+  if (fused) {
+    const detail::FusedMerge mg{out, so_b, so_h, w.tickets, nsd};
+    if (int e = detail::flash_fused_launch(q, sq_b, sq_h, norm, fk, fv, B, Hq, Hkv, c, D, scale, w.ml, w.part,
+                                           out ? &mg : nullptr, st))
+      return e;
+    *merged = out != nullptr;
+  } else if (c) {
+    const iq_segment& kg = k[1];
+    const iq_segment& vg = v[1];
+    if (int e = detail::qk_record_launch(q, sq_b, sq_h, norm, B, Hq, Hkv, D, kg.group, kg.bits, w.qrec, st))
+      return e;
+    const detail::FlashOut f{w.ml, w.vrec, vg.bits, vg.group};
+    if (int e = detail::qk_flash_launch(w.qrec, norm != nullptr, kg.codes, kg.meta, kg.t_cap, B, Hq, Hkv,
+                                        kg.t0 + (a0 - ks), c, D, kg.group, kg.bits, kg.mode, scale, f, st))
+      return e;
+    if (int e = detail::av_flash_launch(w.vrec, vg.codes, vg.meta, vg.t_cap, B, Hq, Hkv, vg.t0 + (a0 - vs), c, D,
+                                        vg.group, vg.bits, vg.mode, w.part, st))
+      return e;
+  }
   *nsplit = nsf + nsd;
   return IQ_OK;
 }
@@ -582,9 +597,10 @@ int launch_combine(const Workspace& w, int nsplit, int B, int Hq, int D, void* o
 // The decode workspace (records, split statistics, partials) of
 // iq_decode_attention_noalloc lives in this file-scope device array: each GPU
 // the library runs on holds its own copy, at its own address, until the
-// process ends.  Nothing in it has to start at zero: every split slot the
-// combine reads is written by the split stage of the same call.  Calls that
-// overlap on one GPU share the array and race.
+// process ends.  Nothing in it has to be initialized: a run-ticket word
+// without its tag counts as zero, and every split slot the merge reads is
+// written by the same call.  Calls that overlap on one GPU share the
+// array and race.
 constexpr size_t SCRATCH_BYTES = size_t(64) << 20;
 static __device__ __align__(256) unsigned char scratch[SCRATCH_BYTES];
 
@@ -628,8 +644,11 @@ int iq_decode_attention_noalloc(const void* q, int64_t sq_b, int64_t sq_h, const
   if (int e = scratch_address(&ws)) return e;
   const Workspace w = carve(ws, B, Hq, T, D);
   int nsplit = 0;
-  if (int e = launch_splits(q, sq_b, sq_h, norm, k, v, B, Hq, Hkv, T, D, scale, w, &nsplit, (hipStream_t)stream))
+  bool merged = false;
+  if (int e = launch_splits(q, sq_b, sq_h, norm, k, v, B, Hq, Hkv, T, D, scale, w, &nsplit, out, so_b, so_h,
+                            &merged, (hipStream_t)stream))
     return e;
+  if (merged) return IQ_OK;
   return launch_combine(w, nsplit, B, Hq, D, out, so_b, so_h, (hipStream_t)stream);
 }
 
@@ -639,8 +658,8 @@ size_t iq_decode_workspace_bytes(int B, int Hq, int T, int D) {
   size_t vrec = 0;
   for (int g : {32, 64, 128}) vrec = std::max(vrec, rec_bytes_bound(int64_t(B) * Hq, T / g, g));
   const size_t ns = size_t(nsplit_max(T)) + NSD_MAX;
-  return detail::qk_record_bytes(B, Hq, D) + align256(vrec) + align256(ns * rows * 2 * 4) +
-         align256(ns * rows * D * 4);
+  return align256(rows * sizeof(unsigned long long)) + detail::qk_record_bytes(B, Hq, D) + align256(vrec) +
+         align256(ns * rows * 2 * 4) + align256(ns * rows * D * 4);
 }
 
 int iq_decode_attention_splits(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, const iq_segment* k,
@@ -650,8 +669,9 @@ int iq_decode_attention_splits(const void* q, int64_t sq_b, int64_t sq_h, const 
   if (int e = check_decode(q, k, v, B, Hq, Hkv, T, D, workspace, workspace_bytes)) return e;
   *nsplit = 0;
   if (B == 0) return IQ_OK;
+  bool merged = false;
   return launch_splits(q, sq_b, sq_h, norm, k, v, B, Hq, Hkv, T, D, scale, carve(workspace, B, Hq, T, D), nsplit,
-                       (hipStream_t)stream);
+                       nullptr, 0, 0, &merged, (hipStream_t)stream);
 }
 
 int iq_decode_attention_combine(int nsplit, int B, int Hq, int T, int D, void* out, int64_t so_b, int64_t so_h,
@@ -673,8 +693,11 @@ int iq_decode_attention(const void* q, int64_t sq_b, int64_t sq_h, const void* n
   if (B == 0) return IQ_OK;
   const Workspace w = carve(workspace, B, Hq, T, D);
   int nsplit = 0;
-  if (int e = launch_splits(q, sq_b, sq_h, norm, k, v, B, Hq, Hkv, T, D, scale, w, &nsplit, (hipStream_t)stream))
+  bool merged = false;
+  if (int e = launch_splits(q, sq_b, sq_h, norm, k, v, B, Hq, Hkv, T, D, scale, w, &nsplit, out, so_b, so_h,
+                            &merged, (hipStream_t)stream))
     return e;
+  if (merged) return IQ_OK;
   return launch_combine(w, nsplit, B, Hq, D, out, so_b, so_h, (hipStream_t)stream);
 }
 
