@@ -287,53 +287,54 @@ __global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs a) {
 }
 
 // out[bq, d] = sum_s e^{m_s - M} o_s[bq, d] / sum_s e^{m_s - M} l_s
-// One wave per row bq, lane = head_dim columns DPL*lane .. DPL*lane+DPL-1.  A
-// split slot with m = -inf carries no tokens and its partial may be unwritten:
-// it is never used.  The fused kernel puts the partials of a (batch, KV head)
-// into its first split slots and the dense tokens take the last NSD_MAX at
-// most, so one round of loads - every slot's (m, l) and, unconditionally, the
-// partials of the first CSPEC slots and of the last CTAIL - finds the usual
-// layout whole; a slot is used only if its weight is nonzero (a select: an
-// unwritten partial cannot reach the sum).  Nonempty slots outside those sets
-// (the unfused path writes every slot) are listed in LDS and read in a second
-// round, CSPEC loads in flight at a time.
+// One wave per row bq, lane = head_dim columns DPL*lane .. DPL*lane+DPL-1,
+// over the row's live split slots, listed in slot order: the fused kernel's
+// run partials of the row's (batch, KV head), slots 0 .. nr-1, then the dense
+// slices' slots nsf .. nsplit-1.  With the fused kernel's workgroup count
+// (grid > 0) nr follows from its share arithmetic: the runs of a (batch, KV
+// head) come from the consecutive shares that hold its splits, one run each.
+// Without it (grid = 0: the unfused path, which writes every slot, or a
+// caller of the split stage alone, whose fused kernel wrote empty statistics
+// in the slots past the runs) every slot 0 .. nsplit-1 is read.  One round of
+// loads - the live slots' (m, l) and, unconditionally, the partials of the
+// first CSPEC listed slots (indices clamped so that every load is issued at
+// once) - covers up to CSPEC live slots; a slot is used only if its weight is
+// nonzero (a select: an unwritten partial cannot reach the sum).  Further
+// live slots are listed in LDS and read CSPEC at a time.
 constexpr int MAXSPLIT = 1024;  // split slots of one step, at most
 constexpr int CSPEC = 8;
-constexpr int CTAIL = NSD_MAX;
 template <int DPL, int E>
 __global__ __launch_bounds__(64) void flash_combine_kernel(const float* __restrict__ ml, const float* __restrict__ part,
-                                                           int nsplit, int64_t rows, int Hq,
-                                                           uint16_t* __restrict__ out, int64_t sob, int64_t soh) {
+                                                           int nsplit, int nsf, int grid, int nrep, int64_t rows,
+                                                           int Hq, uint16_t* __restrict__ out, int64_t sob,
+                                                           int64_t soh) {
   using Vec = float __attribute__((ext_vector_type(DPL)));
   constexpr int D = 64 * DPL;
   __shared__ int sidx[64 * E];
   __shared__ float swgt[64 * E];
   const int64_t bq = blockIdx.x;
   const int lane = threadIdx.x;
-  const float2* st = reinterpret_cast<const float2*>(ml) + bq;       // slot s: st[s * rows]
+  int nr = nsf;
+  if (grid > 0) {
+    const int64_t bh = bq / nrep, nitems = rows / nrep * nsf;
+    auto share_of = [&](int64_t s) { return ((s + 1) * grid + nitems - 1) / nitems - 1; };
+    nr = int(share_of((bh + 1) * nsf - 1) - share_of(bh * nsf) + 1);
+  }
+  const int n = nr + (nsplit - nsf);                                   // live slots
+  auto slot = [&](int i) { return i < nr ? i : nsf + (i - nr); };     // i-th live slot
+  const float2* st = reinterpret_cast<const float2*>(ml) + bq;         // slot s: st[s * rows]
   const Vec* pr = reinterpret_cast<const Vec*>(part + bq * D) + lane;  // slot s: pr[s * rows * 64]
   const int64_t pstride = rows * 64;
-  const int last = nsplit - 1;
-  // ---- one round: statistics of every slot, partials of the likely ones
-  // (indices clamped to the last slot, so that every load is issued
-  // unconditionally and all are in flight together) ----
+  // ---- one round: statistics of the live slots, partials of the first CSPEC ----
   float2 sl[E];
 #pragma unroll
-  for (int e = 0; e < E; ++e) sl[e] = st[int64_t(min(e * 64 + lane, last)) * rows];
-  Vec pv[CSPEC], pt[CTAIL];
-#pragma unroll
-  for (int j = 0; j < CSPEC; ++j) pv[j] = pr[int64_t(min(j, last)) * pstride];
-  const int tail0 = max(nsplit - CTAIL, CSPEC);  // first tail slot not among the first CSPEC
-  float mt[CTAIL];
-#pragma unroll
-  for (int k = 0; k < CTAIL; ++k) {
-    const int s = min(tail0 + k, last);
-    pt[k] = pr[int64_t(s) * pstride];
-    mt[k] = st[int64_t(s) * rows].x;
+  for (int e = 0; e < E; ++e) {
+    const int i = e * 64 + lane;
+    sl[e] = i < n ? st[int64_t(slot(i)) * rows] : make_float2(-INFINITY, 0.f);
   }
+  Vec pv[CSPEC];
 #pragma unroll
-  for (int e = 0; e < E; ++e)
-    if (e * 64 + lane > last) sl[e] = make_float2(-INFINITY, 0.f);
+  for (int j = 0; j < CSPEC; ++j) pv[j] = pr[int64_t(slot(min(j, n - 1))) * pstride];
   float Mv[1] = {-INFINITY};
 #pragma unroll
   for (int e = 0; e < E; ++e) Mv[0] = fmaxf(Mv[0], sl[e].x);
@@ -350,36 +351,33 @@ __global__ __launch_bounds__(64) void flash_combine_kernel(const float* __restri
   Vec acc = 0.f;
 #pragma unroll
   for (int j = 0; j < CSPEC; ++j) {
-    const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w[0]), j));  // slot j: lane j
+    const float wj = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(w[0]), j));  // live slot j: lane j
     if (wj != 0.f) acc += wj * pv[j];
   }
-#pragma unroll
-  for (int k = 0; k < CTAIL; ++k)
-    if (tail0 + k <= last && mt[k] != -INFINITY) acc += __expf(mt[k] - M) * pt[k];
-  // ---- the rest: nonempty slots in [CSPEC, tail0) ----
-  int n = 0;
+  // ---- the rest: nonempty live slots past the first CSPEC ----
+  int m = 0;
 #pragma unroll
   for (int e = 0; e < E; ++e) {
-    if (e * 64 >= nsplit) break;
-    const int s = e * 64 + lane;
-    const bool take = w[e] != 0.f && s >= CSPEC && s < tail0;
+    if (e * 64 >= n) break;
+    const int i = e * 64 + lane;
+    const bool take = w[e] != 0.f && i >= CSPEC;
     const unsigned long long bal = __ballot(take);
     if (take) {
-      const int k = n + __popcll(bal & ((1ull << lane) - 1ull));
-      sidx[k] = s;
+      const int k = m + __popcll(bal & ((1ull << lane) - 1ull));
+      sidx[k] = slot(i);
       swgt[k] = w[e];
     }
-    n += __popcll(bal);
+    m += __popcll(bal);
   }
-  if (n) {
+  if (m) {
     __syncthreads();
-    for (int k0 = 0; k0 < n; k0 += CSPEC) {
+    for (int k0 = 0; k0 < m; k0 += CSPEC) {
       Vec v[CSPEC];
 #pragma unroll
-      for (int u = 0; u < CSPEC; ++u) v[u] = pr[int64_t(sidx[min(k0 + u, n - 1)]) * pstride];
+      for (int u = 0; u < CSPEC; ++u) v[u] = pr[int64_t(sidx[min(k0 + u, m - 1)]) * pstride];
 #pragma unroll
       for (int u = 0; u < CSPEC; ++u)
-        if (k0 + u < n) acc += swgt[k0 + u] * v[u];
+        if (k0 + u < m) acc += swgt[k0 + u] * v[u];
     }
   }
   uint16_t* o = out + (bq / Hq) * sob + (bq % Hq) * soh + DPL * lane;
@@ -408,7 +406,6 @@ Seg to_seg(const iq_segment& s, int start) {
 namespace {
 
 struct Workspace {
-  unsigned long long* tickets;  // [B*Hq] {tag, count} run tickets of the in-kernel merge
   uint32_t* qrec;  // query operand records (unfused path)
   uint32_t* vrec;  // probability operand records (unfused path)
   float* ml;       // [nsplit][B*Hq][2] split (max, sum)
@@ -419,8 +416,6 @@ Workspace carve(void* workspace, int B, int Hq, int T, int D) {
   const size_t rows = size_t(B) * Hq;
   char* ws = (char*)workspace;
   Workspace w{};
-  w.tickets = (unsigned long long*)ws;
-  ws += align256(rows * sizeof(unsigned long long));
   w.qrec = (uint32_t*)ws;
   ws += detail::qk_record_bytes(B, Hq, D);
   size_t vrec_bytes = 0;
@@ -468,15 +463,22 @@ int check_decode(const void* q, const iq_segment* k, const iq_segment* v, int B,
   return IQ_OK;
 }
 
-// Launches everything up to the split statistics and partials; *nsplit = their
-// count.  With `out` (fp16, strides so_b, so_h) the fused kernel merges them
-// into out itself when it covers the packed range (*merged = true; the dense
-// slices run first so that their slots are complete); otherwise, or without
-// `out`, the combine kernel merges them.
+// What the split stage launched: nsplit split slots, nsf of them for the
+// packed range (the rest are dense slices); grid = the fused kernel's
+// workgroup count (0: it did not run, or it wrote empty statistics for a
+// combine that scans every slot).
+struct SplitPlan {
+  int nsplit = 0, nsf = 0, grid = 0, nrep = 1;
+};
+
+// Launches everything up to the split statistics and partials.  `live`: the
+// combine will be told the fused kernel's workgroup count and read only the
+// live slots (the fused kernel then writes no empty statistics).
 int launch_splits(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, const iq_segment* k,
                   const iq_segment* v, int B, int Hq, int Hkv, int T, int D, float scale, const Workspace& w,
-                  int* nsplit, void* out, int64_t so_b, int64_t so_h, bool* merged, hipStream_t st) {
-  *merged = false;
+                  SplitPlan* plan, bool live, hipStream_t st) {
+  *plan = SplitPlan{};
+  plan->nrep = Hq / Hkv;
   const int64_t rows = int64_t(B) * Hq;
   // fused range: packed in both K and V, aligned to K blocks and V groups
   const int ks = k[0].n, vs = v[0].n;
@@ -550,11 +552,11 @@ int launch_splits(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, c
   }
 
   if (fused) {
-    const detail::FusedMerge mg{out, so_b, so_h, w.tickets, nsd};
+    int grid = 0;
     if (int e = detail::flash_fused_launch(q, sq_b, sq_h, norm, fk, fv, B, Hq, Hkv, c, D, scale, w.ml, w.part,
-                                           out ? &mg : nullptr, st))
+                                           live ? &grid : nullptr, st))
       return e;
-    *merged = out != nullptr;
+    plan->grid = grid;
   } else if (c) {
     const iq_segment& kg = k[1];
     const iq_segment& vg = v[1];
@@ -568,17 +570,20 @@ int launch_splits(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, c
                                         vg.group, vg.bits, vg.mode, w.part, st))
       return e;
   }
-  *nsplit = nsf + nsd;
+  plan->nsplit = nsf + nsd;
+  plan->nsf = nsf;
   return IQ_OK;
 }
 
-int launch_combine(const Workspace& w, int nsplit, int B, int Hq, int D, void* out, int64_t so_b, int64_t so_h,
-                   hipStream_t st) {
+int launch_combine(const Workspace& w, const SplitPlan& plan, int B, int Hq, int D, void* out, int64_t so_b,
+                   int64_t so_h, hipStream_t st) {
   const int64_t rows = int64_t(B) * Hq;
+  const int nsplit = plan.nsplit;
   // statistics registers per lane: the smallest power of two with 64 E >= nsplit
   auto go = [&]<int DPL, int E>() {
-    flash_combine_kernel<DPL, E><<<dim3(unsigned(rows)), 64, 0, st>>>(w.ml, w.part, nsplit, rows, Hq,
-                                                                      (uint16_t*)out, so_b, so_h);
+    flash_combine_kernel<DPL, E><<<dim3(unsigned(rows)), 64, 0, st>>>(w.ml, w.part, nsplit, plan.nsf, plan.grid,
+                                                                      plan.nrep, rows, Hq, (uint16_t*)out, so_b,
+                                                                      so_h);
   };
   auto by_e = [&]<int DPL>() {
     if (nsplit <= 64) go.template operator()<DPL, 1>();
@@ -597,10 +602,9 @@ int launch_combine(const Workspace& w, int nsplit, int B, int Hq, int D, void* o
 // The decode workspace (records, split statistics, partials) of
 // iq_decode_attention_noalloc lives in this file-scope device array: each GPU
 // the library runs on holds its own copy, at its own address, until the
-// process ends.  Nothing in it has to be initialized: a run-ticket word
-// without its tag counts as zero, and every split slot the merge reads is
-// written by the same call.  Calls that overlap on one GPU share the
-// array and race.
+// process ends.  Nothing in it has to start at zero: every split slot the
+// combine reads is written by the split stage of the same call.  Calls that
+// overlap on one GPU share the array and race.
 constexpr size_t SCRATCH_BYTES = size_t(64) << 20;
 static __device__ __align__(256) unsigned char scratch[SCRATCH_BYTES];
 
@@ -643,13 +647,10 @@ int iq_decode_attention_noalloc(const void* q, int64_t sq_b, int64_t sq_h, const
   void* ws = nullptr;
   if (int e = scratch_address(&ws)) return e;
   const Workspace w = carve(ws, B, Hq, T, D);
-  int nsplit = 0;
-  bool merged = false;
-  if (int e = launch_splits(q, sq_b, sq_h, norm, k, v, B, Hq, Hkv, T, D, scale, w, &nsplit, out, so_b, so_h,
-                            &merged, (hipStream_t)stream))
+  SplitPlan plan;
+  if (int e = launch_splits(q, sq_b, sq_h, norm, k, v, B, Hq, Hkv, T, D, scale, w, &plan, true, (hipStream_t)stream))
     return e;
-  if (merged) return IQ_OK;
-  return launch_combine(w, nsplit, B, Hq, D, out, so_b, so_h, (hipStream_t)stream);
+  return launch_combine(w, plan, B, Hq, D, out, so_b, so_h, (hipStream_t)stream);
 }
 
 size_t iq_decode_workspace_bytes(int B, int Hq, int T, int D) {
@@ -658,8 +659,8 @@ size_t iq_decode_workspace_bytes(int B, int Hq, int T, int D) {
   size_t vrec = 0;
   for (int g : {32, 64, 128}) vrec = std::max(vrec, rec_bytes_bound(int64_t(B) * Hq, T / g, g));
   const size_t ns = size_t(nsplit_max(T)) + NSD_MAX;
-  return align256(rows * sizeof(unsigned long long)) + detail::qk_record_bytes(B, Hq, D) + align256(vrec) +
-         align256(ns * rows * 2 * 4) + align256(ns * rows * D * 4);
+  return detail::qk_record_bytes(B, Hq, D) + align256(vrec) + align256(ns * rows * 2 * 4) +
+         align256(ns * rows * D * 4);
 }
 
 int iq_decode_attention_splits(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, const iq_segment* k,
@@ -669,9 +670,12 @@ int iq_decode_attention_splits(const void* q, int64_t sq_b, int64_t sq_h, const 
   if (int e = check_decode(q, k, v, B, Hq, Hkv, T, D, workspace, workspace_bytes)) return e;
   *nsplit = 0;
   if (B == 0) return IQ_OK;
-  bool merged = false;
-  return launch_splits(q, sq_b, sq_h, norm, k, v, B, Hq, Hkv, T, D, scale, carve(workspace, B, Hq, T, D), nsplit,
-                       nullptr, 0, 0, &merged, (hipStream_t)stream);
+  SplitPlan plan;
+  // the split stage alone: empty statistics for a combine that scans every slot
+  const int e = launch_splits(q, sq_b, sq_h, norm, k, v, B, Hq, Hkv, T, D, scale, carve(workspace, B, Hq, T, D),
+                              &plan, false, (hipStream_t)stream);
+  *nsplit = plan.nsplit;
+  return e;
 }
 
 int iq_decode_attention_combine(int nsplit, int B, int Hq, int T, int D, void* out, int64_t so_b, int64_t so_h,
@@ -682,7 +686,9 @@ int iq_decode_attention_combine(int nsplit, int B, int Hq, int T, int D, void* o
   IQ_CHECK(workspace_bytes >= iq_decode_workspace_bytes(B, Hq, T, D), IQ_ERR_WORKSPACE);
   IQ_CHECK(aligned(workspace, 256), IQ_ERR_ALIGN);
   if (B == 0) return IQ_OK;
-  return launch_combine(carve(workspace, B, Hq, T, D), nsplit, B, Hq, D, out, so_b, so_h, (hipStream_t)stream);
+  SplitPlan plan;
+  plan.nsplit = plan.nsf = nsplit;  // every slot
+  return launch_combine(carve(workspace, B, Hq, T, D), plan, B, Hq, D, out, so_b, so_h, (hipStream_t)stream);
 }
 
 int iq_decode_attention(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, const iq_segment* k,
@@ -692,13 +698,10 @@ int iq_decode_attention(const void* q, int64_t sq_b, int64_t sq_h, const void* n
   if (int e = check_decode(q, k, v, B, Hq, Hkv, T, D, workspace, workspace_bytes)) return e;
   if (B == 0) return IQ_OK;
   const Workspace w = carve(workspace, B, Hq, T, D);
-  int nsplit = 0;
-  bool merged = false;
-  if (int e = launch_splits(q, sq_b, sq_h, norm, k, v, B, Hq, Hkv, T, D, scale, w, &nsplit, out, so_b, so_h,
-                            &merged, (hipStream_t)stream))
+  SplitPlan plan;
+  if (int e = launch_splits(q, sq_b, sq_h, norm, k, v, B, Hq, Hkv, T, D, scale, w, &plan, true, (hipStream_t)stream))
     return e;
-  if (merged) return IQ_OK;
-  return launch_combine(w, nsplit, B, Hq, D, out, so_b, so_h, (hipStream_t)stream);
+  return launch_combine(w, plan, B, Hq, D, out, so_b, so_h, (hipStream_t)stream);
 }
 
 }  // extern "C"

@@ -124,7 +124,6 @@ struct FusedSmem {
   float m[FS::NW][NREP];
   float l[FS::NW][NREP];
   int next_block;  // the current run's next unclaimed wave block
-  int ticket;      // finished runs of the head before this one (in-kernel merge)
 };
 
 // ---- raw buffer loads -------------------------------------------------------
@@ -140,7 +139,6 @@ struct FusedSmem {
 // of it changed nothing).  The query, reused by every workgroup of a head,
 // keeps the default policy.
 constexpr int STREAM = 2;  // cache policy bits of a streaming load: nt
-constexpr uint32_t TICKET_TAG = 0x9e3779b9u;  // high word of a valid run-ticket word
 constexpr unsigned XCDS = 8;  // accelerator complex dies of an MI355X
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
@@ -423,8 +421,6 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS, AVO>::NT), (fused_waves_pe
     // every read of the statistics is done: a wave that runs ahead into its
     // next run may overwrite them after this barrier
     lds_barrier();
-    // agent-scope stores: complete at the device's coherence point (not held
-    // in this XCD's L2), so a merge on another XCD can read them (merge_head)
     float* dst = a.part + (int64_t(slot) * rows + int64_t(bh) * NREP) * D;
 #pragma unroll
     for (int r = tid; r < NREP * D; r += NT) {
@@ -432,78 +428,13 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS, AVO>::NT), (fused_waves_pe
       float val = 0.f;
 #pragma unroll
       for (int w = 0; w < NW; ++w) val += sm.red[w][h][dd];
-      __hip_atomic_store(dst + r, val, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      dst[r] = val;
     }
     if (!AVO && tid < NREP) {
       float* ml = a.ml + (int64_t(slot) * rows + int64_t(bh) * NREP + tid) * 2;
-      __hip_atomic_store(ml, mls, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(ml + 1, lls, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      ml[0] = mls;
+      ml[1] = lls;
     }
-  };
-
-  // In-kernel merge (decode, a.out set): publish this run's partial, take a
-  // ticket, and if it is the head's last run to finish, merge the head's nr
-  // run partials (slots 0 .. nr-1) and its dense split slots in slot order -
-  // the combine kernel's arithmetic, without its launch.  Publication: the
-  // partial went out with agent-scope stores (flush_run), which count as
-  // complete only once they reach the device's coherence point, so waiting
-  // for them before taking the ticket makes them visible to every XCD; the
-  // merging workgroup reads them with agent-scope loads, which do not hit
-  // stale lines of its own L2.  (An L2 writeback and invalidate per run, the
-  // generic agent-scope fences, cost +10 us per headline launch from one
-  // thread per workgroup and +60 us from every thread, measured; these
-  // accesses +1.3 us.)  A ticket word holds {TICKET_TAG,
-  // count}; a word without the tag counts as zero, so whatever the memory held
-  // before does not matter, and the merging run resets its head's word to
-  // {TICKET_TAG, 0} for the next launch (a replayed graph included).  The
-  // compare-and-swap loop ends: each failed attempt means another run of the
-  // head took a ticket, and a head has nr runs.
-  auto merge_head = [&](int bh, int nr) {
-    __builtin_amdgcn_s_waitcnt(0);  // this thread's partial stores are complete
-    __syncthreads();
-    unsigned long long* tw = a.tickets + bh;
-    constexpr unsigned long long ep = (unsigned long long)TICKET_TAG << 32;
-    if (tid == 0) {
-      unsigned long long cur = __hip_atomic_load(tw, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      sm.ticket = -1;
-      for (int tries = 0; tries <= nr; ++tries) {
-        const unsigned long long nxt = (cur & ~0xffffffffull) == ep ? cur + 1 : ep + 1;
-        const unsigned long long prev = atomicCAS(tw, cur, nxt);
-        if (prev == cur) {
-          sm.ticket = int(uint32_t(nxt)) - 1;
-          break;
-        }
-        cur = prev;
-      }
-    }
-    __syncthreads();
-    if (sm.ticket != nr - 1) return;  // uniform over the workgroup
-    const int b = bh / a.Hkv, kvh = bh - b * a.Hkv;
-    auto ld = [](const float* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
-    const int nl = nr + a.nsd;
-    for (int r = tid; r < NREP * D; r += NT) {
-      const int h = r / D, dd = r - h * D;
-      const int64_t row = int64_t(bh) * NREP + h;
-      float M = -INFINITY;
-      for (int i = 0; i < nl; ++i) {
-        const int sl = i < nr ? i : a.nsplit + (i - nr);
-        M = fmaxf(M, ld(a.ml + (int64_t(sl) * rows + row) * 2));
-      }
-      float L = 0.f, acc = 0.f;
-      for (int i = 0; i < nl; ++i) {
-        const int sl = i < nr ? i : a.nsplit + (i - nr);
-        const float* st = a.ml + (int64_t(sl) * rows + row) * 2;
-        const float ms = ld(st);
-        if (ms != -INFINITY) {
-          const float w = __expf(ms - M);
-          L = fmaf(w, ld(st + 1), L);
-          acc = fmaf(w, ld(a.part + (int64_t(sl) * rows + row) * D + dd), acc);
-        }
-      }
-      a.out[b * a.osb + int64_t(kvh * NREP + h) * a.osh + dd] = __half_as_ushort(__float2half_rn(acc / L));
-    }
-    // every run of the head has taken its ticket: none touches the word again in this launch
-    if (tid == 0) __hip_atomic_store(tw, ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   };
 
   // the lane's tokens' slots in the attn.V operand records and their code biases
@@ -712,10 +643,7 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS, AVO>::NT), (fused_waves_pe
     run_slots(run, slot, nr);
     if constexpr (QKO) lds_barrier();  // every wave is past its last QK^T of the run
     else flush_run(run.bh, slot);
-    if constexpr (!AVO && !QKO) {
-      if (a.out) merge_head(run.bh, nr);
-    }
-    if (!AVO && !QKO && !a.out && wave == 0 && lane < NREP) {
+    if (!AVO && !QKO && a.empty_stats && wave == 0 && lane < NREP) {
       for (int sp = max(run.split0, nr); sp < run.split0 + run.nsplit; ++sp) {
         float* ml = a.ml + (int64_t(sp) * rows + int64_t(run.bh) * NREP + lane) * 2;
         ml[0] = -INFINITY;
@@ -759,7 +687,8 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS, AVO>::NT), (fused_waves_pe
 // Launch of the fused kernel for K bit width KB (the arguments filled by
 // flash_fused_launch): persistent grid, one workgroup per CU.
 template <int KB>
-int fused_launch_kb(const FusedArgs& a, int vbits, int group, int D, int nrep, bool norm, hipStream_t stream) {
+int fused_launch_kb(const FusedArgs& a, int vbits, int group, int D, int nrep, bool norm, int* grid_out,
+                    hipStream_t stream) {
   return dispatch_shape(vbits, group, D, nrep, 0, [&]<int VB, int G, int DD, int R, bool S>() {
     auto* kern = norm ? flash_fused_kernel<KB, VB, G, DD, R, true> : flash_fused_kernel<KB, VB, G, DD, R, false>;
     const int nt = norm ? FusedShape<G, R, true>::NT : FusedShape<G, R, false>::NT;
@@ -772,6 +701,7 @@ int fused_launch_kb(const FusedArgs& a, int vbits, int group, int D, int nrep, b
       pc = n;
     }
     const int grid = int(std::min<int64_t>(a.nitems, int64_t(pc) * detail::num_cus()));
+    if (grid_out) *grid_out = grid;
     kern<<<dim3(grid), nt, 0, stream>>>(a);
     return launch_status();
   });

@@ -26,7 +26,7 @@ bool flash_fused_supported(const void* q, int64_t sq_b, int64_t sq_h, const void
 
 int flash_fused_launch(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, const FusedStore& k,
                        const FusedStore& v, int B, int Hq, int Hkv, int T, int D, float scale, float* ml,
-                       float* part, const FusedMerge* merge, hipStream_t stream) {
+                       float* part, int* grid, hipStream_t stream) {
   if (B == 0 || T == 0) return IQ_OK;
   if (k.group != v.group) return IQ_ERR_GROUP;
   if (T % k.group || FSPLIT != flash_split_tokens()) return IQ_ERR_GROUP;
@@ -50,14 +50,11 @@ int flash_fused_launch(const void* q, int64_t sq_b, int64_t sq_h, const void* no
   a.norm_bytes = norm ? uint32_t(D * 2) : 0u;
   a.scale_log2 = scale * 1.4426950408889634f;
   a.ml = ml; a.part = part;
-  if (merge) {
-    a.out = (uint16_t*)merge->out; a.osb = merge->osb; a.osh = merge->osh;
-    a.tickets = merge->tickets; a.nsd = merge->nsd;
-  }
+  a.empty_stats = grid ? 0 : 1;  // a caller that takes the workgroup count reads only the run slots
   switch (k.bits) {
-    case 2: return flash_fused_launch_k2(a, v.bits, k.group, D, Hq / Hkv, norm != nullptr, stream);
-    case 3: return flash_fused_launch_k3(a, v.bits, k.group, D, Hq / Hkv, norm != nullptr, stream);
-    case 4: return flash_fused_launch_k4(a, v.bits, k.group, D, Hq / Hkv, norm != nullptr, stream);
+    case 2: return flash_fused_launch_k2(a, v.bits, k.group, D, Hq / Hkv, norm != nullptr, grid, stream);
+    case 3: return flash_fused_launch_k3(a, v.bits, k.group, D, Hq / Hkv, norm != nullptr, grid, stream);
+    case 4: return flash_fused_launch_k4(a, v.bits, k.group, D, Hq / Hkv, norm != nullptr, grid, stream);
     default: return IQ_ERR_BITS;
   }
 }

@@ -369,16 +369,9 @@ struct FusedStore {
 // the fused kernel reads each (batch, KV head) slice through 32-bit buffer offsets
 bool flash_fused_supported(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, const FusedStore& k,
                            const FusedStore& v, int Hq, int Hkv, int D);
-// merged output of the fused decode kernel (see FusedArgs::out)
-struct FusedMerge {
-  void* out;
-  int64_t osb, osh;
-  unsigned long long* tickets;
-  int nsd;
-};
 int flash_fused_launch(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, const FusedStore& k,
                        const FusedStore& v, int B, int Hq, int Hkv, int T, int D, float scale, float* ml,
-                       float* part, const FusedMerge* merge, hipStream_t stream);
+                       float* part, int* grid, hipStream_t stream);
 // the fused kernel's arguments (filled by flash_fused_launch)
 struct FusedArgs {
   const uint16_t* q;
@@ -399,21 +392,18 @@ struct FusedArgs {
   float* ml;           // [nsplit][B*Hq][2]
   float* part;         // [nsplit][B*Hq][D]
   int64_t sob, soh;    // QK^T only: strides of the logits output (part)
-  // Merge inside the kernel (decode): the last run of each (batch, KV head)
-  // to finish merges the head's run partials and its nsd dense split slots
-  // (slots nsplit .. nsplit + nsd - 1, written before the launch) into out.
-  // out == nullptr: the partials stay in the workspace for a combine kernel.
-  uint16_t* out;       // fp16 [B, Hq, D], strides osb, osh
-  int64_t osb, osh;
-  // [B*Hkv] finished-run counts as {tag, count} words: a word without the tag
-  // counts as zero, so their prior contents do not matter
-  unsigned long long* tickets;
-  int nsd;
+  // 1: empty statistics in the split slots past a (batch, KV head)'s run
+  // partials (a combine that scans every slot needs them; one told the
+  // launch's workgroup count reads only the run slots)
+  int empty_stats;
 };
 // its launch per K bit width (iq_flash_k{2,3,4}.hip)
-int flash_fused_launch_k2(const FusedArgs& a, int vbits, int group, int D, int nrep, bool norm, hipStream_t stream);
-int flash_fused_launch_k3(const FusedArgs& a, int vbits, int group, int D, int nrep, bool norm, hipStream_t stream);
-int flash_fused_launch_k4(const FusedArgs& a, int vbits, int group, int D, int nrep, bool norm, hipStream_t stream);
+int flash_fused_launch_k2(const FusedArgs& a, int vbits, int group, int D, int nrep, bool norm, int* grid,
+                          hipStream_t stream);
+int flash_fused_launch_k3(const FusedArgs& a, int vbits, int group, int D, int nrep, bool norm, int* grid,
+                          hipStream_t stream);
+int flash_fused_launch_k4(const FusedArgs& a, int vbits, int group, int D, int nrep, bool norm, int* grid,
+                          hipStream_t stream);
 size_t qk_record_bytes(int B, int Hq, int D);
 size_t av_record_bytes(int B, int Hq, int T, int group);
 size_t av_part_bytes(int B, int Hq, int T, int D, int group);
