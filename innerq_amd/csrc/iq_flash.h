@@ -172,17 +172,17 @@ __device__ __forceinline__ uint16_t bload_u16(rsrc_t r, uint32_t voff, uint32_t 
 
 // {scale, zero} of a lane's token (K) or column (V) from its meta dword: asym
 // meta is one {scale, zero} dword per lane; sym meta is one fp16 scale per
-// lane, read as the dword holding the scales of lanes 2i and 2i + 1.
+// lane, read as the dword holding the scales of lanes 2i and 2i + 1.  sh is
+// the lane's shift to its scale: 0 for asym, 16 * (lane & 1) for sym (fixed
+// per store), so both modes take one shift, two conversions, one multiply and
+// one select.
 __device__ __forceinline__ uint32_t meta_voff(int lane, int sym) { return sym ? uint32_t(lane & ~1) * 2 : uint32_t(lane) * 4; }
+__device__ __forceinline__ uint32_t meta_shift(int lane, int sym) { return sym ? uint32_t(lane & 1) * 16 : 0u; }
 template <int BITS>
-__device__ __forceinline__ void meta_sz(uint32_t mw, int lane, int sym, float& s, float& z) {
-  if (sym) {
-    s = h2f(uint16_t((lane & 1) ? (mw >> 16) : (mw & 0xffffu)));
-    z = -float(1 << (BITS - 1)) * s;  // offset-binary codes: signed = u - 2^(b-1)
-  } else {
-    s = h2f(uint16_t(mw & 0xffffu));
-    z = h2f(uint16_t(mw >> 16));
-  }
+__device__ __forceinline__ void meta_sz(uint32_t mw, uint32_t sh, int sym, float& s, float& z) {
+  s = h2f(uint16_t(mw >> sh));
+  const float zh = h2f(uint16_t(mw >> 16));
+  z = sym ? -float(1 << (BITS - 1)) * s : zh;  // offset-binary sym codes: signed = u - 2^(b-1)
 }
 
 // Workgroup barrier for data exchanged through LDS.  __syncthreads() would
@@ -234,6 +234,7 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS, AVO>::NT), (fused_waves_pe
   constexpr bool qsplit = QS;  // key normalization: hi/lo query rows
   const int kms = a.ksym ? 2 : 4, vms = a.vsym ? 2 : 4;  // meta bytes per token / column
   const uint32_t kmv = meta_voff(lane, a.ksym), vmv = meta_voff(lane, a.vsym);
+  const uint32_t ksh = meta_shift(lane, a.ksym), vsh = meta_shift(lane, a.vsym);
   const int64_t rows = int64_t(a.nitems / a.nsplit) * NREP;
 
   struct KRegs { uint32_t w[NG][FBPW][KW]; uint32_t m[NG][FBPW]; };
@@ -378,11 +379,17 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS, AVO>::NT), (fused_waves_pe
   };
 
   // running softmax state of the wave over the current run (log2 domain)
-  float m_run[NREP], l_run[NREP], o_run[NREP][DPL];
+  // Lazy running max: the reference max only has to bound a block's logits,
+  // so it is raised (a wave reduction and a rescale) only when one exceeds it
+  // by more than LAZY_MAX (log2 units): p <= 2^LAZY_MAX, well inside fp16, and
+  // softmax does not depend on the reference.  m_thr = m_run + LAZY_MAX.
+  constexpr float LAZY_MAX = 8.f;
+  float m_run[NREP], m_thr[NREP], l_run[NREP], o_run[NREP][DPL];
   auto reset_run = [&]() {
 #pragma unroll
     for (int h = 0; h < NREP; ++h) {
       m_run[h] = -INFINITY;
+      m_thr[h] = -INFINITY;
       l_run[h] = 0.f;
 #pragma unroll
       for (int e = 0; e < DPL; ++e) o_run[h][e] = 0.f;
@@ -480,7 +487,7 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS, AVO>::NT), (fused_waves_pe
 #pragma unroll
           for (int j = 0; j < FBPW; ++j) {
             float s, z;
-            meta_sz<KB>(kc.m[g][j], lane, a.ksym, s, z);
+            meta_sz<KB>(kc.m[g][j], ksh, a.ksym, s, z);
 #pragma unroll
             for (int h = 0; h < NREP; ++h) {
               const float qs = __uint_as_float(sm.qrec[g][QOS + h]);
@@ -509,22 +516,27 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS, AVO>::NT), (fused_waves_pe
       float mw[NREP], ps[VPW][NREP], alpha[NREP];
       bool rescale = false;  // the running max moved: the run state is rescaled by alpha
       if constexpr (!AVO) {
-        // Lazy running max: the reference max only has to bound the block's
-        // logits, so it is raised (a wave reduction and a rescale) only when
-        // one exceeds it by more than LAZY_MAX (log2 units): p <= 2^LAZY_MAX,
-        // well inside fp16, and softmax does not depend on the reference.
-        constexpr float LAZY_MAX = 8.f;
-        bool need = false;
+        // Each comparison with the lazy threshold is its own ballot (a lane
+        // mask ORed by the scalar unit): one compare per logit.
 #pragma unroll
-        for (int j = 0; j < FBPW; ++j) {
-          const bool live = wt0 + j * TOKEN_BLOCK + lane < a.T;
+        for (int j = 0; j < FBPW; ++j)
 #pragma unroll
-          for (int h = 0; h < NREP; ++h) {
-            acc[j][h] = live ? acc[j][h] * a.scale_log2 : -INFINITY;
-            need |= !(acc[j][h] <= m_run[h] + LAZY_MAX);
+          for (int h = 0; h < NREP; ++h) acc[j][h] *= a.scale_log2;
+        if (wt0 + WTOK > a.T) {  // only a run's last block reaches past the range
+          asm volatile("");      // a real branch: the masking costs nothing in full blocks
+#pragma unroll
+          for (int j = 0; j < FBPW; ++j) {
+            const bool live = wt0 + j * TOKEN_BLOCK + lane < a.T;
+#pragma unroll
+            for (int h = 0; h < NREP; ++h) acc[j][h] = live ? acc[j][h] : -INFINITY;
           }
         }
-        rescale = __builtin_amdgcn_ballot_w64(need) != 0;
+        unsigned long long need = 0;
+#pragma unroll
+        for (int j = 0; j < FBPW; ++j)
+#pragma unroll
+          for (int h = 0; h < NREP; ++h) need |= __builtin_amdgcn_ballot_w64(acc[j][h] > m_thr[h]);
+        rescale = need != 0;
         if (rescale) {
           asm volatile("");  // a real branch: keeps the compiler from flattening it into selects
 #pragma unroll
@@ -539,6 +551,7 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS, AVO>::NT), (fused_waves_pe
             const float mn = fmaxf(m_run[h], mw[h]);
             alpha[h] = m_run[h] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run[h] - mn);
             m_run[h] = mn;
+            m_thr[h] = mn + LAZY_MAX;
           }
         }
       }
@@ -554,7 +567,10 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS, AVO>::NT), (fused_waves_pe
           if constexpr (AVO) {
             p16 = uint16_t(kc.p[j][h]);  // the given probability, as it is
           } else {
-            const float p = acc[j][h] == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(acc[j][h] - m_run[h]);
+            // the running max is finite from the run's first block on (a block
+            // holds at least one token of the range), so a masked logit's
+            // exp2(-inf) is 0 without a test
+            const float p = __builtin_amdgcn_exp2f(acc[j][h] - m_run[h]);
             p16 = __half_as_ushort(__float2half_rn(p));
           }
           const int tl = j * TOKEN_BLOCK + lane;  // token within the wave
@@ -620,7 +636,7 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS, AVO>::NT), (fused_waves_pe
 #pragma unroll
           for (int e = 0; e < DPL; ++e) {
             float s, z;
-            meta_sz<VB>(v.m[u][e], lane, a.vsym, s, z);
+            meta_sz<VB>(v.m[u][e], vsh, a.vsym, s, z);
 #pragma unroll
             for (int h = 0; h < NREP; ++h)
               o_run[h][e] = fmaf(s, dv[e][h / 4][h % 4], fmaf(z, ps[u][h], o_run[h][e]));
