@@ -381,7 +381,16 @@ class InnerqDynamicLayer(CacheLayerMixin):
 
 
 class InnerqDynamicSlidingWindowLayer(InnerqDynamicLayer):
-    """cache.py:421-461."""
+    """cache.py:421-461.
+
+    By default update() behaves as the reference's: once the past exceeds the
+    window it indexes ``[:, :, -w, :]``, a single token with the token axis
+    dropped (cache.py:443-444), and one call earlier it returns one token more
+    than get_mask_sizes() announces, so a model cannot decode past the window.
+    The configuration attribute ``fix_sliding_window = True`` (not in the
+    reference) returns instead the last w - 1 + q tokens of a q-token call once
+    the past reaches the window: the kv_length that get_mask_sizes() announces.
+    """
     is_sliding = True
 
     def __init__(self, config, layer_idx: int, sliding_window: int):
@@ -389,6 +398,7 @@ class InnerqDynamicSlidingWindowLayer(InnerqDynamicLayer):
         self.sliding_window = sliding_window
         self.cumulative_length = 0
         self._sliding_window_tensor = torch.tensor(self.sliding_window, dtype=torch.long)
+        self.fix_sliding_window = bool(getattr(config, "fix_sliding_window", False))
 
     def lazy_initialization(self, key_states: torch.Tensor, value_states: torch.Tensor) -> None:
         super().lazy_initialization(key_states, value_states)
@@ -396,10 +406,16 @@ class InnerqDynamicSlidingWindowLayer(InnerqDynamicLayer):
 
     def update(self, key_states, value_states, cache_kwargs=None):
         full_key_states, full_value_states = super().update(key_states, value_states, cache_kwargs)
-        if self.cumulative_length - key_states.shape[-2] > self.sliding_window:
-            # the reference indexes a single token here (cache.py:443-444); kept as is
-            full_key_states = full_key_states[:, :, -self.sliding_window, :]
-            full_value_states = full_value_states[:, :, -self.sliding_window, :]
+        q = key_states.shape[-2]
+        past = self.cumulative_length - q
+        w = self.sliding_window
+        if not self.fix_sliding_window:
+            if past > w:
+                full_key_states = full_key_states[:, :, -w, :]
+                full_value_states = full_value_states[:, :, -w, :]
+        elif past >= w:
+            full_key_states = full_key_states[:, :, -(w - 1 + q):]
+            full_value_states = full_value_states[:, :, -(w - 1 + q):]
         return full_key_states, full_value_states
 
     def get_mask_sizes(self, query_length) -> tuple[int, int]:

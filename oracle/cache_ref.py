@@ -10,6 +10,7 @@ Follows ``src/innerq/cache.py`` of mthcom/innerq:
 * recent-window flush               cache.py:283-312
 * append quantization + concat      cache.py:314-380
 * update()                          cache.py:382-396
+* sliding-window layer              cache.py:421-461 (SlidingLayerRef)
 
 State is held as numpy arrays ([B,H,T,D] fp16 for sinks / recents, the
 quant_ref triples for the quantized middle).  ``update`` returns the dense
@@ -144,6 +145,42 @@ class CacheLayerRef:
 
     def get_seq_length(self):
         return self.cumulative_length
+
+
+class SlidingLayerRef(CacheLayerRef):
+    """cache.py:421-461: the layer above behind a sliding window of w tokens.
+
+    fix=False keeps the reference's indexing: once the past exceeds the window
+    (cache.py:442), K and V become ``[:, :, -w, :]``, a single token with the
+    token axis dropped (cache.py:443-444), and one call earlier they hold one
+    token more than get_mask_sizes() announces.  fix=True returns the last
+    w - 1 + q tokens of a q-token call once the past reaches the window, the
+    kv_length get_mask_sizes() announces for it (cache.py:448-456)."""
+
+    def __init__(self, config, sliding_window, fix=False):
+        super().__init__(config)
+        self.sliding_window = sliding_window
+        self.fix = fix
+
+    def update(self, k, v):
+        K, V = super().update(k, v)
+        q = np.asarray(k).shape[-2]
+        past = self.cumulative_length - q
+        w = self.sliding_window
+        if not self.fix:
+            if past > w:
+                K, V = K[:, :, -w, :], V[:, :, -w, :]
+        elif past >= w:
+            K, V = K[:, :, -(w - 1 + q):], V[:, :, -(w - 1 + q):]
+        return K, V
+
+    def get_mask_sizes(self, query_length):
+        """cache.py:448-456 (kv_length, kv_offset), before the call's update."""
+        w = self.sliding_window
+        kv_offset = max(self.cumulative_length - w + 1, 0)
+        if self.cumulative_length >= w:
+            return w - 1 + query_length, kv_offset
+        return self.cumulative_length + query_length, kv_offset
 
 
 def schedule(n_prefill, n_steps, w_sink, w_recent, flush, quantize=True, over_token=False):

@@ -17,8 +17,14 @@ cache_golden.npz    InnerqDynamicLayer.update() traces: prefill + decode steps
                     seed with innerq_amd.synth); full dense K/V of the last
                     decode call, SHA-256 of every call's K/V bytes,
                     and the recent-window lengths after every call.
+sliding_golden.npz  InnerqDynamicSlidingWindowLayer.update() traces
+                    (cache.py:421-461) across the window boundary: per call the
+                    shapes and SHA-256 of the returned K/V (a single token, the
+                    dimension dropped, once the past exceeds the window: the
+                    reference indexes [:, :, -w, :]), the recent-window lengths
+                    and get_mask_sizes() before the call.
 
-Usage:  python tests/golden/make_golden.py [/root/reference]
+Usage:  python tests/golden/make_golden.py [/root/reference] [--sliding-only]
 """
 from __future__ import annotations
 
@@ -78,8 +84,60 @@ def quant_input():
     return x.astype(np.float16)
 
 
-def main(root):
+SLIDING_PRESETS = {
+    "sliding_asym4": dict(k_bits=4, v_bits=4, key_flush_size=1, value_flush_size=32, key_group_size=32,
+                          value_group_size=32, key_w_recent=32, value_w_recent=64, key_w_sink=0, value_w_sink=0,
+                          key_normalize=False, key_quantize_over_token=False, value_quantize_over_token=True,
+                          key_quantize_mode="asymmetric", value_quantize_mode="asymmetric"),
+    "sliding_sym3_sinks": dict(k_bits=3, v_bits=3, key_flush_size=1, value_flush_size=32, key_group_size=32,
+                               value_group_size=32, key_w_recent=40, value_w_recent=40, key_w_sink=8,
+                               value_w_sink=8, key_normalize=True, key_quantize_over_token=False,
+                               value_quantize_over_token=True, key_quantize_mode="symmetric",
+                               value_quantize_mode="symmetric"),
+}
+SLIDING = dict(B=1, H=2, D=64, window=96, prefill=80, steps=40)
+
+
+def sliding_traces(cache):
+    """Traces of the reference sliding-window layer across its window."""
+    class Layer(cache.InnerqDynamicSlidingWindowLayer):
+        def get_max_length(self):   # abstract in the installed transformers
+            return self.sliding_window
+
+    class Cfg:
+        pass
+
+    out = {}
+    B, H, D, w, prefill, steps = (SLIDING[k] for k in ("B", "H", "D", "window", "prefill", "steps"))
+    for name, kw in SLIDING_PRESETS.items():
+        cfg = Cfg()
+        for k, v in kw.items():
+            setattr(cfg, k, v)
+        layer = Layer(cfg, 0, w)
+        seed = sum(map(ord, name))
+        kx = synth.kv_tensor(B, H, prefill + steps, D, seed=seed, n_out=2, factor=8.0)
+        vx = synth.kv_tensor(B, H, prefill + steps, D, seed=seed + 1, n_out=2, factor=8.0)
+        out[f"{name}_seed"] = np.array([seed, B, H, D, w, prefill, steps])
+        kt, vt = torch.from_numpy(kx), torch.from_numpy(vx)
+        for s in range(steps + 1):
+            lo, hi = (0, prefill) if s == 0 else (prefill + s - 1, prefill + s)
+            q_len = hi - lo
+            mask = layer.get_mask_sizes(torch.arange(q_len)) if s else (0, 0)
+            K, V = layer.update(kt[:, :, lo:hi].clone(), vt[:, :, lo:hi].clone())
+            shape = list(K.shape) + [0] * (4 - K.dim())
+            out[f"{name}_step{s}_shape"] = np.array([K.dim()] + shape + list(V.shape) + [0] * (4 - V.dim()))
+            out[f"{name}_step{s}_sha256"] = digest(np.concatenate([f16(K).ravel(), f16(V).ravel()]))
+            out[f"{name}_step{s}_state"] = np.array([layer.keys_recent.shape[-2], layer.values_recent.shape[-2],
+                                                     layer.cumulative_length, mask[0], mask[1]])
+    return out
+
+
+def main(root, sliding_only=False):
     quant, cache = load_reference(root)
+    np.savez_compressed(os.path.join(HERE, "sliding_golden.npz"), **sliding_traces(cache))
+    print("wrote", os.path.join(HERE, "sliding_golden.npz"))
+    if sliding_only:
+        return
     out = {}
     x = quant_input()
     out["x"] = x.view(np.uint16)
@@ -186,4 +244,5 @@ def main(root):
 
 
 if __name__ == "__main__":
-    main(sys.argv[1] if len(sys.argv) > 1 else "/root/reference")
+    args = [a for a in sys.argv[1:] if not a.startswith("--")]
+    main(args[0] if args else "/root/reference", sliding_only="--sliding-only" in sys.argv)

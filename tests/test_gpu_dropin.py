@@ -291,3 +291,113 @@ def test_fused_cache_follows_an_attention_switch():
     ref, got = logits["reference"], logits["switching"]
     err = ((got - ref).abs().amax(dim=(1, 2)) / ref.abs().amax(dim=(1, 2)))
     assert err.max().item() < 2e-2, err.tolist()
+
+
+# ------------------------------------------------------------------------------------------
+# sliding-window layer (cache.py:421-461)
+from tests.test_oracle_cache import SLIDING, _shape_row, sliding_inputs  # noqa: E402
+
+
+@pytest.fixture(scope="module")
+def sliding_golden():
+    import os
+    from tests.conftest import GOLDEN
+    return np.load(os.path.join(GOLDEN, "sliding_golden.npz"))
+
+
+@pytest.mark.parametrize("name", list(SLIDING))
+def test_sliding_layer_matches_reference_trace(sliding_golden, name):
+    """The drop-in sliding layer without the fix reproduces the live reference's
+    trace call by call: shapes (a single token, rank 3, once the past exceeds
+    the window), recent-window lengths and mask sizes equal to the trace; K/V
+    equal in value to the oracle's (pinned bit-exact to the trace) and, for the
+    asym preset, in bytes to the trace.  (Values, not bits, for sym: the packed
+    sym format does not keep the sign of a zero code.)"""
+    from oracle import cache_ref
+    g = sliding_golden
+    kx, vx, w, prefill, steps = sliding_inputs(g, name)
+    layer = C.InnerqDynamicSlidingWindowLayer(Cfg(**SLIDING[name]), 0, w)
+    ref = cache_ref.SlidingLayerRef(Cfg(**SLIDING[name]), w)
+    kt, vt = torch.from_numpy(kx).to(DEV), torch.from_numpy(vx).to(DEV)
+    for s in range(steps + 1):
+        lo, hi = (0, prefill) if s == 0 else (prefill + s - 1, prefill + s)
+        mask = layer.get_mask_sizes(torch.arange(hi - lo)) if s else (0, 0)
+        K, V = layer.update(kt[:, :, lo:hi], vt[:, :, lo:hi])
+        Kr, Vr = ref.update(kx[:, :, lo:hi], vx[:, :, lo:hi])
+        K, V = K.cpu().numpy(), V.cpu().numpy()
+        np.testing.assert_array_equal(_shape_row(K, V), g[f"{name}_step{s}_shape"], err_msg=f"step {s}")
+        np.testing.assert_array_equal(K, Kr, err_msg=f"K step {s}")
+        np.testing.assert_array_equal(V, Vr, err_msg=f"V step {s}")
+        if SLIDING[name]["key_quantize_mode"] == "asymmetric":
+            b = np.concatenate([K.view(np.uint16).ravel(), V.view(np.uint16).ravel()])
+            np.testing.assert_array_equal(_sha(b), g[f"{name}_step{s}_sha256"], err_msg=f"step {s}")
+        state = [layer.keys_recent.shape[-2], layer.values_recent.shape[-2], layer.cumulative_length, *mask]
+        np.testing.assert_array_equal(state, g[f"{name}_step{s}_state"], err_msg=f"step {s}")
+
+
+@pytest.mark.parametrize("name", list(SLIDING))
+def test_sliding_layer_fix_matches_oracle(name):
+    """fix_sliding_window = True: K/V equal to the oracle's fixed layer at every
+    call (values: sym zero codes come back as +0.0), as long as
+    get_mask_sizes() announces."""
+    from oracle import cache_ref
+    cfg = Cfg(**SLIDING[name], fix_sliding_window=True)
+    kx = synth.kv_tensor(1, 2, 140, 64, seed=9, n_out=2, factor=8.0)
+    vx = synth.kv_tensor(1, 2, 140, 64, seed=10, n_out=2, factor=8.0)
+    w = 96
+    ref = cache_ref.SlidingLayerRef(cfg, w, fix=True)
+    layer = C.InnerqDynamicSlidingWindowLayer(cfg, 0, w)
+    kt, vt = torch.from_numpy(kx).to(DEV), torch.from_numpy(vx).to(DEV)
+    for s in range(61):
+        lo, hi = (0, 80) if s == 0 else (79 + s, 80 + s)
+        kv_len, kv_off = layer.get_mask_sizes(hi - lo)
+        assert (kv_len, kv_off) == ref.get_mask_sizes(hi - lo)
+        K, V = layer.update(kt[:, :, lo:hi], vt[:, :, lo:hi])
+        Kr, Vr = ref.update(kx[:, :, lo:hi], vx[:, :, lo:hi])
+        assert K.shape[-2] == kv_len
+        np.testing.assert_array_equal(K.cpu().numpy(), Kr, err_msg=f"step {s}")
+        np.testing.assert_array_equal(V.cpu().numpy(), Vr, err_msg=f"step {s}")
+
+
+def _tiny_mistral(preset, window=48):
+    from transformers import MistralConfig
+    from innerq_amd.models import InnerqMistralForCausalLM
+    cfg = MistralConfig(num_hidden_layers=2, num_attention_heads=8, num_key_value_heads=2, hidden_size=512,
+                        intermediate_size=256, vocab_size=64, max_position_embeddings=512, sliding_window=window)
+    for k, v in preset.items():
+        setattr(cfg, k, v)
+    cfg.fix_sliding_window = True
+    cfg._attn_implementation = "eager"
+    torch.manual_seed(0)
+    return InnerqMistralForCausalLM(cfg).to(device=DEV, dtype=torch.float16).eval()
+
+
+def _decode(model, cache, ids, dec):
+    steps = []
+    with torch.no_grad():
+        model(ids, past_key_values=cache, use_cache=True)
+        for t in range(dec.shape[1]):
+            steps.append(model(dec[:, t:t + 1], past_key_values=cache, use_cache=True).logits[:, -1].float())
+    return torch.stack(steps)
+
+
+def test_mistral_decodes_past_the_window_with_the_fix():
+    """A random 2-layer Mistral (sliding window 48) on the drop-in cache with
+    fix_sliding_window = True decodes 30 steps past its window (the reference's
+    layer cannot: its K/V lose the token axis).  With quantization off (16-bit
+    K and V) the window is exactly transformers' own sliding cache's: logits
+    equal to fp16 rounding; with 4-bit K and V the steps run and stay finite."""
+    from transformers import DynamicCache as HFCache
+    gen = torch.Generator(device=DEV).manual_seed(3)
+    ids = torch.randint(0, 64, (1, 40), generator=gen, device=DEV)
+    dec = torch.randint(0, 64, (1, 30), generator=gen, device=DEV)
+    model = _tiny_mistral(dict(SLIDING["sliding_asym4"], k_bits=16, v_bits=16))
+    cache = C.DynamicCache(config=model.config)
+    assert all(isinstance(l, C.InnerqDynamicSlidingWindowLayer) for l in cache.layers)
+    got = _decode(model, cache, ids, dec)
+    ref = _decode(model, HFCache(config=model.config), ids, dec)
+    assert ((got - ref).abs().max() / ref.abs().max()).item() < 1e-3
+    model = _tiny_mistral(SLIDING["sliding_asym4"])
+    cache = C.DynamicCache(config=model.config)
+    got = _decode(model, cache, ids, dec)
+    assert torch.isfinite(got).all() and cache.get_seq_length() == 70

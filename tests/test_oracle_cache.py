@@ -92,3 +92,76 @@ def test_value_recent_window_drains():
     nr = [x[2] for x in sched]
     assert nr[0] == 84  # (468 - r) % 32 == 0 -> r = 84
     assert min(nr[1:]) < 32 and max(nr[1:]) <= 96
+
+
+# ------------------------------------------------------------------------------------------
+# sliding-window layer (cache.py:421-461) against the live reference's traces
+SLIDING = {
+    "sliding_asym4": dict(k_bits=4, v_bits=4, key_flush_size=1, value_flush_size=32, key_group_size=32,
+                          value_group_size=32, key_w_recent=32, value_w_recent=64, key_w_sink=0, value_w_sink=0,
+                          key_normalize=False, key_quantize_over_token=False, value_quantize_over_token=True,
+                          key_quantize_mode="asymmetric", value_quantize_mode="asymmetric"),
+    "sliding_sym3_sinks": dict(k_bits=3, v_bits=3, key_flush_size=1, value_flush_size=32, key_group_size=32,
+                               value_group_size=32, key_w_recent=40, value_w_recent=40, key_w_sink=8,
+                               value_w_sink=8, key_normalize=True, key_quantize_over_token=False,
+                               value_quantize_over_token=True, key_quantize_mode="symmetric",
+                               value_quantize_mode="symmetric"),
+}
+
+
+def sliding_inputs(g, name):
+    seed, B, H, D, w, prefill, steps = (int(x) for x in g[f"{name}_seed"])
+    kx = synth.kv_tensor(B, H, prefill + steps, D, seed=seed, n_out=2, factor=8.0)
+    vx = synth.kv_tensor(B, H, prefill + steps, D, seed=seed + 1, n_out=2, factor=8.0)
+    return kx, vx, w, prefill, steps
+
+
+def _shape_row(K, V):
+    return np.array([K.ndim] + list(K.shape) + [0] * (4 - K.ndim) + list(V.shape) + [0] * (4 - V.ndim))
+
+
+@pytest.fixture(scope="module")
+def sliding_golden():
+    import os
+    from tests.conftest import GOLDEN
+    return np.load(os.path.join(GOLDEN, "sliding_golden.npz"))
+
+
+@pytest.mark.parametrize("name", list(SLIDING))
+def test_sliding_oracle_matches_reference_trace(sliding_golden, name):
+    """The reference's sliding layer, bug included: per call the shapes and
+    SHA-256 of K/V, the recent-window lengths, the cumulative length and the
+    mask sizes announced before the call."""
+    g = sliding_golden
+    kx, vx, w, prefill, steps = sliding_inputs(g, name)
+    layer = cache_ref.SlidingLayerRef(Cfg(**SLIDING[name]), w)
+    for s in range(steps + 1):
+        lo, hi = (0, prefill) if s == 0 else (prefill + s - 1, prefill + s)
+        mask = layer.get_mask_sizes(hi - lo) if s else (0, 0)
+        K, V = layer.update(kx[:, :, lo:hi], vx[:, :, lo:hi])
+        np.testing.assert_array_equal(_shape_row(K, V), g[f"{name}_step{s}_shape"], err_msg=f"step {s}")
+        np.testing.assert_array_equal(_sha(K, V), g[f"{name}_step{s}_sha256"], err_msg=f"step {s}")
+        state = [layer.keys_recent.shape[-2], layer.values_recent.shape[-2], layer.cumulative_length, *mask]
+        np.testing.assert_array_equal(state, g[f"{name}_step{s}_state"], err_msg=f"step {s}")
+    # the reference hands back one token, rank 3, once the past exceeds the window
+    assert K.ndim == 3
+
+
+@pytest.mark.parametrize("name", list(SLIDING))
+def test_sliding_fix_returns_the_announced_window(name):
+    """fix=True: every call returns the last kv_length tokens of the full layer's
+    K/V, kv_length as get_mask_sizes() announced it before the call."""
+    cfg = Cfg(**SLIDING[name])
+    kx = synth.kv_tensor(1, 2, 140, 64, seed=9, n_out=2, factor=8.0)
+    vx = synth.kv_tensor(1, 2, 140, 64, seed=10, n_out=2, factor=8.0)
+    w = 96
+    fixed = cache_ref.SlidingLayerRef(cfg, w, fix=True)
+    full = cache_ref.CacheLayerRef(cfg)
+    for s in range(61):
+        lo, hi = (0, 80) if s == 0 else (79 + s, 80 + s)
+        kv_len, _ = fixed.get_mask_sizes(hi - lo)
+        K, V = fixed.update(kx[:, :, lo:hi], vx[:, :, lo:hi])
+        Kf, Vf = full.update(kx[:, :, lo:hi], vx[:, :, lo:hi])
+        assert K.shape[-2] == kv_len, (s, K.shape, kv_len)
+        np.testing.assert_array_equal(K, Kf[:, :, -kv_len:])
+        np.testing.assert_array_equal(V, Vf[:, :, -kv_len:])
