@@ -19,7 +19,9 @@
  *    points also take 1 with IQ_MODE_ASYM: the asym half of 2-bit hybrid
  *    quantization, quant.py:136); group in {32,64,128}; head_dim D in {64,128};
  *    query heads per KV head (Hq/Hkv) in {1,2,4,8}; mode IQ_MODE_ASYM or
- *    IQ_MODE_SYM (quant.py:43-56 'asymmetric' / 'symmetric').
+ *    IQ_MODE_SYM (quant.py:43-56 'asymmetric' / 'symmetric'); packed stores
+ *    also IQ_MODE_HYBRID ('hybrid', bits 2-4, below), which the V side of
+ *    iq_av_gemv and of the decode entry points reads.
  *
  * Packed stores (layout owned by this library)
  *  K store, groups along head_dim (quant.py:75-77 channeldim):
@@ -31,6 +33,14 @@
  *  Inside a group, code i occupies bits [bits*i, bits*i+bits) LSB first
  *  (speedtest/benchmark_quantization.cu:25-84); asym stores the code, sym
  *  sign*magnitude + 2^(bits-1) (offset binary, benchmark_quantization.cu:128).
+ *  Hybrid stores (quant.py:133-176) keep one representation per group, the
+ *  one the reference's mask selects, in b-bit fields and an asym-sized meta
+ *  word (M = 2): flag = bit 15 of the scale half (tested as a bit, so a -0.0
+ *  scale reads as flagged).  Flag clear: the group's (b-1)-bit asym code,
+ *  {scale, zero}.  Flag set: the b-bit sym code (offset binary), {scale |
+ *  0x8000, 0}.  The flag is the sign bit of the fp16 scale, as in the
+ *  reference's hybrid attn.V proxy (speedtest/benchmark_attn_v.cu:541-636),
+ *  which marks its asym groups there.
  */
 #ifndef INNERQ_ABI_H
 #define INNERQ_ABI_H
@@ -53,12 +63,12 @@ enum iq_status {
   IQ_ERR_SHAPE = -4,      /* a size is negative / zero where not allowed / unsupported head_dim or GQA ratio */
   IQ_ERR_ALIGN = -5,      /* pointer or stride not aligned as the kernel needs */
   IQ_ERR_WORKSPACE = -6,  /* workspace missing or smaller than *_workspace_bytes() */
-  IQ_ERR_MODE = -7,       /* mode not IQ_MODE_ASYM / IQ_MODE_SYM */
+  IQ_ERR_MODE = -7,       /* mode not IQ_MODE_ASYM / IQ_MODE_SYM (/ IQ_MODE_HYBRID where taken) */
   IQ_ERR_RANGE = -8,      /* token offset + count exceeds the store capacity */
   IQ_ERR_HIP = -9         /* a HIP launch failed */
 };
 
-enum iq_mode { IQ_MODE_ASYM = 0, IQ_MODE_SYM = 1 };
+enum iq_mode { IQ_MODE_ASYM = 0, IQ_MODE_SYM = 1, IQ_MODE_HYBRID = 2 };
 
 /* ABI version (IQ_ABI_VERSION) and error names. */
 int iq_abi_version(void);
@@ -78,6 +88,10 @@ int iq_v_store_bytes(int64_t B, int64_t H, int64_t t_cap, int64_t D, int group, 
  * plus the torch.cat append of cache.py:314-339 (quantize_new_keys).
  * norm: optional fp16 [B,H,D] key-normalization factor; x is divided by it
  * in fp16 first (cache.py:121-126).  Codes are bit-exact to quant.py.
+ * IQ_MODE_HYBRID (bits 2-4) quantizes each group both ways, (bits-1)-bit
+ * asym and bits-bit sym, and keeps the sym codes where the asym L1 error is
+ * the larger (quant.py:133-151; error sums in fp64, see iq_hybrid_mask); it
+ * writes the store only (dense outputs NULL).
  * Optional dense outputs (NULL to skip), contiguous:
  *   codes_i32 int32 [B,H,n,D]   exactly quant.py's codes (INT32_MIN for NaN);
  *                               for sym the magnitude codes
@@ -102,7 +116,8 @@ int iq_quantize_v(const void* x, int64_t sx_b, int64_t sx_h, int64_t sx_t,
  * c*s for sym, then * norm when given), written as fp16 (out16) and/or fp32
  * (out32) with element strides so_b, so_h, so_t.  Replaces
  * dequantize_channeldim_{asym,sym} (quant.py:83-87, 121-125) and the
- * unnormalize step of cache.py:241-250 (get_keys_deq). */
+ * unnormalize step of cache.py:241-250 (get_keys_deq).  Hybrid stores: each
+ * group as its flag says, i.e. dequantize_hybrid (quant.py:153-176). */
 int iq_dequant_k(const uint32_t* k_codes, const uint16_t* k_meta, int64_t t_cap, const void* norm,
                  int B, int H, int t0, int T, int D, int group, int bits, int mode,
                  void* out16, float* out32, int64_t so_b, int64_t so_h, int64_t so_t, void* stream);
@@ -130,7 +145,10 @@ int iq_dequant_dense(const int32_t* codes, const void* scale16, const void* zs16
  * does not keep), all contiguous.  K: scale/zero [B,H,T,D/G]; V (t0, T
  * multiples of group): scale/zero [B,H,T/G,D].  Backs the state attributes
  * keys_q / keys_scale_factor / keys_zp_sign (and values_*) of
- * cache.py:190-210 for callers that read them. */
+ * cache.py:190-210 for callers that read them.  Hybrid stores give the raw
+ * fields: codes_i32 the stored field (flagged groups: offset binary),
+ * scale16 the meta scale half with its flag bit, zs16 the zero half
+ * ([.., units] as asym); the caller splits them into quant.py's dicts. */
 int iq_unpack_k(const uint32_t* k_codes, const uint16_t* k_meta, int64_t t_cap, int B, int H, int t0, int T, int D,
                 int group, int bits, int mode, int32_t* codes_i32, void* scale16, void* zs16, void* stream);
 int iq_unpack_v(const uint32_t* v_codes, const uint16_t* v_meta, int64_t t_cap, int B, int H, int t0, int T, int D,
@@ -187,7 +205,10 @@ size_t iq_av_workspace_bytes(int B, int Hq, int T, int D, int group);
  * go to the workspace and an atomic-free second pass sums them.  If accumulate
  * is nonzero the result is added to out32 (fp32 [B,Hq,D], strides so_*)
  * instead of overwriting it.  out16 (fp16, same strides) optional.  Replaces
- * matmul(p, repeat_kv(V_deq)) (TF/models/llama/modeling_llama.py:210). */
+ * matmul(p, repeat_kv(V_deq)) (TF/models/llama/modeling_llama.py:210).  A
+ * hybrid store (mode IQ_MODE_HYBRID) takes s = |scale| and z = zero, or
+ * -2^(bits-1) |scale| for flagged groups: the single pass of
+ * speedtest/benchmark_attn_v.cu:541-636 over the exact hybrid format. */
 int iq_av_gemv(const void* p, int64_t sp_b, int64_t sp_h,
                const uint32_t* v_codes, const uint16_t* v_meta, int64_t t_cap,
                int B, int Hq, int Hkv, int t0, int T, int D, int group, int bits, int mode,
@@ -218,7 +239,8 @@ size_t iq_decode_workspace_bytes(int B, int Hq, int T, int D);
  * (TF/models/llama/modeling_llama.py:208), then p.V over V = [vs | vq | vr].
  * k[3] / v[3] are the sink, quantized and recent segments; the token counts of
  * K and V must each sum to T.  norm: optional fp16 [B,Hkv,D] key
- * normalization factor of the quantized K segment.  out fp16 [B,Hq,D]
+ * normalization factor of the quantized K segment; the quantized V segment
+ * may be a hybrid store (K: asym or sym).  out fp16 [B,Hq,D]
  * (strides so_b, so_h).  Replaces update()'s dense read path (cache.py:278-281,
  * 395) plus the eager attention of TF/models/llama/modeling_llama.py:201-210. */
 int iq_decode_attention(const void* q, int64_t sq_b, int64_t sq_h, const void* norm,

@@ -14,6 +14,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libinnerq_h
 IQ_OK = 0
 IQ_MODE_ASYM = 0
 IQ_MODE_SYM = 1
+IQ_MODE_HYBRID = 2
 TOKEN_BLOCK = 64
 
 STATUS = {

@@ -37,57 +37,33 @@ class _Quantized:
     """The packed tokens of one role (K or V) of a layer.
 
     axis 'channel' groups along head_dim (quant.py:75-77), 'token' along tokens
-    (quant.py:79-81).  Hybrid keeps an asym store (bits-1), a sym store (bits)
-    and the per-group choice (quant.py:133-176).
+    (quant.py:79-81).  Hybrid (quant.py:133-176) is one packed store that keeps,
+    per group, the representation the reference's mask selects: (bits-1)-bit
+    asym or bits-bit sym codes, marked by a flag bit in the group's scale.
     """
 
     def __init__(self, axis: str, like: torch.Tensor, group: int, bits: int, mode: QMode):
         B, H, _, D = like.shape
         self.axis, self.group, self.bits, self.mode = axis, group, bits, mode
-        dev = like.device
-        if mode == QMode.HYBRID:
-            self.zp = ops.PackedStore(axis, B, H, D, group, bits - 1, "asymmetric", dev)
-            self.nozp = ops.PackedStore(axis, B, H, D, group, bits, "symmetric", dev)
-            self.mask: Optional[torch.Tensor] = None
-            self.store = None
-        else:
-            self.store = ops.PackedStore(axis, B, H, D, group, bits, mode.value, dev)
+        self.store = ops.PackedStore(axis, B, H, D, group, bits, mode.value, like.device)
 
     @property
     def length(self) -> int:
-        return (self.store or self.zp).length
+        return self.store.length
 
     def append(self, x: torch.Tensor, norm: Optional[torch.Tensor]) -> None:
         """Quantize x [B,H,n,D] (divided by norm in fp16 first, keys only) and append it."""
         if norm is not None and self.axis != "channel":
             raise NotImplementedError("key normalization is supported for keys grouped along head_dim")
-        if self.mode != QMode.HYBRID:
-            self.store.append(x, norm=norm)
-            return
-        t0, n = self.zp.length, x.shape[2]
-        self.zp.append(x, norm=norm)
-        self.nozp.append(x, norm=norm)
-        da = self.zp.dequant(t0, n, dtype=torch.float32)
-        ds = self.nozp.dequant(t0, n, dtype=torch.float32)
-        mask = ops.hybrid_mask(x.contiguous(), da, ds, self.group, self.axis, norm=norm)
-        self.mask = mask if self.mask is None else torch.cat([self.mask, mask], dim=2)
+        self.store.append(x, norm=norm)
 
     def dequant_into(self, out: torch.Tensor, norm: Optional[torch.Tensor]) -> None:
         """Dense values (times norm) of every packed token, written into the fp16 view ``out``."""
-        if self.mode != QMode.HYBRID:
-            self.store.dequant(0, self.length, out=out, norm=norm)
-            return
-        da = self.zp.dequant(dtype=torch.float32, norm=norm)
-        ds = self.nozp.dequant(dtype=torch.float32, norm=norm)
-        out.copy_(ops.hybrid_select(da, ds, self.mask, self.group, self.axis, dtype=out.dtype))
+        self.store.dequant(0, self.length, out=out, norm=norm)
 
     def reference_tensors(self):
         """(codes, scale, zero|signs) as quant.py returns them (dicts for hybrid)."""
-        if self.mode != QMode.HYBRID:
-            return ops.unpack_store(self.store)
-        cz, sz, zz = ops.unpack_store(self.zp)
-        cs, ss, gs = ops.unpack_store(self.nozp)
-        return {'zp': cz, 'nozp': cs}, {'zp': sz, 'nozp': ss, 'mask': self.mask}, {'zp': zz, 'nozp': gs}
+        return ops.unpack_store(self.store)
 
 
 class InnerqDynamicLayer(CacheLayerMixin):
@@ -323,14 +299,22 @@ class InnerqDynamicLayer(CacheLayerMixin):
         else:
             self.add_to_cache(key_states, value_states)
 
+    def _fused_refusal(self) -> Optional[str]:
+        """Why attend() cannot read this layer's stores (None if it can): K must be
+        grouped along head_dim (asym or sym), V along tokens (asym, sym or hybrid)."""
+        if self._kq is not None and (self._kq.axis != "channel" or self._kq.mode == QMode.HYBRID):
+            return "fused decode reads keys grouped along the head_dim axis, asym or sym"
+        if self._vq is not None and self._vq.axis != "token":
+            return "fused decode reads values grouped along the token axis"
+        return None
+
     def fused_decode_ready(self, key_states: torch.Tensor) -> bool:
         """Whether attend() can serve this step: one new token per sequence, a
-        prefilled full-attention layer, K grouped along head_dim and V along
-        tokens (asym or sym)."""
+        prefilled full-attention layer, K grouped along head_dim (asym or sym) and
+        V along tokens (asym, sym or hybrid)."""
         if self.is_sliding or not self.is_initialized or key_states.shape[-2] != 1:
             return False
-        return all(q is None or (q.mode != QMode.HYBRID and q.axis == want)
-                   for q, want in ((self._kq, "channel"), (self._vq, "token")))
+        return self._fused_refusal() is None
 
     def attend(self, query_states: torch.Tensor, scaling: float) -> torch.Tensor:
         """Decode attention of one new token per sequence over this layer's cache:
@@ -340,10 +324,9 @@ class InnerqDynamicLayer(CacheLayerMixin):
             raise ValueError("attend() takes one query token per sequence: [B, Hq, 1, D]")
         if not self.is_initialized:
             raise RuntimeError("attend() needs a prefilled cache")
-        for q, name, want in ((self._kq, "keys", "channel"), (self._vq, "values", "token")):
-            if q is not None and (q.mode == QMode.HYBRID or q.axis != want):
-                raise NotImplementedError(f"fused decode reads {name} grouped along the "
-                                          f"{'head_dim' if want == 'channel' else 'token'} axis, asym or sym")
+        why = self._fused_refusal()
+        if why is not None:
+            raise NotImplementedError(why)
         q = query_states[:, :, 0]
         out = ops.decode_attention(
             q, self.keys_sink if self.keys_sink.shape[-2] else None, self._kq.store if self._kq else None,

@@ -58,6 +58,7 @@ struct AVArgs {
   int64_t cap_groups;
   int Hkv, g0, ngroups, gpw;
   float* part;           // [nsplit][B*Hq][D]
+  int hyb;               // hybrid store (per-group flag in the meta dword)
 };
 
 template <int BITS, int G, int D, int NREP, bool SYM>
@@ -126,8 +127,9 @@ __global__ __launch_bounds__(WG) void av_kernel(AVArgs a) {
                                        lane & 3, pr, dv);
 #pragma unroll
         for (int e = 0; e < DPL; ++e) {
-          const float s = h2f(uint16_t(cm[u][e] & 0xffffu));
-          const float z = SYM ? -float(1 << (BITS - 1)) * s : h2f(uint16_t(cm[u][e] >> 16));
+          float s = h2f(uint16_t(cm[u][e] & 0xffffu));
+          float z = SYM ? -float(1 << (BITS - 1)) * s : h2f(uint16_t(cm[u][e] >> 16));
+          if (!SYM && a.hyb) meta_sz_hyb<BITS>(cm[u][e], s, z);
 #pragma unroll
           for (int h = 0; h < NREP; ++h) {
             const float ps = rec_f32(rec, NP * NREP + h);
@@ -194,7 +196,7 @@ int groups_per_wg(int B, int Hkv, int ngroups) {
 int check_av(const void* p, const uint32_t* v_codes, const uint16_t* v_meta, int64_t t_cap, int B, int Hq, int Hkv,
              int t0, int T, int D, int group, int bits, int mode) {
   IQ_CHECK(p && v_codes && v_meta, IQ_ERR_NULL);
-  if (int e = check_common(bits, group, mode)) return e;
+  if (int e = check_v_common(bits, group, mode)) return e;
   IQ_CHECK(B >= 0 && T >= 0 && t0 >= 0 && Hkv > 0 && Hq > 0, IQ_ERR_SHAPE);
   IQ_CHECK(d_ok(D) && Hq % Hkv == 0 && nrep_ok(Hq / Hkv), IQ_ERR_SHAPE);
   IQ_CHECK(T % group == 0 && t0 % group == 0 && t_cap % group == 0, IQ_ERR_GROUP);
@@ -245,7 +247,7 @@ int av_launch_gpw(const uint32_t* rec, const uint32_t* v_codes, const uint16_t* 
                   hipStream_t stream) {
   const int ng = T / group;
   const int nsplit = int(ceil_div(ng, gpw));
-  AVArgs a{rec, v_codes, v_meta, t_cap / group, Hkv, t0 / group, ng, gpw, part};
+  AVArgs a{rec, v_codes, v_meta, t_cap / group, Hkv, t0 / group, ng, gpw, part, mode == IQ_MODE_HYBRID};
   return dispatch_shape(bits, group, D, Hq / Hkv, mode == IQ_MODE_SYM, [&]<int BITS, int G, int DD, int R, bool S>() {
     av_kernel<BITS, G, DD, R, S><<<dim3(nsplit, B * Hkv), WG, 0, stream>>>(a);
     return launch_status();
@@ -299,16 +301,19 @@ int av_fused_launch(const void* p, int64_t sp_b, int64_t sp_h, const uint32_t* v
   a.v_meta_bytes = uint32_t(int64_t(T / group) * D * (a.vsym ? 2 : 4));
   a.q_bytes = uint32_t((int64_t(nrep - 1) * sp_h + T) * 2);
   a.part = part;
+  const bool hyb = mode == IQ_MODE_HYBRID;
   return dispatch_shape(bits, group, D, nrep, 0, [&]<int VB, int G, int DD, int R, bool S>() {
-    auto* kern = flash_fused_kernel<VB, VB, G, DD, R, false, true>;
+    auto* kern = hyb ? flash_fused_kernel<VB, VB, G, DD, R, false, true, false, true>
+                     : flash_fused_kernel<VB, VB, G, DD, R, false, true>;
     const int nt = FusedShape<G, R, false, true>::NT;
-    static int per_cu = 0;  // workgroups per CU at once
-    if (per_cu == 0) {
+    static int per_cu[2] = {0, 0};  // workgroups per CU at once
+    int& pc = per_cu[hyb ? 1 : 0];
+    if (pc == 0) {
       int n = 0;
       if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, nt, 0) != hipSuccess || n <= 0) n = 1;
-      per_cu = n;
+      pc = n;
     }
-    *grid = int(std::min<int64_t>(a.nitems, int64_t(per_cu) * num_cus()));
+    *grid = int(std::min<int64_t>(a.nitems, int64_t(pc) * num_cus()));
     kern<<<dim3(*grid), nt, 0, stream>>>(a);
     return launch_status();
   });

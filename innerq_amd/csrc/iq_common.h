@@ -13,6 +13,7 @@ namespace iq {
 inline bool bits_ok(int bits) { return bits == 2 || bits == 3 || bits == 4; }
 inline bool group_ok(int g) { return g == 32 || g == 64 || g == 128; }
 inline bool mode_ok(int m) { return m == IQ_MODE_ASYM || m == IQ_MODE_SYM; }
+inline bool store_mode_ok(int m) { return mode_ok(m) || m == IQ_MODE_HYBRID; }
 inline bool d_ok(int d) { return d == 64 || d == 128; }
 inline bool nrep_ok(int r) { return r == 1 || r == 2 || r == 4 || r == 8; }
 inline bool aligned(const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; }
@@ -29,15 +30,28 @@ inline int check_common(int bits, int group, int mode) {
   return IQ_OK;
 }
 
-// Packed stores also hold 1-bit asym codes: the asym half of 2-bit hybrid
-// quantization (quant.py:136).  The GEMVs take 2-4 bits only.
+// Packed stores also hold 1-bit asym codes (the asym half of 2-bit hybrid
+// quantization, quant.py:136) and hybrid groups (bits 2-4).  The GEMVs take
+// 2-4 bits only.
 inline int check_store(int bits, int group, int mode) {
   IQ_CHECK(bits_ok(bits) || bits == 1, IQ_ERR_BITS);
   IQ_CHECK(group_ok(group), IQ_ERR_GROUP);
-  IQ_CHECK(mode_ok(mode), IQ_ERR_MODE);
+  IQ_CHECK(store_mode_ok(mode), IQ_ERR_MODE);
   IQ_CHECK(bits != 1 || mode == IQ_MODE_ASYM, IQ_ERR_BITS);
   return IQ_OK;
 }
+
+// a V store read by the attn.V GEMV / decode: asym, sym or hybrid
+inline int check_v_common(int bits, int group, int mode) {
+  IQ_CHECK(bits_ok(bits), IQ_ERR_BITS);
+  IQ_CHECK(group_ok(group), IQ_ERR_GROUP);
+  IQ_CHECK(store_mode_ok(mode), IQ_ERR_MODE);
+  return IQ_OK;
+}
+
+// meta bytes per unit (K token-group, V group-column): sym stores keep the
+// scale only, asym and hybrid {scale, zero}
+inline int meta_unit_bytes(int mode) { return mode == IQ_MODE_SYM ? 2 : 4; }
 
 inline int launch_status() {
   hipError_t e = hipGetLastError();

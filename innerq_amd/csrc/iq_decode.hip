@@ -39,7 +39,7 @@ struct Seg {
   const uint32_t* codes;
   const uint16_t* meta;
   int64_t t_cap;
-  int t0, bits, group, sym;
+  int t0, bits, group, mode;
 };
 
 __device__ __forceinline__ uint32_t field(const uint32_t* w, int bits, int i) {
@@ -49,12 +49,13 @@ __device__ __forceinline__ uint32_t field(const uint32_t* w, int bits, int i) {
   return f & ((1u << bits) - 1u);
 }
 
-__device__ __forceinline__ float deq(uint32_t f, int bits, int sym, const uint16_t* meta, int64_t unit) {
-  if (sym) {
+__device__ __forceinline__ float deq(uint32_t f, int bits, int mode, const uint16_t* meta, int64_t unit) {
+  if (mode == IQ_MODE_SYM) {
     const int c = int(f) - (1 << (bits - 1));  // offset binary
     return __fmul_rn(float(c), h2f(meta[unit]));
   }
   const uint32_t sz = reinterpret_cast<const uint32_t*>(meta)[unit];
+  if (mode == IQ_MODE_HYBRID) return hyb_value(f, bits, sz);
   return __fadd_rn(__fmul_rn(float(f), h2f(uint16_t(sz & 0xffffu))), h2f(uint16_t(sz >> 16)));
 }
 
@@ -67,12 +68,12 @@ __device__ float packed_elem(const Seg& g, bool is_k, int64_t bh, int D, int tl,
     const int ng = D / g.group;
     const int64_t unit = ((bh * (g.t_cap / TOKEN_BLOCK) + st / TOKEN_BLOCK) * ng + d / g.group) * TOKEN_BLOCK +
                          st % TOKEN_BLOCK;
-    float v = deq(field(g.codes + unit * W, g.bits, d % g.group), g.bits, g.sym, g.meta, unit);
+    float v = deq(field(g.codes + unit * W, g.bits, d % g.group), g.bits, g.mode, g.meta, unit);
     if (norm) v = __fmul_rn(v, h2f(norm[bh * D + d]));
     return v;
   }
   const int64_t unit = (bh * (g.t_cap / g.group) + st / g.group) * D + d;
-  return deq(field(g.codes + unit * W, g.bits, st % g.group), g.bits, g.sym, g.meta, unit);
+  return deq(field(g.codes + unit * W, g.bits, st % g.group), g.bits, g.mode, g.meta, unit);
 }
 
 // fp16 elements [d0, d0 + N) of token t's row (a K or V segment list), as N/2
@@ -395,7 +396,7 @@ Seg to_seg(const iq_segment& s, int start) {
   g.sb = s.s_b; g.sh = s.s_h; g.st = s.s_t;
   g.n = s.n; g.start = start;
   g.codes = s.codes; g.meta = s.meta; g.t_cap = s.t_cap; g.t0 = s.t0;
-  g.bits = s.bits; g.group = s.group; g.sym = s.mode == IQ_MODE_SYM;
+  g.bits = s.bits; g.group = s.group; g.mode = s.mode;
   if (s.n && s.codes) g.dense = nullptr;
   g.vec = g.dense && aligned(g.dense, 16) && s.s_b % 8 == 0 && s.s_h % 8 == 0 && s.s_t % 8 == 0;
   return g;
@@ -453,7 +454,7 @@ int check_decode(const void* q, const iq_segment* k, const iq_segment* v, int B,
   if (v[1].n) {
     const iq_segment& g = v[1];
     IQ_CHECK(g.codes && g.meta, IQ_ERR_NULL);
-    if (int e = check_common(g.bits, g.group, g.mode)) return e;
+    if (int e = check_v_common(g.bits, g.group, g.mode)) return e;
     IQ_CHECK(g.n % g.group == 0 && g.t0 % g.group == 0 && g.t0 >= 0 && g.t_cap % g.group == 0, IQ_ERR_GROUP);
     IQ_CHECK(int64_t(g.t0) + g.n <= g.t_cap, IQ_ERR_RANGE);
     IQ_CHECK(aligned(g.codes, 16) && aligned(g.meta, 8), IQ_ERR_ALIGN);

@@ -196,6 +196,21 @@ __device__ __forceinline__ float round_f16(float x) {
   return __half2float(__float2half_rn(x));
 }
 
+// Hybrid stores: a group's meta dword is {scale | flag << 15, zero}; the flag
+// (bit 15, tested as a bit: a -0.0 scale is flagged) marks b-bit sym codes in
+// offset binary, else the field holds the (b-1)-bit asym code.
+constexpr uint32_t HYB_FLAG = 0x8000u;
+__device__ __forceinline__ bool hyb_sym(uint32_t mw) { return (mw & HYB_FLAG) != 0u; }
+__device__ __forceinline__ float hyb_scale(uint32_t mw) { return h2f(uint16_t(mw & 0x7fffu)); }
+
+// the reference's value of one field of a hybrid group (quant.py:153-176):
+// asym u*s + z (fp32, c*s exact), sym (u - 2^(b-1))*s (exact)
+__device__ __forceinline__ float hyb_value(uint32_t u, int bits, uint32_t mw) {
+  const float s = hyb_scale(mw);
+  if (hyb_sym(mw)) return __fmul_rn(float(int(u) - (1 << (bits - 1))), s);
+  return __fadd_rn(__fmul_rn(float(u), s), h2f(uint16_t(mw >> 16)));
+}
+
 // ---------------------------------------------------------------------------
 // wave64 reductions
 // ---------------------------------------------------------------------------

@@ -185,6 +185,16 @@ __device__ __forceinline__ void meta_sz(uint32_t mw, uint32_t sh, int sym, float
   z = sym ? -float(1 << (BITS - 1)) * s : zh;  // offset-binary sym codes: signed = u - 2^(b-1)
 }
 
+// {scale, zero} of a hybrid V group-column from its meta dword: the flag bit
+// (bit 15, tested as a bit) marks b-bit sym codes (offset binary, zero
+// -2^(b-1) |scale|), else (b-1)-bit asym codes with the stored zero.
+template <int BITS>
+__device__ __forceinline__ void meta_sz_hyb(uint32_t mw, float& s, float& z) {
+  s = hyb_scale(mw);
+  const float zh = h2f(uint16_t(mw >> 16));
+  z = hyb_sym(mw) ? -float(1 << (BITS - 1)) * s : zh;
+}
+
 // Workgroup barrier for data exchanged through LDS.  __syncthreads() would
 // also wait for every outstanding global load, i.e. for the next split's
 // prefetch; only the LDS writes need to be complete.
@@ -211,7 +221,8 @@ __device__ __forceinline__ float seg_sum(float v) {
 // softmax; each block's scaled logits (scale_log2 holds the plain scale) go to
 // the fp32 output at part (element strides sob, soh per batch and query head,
 // 1 per token).
-template <int KB, int VB, int G, int D, int NREP, bool QS, bool AVO = false, bool QKO = false>
+// VH: the V store is hybrid (per-group flag in its meta, meta_sz_hyb).
+template <int KB, int VB, int G, int D, int NREP, bool QS, bool AVO = false, bool QKO = false, bool VH = false>
 __global__ __launch_bounds__((FusedShape<G, NREP, QS, AVO>::NT), (fused_waves_per_simd<G, NREP, QS, AVO>())) void flash_fused_kernel(FusedArgs a) {
   using FS = FusedShape<G, NREP, QS, AVO>;
   constexpr int NW = FS::NW, NT = FS::NT, WTOK = FS::WTOK, FBPW = FS::FBPW, VPW = FS::VPW;
@@ -636,7 +647,8 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS, AVO>::NT), (fused_waves_pe
 #pragma unroll
           for (int e = 0; e < DPL; ++e) {
             float s, z;
-            meta_sz<VB>(v.m[u][e], vsh, a.vsym, s, z);
+            if constexpr (VH) meta_sz_hyb<VB>(v.m[u][e], s, z);
+            else meta_sz<VB>(v.m[u][e], vsh, a.vsym, s, z);
 #pragma unroll
             for (int h = 0; h < NREP; ++h)
               o_run[h][e] = fmaf(s, dv[e][h / 4][h % 4], fmaf(z, ps[u][h], o_run[h][e]));
@@ -701,12 +713,13 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS, AVO>::NT), (fused_waves_pe
 }
 
 // Launch of the fused kernel for K bit width KB (the arguments filled by
-// flash_fused_launch): persistent grid, one workgroup per CU.
-template <int KB>
+// flash_fused_launch): persistent grid, one workgroup per CU.  VH: hybrid V.
+template <int KB, bool VH = false>
 int fused_launch_kb(const FusedArgs& a, int vbits, int group, int D, int nrep, bool norm, int* grid_out,
                     hipStream_t stream) {
   return dispatch_shape(vbits, group, D, nrep, 0, [&]<int VB, int G, int DD, int R, bool S>() {
-    auto* kern = norm ? flash_fused_kernel<KB, VB, G, DD, R, true> : flash_fused_kernel<KB, VB, G, DD, R, false>;
+    auto* kern = norm ? flash_fused_kernel<KB, VB, G, DD, R, true, false, false, VH>
+                      : flash_fused_kernel<KB, VB, G, DD, R, false, false, false, VH>;
     const int nt = norm ? FusedShape<G, R, true>::NT : FusedShape<G, R, false>::NT;
     // as many workgroups as fit at once on the device
     static int per_cu[2] = {0, 0};

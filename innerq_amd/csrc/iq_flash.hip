@@ -51,6 +51,15 @@ int flash_fused_launch(const void* q, int64_t sq_b, int64_t sq_h, const void* no
   a.scale_log2 = scale * 1.4426950408889634f;
   a.ml = ml; a.part = part;
   a.empty_stats = grid ? 0 : 1;  // a caller that takes the workgroup count reads only the run slots
+  if (k.mode == IQ_MODE_HYBRID) return IQ_ERR_MODE;
+  if (v.mode == IQ_MODE_HYBRID) {
+    switch (k.bits) {
+      case 2: return flash_fused_launch_vh_k2(a, v.bits, k.group, D, Hq / Hkv, norm != nullptr, grid, stream);
+      case 3: return flash_fused_launch_vh_k3(a, v.bits, k.group, D, Hq / Hkv, norm != nullptr, grid, stream);
+      case 4: return flash_fused_launch_vh_k4(a, v.bits, k.group, D, Hq / Hkv, norm != nullptr, grid, stream);
+      default: return IQ_ERR_BITS;
+    }
+  }
   switch (k.bits) {
     case 2: return flash_fused_launch_k2(a, v.bits, k.group, D, Hq / Hkv, norm != nullptr, grid, stream);
     case 3: return flash_fused_launch_k3(a, v.bits, k.group, D, Hq / Hkv, norm != nullptr, grid, stream);

@@ -1,0 +1,13 @@
+// Instantiations of the fused flash-decoding kernel for 2-bit K and a hybrid
+// V store (every V bit width, group size, head_dim and query heads per KV
+// head).
+#include "iq_flash.h"
+
+namespace iq::detail {
+
+int flash_fused_launch_vh_k2(const FusedArgs& a, int vbits, int group, int D, int nrep, bool norm, int* grid,
+                             hipStream_t stream) {
+  return fused_launch_kb<2, true>(a, vbits, group, D, nrep, norm, grid, stream);
+}
+
+}  // namespace iq::detail

@@ -404,6 +404,13 @@ int flash_fused_launch_k3(const FusedArgs& a, int vbits, int group, int D, int n
                           hipStream_t stream);
 int flash_fused_launch_k4(const FusedArgs& a, int vbits, int group, int D, int nrep, bool norm, int* grid,
                           hipStream_t stream);
+// and for a hybrid V store (iq_flash_vh_k{2,3,4}.hip)
+int flash_fused_launch_vh_k2(const FusedArgs& a, int vbits, int group, int D, int nrep, bool norm, int* grid,
+                             hipStream_t stream);
+int flash_fused_launch_vh_k3(const FusedArgs& a, int vbits, int group, int D, int nrep, bool norm, int* grid,
+                             hipStream_t stream);
+int flash_fused_launch_vh_k4(const FusedArgs& a, int vbits, int group, int D, int nrep, bool norm, int* grid,
+                             hipStream_t stream);
 size_t qk_record_bytes(int B, int Hq, int D);
 size_t av_record_bytes(int B, int Hq, int T, int group);
 size_t av_part_bytes(int B, int Hq, int T, int D, int group);

@@ -43,58 +43,114 @@ __device__ __forceinline__ int32_t code_of(float y, float L) {
   return (int32_t)rintf(y);
 }
 
+// Group statistics and per-element codes of the two quantizers, one fp16
+// rounding per reference op.
+// asym (quant.py:66-71): scale and zero (the group minimum) of b-bit codes
+template <int BITS, int G>
+__device__ __forceinline__ void asym_params(const float* v, float& s, float& mn) {
+  float mx = v[0];
+  bool nan = false;
+  mn = v[0];
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    nan |= is_nan(v[i]);
+    mn = fminf(mn, v[i]);
+    mx = fmaxf(mx, v[i]);
+  }
+  if (nan) { mn = __builtin_nanf(""); mx = mn; }
+  s = round_f16(round_f16(mx - mn) / float((1 << BITS) - 1));      // quant.py:68
+}
+template <int BITS>
+__device__ __forceinline__ int32_t asym_code(float x, float mn, float s) {
+  return code_of(round_f16(round_f16(x - mn) / s), float((1 << BITS) - 1));  // quant.py:69-71
+}
+// sym (quant.py:104-109): scale of b-bit codes (one bit is the sign)
+template <int BITS, int G>
+__device__ __forceinline__ float sym_scale(const float* v) {
+  float mx = 0.f;
+  bool nan = false;
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    nan |= is_nan(v[i]);
+    mx = fmaxf(mx, fabsf(v[i]));
+  }
+  if (nan) mx = __builtin_nanf("");
+  return round_f16(mx / float((1 << (BITS - 1)) - 1));              // quant.py:107
+}
+template <int BITS>
+__device__ __forceinline__ int32_t sym_code(float x, float s) {
+  return code_of(round_f16(fabsf(x) / s), float((1 << (BITS - 1)) - 1));  // quant.py:108-109
+}
+__device__ __forceinline__ float sign_of(float x) { return x > 0.f ? 1.f : (x < 0.f ? -1.f : 0.f); }  // torch.sign
+// stored fields: the asym code (0 for NaN); sym sign*magnitude + 2^(b-1)
+template <int BITS>
+__device__ __forceinline__ uint32_t asym_field(int32_t c) {
+  return (c == I32_MIN) ? 0u : (uint32_t(c) & ((1u << BITS) - 1u));
+}
+template <int BITS>
+__device__ __forceinline__ uint32_t sym_field(int32_t c, float sg) {
+  const int32_t sc = (c == I32_MIN) ? 0 : (sg > 0.f ? c : (sg < 0.f ? -c : 0));
+  return uint32_t(sc + (1 << (BITS - 1))) & ((1u << BITS) - 1u);  // offset binary
+}
+
 // Quantize G values held as fp32 copies of fp16 numbers.  fields[] receives
 // the b-bit stored field, codes[] the dense reference code, sgn[] the sign.
 template <int BITS, int G>
 __device__ __forceinline__ void quantize_group(const float* v, bool sym, uint32_t* fields, int32_t* codes,
                                                float* sgn, float& s_out, float& z_out) {
-  constexpr uint32_t FMASK = (1u << BITS) - 1u;
   if (!sym) {
-    float mn = v[0], mx = v[0];
-    bool nan = false;
+    float s, mn;
+    asym_params<BITS, G>(v, s, mn);
 #pragma unroll
     for (int i = 0; i < G; ++i) {
-      nan |= is_nan(v[i]);
-      mn = fminf(mn, v[i]);
-      mx = fmaxf(mx, v[i]);
-    }
-    if (nan) { mn = __builtin_nanf(""); mx = mn; }
-    const float L = float((1 << BITS) - 1);
-    const float s = round_f16(round_f16(mx - mn) / L);          // quant.py:68
-#pragma unroll
-    for (int i = 0; i < G; ++i) {
-      const float y = round_f16(round_f16(v[i] - mn) / s);      // quant.py:69-70
-      const int32_t c = code_of(y, L);                          // quant.py:71
+      const int32_t c = asym_code<BITS>(v[i], mn, s);
       codes[i] = c;
-      fields[i] = (c == I32_MIN) ? 0u : (uint32_t(c) & FMASK);
+      fields[i] = asym_field<BITS>(c);
       sgn[i] = 0.f;
     }
     s_out = s;
     z_out = mn;
   } else {
-    float mx = 0.f;
-    bool nan = false;
+    const float s = sym_scale<BITS, G>(v);
 #pragma unroll
     for (int i = 0; i < G; ++i) {
-      nan |= is_nan(v[i]);
-      mx = fmaxf(mx, fabsf(v[i]));
-    }
-    if (nan) mx = __builtin_nanf("");
-    const float L = float((1 << (BITS - 1)) - 1);
-    const float s = round_f16(mx / L);                          // quant.py:107
-#pragma unroll
-    for (int i = 0; i < G; ++i) {
-      const float y = round_f16(fabsf(v[i]) / s);               // quant.py:108
-      const int32_t c = code_of(y, L);                          // quant.py:109
-      const float sg = v[i] > 0.f ? 1.f : (v[i] < 0.f ? -1.f : 0.f);  // torch.sign
+      const int32_t c = sym_code<BITS>(v[i], s);
+      const float sg = sign_of(v[i]);
       codes[i] = c;
-      const int32_t sc = (c == I32_MIN) ? 0 : (sg > 0.f ? c : (sg < 0.f ? -c : 0));
-      fields[i] = uint32_t(sc + (1 << (BITS - 1))) & FMASK;  // offset binary
+      fields[i] = sym_field<BITS>(c, sg);
       sgn[i] = sg;
     }
     s_out = s;
     z_out = 0.f;
   }
+}
+
+// Hybrid (quant.py:133-151): the group quantized both ways, (b-1)-bit asym
+// and b-bit sym; their fp32 dequantizations as the reference computes them
+// (asym c*s + z, sym c*s*sign, a NaN code as INT32_MIN: quant.py:83-93,
+// 121-131); the sym codes are kept iff the asym L1 error is the larger.  The
+// error sums are accumulated in fp64 (as iq_hybrid_mask).  fields[] gets the
+// kept b-bit fields, mw the meta dword {scale | flag << 15, zero}.
+template <int BITS, int G>
+__device__ __forceinline__ void quantize_group_hybrid(const float* v, uint32_t* fields, uint32_t& mw) {
+  float sa, za;
+  asym_params<BITS - 1, G>(v, sa, za);
+  const float ss = sym_scale<BITS, G>(v);
+  double ea = 0.0, es = 0.0;
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    const float da = __fadd_rn(__fmul_rn(float(asym_code<BITS - 1>(v[i], za, sa)), sa), za);
+    const float ds = __fmul_rn(__fmul_rn(float(sym_code<BITS>(v[i], ss)), ss), sign_of(v[i]));
+    ea += double(fabsf(__fsub_rn(da, v[i])));
+    es += double(fabsf(__fsub_rn(ds, v[i])));
+  }
+  const bool sym = ea > es;
+#pragma unroll
+  for (int i = 0; i < G; ++i)
+    fields[i] = sym ? sym_field<BITS>(sym_code<BITS>(v[i], ss), sign_of(v[i]))
+                    : asym_field<BITS>(asym_code<BITS - 1>(v[i], za, sa));
+  const uint32_t sh = __half_as_ushort(__float2half_rn(sym ? ss : sa));
+  mw = sym ? (sh | HYB_FLAG) : ((sh & 0x7fffu) | (uint32_t(__half_as_ushort(__float2half_rn(za))) << 16));
 }
 
 template <int BITS, int G>
@@ -111,6 +167,25 @@ __device__ __forceinline__ void pack_fields(const uint32_t* f, uint32_t* w) {
     w[wi] |= f[i] << o;
     if (o + BITS > 32) w[wi + 1] |= f[i] >> (32 - o);
   }
+}
+
+// one group's fields and meta into the store: W code words at unit * W;
+// meta one fp16 scale (sym) or one {scale, zero} dword (asym, hybrid)
+template <int BITS, int G>
+__device__ __forceinline__ void store_group(const QuantOut& o, int64_t unit, const uint32_t* f, bool half_meta,
+                                            uint32_t mw) {
+  constexpr int W = G * BITS / 32;
+  uint32_t w[W];
+  pack_fields<BITS, G>(f, w);
+  uint32_t* cp = o.codes + unit * W;
+#pragma unroll
+  for (int j = 0; j < W; ++j) cp[j] = w[j];
+  if (half_meta) o.meta[unit] = uint16_t(mw);
+  else reinterpret_cast<uint32_t*>(o.meta)[unit] = mw;
+}
+
+__device__ __forceinline__ uint32_t meta_word(float s, float z) {
+  return uint32_t(__half_as_ushort(__float2half_rn(s))) | (uint32_t(__half_as_ushort(__float2half_rn(z))) << 16);
 }
 
 template <int BITS, int G>
@@ -130,11 +205,11 @@ __device__ __forceinline__ void unpack_fields(const uint32_t* w, bool sym, int32
 }
 
 // ---- K: groups along head_dim, one thread per (b, h, t, g) ----------------
-template <int BITS, int G, bool DENSE>
+// HYB: a hybrid store (store only, no dense outputs)
+template <int BITS, int G, bool DENSE, bool HYB = false>
 __global__ __launch_bounds__(256) void quant_k_kernel(const uint16_t* __restrict__ x, int64_t sxb, int64_t sxh,
                                                       int64_t sxt, const uint16_t* __restrict__ norm, int B,
                                                       int H, int n, int D, int sym, QuantOut o) {
-  constexpr int W = G * BITS / 32;
   const int ng = D / G;
   const int64_t gid = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   const int64_t total = int64_t(B) * H * n * ng;
@@ -163,30 +238,23 @@ __global__ __launch_bounds__(256) void quant_k_kernel(const uint16_t* __restrict
 #pragma unroll
     for (int i = 0; i < G; ++i) v[i] = round_f16(v[i] / h2f(np_[i]));
   }
+  const int64_t bh = int64_t(b) * H + h;
+  const int64_t tt = o.t_off + t;
+  const int64_t unit = ((bh * o.cap_units + tt / TOKEN_BLOCK) * ng + g) * TOKEN_BLOCK + tt % TOKEN_BLOCK;
   uint32_t f[G];
+  if constexpr (HYB) {
+    if constexpr (BITS >= 2) {
+      uint32_t mw;
+      quantize_group_hybrid<BITS, G>(v, f, mw);
+      store_group<BITS, G>(o, unit, f, false, mw);
+    }
+    return;
+  }
   int32_t c[G];
   float sg[G];
   float s, z;
   quantize_group<BITS, G>(v, sym != 0, f, c, sg, s, z);
-
-  const int64_t bh = int64_t(b) * H + h;
-  if (o.codes) {
-    uint32_t w[W];
-    pack_fields<BITS, G>(f, w);
-    const int64_t tt = o.t_off + t;
-    const int64_t blk = tt / TOKEN_BLOCK, row = tt % TOKEN_BLOCK;
-    const int64_t unit = ((bh * o.cap_units + blk) * ng + g) * TOKEN_BLOCK + row;
-    uint32_t* cp = o.codes + unit * W;
-#pragma unroll
-    for (int j = 0; j < W; ++j) cp[j] = w[j];
-    if (sym) {
-      o.meta[unit] = __half_as_ushort(__float2half_rn(s));
-    } else {
-      const uint32_t sz = uint32_t(__half_as_ushort(__float2half_rn(s))) |
-                          (uint32_t(__half_as_ushort(__float2half_rn(z))) << 16);
-      reinterpret_cast<uint32_t*>(o.meta)[unit] = sz;
-    }
-  }
+  if (o.codes) store_group<BITS, G>(o, unit, f, sym != 0, meta_word(s, z));
   if constexpr (DENSE) {  // the reference-format outputs (quant.py API)
     const int64_t row_el = (bh * n + t) * D + g * G;
     if (o.codes_i32) {
@@ -204,11 +272,10 @@ __global__ __launch_bounds__(256) void quant_k_kernel(const uint16_t* __restrict
 }
 
 // ---- V: groups along tokens, one thread per (b, h, token-group, d) --------
-template <int BITS, int G, bool DENSE>
+template <int BITS, int G, bool DENSE, bool HYB = false>
 __global__ __launch_bounds__(256) void quant_v_kernel(const uint16_t* __restrict__ x, int64_t sxb, int64_t sxh,
                                                       int64_t sxt, int B, int H, int n, int D, int sym,
                                                       QuantOut o) {
-  constexpr int W = G * BITS / 32;
   const int ngn = n / G;
   const int64_t gid = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   const int64_t total = int64_t(B) * H * ngn * D;
@@ -224,29 +291,22 @@ __global__ __launch_bounds__(256) void quant_v_kernel(const uint16_t* __restrict
   float v[G];
 #pragma unroll
   for (int i = 0; i < G; ++i) v[i] = h2f(xp[i * sxt]);
+  const int64_t bh = int64_t(b) * H + h;
+  const int64_t unit = (bh * o.cap_units + o.t_off / G + gi) * D + d;
   uint32_t f[G];
+  if constexpr (HYB) {
+    if constexpr (BITS >= 2) {
+      uint32_t mw;
+      quantize_group_hybrid<BITS, G>(v, f, mw);
+      store_group<BITS, G>(o, unit, f, false, mw);
+    }
+    return;
+  }
   int32_t c[G];
   float sg[G];
   float s, z;
   quantize_group<BITS, G>(v, sym != 0, f, c, sg, s, z);
-
-  const int64_t bh = int64_t(b) * H + h;
-  if (o.codes) {
-    uint32_t w[W];
-    pack_fields<BITS, G>(f, w);
-    const int64_t gabs = o.t_off / G + gi;
-    const int64_t unit = (bh * o.cap_units + gabs) * D + d;
-    uint32_t* cp = o.codes + unit * W;
-#pragma unroll
-    for (int j = 0; j < W; ++j) cp[j] = w[j];
-    if (sym) {
-      o.meta[unit] = __half_as_ushort(__float2half_rn(s));
-    } else {
-      const uint32_t sz = uint32_t(__half_as_ushort(__float2half_rn(s))) |
-                          (uint32_t(__half_as_ushort(__float2half_rn(z))) << 16);
-      reinterpret_cast<uint32_t*>(o.meta)[unit] = sz;
-    }
-  }
+  if (o.codes) store_group<BITS, G>(o, unit, f, sym != 0, meta_word(s, z));
   if constexpr (DENSE) {  // the reference-format outputs (quant.py API)
     if (o.codes_i32 || o.signs16) {
 #pragma unroll
@@ -274,11 +334,34 @@ __device__ __forceinline__ void put(const DeqOut& o, int64_t off, float v) {
   if (o.out32) o.out32[off] = v;
 }
 
+// signed codes and {scale, zero} of one group such that value = c*s + z:
+// asym {s, z}; sym offset binary, z = 0; hybrid as the group's flag says
+// (quant.py:153-176: the sym codes where the mask is set)
+template <int BITS, int G>
+__device__ __forceinline__ void group_deq_params(const uint32_t* w, const uint16_t* meta, int64_t unit, int mode,
+                                                 int32_t* c, float& s, float& z) {
+  unpack_fields<BITS, G>(w, mode == IQ_MODE_SYM, c);
+  z = 0.f;
+  if (mode == IQ_MODE_SYM) {
+    s = h2f(meta[unit]);
+    return;
+  }
+  const uint32_t mw = reinterpret_cast<const uint32_t*>(meta)[unit];
+  if (mode == IQ_MODE_HYBRID && hyb_sym(mw)) {
+#pragma unroll
+    for (int i = 0; i < G; ++i) c[i] -= 1 << (BITS - 1);
+    s = hyb_scale(mw);
+    return;
+  }
+  s = mode == IQ_MODE_HYBRID ? hyb_scale(mw) : h2f(uint16_t(mw & 0xffffu));
+  z = h2f(uint16_t(mw >> 16));
+}
+
 template <int BITS, int G>
 __global__ __launch_bounds__(256) void dequant_k_kernel(const uint32_t* __restrict__ kc,
                                                         const uint16_t* __restrict__ km, int64_t cap_blocks,
                                                         const uint16_t* __restrict__ norm, int B, int H, int t0,
-                                                        int T, int D, int sym, DeqOut o) {
+                                                        int T, int D, int mode, DeqOut o) {
   constexpr int W = G * BITS / 32;
   const int ng = D / G;
   const int64_t gid = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -297,15 +380,8 @@ __global__ __launch_bounds__(256) void dequant_k_kernel(const uint32_t* __restri
 #pragma unroll
   for (int j = 0; j < W; ++j) w[j] = kc[unit * W + j];
   int32_t c[G];
-  unpack_fields<BITS, G>(w, sym != 0, c);
-  float s, z = 0.f;
-  if (sym) {
-    s = h2f(km[unit]);
-  } else {
-    const uint32_t sz = reinterpret_cast<const uint32_t*>(km)[unit];
-    s = h2f(uint16_t(sz & 0xffffu));
-    z = h2f(uint16_t(sz >> 16));
-  }
+  float s, z;
+  group_deq_params<BITS, G>(w, km, unit, mode, c, s, z);
   const int64_t base = b * o.sob + h * o.soh + t * o.sot + g * G;
 #pragma unroll
   for (int i = 0; i < G; ++i) {
@@ -318,7 +394,7 @@ __global__ __launch_bounds__(256) void dequant_k_kernel(const uint32_t* __restri
 template <int BITS, int G>
 __global__ __launch_bounds__(256) void dequant_v_kernel(const uint32_t* __restrict__ vc,
                                                         const uint16_t* __restrict__ vm, int64_t cap_groups,
-                                                        int B, int H, int g0, int ngT, int D, int sym, DeqOut o) {
+                                                        int B, int H, int g0, int ngT, int D, int mode, DeqOut o) {
   constexpr int W = G * BITS / 32;
   const int64_t gid = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   const int64_t total = int64_t(B) * H * ngT * D;
@@ -335,15 +411,8 @@ __global__ __launch_bounds__(256) void dequant_v_kernel(const uint32_t* __restri
 #pragma unroll
   for (int j = 0; j < W; ++j) w[j] = vc[unit * W + j];
   int32_t c[G];
-  unpack_fields<BITS, G>(w, sym != 0, c);
-  float s, z = 0.f;
-  if (sym) {
-    s = h2f(vm[unit]);
-  } else {
-    const uint32_t sz = reinterpret_cast<const uint32_t*>(vm)[unit];
-    s = h2f(uint16_t(sz & 0xffffu));
-    z = h2f(uint16_t(sz >> 16));
-  }
+  float s, z;
+  group_deq_params<BITS, G>(w, vm, unit, mode, c, s, z);
 #pragma unroll
   for (int i = 0; i < G; ++i) {
     const float v = __fadd_rn(__fmul_rn(float(c[i]), s), z);  // quant.py:90-91
@@ -496,7 +565,7 @@ int iq_k_store_bytes(int64_t B, int64_t H, int64_t t_cap, int64_t D, int group, 
   IQ_CHECK(D % group == 0, IQ_ERR_GROUP);
   IQ_CHECK(t_cap % TOKEN_BLOCK == 0, IQ_ERR_ALIGN);
   *codes_bytes = B * H * t_cap * D * bits / 8;
-  *meta_bytes = B * H * t_cap * (D / group) * (mode == IQ_MODE_SYM ? 2 : 4);
+  *meta_bytes = B * H * t_cap * (D / group) * meta_unit_bytes(mode);
   return IQ_OK;
 }
 
@@ -507,7 +576,7 @@ int iq_v_store_bytes(int64_t B, int64_t H, int64_t t_cap, int64_t D, int group, 
   IQ_CHECK(B >= 0 && H >= 0 && t_cap >= 0 && D > 0, IQ_ERR_SHAPE);
   IQ_CHECK(t_cap % group == 0, IQ_ERR_GROUP);
   *codes_bytes = B * H * t_cap * D * bits / 8;
-  *meta_bytes = B * H * (t_cap / group) * D * (mode == IQ_MODE_SYM ? 2 : 4);
+  *meta_bytes = B * H * (t_cap / group) * D * meta_unit_bytes(mode);
   return IQ_OK;
 }
 
@@ -528,6 +597,8 @@ int iq_quantize_k(const void* x, int64_t sx_b, int64_t sx_h, int64_t sx_t, const
   }
   IQ_CHECK(!(mode == IQ_MODE_SYM && zero16), IQ_ERR_MODE);
   IQ_CHECK(!(mode == IQ_MODE_ASYM && signs16), IQ_ERR_MODE);
+  const bool dense = codes_i32 || scale16 || zero16 || signs16;
+  IQ_CHECK(mode != IQ_MODE_HYBRID || (k_codes && !dense), IQ_ERR_MODE);
   const int64_t total = int64_t(B) * H * n * (D / group);
   if (total == 0) return IQ_OK;
   QuantOut o{k_codes, k_meta, t_cap / TOKEN_BLOCK, t_off, codes_i32, (uint16_t*)scale16, (uint16_t*)zero16,
@@ -535,8 +606,9 @@ int iq_quantize_k(const void* x, int64_t sx_b, int64_t sx_h, int64_t sx_t, const
   const int sym = mode == IQ_MODE_SYM;
   return dispatch_store_bits_group(bits, group, [&]<int BITS, int G>() {
     // the store-only append (no reference-format outputs) drops their registers
-    auto* kern = (codes_i32 || scale16 || zero16 || signs16) ? quant_k_kernel<BITS, G, true>
-                                                              : quant_k_kernel<BITS, G, false>;
+    auto* kern = mode == IQ_MODE_HYBRID ? quant_k_kernel<BITS, G, false, true>
+                 : dense               ? quant_k_kernel<BITS, G, true>
+                                       : quant_k_kernel<BITS, G, false>;
     kern<<<dim3(unsigned(ceil_div(total, 256))), 256, 0, (hipStream_t)stream>>>(
         (const uint16_t*)x, sx_b, sx_h, sx_t, (const uint16_t*)norm, B, H, n, D, sym, o);
     return launch_status();
@@ -559,14 +631,17 @@ int iq_quantize_v(const void* x, int64_t sx_b, int64_t sx_h, int64_t sx_t, int B
   }
   IQ_CHECK(!(mode == IQ_MODE_SYM && zero16), IQ_ERR_MODE);
   IQ_CHECK(!(mode == IQ_MODE_ASYM && signs16), IQ_ERR_MODE);
+  const bool dense = codes_i32 || scale16 || zero16 || signs16;
+  IQ_CHECK(mode != IQ_MODE_HYBRID || (v_codes && !dense), IQ_ERR_MODE);
   const int64_t total = int64_t(B) * H * (n / group) * D;
   if (total == 0) return IQ_OK;
   QuantOut o{v_codes, v_meta, t_cap / group, t_off, codes_i32, (uint16_t*)scale16, (uint16_t*)zero16,
              (uint16_t*)signs16};
   const int sym = mode == IQ_MODE_SYM;
   return dispatch_store_bits_group(bits, group, [&]<int BITS, int G>() {
-    auto* kern = (codes_i32 || scale16 || zero16 || signs16) ? quant_v_kernel<BITS, G, true>
-                                                              : quant_v_kernel<BITS, G, false>;
+    auto* kern = mode == IQ_MODE_HYBRID ? quant_v_kernel<BITS, G, false, true>
+                 : dense               ? quant_v_kernel<BITS, G, true>
+                                       : quant_v_kernel<BITS, G, false>;
     kern<<<dim3(unsigned(ceil_div(total, 256))), 256, 0, (hipStream_t)stream>>>(
         (const uint16_t*)x, sx_b, sx_h, sx_t, B, H, n, D, sym, o);
     return launch_status();
@@ -586,10 +661,9 @@ int iq_dequant_k(const uint32_t* k_codes, const uint16_t* k_meta, int64_t t_cap,
   const int64_t total = int64_t(B) * H * T * (D / group);
   if (total == 0) return IQ_OK;
   DeqOut o{(uint16_t*)out16, out32, so_b, so_h, so_t};
-  const int sym = mode == IQ_MODE_SYM;
   return dispatch_store_bits_group(bits, group, [&]<int BITS, int G>() {
     dequant_k_kernel<BITS, G><<<dim3(unsigned(ceil_div(total, 256))), 256, 0, (hipStream_t)stream>>>(
-        k_codes, k_meta, t_cap / TOKEN_BLOCK, (const uint16_t*)norm, B, H, t0, T, D, sym, o);
+        k_codes, k_meta, t_cap / TOKEN_BLOCK, (const uint16_t*)norm, B, H, t0, T, D, mode, o);
     return launch_status();
   });
 }
@@ -606,10 +680,9 @@ int iq_dequant_v(const uint32_t* v_codes, const uint16_t* v_meta, int64_t t_cap,
   const int64_t total = int64_t(B) * H * (T / group) * D;
   if (total == 0) return IQ_OK;
   DeqOut o{(uint16_t*)out16, out32, so_b, so_h, so_t};
-  const int sym = mode == IQ_MODE_SYM;
   return dispatch_store_bits_group(bits, group, [&]<int BITS, int G>() {
     dequant_v_kernel<BITS, G><<<dim3(unsigned(ceil_div(total, 256))), 256, 0, (hipStream_t)stream>>>(
-        v_codes, v_meta, t_cap / G, B, H, t0 / G, T / G, D, sym, o);
+        v_codes, v_meta, t_cap / G, B, H, t0 / G, T / G, D, mode, o);
     return launch_status();
   });
 }

@@ -12,9 +12,10 @@ from typing import Optional, Sequence
 import torch
 
 from . import _lib
-from ._lib import IQ_MODE_ASYM, IQ_MODE_SYM, TOKEN_BLOCK, call
+from ._lib import IQ_MODE_ASYM, IQ_MODE_HYBRID, IQ_MODE_SYM, TOKEN_BLOCK, call
 
-MODES = {"asymmetric": IQ_MODE_ASYM, "symmetric": IQ_MODE_SYM}
+MODES = {"asymmetric": IQ_MODE_ASYM, "symmetric": IQ_MODE_SYM, "hybrid": IQ_MODE_HYBRID}
+MODE_NAMES = {v: k for k, v in MODES.items()}
 
 
 def _p(t: Optional[torch.Tensor]):
@@ -37,7 +38,7 @@ def mode_id(mode) -> int:
         return mode
     m = getattr(mode, "value", mode)
     if m not in MODES:
-        raise ValueError(f"packed kernels support 'asymmetric' and 'symmetric', not {m!r}")
+        raise ValueError(f"packed kernels support 'asymmetric', 'symmetric' and 'hybrid', not {m!r}")
     return MODES[m]
 
 
@@ -214,8 +215,10 @@ class PackedStore:
     # 64-token block for axis 'channel', a G-token group for 'token'; the word
     # and half order inside a unit is the store layout), plus string metadata:
     # format "innerq-packed-store", version, axis, B, H, D, group, bits, mode
-    # ("asymmetric" | "symmetric"), length, unit.  Codes are LSB-first fields of
-    # little-endian u32 words; sym fields are offset binary.
+    # ("asymmetric" | "symmetric" | "hybrid"), length, unit.  Codes are
+    # LSB-first fields of little-endian u32 words; sym fields are offset
+    # binary; a hybrid unit's meta is {scale | flag << 15, zero} (flag set: the
+    # group holds sym fields).
     WIRE_FORMAT, WIRE_VERSION = "innerq-packed-store", "1"
 
     @staticmethod
@@ -249,7 +252,7 @@ class PackedStore:
             torch.empty(bh, 0, 0, dtype=torch.int16)
         md = {"format": self.WIRE_FORMAT, "version": self.WIRE_VERSION, "axis": self.axis, "B": self.B,
               "H": self.H, "D": self.D, "group": self.group, "bits": self.bits,
-              "mode": "symmetric" if self.mode == IQ_MODE_SYM else "asymmetric", "length": self.length, "unit": u}
+              "mode": MODE_NAMES[self.mode], "length": self.length, "unit": u}
         return self._safetensors({"codes": codes, "meta": meta}, {k: str(v) for k, v in md.items()})
 
     @classmethod
@@ -355,6 +358,9 @@ def quantize_dense(x: torch.Tensor, group: int, bits: int, mode, axis: str):
     """
     require_device(x, "tensor")
     m = mode_id(mode)
+    if m == IQ_MODE_HYBRID:
+        raise ValueError("quantize_dense takes 'asymmetric' or 'symmetric'; hybrid quantization is "
+                         "quant.quantize_hybrid (both halves) or a hybrid PackedStore")
     shape = tuple(x.shape)
     x = x.contiguous()
     dev = x.device
@@ -553,7 +559,8 @@ def decode_attention_combine(nsplit: int, B: int, Hq: int, T: int, D: int, devic
 
 # --- cache-side helpers --------------------------------------------------------
 def unpack_store(store: PackedStore, t0: int = 0, T: Optional[int] = None):
-    """Reference-format (codes int32, scale fp16, zero | signs fp16) of store tokens [t0, t0+T)."""
+    """Reference-format (codes int32, scale fp16, zero | signs fp16) of store tokens [t0, t0+T);
+    for a hybrid store the dicts of quant.py:146-149 (see split_hybrid)."""
     T = store.length - t0 if T is None else T
     check_range(store, "unpack", t0, T)
     B, H, D, G = store.B, store.H, store.D, store.group
@@ -561,10 +568,33 @@ def unpack_store(store: PackedStore, t0: int = 0, T: Optional[int] = None):
     codes = torch.empty(B, H, T, D, dtype=torch.int32, device=dev)
     red = (B, H, T, D // G) if store.axis == "channel" else (B, H, T // G, D)
     scale = torch.empty(red, dtype=torch.float16, device=dev)
-    zs = torch.empty(red if store.mode == IQ_MODE_ASYM else (B, H, T, D), dtype=torch.float16, device=dev)
+    zs = torch.empty(red if store.mode != IQ_MODE_SYM else (B, H, T, D), dtype=torch.float16, device=dev)
     fn = "iq_unpack_k" if store.axis == "channel" else "iq_unpack_v"
     call(fn, _p(store.codes), _p(store.meta), store.t_cap, B, H, t0, T, D, G, store.bits, store.mode, _p(codes),
          _p(scale), _p(zs), _stream(dev))
+    if store.mode == IQ_MODE_HYBRID:
+        return split_hybrid(codes, scale, zs, store.bits, store.group, store.axis)
+    return codes, scale, zs
+
+
+def split_hybrid(fields: torch.Tensor, scale_raw: torch.Tensor, zero: torch.Tensor, bits: int, group: int,
+                 axis: str):
+    """quant.py's hybrid dicts (quant.py:146-149) from the raw unpack of a hybrid store:
+    ``fields`` int32 [B,H,T,D] (the stored b-bit fields), ``scale_raw`` the meta's scale half
+    with the flag in bit 15, ``zero`` the meta's zero half.  mask = the flag bit (a bit test,
+    so a -0.0 scale counts as flagged).  The store keeps only the representation the mask
+    selects; the other half of each group reads as zeros (codes, scale, zero point, sign),
+    which dequantize_hybrid (quant.py:153-176) never selects."""
+    raw = scale_raw.view(torch.int16)
+    mask = torch.bitwise_and(raw, -0x8000) != 0
+    el = torch.repeat_interleave(mask, group, dim=-1 if axis == "channel" else 2)
+    signed = fields - (1 << (bits - 1))
+    zero_i, zero_h = torch.zeros((), dtype=torch.int32, device=fields.device), \
+        torch.zeros((), dtype=torch.float16, device=fields.device)
+    s_abs = torch.bitwise_and(raw, 0x7fff).view(torch.float16)
+    codes = {"zp": torch.where(el, zero_i, fields), "nozp": torch.where(el, signed.abs(), zero_i)}
+    scale = {"zp": torch.where(mask, zero_h, s_abs), "nozp": torch.where(mask, s_abs, zero_h), "mask": mask}
+    zs = {"zp": torch.where(mask, zero_h, zero), "nozp": torch.where(el, torch.sign(signed).to(torch.float16), zero_h)}
     return codes, scale, zs
 
 

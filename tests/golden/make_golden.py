@@ -11,7 +11,9 @@ Fixtures
 quant_golden.npz    quantize_{channeldim,tokendim}_{asym,sym} outputs for
                     bits 2/3/4, group 32/64 on a [1,2,64,128] fp16 input with
                     outlier channels, constant groups and rounding ties; the
-                    hybrid quantizer for bits 3/4; config-0 SHA-256 digests.
+                    hybrid quantizer for bits 2/3/4 (masks, digests of the
+                    dequantized values, also with -0.0 read as +0.0);
+                    config-0 SHA-256 digests.
 cache_golden.npz    InnerqDynamicLayer.update() traces: prefill + decode steps
                     for several presets (inputs regenerated from the stored
                     seed with innerq_amd.synth); full dense K/V of the last
@@ -164,11 +166,15 @@ def main(root, sliding_only=False):
         ds = getattr(quant, f"dequantize_{axis}dim_sym")
         hq = quant.quantize_hybrid(qa, qs, da, ds)
         hd = quant.dequantize_hybrid(da, ds)
-        for bits in (3, 4):
+        for bits in (2, 3, 4):
             c, s, z = hq(xt.clone(), 32, bits)
             key = f"{axis}_hybrid_b{bits}_g32"
             out[key + "_mask"] = s["mask"].cpu().numpy()
-            out[key + "_deq_sha256"] = digest(hd(c, s, z, 32).cpu().numpy().astype(np.float32))
+            deq = hd(c, s, z, 32).cpu().numpy().astype(np.float32)
+            out[key + "_deq_sha256"] = digest(deq)
+            # the same values with -0.0 read as +0.0 (x + 0.0): a packed sym
+            # field keeps no sign for a zero code
+            out[key + "_deq_pz_sha256"] = digest(deq + np.float32(0.0))
         c, s, z = qa(xt.clone(), 32, 4)
         out[f"{axis}_asym_b4_g32_deq_sha256"] = digest(da(c, s, z, 32).cpu().numpy().astype(np.float32))
         c, s, z = qs(xt.clone(), 32, 3)

@@ -53,7 +53,13 @@ def test_store_sizes():
     assert _store_bytes("iq_k_store_bytes", 1, 1, 64, 128, 32, 5, 0)[0] == -2    # bits
     assert _store_bytes("iq_k_store_bytes", 1, 1, 64, 96, 64, 4, 0)[0] == -3     # D % G
     assert _store_bytes("iq_v_store_bytes", 1, 1, 48, 128, 32, 4, 0)[0] == -3    # t_cap % G
-    assert _store_bytes("iq_v_store_bytes", 1, 1, 64, 128, 32, 4, 2)[0] == -7    # mode
+    assert _store_bytes("iq_v_store_bytes", 1, 1, 64, 128, 32, 4, 3)[0] == -7    # mode
+    # hybrid: b-bit fields, an asym-sized {scale | flag, zero} meta word per unit
+    st, cb, mb = _store_bytes("iq_v_store_bytes", 2, 4, 4096, 128, 32, 2, 2)
+    assert st == 0 and cb == 2 * 4 * 4096 * 32 and mb == 2 * 4 * 128 * 128 * 4
+    st, cb, mb = _store_bytes("iq_k_store_bytes", 2, 4, 4096, 128, 32, 3, 2)
+    assert st == 0 and cb == 2 * 4 * 4096 * 48 and mb == 2 * 4 * 4096 * 4 * 4
+    assert _store_bytes("iq_v_store_bytes", 1, 1, 64, 128, 32, 1, 2)[0] == -2    # hybrid needs bits >= 2
 
 
 def qk_args(**kw):
@@ -67,7 +73,7 @@ def qk_args(**kw):
 @pytest.mark.parametrize("kw,err", [
     (dict(q=None), -1), (dict(kc=None), -1), (dict(out=None), -1),
     (dict(bits=5), -2), (dict(bits=1), -2), (dict(G=48), -3), (dict(G=256), -3),
-    (dict(mode=3), -7), (dict(D=96), -4), (dict(Hkv=5), -4), (dict(Hq=48), -4),
+    (dict(mode=3), -7), (dict(mode=2), -7), (dict(D=96), -4), (dict(Hkv=5), -4), (dict(Hq=48), -4),
     (dict(T=-1), -4), (dict(t0=32), -5), (dict(t_cap=1000), -5), (dict(T=1100), -8),
     (dict(kc=ctypes.c_void_p(0x1004)), -5), (dict(ws=None), -6), (dict(wsb=64), -6),
     (dict(ws=ctypes.c_void_p(0x1008)), -5),
@@ -86,6 +92,7 @@ def av_args(**kw):
 @pytest.mark.parametrize("kw,err", [
     (dict(p=None), -1), (dict(vm=None), -1), (dict(out32=None), -1), (dict(out32=None, acc=1, out16=FAKE), -1),
     (dict(bits=0), -2), (dict(G=16), -3), (dict(T=500), -3), (dict(t0=16), -3), (dict(mode=-1), -7),
+    (dict(mode=3), -7), (dict(mode=2, bits=1), -2),
     (dict(D=256), -4), (dict(Hq=12), -4), (dict(T=2048), -8), (dict(vc=ctypes.c_void_p(0x1008)), -5),
     (dict(ws=None, wsb=0), -6), (dict(ws=FAKE, wsb=16), -6),
 ])
@@ -113,7 +120,9 @@ def quant_k_args(**kw):
 
 @pytest.mark.parametrize("kw,err", [
     (dict(x=None), -1), (dict(kc=None), -1), (dict(bits=8), -2), (dict(G=64, D=96), -3), (dict(G=33), -3),
-    (dict(mode=2), -7), (dict(n=-1), -4), (dict(t_off=62), -8), (dict(t_cap=100), -5),
+    (dict(mode=3), -7), (dict(n=-1), -4), (dict(t_off=62), -8), (dict(t_cap=100), -5),
+    (dict(mode=2, c32=FAKE), -7), (dict(mode=2, s16=FAKE), -7), (dict(mode=2, kc=None, km=None), -7),
+    (dict(mode=2, bits=1), -2),
     (dict(x=ctypes.c_void_p(0x1002)), -5), (dict(sxt=100), -5), (dict(mode=1, z16=FAKE), -7),
     (dict(mode=0, sg16=FAKE), -7),
 ])
@@ -130,7 +139,8 @@ def quant_v_args(**kw):
 
 @pytest.mark.parametrize("kw,err", [
     (dict(x=None), -1), (dict(vm=None), -1), (dict(bits=1, mode=1), -2), (dict(n=48), -3), (dict(t_off=32), -8),
-    (dict(t_off=16), -5), (dict(t_cap=48), -5), (dict(mode=7), -7),
+    (dict(t_off=16), -5), (dict(t_cap=48), -5), (dict(mode=7), -7), (dict(mode=2, sg16=FAKE), -7),
+    (dict(mode=2, vc=None, vm=None), -7),
 ])
 def test_quantize_v_rejects(kw, err):
     assert _lib.lib().iq_quantize_v(*quant_v_args(**kw)) == err
@@ -158,6 +168,10 @@ def test_decode_rejects():
     seg[1].codes, seg[1].meta, seg[1].t_cap, seg[1].bits, seg[1].group, seg[1].mode = 0x1000, 0x1000, 64, 7, 32, 0
     assert lib.iq_decode_attention(FAKE, 1, 1, None, seg, vseg, 1, 32, 8, 10, 128, 1.0, FAKE, 1, 1, FAKE, 1 << 30,
                                    None) == -2
+    # a hybrid store on the K side is refused (V side only)
+    seg[1].bits, seg[1].mode = 4, 2
+    assert lib.iq_decode_attention(FAKE, 1, 1, None, seg, vseg, 1, 32, 8, 10, 128, 1.0, FAKE, 1, 1, FAKE, 1 << 30,
+                                   None) == -7
 
 
 def test_dequant_rejects():

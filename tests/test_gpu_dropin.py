@@ -126,7 +126,7 @@ def test_cache_update_matches_reference_trace(cache_golden, name):
     assert layer.get_seq_length() == prefill + steps
 
 
-@pytest.mark.parametrize("name", [n for n in PRESETS if PRESETS[n].get("value_quantize_mode") != "hybrid"])
+@pytest.mark.parametrize("name", list(PRESETS))
 @pytest.mark.parametrize("nrep", [1, 4])
 def test_cache_attend_matches_dense_attention(cache_golden, name, nrep):
     """append() + attend() (fused, packed) within 1e-3 of float64 attention over the
@@ -216,7 +216,7 @@ def test_fused_attention_in_llama_matches_reference_path(preset, monkeypatch):
     """A random 2-layer Llama (8 query / 2 KV heads, head_dim 64) on the drop-in
     cache, teacher-forced through 40 decode steps after a 200-token prefill:
     logits with attn_implementation="innerq_fused" (attend() over the packed
-    cache; hybrid V falls back to the dequantized cache) against the
+    cache, hybrid V included) against the
     reference's path (update() dequantizes the cache, eager attention), same
     weights and tokens."""
     model = _tiny_llama(preset)
@@ -238,8 +238,8 @@ def test_fused_attention_in_llama_matches_reference_path(preset, monkeypatch):
         logits[attn] = torch.stack(steps)
     ref, got = logits["eager"], logits["innerq_fused"]
     assert ((got - ref).abs().max() / ref.abs().max()).item() < 2e-2
-    # every decode step of both layers went through attend(), except for hybrid V
-    assert calls[0] == (0 if preset == "hybrid_v" else 2 * dec.shape[1])
+    # every decode step of both layers went through attend()
+    assert calls[0] == 2 * dec.shape[1]
 
 
 def test_fused_attention_generate(monkeypatch):

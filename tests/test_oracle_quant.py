@@ -44,7 +44,7 @@ def test_dequantize_matches_reference_golden(quant_golden, axis):
 
 
 @pytest.mark.parametrize("axis", ["channel", "token"])
-@pytest.mark.parametrize("bits", [3, 4])
+@pytest.mark.parametrize("bits", [2, 3, 4])
 def test_hybrid_matches_reference_golden(quant_golden, axis, bits):
     x = quant_golden["x"].view(np.float16)
     qf = getattr(Q, f"quantize_{axis}dim_hybrid")
@@ -52,8 +52,10 @@ def test_hybrid_matches_reference_golden(quant_golden, axis, bits):
     c, s, z = qf(x, 32, bits)
     key = f"{axis}_hybrid_b{bits}_g32"
     np.testing.assert_array_equal(s["mask"], quant_golden[key + "_mask"])
-    d = df(c, s, z, 32)
-    np.testing.assert_array_equal(_sha(d.astype(np.float32)), quant_golden[key + "_deq_sha256"])
+    assert 0 < s["mask"].mean() < 1  # both representations occur in the fixture
+    d = df(c, s, z, 32).astype(np.float32)
+    np.testing.assert_array_equal(_sha(d), quant_golden[key + "_deq_sha256"])
+    np.testing.assert_array_equal(_sha(d + np.float32(0.0)), quant_golden[key + "_deq_pz_sha256"])
 
 
 def test_config0_digests(quant_golden):
