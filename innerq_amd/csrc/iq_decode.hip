@@ -40,50 +40,38 @@ struct Seg {
   const uint16_t* meta;
   int64_t t_cap;
   int t0, bits, group, mode;
+  int gsh;            // log2(group)
+  int64_t cap_groups;  // t_cap / group
 };
 
-__device__ __forceinline__ uint32_t field(const uint32_t* w, int bits, int i) {
-  const int bit = bits * i, wi = bit >> 5, o = bit & 31;
-  uint32_t f = w[wi] >> o;
-  if (o + bits > 32) f |= w[wi + 1] << (32 - o);
-  return f & ((1u << bits) - 1u);
-}
-
-__device__ __forceinline__ float deq(uint32_t f, int bits, int mode, const uint16_t* meta, int64_t unit) {
+// {scale, zero} of a packed unit from its meta (mw: the unit's dword, or
+// its fp16 scale for sym) with value = u * s + z for its b-bit field u (exact
+// in fp32: sym offset binary folds into z = -2^(b-1) s; a hybrid unit as its
+// flag says)
+__device__ __forceinline__ void unit_sz(uint32_t mw, int mode, int bits, float& s, float& z) {
   if (mode == IQ_MODE_SYM) {
-    const int c = int(f) - (1 << (bits - 1));  // offset binary
-    return __fmul_rn(float(c), h2f(meta[unit]));
+    s = h2f(uint16_t(mw));
+    z = -float(1 << (bits - 1)) * s;
+  } else if (mode == IQ_MODE_HYBRID) {
+    s = hyb_scale(mw);
+    z = hyb_sym(mw) ? -float(1 << (bits - 1)) * s : h2f(uint16_t(mw >> 16));
+  } else {
+    s = h2f(uint16_t(mw & 0xffffu));
+    z = h2f(uint16_t(mw >> 16));
   }
-  const uint32_t sz = reinterpret_cast<const uint32_t*>(meta)[unit];
-  if (mode == IQ_MODE_HYBRID) return hyb_value(f, bits, sz);
-  return __fadd_rn(__fmul_rn(float(f), h2f(uint16_t(sz & 0xffffu))), h2f(uint16_t(sz >> 16)));
 }
 
-// element (segment-local token tl, column d) of a packed K (channel-grouped)
-// or V (token-grouped) segment, dequantized as the reference does
-__device__ float packed_elem(const Seg& g, bool is_k, int64_t bh, int D, int tl, int d, const uint16_t* norm) {
-  const int st = g.t0 + tl;
-  const int W = g.group * g.bits / 32;
-  if (is_k) {
-    const int ng = D / g.group;
-    const int64_t unit = ((bh * (g.t_cap / TOKEN_BLOCK) + st / TOKEN_BLOCK) * ng + d / g.group) * TOKEN_BLOCK +
-                         st % TOKEN_BLOCK;
-    float v = deq(field(g.codes + unit * W, g.bits, d % g.group), g.bits, g.mode, g.meta, unit);
-    if (norm) v = __fmul_rn(v, h2f(norm[bh * D + d]));
-    return v;
-  }
-  const int64_t unit = (bh * (g.t_cap / g.group) + st / g.group) * D + d;
-  return deq(field(g.codes + unit * W, g.bits, st % g.group), g.bits, g.mode, g.meta, unit);
+__device__ __forceinline__ uint32_t unit_meta(const Seg& g, int64_t unit) {
+  return g.mode == IQ_MODE_SYM ? uint32_t(g.meta[unit]) : reinterpret_cast<const uint32_t*>(g.meta)[unit];
 }
 
 // fp16 elements [d0, d0 + N) of token t's row (a K or V segment list), as N/2
-// dwords; a token outside every segment gives zeros.  Dense rows load as
-// 16-byte vectors where aligned; packed rows (tokens packed in only one of K
-// and V) are dequantized element by element.  PK = false: the caller has no
-// packed segment (their code is left out: a short kernel fetches less code).
-template <int N, bool PK>
-__device__ __forceinline__ void gather_row(const Seg* s, bool is_k, int64_t b, int64_t kvh, int64_t Hkv, int D, int t,
-                                           int d0, const uint16_t* norm, uint32_t (&out)[N / 2]) {
+// dwords; a token outside every dense segment gives zeros.  Dense rows load
+// as 16-byte vectors where aligned.  Returns whether the token lies in the
+// list's packed segment (its row is decoded by packed_to_lds instead).
+template <int N>
+__device__ __forceinline__ bool gather_row(const Seg* s, int64_t b, int64_t kvh, int t, int d0,
+                                           uint32_t (&out)[N / 2]) {
 #pragma unroll
   for (int i = 0; i < N / 2; ++i) out[i] = 0u;
   // The lane's segment, chosen by value: every segment's fields are read with
@@ -91,8 +79,7 @@ __device__ __forceinline__ void gather_row(const Seg* s, bool is_k, int64_t b, i
   // lane selects its row pointer; a per-lane pointer to the segment would turn
   // every field into a dependent load through memory.
   const uint16_t* row = nullptr;
-  bool vec = false;
-  int pseg = -1, ptl = 0;  // packed segment of the lane and its local token
+  bool vec = false, packed = false;
 #pragma unroll
   for (int i = 0; i < 3; ++i) {
     const bool in = t >= s[i].start && t < s[i].start + s[i].n;
@@ -100,8 +87,7 @@ __device__ __forceinline__ void gather_row(const Seg* s, bool is_k, int64_t b, i
       row = s[i].dense + b * s[i].sb + kvh * s[i].sh + int64_t(t - s[i].start) * s[i].st + d0;
       vec = s[i].vec != 0;
     } else if (in) {
-      pseg = i;
-      ptl = t - s[i].start;
+      packed = true;
     }
   }
   if (row) {
@@ -115,17 +101,8 @@ __device__ __forceinline__ void gather_row(const Seg* s, bool is_k, int64_t b, i
 #pragma unroll
       for (int j = 0; j < N / 2; ++j) out[j] = uint32_t(row[2 * j]) | (uint32_t(row[2 * j + 1]) << 16);
     }
-  } else if constexpr (PK) {
-    if (pseg >= 0) {
-      const Seg& g = s[pseg];
-      const int64_t bh = b * Hkv + kvh;
-      for (int j = 0; j < N / 2; ++j) {
-        const float x0 = packed_elem(g, is_k, bh, D, ptl, d0 + 2 * j, norm);
-        const float x1 = packed_elem(g, is_k, bh, D, ptl, d0 + 2 * j + 1, norm);
-        out[j] = uint32_t(__half_as_ushort(__float2half_rn(x0))) | (uint32_t(__half_as_ushort(__float2half_rn(x1))) << 16);
-      }
-    }
   }
+  return packed;
 }
 
 struct DenseArgs {
@@ -139,6 +116,151 @@ struct DenseArgs {
   float* ml;  // the dense split slots' statistics: slot s at ml + s * rows * 2
   float* o;   // and partial outputs: slot s at o + s * rows * D
 };
+
+// ---- packed rows of a dense chunk (kernels with packed segments) ----
+// Tokens in the quantized segment of a list (the middle one: sinks and recent
+// windows are fp16) that fall in the dense range are dequantized into the
+// chunk's LDS tiles.  A chunk's rows form at most two runs of consecutive
+// tokens (one per dense range); per run, the packed units its tokens need -
+// at most two 64-token K blocks, at most three V groups - are copied into LDS
+// with 16-byte loads (one round trip, every load issued before the first LDS
+// write), then each element is decoded from LDS.  Per-element loads from
+// global memory paid one latency per few elements; unrolled per-element code
+// overflowed the instruction cache.
+template <int D>
+struct Stage {
+  static constexpr int KC = 2 * 64 * D * 4 / 32;  // K codes: two blocks at 4 bits (dwords)
+  static constexpr int VC = 32 * D;               // V codes: 3 x D x 4 (G 32), 2 x D x 8 (64), 2 x D x 16 (128)
+  static constexpr int KM = 2 * 64 * (D / 32);    // K meta: two blocks, D / 32 groups, a dword per unit
+  static constexpr int VM = 3 * D;                // V meta: three groups of D units
+  static constexpr int NM = D / 2;                // the key normalization factor
+  static constexpr int KC0 = 0, VC0 = KC, KM0 = VC0 + VC, VM0 = KM0 + KM, NM0 = VM0 + VM, N = NM0 + NM;
+};
+
+// meta halves per unit: 1 (sym: the scale), 2 ({scale, zero})
+__device__ __forceinline__ int meta_halves(const Seg& g) { return g.mode == IQ_MODE_SYM ? 1 : 2; }
+
+// field + meta of a staged unit -> value (u * s + z), as the reference computes it
+__device__ __forceinline__ float staged_value(const uint32_t* codes, const uint32_t* meta, const Seg& g, int u, int bit) {
+  const int W = (g.bits << g.gsh) >> 5;
+  const int wi = min(bit >> 5, W - 2);
+  const uint32_t* w = codes + u * W + wi;
+  const uint32_t f = uint32_t(((uint64_t(w[1]) << 32) | w[0]) >> (bit - 32 * wi)) & ((1u << g.bits) - 1u);
+  const uint32_t mw = g.mode == IQ_MODE_SYM ? uint32_t(reinterpret_cast<const uint16_t*>(meta)[u]) : meta[u];
+  float s, z;
+  unit_sz(mw, g.mode, g.bits, s, z);
+  return __fadd_rn(__fmul_rn(float(f), s), z);
+}
+
+// one run of the chunk: rows [r0, r1) hold tokens base + r.  Stages, decodes
+// and leaves the workgroup synchronized (the tiles' packed rows written).
+template <int D>
+__device__ __forceinline__ void packed_run(const Seg& K, const Seg& V, const uint16_t* norm, int64_t bh, int base,
+                                           int r0, int r1, uint32_t* stg, uint16_t* ktile, int kld,
+                                           uint16_t* vtile) {
+  using S = Stage<D>;
+  const int tid = threadIdx.x;
+  // the run's packed rows per list: [ka, kb) and [va, vb)
+  const int ka = max(r0, K.start - base), kb = K.dense ? ka : min(r1, K.start + K.n - base);
+  const int va = max(r0, V.start - base), vb = V.dense ? va : min(r1, V.start + V.n - base);
+  const bool kon = kb > ka, von = vb > va;
+  if (!kon && !von) return;  // uniform
+  // ---- stage: every load first ----
+  int kblk0 = 0, vg0 = 0, nk4 = 0, nv4 = 0, nkm = 0, nvm = 0;
+  const uint4 *kc = nullptr, *vc = nullptr;
+  const uint32_t *km = nullptr, *vm = nullptr;
+  if (kon) {
+    const int sa = K.t0 + (base + ka - K.start), sb = K.t0 + (base + kb - 1 - K.start);
+    kblk0 = sa >> 6;
+    const int nb = (sb >> 6) - kblk0 + 1;
+    const int upb = (D >> K.gsh) * TOKEN_BLOCK;  // units per block
+    const int W = (K.bits << K.gsh) >> 5;
+    const int64_t u0 = (bh * (K.t_cap >> 6) + kblk0) * upb;
+    kc = reinterpret_cast<const uint4*>(K.codes + u0 * W);
+    nk4 = nb * upb * W / 4;
+    km = reinterpret_cast<const uint32_t*>(K.meta + u0 * meta_halves(K));
+    nkm = nb * upb * meta_halves(K) / 2;
+  }
+  if (von) {
+    const int sa = V.t0 + (base + va - V.start), sb = V.t0 + (base + vb - 1 - V.start);
+    vg0 = sa >> V.gsh;
+    const int ng = (sb >> V.gsh) - vg0 + 1;
+    const int W = (V.bits << V.gsh) >> 5;
+    const int64_t u0 = (bh * V.cap_groups + vg0) * D;
+    vc = reinterpret_cast<const uint4*>(V.codes + u0 * W);
+    nv4 = ng * D * W / 4;
+    vm = reinterpret_cast<const uint32_t*>(V.meta + u0 * meta_halves(V));
+    nvm = ng * D * meta_halves(V) / 2;
+  }
+  constexpr int LK = S::KC / 4 / 256, LV = S::VC / 4 / 256, LKM = (S::KM + 255) / 256, LVM = (S::VM + 255) / 256;
+  // loads at clamped indices (straight-line code), then stores at the same
+  // indices: a repeated index stores the value it already holds.  Plain dword
+  // registers (an array of uint4 was kept in scratch).
+  uint32_t rk[4 * LK], rv[4 * LV], rkm[LKM], rvm[LVM], rn = 0;
+  if (kon) {
+#pragma unroll
+    for (int j = 0; j < LK; ++j) {
+      const uint4 x = kc[min(tid + 256 * j, nk4 - 1)];
+      rk[4 * j] = x.x; rk[4 * j + 1] = x.y; rk[4 * j + 2] = x.z; rk[4 * j + 3] = x.w;
+    }
+#pragma unroll
+    for (int j = 0; j < LKM; ++j) rkm[j] = km[min(tid + 256 * j, nkm - 1)];
+  }
+  if (von) {
+#pragma unroll
+    for (int j = 0; j < LV; ++j) {
+      const uint4 x = vc[min(tid + 256 * j, nv4 - 1)];
+      rv[4 * j] = x.x; rv[4 * j + 1] = x.y; rv[4 * j + 2] = x.z; rv[4 * j + 3] = x.w;
+    }
+#pragma unroll
+    for (int j = 0; j < LVM; ++j) rvm[j] = vm[min(tid + 256 * j, nvm - 1)];
+  }
+  const bool stn = kon && norm && tid < D / 2;
+  if (stn) rn = reinterpret_cast<const uint32_t*>(norm + bh * D)[tid];
+  if (kon) {
+#pragma unroll
+    for (int j = 0; j < LK; ++j)
+      reinterpret_cast<uint4*>(stg + S::KC0)[min(tid + 256 * j, nk4 - 1)] =
+          make_uint4(rk[4 * j], rk[4 * j + 1], rk[4 * j + 2], rk[4 * j + 3]);
+#pragma unroll
+    for (int j = 0; j < LKM; ++j) stg[S::KM0 + min(tid + 256 * j, nkm - 1)] = rkm[j];
+  }
+  if (von) {
+#pragma unroll
+    for (int j = 0; j < LV; ++j)
+      reinterpret_cast<uint4*>(stg + S::VC0)[min(tid + 256 * j, nv4 - 1)] =
+          make_uint4(rv[4 * j], rv[4 * j + 1], rv[4 * j + 2], rv[4 * j + 3]);
+#pragma unroll
+    for (int j = 0; j < LVM; ++j) stg[S::VM0 + min(tid + 256 * j, nvm - 1)] = rvm[j];
+  }
+  if (stn) stg[S::NM0 + tid] = rn;
+  __syncthreads();
+  // ---- decode: element e of the rows, row-major, columns across lanes ----
+  if (kon) {
+    const int cnt = (kb - ka) * D;
+#pragma unroll 4
+    for (int e = tid; e < cnt; e += 256) {
+      const int r = ka + e / D, d = e % D;
+      const int st = K.t0 + (base + r - K.start);
+      const int u = (((st >> 6) - kblk0) * (D >> K.gsh) + (d >> K.gsh)) * TOKEN_BLOCK + (st & 63);
+      float v = staged_value(stg + S::KC0, stg + S::KM0, K, u, (d & (K.group - 1)) * K.bits);
+      if (norm) v = __fmul_rn(v, h2f(reinterpret_cast<const uint16_t*>(stg + S::NM0)[d]));
+      ktile[r * kld + d] = __half_as_ushort(__float2half_rn(v));
+    }
+  }
+  if (von) {
+    const int cnt = (vb - va) * D;
+#pragma unroll 4
+    for (int e = tid; e < cnt; e += 256) {
+      const int r = va + e / D, d = e % D;
+      const int st = V.t0 + (base + r - V.start);
+      const int u = ((st >> V.gsh) - vg0) * D + d;
+      const float v = staged_value(stg + S::VC0, stg + S::VM0, V, u, (st & (V.group - 1)) * V.bits);
+      vtile[r * D + d] = __half_as_ushort(__float2half_rn(v));
+    }
+  }
+  __syncthreads();  // the staging area is reused by the next run
+}
 
 // Online softmax over the dense tokens (fp16 sinks and recent windows, and
 // tokens packed in only one of K and V).  Workgroup (s, b * Hkv + kvh) takes
@@ -161,6 +283,7 @@ __global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs a) {
   __shared__ float qs[NREP][D];
   __shared__ float ps[NREP][DT];
   __shared__ float al[NREP];
+  __shared__ __align__(16) uint32_t stg[PK ? Stage<D>::N : 4];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int bh = blockIdx.y, b = bh / a.Hkv, kvh = bh % a.Hkv;
@@ -171,11 +294,12 @@ __global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs a) {
   // gathering: thread = (row tid / 4, quarter tid % 4 of the row)
   const int gr = tid >> 2, gq = tid & 3;
   uint32_t kr[RE / 2], vr[RE / 2];
+  bool kpk = false, vpk = false;  // the thread's row is in the packed K / V segment
   auto gather = [&](int c0) {
     const int i = c0 + gr;
     const int t = i < i1 ? (i < n0 ? a.lo0 + i : a.lo1 + (i - n0)) : -1;
-    gather_row<RE, PK>(a.k, true, b, kvh, a.Hkv, D, t, gq * RE, a.norm, kr);
-    gather_row<RE, PK>(a.v, false, b, kvh, a.Hkv, D, t, gq * RE, nullptr, vr);
+    kpk = gather_row<RE>(a.k, b, kvh, t, gq * RE, kr);
+    vpk = gather_row<RE>(a.v, b, kvh, t, gq * RE, vr);
   };
   // the first chunk's rows and the query are loaded together (one round trip)
   if (i0 < i1) gather(i0);
@@ -189,10 +313,23 @@ __global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs a) {
   for (int it = 0; it < OPT; ++it) o[it][0] = o[it][1] = 0.f;
 
   for (int c0 = i0; c0 < i1; c0 += DT) {
+    // the fp16 rows from registers; packed rows are decoded into the tiles
+    // (disjoint rows: no ordering needed between the two)
+    if (!kpk) {
 #pragma unroll
-    for (int j = 0; j < RE / 2; ++j) {
-      kt[gr][gq * (RE / 2) + j] = kr[j];
-      vt[gr][gq * (RE / 2) + j] = vr[j];
+      for (int j = 0; j < RE / 2; ++j) kt[gr][gq * (RE / 2) + j] = kr[j];
+    }
+    if (!vpk) {
+#pragma unroll
+      for (int j = 0; j < RE / 2; ++j) vt[gr][gq * (RE / 2) + j] = vr[j];
+    }
+    if constexpr (PK) {  // runs: dense range 0 (rows < n0 - c0), then range 1
+      const int64_t bh64 = int64_t(b) * a.Hkv + kvh;
+      const int rend = min(DT, i1 - c0), rs = min(max(n0 - c0, 0), rend);
+      uint16_t* kth = reinterpret_cast<uint16_t*>(&kt[0][0]);
+      uint16_t* vth = reinterpret_cast<uint16_t*>(&vt[0][0]);
+      packed_run<D>(a.k[1], a.v[1], a.norm, bh64, a.lo0 + c0, 0, rs, stg, kth, 2 * KS, vth);
+      packed_run<D>(a.k[1], a.v[1], a.norm, bh64, a.lo1 + c0 - n0, rs, rend, stg, kth, 2 * KS, vth);
     }
     __syncthreads();
     if (c0 + DT < i1) gather(c0 + DT);  // in flight through this chunk
@@ -397,6 +534,8 @@ Seg to_seg(const iq_segment& s, int start) {
   g.n = s.n; g.start = start;
   g.codes = s.codes; g.meta = s.meta; g.t_cap = s.t_cap; g.t0 = s.t0;
   g.bits = s.bits; g.group = s.group; g.mode = s.mode;
+  g.gsh = s.group > 0 ? __builtin_ctz(unsigned(s.group)) : 0;
+  g.cap_groups = s.group > 0 ? s.t_cap / s.group : 0;
   if (s.n && s.codes) g.dense = nullptr;
   g.vec = g.dense && aligned(g.dense, 16) && s.s_b % 8 == 0 && s.s_h % 8 == 0 && s.s_t % 8 == 0;
   return g;
