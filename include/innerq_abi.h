@@ -231,6 +231,36 @@ typedef struct iq_segment {
   int bits, group, mode;
 } iq_segment;
 
+/* One role (K or V) of a layer's decode-step append: the fp16 recent window
+ * lives in a caller-owned buffer, and the oldest tokens flush into the
+ * layer's packed store. */
+typedef struct iq_window {
+  void* buf;                  /* fp16 window buffer [B,H,cap,D] (strides s_b, s_h, s_t; D contiguous) */
+  int64_t s_b, s_h, s_t;
+  int cap;                    /* buffer capacity in tokens */
+  int start, n;               /* the window before the call: buffer tokens [start, start + n) */
+  const void* x;              /* m new tokens [B,H,m,D] (strides sx_*; D contiguous) */
+  int64_t sx_b, sx_h, sx_t;
+  int m;                      /* written at buffer tokens start + n .. start + n + m - 1 */
+  int flush;                  /* quantize the first `flush` tokens of [window | new] into the store */
+  uint32_t* codes;            /* the store, written from token t_off (as iq_quantize_k / _v) */
+  uint16_t* meta;
+  int64_t t_cap, t_off;
+  int bits, group, mode;
+  int axis;                   /* 0: groups along head_dim (K store layout), 1: along tokens (V layout) */
+  const void* norm;           /* axis 0: fp16 [B,H,D] key normalization factor (x / norm in fp16 first), or NULL */
+} iq_window;
+
+/* One decode step of a layer's recent windows, both roles in one launch:
+ * each role's m new tokens are written into its buffer after the window, and
+ * the first `flush` tokens of [window | new] are quantized into its store,
+ * bit-exact to iq_quantize_k / iq_quantize_v (asym, sym or hybrid).  The
+ * caller then advances the window by `flush` tokens (start += flush, n += m -
+ * flush) and the store length by `flush`.  Replaces the torch.cat / slice of
+ * update_keys_recent / update_values_recent plus quantize_new_keys /
+ * quantize_new_values (cache.py:283-365).  k or v may be NULL (role absent). */
+int iq_window_append(const iq_window* k, const iq_window* v, int B, int H, int D, void* stream);
+
 /* Workspace of the decode entry points (no initialization needed). */
 size_t iq_decode_workspace_bytes(int B, int Hq, int T, int D);
 

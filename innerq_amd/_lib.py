@@ -50,6 +50,21 @@ L = ctypes.c_int64
 F = ctypes.c_float
 S = ctypes.c_size_t
 
+class iq_window(ctypes.Structure):
+    _fields_ = [
+        ("buf", ctypes.c_void_p),
+        ("s_b", ctypes.c_int64), ("s_h", ctypes.c_int64), ("s_t", ctypes.c_int64),
+        ("cap", ctypes.c_int), ("start", ctypes.c_int), ("n", ctypes.c_int),
+        ("x", ctypes.c_void_p),
+        ("sx_b", ctypes.c_int64), ("sx_h", ctypes.c_int64), ("sx_t", ctypes.c_int64),
+        ("m", ctypes.c_int), ("flush", ctypes.c_int),
+        ("codes", ctypes.c_void_p), ("meta", ctypes.c_void_p),
+        ("t_cap", ctypes.c_int64), ("t_off", ctypes.c_int64),
+        ("bits", ctypes.c_int), ("group", ctypes.c_int), ("mode", ctypes.c_int), ("axis", ctypes.c_int),
+        ("norm", ctypes.c_void_p),
+    ]
+
+
 SIGNATURES = {
     "iq_abi_version": (I, []),
     "iq_strerror": (ctypes.c_char_p, [I]),
@@ -70,6 +85,7 @@ SIGNATURES = {
     "iq_av_workspace_bytes": (S, [I, I, I, I, I]),
     "iq_av_gemv": (I, [P, L, L, P, P, L, I, I, I, I, I, I, I, I, I, P, P, L, L, I, P, S, P]),
     "iq_decode_workspace_bytes": (S, [I, I, I, I]),
+    "iq_window_append": (I, [ctypes.POINTER(iq_window), ctypes.POINTER(iq_window), I, I, I, P]),
     "iq_decode_attention": (I, [P, L, L, P, ctypes.POINTER(iq_segment), ctypes.POINTER(iq_segment),
                                 I, I, I, I, I, F, P, L, L, P, S, P]),
     "iq_decode_attention_splits": (I, [P, L, L, P, ctypes.POINTER(iq_segment), ctypes.POINTER(iq_segment),

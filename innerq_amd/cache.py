@@ -101,6 +101,26 @@ class InnerqDynamicLayer(CacheLayerMixin):
         self.value_quantize_mode = QMode.from_str(getattr(config, 'value_quantize_mode', 'symmetric'))
         self._kq: Optional[_Quantized] = None
         self._vq: Optional[_Quantized] = None
+        self._kwin: Optional[ops.RecentWindow] = None
+        self._vwin: Optional[ops.RecentWindow] = None
+
+    # ---- recent windows (cache.py keys_recent / values_recent): views of
+    # RecentWindow buffers that a decode step appends to in place ----
+    @property
+    def keys_recent(self):
+        return None if self._kwin is None else self._kwin.tensor
+
+    @keys_recent.setter
+    def keys_recent(self, x):
+        self._kwin = None if x is None else ops.RecentWindow(x)
+
+    @property
+    def values_recent(self):
+        return None if self._vwin is None else self._vwin.tensor
+
+    @values_recent.setter
+    def values_recent(self, x):
+        self._vwin = None if x is None else ops.RecentWindow(x)
 
     # ---- reference state attributes (read-only views of the packed stores) ----
     def _ref(self, q: Optional[_Quantized], i: int):
@@ -186,23 +206,28 @@ class InnerqDynamicLayer(CacheLayerMixin):
         self.values_recent = value_states[:, :, nq:, :].contiguous()
         return value_states[:, :, :nq, :].contiguous()
 
+    def _kq_for(self, like: torch.Tensor) -> _Quantized:
+        if self._kq is None:
+            axis = "token" if self.key_quantize_over_token else "channel"
+            self._kq = _Quantized(axis, like, self.key_group_size, self.key_bits, self.key_quantize_mode)
+        return self._kq
+
+    def _vq_for(self, like: torch.Tensor) -> _Quantized:
+        if self._vq is None:
+            axis = "token" if self.value_quantize_over_token else "channel"
+            self._vq = _Quantized(axis, like, self.value_group_size, self.value_bits, self.value_quantize_mode)
+        return self._vq
+
     def _quantize_keys(self, key_states: torch.Tensor) -> None:
         if key_states.numel() == 0:
             return
         norm = self.normalize_keys(key_states)
-        if self._kq is None:
-            axis = "token" if self.key_quantize_over_token else "channel"
-            self._kq = _Quantized(axis, key_states, self.key_group_size, self.key_bits, self.key_quantize_mode)
-        self._kq.append(key_states, norm)
+        self._kq_for(key_states).append(key_states, norm)
 
     def _quantize_values(self, value_states: torch.Tensor) -> None:
         if value_states.numel() == 0:
             return
-        if self._vq is None:
-            axis = "token" if self.value_quantize_over_token else "channel"
-            self._vq = _Quantized(axis, value_states, self.value_group_size, self.value_bits,
-                                  self.value_quantize_mode)
-        self._vq.append(value_states, None)
+        self._vq_for(value_states).append(value_states, None)
 
     def initialize_keys_q(self, key_states: torch.Tensor) -> None:
         if self.key_quantize:
@@ -225,28 +250,41 @@ class InnerqDynamicLayer(CacheLayerMixin):
         self.is_initialized = True
 
     # ---- decode (cache.py:283-396) ----
+    def _flush_sizes(self, m: int) -> tuple[int, int]:
+        """Tokens flushed from [window | m new tokens] into the stores (cache.py:283-306)."""
+        kf = self.key_flush_size if self.key_quantize and self._kwin.n + m >= self.key_flush_size else 0
+        vf = self.value_flush_size if self.value_quantize and self._vwin.n + m >= self.value_flush_size else 0
+        return kf, vf
+
     def update_keys_recent(self, key_states: torch.Tensor) -> torch.Tensor:
-        self.keys_recent = torch.cat([self.keys_recent, key_states], dim=-2)
-        n = self.key_flush_size if self.key_quantize and self.keys_recent.shape[-2] >= self.key_flush_size else 0
-        key_states = self.keys_recent[:, :, :n]
-        self.keys_recent = self.keys_recent[:, :, n:]
-        return key_states
+        """cache.py:283-294: append to the window, return (and drop) the tokens to flush."""
+        kf = self._flush_sizes(key_states.shape[-2])[0]
+        full = torch.cat([self.keys_recent, key_states], dim=-2)
+        self.keys_recent = full[:, :, kf:]
+        return full[:, :, :kf]
 
     def update_values_recent(self, value_states: torch.Tensor) -> torch.Tensor:
-        self.values_recent = torch.cat([self.values_recent, value_states], dim=-2)
-        n = (self.value_flush_size
-             if self.value_quantize and self.values_recent.shape[-2] >= self.value_flush_size else 0)
-        value_states = self.values_recent[:, :, :n]
-        self.values_recent = self.values_recent[:, :, n:]
-        return value_states
+        """cache.py:296-307: append to the window, return (and drop) the tokens to flush."""
+        vf = self._flush_sizes(value_states.shape[-2])[1]
+        full = torch.cat([self.values_recent, value_states], dim=-2)
+        self.values_recent = full[:, :, vf:]
+        return full[:, :, :vf]
 
     def add_to_cache(self, key_states: torch.Tensor, value_states: torch.Tensor) -> None:
-        key_states = self.update_keys_recent(key_states)
-        value_states = self.update_values_recent(value_states)
-        if key_states.numel() != 0:
-            self._quantize_keys(key_states)
-        if value_states.numel() != 0:
-            self._quantize_values(value_states)
+        """cache.py:309-365 in one launch (ops.window_append): the new tokens join the
+        recent windows, the oldest flush into the packed stores."""
+        kf, vf = self._flush_sizes(key_states.shape[-2])
+        norm = None
+        if kf:
+            kq = self._kq_for(key_states)
+            if self.key_normalize:
+                if self.key_normalization_factor is None:  # the first flushed keys set it (cache.py:121-126)
+                    self.normalize_keys(torch.cat([self.keys_recent, key_states], dim=-2)[:, :, :kf])
+                norm = self.key_normalization_factor
+        if vf:
+            self._vq_for(value_states)
+        ops.window_append(self._kwin, key_states, kf, self._kq.store if kf else None, norm,
+                          self._vwin, value_states, vf, self._vq.store if vf else None)
 
     def _dense(self, sink, q: Optional[_Quantized], recent, norm, dtype) -> torch.Tensor:
         """[sink | dequantized (times norm) | recent] in dtype: one rounding of the

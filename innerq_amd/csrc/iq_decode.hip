@@ -647,8 +647,9 @@ int launch_splits(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, c
   const bool fused =
       c && k[1].group == v[1].group && detail::flash_fused_supported(q, sq_b, sq_h, norm, fk, fv, Hq, Hkv, D);
 
-  // dense tokens -> split slots nsf, nsf + 1, ...: enough workgroups to
-  // spread over the CUs, at least DSLICE tokens each
+  // dense tokens -> split slots nsf, nsf + 1, ...: up to two workgroups per
+  // CU (a workgroup's chunks run one after another, each a chain of memory
+  // round trips), at least DSLICE tokens each
   DenseArgs da{};
   da.q = (const uint16_t*)q; da.sqb = sq_b; da.sqh = sq_h; da.norm = (const uint16_t*)norm;
   int start = 0;
@@ -664,7 +665,7 @@ int launch_splits(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, c
   int nsd = 0;
   if (n_dense > 0) {
     const int64_t bhs = int64_t(B) * Hkv;
-    nsd = int(std::min<int64_t>({NSD_MAX, ceil_div(n_dense, DSLICE), std::max<int64_t>(1, ceil_div(detail::num_cus(), bhs))}));
+    nsd = int(std::min<int64_t>({NSD_MAX, ceil_div(n_dense, DSLICE), std::max<int64_t>(1, ceil_div(2 * detail::num_cus(), bhs))}));
     const dim3 grid{unsigned(nsd), unsigned(bhs), 1u};
     // any packed segment (tokens packed in only one of K and V) needs the
     // general gather; a dense-only step takes the short kernel

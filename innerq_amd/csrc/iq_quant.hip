@@ -44,8 +44,32 @@ __device__ __forceinline__ int32_t code_of(float y, float L) {
 }
 
 // Group statistics and per-element codes of the two quantizers, one fp16
-// rounding per reference op.
-// asym (quant.py:66-71): scale and zero (the group minimum) of b-bit codes
+// rounding per reference op (runtime bit width; the templates below pass a
+// constant).
+// asym (quant.py:66-71): scale of b-bit codes from the group's min and max
+__device__ __forceinline__ float asym_scale_b(float mn, float mx, int bits) {
+  return round_f16(round_f16(mx - mn) / float((1 << bits) - 1));    // quant.py:68
+}
+__device__ __forceinline__ int32_t asym_code_b(float x, float mn, float s, int bits) {
+  return code_of(round_f16(round_f16(x - mn) / s), float((1 << bits) - 1));  // quant.py:69-71
+}
+// sym (quant.py:104-109): scale of b-bit codes (one bit is the sign)
+__device__ __forceinline__ float sym_scale_b(float mx, int bits) {
+  return round_f16(mx / float((1 << (bits - 1)) - 1));              // quant.py:107
+}
+__device__ __forceinline__ int32_t sym_code_b(float x, float s, int bits) {
+  return code_of(round_f16(fabsf(x) / s), float((1 << (bits - 1)) - 1));  // quant.py:108-109
+}
+__device__ __forceinline__ float sign_of(float x) { return x > 0.f ? 1.f : (x < 0.f ? -1.f : 0.f); }  // torch.sign
+// stored fields: the asym code (0 for NaN); sym sign*magnitude + 2^(b-1)
+__device__ __forceinline__ uint32_t asym_field_b(int32_t c, int bits) {
+  return (c == I32_MIN) ? 0u : (uint32_t(c) & ((1u << bits) - 1u));
+}
+__device__ __forceinline__ uint32_t sym_field_b(int32_t c, float sg, int bits) {
+  const int32_t sc = (c == I32_MIN) ? 0 : (sg > 0.f ? c : (sg < 0.f ? -c : 0));
+  return uint32_t(sc + (1 << (bits - 1))) & ((1u << bits) - 1u);  // offset binary
+}
+
 template <int BITS, int G>
 __device__ __forceinline__ void asym_params(const float* v, float& s, float& mn) {
   float mx = v[0];
@@ -58,13 +82,10 @@ __device__ __forceinline__ void asym_params(const float* v, float& s, float& mn)
     mx = fmaxf(mx, v[i]);
   }
   if (nan) { mn = __builtin_nanf(""); mx = mn; }
-  s = round_f16(round_f16(mx - mn) / float((1 << BITS) - 1));      // quant.py:68
+  s = asym_scale_b(mn, mx, BITS);
 }
 template <int BITS>
-__device__ __forceinline__ int32_t asym_code(float x, float mn, float s) {
-  return code_of(round_f16(round_f16(x - mn) / s), float((1 << BITS) - 1));  // quant.py:69-71
-}
-// sym (quant.py:104-109): scale of b-bit codes (one bit is the sign)
+__device__ __forceinline__ int32_t asym_code(float x, float mn, float s) { return asym_code_b(x, mn, s, BITS); }
 template <int BITS, int G>
 __device__ __forceinline__ float sym_scale(const float* v) {
   float mx = 0.f;
@@ -75,23 +96,14 @@ __device__ __forceinline__ float sym_scale(const float* v) {
     mx = fmaxf(mx, fabsf(v[i]));
   }
   if (nan) mx = __builtin_nanf("");
-  return round_f16(mx / float((1 << (BITS - 1)) - 1));              // quant.py:107
+  return sym_scale_b(mx, BITS);
 }
 template <int BITS>
-__device__ __forceinline__ int32_t sym_code(float x, float s) {
-  return code_of(round_f16(fabsf(x) / s), float((1 << (BITS - 1)) - 1));  // quant.py:108-109
-}
-__device__ __forceinline__ float sign_of(float x) { return x > 0.f ? 1.f : (x < 0.f ? -1.f : 0.f); }  // torch.sign
-// stored fields: the asym code (0 for NaN); sym sign*magnitude + 2^(b-1)
+__device__ __forceinline__ int32_t sym_code(float x, float s) { return sym_code_b(x, s, BITS); }
 template <int BITS>
-__device__ __forceinline__ uint32_t asym_field(int32_t c) {
-  return (c == I32_MIN) ? 0u : (uint32_t(c) & ((1u << BITS) - 1u));
-}
+__device__ __forceinline__ uint32_t asym_field(int32_t c) { return asym_field_b(c, BITS); }
 template <int BITS>
-__device__ __forceinline__ uint32_t sym_field(int32_t c, float sg) {
-  const int32_t sc = (c == I32_MIN) ? 0 : (sg > 0.f ? c : (sg < 0.f ? -c : 0));
-  return uint32_t(sc + (1 << (BITS - 1))) & ((1u << BITS) - 1u);  // offset binary
-}
+__device__ __forceinline__ uint32_t sym_field(int32_t c, float sg) { return sym_field_b(c, sg, BITS); }
 
 // Quantize G values held as fp32 copies of fp16 numbers.  fields[] receives
 // the b-bit stored field, codes[] the dense reference code, sgn[] the sign.
@@ -532,6 +544,172 @@ __global__ __launch_bounds__(256) void unpack_v_kernel(const uint32_t* __restric
   }
 }
 
+// ---- one decode step of a layer's recent windows (cache.py:283-365) ----
+// Per role (K, V): the m new tokens are written after the window in its
+// buffer, and the first F tokens of [window | new tokens] are quantized into
+// the store, in one launch for both roles.  The quantizer here takes the bit
+// width, group size and mode at run time and reads each group from memory
+// once per pass (no per-group register arrays); every element goes through
+// the same fp16 ops as quantize_group / quantize_group_hybrid.
+struct WinRole {
+  uint16_t* buf;
+  int64_t sb, sh, st;
+  int start, n;  // the window before the step: buffer tokens [start, start + n)
+  const uint16_t* x;
+  int64_t sxb, sxh, sxt;
+  int m;  // new tokens, written at buffer token start + n + j
+  int F;  // tokens flushed into the store: the first F of [window | new]
+  uint32_t* codes;
+  uint16_t* meta;
+  int64_t cap_units, t_off;
+  int bits, group, gsh, mode, axis;  // axis 0: groups along head_dim (K layout), 1: along tokens (V layout)
+  const uint16_t* norm;              // axis 0: fp16 [B,H,D] key normalization factor, or null
+  int vec_buf, vec_x;                // rows of the buffer / of x are 16-byte aligned (base and strides)
+};
+
+struct AppendArgs {
+  WinRole r[2];
+  int H, D;
+  // work items: copies of role 0, copies of role 1, groups of role 0, groups
+  // of role 1; segment k covers [start[k], start[k] + count[k]), starts
+  // aligned to the block size
+  int64_t start[4], count[4];
+};
+
+// One group, quantized as quantize_group / quantize_group_hybrid do, with
+// the bit width and mode known at run time: v[] holds the group's G inputs
+// (registers; loaded together, one memory latency per group), the fields are
+// stored word by word as they fill, the meta word last.
+template <int G>
+__device__ __forceinline__ void quant_group_rt(const float* v, int bits, int mode, uint32_t* out, uint16_t* meta,
+                                               int64_t unit) {
+  const int abits = mode == IQ_MODE_HYBRID ? bits - 1 : bits;
+  float mn = v[0], mx = v[0], amx = 0.f;
+  bool nan = false;
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    nan |= is_nan(v[i]);
+    mn = fminf(mn, v[i]);
+    mx = fmaxf(mx, v[i]);
+    amx = fmaxf(amx, fabsf(v[i]));
+  }
+  if (nan) { mn = __builtin_nanf(""); mx = mn; amx = mn; }
+  const float sa = asym_scale_b(mn, mx, abits), ss = sym_scale_b(amx, bits);
+  bool sym = mode == IQ_MODE_SYM;
+  if (mode == IQ_MODE_HYBRID) {  // quantize_group_hybrid's choice
+    double ea = 0.0, es = 0.0;
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+      const float da = __fadd_rn(__fmul_rn(float(asym_code_b(v[i], mn, sa, abits)), sa), mn);
+      const float ds = __fmul_rn(__fmul_rn(float(sym_code_b(v[i], ss, bits)), ss), sign_of(v[i]));
+      ea += double(fabsf(__fsub_rn(da, v[i])));
+      es += double(fabsf(__fsub_rn(ds, v[i])));
+    }
+    sym = ea > es;
+  }
+  uint64_t acc = 0;
+  int pos = 0, wj = 0;
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    const uint32_t fld = sym ? sym_field_b(sym_code_b(v[i], ss, bits), sign_of(v[i]), bits)
+                             : asym_field_b(asym_code_b(v[i], mn, sa, abits), bits);
+    acc |= uint64_t(fld) << pos;
+    pos += bits;
+    if (pos >= 32) {
+      out[wj++] = uint32_t(acc);
+      acc >>= 32;
+      pos -= 32;
+    }
+  }
+  if (mode == IQ_MODE_SYM) {
+    meta[unit] = __half_as_ushort(__float2half_rn(ss));
+  } else if (mode == IQ_MODE_HYBRID) {
+    const uint32_t sh = __half_as_ushort(__float2half_rn(sym ? ss : sa));
+    reinterpret_cast<uint32_t*>(meta)[unit] =
+        sym ? (sh | HYB_FLAG) : ((sh & 0x7fffu) | (uint32_t(__half_as_ushort(__float2half_rn(mn))) << 16));
+  } else {
+    reinterpret_cast<uint32_t*>(meta)[unit] = meta_word(sa, mn);
+  }
+}
+
+// one group of the flushed tokens of role r (group item q): element i is
+// token f0 + i * fstep of [window | new], column d0 + i * dstep
+template <int G>
+__device__ __forceinline__ void append_group(const WinRole& r, int H, int D, int64_t q) {
+  int64_t bh, unit;
+  int f0, fstep, d0, dstep;
+  if (r.axis == 0) {
+    const int ng = D / G;
+    const int g = int(q % ng);
+    const int64_t rest = q / ng;
+    const int f = int(rest % r.F);
+    bh = rest / r.F;
+    const int64_t tt = r.t_off + f;
+    unit = ((bh * r.cap_units + (tt >> 6)) * ng + g) * TOKEN_BLOCK + (tt & 63);
+    f0 = f; fstep = 0; d0 = g * G; dstep = 1;
+  } else {
+    const int d = int(q % D);
+    const int64_t rest = q / D;
+    const int ngf = r.F / G;
+    const int gi = int(rest % ngf);
+    bh = rest / ngf;
+    unit = (bh * r.cap_units + r.t_off / G + gi) * D + d;
+    f0 = gi * G; fstep = 1; d0 = d; dstep = 0;
+  }
+  const int64_t b = bh / H, h = bh % H;
+  float v[G];
+  if (r.axis == 0 && (f0 < r.n ? r.vec_buf : r.vec_x)) {  // G contiguous fp16, 16-byte aligned rows
+    const uint16_t* p = f0 < r.n ? r.buf + b * r.sb + h * r.sh + int64_t(r.start + f0) * r.st + d0
+                                 : r.x + b * r.sxb + h * r.sxh + int64_t(f0 - r.n) * r.sxt + d0;
+#pragma unroll
+    for (int c = 0; c < G / 8; ++c) {
+      const uint4 u = reinterpret_cast<const uint4*>(p)[c];
+      const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        v[8 * c + 2 * j] = h2f(uint16_t(w[j] & 0xffffu));
+        v[8 * c + 2 * j + 1] = h2f(uint16_t(w[j] >> 16));
+      }
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+      const int f = f0 + i * fstep, d = d0 + i * dstep;
+      const uint16_t* p = f < r.n ? r.buf + b * r.sb + h * r.sh + int64_t(r.start + f) * r.st + d
+                                  : r.x + b * r.sxb + h * r.sxh + int64_t(f - r.n) * r.sxt + d;
+      v[i] = h2f(*p);
+    }
+  }
+  if (r.norm) {  // cache.py:125  x / key_normalization_factor in fp16
+#pragma unroll
+    for (int i = 0; i < G; ++i) v[i] = round_f16(v[i] / h2f(r.norm[bh * D + d0 + i * dstep]));
+  }
+  quant_group_rt<G>(v, r.bits, r.mode, r.codes + unit * ((G * r.bits) >> 5), r.meta, unit);
+}
+
+// element e of the new tokens (b, h, j, d) into the window buffer
+__device__ __forceinline__ void window_copy(const WinRole& r, int H, int D, int64_t e) {
+  const int64_t per_bh = int64_t(r.m) * D;
+  const int64_t bh = e / per_bh, b = bh / H, h = bh % H;
+  const int j = int((e % per_bh) / D), d = int(e % D);
+  r.buf[b * r.sb + h * r.sh + int64_t(r.start + r.n + j) * r.st + d] = r.x[b * r.sxb + h * r.sxh + int64_t(j) * r.sxt + d];
+}
+
+template <int GK, int GV>
+__global__ __launch_bounds__(256) void window_append_kernel(AppendArgs a) {
+  const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  int k = 0;
+#pragma unroll
+  for (int s = 1; s < 4; ++s) k = i >= a.start[s] ? s : k;
+  const int64_t e = i - a.start[k];
+  if (e >= a.count[k]) return;
+  // (block-uniform k: each role's fields are read with a constant index)
+  if (k == 0) window_copy(a.r[0], a.H, a.D, e);
+  else if (k == 1) window_copy(a.r[1], a.H, a.D, e);
+  else if (k == 2) append_group<GK>(a.r[0], a.H, a.D, e);
+  else append_group<GV>(a.r[1], a.H, a.D, e);
+}
+
 }  // namespace
 
 // =============================================================================
@@ -698,6 +876,81 @@ int iq_dequant_dense(const int32_t* codes, const void* scale16, const void* zs16
   dequant_dense_kernel<<<dim3(unsigned(ceil_div(total, 256))), 256, 0, (hipStream_t)stream>>>(
       codes, (const uint16_t*)scale16, (const uint16_t*)zs16, outer, n, inner, group, mode == IQ_MODE_SYM, out_f16,
       out);
+  return launch_status();
+}
+
+namespace {
+int check_window(const iq_window* w, int D) {
+  if (!w) return IQ_OK;
+  IQ_CHECK(w->start >= 0 && w->n >= 0 && w->m >= 0 && w->flush >= 0 && w->cap >= 0, IQ_ERR_SHAPE);
+  IQ_CHECK(int64_t(w->start) + w->n + w->m <= w->cap, IQ_ERR_RANGE);
+  IQ_CHECK(w->flush <= w->n + w->m, IQ_ERR_SHAPE);
+  IQ_CHECK((w->n + w->m == 0 && w->flush == 0) || w->buf, IQ_ERR_NULL);
+  IQ_CHECK(w->m == 0 || w->x, IQ_ERR_NULL);
+  IQ_CHECK(aligned(w->buf, 2) && aligned(w->x, 2), IQ_ERR_ALIGN);
+  if (w->flush == 0) return IQ_OK;
+  IQ_CHECK(w->codes && w->meta, IQ_ERR_NULL);
+  if (int e = check_store(w->bits, w->group, w->mode)) return e;
+  IQ_CHECK(w->axis == 0 || w->axis == 1, IQ_ERR_SHAPE);
+  IQ_CHECK(!w->norm || w->axis == 0, IQ_ERR_SHAPE);
+  IQ_CHECK(w->t_off >= 0 && w->t_off + w->flush <= w->t_cap, IQ_ERR_RANGE);
+  if (w->axis == 0) {
+    IQ_CHECK(D % w->group == 0, IQ_ERR_GROUP);
+    IQ_CHECK(w->t_cap % TOKEN_BLOCK == 0, IQ_ERR_ALIGN);
+  } else {
+    IQ_CHECK(w->flush % w->group == 0 && w->t_off % w->group == 0 && w->t_cap % w->group == 0, IQ_ERR_GROUP);
+  }
+  IQ_CHECK(aligned(w->codes, 4) && aligned(w->meta, 4), IQ_ERR_ALIGN);
+  return IQ_OK;
+}
+
+WinRole to_role(const iq_window* w) {
+  WinRole r{};
+  if (!w) return r;
+  r.buf = (uint16_t*)w->buf; r.sb = w->s_b; r.sh = w->s_h; r.st = w->s_t;
+  r.start = w->start; r.n = w->n;
+  r.x = (const uint16_t*)w->x; r.sxb = w->sx_b; r.sxh = w->sx_h; r.sxt = w->sx_t; r.m = w->m;
+  r.F = w->flush;
+  r.codes = w->codes; r.meta = w->meta; r.t_off = w->t_off;
+  r.bits = w->bits; r.group = w->group; r.mode = w->mode; r.axis = w->axis;
+  r.gsh = w->group > 0 ? __builtin_ctz(unsigned(w->group)) : 0;
+  r.cap_units = w->flush ? (w->axis == 0 ? w->t_cap / TOKEN_BLOCK : w->t_cap / w->group) : 0;
+  r.norm = (const uint16_t*)w->norm;
+  r.vec_buf = aligned(w->buf, 16) && w->s_b % 8 == 0 && w->s_h % 8 == 0 && w->s_t % 8 == 0;
+  r.vec_x = aligned(w->x, 16) && w->sx_b % 8 == 0 && w->sx_h % 8 == 0 && w->sx_t % 8 == 0;
+  return r;
+}
+}  // namespace
+
+int iq_window_append(const iq_window* k, const iq_window* v, int B, int H, int D, void* stream) {
+  IQ_CHECK(B >= 0 && H >= 0 && D > 0, IQ_ERR_SHAPE);
+  if (int e = check_window(k, D)) return e;
+  if (int e = check_window(v, D)) return e;
+  AppendArgs a{};
+  a.r[0] = to_role(k);
+  a.r[1] = to_role(v);
+  a.H = H; a.D = D;
+  const int64_t bh = int64_t(B) * H;
+  for (int r = 0; r < 2; ++r) {
+    const WinRole& w = a.r[r];
+    a.count[r] = bh * w.m * D;
+    a.count[2 + r] = w.F == 0 ? 0 : (w.axis == 0 ? bh * w.F * (D / w.group) : bh * (w.F / w.group) * D);
+  }
+  int64_t at = 0;
+  for (int s = 0; s < 4; ++s) {
+    a.start[s] = at;
+    at += ceil_div(a.count[s], 256) * 256;
+  }
+  if (at == 0) return IQ_OK;
+  auto go = [&]<int GK>(int gv) {
+    auto* kern = gv == 128 ? window_append_kernel<GK, 128> : gv == 64 ? window_append_kernel<GK, 64>
+                                                                      : window_append_kernel<GK, 32>;
+    kern<<<dim3(unsigned(at / 256)), 256, 0, (hipStream_t)stream>>>(a);
+  };
+  const int gk = a.r[0].F ? a.r[0].group : 32, gv = a.r[1].F ? a.r[1].group : 32;
+  if (gk == 128) go.template operator()<128>(gv);
+  else if (gk == 64) go.template operator()<64>(gv);
+  else go.template operator()<32>(gv);
   return launch_status();
 }
 

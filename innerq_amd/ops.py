@@ -350,6 +350,95 @@ class PackedStore:
         return out
 
 
+class RecentWindow:
+    """An fp16 recent window [B,H,n,D] (cache.py's keys_recent / values_recent)
+    kept in a buffer with room to grow: tokens [start, start + n) of ``buf``.
+    A decode step writes its new tokens after the window and advances
+    ``start`` past the flushed ones (window_append), so no step copies the
+    window.  When the buffer is full the window moves to the front of a new,
+    larger buffer; a view returned earlier keeps its old buffer and values."""
+
+    def __init__(self, x: torch.Tensor):
+        require_device(x, "recent window")
+        B, H, n, D = x.shape
+        self.buf = torch.empty(B, H, max(2 * n, n + 64), D, dtype=x.dtype, device=x.device)
+        self.buf[:, :, :n].copy_(x)
+        self.start, self.n = 0, n
+
+    @property
+    def tensor(self) -> torch.Tensor:
+        return self.buf[:, :, self.start:self.start + self.n]
+
+    def reserve(self, m: int) -> None:
+        """Room for m more tokens after the window."""
+        B, H, cap, D = self.buf.shape
+        if self.start + self.n + m <= cap:
+            return
+        buf = torch.empty(B, H, max(2 * (self.n + m), self.n + m + 64), D, dtype=self.buf.dtype, device=self.buf.device)
+        buf[:, :, :self.n].copy_(self.tensor)
+        self.buf, self.start = buf, 0
+
+
+def window_append(kwin: Optional[RecentWindow], knew: Optional[torch.Tensor], kflush: int,
+                  kstore: Optional[PackedStore], knorm: Optional[torch.Tensor],
+                  vwin: Optional[RecentWindow], vnew: Optional[torch.Tensor], vflush: int,
+                  vstore: Optional[PackedStore]) -> None:
+    """One decode step of a layer's recent windows in one launch: the new tokens
+    [B,H,m,D] go after each window, the first ``flush`` tokens of [window | new]
+    are quantized into the store (cache.py:283-365), the windows advance past
+    them and the stores grow by them."""
+    roles, keep, shape = [], [], None
+    for win, x, fl, st, norm in ((kwin, knew, kflush, kstore, knorm), (vwin, vnew, vflush, vstore, None)):
+        if win is None:
+            roles.append(None)
+            continue
+        require_device(x, "new tokens")
+        if x.stride(-1) != 1:
+            x = x.contiguous()
+        B, H, m, D = x.shape
+        if win.buf.shape[0] != B or win.buf.shape[1] != H or win.buf.shape[3] != D:
+            _shape_error(f"window_append: new tokens {tuple(x.shape)} do not fit a window of "
+                         f"[{win.buf.shape[0]}, {win.buf.shape[1]}, n, {win.buf.shape[3]}]")
+        shape = (B, H, D)
+        win.reserve(m)
+        w = _lib.iq_window()
+        w.buf = win.buf.data_ptr()
+        w.s_b, w.s_h, w.s_t = win.buf.stride()[:3]
+        w.cap, w.start, w.n = win.buf.shape[2], win.start, win.n
+        w.x = x.data_ptr()
+        w.sx_b, w.sx_h, w.sx_t = x.stride()[:3]
+        w.m, w.flush = m, fl
+        if fl:
+            if st is None:
+                raise ValueError("window_append: flushing tokens needs a store")
+            if st.axis == "token" and fl % st.group:
+                _shape_error(f"window_append: a token-grouped store takes whole groups of {st.group} tokens, "
+                             f"got {fl}")
+            st.reserve(st.length + fl)
+            w.codes, w.meta = st.codes.data_ptr(), st.meta.data_ptr()
+            w.t_cap, w.t_off = st.t_cap, st.length
+            w.bits, w.group, w.mode = st.bits, st.group, st.mode
+            w.axis = 0 if st.axis == "channel" else 1
+            if norm is not None:
+                if st.axis != "channel":
+                    raise NotImplementedError("key normalization is supported for keys grouped along head_dim")
+                norm = norm.reshape(B, H, D).contiguous()
+                w.norm = norm.data_ptr()
+        keep.append((x, norm))
+        roles.append(w)
+    if shape is None:
+        return
+    call("iq_window_append", ctypes.byref(roles[0]) if roles[0] is not None else None,
+         ctypes.byref(roles[1]) if roles[1] is not None else None, *shape, _stream(knew.device if knew is not None
+                                                                                   else vnew.device))
+    for win, x, fl, st in ((kwin, knew, kflush, kstore), (vwin, vnew, vflush, vstore)):
+        if win is not None:
+            win.start += fl
+            win.n += x.shape[-2] - fl
+            if fl:
+                st.length += fl
+
+
 def quantize_dense(x: torch.Tensor, group: int, bits: int, mode, axis: str):
     """Reference-format quantization of a [rows, n, inner]-viewable fp16 tensor.
 

@@ -229,3 +229,32 @@ def test_decode_noalloc_limits():
                                            None) == -4
     assert lib.iq_decode_attention_noalloc(FAKE, 4096, 128, None, k, v, 64, 32, 8, T, 128, 1.0, None, 4096, 128,
                                            None) == -1
+
+
+def _window(**kw):
+    w = _lib.iq_window()
+    d = dict(buf=0x1000, s_b=0, s_h=0, s_t=128, cap=64, start=0, n=8, x=0x2000, sx_b=0, sx_h=0, sx_t=128, m=1,
+             flush=0, codes=None, meta=None, t_cap=0, t_off=0, bits=4, group=32, mode=0, axis=0, norm=None)
+    d.update(kw)
+    for k, v in d.items():
+        setattr(w, k, v)
+    return w
+
+
+@pytest.mark.parametrize("kw,err", [
+    (dict(start=60, n=4, m=1), -8),                         # no room after the window
+    (dict(m=-1), -4), (dict(flush=10, n=8, m=1), -4),        # flush beyond [window | new]
+    (dict(x=None), -1), (dict(buf=None), -1),
+    (dict(flush=1), -1),                                     # flushing without a store
+    (dict(flush=1, codes=0x3000, meta=0x4000, t_cap=64, bits=5), -2),
+    (dict(flush=1, codes=0x3000, meta=0x4000, t_cap=64, mode=3), -7),
+    (dict(flush=1, codes=0x3000, meta=0x4000, t_cap=64, t_off=64), -8),
+    (dict(flush=1, codes=0x3000, meta=0x4000, t_cap=100), -5),              # K layout: t_cap % 64
+    (dict(flush=8, n=8, m=1, codes=0x3000, meta=0x4000, t_cap=64, axis=1), -3),  # V layout: whole groups
+    (dict(flush=1, codes=0x3000, meta=0x4000, t_cap=64, axis=1, norm=0x5000), -4),
+])
+def test_window_append_rejects(kw, err):
+    """Every bad argument is refused on the host before any launch."""
+    w = _window(**kw)
+    assert _lib.lib().iq_window_append(ctypes.byref(w), None, 1, 1, 128, None) == err
+    assert _lib.lib().iq_window_append(None, ctypes.byref(w), 1, 1, 128, None) == err

@@ -1,0 +1,94 @@
+"""iq_window_append (one decode step of a layer's recent windows, both roles in
+one launch) against the separate path it replaces: the new tokens land after
+the window, and the flushed tokens' packed bytes equal those of
+PackedStore.append (iq_quantize_k / iq_quantize_v) on the same tokens, for both
+store layouts, every mode (hybrid included), key normalization, flushes that
+reach into the new tokens, and a buffer that has to grow."""
+import numpy as np
+import pytest
+import torch
+
+from innerq_amd import ops, synth
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def _t(a):
+    return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
+
+
+def _mixed(B, H, T, D, seed):
+    x = synth.kv_tensor(B, H, T, D, seed=seed, n_out=3, factor=8.0).astype(np.float32)
+    x[..., :40] += 5.0  # offset columns: hybrid groups of both kinds
+    x[0, 0, 70, :] = 0.0         # an all-zero key token (constant channel groups)
+    x[0, 1, 2 * 32:3 * 32, 5] = -2.0  # a constant token group of a value column
+    return x.astype(np.float16)
+
+
+def _bytes(st):
+    u = st.unit
+    n = -(-st.length // u)
+    bh = st.B * st.H
+    c = st.codes.view(bh, st.t_cap // u, -1)[:, :n].cpu().numpy()
+    m = st.meta.view(bh, st.t_cap // u, -1)[:, :n].cpu().numpy()
+    return c, m
+
+
+@pytest.mark.parametrize("kmode,vmode", [("asymmetric", "symmetric"), ("symmetric", "hybrid"), ("hybrid", "asymmetric")])
+@pytest.mark.parametrize("bits,G", [(2, 32), (3, 64), (4, 128)])
+@pytest.mark.parametrize("norm", [False, True])
+def test_window_append_matches_separate_path(kmode, vmode, bits, G, norm):
+    B, H, D = 2, 3, 128
+    T = 4 * G + 50
+    kx, vx = _mixed(B, H, T, D, seed=bits + G), _mixed(B, H, T, D, seed=bits * G + 1)
+    kt, vt = _t(kx), _t(vx)
+    knorm = ops.key_norm_factor(kt[:, :, :64]) if norm else None
+    # windows of 20 (K) and G + 5 (V) tokens after a first store part
+    k0, v0 = 64, 2 * G
+    ks = ops.PackedStore("channel", B, H, D, G, bits, kmode, DEV)
+    vs = ops.PackedStore("token", B, H, D, G, bits, vmode, DEV)
+    ks.append(kt[:, :, :k0], norm=knorm)
+    vs.append(vt[:, :, :v0])
+    kw, vw = ops.RecentWindow(kt[:, :, k0:k0 + 20]), ops.RecentWindow(vt[:, :, v0:v0 + G + 5])
+    kref = ops.PackedStore("channel", B, H, D, G, bits, kmode, DEV)
+    vref = ops.PackedStore("token", B, H, D, G, bits, vmode, DEV)
+    kref.append(kt[:, :, :k0], norm=knorm)
+    vref.append(vt[:, :, :v0])
+    kpos, vpos = k0 + 20, v0 + G + 5   # next new token of each role
+    kdone, vdone = k0, v0          # tokens in the stores
+    # the last step flushes the whole K window and two of its three new tokens
+    steps = [(1, 1, 0), (1, 3, 0), (2, 0, G), (1, 1, 0), (3, 22, 0)]
+    for m, kf, vf in steps:
+        # m new tokens (a key-value pair each), kf keys and vf values flushed
+        knew, vnew = kt[:, :, kpos:kpos + m], vt[:, :, vpos:vpos + m]
+        ops.window_append(kw, knew, kf, ks if kf else None, knorm if kf else None, vw, vnew, vf, vs if vf else None)
+        if kf:
+            kref.append(kt[:, :, kdone:kdone + kf], norm=knorm)
+        if vf:
+            vref.append(vt[:, :, vdone:vdone + vf])
+        kpos, vpos, kdone, vdone = kpos + m, vpos + m, kdone + kf, vdone + vf
+        torch.cuda.synchronize()
+        assert torch.equal(kw.tensor, kt[:, :, kdone:kpos]) and torch.equal(vw.tensor, vt[:, :, vdone:vpos])
+        assert ks.length == kref.length and vs.length == vref.length
+        for a, b in ((ks, kref), (vs, vref)):
+            ca, ma = _bytes(a)
+            cb, mb = _bytes(b)
+            np.testing.assert_array_equal(ca, cb)
+            np.testing.assert_array_equal(ma, mb)
+
+
+def test_window_grows_and_keeps_old_views():
+    """Appending past the buffer's end moves the window to a larger buffer; a
+    view taken before keeps its values."""
+    B, H, D = 1, 2, 64
+    x = _t(synth.kv_tensor(B, H, 400, D, seed=5))
+    w = ops.RecentWindow(x[:, :, :10])
+    views = []
+    for i in range(10, 400, 7):
+        ops.window_append(w, x[:, :, i:i + 7], 0, None, None, None, None, 0, None)
+        views.append((w.tensor, min(i + 7, 400)))
+    torch.cuda.synchronize()
+    assert w.n == 400 and torch.equal(w.tensor, x)
+    for v, end in views:
+        assert torch.equal(v, x[:, :, :end])
