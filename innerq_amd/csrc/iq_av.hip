@@ -168,11 +168,8 @@ __global__ __launch_bounds__(256) void av_combine_kernel(const float* __restrict
   const int64_t bq = i / D;
   const int d = int(i % D);
   int n = nsplit;
-  if (grid > 0) {  // the runs of the (batch, KV head) in the persistent kernel's shares
-    const int64_t bh = bq / nrep, nitems = rows / nrep * nsplit;
-    auto share_of = [&](int64_t s) { return (s + 1) * grid / nitems + ((s + 1) * grid % nitems ? 1 : 0) - 1; };
-    n = int(share_of((bh + 1) * nsplit - 1) - share_of(bh * nsplit) + 1);
-  }
+  if (grid > 0)  // the runs of the (batch, KV head) in the persistent kernel's shares
+    n = detail::ShareMap::make(grid, int(rows / nrep), nsplit, 0).nruns(int(bq / nrep));  // plain partition
   float v = 0.f;
   for (int s = 0; s < n; ++s) v += part[(int64_t(s) * rows + bq) * D + d];
   const int64_t off32 = (bq / Hq) * o.s32b + (bq % Hq) * o.s32h + d;

@@ -429,8 +429,9 @@ __global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs a) {
 // over the row's live split slots, listed in slot order: the fused kernel's
 // run partials of the row's (batch, KV head), slots 0 .. nr-1, then the dense
 // slices' slots nsf .. nsplit-1.  With the fused kernel's workgroup count
-// (grid > 0) nr follows from its share arithmetic: the runs of a (batch, KV
-// head) come from the consecutive shares that hold its splits, one run each.
+// (grid > 0) nr follows from its share arithmetic (detail::ShareMap): the
+// runs of a (batch, KV head) come from the shares that hold its splits, one
+// run each.
 // Without it (grid = 0: the unfused path, which writes every slot, or a
 // caller of the split stage alone, whose fused kernel wrote empty statistics
 // in the slots past the runs) every slot 0 .. nsplit-1 is read.  One round of
@@ -443,9 +444,9 @@ constexpr int MAXSPLIT = 1024;  // split slots of one step, at most
 constexpr int CSPEC = 8;
 template <int DPL, int E>
 __global__ __launch_bounds__(64) void flash_combine_kernel(const float* __restrict__ ml, const float* __restrict__ part,
-                                                           int nsplit, int nsf, int grid, int nrep, int64_t rows,
-                                                           int Hq, uint16_t* __restrict__ out, int64_t sob,
-                                                           int64_t soh) {
+                                                           int nsplit, int nsf, int grid, int pair_e0, int nrep,
+                                                           int64_t rows, int Hq, uint16_t* __restrict__ out,
+                                                           int64_t sob, int64_t soh) {
   using Vec = float __attribute__((ext_vector_type(DPL)));
   constexpr int D = 64 * DPL;
   __shared__ int sidx[64 * E];
@@ -453,11 +454,8 @@ __global__ __launch_bounds__(64) void flash_combine_kernel(const float* __restri
   const int64_t bq = blockIdx.x;
   const int lane = threadIdx.x;
   int nr = nsf;
-  if (grid > 0) {
-    const int64_t bh = bq / nrep, nitems = rows / nrep * nsf;
-    auto share_of = [&](int64_t s) { return ((s + 1) * grid + nitems - 1) / nitems - 1; };
-    nr = int(share_of((bh + 1) * nsf - 1) - share_of(bh * nsf) + 1);
-  }
+  if (grid > 0)  // the runs of the (batch, KV head) in the fused kernel's shares
+    nr = detail::ShareMap::make(grid, int(rows / nrep), nsf, pair_e0).nruns(int(bq / nrep));
   const int n = nr + (nsplit - nsf);                                   // live slots
   auto slot = [&](int i) { return i < nr ? i : nsf + (i - nr); };     // i-th live slot
   const float2* st = reinterpret_cast<const float2*>(ml) + bq;         // slot s: st[s * rows]
@@ -609,6 +607,7 @@ int check_decode(const void* q, const iq_segment* k, const iq_segment* v, int B,
 // combine that scans every slot).
 struct SplitPlan {
   int nsplit = 0, nsf = 0, grid = 0, nrep = 1;
+  int pair_e0 = 0;  // the fused kernel's partition (detail::ShareMap)
 };
 
 // Launches everything up to the split statistics and partials.  `live`: the
@@ -698,6 +697,7 @@ int launch_splits(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, c
                                            live ? &grid : nullptr, st))
       return e;
     plan->grid = grid;
+    plan->pair_e0 = detail::fused_pair_e0(k[1].bits, v[1].bits, v[1].mode == IQ_MODE_HYBRID);
   } else if (c) {
     const iq_segment& kg = k[1];
     const iq_segment& vg = v[1];
@@ -723,8 +723,8 @@ int launch_combine(const Workspace& w, const SplitPlan& plan, int B, int Hq, int
   // statistics registers per lane: the smallest power of two with 64 E >= nsplit
   auto go = [&]<int DPL, int E>() {
     flash_combine_kernel<DPL, E><<<dim3(unsigned(rows)), 64, 0, st>>>(w.ml, w.part, nsplit, plan.nsf, plan.grid,
-                                                                      plan.nrep, rows, Hq, (uint16_t*)out, so_b,
-                                                                      so_h);
+                                                                      plan.pair_e0, plan.nrep, rows, Hq,
+                                                                      (uint16_t*)out, so_b, so_h);
   };
   auto by_e = [&]<int DPL>() {
     if (nsplit <= 64) go.template operator()<DPL, 1>();

@@ -9,9 +9,11 @@
 // the instantiations compile in parallel) and iq_flash.hip holds the entry.
 //
 // Persistent and software pipelined.  One workgroup per CU (waves per SIMD:
-// fused_waves_per_simd) takes an equal contiguous share of the (batch, KV
-// head)-major list of FSPLIT-token splits (each XCD one contiguous eighth of
-// the list), loaded with the non-temporal cache policy, and processes it as
+// fused_waves_per_simd) takes an equal contiguous share of a list of
+// FSPLIT-token splits (detail::ShareMap: the (batch, KV head)-major list, or
+// for 4-bit K and V each head's splits cut 68:60 between the even and the
+// odd XCDs, whose workgroups measured ~3 us slower), loaded with the
+// non-temporal cache policy, and processes it as
 // runs, the maximal pieces of one (batch, KV head).  Inside a run the waves
 // claim wave blocks of WTOK tokens (lane = token for QK^T) from a counter in
 // LDS, so they finish the run together, and each wave keeps a running
@@ -139,7 +141,6 @@ struct FusedSmem {
 // of it changed nothing).  The query, reused by every workgroup of a head,
 // keeps the default policy.
 constexpr int STREAM = 2;  // cache policy bits of a streaming load: nt
-constexpr unsigned XCDS = 8;  // accelerator complex dies of an MI355X
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
 __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, int(bytes), 0x00020000);
@@ -345,45 +346,49 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS, AVO>::NT), (fused_waves_pe
 
   const PlanRegs<KB> prk;
   const PlanRegs<VB> prv;
-  // ---- work: this workgroup's splits [i0, i1) of the (batch, KV head)-major
-  // split list (contiguous, equal shares: one workgroup per CU), processed as
-  // runs, the maximal pieces of one (batch, KV head).  Inside a run the waves
-  // claim wave blocks from a counter in LDS (the first two per wave are
+  // ---- work: this workgroup's share [i0, i1) of its side's list of splits
+  // (detail::ShareMap: contiguous, equal shares, one workgroup per CU; each
+  // XCD, or each XCD pair, streams a contiguous part of the cache), processed
+  // as runs, the maximal pieces of one (batch, KV head).  Inside a run the
+  // waves claim wave blocks from a counter in LDS (the first two per wave are
   // fixed), so they all finish the run within about one block of each other
   // whatever the issue arbitration favours. ----
-  // Share sh of the list for workgroup b: workgroups are dealt to the XCDs
-  // round robin (b runs on XCD b % 8), so sh = (b % 8) * (grid / 8) + b / 8
-  // gives each XCD one contiguous eighth of the list (its own heads, whole)
-  // instead of every eighth share: -1 us per headline step (A/B, five rounds).
-  const int sh = gridDim.x % XCDS == 0 ? int(blockIdx.x % XCDS) * int(gridDim.x / XCDS) + int(blockIdx.x / XCDS)
-                                       : int(blockIdx.x);
-  const int i0 = int(int64_t(sh) * a.nitems / gridDim.x);
-  const int i1 = int(int64_t(sh + 1) * a.nitems / gridDim.x);
+  const detail::ShareMap smap = detail::ShareMap::make(int(gridDim.x), a.nitems / a.nsplit, a.nsplit, a.pair_e0);
+  int side, sh;
+  smap.share(int(blockIdx.x), side, sh);
+  const int plen = smap.len(side), pfirst = smap.first(side);  // a head's splits on this side
+  const int i0 = int(smap.begin(side, sh));
+  const int i1 = int(smap.begin(side, sh + 1));
   if (i0 >= i1) return;  // uniform over the workgroup, before any barrier
   struct Run {
     int bh, split0, nsplit, nb;  // (batch, KV head), first split, splits, wave blocks
   };
-  auto run_at = [&](int s0) {
+  auto run_at = [&](int s0) {  // the run at list position s0
     Run r;
-    r.bh = s0 / a.nsplit;
-    r.split0 = s0 - r.bh * a.nsplit;
-    r.nsplit = min(i1, (r.bh + 1) * a.nsplit) - s0;
+    r.bh = s0 / plen;
+    r.split0 = pfirst + (s0 - r.bh * plen);
+    r.nsplit = min(i1, (r.bh + 1) * plen) - s0;
     r.nb = r.nsplit * BPS;
     return r;
   };
   // wave block (within the (batch, KV head)) of run-relative index idx
   auto block_of = [&](const Run& r, int idx) { return r.split0 * BPS + idx; };
-  // the share holding global split s: max c with c*nitems/grid <= s
-  auto share_of = [&](int s) {
-    return int(((int64_t(s) + 1) * gridDim.x + a.nitems - 1) / a.nitems) - 1;
-  };
-  // The runs of one (batch, KV head) come from the consecutive shares
-  // share_of(first split) .. share_of(last split), one run each: run k of them
-  // writes its partial into split slot k, so the nr partials of a (batch, KV
-  // head) fill slots [0, nr) and the combine finds them without a search; the
-  // slots [nr, nsplit) carry empty statistics, each written by the run whose
-  // splits hold it.
+  // A (batch, KV head)'s runs come from consecutive shares of each side, one
+  // run per share: they write their partials into split slots [0, nr) in
+  // share order, side 0 first, so the combine finds them without a search;
+  // the slots [nr, nsplit) carry empty statistics, each written by the run
+  // whose splits hold it.
+  // paired: one slot for every run of the share and a fixed run count
+  // (computed here, so that only two values stay live through the loop)
+  const int fslot = smap.paired ? smap.paired_slot(side, sh) : -1, fnr = 2 * smap.kk;
   auto run_slots = [&](const Run& r, int& slot, int& nr) {
+    if (fslot >= 0) {
+      slot = fslot;
+      nr = fnr;
+      return;
+    }
+    // plain: the shares holding the head's first and last split
+    auto share_of = [&](int s) { return int(((int64_t(s) + 1) * gridDim.x + a.nitems - 1) / a.nitems) - 1; };
     const int c0 = share_of(r.bh * a.nsplit);
     slot = sh - c0;
     nr = share_of((r.bh + 1) * a.nsplit - 1) - c0 + 1;

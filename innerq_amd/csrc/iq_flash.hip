@@ -51,6 +51,7 @@ int flash_fused_launch(const void* q, int64_t sq_b, int64_t sq_h, const void* no
   a.scale_log2 = scale * 1.4426950408889634f;
   a.ml = ml; a.part = part;
   a.empty_stats = grid ? 0 : 1;  // a caller that takes the workgroup count reads only the run slots
+  a.pair_e0 = fused_pair_e0(k.bits, v.bits, v.mode == IQ_MODE_HYBRID);
   if (k.mode == IQ_MODE_HYBRID) return IQ_ERR_MODE;
   if (v.mode == IQ_MODE_HYBRID) {
     switch (k.bits) {

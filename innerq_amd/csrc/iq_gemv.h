@@ -372,6 +372,98 @@ bool flash_fused_supported(const void* q, int64_t sq_b, int64_t sq_h, const void
 int flash_fused_launch(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, const FusedStore& k,
                        const FusedStore& v, int B, int Hq, int Hkv, int T, int D, float scale, float* ml,
                        float* part, int* grid, hipStream_t stream);
+// Work partition of the persistent fused kernel: which splits of the
+// (batch, KV head)-major split list each workgroup streams, and in which
+// split slot each of its runs (maximal pieces of one (batch, KV head))
+// leaves its partial.  The kernel and both combine kernels derive it from
+// (grid, heads, splits per head) alone.  Workgroups are dealt to the XCDs
+// round robin (workgroup b runs on XCD b % 8).
+//
+// plain:  one list (every head's splits in order), one equal contiguous share
+//         per workgroup; share (b % 8) * (grid / 8) + b / 8 for workgroup b, so
+//         XCD x streams the x-th contiguous eighth of the list.  The runs of a
+//         head come from the consecutive shares holding its splits and take
+//         slots [0, nr) in share order.
+// paired: each head's splits are cut at e0: [0, e0) belong to side 0, [e0,
+//         nsplit) to side 1.  Side s's parts of all heads, in head order,
+//         form list s; the even XCDs (side 0) and the odd XCDs (side 1) each
+//         take their list in equal contiguous shares, XCD 2k / 2k + 1 the k-th
+//         quarter, so an XCD pair streams the two parts of the same heads.
+//         Used where shares and head parts align (workgroups per side a
+//         multiple of the heads, kk shares per part, or the other way round,
+//         whole parts per share): a run of side s in share sh takes slot
+//         s * kk + sh % kk of its head's 2 kk.
+//         The cut is e0_num / 128 of a head (fused_pair_e0: which kernels
+//         use it, and where).
+struct ShareMap {
+  static constexpr int XCDS = 8;  // accelerator complex dies of an MI355X
+  static constexpr int E0_DEN = 128;
+  int grid, nhead, nsplit;
+  int e0;      // splits of a head on side 0 (plain: nsplit)
+  int paired;  // 1: two sides
+  int kk;      // paired: shares per head part (1: whole parts per share)
+
+  // e0_num > 0 asks for the paired partition: used wherever the grid deals
+  // evenly over the XCDs, a head has at least four splits, a workgroup
+  // streams at least eight splits on average, and shares align with head
+  // parts; plain otherwise
+  __host__ __device__ static ShareMap make(int grid, int nhead, int nsplit, int e0_num) {
+    ShareMap m{grid, nhead, nsplit, nsplit, 0, 1};
+    const int w = grid / 2;
+    if (e0_num > 0 && grid >= 2 * XCDS && grid % XCDS == 0 && nsplit >= 4 && nhead > 0 &&
+        int64_t(nhead) * nsplit >= int64_t(8) * grid && (w % nhead == 0 || nhead % w == 0)) {
+      m.paired = 1;
+      m.kk = w >= nhead ? w / nhead : 1;
+      m.e0 = (nsplit * e0_num + E0_DEN / 2) / E0_DEN;
+      m.e0 = m.e0 < m.kk ? m.kk : m.e0 > nsplit - m.kk ? nsplit - m.kk : m.e0;
+    }
+    return m;
+  }
+  __host__ __device__ int len(int side) const { return side ? nsplit - e0 : e0; }
+  __host__ __device__ int first(int side) const { return side ? e0 : 0; }  // a head's first split of the side
+  __host__ __device__ int width() const { return paired ? grid / 2 : grid; }  // workgroups per side
+  __host__ __device__ int64_t items(int side) const { return int64_t(nhead) * len(side); }
+  // side and side-local share of workgroup b
+  __host__ __device__ void share(int b, int& side, int& sh) const {
+    if (grid % XCDS) {
+      side = 0;
+      sh = b;
+      return;
+    }
+    const int x = b % XCDS, r = b / XCDS, per = grid / XCDS;
+    side = paired ? x & 1 : 0;
+    sh = (paired ? x >> 1 : x) * per + r;
+  }
+  // first list position of share sh of a side (sh = width(): the list's end)
+  __host__ __device__ int64_t begin(int side, int sh) const { return int64_t(sh) * items(side) / width(); }
+  // plain: the share holding list position j
+  __host__ __device__ int share_of(int64_t j) const { return int(((j + 1) * grid + items(0) - 1) / items(0)) - 1; }
+  // runs (= partial slots) of head h
+  __host__ __device__ int nruns(int h) const {
+    if (paired) return 2 * kk;
+    return share_of(int64_t(h + 1) * nsplit - 1) - share_of(int64_t(h) * nsplit) + 1;
+  }
+  // paired: the slot of every run in share sh of a side
+  __host__ __device__ int paired_slot(int side, int sh) const { return side * kk + sh % kk; }
+  // split slot of head h's run in share sh of a side
+  __host__ __device__ int slot(int side, int sh, int h) const {
+    return paired ? paired_slot(side, sh) : sh - share_of(int64_t(h) * nsplit);
+  }
+};
+
+// The decode kernel's partition per store format: 4-bit K and V take the
+// paired partition with a 68/128 cut (ShareMap e0_num), every other format
+// the plain one.  Per-workgroup end times of the 4/4-bit kernel at the
+// headline shape showed the odd XCDs of an MI355X finishing ~3 us after the
+// even ones on every launch of equal shares (two boxes); cuts of 66-68 / 128
+// measured 1.1-1.9 us faster per launch there (four boxes, same-box A/B).
+// The same A/B at the other formats measured: 2-bit K / 4-bit V (config-4
+// layer) equal at 66 and 0.5-1.5 us slower at 64 and 68-70, 3-bit sym K and V
+// 0.7 us slower at 66-68, attn.V only (2-bit, G = 64) 1.1-2.4 us slower.
+__host__ __device__ inline int fused_pair_e0(int kbits, int vbits, bool hybrid_v) {
+  return kbits == 4 && vbits == 4 && !hybrid_v ? 68 : 0;
+}
+
 // the fused kernel's arguments (filled by flash_fused_launch)
 struct FusedArgs {
   const uint16_t* q;
@@ -396,6 +488,7 @@ struct FusedArgs {
   // partials (a combine that scans every slot needs them; one told the
   // launch's workgroup count reads only the run slots)
   int empty_stats;
+  int pair_e0;  // the partition (ShareMap e0_num; 0: plain)
 };
 // its launch per K bit width (iq_flash_k{2,3,4}.hip)
 int flash_fused_launch_k2(const FusedArgs& a, int vbits, int group, int D, int nrep, bool norm, int* grid,
