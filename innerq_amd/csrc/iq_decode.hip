@@ -340,7 +340,7 @@ __global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs a) {
     // no per-iteration guard on the head (a wave-uniform branch in the loop
     // serialized it on LDS latency): heads past NREP read the last head's
     // query and their logits are dropped below
-#pragma unroll 8
+#pragma unroll 16
     for (int i = 0; i < D / 2; ++i) {
       const uint32_t k2 = kt[lane][i];
       const float k0 = h2f(uint16_t(k2 & 0xffffu)), k1 = h2f(uint16_t(k2 >> 16));
@@ -379,22 +379,29 @@ __global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs a) {
       }
     }
     __syncthreads();
-    // ---- attn.V: thread = (head, column pair) ----
-    const int cnt = min(DT, i1 - c0);
+    // ---- attn.V: thread = (head, column pair), eight tokens per step in two
+    // accumulation chains (the tile rows past the chunk's tokens are zero and
+    // their p is 0, so the chunk is read in whole steps) ----
+    const int cnt8 = (min(DT, i1 - c0) + 7) & ~7;
 #pragma unroll
     for (int it = 0; it < OPT; ++it) {
       const int idx = tid + 256 * it;
       if (idx < NREP * NPR) {
         const int h = idx / NPR, dp = idx % NPR;
-        float o0 = o[it][0] * al[h], o1 = o[it][1] * al[h];
-        for (int j = 0; j < cnt; ++j) {
-          const float p = ps[h][j];
-          const uint32_t v2 = vt[j][dp];
-          o0 = fmaf(p, h2f(uint16_t(v2 & 0xffffu)), o0);
-          o1 = fmaf(p, h2f(uint16_t(v2 >> 16)), o1);
+        float o0 = o[it][0] * al[h], o1 = o[it][1] * al[h], e0 = 0.f, e1 = 0.f;
+        for (int j = 0; j < cnt8; j += 8) {
+#pragma unroll
+          for (int u = 0; u < 8; u += 2) {
+            const float pa = ps[h][j + u], pb = ps[h][j + u + 1];
+            const uint32_t va = vt[j + u][dp], vb = vt[j + u + 1][dp];
+            o0 = fmaf(pa, h2f(uint16_t(va & 0xffffu)), o0);
+            o1 = fmaf(pa, h2f(uint16_t(va >> 16)), o1);
+            e0 = fmaf(pb, h2f(uint16_t(vb & 0xffffu)), e0);
+            e1 = fmaf(pb, h2f(uint16_t(vb >> 16)), e1);
+          }
         }
-        o[it][0] = o0;
-        o[it][1] = o1;
+        o[it][0] = o0 + e0;
+        o[it][1] = o1 + e1;
       }
     }
     __syncthreads();

@@ -22,6 +22,11 @@ namespace {
 
 constexpr int32_t I32_MIN = (int32_t)0x80000000u;
 
+// groups of a K quantize call up to which it runs one lane per value
+// (quant_k_lane_kernel); past it, one thread per group (~2x fewer
+// instructions per value, and enough threads to fill the device)
+constexpr int64_t LANE_MAX_GROUPS = 65536;
+
 struct QuantOut {
   uint32_t* codes;     // packed store codes (or null)
   uint16_t* meta;      // packed store meta
@@ -280,6 +285,121 @@ __global__ __launch_bounds__(256) void quant_k_kernel(const uint16_t* __restrict
     const int64_t red = (bh * n + t) * ng + g;
     if (o.scale16) o.scale16[red] = __half_as_ushort(__float2half_rn(s));
     if (o.zero16) o.zero16[red] = __half_as_ushort(__float2half_rn(z));
+  }
+}
+
+// ---- one group across G lanes (small appends) ------------------------------
+// The one-thread-per-group kernels run each group as one thread's chain of
+// ~G * 25 dependent instructions: fine for a prompt (many groups), but a
+// decode step's append is a few hundred groups, i.e. one or two workgroups
+// and ~8 us of latency (a one-token K append at B=16: measured).  Here the
+// G <= 64 lanes of an aligned segment of one wave hold one group, lane i its
+// element i; the extremes, the NaN test and the packed words are reduced
+// across the segment.  The per-value arithmetic is quantize_group's /
+// quant_group_rt's, the extremes are exact and the words are ORs of disjoint
+// bit fields, so the fields and meta are the same bit for bit.  Asym and sym
+// only: hybrid's error sums keep the one-thread-per-group order.
+template <int G>
+__device__ __forceinline__ uint64_t seg_mask() {
+  const int lane = threadIdx.x & 63;
+  return G == 64 ? ~0ull : ((1ull << G) - 1ull) << (lane & ~(G - 1));
+}
+template <int G>
+__device__ __forceinline__ float seg_fmin(float x) {
+#pragma unroll
+  for (int o = 1; o < G; o <<= 1) x = fminf(x, __shfl_xor(x, o, 64));
+  return x;
+}
+template <int G>
+__device__ __forceinline__ float seg_fmax(float x) {
+#pragma unroll
+  for (int o = 1; o < G; o <<= 1) x = fmaxf(x, __shfl_xor(x, o, 64));
+  return x;
+}
+template <int G>
+__device__ __forceinline__ uint32_t seg_or(uint32_t x) {
+#pragma unroll
+  for (int o = 1; o < G; o <<= 1) x |= uint32_t(__shfl_xor(int(x), o, 64));
+  return x;
+}
+
+// lane i of the segment holds element v of the group; every lane of the
+// segment must be active.  Writes the group's words (lane w writes word w)
+// and its meta (lane 0) when `store`; returns the dense code and sets sg (the
+// sign, sym) and s, z (scale; zero point, asym) for the reference outputs.
+template <int G>
+__device__ __forceinline__ int32_t quant_group_lanes(float v, int i, int bits, int mode, bool store, uint32_t* out,
+                                                     uint16_t* meta, int64_t unit, float& sg, float& s, float& z) {
+  const bool nan = (__ballot(is_nan(v)) & seg_mask<G>()) != 0ull;
+  int32_t c;
+  uint32_t fld;
+  if (mode == IQ_MODE_SYM) {
+    float amx = seg_fmax<G>(fabsf(v));
+    if (nan) amx = __builtin_nanf("");
+    s = sym_scale_b(amx, bits);
+    z = 0.f;
+    c = sym_code_b(v, s, bits);
+    sg = sign_of(v);
+    fld = sym_field_b(c, sg, bits);
+  } else {
+    float mn = seg_fmin<G>(v), mx = seg_fmax<G>(v);
+    if (nan) { mn = __builtin_nanf(""); mx = mn; }
+    s = asym_scale_b(mn, mx, bits);
+    z = mn;
+    c = asym_code_b(v, mn, s, bits);
+    sg = 0.f;
+    fld = asym_field_b(c, bits);
+  }
+  const int bit = bits * i, wi = bit >> 5, o = bit & 31;
+  const uint32_t lo = fld << o, hi = o + bits > 32 ? fld >> (32 - o) : 0u;
+  const int W = (G * bits) >> 5;
+#pragma unroll
+  for (int w = 0; w < (G * 4) / 32; ++w) {  // up to 4-bit fields
+    const uint32_t word = seg_or<G>((wi == w ? lo : 0u) | (wi + 1 == w ? hi : 0u));
+    if (store && w < W && i == w) out[w] = word;
+  }
+  if (store && i == 0) {
+    if (mode == IQ_MODE_SYM) meta[unit] = __half_as_ushort(__float2half_rn(s));
+    else reinterpret_cast<uint32_t*>(meta)[unit] = meta_word(s, z);
+  }
+  return c;
+}
+
+// ---- K, small calls (a decode step's tokens): one lane per value ------------
+// quant_group_lanes over G <= 64 lanes, asym or sym; the same stores and
+// reference-format outputs as quant_k_kernel.
+template <int G>
+__global__ __launch_bounds__(256) void quant_k_lane_kernel(const uint16_t* __restrict__ x, int64_t sxb,
+                                                           int64_t sxh, int64_t sxt,
+                                                           const uint16_t* __restrict__ norm, int B, int H, int n,
+                                                           int D, int bits, int mode, QuantOut o) {
+  const int ng = D / G;
+  const int64_t e = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  const int64_t gid = e / G;
+  const int i = int(e % G);
+  if (gid >= int64_t(B) * H * n * ng) return;  // whole G-lane segments
+  const int g = int(gid % ng);
+  int64_t r = gid / ng;
+  const int t = int(r % n);
+  r /= n;
+  const int h = int(r % H);
+  const int b = int(r / H);
+  const int64_t bh = int64_t(b) * H + h;
+  float v = h2f(x[b * sxb + h * sxh + t * sxt + g * G + i]);
+  if (norm) v = round_f16(v / h2f(norm[bh * D + g * G + i]));  // cache.py:125
+  const int64_t tt = o.t_off + t;
+  const int64_t unit = ((bh * o.cap_units + tt / TOKEN_BLOCK) * ng + g) * TOKEN_BLOCK + tt % TOKEN_BLOCK;
+  float sg, sc, zp;
+  const int32_t c = quant_group_lanes<G>(v, i, bits, mode, o.codes != nullptr,
+                                         o.codes ? o.codes + unit * ((G * bits) >> 5) : nullptr, o.meta, unit, sg,
+                                         sc, zp);
+  const int64_t row_el = (bh * n + t) * D + g * G;
+  if (o.codes_i32) o.codes_i32[row_el + i] = c;
+  if (o.signs16) o.signs16[row_el + i] = __half_as_ushort(__float2half_rn(sg));
+  if (i == 0) {
+    const int64_t red = (bh * n + t) * ng + g;
+    if (o.scale16) o.scale16[red] = __half_as_ushort(__float2half_rn(sc));
+    if (o.zero16) o.zero16[red] = __half_as_ushort(__float2half_rn(zp));
   }
 }
 
@@ -687,6 +807,45 @@ __device__ __forceinline__ void append_group(const WinRole& r, int H, int D, int
   quant_group_rt<G>(v, r.bits, r.mode, r.codes + unit * ((G * r.bits) >> 5), r.meta, unit);
 }
 
+// append_group with one lane per element (G <= 64, asym or sym): item q of
+// the role's groups, element i
+template <int G>
+__device__ __forceinline__ void append_group_lanes(const WinRole& r, int H, int D, int64_t q, int i) {
+  int64_t bh, unit;
+  int f, d;
+  if (r.axis == 0) {
+    const int ng = D / G;
+    const int g = int(q % ng);
+    const int64_t rest = q / ng;
+    f = int(rest % r.F);
+    bh = rest / r.F;
+    const int64_t tt = r.t_off + f;
+    unit = ((bh * r.cap_units + (tt >> 6)) * ng + g) * TOKEN_BLOCK + (tt & 63);
+    d = g * G + i;
+  } else {
+    d = int(q % D);
+    const int64_t rest = q / D;
+    const int ngf = r.F / G;
+    const int gi = int(rest % ngf);
+    bh = rest / ngf;
+    unit = (bh * r.cap_units + r.t_off / G + gi) * D + d;
+    f = gi * G + i;
+  }
+  const int64_t b = bh / H, h = bh % H;
+  const uint16_t* p = f < r.n ? r.buf + b * r.sb + h * r.sh + int64_t(r.start + f) * r.st + d
+                              : r.x + b * r.sxb + h * r.sxh + int64_t(f - r.n) * r.sxt + d;
+  float v = h2f(*p);
+  if (r.norm) v = round_f16(v / h2f(r.norm[bh * D + d]));  // cache.py:125
+  float sg, sc, zp;
+  quant_group_lanes<G>(v, i, r.bits, r.mode, true, r.codes + unit * ((G * r.bits) >> 5), r.meta, unit, sg, sc, zp);
+}
+
+// lanes per group item of a role: one lane per element where quant_group_lanes
+// applies, else one thread per group
+__host__ __device__ inline int role_lanes(int group, int mode) {
+  return group <= 64 && mode != IQ_MODE_HYBRID ? group : 1;
+}
+
 // element e of the new tokens (b, h, j, d) into the window buffer
 __device__ __forceinline__ void window_copy(const WinRole& r, int H, int D, int64_t e) {
   const int64_t per_bh = int64_t(r.m) * D;
@@ -704,10 +863,27 @@ __global__ __launch_bounds__(256) void window_append_kernel(AppendArgs a) {
   const int64_t e = i - a.start[k];
   if (e >= a.count[k]) return;
   // (block-uniform k: each role's fields are read with a constant index)
+  // (a group role's items are whole aligned G-lane segments, so a segment is
+  // either all past the count or all active)
   if (k == 0) window_copy(a.r[0], a.H, a.D, e);
   else if (k == 1) window_copy(a.r[1], a.H, a.D, e);
-  else if (k == 2) append_group<GK>(a.r[0], a.H, a.D, e);
-  else append_group<GV>(a.r[1], a.H, a.D, e);
+  else if (k == 2) {
+    if constexpr (GK <= 64) {
+      if (role_lanes(GK, a.r[0].mode) > 1) {
+        append_group_lanes<GK>(a.r[0], a.H, a.D, e / GK, int(e % GK));
+        return;
+      }
+    }
+    append_group<GK>(a.r[0], a.H, a.D, e);
+  } else {
+    if constexpr (GV <= 64) {
+      if (role_lanes(GV, a.r[1].mode) > 1) {
+        append_group_lanes<GV>(a.r[1], a.H, a.D, e / GV, int(e % GV));
+        return;
+      }
+    }
+    append_group<GV>(a.r[1], a.H, a.D, e);
+  }
 }
 
 }  // namespace
@@ -782,6 +958,15 @@ int iq_quantize_k(const void* x, int64_t sx_b, int64_t sx_h, int64_t sx_t, const
   QuantOut o{k_codes, k_meta, t_cap / TOKEN_BLOCK, t_off, codes_i32, (uint16_t*)scale16, (uint16_t*)zero16,
              (uint16_t*)signs16};
   const int sym = mode == IQ_MODE_SYM;
+  // a call of few groups (a decode step's tokens) takes one lane per value:
+  // one thread per group would leave most of the device idle on long chains
+  if (mode != IQ_MODE_HYBRID && group <= 64 && total <= LANE_MAX_GROUPS) {
+    const int64_t lanes = total * group;
+    auto* kern = group == 64 ? quant_k_lane_kernel<64> : quant_k_lane_kernel<32>;
+    kern<<<dim3(unsigned(ceil_div(lanes, 256))), 256, 0, (hipStream_t)stream>>>(
+        (const uint16_t*)x, sx_b, sx_h, sx_t, (const uint16_t*)norm, B, H, n, D, bits, mode, o);
+    return launch_status();
+  }
   return dispatch_store_bits_group(bits, group, [&]<int BITS, int G>() {
     // the store-only append (no reference-format outputs) drops their registers
     auto* kern = mode == IQ_MODE_HYBRID ? quant_k_kernel<BITS, G, false, true>
@@ -934,7 +1119,8 @@ int iq_window_append(const iq_window* k, const iq_window* v, int B, int H, int D
   for (int r = 0; r < 2; ++r) {
     const WinRole& w = a.r[r];
     a.count[r] = bh * w.m * D;
-    a.count[2 + r] = w.F == 0 ? 0 : (w.axis == 0 ? bh * w.F * (D / w.group) : bh * (w.F / w.group) * D);
+    a.count[2 + r] = w.F == 0 ? 0 : (w.axis == 0 ? bh * w.F * (D / w.group) : bh * (w.F / w.group) * D) *
+                                        role_lanes(w.group, w.mode);
   }
   int64_t at = 0;
   for (int s = 0; s < 4; ++s) {
