@@ -52,7 +52,7 @@
 extern "C" {
 #endif
 
-#define IQ_ABI_VERSION 1
+#define IQ_ABI_VERSION 2
 #define IQ_TOKEN_BLOCK 64
 
 enum iq_status {
@@ -68,7 +68,19 @@ enum iq_status {
   IQ_ERR_HIP = -9         /* a HIP launch failed */
 };
 
-enum iq_mode { IQ_MODE_ASYM = 0, IQ_MODE_SYM = 1, IQ_MODE_HYBRID = 2 };
+enum iq_mode {
+  IQ_MODE_ASYM = 0,
+  IQ_MODE_SYM = 1,
+  IQ_MODE_HYBRID = 2,
+  /* OR-ed into the mode of a quantize, dequantize, unpack or window-append
+   * call (and of a store written that way): the activations - inputs, scales,
+   * zero points, signs, 16-bit outputs - are bf16 instead of fp16, and every
+   * rounding of the reference's ops is to bf16, as quant.py computes on a
+   * bf16 model's tensors (LongBench/pred.py:240 loads the model in bf16).
+   * The decode GEMVs and decode attention take fp16 only and refuse a
+   * flagged store with IQ_ERR_MODE. */
+  IQ_MODE_BF16 = 0x100
+};
 
 /* ABI version (IQ_ABI_VERSION) and error names. */
 int iq_abi_version(void);
@@ -156,9 +168,11 @@ int iq_unpack_v(const uint32_t* v_codes, const uint16_t* v_meta, int64_t t_cap, 
 
 /* Key normalization factor out16[b,h,d] = fp16(sqrt(max_t |k[b,h,t,d]|)) over
  * T tokens of k (fp16, element strides sk_b, sk_h, sk_t; D contiguous).
- * Replaces key_states.abs().max(dim=-2).values.sqrt() (cache.py:121-126). */
+ * mode: 0, or IQ_MODE_BF16 for bf16 k and out16 (any other bit:
+ * IQ_ERR_MODE).  Replaces key_states.abs().max(dim=-2).values.sqrt()
+ * (cache.py:121-126). */
 int iq_key_norm_factor(const void* k, int64_t sk_b, int64_t sk_h, int64_t sk_t, int B, int H, int T, int D,
-                       void* out16, void* stream);
+                       int mode, void* out16, void* stream);
 
 /* Hybrid quantization (quant.py:133-176): per group, mask = L1 error of the
  * asym dequantization > L1 error of the sym one, i.e. use the sym codes.
@@ -169,10 +183,10 @@ int iq_key_norm_factor(const void* k, int64_t sk_b, int64_t sk_h, int64_t sk_t, 
  * Error sums are accumulated in fp64 (the reference sums fp32 in torch's
  * reduction order; exact ties may resolve differently). */
 int iq_hybrid_mask(const void* x16, const void* norm16, const float* deq_a, const float* deq_s, int64_t BH, int T,
-                   int D, int group, int axis, uint8_t* mask, void* stream);
+                   int D, int group, int axis, int mode, uint8_t* mask, void* stream);  /* mode: 0 or IQ_MODE_BF16 */
 
 /* out = mask ? deq_s : deq_a elementwise over [BH,T,D] (mask as produced by
- * iq_hybrid_mask), written as fp32 (out_f16 = 0) or fp16 (out_f16 = 1).
+ * iq_hybrid_mask), written as fp32 (out_f16 = 0), fp16 (1) or bf16 (2).
  * Replaces the torch.where of dequantize_hybrid (quant.py:153-176). */
 int iq_hybrid_select(const float* deq_a, const float* deq_s, const uint8_t* mask, int64_t BH, int T, int D, int group,
                      int axis, int out_f16, void* out, void* stream);

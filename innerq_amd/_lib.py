@@ -15,6 +15,8 @@ IQ_OK = 0
 IQ_MODE_ASYM = 0
 IQ_MODE_SYM = 1
 IQ_MODE_HYBRID = 2
+IQ_MODE_BF16 = 0x100  # OR-ed into a mode: bf16 activations
+ABI_VERSION = 2
 TOKEN_BLOCK = 64
 
 STATUS = {
@@ -77,8 +79,8 @@ SIGNATURES = {
     "iq_dequant_dense": (I, [P, P, P, L, L, L, I, I, I, P, P]),
     "iq_unpack_k": (I, [P, P, L, I, I, I, I, I, I, I, I, P, P, P, P]),
     "iq_unpack_v": (I, [P, P, L, I, I, I, I, I, I, I, I, P, P, P, P]),
-    "iq_key_norm_factor": (I, [P, L, L, L, I, I, I, I, P, P]),
-    "iq_hybrid_mask": (I, [P, P, P, P, L, I, I, I, I, P, P]),
+    "iq_key_norm_factor": (I, [P, L, L, L, I, I, I, I, I, P, P]),
+    "iq_hybrid_mask": (I, [P, P, P, P, L, I, I, I, I, I, P, P]),
     "iq_hybrid_select": (I, [P, P, P, L, I, I, I, I, I, P, P]),
     "iq_qk_gemv": (I, [P, L, L, P, P, P, L, I, I, I, I, I, I, I, I, I, F, P, L, L, P, S, P]),
     "iq_qk_workspace_bytes": (S, [I, I, I]),
@@ -114,7 +116,7 @@ def lib() -> ctypes.CDLL:
                     f = getattr(h, name)
                     f.restype = res
                     f.argtypes = args
-                if h.iq_abi_version() != 1:
+                if h.iq_abi_version() != ABI_VERSION:
                     raise RuntimeError("libinnerq_hip.so ABI version mismatch")
                 _lib = h
     return _lib

@@ -45,7 +45,7 @@ class _Quantized:
     def __init__(self, axis: str, like: torch.Tensor, group: int, bits: int, mode: QMode):
         B, H, _, D = like.shape
         self.axis, self.group, self.bits, self.mode = axis, group, bits, mode
-        self.store = ops.PackedStore(axis, B, H, D, group, bits, mode.value, like.device)
+        self.store = ops.PackedStore(axis, B, H, D, group, bits, mode.value, like.device, dtype=like.dtype)
 
     @property
     def length(self) -> int:
@@ -58,7 +58,8 @@ class _Quantized:
         self.store.append(x, norm=norm)
 
     def dequant_into(self, out: torch.Tensor, norm: Optional[torch.Tensor]) -> None:
-        """Dense values (times norm) of every packed token, written into the fp16 view ``out``."""
+        """Dense values (times norm) of every packed token, written into the view ``out`` (the
+        activation dtype or fp32)."""
         self.store.dequant(0, self.length, out=out, norm=norm)
 
     def reference_tensors(self):
@@ -238,8 +239,8 @@ class InnerqDynamicLayer(CacheLayerMixin):
             self._quantize_values(value_states)
 
     def lazy_initialization(self, key_states: torch.Tensor, value_states: torch.Tensor) -> None:
-        ops.require_device(key_states, "key_states")
-        ops.require_device(value_states, "value_states")
+        ops.require_act(key_states, "key_states")
+        ops.require_act(value_states, "value_states", key_states.dtype)
         self.dtype, self.device = key_states.dtype, key_states.device
         key_states = self.initialize_keys_sink(key_states)
         value_states = self.initialize_values_sink(value_states)
@@ -339,7 +340,9 @@ class InnerqDynamicLayer(CacheLayerMixin):
 
     def _fused_refusal(self) -> Optional[str]:
         """Why attend() cannot read this layer's stores (None if it can): K must be
-        grouped along head_dim (asym or sym), V along tokens (asym, sym or hybrid)."""
+        grouped along head_dim (asym or sym), V along tokens (asym, sym or hybrid), fp16."""
+        if self.dtype != torch.float16:
+            return "fused decode takes fp16 activations (bf16 layers take the dequantize-then-attend path)"
         if self._kq is not None and (self._kq.axis != "channel" or self._kq.mode == QMode.HYBRID):
             return "fused decode reads keys grouped along the head_dim axis, asym or sym"
         if self._vq is not None and self._vq.axis != "token":

@@ -9,10 +9,11 @@ using namespace iq;
 namespace {
 
 // out[bh, d] = fp16(sqrt(max_t |k[bh, t, d]|)): cache.py:121-126 computes
-// key_states.abs().max(dim=-2).values.sqrt() in fp16, i.e. the correctly
-// rounded fp32 square root of an fp16 value, rounded to fp16.
+// key_states.abs().max(dim=-2).values.sqrt() in the activation dtype, i.e.
+// the correctly rounded fp32 square root of an fp16 (bf16) value, rounded to
+// fp16 (bf16).
 __global__ __launch_bounds__(256) void key_norm_kernel(const uint16_t* __restrict__ k, int64_t skb, int64_t skh,
-                                                       int64_t skt, int H, int T, int D, int64_t n,
+                                                       int64_t skt, int H, int T, int D, int64_t n, int bf,
                                                        uint16_t* __restrict__ out) {
   const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= n) return;
@@ -20,8 +21,8 @@ __global__ __launch_bounds__(256) void key_norm_kernel(const uint16_t* __restric
   const int64_t bh = i / D;
   const uint16_t* p = k + (bh / H) * skb + (bh % H) * skh + d;
   float mx = 0.f;
-  for (int t = 0; t < T; ++t) mx = fmaxf(mx, fabsf(h2f(p[int64_t(t) * skt])));
-  out[i] = __half_as_ushort(__float2half_rn(__fsqrt_rn(mx)));
+  for (int t = 0; t < T; ++t) mx = fmaxf(mx, fabsf(act2f(p[int64_t(t) * skt], bf != 0)));
+  out[i] = f2act(__fsqrt_rn(mx), bf != 0);
 }
 
 // Hybrid selection mask (quant.py:133-151): per group, the L1 error of the
@@ -34,7 +35,7 @@ __global__ __launch_bounds__(256) void key_norm_kernel(const uint16_t* __restric
 __global__ __launch_bounds__(256) void hybrid_mask_kernel(const uint16_t* __restrict__ x,
                                                           const uint16_t* __restrict__ norm,
                                                           const float* __restrict__ da, const float* __restrict__ ds,
-                                                          int T, int D, int group, int axis, int64_t n,
+                                                          int T, int D, int group, int axis, int64_t n, int bf,
                                                           uint8_t* __restrict__ mask) {
   const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= n) return;
@@ -60,15 +61,16 @@ __global__ __launch_bounds__(256) void hybrid_mask_kernel(const uint16_t* __rest
   double ea = 0.0, es = 0.0;
   for (int j = 0; j < group; ++j) {
     const int64_t e = e0 + j * step;
-    float v = h2f(x[e]);
-    if (norm) v = round_f16(v / h2f(norm[bh * D + dcol + (axis == 0 ? j : 0)]));
+    float v = act2f(x[e], bf != 0);
+    if (norm) v = round_act(v / act2f(norm[bh * D + dcol + (axis == 0 ? j : 0)], bf != 0), bf != 0);
     ea += double(fabsf(__fsub_rn(da[e], v)));
     es += double(fabsf(__fsub_rn(ds[e], v)));
   }
   mask[i] = ea > es ? 1 : 0;
 }
 
-// out = mask ? deq_s : deq_a (quant.py:153-176 dequantize_hybrid), fp32 or fp16.
+// out = mask ? deq_s : deq_a (quant.py:153-176 dequantize_hybrid), fp32, fp16
+// (out_f16 = 1) or bf16 (out_f16 = 2).
 __global__ __launch_bounds__(256) void hybrid_select_kernel(const float* __restrict__ da,
                                                             const float* __restrict__ ds,
                                                             const uint8_t* __restrict__ mask, int T, int D,
@@ -87,7 +89,7 @@ __global__ __launch_bounds__(256) void hybrid_select_kernel(const float* __restr
     mi = (bh * (T / group) + t / group) * D + d;
   }
   const float v = mask[mi] ? ds[e] : da[e];
-  if (out_f16) static_cast<uint16_t*>(out)[e] = __half_as_ushort(__float2half_rn(v));
+  if (out_f16) static_cast<uint16_t*>(out)[e] = f2act(v, out_f16 == 2);
   else static_cast<float*>(out)[e] = v;
 }
 
@@ -103,35 +105,38 @@ int check_hybrid(int64_t BH, int T, int D, int group, int axis) {
 extern "C" {
 
 int iq_key_norm_factor(const void* k, int64_t sk_b, int64_t sk_h, int64_t sk_t, int B, int H, int T, int D,
-                       void* out16, void* stream) {
+                       int mode, void* out16, void* stream) {
   IQ_CHECK(k && out16, IQ_ERR_NULL);
+  IQ_CHECK(base_mode(mode) == 0, IQ_ERR_MODE);  // only the dtype flag
   IQ_CHECK(B >= 0 && H >= 0 && T > 0 && D > 0, IQ_ERR_SHAPE);
   const int64_t n = int64_t(B) * H * D;
   if (n == 0) return IQ_OK;
   key_norm_kernel<<<dim3(unsigned(ceil_div(n, 256))), 256, 0, (hipStream_t)stream>>>(
-      (const uint16_t*)k, sk_b, sk_h, sk_t, H, T, D, n, (uint16_t*)out16);
+      (const uint16_t*)k, sk_b, sk_h, sk_t, H, T, D, n, act_bf16(mode) ? 1 : 0, (uint16_t*)out16);
   return launch_status();
 }
 
 int iq_hybrid_mask(const void* x16, const void* norm16, const float* deq_a, const float* deq_s, int64_t BH, int T,
-                   int D, int group, int axis, uint8_t* mask, void* stream) {
+                   int D, int group, int axis, int mode, uint8_t* mask, void* stream) {
   IQ_CHECK(x16 && deq_a && deq_s && mask, IQ_ERR_NULL);
+  IQ_CHECK(base_mode(mode) == 0, IQ_ERR_MODE);  // only the dtype flag
   if (int e = check_hybrid(BH, T, D, group, axis)) return e;
   const int64_t n = axis == 0 ? BH * T * (D / group) : BH * (T / group) * D;
   if (n == 0) return IQ_OK;
   hybrid_mask_kernel<<<dim3(unsigned(ceil_div(n, 256))), 256, 0, (hipStream_t)stream>>>(
-      (const uint16_t*)x16, (const uint16_t*)norm16, deq_a, deq_s, T, D, group, axis, n, mask);
+      (const uint16_t*)x16, (const uint16_t*)norm16, deq_a, deq_s, T, D, group, axis, n, act_bf16(mode) ? 1 : 0, mask);
   return launch_status();
 }
 
 int iq_hybrid_select(const float* deq_a, const float* deq_s, const uint8_t* mask, int64_t BH, int T, int D, int group,
                      int axis, int out_f16, void* out, void* stream) {
   IQ_CHECK(deq_a && deq_s && mask && out, IQ_ERR_NULL);
+  IQ_CHECK(out_f16 >= 0 && out_f16 <= 2, IQ_ERR_SHAPE);
   if (int e = check_hybrid(BH, T, D, group, axis)) return e;
   const int64_t n = BH * T * int64_t(D);
   if (n == 0) return IQ_OK;
   hybrid_select_kernel<<<dim3(unsigned(ceil_div(n, 256))), 256, 0, (hipStream_t)stream>>>(
-      deq_a, deq_s, mask, T, D, group, axis, n, out_f16 ? 1 : 0, out);
+      deq_a, deq_s, mask, T, D, group, axis, n, out_f16, out);
   return launch_status();
 }
 

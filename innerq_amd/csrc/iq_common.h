@@ -13,6 +13,11 @@ namespace iq {
 inline bool bits_ok(int bits) { return bits == 2 || bits == 3 || bits == 4; }
 inline bool group_ok(int g) { return g == 32 || g == 64 || g == 128; }
 inline bool mode_ok(int m) { return m == IQ_MODE_ASYM || m == IQ_MODE_SYM; }
+// a mode argument's activation flag: bf16 instead of fp16 inputs, scales,
+// zero points, signs and outputs (entry points that take it strip it first;
+// everywhere else a flagged mode fails mode_ok)
+inline bool act_bf16(int m) { return (m & IQ_MODE_BF16) != 0; }
+inline int base_mode(int m) { return m & ~int(IQ_MODE_BF16); }
 inline bool store_mode_ok(int m) { return mode_ok(m) || m == IQ_MODE_HYBRID; }
 inline bool d_ok(int d) { return d == 64 || d == 128; }
 inline bool nrep_ok(int r) { return r == 1 || r == 2 || r == 4 || r == 8; }

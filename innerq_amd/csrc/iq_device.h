@@ -196,19 +196,38 @@ __device__ __forceinline__ float round_f16(float x) {
   return __half2float(__float2half_rn(x));
 }
 
+// bf16 activations (IQ_MODE_BF16): the same ops with bf16 in place of fp16
+// at every rounding and storage point, as torch computes bf16 tensor ops (in
+// fp32, rounded to nearest even; NaN becomes 0x7fc0).
+__device__ __forceinline__ float bf2f(uint16_t bits) { return __uint_as_float(uint32_t(bits) << 16); }
+__device__ __forceinline__ uint16_t f2bf(float x) {
+  const uint32_t u = __float_as_uint(x);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
+  return uint16_t((u + 0x7fffu + ((u >> 16) & 1u)) >> 16);
+}
+// the activation dtype's value of 16 stored bits, rounding, and bits
+__device__ __forceinline__ float act2f(uint16_t bits, bool bf) { return bf ? bf2f(bits) : h2f(bits); }
+__device__ __forceinline__ float round_act(float x, bool bf) { return bf ? bf2f(f2bf(x)) : round_f16(x); }
+__device__ __forceinline__ uint16_t f2act(float x, bool bf) {
+  return bf ? f2bf(x) : __half_as_ushort(__float2half_rn(x));
+}
+
 // Hybrid stores: a group's meta dword is {scale | flag << 15, zero}; the flag
 // (bit 15, tested as a bit: a -0.0 scale is flagged) marks b-bit sym codes in
-// offset binary, else the field holds the (b-1)-bit asym code.
+// offset binary, else the field holds the (b-1)-bit asym code.  (bf16 and fp16
+// both keep their sign in bit 15.)
 constexpr uint32_t HYB_FLAG = 0x8000u;
 __device__ __forceinline__ bool hyb_sym(uint32_t mw) { return (mw & HYB_FLAG) != 0u; }
-__device__ __forceinline__ float hyb_scale(uint32_t mw) { return h2f(uint16_t(mw & 0x7fffu)); }
+__device__ __forceinline__ float hyb_scale(uint32_t mw, bool bf = false) {
+  return act2f(uint16_t(mw & 0x7fffu), bf);
+}
 
 // the reference's value of one field of a hybrid group (quant.py:153-176):
 // asym u*s + z (fp32, c*s exact), sym (u - 2^(b-1))*s (exact)
-__device__ __forceinline__ float hyb_value(uint32_t u, int bits, uint32_t mw) {
-  const float s = hyb_scale(mw);
+__device__ __forceinline__ float hyb_value(uint32_t u, int bits, uint32_t mw, bool bf = false) {
+  const float s = hyb_scale(mw, bf);
   if (hyb_sym(mw)) return __fmul_rn(float(int(u) - (1 << (bits - 1))), s);
-  return __fadd_rn(__fmul_rn(float(u), s), h2f(uint16_t(mw >> 16)));
+  return __fadd_rn(__fmul_rn(float(u), s), act2f(uint16_t(mw >> 16), bf));
 }
 
 // ---------------------------------------------------------------------------

@@ -48,22 +48,22 @@ __device__ __forceinline__ int32_t code_of(float y, float L) {
   return (int32_t)rintf(y);
 }
 
-// Group statistics and per-element codes of the two quantizers, one fp16
-// rounding per reference op (runtime bit width; the templates below pass a
-// constant).
+// Group statistics and per-element codes of the two quantizers, one rounding
+// to the activation dtype (fp16, or bf16 with bf) per reference op (runtime
+// bit width; the templates below pass a constant).
 // asym (quant.py:66-71): scale of b-bit codes from the group's min and max
-__device__ __forceinline__ float asym_scale_b(float mn, float mx, int bits) {
-  return round_f16(round_f16(mx - mn) / float((1 << bits) - 1));    // quant.py:68
+__device__ __forceinline__ float asym_scale_b(float mn, float mx, int bits, bool bf = false) {
+  return round_act(round_act(mx - mn, bf) / float((1 << bits) - 1), bf);    // quant.py:68
 }
-__device__ __forceinline__ int32_t asym_code_b(float x, float mn, float s, int bits) {
-  return code_of(round_f16(round_f16(x - mn) / s), float((1 << bits) - 1));  // quant.py:69-71
+__device__ __forceinline__ int32_t asym_code_b(float x, float mn, float s, int bits, bool bf = false) {
+  return code_of(round_act(round_act(x - mn, bf) / s, bf), float((1 << bits) - 1));  // quant.py:69-71
 }
 // sym (quant.py:104-109): scale of b-bit codes (one bit is the sign)
-__device__ __forceinline__ float sym_scale_b(float mx, int bits) {
-  return round_f16(mx / float((1 << (bits - 1)) - 1));              // quant.py:107
+__device__ __forceinline__ float sym_scale_b(float mx, int bits, bool bf = false) {
+  return round_act(mx / float((1 << (bits - 1)) - 1), bf);              // quant.py:107
 }
-__device__ __forceinline__ int32_t sym_code_b(float x, float s, int bits) {
-  return code_of(round_f16(fabsf(x) / s), float((1 << (bits - 1)) - 1));  // quant.py:108-109
+__device__ __forceinline__ int32_t sym_code_b(float x, float s, int bits, bool bf = false) {
+  return code_of(round_act(fabsf(x) / s, bf), float((1 << (bits - 1)) - 1));  // quant.py:108-109
 }
 __device__ __forceinline__ float sign_of(float x) { return x > 0.f ? 1.f : (x < 0.f ? -1.f : 0.f); }  // torch.sign
 // stored fields: the asym code (0 for NaN); sym sign*magnitude + 2^(b-1)
@@ -201,8 +201,8 @@ __device__ __forceinline__ void store_group(const QuantOut& o, int64_t unit, con
   else reinterpret_cast<uint32_t*>(o.meta)[unit] = mw;
 }
 
-__device__ __forceinline__ uint32_t meta_word(float s, float z) {
-  return uint32_t(__half_as_ushort(__float2half_rn(s))) | (uint32_t(__half_as_ushort(__float2half_rn(z))) << 16);
+__device__ __forceinline__ uint32_t meta_word(float s, float z, bool bf = false) {
+  return uint32_t(f2act(s, bf)) | (uint32_t(f2act(z, bf)) << 16);
 }
 
 template <int BITS, int G>
@@ -301,8 +301,12 @@ __global__ __launch_bounds__(256) void quant_k_kernel(const uint16_t* __restrict
 // only: hybrid's error sums keep the one-thread-per-group order.
 template <int G>
 __device__ __forceinline__ uint64_t seg_mask() {
-  const int lane = threadIdx.x & 63;
-  return G == 64 ? ~0ull : ((1ull << G) - 1ull) << (lane & ~(G - 1));
+  if constexpr (G == 64) {
+    return ~0ull;
+  } else {
+    const int lane = threadIdx.x & 63;
+    return ((1ull << G) - 1ull) << (lane & ~(G - 1));
+  }
 }
 template <int G>
 __device__ __forceinline__ float seg_fmin(float x) {
@@ -328,25 +332,26 @@ __device__ __forceinline__ uint32_t seg_or(uint32_t x) {
 // and its meta (lane 0) when `store`; returns the dense code and sets sg (the
 // sign, sym) and s, z (scale; zero point, asym) for the reference outputs.
 template <int G>
-__device__ __forceinline__ int32_t quant_group_lanes(float v, int i, int bits, int mode, bool store, uint32_t* out,
-                                                     uint16_t* meta, int64_t unit, float& sg, float& s, float& z) {
+__device__ __forceinline__ int32_t quant_group_lanes(float v, int i, int bits, int mode, bool bf, bool store,
+                                                     uint32_t* out, uint16_t* meta, int64_t unit, float& sg, float& s,
+                                                     float& z) {
   const bool nan = (__ballot(is_nan(v)) & seg_mask<G>()) != 0ull;
   int32_t c;
   uint32_t fld;
   if (mode == IQ_MODE_SYM) {
     float amx = seg_fmax<G>(fabsf(v));
     if (nan) amx = __builtin_nanf("");
-    s = sym_scale_b(amx, bits);
+    s = sym_scale_b(amx, bits, bf);
     z = 0.f;
-    c = sym_code_b(v, s, bits);
+    c = sym_code_b(v, s, bits, bf);
     sg = sign_of(v);
     fld = sym_field_b(c, sg, bits);
   } else {
     float mn = seg_fmin<G>(v), mx = seg_fmax<G>(v);
     if (nan) { mn = __builtin_nanf(""); mx = mn; }
-    s = asym_scale_b(mn, mx, bits);
+    s = asym_scale_b(mn, mx, bits, bf);
     z = mn;
-    c = asym_code_b(v, mn, s, bits);
+    c = asym_code_b(v, mn, s, bits, bf);
     sg = 0.f;
     fld = asym_field_b(c, bits);
   }
@@ -359,48 +364,212 @@ __device__ __forceinline__ int32_t quant_group_lanes(float v, int i, int bits, i
     if (store && w < W && i == w) out[w] = word;
   }
   if (store && i == 0) {
-    if (mode == IQ_MODE_SYM) meta[unit] = __half_as_ushort(__float2half_rn(s));
-    else reinterpret_cast<uint32_t*>(meta)[unit] = meta_word(s, z);
+    if (mode == IQ_MODE_SYM) meta[unit] = f2act(s, bf);
+    else reinterpret_cast<uint32_t*>(meta)[unit] = meta_word(s, z, bf);
   }
   return c;
 }
 
-// ---- K, small calls (a decode step's tokens): one lane per value ------------
-// quant_group_lanes over G <= 64 lanes, asym or sym; the same stores and
-// reference-format outputs as quant_k_kernel.
+// ---- one lane per value (quant_group_lanes), either axis -------------------
+// G <= 64, asym or sym, fp16 or bf16 activations; the same stores and
+// reference-format outputs as quant_k_kernel (axis 0, groups along D) and
+// quant_v_kernel (axis 1, groups along tokens).  Serves small K calls (a
+// decode step's tokens, where one thread per group would idle the device)
+// and every bf16 quantization of those formats.
+struct LaneArgs {
+  const uint16_t* x;
+  int64_t sxb, sxh, sxt;
+  const uint16_t* norm;  // axis 0 only
+  int B, H, n, D, bits, mode, bf, axis;
+};
 template <int G>
-__global__ __launch_bounds__(256) void quant_k_lane_kernel(const uint16_t* __restrict__ x, int64_t sxb,
-                                                           int64_t sxh, int64_t sxt,
-                                                           const uint16_t* __restrict__ norm, int B, int H, int n,
-                                                           int D, int bits, int mode, QuantOut o) {
-  const int ng = D / G;
+__global__ __launch_bounds__(256) void quant_lane_kernel(LaneArgs a, QuantOut o) {
   const int64_t e = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   const int64_t gid = e / G;
   const int i = int(e % G);
-  if (gid >= int64_t(B) * H * n * ng) return;  // whole G-lane segments
-  const int g = int(gid % ng);
-  int64_t r = gid / ng;
-  const int t = int(r % n);
-  r /= n;
-  const int h = int(r % H);
-  const int b = int(r / H);
-  const int64_t bh = int64_t(b) * H + h;
-  float v = h2f(x[b * sxb + h * sxh + t * sxt + g * G + i]);
-  if (norm) v = round_f16(v / h2f(norm[bh * D + g * G + i]));  // cache.py:125
-  const int64_t tt = o.t_off + t;
-  const int64_t unit = ((bh * o.cap_units + tt / TOKEN_BLOCK) * ng + g) * TOKEN_BLOCK + tt % TOKEN_BLOCK;
-  float sg, sc, zp;
-  const int32_t c = quant_group_lanes<G>(v, i, bits, mode, o.codes != nullptr,
-                                         o.codes ? o.codes + unit * ((G * bits) >> 5) : nullptr, o.meta, unit, sg,
-                                         sc, zp);
-  const int64_t row_el = (bh * n + t) * D + g * G;
-  if (o.codes_i32) o.codes_i32[row_el + i] = c;
-  if (o.signs16) o.signs16[row_el + i] = __half_as_ushort(__float2half_rn(sg));
-  if (i == 0) {
-    const int64_t red = (bh * n + t) * ng + g;
-    if (o.scale16) o.scale16[red] = __half_as_ushort(__float2half_rn(sc));
-    if (o.zero16) o.zero16[red] = __half_as_ushort(__float2half_rn(zp));
+  const bool bf = a.bf != 0;
+  int64_t bh, unit, xoff, el, red, row_el = 0;
+  int dcol;
+  if (a.axis == 0) {
+    const int ng = a.D / G;
+    if (gid >= int64_t(a.B) * a.H * a.n * ng) return;  // whole G-lane segments
+    const int g = int(gid % ng);
+    const int64_t row = gid / ng;  // bh * n + t
+    const int t = int(row % a.n);
+    bh = row / a.n;
+    dcol = g * G + i;
+    xoff = (bh / a.H) * a.sxb + (bh % a.H) * a.sxh + t * a.sxt + dcol;
+    const int64_t tt = o.t_off + t;
+    unit = ((bh * o.cap_units + tt / TOKEN_BLOCK) * ng + g) * TOKEN_BLOCK + tt % TOKEN_BLOCK;
+    row_el = row * a.D + g * G;
+    el = row_el + i;
+    red = row * ng + g;
+  } else {
+    const int ngn = a.n / G;
+    if (gid >= int64_t(a.B) * a.H * ngn * a.D) return;
+    const int d = int(gid % a.D);
+    const int64_t r = gid / a.D;  // bh * ngn + gi
+    const int gi = int(r % ngn);
+    bh = r / ngn;
+    dcol = d;
+    const int t = gi * G + i;
+    xoff = (bh / a.H) * a.sxb + (bh % a.H) * a.sxh + int64_t(t) * a.sxt + d;
+    unit = (bh * o.cap_units + o.t_off / G + gi) * a.D + d;
+    el = (bh * a.n + t) * a.D + d;
+    red = r * a.D + d;
   }
+  float v = act2f(a.x[xoff], bf);
+  if (a.norm) v = round_act(v / act2f(a.norm[bh * a.D + dcol], bf), bf);  // cache.py:125
+  float sg, sc, zp;
+  const int32_t c = quant_group_lanes<G>(v, i, a.bits, a.mode, bf, o.codes != nullptr,
+                                         o.codes ? o.codes + unit * ((G * a.bits) >> 5) : nullptr, o.meta, unit, sg,
+                                         sc, zp);
+  if (o.codes_i32) o.codes_i32[el] = c;
+  if (o.signs16) o.signs16[el] = f2act(sg, bf);
+  if (i == 0) {
+    if (o.scale16) o.scale16[red] = f2act(sc, bf);
+    if (o.zero16) o.zero16[red] = f2act(zp, bf);
+  }
+}
+
+// One group, quantized as quantize_group / quantize_group_hybrid do, with
+// the bit width, mode and activation dtype known at run time: v[] holds the
+// group's G inputs (registers; loaded together, one memory latency per group),
+// the fields are stored word by word as they fill, the meta word last.
+// Optional reference-format outputs (RtRef, asym or sym): element i's code and
+// sign at codes[el0 + i * el_step], signs[...], the scale and zero at red.
+struct RtRef {
+  int32_t* codes;
+  uint16_t* signs;
+  uint16_t* scale;
+  uint16_t* zero;
+  int64_t el0, el_step, red;
+};
+template <int G>
+__device__ __forceinline__ void quant_group_rt(const float* v, int bits, int mode, bool bf, uint32_t* out,
+                                               uint16_t* meta, int64_t unit, const RtRef* ref = nullptr) {
+  const int abits = mode == IQ_MODE_HYBRID ? bits - 1 : bits;
+  float mn = v[0], mx = v[0], amx = 0.f;
+  bool nan = false;
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    nan |= is_nan(v[i]);
+    mn = fminf(mn, v[i]);
+    mx = fmaxf(mx, v[i]);
+    amx = fmaxf(amx, fabsf(v[i]));
+  }
+  if (nan) { mn = __builtin_nanf(""); mx = mn; amx = mn; }
+  const float sa = asym_scale_b(mn, mx, abits, bf), ss = sym_scale_b(amx, bits, bf);
+  bool sym = mode == IQ_MODE_SYM;
+  if (mode == IQ_MODE_HYBRID) {  // quantize_group_hybrid's choice
+    double ea = 0.0, es = 0.0;
+#pragma unroll
+    for (int i = 0; i < G; ++i) {
+      const float da = __fadd_rn(__fmul_rn(float(asym_code_b(v[i], mn, sa, abits, bf)), sa), mn);
+      const float ds = __fmul_rn(__fmul_rn(float(sym_code_b(v[i], ss, bits, bf)), ss), sign_of(v[i]));
+      ea += double(fabsf(__fsub_rn(da, v[i])));
+      es += double(fabsf(__fsub_rn(ds, v[i])));
+    }
+    sym = ea > es;
+  }
+  uint64_t acc = 0;
+  int pos = 0, wj = 0;
+#pragma unroll
+  for (int i = 0; i < G; ++i) {
+    const int32_t c = sym ? sym_code_b(v[i], ss, bits, bf) : asym_code_b(v[i], mn, sa, abits, bf);
+    const uint32_t fld = sym ? sym_field_b(c, sign_of(v[i]), bits) : asym_field_b(c, bits);
+    if (ref) {
+      if (ref->codes) ref->codes[ref->el0 + i * ref->el_step] = c;
+      if (ref->signs) ref->signs[ref->el0 + i * ref->el_step] = f2act(sign_of(v[i]), bf);
+    }
+    acc |= uint64_t(fld) << pos;
+    pos += bits;
+    if (pos >= 32) {
+      if (out) out[wj] = uint32_t(acc);
+      ++wj;
+      acc >>= 32;
+      pos -= 32;
+    }
+  }
+  if (ref) {
+    if (ref->scale) ref->scale[ref->red] = f2act(sym ? ss : sa, bf);
+    if (ref->zero) ref->zero[ref->red] = f2act(mn, bf);
+  }
+  if (!out) return;
+  if (mode == IQ_MODE_SYM) {
+    meta[unit] = f2act(ss, bf);
+  } else if (mode == IQ_MODE_HYBRID) {
+    const uint32_t sh = f2act(sym ? ss : sa, bf);
+    reinterpret_cast<uint32_t*>(meta)[unit] =
+        sym ? (sh | HYB_FLAG) : ((sh & 0x7fffu) | (uint32_t(f2act(mn, bf)) << 16));
+  } else {
+    reinterpret_cast<uint32_t*>(meta)[unit] = meta_word(sa, mn, bf);
+  }
+}
+
+// ---- one thread per group, bit width / mode / dtype at run time -----------
+// (quant_group_rt) The bf16 formats quant_lane_kernel does not take: groups
+// of 128 and hybrid stores; either axis, stores and reference outputs.
+template <int G>
+__global__ __launch_bounds__(256) void quant_rt_kernel(LaneArgs a, QuantOut o) {
+  const int64_t gid = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
+  const bool bf = a.bf != 0;
+  float v[G];
+  int64_t bh, unit;
+  RtRef ref{o.codes_i32, o.signs16, o.scale16, o.zero16, 0, 0, 0};
+  if (a.axis == 0) {
+    const int ng = a.D / G;
+    if (gid >= int64_t(a.B) * a.H * a.n * ng) return;
+    const int g = int(gid % ng);
+    const int64_t row = gid / ng;  // bh * n + t
+    const int t = int(row % a.n);
+    bh = row / a.n;
+    const uint16_t* xp = a.x + (bh / a.H) * a.sxb + (bh % a.H) * a.sxh + t * a.sxt + g * G;
+#pragma unroll
+    for (int i = 0; i < G; ++i) v[i] = act2f(xp[i], bf);
+    if (a.norm) {  // cache.py:125
+#pragma unroll
+      for (int i = 0; i < G; ++i) v[i] = round_act(v[i] / act2f(a.norm[bh * a.D + g * G + i], bf), bf);
+    }
+    const int64_t tt = o.t_off + t;
+    unit = ((bh * o.cap_units + tt / TOKEN_BLOCK) * ng + g) * TOKEN_BLOCK + tt % TOKEN_BLOCK;
+    ref.el0 = row * a.D + g * G;
+    ref.el_step = 1;
+    ref.red = row * ng + g;
+  } else {
+    const int ngn = a.n / G;
+    if (gid >= int64_t(a.B) * a.H * ngn * a.D) return;
+    const int d = int(gid % a.D);
+    const int64_t r = gid / a.D;  // bh * ngn + gi
+    const int gi = int(r % ngn);
+    bh = r / ngn;
+    const uint16_t* xp = a.x + (bh / a.H) * a.sxb + (bh % a.H) * a.sxh + int64_t(gi) * G * a.sxt + d;
+#pragma unroll
+    for (int i = 0; i < G; ++i) v[i] = act2f(xp[int64_t(i) * a.sxt], bf);
+    unit = (bh * o.cap_units + o.t_off / G + gi) * a.D + d;
+    ref.el0 = (bh * a.n + int64_t(gi) * G) * a.D + d;
+    ref.el_step = a.D;
+    ref.red = r * a.D + d;
+  }
+  const bool any_ref = o.codes_i32 || o.signs16 || o.scale16 || o.zero16;
+  quant_group_rt<G>(v, a.bits, a.mode, bf, o.codes ? o.codes + unit * ((G * a.bits) >> 5) : nullptr, o.meta, unit,
+                    any_ref ? &ref : nullptr);
+}
+
+// bf16 quantization, or a small fp16 K call: one lane per value where the
+// format allows (G <= 64, asym / sym), else one thread per group at run time
+int launch_lane_or_rt(const LaneArgs& a, const QuantOut& o, int group, hipStream_t st) {
+  const int64_t groups = a.axis == 0 ? int64_t(a.B) * a.H * a.n * (a.D / group)
+                                     : int64_t(a.B) * a.H * (a.n / group) * a.D;
+  if (groups == 0) return IQ_OK;
+  if (group <= 64 && a.mode != IQ_MODE_HYBRID) {
+    auto* kern = group == 64 ? quant_lane_kernel<64> : quant_lane_kernel<32>;
+    kern<<<dim3(unsigned(ceil_div(groups * group, 256))), 256, 0, st>>>(a, o);
+  } else {
+    auto* kern = group == 128 ? quant_rt_kernel<128> : group == 64 ? quant_rt_kernel<64> : quant_rt_kernel<32>;
+    kern<<<dim3(unsigned(ceil_div(groups, 256))), 256, 0, st>>>(a, o);
+  }
+  return launch_status();
 }
 
 // ---- V: groups along tokens, one thread per (b, h, token-group, d) --------
@@ -456,13 +625,14 @@ __global__ __launch_bounds__(256) void quant_v_kernel(const uint16_t* __restrict
 
 // ---- dequantization (dense read path) --------------------------------------
 struct DeqOut {
-  uint16_t* out16;
+  uint16_t* out16;  // in the activation dtype
   float* out32;
   int64_t sob, soh, sot;
+  int bf;           // bf16 activations: meta, norm and out16
 };
 
 __device__ __forceinline__ void put(const DeqOut& o, int64_t off, float v) {
-  if (o.out16) o.out16[off] = __half_as_ushort(__float2half_rn(v));
+  if (o.out16) o.out16[off] = f2act(v, o.bf != 0);
   if (o.out32) o.out32[off] = v;
 }
 
@@ -471,22 +641,22 @@ __device__ __forceinline__ void put(const DeqOut& o, int64_t off, float v) {
 // (quant.py:153-176: the sym codes where the mask is set)
 template <int BITS, int G>
 __device__ __forceinline__ void group_deq_params(const uint32_t* w, const uint16_t* meta, int64_t unit, int mode,
-                                                 int32_t* c, float& s, float& z) {
+                                                 bool bf, int32_t* c, float& s, float& z) {
   unpack_fields<BITS, G>(w, mode == IQ_MODE_SYM, c);
   z = 0.f;
   if (mode == IQ_MODE_SYM) {
-    s = h2f(meta[unit]);
+    s = act2f(meta[unit], bf);
     return;
   }
   const uint32_t mw = reinterpret_cast<const uint32_t*>(meta)[unit];
   if (mode == IQ_MODE_HYBRID && hyb_sym(mw)) {
 #pragma unroll
     for (int i = 0; i < G; ++i) c[i] -= 1 << (BITS - 1);
-    s = hyb_scale(mw);
+    s = hyb_scale(mw, bf);
     return;
   }
-  s = mode == IQ_MODE_HYBRID ? hyb_scale(mw) : h2f(uint16_t(mw & 0xffffu));
-  z = h2f(uint16_t(mw >> 16));
+  s = mode == IQ_MODE_HYBRID ? hyb_scale(mw, bf) : act2f(uint16_t(mw & 0xffffu), bf);
+  z = act2f(uint16_t(mw >> 16), bf);
 }
 
 template <int BITS, int G>
@@ -513,12 +683,12 @@ __global__ __launch_bounds__(256) void dequant_k_kernel(const uint32_t* __restri
   for (int j = 0; j < W; ++j) w[j] = kc[unit * W + j];
   int32_t c[G];
   float s, z;
-  group_deq_params<BITS, G>(w, km, unit, mode, c, s, z);
+  group_deq_params<BITS, G>(w, km, unit, mode, o.bf != 0, c, s, z);
   const int64_t base = b * o.sob + h * o.soh + t * o.sot + g * G;
 #pragma unroll
   for (int i = 0; i < G; ++i) {
     float v = __fadd_rn(__fmul_rn(float(c[i]), s), z);       // quant.py:84-85 (c*s exact)
-    if (norm) v = __fmul_rn(v, h2f(norm[bh * D + g * G + i]));  // cache.py:132
+    if (norm) v = __fmul_rn(v, act2f(norm[bh * D + g * G + i], o.bf != 0));  // cache.py:132
     put(o, base + i, v);
   }
 }
@@ -544,7 +714,7 @@ __global__ __launch_bounds__(256) void dequant_v_kernel(const uint32_t* __restri
   for (int j = 0; j < W; ++j) w[j] = vc[unit * W + j];
   int32_t c[G];
   float s, z;
-  group_deq_params<BITS, G>(w, vm, unit, mode, c, s, z);
+  group_deq_params<BITS, G>(w, vm, unit, mode, o.bf != 0, c, s, z);
 #pragma unroll
   for (int i = 0; i < G; ++i) {
     const float v = __fadd_rn(__fmul_rn(float(c[i]), s), z);  // quant.py:90-91
@@ -560,24 +730,25 @@ __global__ __launch_bounds__(256) void dequant_dense_kernel(const int32_t* __res
                                                             const uint16_t* __restrict__ scale,
                                                             const uint16_t* __restrict__ zs, int64_t outer,
                                                             int64_t n, int64_t inner, int G, int sym, int out_f16,
-                                                            void* out) {
+                                                            int bf, void* out) {
   const int64_t i = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   if (i >= outer * n * inner) return;
   const int64_t j = i % inner;
   const int64_t t = (i / inner) % n;
   const int64_t o = i / (inner * n);
   const int64_t red = (o * (n / G) + t / G) * inner + j;
+  const bool b16 = bf != 0;
   const float c = float(codes[i]);
-  const float s = h2f(scale[red]);
+  const float s = act2f(scale[red], b16);
   float v;
   if (!out_f16) {
     v = __fmul_rn(c, s);
-    v = sym ? __fmul_rn(v, h2f(zs[i])) : __fadd_rn(v, h2f(zs[red]));
+    v = sym ? __fmul_rn(v, act2f(zs[i], b16)) : __fadd_rn(v, act2f(zs[red], b16));
     reinterpret_cast<float*>(out)[i] = v;
-  } else {
-    v = round_f16(__fmul_rn(round_f16(c), s));
-    v = sym ? round_f16(__fmul_rn(v, h2f(zs[i]))) : round_f16(__fadd_rn(v, h2f(zs[red])));
-    reinterpret_cast<uint16_t*>(out)[i] = __half_as_ushort(__float2half_rn(v));
+  } else {  // op_dtype = the activation dtype: one rounding per op
+    v = round_act(__fmul_rn(round_act(c, b16), s), b16);
+    v = sym ? round_act(__fmul_rn(v, act2f(zs[i], b16)), b16) : round_act(__fadd_rn(v, act2f(zs[red], b16)), b16);
+    reinterpret_cast<uint16_t*>(out)[i] = f2act(v, b16);
   }
 }
 
@@ -603,12 +774,14 @@ __device__ __forceinline__ void unpack_meta(const uint16_t* meta, int64_t unit, 
   }
 }
 
-__device__ __forceinline__ uint16_t sign16(int32_t c) { return c > 0 ? 0x3c00u : (c < 0 ? 0xbc00u : 0u); }
+__device__ __forceinline__ uint16_t sign16(int32_t c, bool bf) {  // +-1 or 0 in the activation dtype
+  return c > 0 ? (bf ? 0x3f80u : 0x3c00u) : (c < 0 ? (bf ? 0xbf80u : 0xbc00u) : 0u);
+}
 
 template <int BITS, int G>
 __global__ __launch_bounds__(256) void unpack_k_kernel(const uint32_t* __restrict__ kc, const uint16_t* __restrict__ km,
                                                        int64_t cap_blocks, int B, int H, int t0, int T, int D, int sym,
-                                                       UnpackOut o) {
+                                                       int bf, UnpackOut o) {
   constexpr int W = G * BITS / 32;
   const int ng = D / G;
   const int64_t gid = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -631,14 +804,14 @@ __global__ __launch_bounds__(256) void unpack_k_kernel(const uint32_t* __restric
   for (int i = 0; i < G; ++i) {
     const int64_t e = row * D + g * G + i;
     o.codes[e] = c[i] < 0 ? -c[i] : c[i];
-    if (sym) o.zs[e] = sign16(c[i]);
+    if (sym) o.zs[e] = sign16(c[i], bf != 0);
   }
 }
 
 template <int BITS, int G>
 __global__ __launch_bounds__(256) void unpack_v_kernel(const uint32_t* __restrict__ vc, const uint16_t* __restrict__ vm,
                                                        int64_t cap_groups, int B, int H, int g0, int ngT, int D,
-                                                       int sym, UnpackOut o) {
+                                                       int sym, int bf, UnpackOut o) {
   constexpr int W = G * BITS / 32;
   const int64_t gid = int64_t(blockIdx.x) * blockDim.x + threadIdx.x;
   if (gid >= int64_t(B) * H * ngT * D) return;
@@ -660,7 +833,7 @@ __global__ __launch_bounds__(256) void unpack_v_kernel(const uint32_t* __restric
   for (int i = 0; i < G; ++i) {
     const int64_t e = ((bh * ngT + gi) * G + i) * D + d;
     o.codes[e] = c[i] < 0 ? -c[i] : c[i];
-    if (sym) o.zs[e] = sign16(c[i]);
+    if (sym) o.zs[e] = sign16(c[i], bf != 0);
   }
 }
 
@@ -683,6 +856,7 @@ struct WinRole {
   uint16_t* meta;
   int64_t cap_units, t_off;
   int bits, group, gsh, mode, axis;  // axis 0: groups along head_dim (K layout), 1: along tokens (V layout)
+  int bf;                            // bf16 activations (mode's IQ_MODE_BF16 flag, stripped from mode)
   const uint16_t* norm;              // axis 0: fp16 [B,H,D] key normalization factor, or null
   int vec_buf, vec_x;                // rows of the buffer / of x are 16-byte aligned (base and strides)
 };
@@ -695,62 +869,6 @@ struct AppendArgs {
   // aligned to the block size
   int64_t start[4], count[4];
 };
-
-// One group, quantized as quantize_group / quantize_group_hybrid do, with
-// the bit width and mode known at run time: v[] holds the group's G inputs
-// (registers; loaded together, one memory latency per group), the fields are
-// stored word by word as they fill, the meta word last.
-template <int G>
-__device__ __forceinline__ void quant_group_rt(const float* v, int bits, int mode, uint32_t* out, uint16_t* meta,
-                                               int64_t unit) {
-  const int abits = mode == IQ_MODE_HYBRID ? bits - 1 : bits;
-  float mn = v[0], mx = v[0], amx = 0.f;
-  bool nan = false;
-#pragma unroll
-  for (int i = 0; i < G; ++i) {
-    nan |= is_nan(v[i]);
-    mn = fminf(mn, v[i]);
-    mx = fmaxf(mx, v[i]);
-    amx = fmaxf(amx, fabsf(v[i]));
-  }
-  if (nan) { mn = __builtin_nanf(""); mx = mn; amx = mn; }
-  const float sa = asym_scale_b(mn, mx, abits), ss = sym_scale_b(amx, bits);
-  bool sym = mode == IQ_MODE_SYM;
-  if (mode == IQ_MODE_HYBRID) {  // quantize_group_hybrid's choice
-    double ea = 0.0, es = 0.0;
-#pragma unroll
-    for (int i = 0; i < G; ++i) {
-      const float da = __fadd_rn(__fmul_rn(float(asym_code_b(v[i], mn, sa, abits)), sa), mn);
-      const float ds = __fmul_rn(__fmul_rn(float(sym_code_b(v[i], ss, bits)), ss), sign_of(v[i]));
-      ea += double(fabsf(__fsub_rn(da, v[i])));
-      es += double(fabsf(__fsub_rn(ds, v[i])));
-    }
-    sym = ea > es;
-  }
-  uint64_t acc = 0;
-  int pos = 0, wj = 0;
-#pragma unroll
-  for (int i = 0; i < G; ++i) {
-    const uint32_t fld = sym ? sym_field_b(sym_code_b(v[i], ss, bits), sign_of(v[i]), bits)
-                             : asym_field_b(asym_code_b(v[i], mn, sa, abits), bits);
-    acc |= uint64_t(fld) << pos;
-    pos += bits;
-    if (pos >= 32) {
-      out[wj++] = uint32_t(acc);
-      acc >>= 32;
-      pos -= 32;
-    }
-  }
-  if (mode == IQ_MODE_SYM) {
-    meta[unit] = __half_as_ushort(__float2half_rn(ss));
-  } else if (mode == IQ_MODE_HYBRID) {
-    const uint32_t sh = __half_as_ushort(__float2half_rn(sym ? ss : sa));
-    reinterpret_cast<uint32_t*>(meta)[unit] =
-        sym ? (sh | HYB_FLAG) : ((sh & 0x7fffu) | (uint32_t(__half_as_ushort(__float2half_rn(mn))) << 16));
-  } else {
-    reinterpret_cast<uint32_t*>(meta)[unit] = meta_word(sa, mn);
-  }
-}
 
 // one group of the flushed tokens of role r (group item q): element i is
 // token f0 + i * fstep of [window | new], column d0 + i * dstep
@@ -787,8 +905,8 @@ __device__ __forceinline__ void append_group(const WinRole& r, int H, int D, int
       const uint32_t w[4] = {u.x, u.y, u.z, u.w};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        v[8 * c + 2 * j] = h2f(uint16_t(w[j] & 0xffffu));
-        v[8 * c + 2 * j + 1] = h2f(uint16_t(w[j] >> 16));
+        v[8 * c + 2 * j] = act2f(uint16_t(w[j] & 0xffffu), r.bf != 0);
+        v[8 * c + 2 * j + 1] = act2f(uint16_t(w[j] >> 16), r.bf != 0);
       }
     }
   } else {
@@ -797,14 +915,14 @@ __device__ __forceinline__ void append_group(const WinRole& r, int H, int D, int
       const int f = f0 + i * fstep, d = d0 + i * dstep;
       const uint16_t* p = f < r.n ? r.buf + b * r.sb + h * r.sh + int64_t(r.start + f) * r.st + d
                                   : r.x + b * r.sxb + h * r.sxh + int64_t(f - r.n) * r.sxt + d;
-      v[i] = h2f(*p);
+      v[i] = act2f(*p, r.bf != 0);
     }
   }
   if (r.norm) {  // cache.py:125  x / key_normalization_factor in fp16
 #pragma unroll
-    for (int i = 0; i < G; ++i) v[i] = round_f16(v[i] / h2f(r.norm[bh * D + d0 + i * dstep]));
+    for (int i = 0; i < G; ++i) v[i] = round_act(v[i] / act2f(r.norm[bh * D + d0 + i * dstep], r.bf != 0), r.bf != 0);
   }
-  quant_group_rt<G>(v, r.bits, r.mode, r.codes + unit * ((G * r.bits) >> 5), r.meta, unit);
+  quant_group_rt<G>(v, r.bits, r.mode, r.bf != 0, r.codes + unit * ((G * r.bits) >> 5), r.meta, unit);
 }
 
 // append_group with one lane per element (G <= 64, asym or sym): item q of
@@ -834,10 +952,11 @@ __device__ __forceinline__ void append_group_lanes(const WinRole& r, int H, int 
   const int64_t b = bh / H, h = bh % H;
   const uint16_t* p = f < r.n ? r.buf + b * r.sb + h * r.sh + int64_t(r.start + f) * r.st + d
                               : r.x + b * r.sxb + h * r.sxh + int64_t(f - r.n) * r.sxt + d;
-  float v = h2f(*p);
-  if (r.norm) v = round_f16(v / h2f(r.norm[bh * D + d]));  // cache.py:125
+  float v = act2f(*p, r.bf != 0);
+  if (r.norm) v = round_act(v / act2f(r.norm[bh * D + d], r.bf != 0), r.bf != 0);  // cache.py:125
   float sg, sc, zp;
-  quant_group_lanes<G>(v, i, r.bits, r.mode, true, r.codes + unit * ((G * r.bits) >> 5), r.meta, unit, sg, sc, zp);
+  quant_group_lanes<G>(v, i, r.bits, r.mode, r.bf, true, r.codes + unit * ((G * r.bits) >> 5), r.meta, unit, sg, sc,
+                       zp);
 }
 
 // lanes per group item of a role: one lane per element where quant_group_lanes
@@ -939,6 +1058,8 @@ int iq_quantize_k(const void* x, int64_t sx_b, int64_t sx_h, int64_t sx_t, const
                   int64_t t_cap, int64_t t_off, int32_t* codes_i32, void* scale16, void* zero16, void* signs16,
                   void* stream) {
   IQ_CHECK(x, IQ_ERR_NULL);
+  const bool bf = act_bf16(mode);
+  mode = base_mode(mode);
   if (int e = check_store(bits, group, mode)) return e;
   IQ_CHECK(B >= 0 && H >= 0 && n >= 0 && D > 0, IQ_ERR_SHAPE);
   IQ_CHECK(D % group == 0, IQ_ERR_GROUP);
@@ -960,12 +1081,10 @@ int iq_quantize_k(const void* x, int64_t sx_b, int64_t sx_h, int64_t sx_t, const
   const int sym = mode == IQ_MODE_SYM;
   // a call of few groups (a decode step's tokens) takes one lane per value:
   // one thread per group would leave most of the device idle on long chains
-  if (mode != IQ_MODE_HYBRID && group <= 64 && total <= LANE_MAX_GROUPS) {
-    const int64_t lanes = total * group;
-    auto* kern = group == 64 ? quant_k_lane_kernel<64> : quant_k_lane_kernel<32>;
-    kern<<<dim3(unsigned(ceil_div(lanes, 256))), 256, 0, (hipStream_t)stream>>>(
-        (const uint16_t*)x, sx_b, sx_h, sx_t, (const uint16_t*)norm, B, H, n, D, bits, mode, o);
-    return launch_status();
+  if (bf || (mode != IQ_MODE_HYBRID && group <= 64 && total <= LANE_MAX_GROUPS)) {
+    const LaneArgs a{(const uint16_t*)x, sx_b, sx_h, sx_t, (const uint16_t*)norm, B, H, n, D, bits, mode, bf ? 1 : 0,
+                     0};
+    return launch_lane_or_rt(a, o, group, (hipStream_t)stream);
   }
   return dispatch_store_bits_group(bits, group, [&]<int BITS, int G>() {
     // the store-only append (no reference-format outputs) drops their registers
@@ -982,6 +1101,8 @@ int iq_quantize_v(const void* x, int64_t sx_b, int64_t sx_h, int64_t sx_t, int B
                   int group, int bits, int mode, uint32_t* v_codes, uint16_t* v_meta, int64_t t_cap,
                   int64_t t_off, int32_t* codes_i32, void* scale16, void* zero16, void* signs16, void* stream) {
   IQ_CHECK(x, IQ_ERR_NULL);
+  const bool bf = act_bf16(mode);
+  mode = base_mode(mode);
   if (int e = check_store(bits, group, mode)) return e;
   IQ_CHECK(B >= 0 && H >= 0 && n >= 0 && D > 0, IQ_ERR_SHAPE);
   IQ_CHECK(n % group == 0, IQ_ERR_GROUP);
@@ -1000,6 +1121,10 @@ int iq_quantize_v(const void* x, int64_t sx_b, int64_t sx_h, int64_t sx_t, int B
   if (total == 0) return IQ_OK;
   QuantOut o{v_codes, v_meta, t_cap / group, t_off, codes_i32, (uint16_t*)scale16, (uint16_t*)zero16,
              (uint16_t*)signs16};
+  if (bf) {
+    const LaneArgs a{(const uint16_t*)x, sx_b, sx_h, sx_t, nullptr, B, H, n, D, bits, mode, 1, 1};
+    return launch_lane_or_rt(a, o, group, (hipStream_t)stream);
+  }
   const int sym = mode == IQ_MODE_SYM;
   return dispatch_store_bits_group(bits, group, [&]<int BITS, int G>() {
     auto* kern = mode == IQ_MODE_HYBRID ? quant_v_kernel<BITS, G, false, true>
@@ -1016,6 +1141,8 @@ int iq_dequant_k(const uint32_t* k_codes, const uint16_t* k_meta, int64_t t_cap,
                  int64_t so_h, int64_t so_t, void* stream) {
   IQ_CHECK(k_codes && k_meta, IQ_ERR_NULL);
   IQ_CHECK(out16 || out32, IQ_ERR_NULL);
+  const bool bf = act_bf16(mode);
+  mode = base_mode(mode);
   if (int e = check_store(bits, group, mode)) return e;
   IQ_CHECK(B >= 0 && H >= 0 && T >= 0 && t0 >= 0 && D > 0, IQ_ERR_SHAPE);
   IQ_CHECK(D % group == 0, IQ_ERR_GROUP);
@@ -1023,7 +1150,7 @@ int iq_dequant_k(const uint32_t* k_codes, const uint16_t* k_meta, int64_t t_cap,
   IQ_CHECK(int64_t(t0) + T <= t_cap, IQ_ERR_RANGE);
   const int64_t total = int64_t(B) * H * T * (D / group);
   if (total == 0) return IQ_OK;
-  DeqOut o{(uint16_t*)out16, out32, so_b, so_h, so_t};
+  DeqOut o{(uint16_t*)out16, out32, so_b, so_h, so_t, bf ? 1 : 0};
   return dispatch_store_bits_group(bits, group, [&]<int BITS, int G>() {
     dequant_k_kernel<BITS, G><<<dim3(unsigned(ceil_div(total, 256))), 256, 0, (hipStream_t)stream>>>(
         k_codes, k_meta, t_cap / TOKEN_BLOCK, (const uint16_t*)norm, B, H, t0, T, D, mode, o);
@@ -1036,13 +1163,15 @@ int iq_dequant_v(const uint32_t* v_codes, const uint16_t* v_meta, int64_t t_cap,
                  int64_t so_t, void* stream) {
   IQ_CHECK(v_codes && v_meta, IQ_ERR_NULL);
   IQ_CHECK(out16 || out32, IQ_ERR_NULL);
+  const bool bf = act_bf16(mode);
+  mode = base_mode(mode);
   if (int e = check_store(bits, group, mode)) return e;
   IQ_CHECK(B >= 0 && H >= 0 && T >= 0 && t0 >= 0 && D > 0, IQ_ERR_SHAPE);
   IQ_CHECK(T % group == 0 && t0 % group == 0 && t_cap % group == 0, IQ_ERR_GROUP);
   IQ_CHECK(int64_t(t0) + T <= t_cap, IQ_ERR_RANGE);
   const int64_t total = int64_t(B) * H * (T / group) * D;
   if (total == 0) return IQ_OK;
-  DeqOut o{(uint16_t*)out16, out32, so_b, so_h, so_t};
+  DeqOut o{(uint16_t*)out16, out32, so_b, so_h, so_t, bf ? 1 : 0};
   return dispatch_store_bits_group(bits, group, [&]<int BITS, int G>() {
     dequant_v_kernel<BITS, G><<<dim3(unsigned(ceil_div(total, 256))), 256, 0, (hipStream_t)stream>>>(
         v_codes, v_meta, t_cap / G, B, H, t0 / G, T / G, D, mode, o);
@@ -1053,6 +1182,8 @@ int iq_dequant_v(const uint32_t* v_codes, const uint16_t* v_meta, int64_t t_cap,
 int iq_dequant_dense(const int32_t* codes, const void* scale16, const void* zs16, int64_t outer, int64_t n,
                      int64_t inner, int group, int mode, int out_f16, void* out, void* stream) {
   IQ_CHECK(codes && scale16 && zs16 && out, IQ_ERR_NULL);
+  const bool bf = act_bf16(mode);
+  mode = base_mode(mode);
   IQ_CHECK(mode_ok(mode), IQ_ERR_MODE);
   IQ_CHECK(outer >= 0 && n >= 0 && inner >= 0 && (out_f16 == 0 || out_f16 == 1), IQ_ERR_SHAPE);
   IQ_CHECK(group > 0 && n % group == 0, IQ_ERR_GROUP);
@@ -1060,7 +1191,7 @@ int iq_dequant_dense(const int32_t* codes, const void* scale16, const void* zs16
   if (total == 0) return IQ_OK;
   dequant_dense_kernel<<<dim3(unsigned(ceil_div(total, 256))), 256, 0, (hipStream_t)stream>>>(
       codes, (const uint16_t*)scale16, (const uint16_t*)zs16, outer, n, inner, group, mode == IQ_MODE_SYM, out_f16,
-      out);
+      bf ? 1 : 0, out);
   return launch_status();
 }
 
@@ -1075,7 +1206,7 @@ int check_window(const iq_window* w, int D) {
   IQ_CHECK(aligned(w->buf, 2) && aligned(w->x, 2), IQ_ERR_ALIGN);
   if (w->flush == 0) return IQ_OK;
   IQ_CHECK(w->codes && w->meta, IQ_ERR_NULL);
-  if (int e = check_store(w->bits, w->group, w->mode)) return e;
+  if (int e = check_store(w->bits, w->group, base_mode(w->mode))) return e;
   IQ_CHECK(w->axis == 0 || w->axis == 1, IQ_ERR_SHAPE);
   IQ_CHECK(!w->norm || w->axis == 0, IQ_ERR_SHAPE);
   IQ_CHECK(w->t_off >= 0 && w->t_off + w->flush <= w->t_cap, IQ_ERR_RANGE);
@@ -1097,7 +1228,7 @@ WinRole to_role(const iq_window* w) {
   r.x = (const uint16_t*)w->x; r.sxb = w->sx_b; r.sxh = w->sx_h; r.sxt = w->sx_t; r.m = w->m;
   r.F = w->flush;
   r.codes = w->codes; r.meta = w->meta; r.t_off = w->t_off;
-  r.bits = w->bits; r.group = w->group; r.mode = w->mode; r.axis = w->axis;
+  r.bits = w->bits; r.group = w->group; r.mode = base_mode(w->mode); r.bf = act_bf16(w->mode); r.axis = w->axis;
   r.gsh = w->group > 0 ? __builtin_ctz(unsigned(w->group)) : 0;
   r.cap_units = w->flush ? (w->axis == 0 ? w->t_cap / TOKEN_BLOCK : w->t_cap / w->group) : 0;
   r.norm = (const uint16_t*)w->norm;
@@ -1143,6 +1274,8 @@ int iq_window_append(const iq_window* k, const iq_window* v, int B, int H, int D
 int iq_unpack_k(const uint32_t* k_codes, const uint16_t* k_meta, int64_t t_cap, int B, int H, int t0, int T, int D,
                 int group, int bits, int mode, int32_t* codes_i32, void* scale16, void* zs16, void* stream) {
   IQ_CHECK(k_codes && k_meta && codes_i32 && scale16 && zs16, IQ_ERR_NULL);
+  const bool bf = act_bf16(mode);
+  mode = base_mode(mode);
   if (int e = check_store(bits, group, mode)) return e;
   IQ_CHECK(B >= 0 && H >= 0 && T >= 0 && t0 >= 0 && D > 0, IQ_ERR_SHAPE);
   IQ_CHECK(D % group == 0, IQ_ERR_GROUP);
@@ -1153,7 +1286,7 @@ int iq_unpack_k(const uint32_t* k_codes, const uint16_t* k_meta, int64_t t_cap, 
   const UnpackOut o{codes_i32, (uint16_t*)scale16, (uint16_t*)zs16};
   return dispatch_store_bits_group(bits, group, [&]<int BITS, int G>() {
     unpack_k_kernel<BITS, G><<<dim3(unsigned(ceil_div(total, 256))), 256, 0, (hipStream_t)stream>>>(
-        k_codes, k_meta, t_cap / TOKEN_BLOCK, B, H, t0, T, D, mode == IQ_MODE_SYM, o);
+        k_codes, k_meta, t_cap / TOKEN_BLOCK, B, H, t0, T, D, mode == IQ_MODE_SYM, bf ? 1 : 0, o);
     return launch_status();
   });
 }
@@ -1161,6 +1294,8 @@ int iq_unpack_k(const uint32_t* k_codes, const uint16_t* k_meta, int64_t t_cap, 
 int iq_unpack_v(const uint32_t* v_codes, const uint16_t* v_meta, int64_t t_cap, int B, int H, int t0, int T, int D,
                 int group, int bits, int mode, int32_t* codes_i32, void* scale16, void* zs16, void* stream) {
   IQ_CHECK(v_codes && v_meta && codes_i32 && scale16 && zs16, IQ_ERR_NULL);
+  const bool bf = act_bf16(mode);
+  mode = base_mode(mode);
   if (int e = check_store(bits, group, mode)) return e;
   IQ_CHECK(B >= 0 && H >= 0 && T >= 0 && t0 >= 0 && D > 0, IQ_ERR_SHAPE);
   IQ_CHECK(T % group == 0 && t0 % group == 0 && t_cap % group == 0, IQ_ERR_GROUP);
@@ -1170,7 +1305,7 @@ int iq_unpack_v(const uint32_t* v_codes, const uint16_t* v_meta, int64_t t_cap, 
   const UnpackOut o{codes_i32, (uint16_t*)scale16, (uint16_t*)zs16};
   return dispatch_store_bits_group(bits, group, [&]<int BITS, int G>() {
     unpack_v_kernel<BITS, G><<<dim3(unsigned(ceil_div(total, 256))), 256, 0, (hipStream_t)stream>>>(
-        v_codes, v_meta, t_cap / G, B, H, t0 / G, T / G, D, mode == IQ_MODE_SYM, o);
+        v_codes, v_meta, t_cap / G, B, H, t0 / G, T / G, D, mode == IQ_MODE_SYM, bf ? 1 : 0, o);
     return launch_status();
   });
 }

@@ -33,6 +33,27 @@ def require_device(t: torch.Tensor, name: str, dtype=torch.float16) -> None:
         raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
 
 
+def act_flag(dtype) -> int:
+    """The mode bit of an activation dtype: IQ_MODE_BF16 for bf16, 0 for fp16."""
+    if dtype == torch.bfloat16:
+        return _lib.IQ_MODE_BF16
+    if dtype == torch.float16:
+        return 0
+    raise TypeError(f"activations must be torch.float16 or torch.bfloat16, got {dtype}")
+
+
+def require_act(t: torch.Tensor, name: str, dtype=None) -> None:
+    """A HIP device tensor of an activation dtype (fp16 or bf16; exactly ``dtype`` when given)."""
+    require_device(t, name, dtype)
+    act_flag(t.dtype)
+
+
+def require_f16_store(store, role: str) -> None:
+    if store is not None and store.dtype != torch.float16:
+        raise TypeError(f"{role}: the decode kernels take fp16 stores; a {store.dtype} store is read through "
+                        "dequant() (the reference's dequantize-then-attend path)")
+
+
 def mode_id(mode) -> int:
     if isinstance(mode, int):
         return mode
@@ -156,17 +177,24 @@ class PackedStore:
     """
 
     def __init__(self, axis: str, B: int, H: int, D: int, group: int, bits: int, mode, device,
-                 t_cap: int = 0):
+                 t_cap: int = 0, dtype=torch.float16):
         if axis not in ("channel", "token"):
             raise ValueError(axis)
         self.axis, self.B, self.H, self.D = axis, B, H, D
         self.group, self.bits, self.mode = group, bits, mode_id(mode)
+        act_flag(dtype)
+        self.dtype = dtype  # activation dtype: of the appended tokens, the scales / zero points and dequant()
         self.device = torch.device(device)
         self.length = 0
         self.t_cap = 0
         self.codes = torch.empty(0, dtype=torch.int32, device=self.device)
         self.meta = torch.empty(0, dtype=torch.int16, device=self.device)
         self.reserve(t_cap)
+
+    @property
+    def mode_arg(self) -> int:
+        """The mode as the C ABI takes it: the quantizer mode plus the activation dtype's flag."""
+        return self.mode | act_flag(self.dtype)
 
     @property
     def unit(self) -> int:
@@ -252,7 +280,8 @@ class PackedStore:
             torch.empty(bh, 0, 0, dtype=torch.int16)
         md = {"format": self.WIRE_FORMAT, "version": self.WIRE_VERSION, "axis": self.axis, "B": self.B,
               "H": self.H, "D": self.D, "group": self.group, "bits": self.bits,
-              "mode": MODE_NAMES[self.mode], "length": self.length, "unit": u}
+              "mode": MODE_NAMES[self.mode], "length": self.length, "unit": u,
+              "dtype": "bfloat16" if self.dtype == torch.bfloat16 else "float16"}
         return self._safetensors({"codes": codes, "meta": meta}, {k: str(v) for k, v in md.items()})
 
     @classmethod
@@ -269,7 +298,10 @@ class PackedStore:
                              f"v{md.get('version')!r}")
         t = load(blob)
         B, H, D, group, bits, length = (int(md[k]) for k in ("B", "H", "D", "group", "bits", "length"))
-        st = cls(md["axis"], B, H, D, group, bits, md["mode"], device, t_cap=max(t_cap, length))
+        dtype = {"float16": torch.float16, "bfloat16": torch.bfloat16}.get(md.get("dtype", "float16"))
+        if dtype is None:
+            raise ValueError(f"unknown activation dtype {md.get('dtype')!r}")
+        st = cls(md["axis"], B, H, D, group, bits, md["mode"], device, t_cap=max(t_cap, length), dtype=dtype)
         u = st.unit
         used, nu = -(-length // u), st.t_cap // u
         if int(md["unit"]) != u:
@@ -293,8 +325,8 @@ class PackedStore:
 
     # --- writes -------------------------------------------------------------
     def append(self, x: torch.Tensor, norm: Optional[torch.Tensor] = None) -> None:
-        """Quantize x [B,H,n,D] fp16 and append it (quantize-on-append)."""
-        require_device(x, "x")
+        """Quantize x [B,H,n,D] (the store's dtype) and append it (quantize-on-append)."""
+        require_device(x, "x", self.dtype)
         if x.dim() != 4 or (x.shape[0], x.shape[1], x.shape[3]) != (self.B, self.H, self.D):
             _shape_error(f"append: x has shape {tuple(x.shape)}, the store holds [B={self.B}, H={self.H}, n, "
                          f"D={self.D}]")
@@ -308,45 +340,46 @@ class PackedStore:
             if x.stride(-1) != 1 or x.data_ptr() % 16 or any(s % 8 for s in x.stride()[:3]):
                 x = x.contiguous()
             if norm is not None:
-                require_device(norm, "norm")
+                require_device(norm, "norm", self.dtype)
                 norm = norm.reshape(B, H, D).contiguous()
             call("iq_quantize_k", _p(x), x.stride(0), x.stride(1), x.stride(2), _p(norm), B, H, n, D, self.group,
-                 self.bits, self.mode, _p(self.codes), _p(self.meta), self.t_cap, self.length, None, None, None, None,
-                 _stream(x.device))
+                 self.bits, self.mode_arg, _p(self.codes), _p(self.meta), self.t_cap, self.length, None, None, None,
+                 None, _stream(x.device))
         else:
             if x.stride(-1) != 1:
                 x = x.contiguous()
             call("iq_quantize_v", _p(x), x.stride(0), x.stride(1), x.stride(2), B, H, n, D, self.group, self.bits,
-                 self.mode, _p(self.codes), _p(self.meta), self.t_cap, self.length, None, None, None, None,
+                 self.mode_arg, _p(self.codes), _p(self.meta), self.t_cap, self.length, None, None, None, None,
                  _stream(x.device))
         self.length += n
 
     # --- reads --------------------------------------------------------------
     def dequant(self, t0: int = 0, T: Optional[int] = None, out: Optional[torch.Tensor] = None,
-                norm: Optional[torch.Tensor] = None, dtype=torch.float16) -> torch.Tensor:
-        """Dense [B,H,T,D] values of tokens [t0, t0+T) (fp16 or fp32); ``out`` may be a strided view."""
+                norm: Optional[torch.Tensor] = None, dtype=None) -> torch.Tensor:
+        """Dense [B,H,T,D] values of tokens [t0, t0+T) (the store's dtype, or fp32); ``out`` may be a
+        strided view."""
         T = self.length - t0 if T is None else T
         check_range(self, "dequant", t0, T)
         if out is None:
-            out = torch.empty(self.B, self.H, T, self.D, dtype=dtype, device=self.device)
+            out = torch.empty(self.B, self.H, T, self.D, dtype=dtype or self.dtype, device=self.device)
         check_out(out.shape, (self.B, self.H, T, self.D))
         if out.stride(-1) != 1:
             _shape_error("dequant output must have a contiguous last dimension")
-        o16 = _p(out) if out.dtype == torch.float16 else None
+        o16 = _p(out) if out.dtype == self.dtype else None
         o32 = _p(out) if out.dtype == torch.float32 else None
         if o16 is None and o32 is None:
-            raise TypeError("dequant output must be fp16 or fp32")
+            raise TypeError(f"dequant output must be {self.dtype} or fp32")
         st = out.stride()
         if self.axis == "channel":
             if norm is not None:
                 norm = norm.reshape(self.B, self.H, self.D).contiguous()
             call("iq_dequant_k", _p(self.codes), _p(self.meta), self.t_cap, _p(norm), self.B, self.H, t0, T, self.D,
-                 self.group, self.bits, self.mode, o16, o32, st[0], st[1], st[2], _stream(out.device))
+                 self.group, self.bits, self.mode_arg, o16, o32, st[0], st[1], st[2], _stream(out.device))
         else:
             if norm is not None:
                 raise ValueError("a key normalization factor applies to head_dim-grouped (K) stores only")
             call("iq_dequant_v", _p(self.codes), _p(self.meta), self.t_cap, self.B, self.H, t0, T, self.D,
-                 self.group, self.bits, self.mode, o16, o32, st[0], st[1], st[2], _stream(out.device))
+                 self.group, self.bits, self.mode_arg, o16, o32, st[0], st[1], st[2], _stream(out.device))
         return out
 
 
@@ -359,7 +392,7 @@ class RecentWindow:
     larger buffer; a view returned earlier keeps its old buffer and values."""
 
     def __init__(self, x: torch.Tensor):
-        require_device(x, "recent window")
+        require_act(x, "recent window")
         B, H, n, D = x.shape
         self.buf = torch.empty(B, H, max(2 * n, n + 64), D, dtype=x.dtype, device=x.device)
         self.buf[:, :, :n].copy_(x)
@@ -392,7 +425,7 @@ def window_append(kwin: Optional[RecentWindow], knew: Optional[torch.Tensor], kf
         if win is None:
             roles.append(None)
             continue
-        require_device(x, "new tokens")
+        require_device(x, "new tokens", win.buf.dtype)
         if x.stride(-1) != 1:
             x = x.contiguous()
         B, H, m, D = x.shape
@@ -417,7 +450,9 @@ def window_append(kwin: Optional[RecentWindow], knew: Optional[torch.Tensor], kf
             st.reserve(st.length + fl)
             w.codes, w.meta = st.codes.data_ptr(), st.meta.data_ptr()
             w.t_cap, w.t_off = st.t_cap, st.length
-            w.bits, w.group, w.mode = st.bits, st.group, st.mode
+            if st.dtype != x.dtype:
+                raise TypeError(f"window_append: {x.dtype} tokens into a {st.dtype} store")
+            w.bits, w.group, w.mode = st.bits, st.group, st.mode_arg
             w.axis = 0 if st.axis == "channel" else 1
             if norm is not None:
                 if st.axis != "channel":
@@ -440,13 +475,14 @@ def window_append(kwin: Optional[RecentWindow], knew: Optional[torch.Tensor], kf
 
 
 def quantize_dense(x: torch.Tensor, group: int, bits: int, mode, axis: str):
-    """Reference-format quantization of a [rows, n, inner]-viewable fp16 tensor.
+    """Reference-format quantization of a [rows, n, inner]-viewable fp16 or bf16 tensor.
 
-    Returns (codes int32 like x, scale fp16, zero fp16 | signs fp16) exactly as
+    Returns (codes int32 like x, scale, zero | signs in x's dtype) exactly as
     quant.py's quantize_{channeldim,tokendim}_{asym,sym}.
     """
-    require_device(x, "tensor")
+    require_act(x, "tensor")
     m = mode_id(mode)
+    dt = x.dtype
     if m == IQ_MODE_HYBRID:
         raise ValueError("quantize_dense takes 'asymmetric' or 'symmetric'; hybrid quantization is "
                          "quant.quantize_hybrid (both halves) or a hybrid PackedStore")
@@ -458,18 +494,19 @@ def quantize_dense(x: torch.Tensor, group: int, bits: int, mode, axis: str):
         n = shape[-1]
         rows = x.numel() // max(n, 1)
         red = shape[:-1] + (n // group,)
-        scale = torch.empty(red, dtype=torch.float16, device=dev)
-        zs = torch.empty(red if m == IQ_MODE_ASYM else shape, dtype=torch.float16, device=dev)
-        call("iq_quantize_k", _p(x), 0, 0, n, None, 1, 1, rows, n, group, bits, m, None, None, 0, 0,
+        scale = torch.empty(red, dtype=dt, device=dev)
+        zs = torch.empty(red if m == IQ_MODE_ASYM else shape, dtype=dt, device=dev)
+        call("iq_quantize_k", _p(x), 0, 0, n, None, 1, 1, rows, n, group, bits, m | act_flag(dt), None, None, 0, 0,
              _p(codes), _p(scale), _p(zs) if m == IQ_MODE_ASYM else None, _p(zs) if m == IQ_MODE_SYM else None,
              _stream(dev))
     else:
         n, inner = shape[-2], shape[-1]
         outer = x.numel() // max(n * inner, 1)
         red = shape[:-2] + (n // group, inner)
-        scale = torch.empty(red, dtype=torch.float16, device=dev)
-        zs = torch.empty(red if m == IQ_MODE_ASYM else shape, dtype=torch.float16, device=dev)
-        call("iq_quantize_v", _p(x), 0, n * inner, inner, 1, outer, n, inner, group, bits, m, None, None, 0, 0,
+        scale = torch.empty(red, dtype=dt, device=dev)
+        zs = torch.empty(red if m == IQ_MODE_ASYM else shape, dtype=dt, device=dev)
+        call("iq_quantize_v", _p(x), 0, n * inner, inner, 1, outer, n, inner, group, bits, m | act_flag(dt), None,
+             None, 0, 0,
              _p(codes), _p(scale), _p(zs) if m == IQ_MODE_ASYM else None, _p(zs) if m == IQ_MODE_SYM else None,
              _stream(dev))
     return codes, scale, zs
@@ -478,19 +515,20 @@ def quantize_dense(x: torch.Tensor, group: int, bits: int, mode, axis: str):
 def dequantize_dense(codes: torch.Tensor, scale: torch.Tensor, zs: torch.Tensor, group: int, mode, axis: str,
                      dtype=torch.float32) -> torch.Tensor:
     require_device(codes, "tensor", torch.int32)
-    require_device(scale, "scale")
-    require_device(zs, "zero_points/signs")
+    require_act(scale, "scale")
+    require_device(zs, "zero_points/signs", scale.dtype)
     shape = tuple(codes.shape)
     if axis == "channel":
         outer, n, inner = codes.numel() // max(shape[-1], 1), shape[-1], 1
     else:
         n, inner = shape[-2], shape[-1]
         outer = codes.numel() // max(n * inner, 1)
+    if dtype not in (torch.float32, scale.dtype):
+        raise TypeError(f"op_dtype must be torch.float32 or the scales' {scale.dtype}")
     out = torch.empty(shape, dtype=dtype, device=codes.device)
-    if dtype not in (torch.float32, torch.float16):
-        raise TypeError("op_dtype must be torch.float32 or torch.float16")
     call("iq_dequant_dense", _p(codes.contiguous()), _p(scale.contiguous()), _p(zs.contiguous()), outer, n, inner,
-         group, mode_id(mode), 1 if dtype == torch.float16 else 0, _p(out), _stream(codes.device))
+         group, mode_id(mode) | act_flag(scale.dtype), 0 if dtype == torch.float32 else 1, _p(out),
+         _stream(codes.device))
     return out
 
 
@@ -509,6 +547,7 @@ def _workspace(device: torch.device, nbytes: int) -> torch.Tensor:
 def qk_gemv(q: torch.Tensor, k: PackedStore, scale: float, norm: Optional[torch.Tensor] = None, t0: int = 0,
             T: Optional[int] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """logits [B,Hq,T] fp32 = scale * q . K[t0:t0+T] over a channel-grouped store."""
+    require_f16_store(k, "qk_gemv")
     require_device(q, "q")
     T = k.length - t0 if T is None else T
     check_qk_shapes(q.shape, k, t0, T, None if out is None else out.shape,
@@ -534,6 +573,7 @@ def av_gemv(p: torch.Tensor, v: PackedStore, t0: int = 0, T: Optional[int] = Non
             out: Optional[torch.Tensor] = None, out32: Optional[torch.Tensor] = None,
             accumulate: bool = False) -> torch.Tensor:
     """out [B,Hq,D] = p . V[t0:t0+T] over a token-grouped store (fp16 and/or fp32 outputs)."""
+    require_f16_store(v, "av_gemv")
     require_device(p, "p")
     T = v.length - t0 if T is None else T
     check_av_shapes(p.shape, v, t0, T, [o.shape for o in (out, out32) if o is not None])
@@ -577,6 +617,8 @@ def _segment(dense: Optional[torch.Tensor], store: Optional[PackedStore], n: int
 
 
 def _decode_args(q, k_sink, k_store, k_recent, v_sink, v_store, v_recent, norm, out=None):
+    require_f16_store(k_store, "decode attention K")
+    require_f16_store(v_store, "decode attention V")
     require_device(q, "q")
 
     def shp(t):
@@ -656,10 +698,10 @@ def unpack_store(store: PackedStore, t0: int = 0, T: Optional[int] = None):
     dev = store.device
     codes = torch.empty(B, H, T, D, dtype=torch.int32, device=dev)
     red = (B, H, T, D // G) if store.axis == "channel" else (B, H, T // G, D)
-    scale = torch.empty(red, dtype=torch.float16, device=dev)
-    zs = torch.empty(red if store.mode != IQ_MODE_SYM else (B, H, T, D), dtype=torch.float16, device=dev)
+    scale = torch.empty(red, dtype=store.dtype, device=dev)
+    zs = torch.empty(red if store.mode != IQ_MODE_SYM else (B, H, T, D), dtype=store.dtype, device=dev)
     fn = "iq_unpack_k" if store.axis == "channel" else "iq_unpack_v"
-    call(fn, _p(store.codes), _p(store.meta), store.t_cap, B, H, t0, T, D, G, store.bits, store.mode, _p(codes),
+    call(fn, _p(store.codes), _p(store.meta), store.t_cap, B, H, t0, T, D, G, store.bits, store.mode_arg, _p(codes),
          _p(scale), _p(zs), _stream(dev))
     if store.mode == IQ_MODE_HYBRID:
         return split_hybrid(codes, scale, zs, store.bits, store.group, store.axis)
@@ -678,30 +720,32 @@ def split_hybrid(fields: torch.Tensor, scale_raw: torch.Tensor, zero: torch.Tens
     mask = torch.bitwise_and(raw, -0x8000) != 0
     el = torch.repeat_interleave(mask, group, dim=-1 if axis == "channel" else 2)
     signed = fields - (1 << (bits - 1))
+    dt = scale_raw.dtype
     zero_i, zero_h = torch.zeros((), dtype=torch.int32, device=fields.device), \
-        torch.zeros((), dtype=torch.float16, device=fields.device)
-    s_abs = torch.bitwise_and(raw, 0x7fff).view(torch.float16)
+        torch.zeros((), dtype=dt, device=fields.device)
+    s_abs = torch.bitwise_and(raw, 0x7fff).view(dt)
     codes = {"zp": torch.where(el, zero_i, fields), "nozp": torch.where(el, signed.abs(), zero_i)}
     scale = {"zp": torch.where(mask, zero_h, s_abs), "nozp": torch.where(mask, s_abs, zero_h), "mask": mask}
-    zs = {"zp": torch.where(mask, zero_h, zero), "nozp": torch.where(el, torch.sign(signed).to(torch.float16), zero_h)}
+    zs = {"zp": torch.where(mask, zero_h, zero), "nozp": torch.where(el, torch.sign(signed).to(dt), zero_h)}
     return codes, scale, zs
 
 
 def key_norm_factor(k: torch.Tensor) -> torch.Tensor:
-    """fp16 sqrt(max_t |k|) of k [B,H,T,D] as [B,H,1,D] (cache.py:121-126)."""
-    require_device(k, "key_states")
+    """sqrt(max_t |k|) of k [B,H,T,D] as [B,H,1,D] in k's dtype (cache.py:121-126)."""
+    require_act(k, "key_states")
     if k.stride(-1) != 1:
         k = k.contiguous()
     B, H, T, D = k.shape
-    out = torch.empty(B, H, 1, D, dtype=torch.float16, device=k.device)
-    call("iq_key_norm_factor", _p(k), k.stride(0), k.stride(1), k.stride(2), B, H, T, D, _p(out), _stream(k.device))
+    out = torch.empty(B, H, 1, D, dtype=k.dtype, device=k.device)
+    call("iq_key_norm_factor", _p(k), k.stride(0), k.stride(1), k.stride(2), B, H, T, D, act_flag(k.dtype), _p(out),
+         _stream(k.device))
     return out
 
 
 def hybrid_mask(x: torch.Tensor, deq_a: torch.Tensor, deq_s: torch.Tensor, group: int, axis: str,
                 norm: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Per-group choice of the sym quantization (quant.py:133-151) over [BH,T,D]-viewable tensors."""
-    require_device(x, "tensor")
+    require_act(x, "tensor")
     require_device(deq_a, "deq_zp", torch.float32)
     require_device(deq_s, "deq_nozp", torch.float32)
     *lead, T, D = x.shape
@@ -710,10 +754,10 @@ def hybrid_mask(x: torch.Tensor, deq_a: torch.Tensor, deq_s: torch.Tensor, group
     shape = tuple(lead) + ((T, D // group) if ax == 0 else (T // group, D))
     mask = torch.empty(shape, dtype=torch.bool, device=x.device)
     if norm is not None:
-        require_device(norm, "norm")
+        require_device(norm, "norm", x.dtype)
         norm = norm.reshape(BH, D).contiguous()
     call("iq_hybrid_mask", _p(x.contiguous()), _p(norm), _p(deq_a.contiguous()), _p(deq_s.contiguous()), BH, T, D,
-         group, ax, _p(mask), _stream(x.device))
+         group, ax, act_flag(x.dtype), _p(mask), _stream(x.device))
     return mask
 
 
@@ -725,9 +769,10 @@ def hybrid_select(deq_a: torch.Tensor, deq_s: torch.Tensor, mask: torch.Tensor, 
     require_device(mask, "mask", torch.bool)
     *lead, T, D = deq_a.shape
     BH = int(torch.tensor(lead).prod()) if lead else 1
-    if dtype not in (torch.float32, torch.float16):
-        raise TypeError("op_dtype must be torch.float32 or torch.float16")
+    codes = {torch.float32: 0, torch.float16: 1, torch.bfloat16: 2}
+    if dtype not in codes:
+        raise TypeError("op_dtype must be torch.float32, torch.float16 or torch.bfloat16")
     out = torch.empty(deq_a.shape, dtype=dtype, device=deq_a.device)
     call("iq_hybrid_select", _p(deq_a.contiguous()), _p(deq_s.contiguous()), _p(mask.contiguous()), BH, T, D, group,
-         0 if axis == "channel" else 1, 1 if dtype == torch.float16 else 0, _p(out), _stream(deq_a.device))
+         0 if axis == "channel" else 1, codes[dtype], _p(out), _stream(deq_a.device))
     return out

@@ -38,8 +38,8 @@ class QMode(Enum):
 def _check(tensor, group_size, bit, dim, bits=(2, 3, 4)):
     if not isinstance(tensor, torch.Tensor) or not tensor.is_cuda:
         raise TypeError("innerq_amd.quant works on HIP device tensors (there is no CPU path)")
-    if tensor.dtype != torch.float16:
-        raise TypeError(f"innerq_amd.quant quantizes fp16 tensors, got {tensor.dtype}")
+    if tensor.dtype not in (torch.float16, torch.bfloat16):
+        raise TypeError(f"innerq_amd.quant quantizes fp16 or bf16 tensors, got {tensor.dtype}")
     assert tensor.shape[dim] % group_size == 0
     if group_size not in (32, 64, 128):
         raise ValueError(f"group_size must be 32, 64 or 128, got {group_size}")
@@ -137,6 +137,6 @@ def dequantize_hybrid(zp_func, nozp_func):
         zp_deq = zp_func(tensor['zp'], scale['zp'], sign_or_zp['zp'], group_size, op_dtype)
         nozp_deq = nozp_func(tensor['nozp'], scale['nozp'], sign_or_zp['nozp'], group_size, op_dtype)
         axis = _axis(tuple(tensor['zp'].shape), tuple(scale['zp'].shape))
-        # fp16 -> fp32 is exact, so selecting in fp32 and writing op_dtype is the same selection
+        # fp16 / bf16 -> fp32 is exact, so selecting in fp32 and writing op_dtype is the same selection
         return ops.hybrid_select(zp_deq.float(), nozp_deq.float(), scale['mask'], group_size, axis, dtype=op_dtype)
     return hybrid_func

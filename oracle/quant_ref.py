@@ -63,15 +63,39 @@ def _f16(a):
     return np.asarray(a, dtype=np.float16)
 
 
-def _div16(a, b):
-    """fp16 / fp16 (or fp16 / python int) correctly rounded to fp16."""
+def round_bf16(a):
+    """float32 -> nearest bf16 (ties to even), kept as float32; NaN -> 0x7fc0
+    (torch's c10::BFloat16 conversion).  bf16 arrays here are float32 arrays
+    holding bf16 values."""
+    a = np.asarray(a, np.float32)
+    u = a.view(np.uint32).astype(np.uint64)
+    r = (((u + 0x7FFF + ((u >> 16) & 1)) >> 16) << 16) & 0xFFFF0000
+    r = np.where(np.isnan(a), 0x7FC00000, r).astype(np.uint32)
+    return r.view(np.float32)
+
+
+def bf16_bits(a):
+    return (round_bf16(a).view(np.uint32) >> 16).astype(np.uint16)
+
+
+def bf16_from_bits(u16):
+    return (np.asarray(u16, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def _cast(a, act):
+    """a in the activation dtype: fp16 ('f16') or bf16 values in float32 ('bf16')."""
+    return _f16(a) if act == "f16" else round_bf16(a)
+
+
+def _div16(a, b, act="f16"):
+    """a / b (or a / python int) computed in fp32 and rounded to the activation dtype."""
     with np.errstate(divide="ignore", invalid="ignore", over="ignore"):
-        return (np.asarray(a, np.float32) / np.asarray(b, np.float32)).astype(np.float16)
+        return _cast(np.asarray(a, np.float32) / np.asarray(b, np.float32), act)
 
 
-def _sub16(a, b):
+def _sub16(a, b, act="f16"):
     with np.errstate(invalid="ignore", over="ignore"):
-        return (np.asarray(a, np.float32) - np.asarray(b, np.float32)).astype(np.float16)
+        return _cast(np.asarray(a, np.float32) - np.asarray(b, np.float32), act)
 
 
 def _to_int32_like_torch(y16):
@@ -91,52 +115,53 @@ def _split(x, group, axis):
     return x.reshape(new_shape), red_shape
 
 
-def quantize_asym(x, group_size, bit, expanded_dim):
-    """quant.py:58-73 (asymmetric min/max quantization over groups of ``expanded_dim``)."""
-    x = _f16(x)
+def quantize_asym(x, group_size, bit, expanded_dim, act="f16"):
+    """quant.py:58-73 (asymmetric min/max quantization over groups of ``expanded_dim``).
+    act: 'f16' (fp16 tensors) or 'bf16' (bf16 tensors, every op rounded to bf16)."""
+    x = _cast(x, act)
     shape = x.shape
     xr, red_shape = _split(x, group_size, expanded_dim)
     mn = xr.min(axis=expanded_dim + 1, keepdims=True)      # exact; NaN propagates
     mx = xr.max(axis=expanded_dim + 1, keepdims=True)
     L = 2 ** bit - 1
-    scale = _div16(_sub16(mx, mn), L)                       # quant.py:68
-    y = _div16(_sub16(xr, mn), scale)                       # quant.py:69-70
+    scale = _div16(_sub16(mx, mn, act), L, act)             # quant.py:68
+    y = _div16(_sub16(xr, mn, act), scale, act)             # quant.py:69-70
     y = np.clip(y, 0, L)                                    # clamp keeps NaN
     codes = _to_int32_like_torch(y).reshape(shape)          # quant.py:71
     return codes, scale.reshape(red_shape), mn.reshape(red_shape)
 
 
-def quantize_channeldim_asym(x, group_size, bit):
-    return quantize_asym(x, group_size, bit, np.ndim(x) - 1)
+def quantize_channeldim_asym(x, group_size, bit, act="f16"):
+    return quantize_asym(x, group_size, bit, np.ndim(x) - 1, act)
 
 
-def quantize_tokendim_asym(x, group_size, bit):
-    return quantize_asym(x, group_size, bit, np.ndim(x) - 2)
+def quantize_tokendim_asym(x, group_size, bit, act="f16"):
+    return quantize_asym(x, group_size, bit, np.ndim(x) - 2, act)
 
 
-def quantize_sym(x, group_size, bit, expanded_dim):
+def quantize_sym(x, group_size, bit, expanded_dim, act="f16"):
     """quant.py:95-111 (magnitude codes with b-1 bits + a separate sign tensor)."""
-    x = _f16(x)
+    x = _cast(x, act)
     bit = bit - 1
     shape = x.shape
-    signs = ((x > 0).astype(np.float16) - (x < 0).astype(np.float16))  # torch.sign: +-0, NaN -> 0
+    signs = ((x > 0).astype(x.dtype) - (x < 0).astype(x.dtype))  # torch.sign: +-0, NaN -> 0
     xr, red_shape = _split(x, group_size, expanded_dim)
     a = np.abs(xr)
     mx = a.max(axis=expanded_dim + 1, keepdims=True)
     L = 2 ** bit - 1
-    scale = _div16(mx, L)                                   # quant.py:107
-    y = _div16(a, scale)                                    # quant.py:108
+    scale = _div16(mx, L, act)                              # quant.py:107
+    y = _div16(a, scale, act)                               # quant.py:108
     y = np.clip(y, 0, L)
     codes = _to_int32_like_torch(y).reshape(shape)          # quant.py:109
     return codes, scale.reshape(red_shape), signs
 
 
-def quantize_channeldim_sym(x, group_size, bit):
-    return quantize_sym(x, group_size, bit, np.ndim(x) - 1)
+def quantize_channeldim_sym(x, group_size, bit, act="f16"):
+    return quantize_sym(x, group_size, bit, np.ndim(x) - 1, act)
 
 
-def quantize_tokendim_sym(x, group_size, bit):
-    return quantize_sym(x, group_size, bit, np.ndim(x) - 2)
+def quantize_tokendim_sym(x, group_size, bit, act="f16"):
+    return quantize_sym(x, group_size, bit, np.ndim(x) - 2, act)
 
 
 def dequantize_channeldim_asym(codes, scale, zero, group_size):
@@ -176,10 +201,10 @@ def quantize_hybrid(zp_func, nozp_func, zp_deq_func, nozp_deq_func):
     fp32, so an exact tie-break can differ only when the two errors agree to
     fp32 precision (the golden fixtures pin the reference's choice).
     """
-    def hybrid_func(x, group_size, bit):
-        x = _f16(x)
-        q_zp = zp_func(x, group_size, bit - 1)
-        q_nozp = nozp_func(x, group_size, bit)
+    def hybrid_func(x, group_size, bit, act="f16"):
+        x = _cast(x, act)
+        q_zp = zp_func(x, group_size, bit - 1, act)
+        q_nozp = nozp_func(x, group_size, bit, act)
         d_zp = zp_deq_func(*q_zp, group_size)
         d_nozp = nozp_deq_func(*q_nozp, group_size)
         q_dim = [i for i, (a, b) in enumerate(zip(q_zp[1].shape, x.shape)) if a != b]

@@ -19,6 +19,10 @@ cache_golden.npz    InnerqDynamicLayer.update() traces: prefill + decode steps
                     seed with innerq_amd.synth); full dense K/V of the last
                     decode call, SHA-256 of every call's K/V bytes,
                     and the recent-window lengths after every call.
+bf16_golden.npz     the same quantizers on the quant_golden input cast to bf16
+                    (codes, bf16 scale / zero / sign bits; hybrid masks;
+                    dequantization digests) and update() traces of two presets
+                    on bf16 K/V (a bf16 model's cache: LongBench/pred.py:240).
 sliding_golden.npz  InnerqDynamicSlidingWindowLayer.update() traces
                     (cache.py:421-461) across the window boundary: per call the
                     shapes and SHA-256 of the returned K/V (a single token, the
@@ -26,7 +30,7 @@ sliding_golden.npz  InnerqDynamicSlidingWindowLayer.update() traces
                     reference indexes [:, :, -w, :]), the recent-window lengths
                     and get_mask_sizes() before the call.
 
-Usage:  python tests/golden/make_golden.py [/root/reference] [--sliding-only]
+Usage:  python tests/golden/make_golden.py [/root/reference] [--sliding-only | --bf16-only]
 """
 from __future__ import annotations
 
@@ -134,8 +138,116 @@ def sliding_traces(cache):
     return out
 
 
-def main(root, sliding_only=False):
+PRESETS = {
+    "innerq_base": dict(k_bits=3, v_bits=3, key_flush_size=1, value_flush_size=32, key_group_size=32,
+                        value_group_size=32, key_w_recent=96, value_w_recent=96, key_w_sink=32,
+                        value_w_sink=32, key_normalize=True, key_quantize_over_token=False,
+                        value_quantize_over_token=True, key_quantize_mode="symmetric",
+                        value_quantize_mode="symmetric"),
+    "asym4_nosink": dict(k_bits=4, v_bits=4, key_flush_size=1, value_flush_size=32, key_group_size=32,
+                         value_group_size=32, key_w_recent=32, value_w_recent=64, key_w_sink=0,
+                         value_w_sink=0, key_normalize=False, key_quantize_over_token=False,
+                         value_quantize_over_token=True, key_quantize_mode="asymmetric",
+                         value_quantize_mode="asymmetric"),
+    "mixed_k2v4_flush32": dict(k_bits=2, v_bits=4, key_flush_size=32, value_flush_size=64,
+                               key_group_size=32, value_group_size=32, key_w_recent=40, value_w_recent=70,
+                               key_w_sink=4, value_w_sink=0, key_normalize=False,
+                               key_quantize_over_token=False, value_quantize_over_token=True,
+                               key_quantize_mode="asymmetric", value_quantize_mode="symmetric"),
+    "hybrid_v": dict(k_bits=3, v_bits=2, key_flush_size=1, value_flush_size=32, key_group_size=32,
+                     value_group_size=32, key_w_recent=96, value_w_recent=96, key_w_sink=32,
+                     value_w_sink=32, key_normalize=True, key_quantize_over_token=False,
+                     value_quantize_over_token=True, key_quantize_mode="symmetric",
+                     value_quantize_mode="hybrid"),
+    "k_only": dict(k_bits=4, v_bits=16, key_flush_size=1, key_group_size=64, key_w_recent=16,
+                   key_w_sink=2, key_normalize=False, key_quantize_mode="asymmetric"),
+}
+
+
+def bf16(a):
+    """bf16 tensor -> its uint16 bit patterns."""
+    return a.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+BF16_PRESETS = ("innerq_base", "hybrid_v")
+
+
+def bf16_fixtures(quant, cache, presets):
+    """quant.py and cache.py on bf16 tensors."""
+    out = {}
+    xt = torch.from_numpy(quant_input()).to(torch.bfloat16)
+    out["x"] = bf16(xt)
+    for axis in ("channel", "token"):
+        qa = getattr(quant, f"quantize_{axis}dim_asym")
+        qs = getattr(quant, f"quantize_{axis}dim_sym")
+        da = getattr(quant, f"dequantize_{axis}dim_asym")
+        ds = getattr(quant, f"dequantize_{axis}dim_sym")
+        for bits in (2, 3, 4):
+            for G in (32, 64):
+                c, s, z = qa(xt.clone(), G, bits)
+                key = f"{axis}_asym_b{bits}_g{G}"
+                out[key + "_codes"], out[key + "_scale"], out[key + "_zero"] = codes8(c), bf16(s), bf16(z)
+                c, s, sg = qs(xt.clone(), G, bits)
+                key = f"{axis}_sym_b{bits}_g{G}"
+                out[key + "_codes"], out[key + "_scale"], out[key + "_signs"] = codes8(c), bf16(s), bf16(sg)
+        hq = quant.quantize_hybrid(qa, qs, da, ds)
+        hd = quant.dequantize_hybrid(da, ds)
+        for bits in (2, 3, 4):
+            c, s, z = hq(xt.clone(), 32, bits)
+            key = f"{axis}_hybrid_b{bits}_g32"
+            out[key + "_mask"] = s["mask"].cpu().numpy()
+            deq = hd(c, s, z, 32).cpu().numpy().astype(np.float32)
+            out[key + "_deq_pz_sha256"] = digest(deq + np.float32(0.0))
+        c, s, z = qa(xt.clone(), 32, 4)
+        out[f"{axis}_asym_b4_g32_deq_sha256"] = digest(da(c, s, z, 32).cpu().numpy().astype(np.float32))
+        c, s, z = qs(xt.clone(), 32, 3)
+        out[f"{axis}_sym_b3_g32_deq_pz_sha256"] = digest(ds(c, s, z, 32).cpu().numpy().astype(np.float32)
+                                                         + np.float32(0.0))
+
+    class Layer(cache.InnerqDynamicLayer):
+        def get_max_length(self):   # abstract in the installed transformers
+            return -1
+
+    class Cfg:
+        pass
+
+    B, H, D = 1, 2, 64
+    prefill, steps = 150, 70
+    for name in BF16_PRESETS:
+        cfg = Cfg()
+        for k, v in presets[name].items():
+            setattr(cfg, k, v)
+        layer = Layer(cfg, 0)
+        seed = sum(map(ord, name)) + 16
+        kx = synth.kv_tensor(B, H, prefill + steps, D, seed=seed, n_out=2, factor=8.0)
+        vx = synth.kv_tensor(B, H, prefill + steps, D, seed=seed + 1, n_out=2, factor=8.0)
+        out[f"{name}_seed"] = np.array([seed, B, H, D, prefill, steps])
+        kt = torch.from_numpy(kx).to(torch.bfloat16)
+        vt = torch.from_numpy(vx).to(torch.bfloat16)
+        # digests of the values (fp32, -0.0 read as +0.0: a packed sym field
+        # keeps no sign for a zero code)
+        def pz(K, V):
+            return digest(np.concatenate([K.float().numpy().ravel(), V.float().numpy().ravel()]) + np.float32(0.0))
+
+        K, V = layer.update(kt[:, :, :prefill].clone(), vt[:, :, :prefill].clone())
+        out[f"{name}_step0_pz_sha256"] = pz(K, V)
+        for s in range(steps):
+            K, V = layer.update(kt[:, :, prefill + s:prefill + s + 1].clone(),
+                                vt[:, :, prefill + s:prefill + s + 1].clone())
+            if s == steps - 1:
+                out[f"{name}_step{s + 1}_k"], out[f"{name}_step{s + 1}_v"] = bf16(K), bf16(V)
+            out[f"{name}_step{s + 1}_pz_sha256"] = pz(K, V)
+            out[f"{name}_len{s + 1}"] = np.array([K.shape[-2], V.shape[-2], layer.keys_recent.shape[-2],
+                                                  layer.values_recent.shape[-2]])
+    return out
+
+
+def main(root, sliding_only=False, bf16_only=False):
     quant, cache = load_reference(root)
+    if bf16_only:
+        np.savez_compressed(os.path.join(HERE, "bf16_golden.npz"), **bf16_fixtures(quant, cache, PRESETS))
+        print("wrote", os.path.join(HERE, "bf16_golden.npz"))
+        return
     np.savez_compressed(os.path.join(HERE, "sliding_golden.npz"), **sliding_traces(cache))
     print("wrote", os.path.join(HERE, "sliding_golden.npz"))
     if sliding_only:
@@ -197,30 +309,7 @@ def main(root, sliding_only=False):
     class Cfg:
         pass
 
-    presets = {
-        "innerq_base": dict(k_bits=3, v_bits=3, key_flush_size=1, value_flush_size=32, key_group_size=32,
-                            value_group_size=32, key_w_recent=96, value_w_recent=96, key_w_sink=32,
-                            value_w_sink=32, key_normalize=True, key_quantize_over_token=False,
-                            value_quantize_over_token=True, key_quantize_mode="symmetric",
-                            value_quantize_mode="symmetric"),
-        "asym4_nosink": dict(k_bits=4, v_bits=4, key_flush_size=1, value_flush_size=32, key_group_size=32,
-                             value_group_size=32, key_w_recent=32, value_w_recent=64, key_w_sink=0,
-                             value_w_sink=0, key_normalize=False, key_quantize_over_token=False,
-                             value_quantize_over_token=True, key_quantize_mode="asymmetric",
-                             value_quantize_mode="asymmetric"),
-        "mixed_k2v4_flush32": dict(k_bits=2, v_bits=4, key_flush_size=32, value_flush_size=64,
-                                   key_group_size=32, value_group_size=32, key_w_recent=40, value_w_recent=70,
-                                   key_w_sink=4, value_w_sink=0, key_normalize=False,
-                                   key_quantize_over_token=False, value_quantize_over_token=True,
-                                   key_quantize_mode="asymmetric", value_quantize_mode="symmetric"),
-        "hybrid_v": dict(k_bits=3, v_bits=2, key_flush_size=1, value_flush_size=32, key_group_size=32,
-                         value_group_size=32, key_w_recent=96, value_w_recent=96, key_w_sink=32,
-                         value_w_sink=32, key_normalize=True, key_quantize_over_token=False,
-                         value_quantize_over_token=True, key_quantize_mode="symmetric",
-                         value_quantize_mode="hybrid"),
-        "k_only": dict(k_bits=4, v_bits=16, key_flush_size=1, key_group_size=64, key_w_recent=16,
-                       key_w_sink=2, key_normalize=False, key_quantize_mode="asymmetric"),
-    }
+    presets = PRESETS
     trace = {}
     B, H, D = 1, 2, 64
     prefill, steps = 150, 70
@@ -246,9 +335,11 @@ def main(root, sliding_only=False):
             trace[f"{name}_len{s + 1}"] = np.array([K.shape[-2], V.shape[-2],
                                                     layer.keys_recent.shape[-2], layer.values_recent.shape[-2]])
     np.savez_compressed(os.path.join(HERE, "cache_golden.npz"), **trace)
+    np.savez_compressed(os.path.join(HERE, "bf16_golden.npz"), **bf16_fixtures(quant, cache, PRESETS))
     print("wrote", os.path.join(HERE, "quant_golden.npz"), os.path.join(HERE, "cache_golden.npz"))
 
 
 if __name__ == "__main__":
     args = [a for a in sys.argv[1:] if not a.startswith("--")]
-    main(args[0] if args else "/root/reference", sliding_only="--sliding-only" in sys.argv)
+    main(args[0] if args else "/root/reference", sliding_only="--sliding-only" in sys.argv,
+         bf16_only="--bf16-only" in sys.argv)

@@ -12,9 +12,9 @@ import torch
 from innerq_amd import ops
 
 
-def _filled(axis, bits, mode, length, t_cap, seed):
+def _filled(axis, bits, mode, length, t_cap, seed, dtype=torch.float16):
     g = torch.Generator().manual_seed(seed)
-    st = ops.PackedStore(axis, 2, 3, 128, 32, bits, mode, "cpu", t_cap=t_cap)
+    st = ops.PackedStore(axis, 2, 3, 128, 32, bits, mode, "cpu", t_cap=t_cap, dtype=dtype)
     st.codes.copy_(torch.randint(-2**31, 2**31 - 1, st.codes.shape, dtype=torch.int32, generator=g))
     st.meta.copy_(torch.randint(-2**15, 2**15 - 1, st.meta.shape, dtype=torch.int16, generator=g))
     st.length = length
@@ -55,7 +55,29 @@ def test_header_fields():
     n = struct.unpack("<Q", blob[:8])[0]
     md = json.loads(blob[8:8 + n])["__metadata__"]
     assert md == {"format": "innerq-packed-store", "version": "1", "axis": "channel", "B": "2", "H": "3",
-                  "D": "128", "group": "32", "bits": "4", "mode": "asymmetric", "length": "70", "unit": "64"}
+                  "D": "128", "group": "32", "bits": "4", "mode": "asymmetric", "length": "70", "unit": "64",
+                  "dtype": "float16"}
+
+
+def test_bf16_store_keeps_its_dtype(tmp_path):
+    st = _filled("token", 3, "hybrid", 96, 128, seed=3, dtype=torch.bfloat16)
+    back = ops.PackedStore.from_bytes(st.to_bytes(), "cpu")
+    assert back.dtype == torch.bfloat16 and back.mode_arg == st.mode_arg
+    for a, b in zip(_units(st), _units(back)):
+        assert torch.equal(a, b)
+
+
+def test_blob_without_dtype_reads_as_fp16():
+    # blobs written before the dtype key existed are fp16 stores
+    st = _filled("channel", 4, "asymmetric", 70, 128, seed=1)
+    blob = st.to_bytes()
+    n = struct.unpack("<Q", blob[:8])[0]
+    hdr = json.loads(blob[8:8 + n])
+    del hdr["__metadata__"]["dtype"]
+    h = json.dumps(hdr, sort_keys=True, separators=(",", ":")).encode()
+    h += b" " * (-len(h) % 8)
+    back = ops.PackedStore.from_bytes(struct.pack("<Q", len(h)) + h + blob[8 + n:], "cpu")
+    assert back.dtype == torch.float16
 
 
 def test_foreign_and_inconsistent_blobs_are_refused():
