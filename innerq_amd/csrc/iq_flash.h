@@ -346,6 +346,7 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS, AVO>::NT), (fused_waves_pe
 
   const PlanRegs<KB> prk;
   const PlanRegs<VB> prv;
+  const SumRegs<VB> srv(hl);
   // ---- work: this workgroup's share [i0, i1) of its side's list of splits
   // (detail::ShareMap: contiguous, equal shares, one workgroup per CU; each
   // XCD, or each XCD pair, streams a contiguous part of the cache), processed
@@ -460,11 +461,13 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS, AVO>::NT), (fused_waves_pe
     }
   };
 
-  // the lane's tokens' slots in the attn.V operand records and their code biases
+  // the lane's tokens' slots in the attn.V operand records
   int tk[FBPW], thi[FBPW];
-  float tb[FBPW];
 #pragma unroll
-  for (int j = 0; j < FBPW; ++j) plan_inv<VB>((j * TOKEN_BLOCK + lane) % G, tk[j], thi[j], tb[j]);
+  for (int j = 0; j < FBPW; ++j) {
+    float tb;
+    plan_inv<VB>((j * TOKEN_BLOCK + lane) % G, tk[j], thi[j], tb);
+  }
 
   Run run = run_at(i0);
   int rs2 = i0 + run.nsplit;                // first split of the next run (i1: none)
@@ -529,7 +532,7 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS, AVO>::NT), (fused_waves_pe
       // ---- softmax against the running max (log2 domain); fp16 p straight
       // into the V records ----
       auto& vrec = sm.vrec[wave];
-      float mw[NREP], ps[VPW][NREP], alpha[NREP];
+      float mw[NREP], alpha[NREP];
       bool rescale = false;  // the running max moved: the run state is rescaled by alpha
       if constexpr (!AVO) {
         // Each comparison with the lazy threshold is its own ballot (a lane
@@ -571,12 +574,10 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS, AVO>::NT), (fused_waves_pe
           }
         }
       }
-      // x[h]: p; x[NREP + h]: -p * bias (the attn.V accumulators' seed)
-      float x[2 * NREP], pb[VPW][NREP];
+      // p into the wave's attn.V operand records, as the fp16 the matrix
+      // cores see (the zero-point term and l are sums of the same values)
 #pragma unroll
       for (int h = 0; h < NREP; ++h) {
-        x[h] = 0.f;
-        x[NREP + h] = 0.f;
 #pragma unroll
         for (int j = 0; j < FBPW; ++j) {
           uint16_t p16;
@@ -591,72 +592,49 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS, AVO>::NT), (fused_waves_pe
           }
           const int tl = j * TOKEN_BLOCK + lane;  // token within the wave
           reinterpret_cast<uint16_t*>(&vrec[tl / G][h * NP + tk[j]])[thi[j]] = p16;
-          const float pf = h2f(p16);  // the zero-point term uses the fp16 p the matrix cores see
-          x[h] += pf;
-          x[NREP + h] = fmaf(-pf, tb[j], x[NREP + h]);
-        }
-      }
-      // per (V group, head): sums over the group's tokens
-      if constexpr (G == 32) {  // two groups per wave: lanes 0-31 and 32-63
-        sum_step<0xb1>(x);
-        sum_step<0x4e>(x);
-        sum_step<0x141>(x);
-        sum_step<0x140>(x);
-#pragma unroll
-        for (int h = 0; h < 2 * NREP; ++h) {
-          x[h] += __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x[h]), 0x142, 0xa,
-                                                                        0xf, false));
-          const float s0 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x[h]), 31));
-          const float s1 = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, x[h]), 63));
-          if (h < NREP) { ps[0][h] = s0; ps[1][h] = s1; }
-          else { pb[0][h - NREP] = s0; pb[1][h - NREP] = s1; }
-        }
-      } else {
-        static_assert(VPW == 1, "one V group per wave for G >= 64");
-        wave_sum_dpp(x);
-#pragma unroll
-        for (int h = 0; h < NREP; ++h) {
-          ps[0][h] = x[h];
-          pb[0][h] = x[NREP + h];
         }
       }
       if constexpr (!AVO) {
+        if (rescale) {
+          asm volatile("");
 #pragma unroll
-        for (int h = 0; h < NREP; ++h) {
-          float lsum = 0.f;
-#pragma unroll
-          for (int u = 0; u < VPW; ++u) lsum += ps[u][h];
-          if (rescale) {
-            asm volatile("");
-            l_run[h] = fmaf(l_run[h], alpha[h], lsum);
+          for (int h = 0; h < NREP; ++h) {
+            l_run[h] *= alpha[h];
 #pragma unroll
             for (int e = 0; e < DPL; ++e) o_run[h][e] *= alpha[h];
-          } else {
-            l_run[h] += lsum;
           }
         }
       }
       wave_lds_sync();
 
-      // ---- attn.V over the wave's V groups, from registers ----
+      // ---- attn.V over the wave's V groups, from registers; the same
+      // matrix-core products sum p and p * bias per (group, head) ----
       const int vcnt = max(0, min(VPW, (a.T - wt0) / G));  // the wave's V groups inside the range
 #pragma unroll
       for (int u = 0; u < VPW; ++u) {
         if (u < vcnt) {
-          f4_t init[NQ], dv[DPL][NQ];
+          f4_t dv[DPL][NQ], dsum[NQ];
+          group_mfma_biased_sums<VB, G, NREP, DPL>(v.w[u], &vrec[u][0], hl, prv, srv, dv, dsum);
+          float ps[NREP], pbs[NREP];  // sum(p), sum(p * bias): lanes hl = 0, 1 of every 4-lane block
 #pragma unroll
-          for (int q = 0; q < NQ; ++q)
+          for (int h = 0; h < NREP; ++h) {
+            // (a float first: __builtin_bit_cast of a vector element reads element 0)
+            const int d = __float_as_int(float(dsum[h / 4][h % 4]));
+            ps[h] = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, d, 0x00, 0xf, 0xf, false));
+            pbs[h] = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, d, 0x55, 0xf, 0xf, false));
+          }
+          if constexpr (!AVO) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) init[q][i] = 4 * q + i < NREP ? pb[u][4 * q + i] : 0.f;
-          group_mfma_biased<VB, G, NREP, DPL>(v.w[u], &vrec[u][0], hl, prv, init, dv);
+            for (int h = 0; h < NREP; ++h) l_run[h] += ps[h];
+          }
 #pragma unroll
           for (int e = 0; e < DPL; ++e) {
             float s, z;
             if constexpr (VH) meta_sz_hyb<VB>(v.m[u][e], s, z);
             else meta_sz<VB>(v.m[u][e], vsh, a.vsym, s, z);
 #pragma unroll
-            for (int h = 0; h < NREP; ++h)
-              o_run[h][e] = fmaf(s, dv[e][h / 4][h % 4], fmaf(z, ps[u][h], o_run[h][e]));
+            for (int h = 0; h < NREP; ++h)  // codes = biased codes - bias
+              o_run[h][e] = fmaf(s, dv[e][h / 4][h % 4] - pbs[h], fmaf(z, ps[h], o_run[h][e]));
           }
         }
       }

@@ -129,12 +129,42 @@ __device__ __forceinline__ f4_t mfma4(h4_t a, h4_t b, f4_t c) {
 
 __device__ __forceinline__ h4_t cat_h2(h2_t lo, h2_t hi) { return __builtin_shufflevector(lo, hi, 0, 1, 2, 3); }
 
+// The sum operand of the attn.V products.  In v_mfma_f32_4x4x4f16 each 4-lane
+// block computes D[i][c] = sum_k A[i][k] B[k][c], with A row i from lane i of
+// the block (the record row of head 4q + i) and B column c from lane c.  B
+// column 0 of ones and column 1 of the four fields' code biases (the fields
+// of pairs 2st and 2st + 1 of the plan) make the same A, already loaded for
+// the code products, give sum(p) and sum(p * bias) of every head over the
+// group in lanes hl = 0 and hl = 1 (columns 2 and 3 are zero): one matrix-core
+// instruction per step instead of a 64-lane reduction per head.  One h4 per
+// step of a plan period, lane constants built once per kernel.
+template <int BITS>
+struct SumRegs {
+  static constexpr int NS = Plan<BITS>::NPAIR / 2;  // steps per plan period
+  h4_t b[NS];
+  __device__ __forceinline__ explicit SumRegs(int hl) {
+#pragma unroll
+    for (int st = 0; st < NS; ++st) {
+      const uint32_t ones = 0x3c003c00u;
+      const uint32_t b0 = uint32_t(__half_as_ushort(__float2half_rn(bias_a<BITS>(2 * st)))) |
+                          (uint32_t(__half_as_ushort(__float2half_rn(bias_c<BITS>(2 * st)))) << 16);
+      const uint32_t b1 = uint32_t(__half_as_ushort(__float2half_rn(bias_a<BITS>(2 * st + 1)))) |
+                          (uint32_t(__half_as_ushort(__float2half_rn(bias_c<BITS>(2 * st + 1)))) << 16);
+      uint32_t lo = hl == 0 ? ones : hl == 1 ? b0 : 0u;
+      uint32_t hi = hl == 0 ? ones : hl == 1 ? b1 : 0u;
+      asm("" : "+v"(lo), "+v"(hi));  // kept in VGPRs, not rebuilt in the loops
+      b[st] = cat_h2(__builtin_bit_cast(h2_t, lo), __builtin_bit_cast(h2_t, hi));
+    }
+  }
+};
+
 // Pairs [K0, K0+CH) of one group: A rows from the record (head 4q + hl; heads
-// past NREP read as zero), B from the NB code-word sets.
-template <int BITS, int W, int NREP, int NB, int K0, bool BIASED, typename P, int... K>
+// past NREP read as zero), B from the NB code-word sets; with SUMS also the
+// sums of the A rows (SumRegs) into dsum.
+template <int BITS, int W, int NREP, int NB, int K0, bool BIASED, bool SUMS, typename P, int... K>
 __device__ __forceinline__ void mfma_chunk(const uint32_t (&w)[NB][W], P rec, int NP, int hl,
                                            const PlanRegs<BITS>& pr, f4_t (&dv)[NB][(NREP + 3) / 4],
-                                           std::integer_sequence<int, K...>) {
+                                           const SumRegs<BITS>* sr, f4_t* dsum, std::integer_sequence<int, K...>) {
   constexpr int NPS = Plan<BITS>::NPAIR;
   constexpr int SBW = Plan<BITS>::WORDS;
   constexpr int CH = sizeof...(K);
@@ -168,18 +198,21 @@ __device__ __forceinline__ void mfma_chunk(const uint32_t (&w)[NB][W], P rec, in
       const h4_t a4 = cat_h2(__builtin_bit_cast(h2_t, av[q][2 * st]), __builtin_bit_cast(h2_t, av[q][2 * st + 1]));
 #pragma unroll
       for (int j = 0; j < NB; ++j) dv[j][q] = mfma4(a4, cat_h2(x[j][2 * st], x[j][2 * st + 1]), dv[j][q]);
+      if constexpr (SUMS) dsum[q] = mfma4(a4, sr->b[((K0 + 2 * st) % NPS) / 2], dsum[q]);
     }
   }
 }
 
-template <int BITS, int G, int NREP, int NB, int C, int NCH, bool BIASED, typename P>
+template <int BITS, int G, int NREP, int NB, int C, int NCH, bool BIASED, bool SUMS = false, typename P>
 __device__ __forceinline__ void mfma_chunks(const uint32_t (&w)[NB][G * BITS / 32], P rec, int hl,
-                                            const PlanRegs<BITS>& pr, f4_t (&dv)[NB][(NREP + 3) / 4]) {
+                                            const PlanRegs<BITS>& pr, f4_t (&dv)[NB][(NREP + 3) / 4],
+                                            const SumRegs<BITS>* sr = nullptr, f4_t* dsum = nullptr) {
   if constexpr (C < NCH) {
     constexpr int CH = (G / 2) / NCH;
-    mfma_chunk<BITS, G * BITS / 32, NREP, NB, C * CH, BIASED>(w, rec, G / 2, hl, pr, dv,
-                                                              std::make_integer_sequence<int, CH>{});
-    mfma_chunks<BITS, G, NREP, NB, C + 1, NCH, BIASED>(w, rec, hl, pr, dv);
+    static_assert(!SUMS || (CH % 2 == 0 && (C * CH) % 2 == 0), "sum steps cover whole pairs of pairs");
+    mfma_chunk<BITS, G * BITS / 32, NREP, NB, C * CH, BIASED, SUMS>(w, rec, G / 2, hl, pr, dv, sr, dsum,
+                                                                    std::make_integer_sequence<int, CH>{});
+    mfma_chunks<BITS, G, NREP, NB, C + 1, NCH, BIASED, SUMS>(w, rec, hl, pr, dv, sr, dsum);
   }
 }
 
@@ -263,6 +296,24 @@ __device__ __forceinline__ void group_mfma_biased(const uint32_t (&w)[NB][G * BI
 #pragma unroll
     for (int q = 0; q < (NREP + 3) / 4; ++q) dv[j][q] = init[q];
   mfma_chunks<BITS, G, NREP, NB, 0, NCH, true>(w, rec, hl, pr, dv);
+}
+
+// group_mfma_biased from zero accumulators, plus the record rows' sums:
+// dsum[q] element i holds, in the lanes with hl = 0, sum(p) of head 4q + i
+// over the group and, in the lanes with hl = 1, sum(p * bias) (SumRegs).
+template <int BITS, int G, int NREP, int NB, typename P>
+__device__ __forceinline__ void group_mfma_biased_sums(const uint32_t (&w)[NB][G * BITS / 32], P rec, int hl,
+                                                       const PlanRegs<BITS>& pr, const SumRegs<BITS>& sr,
+                                                       f4_t (&dv)[NB][(NREP + 3) / 4], f4_t (&dsum)[(NREP + 3) / 4]) {
+  constexpr int NP = G / 2;
+  constexpr int NCH = NP <= IQ_MFMA_CH ? 1 : NP / IQ_MFMA_CH;
+#pragma unroll
+  for (int q = 0; q < (NREP + 3) / 4; ++q) {
+    dsum[q] = f4_t{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int j = 0; j < NB; ++j) dv[j][q] = f4_t{0.f, 0.f, 0.f, 0.f};
+  }
+  mfma_chunks<BITS, G, NREP, NB, 0, NCH, true, true>(w, rec, hl, pr, dv, &sr, &dsum[0]);
 }
 
 // Query dot products of NB code sets: d[j][h] = sum_i q'[h,i] c_j[i] over the
