@@ -115,6 +115,14 @@ struct DenseArgs {
   float scale;
   float* ml;  // the dense split slots' statistics: slot s at ml + s * rows * 2
   float* o;   // and partial outputs: slot s at o + s * rows * D
+  // merging instance (after the fused kernel): its run partials (slots
+  // [0, nruns) of the workspace, ShareMap(fgrid, B * Hkv, fnsf, fpair_e0))
+  // and the output, fp16 [B, Hq, D] at b * sob + hq * soh
+  const float* fml;
+  const float* fpart;
+  int fgrid, fnsf, fpair_e0;
+  uint16_t* out;
+  int64_t sob, soh;
 };
 
 // ---- packed rows of a dense chunk (kernels with packed segments) ----
@@ -271,24 +279,40 @@ __device__ __forceinline__ void packed_run(const Seg& K, const Seg& V, const uin
 // running (m, l), and thread (head, column pair) accumulates the output.  The
 // probability that meets V is rounded to fp16, as the reference rounds its
 // softmax output; logits, sums and outputs are fp32.
-template <int D, int NREP, bool PK>
-__global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs a) {
+// MERGE (launched after the fused kernel, one workgroup of two 256-thread
+// halves per (batch, KV head)): each half takes half of the dense tokens as
+// its slice, side by side, and the workgroup then merges the two halves'
+// states with the fused kernel's run partials of the head and writes the
+// output, in place of the dense slots and the combine launch.
+template <int D, int NREP, bool PK, bool MERGE = false>
+__global__ __launch_bounds__(MERGE ? 512 : 256) void dense_attn_kernel(DenseArgs a) {
+  static_assert(!(PK && MERGE), "the merging instance takes fp16 segments only");
+  constexpr int NH = MERGE ? 2 : 1;           // slices per workgroup (256-thread halves)
+  constexpr int NTH = 256 * NH;
   constexpr int KS = D / 2 + 1;               // K tile row stride in dwords (odd: no bank conflicts)
   constexpr int HPW = (NREP + 3) / 4;         // heads per wave
   constexpr int NPR = D / 2;                  // column pairs per head
   constexpr int OPT = (NREP * NPR + 255) / 256;  // (head, pair) items per thread
   constexpr int RE = D / 4;                   // row elements per gathering thread
-  __shared__ uint32_t kt[DT][KS];
-  __shared__ uint32_t vt[DT][D / 2];
+  __shared__ uint32_t kts[NH][DT][KS];
+  __shared__ uint32_t vts[NH][DT][D / 2];
   __shared__ float qs[NREP][D];
-  __shared__ float ps[NREP][DT];
-  __shared__ float al[NREP];
+  __shared__ float pss[NH][NREP][DT];
+  __shared__ float als[NH][NREP];
   __shared__ __align__(16) uint32_t stg[PK ? Stage<D>::N : 4];
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int half = MERGE ? int(threadIdx.x >> 8) : 0;
+  auto& kt = kts[half];
+  auto& vt = vts[half];
+  auto& ps = pss[half];
+  auto& al = als[half];
+  const int tid = int(threadIdx.x) & 255, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave within the half
   const int bh = blockIdx.y, b = bh / a.Hkv, kvh = bh % a.Hkv;
   const int n0 = a.hi0 - a.lo0, n = n0 + (a.hi1 - a.lo1);
-  const int i0 = int(int64_t(blockIdx.x) * n / gridDim.x), i1 = int(int64_t(blockIdx.x + 1) * n / gridDim.x);
+  const int nsl = MERGE ? NH : int(gridDim.x), sl = MERGE ? half : int(blockIdx.x);  // slices, this one
+  const int i0 = int(int64_t(sl) * n / nsl), i1 = int(int64_t(sl + 1) * n / nsl);
+  // chunks: the same count in both halves (their barriers are shared)
+  const int nch = MERGE ? ((n + NH - 1) / NH + DT - 1) / DT : (i1 - i0 + DT - 1) / DT;
   const int64_t rows = int64_t(gridDim.y) * NREP;
 
   // gathering: thread = (row tid / 4, quarter tid % 4 of the row)
@@ -301,9 +325,26 @@ __global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs a) {
     kpk = gather_row<RE>(a.k, b, kvh, t, gq * RE, kr);
     vpk = gather_row<RE>(a.v, b, kvh, t, gq * RE, vr);
   };
-  // the first chunk's rows and the query are loaded together (one round trip)
+  // the first chunk's rows and the query are loaded together (one round trip);
+  // MERGE: so are the fused runs' statistics and partials of the thread's
+  // first output element (up to NRPRE runs; more are read at the merge)
+  constexpr int NRPRE = 4;
+  float pm[NRPRE], pl[NRPRE], po[NRPRE];
+  int nr = 0;
+  if constexpr (MERGE) {
+    nr = detail::ShareMap::make(a.fgrid, int(gridDim.y), a.fnsf, a.fpair_e0).nruns(bh);
+    const int r = int(threadIdx.x);
+    const int64_t row = int64_t(bh) * NREP + min(r / D, NREP - 1);
+#pragma unroll
+    for (int sp = 0; sp < NRPRE; ++sp) {
+      const int64_t sr = int64_t(min(sp, nr - 1)) * rows + row;  // clamped: every load issued at once
+      pm[sp] = a.fml[sr * 2];
+      pl[sp] = a.fml[sr * 2 + 1];
+      po[sp] = a.fpart[sr * D + r % D];
+    }
+  }
   if (i0 < i1) gather(i0);
-  for (int i = tid; i < NREP * D; i += 256)
+  for (int i = int(threadIdx.x); i < NREP * D; i += NTH)
     qs[i / D][i % D] = h2f(a.q[b * a.sqb + (kvh * NREP + i / D) * a.sqh + i % D]);
   float m[HPW], l[HPW];
 #pragma unroll
@@ -312,7 +353,10 @@ __global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs a) {
 #pragma unroll
   for (int it = 0; it < OPT; ++it) o[it][0] = o[it][1] = 0.f;
 
-  for (int c0 = i0; c0 < i1; c0 += DT) {
+  for (int ci = 0; ci < nch; ++ci) {
+    // a chunk past the slice's tokens (MERGE: the shorter half) has no live
+    // token: its logits are -inf and no V row is read
+    const int c0 = i0 + ci * DT;
     // the fp16 rows from registers; packed rows are decoded into the tiles
     // (disjoint rows: no ordering needed between the two)
     if (!kpk) {
@@ -351,7 +395,7 @@ __global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs a) {
       }
     }
     const bool live = c0 + lane < i1;
-    if (wave < 4) {  // DPP reductions over the wave's heads at once
+    {  // DPP reductions over the wave's heads at once
       float x[HPW], mx[HPW], cs[HPW];
 #pragma unroll
       for (int hh = 0; hh < HPW; ++hh) {
@@ -405,6 +449,64 @@ __global__ __launch_bounds__(256) void dense_attn_kernel(DenseArgs a) {
       }
     }
     __syncthreads();
+  }
+  if constexpr (MERGE) {
+    // ---- merge: the two halves' states and the fused runs' partials ----
+    __shared__ float mh[NH][NREP], lh[NH][NREP];
+    __shared__ float oh[NH][NREP][D];
+#pragma unroll
+    for (int hh = 0; hh < HPW; ++hh) {
+      const int h = wave + 4 * hh;
+      if (h < NREP && lane == 0) {
+        mh[half][h] = m[hh];
+        lh[half][h] = l[hh];
+      }
+    }
+#pragma unroll
+    for (int it = 0; it < OPT; ++it) {
+      const int idx = tid + 256 * it;
+      if (idx < NREP * NPR) {
+        const int h = idx / NPR, dp = idx % NPR;
+        oh[half][h][2 * dp] = o[it][0];
+        oh[half][h][2 * dp + 1] = o[it][1];
+      }
+    }
+    __syncthreads();
+    for (int r = int(threadIdx.x); r < NREP * D; r += NTH) {
+      const int h = r / D, dd = r % D;
+      const int64_t row = int64_t(bh) * NREP + h;
+      const bool pre = r < NTH;  // the preloaded element
+      auto run_m = [&](int sp) { return pre && sp < NRPRE ? pm[sp] : a.fml[(int64_t(sp) * rows + row) * 2]; };
+      float M = -INFINITY;
+#pragma unroll
+      for (int hf = 0; hf < NH; ++hf) M = fmaxf(M, mh[hf][h]);
+#pragma unroll
+      for (int sp = 0; sp < NRPRE; ++sp)
+        if (sp < nr) M = fmaxf(M, run_m(sp));
+      for (int sp = NRPRE; sp < nr; ++sp) M = fmaxf(M, run_m(sp));
+      float L = 0.f, acc = 0.f;
+      auto add_run = [&](int sp) {  // the runs in slot order, then the halves
+        const int64_t sr = int64_t(sp) * rows + row;
+        const bool p = pre && sp < NRPRE;
+        const float ms = p ? pm[sp] : a.fml[sr * 2];
+        const float w = ms == -INFINITY ? 0.f : __expf(ms - M);
+        L = fmaf(w, p ? pl[sp] : a.fml[sr * 2 + 1], L);
+        const float pv = p ? po[sp] : a.fpart[sr * D + dd];
+        acc = w != 0.f ? fmaf(w, pv, acc) : acc;
+      };
+#pragma unroll
+      for (int sp = 0; sp < NRPRE; ++sp)
+        if (sp < nr) add_run(sp);
+      for (int sp = NRPRE; sp < nr; ++sp) add_run(sp);
+#pragma unroll
+      for (int hf = 0; hf < NH; ++hf) {
+        const float w = mh[hf][h] == -INFINITY ? 0.f : __expf(mh[hf][h] - M);
+        L = fmaf(w, lh[hf][h], L);
+        acc = fmaf(w, oh[hf][h][dd], acc);
+      }
+      a.out[b * a.sob + (int64_t(kvh) * NREP + h) * a.soh + dd] = __half_as_ushort(__float2half_rn(acc / L));
+    }
+    return;
   }
   // ---- this slice's statistics and unnormalized output (an empty slice:
   // m = -inf, which the combine skips) ----
@@ -614,15 +716,28 @@ int check_decode(const void* q, const iq_segment* k, const iq_segment* v, int B,
 // combine that scans every slot).
 struct SplitPlan {
   int nsplit = 0, nsf = 0, grid = 0, nrep = 1;
-  int pair_e0 = 0;  // the fused kernel's partition (detail::ShareMap)
+  int pair_e0 = 0;      // the fused kernel's partition (detail::ShareMap)
+  bool merged = false;  // the output is written (dense window and merge after the fused kernel)
 };
+
+// The output of a full decode call (what the merging dense kernel writes)
+struct MergeOut {
+  void* out;
+  int64_t so_b, so_h;
+};
+// dense tokens per (batch, KV head), at most, that the merging dense kernel
+// takes (two halves of up to 2 chunks each); longer windows take the slices
+constexpr int MERGE_DENSE_MAX = 4 * DT;
 
 // Launches everything up to the split statistics and partials.  `live`: the
 // combine will be told the fused kernel's workgroup count and read only the
-// live slots (the fused kernel then writes no empty statistics).
+// live slots (the fused kernel then writes no empty statistics).  `mo` (a full
+// call): where the output goes when a short fp16 window is attended after the
+// fused kernel by the merging dense kernel, which also writes the output
+// (plan->merged: no combine launch).
 int launch_splits(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, const iq_segment* k,
                   const iq_segment* v, int B, int Hq, int Hkv, int T, int D, float scale, const Workspace& w,
-                  SplitPlan* plan, bool live, hipStream_t st) {
+                  SplitPlan* plan, bool live, hipStream_t st, const MergeOut* mo = nullptr) {
   *plan = SplitPlan{};
   plan->nrep = Hq / Hkv;
   const int64_t rows = int64_t(B) * Hq;
@@ -668,19 +783,22 @@ int launch_splits(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, c
   da.ml = w.ml + int64_t(nsf) * rows * 2;
   da.o = w.part + int64_t(nsf) * rows * D;
   const int n_dense = (da.hi0 - da.lo0) + (da.hi1 - da.lo1);
+  const int64_t bhs = int64_t(B) * Hkv;
+  // any packed segment (tokens packed in only one of K and V) needs the
+  // general gather; a dense-only step takes the short kernel
+  auto packed_in_range = [&](const Seg& g) {
+    auto meets = [&](int lo, int hi) { return lo < hi && g.start < hi && lo < g.start + g.n; };
+    return g.n > 0 && !g.dense && (meets(da.lo0, da.hi0) || meets(da.lo1, da.hi1));
+  };
+  bool pk = false;
+  for (int s = 0; s < 3; ++s) pk |= packed_in_range(da.k[s]) || packed_in_range(da.v[s]);
+  // A short fp16-only window next to the fused kernel: the dense work and the
+  // merge run in one kernel after the fused one (no dense slots, no combine)
+  const bool merge_dense = mo && live && fused && n_dense > 0 && n_dense <= MERGE_DENSE_MAX && !pk;
   int nsd = 0;
-  if (n_dense > 0) {
-    const int64_t bhs = int64_t(B) * Hkv;
+  if (n_dense > 0 && !merge_dense) {
     nsd = int(std::min<int64_t>({NSD_MAX, ceil_div(n_dense, DSLICE), std::max<int64_t>(1, ceil_div(2 * detail::num_cus(), bhs))}));
     const dim3 grid{unsigned(nsd), unsigned(bhs), 1u};
-    // any packed segment (tokens packed in only one of K and V) needs the
-    // general gather; a dense-only step takes the short kernel
-    auto packed_in_range = [&](const Seg& g) {
-      auto meets = [&](int lo, int hi) { return lo < hi && g.start < hi && lo < g.start + g.n; };
-      return g.n > 0 && !g.dense && (meets(da.lo0, da.hi0) || meets(da.lo1, da.hi1));
-    };
-    bool pk = false;
-    for (int s = 0; s < 3; ++s) pk |= packed_in_range(da.k[s]) || packed_in_range(da.v[s]);
     auto go = [&]<int DD, int R>() {
       if (pk) dense_attn_kernel<DD, R, true><<<grid, 256, 0, st>>>(da);
       else dense_attn_kernel<DD, R, false><<<grid, 256, 0, st>>>(da);
@@ -705,6 +823,30 @@ int launch_splits(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, c
       return e;
     plan->grid = grid;
     plan->pair_e0 = detail::fused_pair_e0(k[1].bits, v[1].bits, v[1].mode == IQ_MODE_HYBRID);
+    if (merge_dense) {
+      da.fml = w.ml;
+      da.fpart = w.part;
+      da.fgrid = grid;
+      da.fnsf = nsf;
+      da.fpair_e0 = plan->pair_e0;
+      da.out = (uint16_t*)mo->out;
+      da.sob = mo->so_b;
+      da.soh = mo->so_h;
+      const dim3 mgrid{1u, unsigned(bhs), 1u};
+      auto go = [&]<int DD, int R>() { dense_attn_kernel<DD, R, false, true><<<mgrid, 512, 0, st>>>(da); };
+      auto by_r = [&]<int DD>() {
+        switch (Hq / Hkv) {
+          case 1: go.template operator()<DD, 1>(); break;
+          case 2: go.template operator()<DD, 2>(); break;
+          case 4: go.template operator()<DD, 4>(); break;
+          default: go.template operator()<DD, 8>(); break;
+        }
+      };
+      if (D == 128) by_r.template operator()<128>();
+      else by_r.template operator()<64>();
+      if (int e = launch_status()) return e;
+      plan->merged = true;
+    }
   } else if (c) {
     const iq_segment& kg = k[1];
     const iq_segment& vg = v[1];
@@ -796,8 +938,11 @@ int iq_decode_attention_noalloc(const void* q, int64_t sq_b, int64_t sq_h, const
   if (int e = scratch_address(&ws)) return e;
   const Workspace w = carve(ws, B, Hq, T, D);
   SplitPlan plan;
-  if (int e = launch_splits(q, sq_b, sq_h, norm, k, v, B, Hq, Hkv, T, D, scale, w, &plan, true, (hipStream_t)stream))
+  const MergeOut mo{out, so_b, so_h};
+  if (int e = launch_splits(q, sq_b, sq_h, norm, k, v, B, Hq, Hkv, T, D, scale, w, &plan, true, (hipStream_t)stream,
+                            &mo))
     return e;
+  if (plan.merged) return IQ_OK;
   return launch_combine(w, plan, B, Hq, D, out, so_b, so_h, (hipStream_t)stream);
 }
 
@@ -847,8 +992,11 @@ int iq_decode_attention(const void* q, int64_t sq_b, int64_t sq_h, const void* n
   if (B == 0) return IQ_OK;
   const Workspace w = carve(workspace, B, Hq, T, D);
   SplitPlan plan;
-  if (int e = launch_splits(q, sq_b, sq_h, norm, k, v, B, Hq, Hkv, T, D, scale, w, &plan, true, (hipStream_t)stream))
+  const MergeOut mo{out, so_b, so_h};
+  if (int e = launch_splits(q, sq_b, sq_h, norm, k, v, B, Hq, Hkv, T, D, scale, w, &plan, true, (hipStream_t)stream,
+                            &mo))
     return e;
+  if (plan.merged) return IQ_OK;
   return launch_combine(w, plan, B, Hq, D, out, so_b, so_h, (hipStream_t)stream);
 }
 
