@@ -438,6 +438,24 @@ def test_decode_attention_fused_and_dense_ranges(kseg, vseg):
     assert err < TOL
 
 
+# fp16 windows of up to 256 tokens next to the fused range (K and V laid out
+# alike) are attended after the fused kernel by the merging dense kernel: two
+# halves of the window side by side, then the merge with the fused runs'
+# partials; 257 tokens take the dense slices and the combine.  Odd and one-token
+# windows (an empty half), sinks and recents together, 8 query heads per KV
+# head (two output elements per thread at D = 128), D = 64.
+@pytest.mark.parametrize("seg,nrep,D", [
+    ((0, 64 * 8, 1), 4, 128),
+    ((16, 64 * 8, 17), 8, 128),
+    ((0, 64 * 6, 255), 2, 64),
+    ((128, 64 * 6, 128), 8, 128),
+    ((1, 64 * 6, 256), 4, 128),
+])
+def test_decode_attention_window_after_fused_kernel(seg, nrep, D):
+    err = _decode_case(2, 2, nrep, D, seg, seg, (4, 32, "asymmetric"), (4, 32, "asymmetric"), seed=sum(seg) + nrep)
+    assert err < TOL
+
+
 @pytest.mark.parametrize("kfmt,vfmt", [((3, 32, "symmetric"), (3, 32, "symmetric")),
                                        ((2, 64, "asymmetric"), (4, 64, "symmetric")),
                                        ((4, 128, "asymmetric"), (2, 128, "asymmetric")),
