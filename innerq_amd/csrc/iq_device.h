@@ -13,25 +13,22 @@
 // v_and_or_b32, which yields two fp16 values {bias_a + c_a, bias_b + c_b}
 // exactly (field LSB weight 1, bias 2^(10-p) for a field at in-half bit p).
 // The fused decode kernel feeds these biased pairs to the matrix cores as
-// they are and removes the biases in the accumulation (exact powers of two):
-// QK^T starts from -sum(q * bias), summed once per query record, and attn.V
-// subtracts sum(p * bias), which the same matrix-core products sum; the
-// unfused kernels remove the bias with one v_pk_add_f16 per pair (exact: both
-// operands are integers below 2048).  A field may sit anywhere in its half's
-// 10-bit mantissa (p = 0 .. 10 - b), so a bias is at most 1024 code units and
-// the biased fp32 partial sums at most ~2^10 times the code sums: a relative
-// error of ~1e-5 per dot product, far below the 1e-3 parity bar.  Allowing
-// p = 0 (instead of p >= 2) saves a shifted window per 4-bit or 2-bit word
-// and four per 3-bit super-block.  Sym codes are offset
-// binary (u = signed + 2^(b-1)), so sum(q*signed) = sum(q*u) - 2^(b-1)*sum(q),
+// they are and starts each accumulation from -sum(operand * bias) (exact
+// powers of two, summed once per operand record), so the bias costs no VALU;
+// the unfused kernels remove it with one v_pk_add_f16 per pair (exact: both
+// operands are integers below 2048).  The plans keep every field at p >= 10 -
+// b - 4 or so, i.e. bias / code unit <= 256 (4-bit), 64 (2-bit), 128 (3-bit):
+// the fp32 partial sums stay within ~2^8 of the result, a relative error of a
+// few 1e-6 per 128-code dot product.  Sym codes are offset binary
+// (u = signed + 2^(b-1)), so sum(q*signed) = sum(q*u) - 2^(b-1)*sum(q),
 // folded into the zero term: sym and asym unpack alike.
 //
-// Plans (found by exhaustive search for the fewest windows; S = window start
-// bit, word-aligned windows are free, every pair is one v_and_or_b32):
-//   4-bit, per word (8 codes):   pairs (i, i+4); S = 0, 0, 8, 8  (1 shift)
-//   2-bit, per word (16 codes):  pairs (i, i+8); S = 0 x5, 6 x3  (1 shift)
-//   3-bit, per 3 words (32 codes): 16 pairs over 7 windows, 4 of them shifts
-//          or alignbits (20 VALU per 32 codes).
+// Plans (found by exhaustive search for the fewest windows under that bias
+// bound; S = window start bit, word-aligned windows are free):
+//   4-bit, per word (8 codes):   pairs (i, i+4); S = -6, 0, 6, 6  (2 shifts)
+//   2-bit, per word (16 codes):  pairs (i, i+8); S = -6,-6, 0,0,0, 6,6,6
+//   3-bit, per 3 words (32 codes): 16 pairs over 11 windows, 8 of them
+//          shifts or alignbits (24 VALU per 32 codes).
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -51,21 +48,21 @@ template <int BITS> struct Plan;
 
 template <> struct Plan<4> {
   static constexpr int WORDS = 1, CODES = 8, NPAIR = 4;
-  static constexpr int S[NPAIR] = {0, 0, 8, 8};
+  static constexpr int S[NPAIR] = {-6, 0, 6, 6};
   static constexpr int A[NPAIR] = {0, 1, 2, 3};
   static constexpr int C[NPAIR] = {4, 5, 6, 7};
 };
 template <> struct Plan<2> {
   static constexpr int WORDS = 1, CODES = 16, NPAIR = 8;
-  static constexpr int S[NPAIR] = {0, 0, 0, 0, 0, 6, 6, 6};
+  static constexpr int S[NPAIR] = {-6, -6, 0, 0, 0, 6, 6, 6};
   static constexpr int A[NPAIR] = {0, 1, 2, 3, 4, 5, 6, 7};
   static constexpr int C[NPAIR] = {8, 9, 10, 11, 12, 13, 14, 15};
 };
 template <> struct Plan<3> {
   static constexpr int WORDS = 3, CODES = 32, NPAIR = 16;
-  static constexpr int S[NPAIR] = {0, 0, 6, 6, 12, 12, 32, 32, 41, 41, 41, 64, 64, 71, 71, 71};
-  static constexpr int A[NPAIR] = {0, 1, 2, 3, 4, 5, 12, 13, 14, 15, 16, 22, 23, 24, 25, 26};
-  static constexpr int C[NPAIR] = {6, 7, 8, 9, 10, 11, 17, 18, 19, 20, 21, 27, 28, 29, 30, 31};
+  static constexpr int S[NPAIR] = {-4, -4, 0, 5, 5, 26, 26, 32, 32, 35, 53, 58, 61, 64, 71, 71};
+  static constexpr int A[NPAIR] = {0, 1, 2, 3, 4, 10, 11, 12, 13, 14, 20, 21, 22, 23, 25, 26};
+  static constexpr int C[NPAIR] = {5, 6, 7, 8, 9, 15, 16, 17, 18, 19, 24, 27, 28, 29, 30, 31};
 };
 
 template <int BITS> __host__ __device__ constexpr int pa_of(int k) { return BITS * Plan<BITS>::A[k] - Plan<BITS>::S[k]; }
@@ -80,15 +77,15 @@ template <int BITS> __host__ __device__ constexpr float bias_a(int k) { return f
 template <int BITS> __host__ __device__ constexpr float bias_c(int k) { return float(1 << (10 - pc_of<BITS>(k))); }
 
 // A plan is valid when its pairs cover every code of the super-block once,
-// every field lies inside its half's 10-bit mantissa (bias <= 1024 code
-// units), and every window is one the window() helper can form.
+// every field lies inside its half's 10-bit mantissa at p >= 2 (bias <= 256
+// code units), and every window is one the window() helper can form.
 template <int BITS>
 constexpr bool plan_valid() {
   using P = Plan<BITS>;
   int seen[P::CODES] = {};
   for (int k = 0; k < P::NPAIR; ++k) {
     const int pa = pa_of<BITS>(k), pc = pc_of<BITS>(k);
-    if (pa < 0 || pa > 10 - BITS || pc < 0 || pc > 10 - BITS) return false;
+    if (pa < 2 || pa > 10 - BITS || pc < 2 || pc > 10 - BITS) return false;
     if (P::S[k] < -9 || P::S[k] >= 32 * P::WORDS) return false;
     ++seen[P::A[k]];
     ++seen[P::C[k]];

@@ -22,10 +22,9 @@
 //
 // The B operand is either the code pair itself (unfused kernels: the bias
 // pair is subtracted with one v_pk_add_f16) or the biased magic-number pair
-// (fused kernel: QK^T accumulations start from -sum(q * bias), taken from the
-// query record; attn.V subtracts sum(p * bias), summed by the same matrix-core
-// products, SumRegs).  The biases are at most 2^10 code units (iq_device.h),
-// a relative error of ~1e-5 per fp32 dot product.
+// (fused kernel: each accumulation starts from -sum(opnd * bias) instead of
+// 0, taken from the operand record).  The pair plans keep the biases within
+// 2^8 code units (iq_device.h), so the fp32 partial sums stay small.
 #pragma once
 
 #include <utility>
