@@ -296,8 +296,8 @@ __global__ __launch_bounds__(MERGE ? 512 : 256) void dense_attn_kernel(DenseArgs
   constexpr int RE = D / 4;                   // row elements per gathering thread
   __shared__ uint32_t kts[NH][DT][KS];
   __shared__ uint32_t vts[NH][DT][D / 2];
-  __shared__ float qs[NREP][D];
-  __shared__ float pss[NH][NREP][DT];
+  __shared__ uint32_t qs2[NREP][D / 2];  // the query heads' fp16 pairs
+  __shared__ __align__(4) uint16_t pss[NH][NREP][DT];  // fp16 probabilities
   __shared__ float als[NH][NREP];
   __shared__ __align__(16) uint32_t stg[PK ? Stage<D>::N : 4];
   const int half = MERGE ? int(threadIdx.x >> 8) : 0;
@@ -344,8 +344,11 @@ __global__ __launch_bounds__(MERGE ? 512 : 256) void dense_attn_kernel(DenseArgs
     }
   }
   if (i0 < i1) gather(i0);
-  for (int i = int(threadIdx.x); i < NREP * D; i += NTH)
-    qs[i / D][i % D] = h2f(a.q[b * a.sqb + (kvh * NREP + i / D) * a.sqh + i % D]);
+  for (int i = int(threadIdx.x); i < NREP * D / 2; i += NTH) {
+    const int h = i / (D / 2), c = i % (D / 2);
+    const uint16_t* qr = a.q + b * a.sqb + (kvh * NREP + h) * a.sqh + 2 * c;
+    qs2[h][c] = uint32_t(qr[0]) | (uint32_t(qr[1]) << 16);
+  }
   float m[HPW], l[HPW];
 #pragma unroll
   for (int hh = 0; hh < HPW; ++hh) { m[hh] = -INFINITY; l[hh] = 0.f; }
@@ -384,14 +387,15 @@ __global__ __launch_bounds__(MERGE ? 512 : 256) void dense_attn_kernel(DenseArgs
     // no per-iteration guard on the head (a wave-uniform branch in the loop
     // serialized it on LDS latency): heads past NREP read the last head's
     // query and their logits are dropped below
+    // one v_dot2_f32_f16 per (head, column pair): both fp16 products exact,
+    // accumulated in fp32
 #pragma unroll 16
     for (int i = 0; i < D / 2; ++i) {
-      const uint32_t k2 = kt[lane][i];
-      const float k0 = h2f(uint16_t(k2 & 0xffffu)), k1 = h2f(uint16_t(k2 >> 16));
+      const h2_t k2 = __builtin_bit_cast(h2_t, kt[lane][i]);
 #pragma unroll
       for (int hh = 0; hh < HPW; ++hh) {
         const int h = min(wave + 4 * hh, NREP - 1);
-        dot[hh] = fmaf(qs[h][2 * i + 1], k1, fmaf(qs[h][2 * i], k0, dot[hh]));
+        dot[hh] = __builtin_amdgcn_fdot2(k2, __builtin_bit_cast(h2_t, qs2[h][i]), dot[hh], false);
       }
     }
     const bool live = c0 + lane < i1;
@@ -414,7 +418,7 @@ __global__ __launch_bounds__(MERGE ? 512 : 256) void dense_attn_kernel(DenseArgs
       for (int hh = 0; hh < HPW; ++hh) {
         const int h = wave + 4 * hh;
         if (h < NREP) {
-          ps[h][lane] = __half2float(__float2half_rn(x[hh]));
+          ps[h][lane] = __half_as_ushort(__float2half_rn(x[hh]));
           const float alpha = m[hh] == -INFINITY ? 0.f : __expf(m[hh] - mx[hh]);
           l[hh] = fmaf(l[hh], alpha, cs[hh]);
           m[hh] = mx[hh];
@@ -425,7 +429,9 @@ __global__ __launch_bounds__(MERGE ? 512 : 256) void dense_attn_kernel(DenseArgs
     __syncthreads();
     // ---- attn.V: thread = (head, column pair), eight tokens per step in two
     // accumulation chains (the tile rows past the chunk's tokens are zero and
-    // their p is 0, so the chunk is read in whole steps) ----
+    // their p is 0, so the chunk is read in whole steps); per two tokens and
+    // column a v_dot2_f32_f16 of (v_j, v_j+1) (one v_perm_b32 from the two
+    // rows' pairs) and the fp16 (p_j, p_j+1) ----
     const int cnt8 = (min(DT, i1 - c0) + 7) & ~7;
 #pragma unroll
     for (int it = 0; it < OPT; ++it) {
@@ -435,13 +441,20 @@ __global__ __launch_bounds__(MERGE ? 512 : 256) void dense_attn_kernel(DenseArgs
         float o0 = o[it][0] * al[h], o1 = o[it][1] * al[h], e0 = 0.f, e1 = 0.f;
         for (int j = 0; j < cnt8; j += 8) {
 #pragma unroll
-          for (int u = 0; u < 8; u += 2) {
-            const float pa = ps[h][j + u], pb = ps[h][j + u + 1];
+          for (int u = 0; u < 8; u += 4) {
+            const uint32_t pq = *reinterpret_cast<const uint32_t*>(&ps[h][j + u]);
+            const uint32_t pr = *reinterpret_cast<const uint32_t*>(&ps[h][j + u + 2]);
             const uint32_t va = vt[j + u][dp], vb = vt[j + u + 1][dp];
-            o0 = fmaf(pa, h2f(uint16_t(va & 0xffffu)), o0);
-            o1 = fmaf(pa, h2f(uint16_t(va >> 16)), o1);
-            e0 = fmaf(pb, h2f(uint16_t(vb & 0xffffu)), e0);
-            e1 = fmaf(pb, h2f(uint16_t(vb >> 16)), e1);
+            const uint32_t vc = vt[j + u + 2][dp], vd = vt[j + u + 3][dp];
+            // columns 2 dp and 2 dp + 1 of tokens (j+u, j+u+1), then (j+u+2, j+u+3)
+            o0 = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_t, __builtin_amdgcn_perm(vb, va, 0x05040100u)),
+                                        __builtin_bit_cast(h2_t, pq), o0, false);
+            o1 = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_t, __builtin_amdgcn_perm(vb, va, 0x07060302u)),
+                                        __builtin_bit_cast(h2_t, pq), o1, false);
+            e0 = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_t, __builtin_amdgcn_perm(vd, vc, 0x05040100u)),
+                                        __builtin_bit_cast(h2_t, pr), e0, false);
+            e1 = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_t, __builtin_amdgcn_perm(vd, vc, 0x07060302u)),
+                                        __builtin_bit_cast(h2_t, pr), e1, false);
           }
         }
         o[it][0] = o0 + e0;
