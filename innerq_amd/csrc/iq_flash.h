@@ -620,8 +620,10 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS, AVO>::NT), (fused_waves_pe
           for (int h = 0; h < NREP; ++h) {
             // (a float first: __builtin_bit_cast of a vector element reads element 0)
             const int d = __float_as_int(float(dsum[h / 4][h % 4]));
-            ps[h] = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, d, 0x00, 0xf, 0xf, false));
-            pbs[h] = __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, d, 0x55, 0xf, 0xf, false));
+            // quad broadcasts; every source lane is valid, so no old value
+            // (update_dpp with an old value cost a v_mov per broadcast)
+            ps[h] = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(d, 0x00, 0xf, 0xf, true));
+            pbs[h] = __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(d, 0x55, 0xf, 0xf, true));
           }
           if constexpr (!AVO) {
 #pragma unroll
