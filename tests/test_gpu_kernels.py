@@ -443,9 +443,11 @@ def test_decode_attention_fused_and_dense_ranges(kseg, vseg):
 # halves of the window side by side, then the merge with the fused runs'
 # partials; 257 tokens take the dense slices and the combine.  Odd and one-token
 # windows (an empty half), sinks and recents together, 8 query heads per KV
-# head (two output elements per thread at D = 128), D = 64.
+# head (two output elements per thread at D = 128), D = 64, and a long packed
+# range (32 fused runs per head: the runs past the four preloaded ones).
 @pytest.mark.parametrize("seg,nrep,D", [
     ((0, 64 * 8, 1), 4, 128),
+    ((0, 64 * 128, 100), 4, 128),
     ((16, 64 * 8, 17), 8, 128),
     ((0, 64 * 6, 255), 2, 64),
     ((128, 64 * 6, 128), 8, 128),
