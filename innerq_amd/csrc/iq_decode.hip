@@ -162,17 +162,19 @@ __device__ __forceinline__ float staged_value(const uint32_t* codes, const uint3
 
 // one run of the chunk: rows [r0, r1) hold tokens base + r.  Stages, decodes
 // and leaves the workgroup synchronized (the tiles' packed rows written).
-template <int D>
+// Run by 256 threads (a workgroup, or one half of a merging workgroup: ALLB,
+// whose halves share the barriers, so both always take both of them).
+template <int D, bool ALLB = false>
 __device__ __forceinline__ void packed_run(const Seg& K, const Seg& V, const uint16_t* norm, int64_t bh, int base,
                                            int r0, int r1, uint32_t* stg, uint16_t* ktile, int kld,
                                            uint16_t* vtile) {
   using S = Stage<D>;
-  const int tid = threadIdx.x;
+  const int tid = int(threadIdx.x) & 255;
   // the run's packed rows per list: [ka, kb) and [va, vb)
   const int ka = max(r0, K.start - base), kb = K.dense ? ka : min(r1, K.start + K.n - base);
   const int va = max(r0, V.start - base), vb = V.dense ? va : min(r1, V.start + V.n - base);
   const bool kon = kb > ka, von = vb > va;
-  if (!kon && !von) return;  // uniform
+  if (!ALLB && !kon && !von) return;  // uniform
   // ---- stage: every load first ----
   int kblk0 = 0, vg0 = 0, nk4 = 0, nv4 = 0, nkm = 0, nvm = 0;
   const uint4 *kc = nullptr, *vc = nullptr;
@@ -286,7 +288,6 @@ __device__ __forceinline__ void packed_run(const Seg& K, const Seg& V, const uin
 // output, in place of the dense slots and the combine launch.
 template <int D, int NREP, bool PK, bool MERGE = false>
 __global__ __launch_bounds__(MERGE ? 512 : 256) void dense_attn_kernel(DenseArgs a) {
-  static_assert(!(PK && MERGE), "the merging instance takes fp16 segments only");
   constexpr int NH = MERGE ? 2 : 1;           // slices per workgroup (256-thread halves)
   constexpr int NTH = 256 * NH;
   constexpr int KS = D / 2 + 1;               // K tile row stride in dwords (odd: no bank conflicts)
@@ -299,12 +300,13 @@ __global__ __launch_bounds__(MERGE ? 512 : 256) void dense_attn_kernel(DenseArgs
   __shared__ uint32_t qs2[NREP][D / 2];  // the query heads' fp16 pairs
   __shared__ __align__(4) uint16_t pss[NH][NREP][DT];  // fp16 probabilities
   __shared__ float als[NH][NREP];
-  __shared__ __align__(16) uint32_t stg[PK ? Stage<D>::N : 4];
+  __shared__ __align__(16) uint32_t stgs[PK ? NH : 1][PK ? Stage<D>::N : 4];  // packed-row staging per half
   const int half = MERGE ? int(threadIdx.x >> 8) : 0;
   auto& kt = kts[half];
   auto& vt = vts[half];
   auto& ps = pss[half];
   auto& al = als[half];
+  uint32_t* stg = stgs[PK ? half : 0];
   const int tid = int(threadIdx.x) & 255, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave within the half
   const int bh = blockIdx.y, b = bh / a.Hkv, kvh = bh % a.Hkv;
@@ -375,8 +377,8 @@ __global__ __launch_bounds__(MERGE ? 512 : 256) void dense_attn_kernel(DenseArgs
       const int rend = min(DT, i1 - c0), rs = min(max(n0 - c0, 0), rend);
       uint16_t* kth = reinterpret_cast<uint16_t*>(&kt[0][0]);
       uint16_t* vth = reinterpret_cast<uint16_t*>(&vt[0][0]);
-      packed_run<D>(a.k[1], a.v[1], a.norm, bh64, a.lo0 + c0, 0, rs, stg, kth, 2 * KS, vth);
-      packed_run<D>(a.k[1], a.v[1], a.norm, bh64, a.lo1 + c0 - n0, rs, rend, stg, kth, 2 * KS, vth);
+      packed_run<D, MERGE>(a.k[1], a.v[1], a.norm, bh64, a.lo0 + c0, 0, rs, stg, kth, 2 * KS, vth);
+      packed_run<D, MERGE>(a.k[1], a.v[1], a.norm, bh64, a.lo1 + c0 - n0, rs, rend, stg, kth, 2 * KS, vth);
     }
     __syncthreads();
     if (c0 + DT < i1) gather(c0 + DT);  // in flight through this chunk
@@ -488,29 +490,32 @@ __global__ __launch_bounds__(MERGE ? 512 : 256) void dense_attn_kernel(DenseArgs
     for (int r = int(threadIdx.x); r < NREP * D; r += NTH) {
       const int h = r / D, dd = r % D;
       const int64_t row = int64_t(bh) * NREP + h;
-      const bool pre = r < NTH;  // the preloaded element
-      auto run_m = [&](int sp) { return pre && sp < NRPRE ? pm[sp] : a.fml[(int64_t(sp) * rows + row) * 2]; };
+      const bool pre = r < NTH;  // the preloaded element (registers indexed by constants only)
       float M = -INFINITY;
 #pragma unroll
       for (int hf = 0; hf < NH; ++hf) M = fmaxf(M, mh[hf][h]);
 #pragma unroll
       for (int sp = 0; sp < NRPRE; ++sp)
-        if (sp < nr) M = fmaxf(M, run_m(sp));
-      for (int sp = NRPRE; sp < nr; ++sp) M = fmaxf(M, run_m(sp));
+        if (sp < nr) M = fmaxf(M, pre ? pm[sp] : a.fml[(int64_t(sp) * rows + row) * 2]);
+      for (int sp = NRPRE; sp < nr; ++sp) M = fmaxf(M, a.fml[(int64_t(sp) * rows + row) * 2]);
       float L = 0.f, acc = 0.f;
-      auto add_run = [&](int sp) {  // the runs in slot order, then the halves
-        const int64_t sr = int64_t(sp) * rows + row;
-        const bool p = pre && sp < NRPRE;
-        const float ms = p ? pm[sp] : a.fml[sr * 2];
+      auto add_run = [&](float ms, float ls, float pv) {  // the runs in slot order, then the halves
         const float w = ms == -INFINITY ? 0.f : __expf(ms - M);
-        L = fmaf(w, p ? pl[sp] : a.fml[sr * 2 + 1], L);
-        const float pv = p ? po[sp] : a.fpart[sr * D + dd];
+        L = fmaf(w, ls, L);
         acc = w != 0.f ? fmaf(w, pv, acc) : acc;
       };
 #pragma unroll
-      for (int sp = 0; sp < NRPRE; ++sp)
-        if (sp < nr) add_run(sp);
-      for (int sp = NRPRE; sp < nr; ++sp) add_run(sp);
+      for (int sp = 0; sp < NRPRE; ++sp) {
+        if (sp < nr) {
+          const int64_t sr = int64_t(sp) * rows + row;
+          if (pre) add_run(pm[sp], pl[sp], po[sp]);
+          else add_run(a.fml[sr * 2], a.fml[sr * 2 + 1], a.fpart[sr * D + dd]);
+        }
+      }
+      for (int sp = NRPRE; sp < nr; ++sp) {
+        const int64_t sr = int64_t(sp) * rows + row;
+        add_run(a.fml[sr * 2], a.fml[sr * 2 + 1], a.fpart[sr * D + dd]);
+      }
 #pragma unroll
       for (int hf = 0; hf < NH; ++hf) {
         const float w = mh[hf][h] == -INFINITY ? 0.f : __expf(mh[hf][h] - M);
@@ -805,9 +810,10 @@ int launch_splits(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, c
   };
   bool pk = false;
   for (int s = 0; s < 3; ++s) pk |= packed_in_range(da.k[s]) || packed_in_range(da.v[s]);
-  // A short fp16-only window next to the fused kernel: the dense work and the
-  // merge run in one kernel after the fused one (no dense slots, no combine)
-  const bool merge_dense = mo && live && fused && n_dense > 0 && n_dense <= MERGE_DENSE_MAX && !pk;
+  // A short window next to the fused kernel (fp16 tokens and tokens packed in
+  // only one of K and V): the dense work and the merge run in one kernel after
+  // the fused one (no dense slots, no combine)
+  const bool merge_dense = mo && live && fused && n_dense > 0 && n_dense <= MERGE_DENSE_MAX;
   int nsd = 0;
   if (n_dense > 0 && !merge_dense) {
     nsd = int(std::min<int64_t>({NSD_MAX, ceil_div(n_dense, DSLICE), std::max<int64_t>(1, ceil_div(2 * detail::num_cus(), bhs))}));
@@ -846,7 +852,10 @@ int launch_splits(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, c
       da.sob = mo->so_b;
       da.soh = mo->so_h;
       const dim3 mgrid{1u, unsigned(bhs), 1u};
-      auto go = [&]<int DD, int R>() { dense_attn_kernel<DD, R, false, true><<<mgrid, 512, 0, st>>>(da); };
+      auto go = [&]<int DD, int R>() {
+        if (pk) dense_attn_kernel<DD, R, true, true><<<mgrid, 512, 0, st>>>(da);
+        else dense_attn_kernel<DD, R, false, true><<<mgrid, 512, 0, st>>>(da);
+      };
       auto by_r = [&]<int DD>() {
         switch (Hq / Hkv) {
           case 1: go.template operator()<DD, 1>(); break;
