@@ -308,23 +308,38 @@ __device__ __forceinline__ uint64_t seg_mask() {
     return ((1ull << G) - 1ull) << (lane & ~(G - 1));
   }
 }
+// Segment reductions (G = 32 or 64 lanes; every lane gets the result): DPP
+// butterflies inside each 16-lane row (quad xor 1, quad xor 2, half-row
+// mirror, row mirror: one VALU instruction each), then the rows: xor 16 by
+// ds_swizzle (bit-mask mode, no address), and for G = 64 the two halves by
+// readlane.  min, max and or give the same result in any order.
+template <int G, typename F>
+__device__ __forceinline__ uint32_t seg_reduce(uint32_t x, F op) {
+  static_assert(G == 32 || G == 64, "segments of 32 or 64 lanes");
+  x = op(x, uint32_t(__builtin_amdgcn_mov_dpp(int(x), 0xb1, 0xf, 0xf, true)));   // quad_perm [1,0,3,2]
+  x = op(x, uint32_t(__builtin_amdgcn_mov_dpp(int(x), 0x4e, 0xf, 0xf, true)));   // quad_perm [2,3,0,1]
+  x = op(x, uint32_t(__builtin_amdgcn_mov_dpp(int(x), 0x141, 0xf, 0xf, true)));  // row_half_mirror
+  x = op(x, uint32_t(__builtin_amdgcn_mov_dpp(int(x), 0x140, 0xf, 0xf, true)));  // row_mirror
+  x = op(x, uint32_t(__builtin_amdgcn_ds_swizzle(int(x), 0x401f)));             // lane ^ 16
+  if constexpr (G == 64)
+    x = op(uint32_t(__builtin_amdgcn_readlane(int(x), 0)), uint32_t(__builtin_amdgcn_readlane(int(x), 32)));
+  return x;
+}
 template <int G>
 __device__ __forceinline__ float seg_fmin(float x) {
-#pragma unroll
-  for (int o = 1; o < G; o <<= 1) x = fminf(x, __shfl_xor(x, o, 64));
-  return x;
+  return __uint_as_float(seg_reduce<G>(__float_as_uint(x), [](uint32_t a, uint32_t b) {
+    return __float_as_uint(fminf(__uint_as_float(a), __uint_as_float(b)));
+  }));
 }
 template <int G>
 __device__ __forceinline__ float seg_fmax(float x) {
-#pragma unroll
-  for (int o = 1; o < G; o <<= 1) x = fmaxf(x, __shfl_xor(x, o, 64));
-  return x;
+  return __uint_as_float(seg_reduce<G>(__float_as_uint(x), [](uint32_t a, uint32_t b) {
+    return __float_as_uint(fmaxf(__uint_as_float(a), __uint_as_float(b)));
+  }));
 }
 template <int G>
 __device__ __forceinline__ uint32_t seg_or(uint32_t x) {
-#pragma unroll
-  for (int o = 1; o < G; o <<= 1) x |= uint32_t(__shfl_xor(int(x), o, 64));
-  return x;
+  return seg_reduce<G>(x, [](uint32_t a, uint32_t b) { return a | b; });
 }
 
 // lane i of the segment holds element v of the group; every lane of the
