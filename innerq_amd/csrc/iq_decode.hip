@@ -30,6 +30,7 @@ namespace {
 constexpr int DT = 64;        // dense tokens per chunk
 constexpr int NSD_MAX = 4;    // split slots of the dense tokens, at most
 constexpr int DSLICE = 32;    // dense tokens per split slot, at least
+constexpr int MERGE_RUNS_MAX = 4;  // fused runs per (batch, KV head) the merging dense kernel preloads
 
 struct Seg {
   const uint16_t* dense;
@@ -330,7 +331,7 @@ __global__ __launch_bounds__(MERGE ? 512 : 256) void dense_attn_kernel(DenseArgs
   // the first chunk's rows and the query are loaded together (one round trip);
   // MERGE: so are the fused runs' statistics and partials of the thread's
   // first output element (up to NRPRE runs; more are read at the merge)
-  constexpr int NRPRE = 4;
+  constexpr int NRPRE = MERGE_RUNS_MAX;
   float pm[NRPRE], pl[NRPRE], po[NRPRE];
   int nr = 0;
   if constexpr (MERGE) {
@@ -810,12 +811,9 @@ int launch_splits(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, c
   };
   bool pk = false;
   for (int s = 0; s < 3; ++s) pk |= packed_in_range(da.k[s]) || packed_in_range(da.v[s]);
-  // A short window next to the fused kernel (fp16 tokens and tokens packed in
-  // only one of K and V): the dense work and the merge run in one kernel after
-  // the fused one (no dense slots, no combine)
-  const bool merge_dense = mo && live && fused && n_dense > 0 && n_dense <= MERGE_DENSE_MAX;
+  // The dense slices: split slots nsf .. nsf + nsd - 1, read by the combine
   int nsd = 0;
-  if (n_dense > 0 && !merge_dense) {
+  auto launch_slices = [&]() -> int {
     nsd = int(std::min<int64_t>({NSD_MAX, ceil_div(n_dense, DSLICE), std::max<int64_t>(1, ceil_div(2 * detail::num_cus(), bhs))}));
     const dim3 grid{unsigned(nsd), unsigned(bhs), 1u};
     auto go = [&]<int DD, int R>() {
@@ -832,8 +830,19 @@ int launch_splits(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, c
     };
     if (D == 128) by_r.template operator()<128>();
     else by_r.template operator()<64>();
-    if (int e = launch_status()) return e;
-  }
+    return launch_status();
+  };
+  // A short window next to the fused kernel (fp16 tokens and tokens packed in
+  // only one of K and V) may be attended after the fused kernel by the merging
+  // dense kernel, which also merges the fused runs and writes the output (no
+  // dense slots, no combine): chosen once the fused kernel's workgroup count
+  // is known, if no (batch, KV head) has more fused runs than that kernel
+  // preloads.  Heads spread over more workgroups (a small batch over a long
+  // context) take the slices and the combine, which reads every slot in one
+  // round of loads.
+  const bool merge_cand = mo && live && fused && n_dense > 0 && n_dense <= MERGE_DENSE_MAX;
+  if (n_dense > 0 && !merge_cand)
+    if (int e = launch_slices()) return e;
 
   if (fused) {
     int grid = 0;
@@ -842,6 +851,13 @@ int launch_splits(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, c
       return e;
     plan->grid = grid;
     plan->pair_e0 = detail::fused_pair_e0(k[1].bits, v[1].bits, v[1].mode == IQ_MODE_HYBRID);
+    bool merge_dense = merge_cand;
+    if (merge_cand) {
+      const detail::ShareMap sm = detail::ShareMap::make(grid, int(bhs), nsf, plan->pair_e0);
+      for (int h = 0; h < int(bhs) && merge_dense; ++h) merge_dense = sm.nruns(h) <= MERGE_RUNS_MAX;
+      if (!merge_dense)
+        if (int e = launch_slices()) return e;
+    }
     if (merge_dense) {
       da.fml = w.ml;
       da.fpart = w.part;

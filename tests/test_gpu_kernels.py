@@ -444,7 +444,9 @@ def test_decode_attention_fused_and_dense_ranges(kseg, vseg):
 # partials; 257 tokens take the dense slices and the combine.  Odd and one-token
 # windows (an empty half), sinks and recents together, 8 query heads per KV
 # head (two output elements per thread at D = 128), D = 64, and a long packed
-# range (32 fused runs per head: the runs past the four preloaded ones).
+# range (32 fused runs per head, more than the merging kernel preloads: the
+# window then takes the dense slices, launched after the fused kernel, and the
+# combine).
 @pytest.mark.parametrize("seg,nrep,D", [
     ((0, 64 * 8, 1), 4, 128),
     ((0, 64 * 128, 100), 4, 128),
