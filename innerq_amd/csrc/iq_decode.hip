@@ -700,7 +700,6 @@ int check_decode(const void* q, const iq_segment* k, const iq_segment* v, int B,
   IQ_CHECK(q && k && v, IQ_ERR_NULL);
   IQ_CHECK(B >= 0 && T > 0 && Hkv > 0 && Hq > 0, IQ_ERR_SHAPE);
   IQ_CHECK(d_ok(D) && Hq % Hkv == 0 && nrep_ok(Hq / Hkv), IQ_ERR_SHAPE);
-  IQ_CHECK(nsplit_max(T) + NSD_MAX <= MAXSPLIT, IQ_ERR_SHAPE);
   for (int s = 0; s < 3; ++s) IQ_CHECK(k[s].n >= 0 && v[s].n >= 0, IQ_ERR_SHAPE);
   IQ_CHECK(k[0].n + k[1].n + k[2].n == T && v[0].n + v[1].n + v[2].n == T, IQ_ERR_SHAPE);
   for (int s : {0, 2}) {
@@ -786,6 +785,13 @@ int launch_splits(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, c
                               v[1].mode};
   const bool fused =
       c && k[1].group == v[1].group && detail::flash_fused_supported(q, sq_b, sq_h, norm, fk, fv, Hq, Hkv, D);
+  // A combine that reads every split slot (the unfused kernels write one per
+  // split; the split stage alone leaves empty statistics in the slots past
+  // the fused runs) holds at most MAXSPLIT of them: checked before any launch.
+  // A full call on the fused path reads only the live slots (a head's fused
+  // runs, at most one per workgroup, and the dense slices), so the context
+  // length is bounded by the workspace alone.
+  if (c && !(fused && live) && nsf + NSD_MAX > MAXSPLIT) return IQ_ERR_SHAPE;
 
   // dense tokens -> split slots nsf, nsf + 1, ...: up to two workgroups per
   // CU (a workgroup's chunks run one after another, each a chain of memory
@@ -851,6 +857,9 @@ int launch_splits(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, c
       return e;
     plan->grid = grid;
     plan->pair_e0 = detail::fused_pair_e0(k[1].bits, v[1].bits, v[1].mode == IQ_MODE_HYBRID);
+    // live slots of a row: at most one run per workgroup, then the slices
+    // (one workgroup per CU: far below the limit)
+    if (live && grid + NSD_MAX > MAXSPLIT) return IQ_ERR_SHAPE;
     bool merge_dense = merge_cand;
     if (merge_cand) {
       const detail::ShareMap sm = detail::ShareMap::make(grid, int(bhs), nsf, plan->pair_e0);
@@ -907,17 +916,20 @@ int launch_combine(const Workspace& w, const SplitPlan& plan, int B, int Hq, int
                    int64_t so_h, hipStream_t st) {
   const int64_t rows = int64_t(B) * Hq;
   const int nsplit = plan.nsplit;
-  // statistics registers per lane: the smallest power of two with 64 E >= nsplit
+  // slots a row reads: with the fused kernel's workgroup count, its runs (at
+  // most one per workgroup) and the dense slices; else every slot
+  const int nlive = plan.grid > 0 ? std::min(nsplit, plan.grid + (nsplit - plan.nsf)) : nsplit;
+  // statistics registers per lane: the smallest power of two with 64 E >= nlive
   auto go = [&]<int DPL, int E>() {
     flash_combine_kernel<DPL, E><<<dim3(unsigned(rows)), 64, 0, st>>>(w.ml, w.part, nsplit, plan.nsf, plan.grid,
                                                                       plan.pair_e0, plan.nrep, rows, Hq,
                                                                       (uint16_t*)out, so_b, so_h);
   };
   auto by_e = [&]<int DPL>() {
-    if (nsplit <= 64) go.template operator()<DPL, 1>();
-    else if (nsplit <= 128) go.template operator()<DPL, 2>();
-    else if (nsplit <= 256) go.template operator()<DPL, 4>();
-    else if (nsplit <= 512) go.template operator()<DPL, 8>();
+    if (nlive <= 64) go.template operator()<DPL, 1>();
+    else if (nlive <= 128) go.template operator()<DPL, 2>();
+    else if (nlive <= 256) go.template operator()<DPL, 4>();
+    else if (nlive <= 512) go.template operator()<DPL, 8>();
     else go.template operator()<DPL, 16>();
   };
   static_assert(MAXSPLIT == 64 * 16, "combine variants");
@@ -999,6 +1011,7 @@ int iq_decode_attention_splits(const void* q, int64_t sq_b, int64_t sq_h, const 
                                void* workspace, size_t workspace_bytes, int* nsplit, void* stream) {
   IQ_CHECK(nsplit, IQ_ERR_NULL);
   if (int e = check_decode(q, k, v, B, Hq, Hkv, T, D, workspace, workspace_bytes)) return e;
+  IQ_CHECK(nsplit_max(T) + NSD_MAX <= MAXSPLIT, IQ_ERR_SHAPE);  // its combine reads every slot
   *nsplit = 0;
   if (B == 0) return IQ_OK;
   SplitPlan plan;

@@ -209,6 +209,29 @@ def test_decode_stage_rejects():
     assert lib.iq_decode_attention_combine(1, 1, 32, 64, 128, FAKE, 4096, 128, FAKE, 64, None) == -6
 
 
+def test_decode_slot_limit_where_every_slot_is_read():
+    """Past 1020 splits of 256 tokens (261,120 tokens), a combine that reads every
+    split slot cannot hold them: the split stage alone and the unfused kernels (K
+    and V of different group sizes) return IQ_ERR_SHAPE before any launch.  A full
+    call on the fused path reads only its live slots and takes any length (GPU
+    test)."""
+    lib = _lib.lib()
+    T = 300032
+    k = (_lib.iq_segment * 3)()
+    v = (_lib.iq_segment * 3)()
+    for seg, group in ((k, 32), (v, 64)):
+        seg[1].n, seg[1].t_cap, seg[1].t0 = T, T, 0
+        seg[1].codes, seg[1].meta, seg[1].bits, seg[1].group, seg[1].mode = 0x1000, 0x1000, 4, group, 0
+    big = 1 << 40
+    assert lib.iq_decode_attention(FAKE, 4096, 128, None, k, v, 1, 32, 8, T, 128, 1.0, FAKE, 4096, 128, FAKE, big,
+                                   None) == -4
+    ns = ctypes.c_int(-7)
+    v[1].group = 32
+    assert lib.iq_decode_attention_splits(FAKE, 4096, 128, None, k, v, 1, 32, 8, T, 128, 1.0, FAKE, big,
+                                          ctypes.byref(ns), None) == -4
+    assert ns.value == -7
+
+
 def test_decode_noalloc_limits():
     """The no-allocation decode entry point: its scratch size, and a call whose
     workspace would exceed it refused with IQ_ERR_WORKSPACE before any HIP call

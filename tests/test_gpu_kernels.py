@@ -460,6 +460,15 @@ def test_decode_attention_window_after_fused_kernel(seg, nrep, D):
     assert err < TOL
 
 
+def test_decode_attention_past_the_split_slot_limit():
+    """300,096 tokens in one call (1,173 splits of 256, past the 1,024 split slots
+    a combine over every slot holds): the fused path's combine reads only the live
+    slots (one run per workgroup here, plus the window's slices)."""
+    seg = (0, 300032, 64)
+    err = _decode_case(1, 1, 4, 128, seg, seg, (4, 32, "asymmetric"), (4, 32, "asymmetric"), seed=41)
+    assert err < TOL
+
+
 @pytest.mark.parametrize("kfmt,vfmt", [((3, 32, "symmetric"), (3, 32, "symmetric")),
                                        ((2, 64, "asymmetric"), (4, 64, "symmetric")),
                                        ((4, 128, "asymmetric"), (2, 128, "asymmetric")),
