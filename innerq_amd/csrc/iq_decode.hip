@@ -567,9 +567,13 @@ __global__ __launch_bounds__(MERGE ? 512 : 256) void dense_attn_kernel(DenseArgs
 // first CSPEC listed slots (indices clamped so that every load is issued at
 // once) - covers up to CSPEC live slots; a slot is used only if its weight is
 // nonzero (a select: an unwritten partial cannot reach the sum).  Further
-// live slots are listed in LDS and read CSPEC at a time.
+// live slots are listed in LDS and read CREST at a time.
 constexpr int MAXSPLIT = 1024;  // split slots of one step, at most
 constexpr int CSPEC = 8;
+// live slots past the first CSPEC are read CREST per round of loads (a head
+// spread over many workgroups, e.g. one (batch, KV head) over a long context,
+// has a run per workgroup: 248 further slots took 31 dependent rounds of 8)
+constexpr int CREST = 32;
 template <int DPL, int E>
 __global__ __launch_bounds__(64) void flash_combine_kernel(const float* __restrict__ ml, const float* __restrict__ part,
                                                            int nsplit, int nsf, int grid, int pair_e0, int nrep,
@@ -635,12 +639,12 @@ __global__ __launch_bounds__(64) void flash_combine_kernel(const float* __restri
   }
   if (m) {
     __syncthreads();
-    for (int k0 = 0; k0 < m; k0 += CSPEC) {
-      Vec v[CSPEC];
+    for (int k0 = 0; k0 < m; k0 += CREST) {
+      Vec v[CREST];
 #pragma unroll
-      for (int u = 0; u < CSPEC; ++u) v[u] = pr[int64_t(sidx[min(k0 + u, m - 1)]) * pstride];
+      for (int u = 0; u < CREST; ++u) v[u] = pr[int64_t(sidx[min(k0 + u, m - 1)]) * pstride];
 #pragma unroll
-      for (int u = 0; u < CSPEC; ++u)
+      for (int u = 0; u < CREST; ++u)
         if (k0 + u < m) acc += swgt[k0 + u] * v[u];
     }
   }
