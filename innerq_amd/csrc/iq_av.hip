@@ -170,8 +170,18 @@ __global__ __launch_bounds__(256) void av_combine_kernel(const float* __restrict
   int n = nsplit;
   if (grid > 0)  // the runs of the (batch, KV head) in the persistent kernel's shares
     n = detail::ShareMap::make(grid, int(rows / nrep), nsplit, 0).nruns(int(bq / nrep));  // plain partition
+  // the slots in order, their loads eight at a time (indices clamped so that a
+  // round's loads are all in flight at once; the sum order is the slot order)
+  constexpr int AB = 8;
   float v = 0.f;
-  for (int s = 0; s < n; ++s) v += part[(int64_t(s) * rows + bq) * D + d];
+  for (int s0 = 0; s0 < n; s0 += AB) {
+    float x[AB];
+#pragma unroll
+    for (int u = 0; u < AB; ++u) x[u] = part[(int64_t(min(s0 + u, n - 1)) * rows + bq) * D + d];
+#pragma unroll
+    for (int u = 0; u < AB; ++u)
+      if (s0 + u < n) v += x[u];
+  }
   const int64_t off32 = (bq / Hq) * o.s32b + (bq % Hq) * o.s32h + d;
   if (accumulate) v += o.out32[off32];
   if (o.out32) o.out32[off32] = v;
