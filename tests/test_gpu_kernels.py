@@ -308,12 +308,16 @@ def test_av_gemv_shapes_and_accumulate(nrep, D):
     assert A.rel_err(o16.cpu().numpy().astype(np.float64), ref) < 2e-3
 
 
-@pytest.mark.parametrize("bits,G,mode", [(2, 64, "asymmetric"), (4, 32, "symmetric")])
-def test_av_gemv_many_runs(bits, G, mode):
+@pytest.mark.parametrize("bits,G,mode,B,Hkv,T", [(2, 64, "asymmetric", 2, 4, 16384),
+                                                  (4, 32, "symmetric", 2, 4, 16384),
+                                                  # one head of 37 splits: a run per workgroup,
+                                                  # the combine's rounds of eight end short
+                                                  (2, 64, "asymmetric", 1, 1, 37 * 256)])
+def test_av_gemv_many_runs(bits, G, mode, B, Hkv, T):
     """A long range over many (batch, KV head)s: the persistent kernel's shares cut the
     heads into several runs each, whose partials the combine sums.  Reference: fp32
     p @ V over V unpacked by the library (unpack is bit-exact to the oracle elsewhere)."""
-    B, Hkv, nrep, D, T = 2, 4, 4, 128, 16384
+    nrep, D = 4, 128
     gen = torch.Generator(device=DEV).manual_seed(bits * G)
     x = torch.randn(B, Hkv, T, D, generator=gen, device=DEV).to(torch.float16)
     st = ops.PackedStore("token", B, Hkv, D, G, bits, mode, DEV, t_cap=T)
