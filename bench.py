@@ -353,6 +353,38 @@ def bench_config(args):
                  + gemv_bytes(B, Hkv, Tq - Tq % G, D, G, 4, "asymmetric", "token"))
         res.update(us=us, us_per_layer=us / L, GBs=b / us / 1e3, us_graph=ug, us_per_layer_graph=ug / L,
                    GBs_graph=b / ug / 1e3, bytes=b)
+    elif cfg == "small":
+        # not a BASELINE config: one sequence (B=1) decode steps and attn.V
+        # calls, where a head is spread over many workgroups (a fused run per
+        # workgroup, many split slots for the combine); 4-bit K and V (attn.V:
+        # 2-bit G=64 V), with and without a 128-token fp16 window
+        D, G = 128, 32
+        clock_warmup(dev)
+        for Hkv, T, R in ((8, 32768, 0), (8, 32768, 128), (8, 131072, 0), (8, 131072, 128),
+                          (1, 131072, 0), (1, 131072, 128)):
+            B, Hq, Tq = 1, 4 * Hkv, T - R
+            ks = make_store("channel", B, Hkv, Tq, D, G, 4, "asymmetric", 70, dev)
+            vs = make_store("token", B, Hkv, Tq, D, G, 4, "asymmetric", 71, dev)
+            kr = torch.randn(B, Hkv, R, D, device=dev, dtype=torch.float16) if R else None
+            vr = torch.randn(B, Hkv, R, D, device=dev, dtype=torch.float16) if R else None
+            q = torch.randn(B, Hq, D, device=dev, dtype=torch.float16)
+            out = torch.empty(B, Hq, D, device=dev, dtype=torch.float16)
+            fn = lambda i: ops.decode_attention(q, None, ks, kr, None, vs, vr, D ** -0.5, out=out)
+            ug = time_graph(fn, 1, max(1, 2 * args.steps))
+            b = gemv_bytes(B, Hkv, Tq, D, G, 4, "asymmetric", "channel") + \
+                gemv_bytes(B, Hkv, Tq, D, G, 4, "asymmetric", "token")
+            res[f"decode_Hkv{Hkv}_T{T}_R{R}"] = dict(us_graph=ug, GBs_graph=b / ug / 1e3, bytes=b)
+            del ks, vs
+        for Hkv, T in ((8, 8192), (8, 131072), (1, 131072)):
+            B, Hq, GV = 1, 4 * Hkv, 64
+            vs = make_store("token", B, Hkv, T, D, GV, 2, "asymmetric", 72, dev)
+            p = torch.softmax(torch.randn(B, Hq, T, device=dev) * 2.0, dim=-1).to(torch.float16)
+            out = torch.empty(B, Hq, D, device=dev, dtype=torch.float16)
+            fn = lambda i: ops.av_gemv(p, vs, out=out)
+            ug = time_graph(fn, 1, max(1, 2 * args.steps))
+            b = gemv_bytes(B, Hkv, T, D, GV, 2, "asymmetric", "token")
+            res[f"av_Hkv{Hkv}_T{T}"] = dict(us_graph=ug, GBs_graph=b / ug / 1e3, bytes=b)
+            del vs
     print(json.dumps(res), flush=True)
 
 
