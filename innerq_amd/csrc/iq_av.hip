@@ -160,6 +160,7 @@ __global__ __launch_bounds__(WG) void av_kernel(AVArgs a) {
   }
 }
 
+template <int AB>
 __global__ __launch_bounds__(256) void av_combine_kernel(const float* __restrict__ part, int nsplit, int Hq, int D,
                                                          int64_t rows, detail::OutPair o, int accumulate, int grid,
                                                          int nrep) {
@@ -170,9 +171,8 @@ __global__ __launch_bounds__(256) void av_combine_kernel(const float* __restrict
   int n = nsplit;
   if (grid > 0)  // the runs of the (batch, KV head) in the persistent kernel's shares
     n = detail::ShareMap::make(grid, int(rows / nrep), nsplit, 0).nruns(int(bq / nrep));  // plain partition
-  // the slots in order, their loads eight at a time (indices clamped so that a
+  // the slots in order, their loads AB at a time (indices clamped so that a
   // round's loads are all in flight at once; the sum order is the slot order)
-  constexpr int AB = 8;
   float v = 0.f;
   for (int s0 = 0; s0 < n; s0 += AB) {
     float x[AB];
@@ -280,8 +280,14 @@ int av_combine_launch(const float* part, int nsplit, int B, int Hq, int D, const
                       hipStream_t stream, int grid, int nrep) {
   const int64_t rows = int64_t(B) * Hq;
   if (rows == 0) return IQ_OK;
-  av_combine_kernel<<<dim3(unsigned(ceil_div(rows * D, 256))), 256, 0, stream>>>(part, nsplit, Hq, D, rows, o,
-                                                                                accumulate, grid, nrep);
+  // loads per round: 8, or 32 where a head can have more than eight runs (the
+  // persistent kernel's workgroups over few (batch, KV head)s, or every split
+  // slot without its workgroup count)
+  const int64_t heads = std::max<int64_t>(1, rows / std::max(nrep, 1));
+  const int64_t runs = grid > 0 ? std::min<int64_t>(nsplit, ceil_div(grid, heads) + 1) : nsplit;
+  const dim3 g{unsigned(ceil_div(rows * D, 256))};
+  if (runs > 8) av_combine_kernel<32><<<g, 256, 0, stream>>>(part, nsplit, Hq, D, rows, o, accumulate, grid, nrep);
+  else av_combine_kernel<8><<<g, 256, 0, stream>>>(part, nsplit, Hq, D, rows, o, accumulate, grid, nrep);
   return launch_status();
 }
 
