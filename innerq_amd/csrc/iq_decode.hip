@@ -569,12 +569,12 @@ __global__ __launch_bounds__(MERGE ? 512 : 256) void dense_attn_kernel(DenseArgs
 // nonzero (a select: an unwritten partial cannot reach the sum).  Further
 // live slots are listed in LDS and read CREST at a time.
 constexpr int MAXSPLIT = 1024;  // split slots of one step, at most
-constexpr int CSPEC = 8;
-// live slots past the first CSPEC are read CREST per round of loads (a head
+// live slots past the first CSPEC (8, or 32 where a head has more than eight
+// runs) are read CREST per round of loads (a head
 // spread over many workgroups, e.g. one (batch, KV head) over a long context,
 // has a run per workgroup: 248 further slots took 31 dependent rounds of 8)
 constexpr int CREST = 32;
-template <int DPL, int E>
+template <int DPL, int E, int CSPEC>
 __global__ __launch_bounds__(64) void flash_combine_kernel(const float* __restrict__ ml, const float* __restrict__ part,
                                                            int nsplit, int nsf, int grid, int pair_e0, int nrep,
                                                            int64_t rows, int Hq, uint16_t* __restrict__ out,
@@ -920,12 +920,21 @@ int launch_combine(const Workspace& w, const SplitPlan& plan, int B, int Hq, int
                    int64_t so_h, hipStream_t st) {
   const int64_t rows = int64_t(B) * Hq;
   const int nsplit = plan.nsplit;
-  // slots a row reads: with the fused kernel's workgroup count, its runs (at
-  // most one per workgroup) and the dense slices; else every slot
-  const int nlive = plan.grid > 0 ? std::min(nsplit, plan.grid + (nsplit - plan.nsf)) : nsplit;
+  // slots a row reads, at most: with the fused kernel's workgroup count, the
+  // most runs of any (batch, KV head) (the share arithmetic the kernel uses)
+  // and the dense slices; else every slot
+  int nlive = nsplit;
+  if (plan.grid > 0) {
+    const int heads = int(rows / std::max(plan.nrep, 1));
+    const detail::ShareMap sm = detail::ShareMap::make(plan.grid, heads, plan.nsf, plan.pair_e0);
+    int maxr = 0;
+    for (int h = 0; h < heads; ++h) maxr = std::max(maxr, sm.nruns(h));
+    nlive = std::min(nsplit, maxr + (nsplit - plan.nsf));
+  }
   // statistics registers per lane: the smallest power of two with 64 E >= nlive
   auto go = [&]<int DPL, int E>() {
-    flash_combine_kernel<DPL, E><<<dim3(unsigned(rows)), 64, 0, st>>>(w.ml, w.part, nsplit, plan.nsf, plan.grid,
+    auto* kern = nlive > 8 ? flash_combine_kernel<DPL, E, 32> : flash_combine_kernel<DPL, E, 8>;
+    kern<<<dim3(unsigned(rows)), 64, 0, st>>>(w.ml, w.part, nsplit, plan.nsf, plan.grid,
                                                                       plan.pair_e0, plan.nrep, rows, Hq,
                                                                       (uint16_t*)out, so_b, so_h);
   };
