@@ -13,10 +13,11 @@ value = algorithmic packed-code + metadata bytes of both GEMVs / step time,
 the steps timed back to back on the GPU (time_backlogged; the median of three
 loops of exactly --steps steps).
 roofline = the dominant kernel (the fused flash-decoding split kernel, which
-reads every packed byte) alone: the split stage of the step, launched back to
-back in the same rotation and timed the same way with HIP events on the stream
-it runs on (medians of three loops of at least 100 launches, alternating with
-full steps over the same launch count); traffic = its HBM bytes from rocprofv3 FETCH_SIZE / WRITE_SIZE
+reads every packed byte) alone: the split stage of the step exactly as the step
+launches it (iq_decode_attention_splits_live: the same kernel and grid, live
+split slots), launched back to back in the same rotation and timed the same way
+with HIP events on the stream it runs on (medians of three loops of at least
+100 launches, alternating with full steps over the same launch count); traffic = its HBM bytes from rocprofv3 FETCH_SIZE / WRITE_SIZE
 (profiles/traffic.json).  cpu_baseline = the
 reference's torch CPU path (dequantize int32 codes -> fp16 -> eager
 attention) on a sample of the same workload, timed on host cores
@@ -213,8 +214,8 @@ def bench_headline(args):
     def step(i):
         ops.decode_attention(q, None, ks[i % C], None, None, vs[i % C], None, scale, out=out)
 
-    def split_stage(i):  # one launch of the fused split kernel (every token packed, one format)
-        return ops.decode_attention_splits(q, None, ks[i % C], None, None, vs[i % C], None, scale)
+    def split_stage(i):  # the step's launch of the fused split kernel (every token packed, one format)
+        return ops.decode_attention_splits_live(q, None, ks[i % C], None, None, vs[i % C], None, scale)
 
     clock_warmup(dev)
     # the step: the median of three timed loops of exactly K steps each
@@ -228,7 +229,8 @@ def bench_headline(args):
     # a step is the kernel plus the combine, so only noise can put the kernel
     # above the step, and a line where it still does says so.
     nl = max(100, args.steps)
-    nsplit = split_stage(0)
+    plan = split_stage(0)
+    nsplit, grid = plan.nsplit, plan.grid
     splits, steps_nl = [], []
     for _ in range(3):
         splits.append(time_backlogged(split_stage, nl, C))
@@ -255,7 +257,7 @@ def bench_headline(args):
                                "4-bit K (groups along head_dim) and V (groups along tokens), asym, G=32",
                    "global_batch": B, "seq_len": T, "parallelism": "single GPU", "copies_rotated": C,
                    "algorithmic_bytes_per_step": step_b},
-        "kernels_us": {"flash_fused_kernel": round(us_split, 2), "splits": nsplit, "launches": nl,
+        "kernels_us": {"flash_fused_kernel": round(us_split, 2), "splits": nsplit, "workgroups": grid, "launches": nl,
                        "step_us_same_rotation": round(us_step_nl, 2), **({"kernel_above_step": True} if inverted else {})},
         "roofline": {"bound": "hbm", "kernel": "flash_fused_kernel", "achieved": round(ach, 1), "peak": PEAK_GBS,
                      "unit": "GB/s", "frac": round(ach / PEAK_GBS, 4),

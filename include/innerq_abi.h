@@ -307,6 +307,32 @@ int iq_decode_attention_splits(const void* q, int64_t sq_b, int64_t sq_h, const 
 int iq_decode_attention_combine(int nsplit, int B, int Hq, int T, int D, void* out, int64_t so_b, int64_t so_h,
                                 void* workspace, size_t workspace_bytes, void* stream);
 
+/* The two stages of iq_decode_attention exactly as that call launches them:
+ * the fused kernel leaves a partial only in the split slots its runs own
+ * (no empty statistics in the others) and the combine reads only those
+ * ("live") slots, so _splits_live launches the same kernel, with the same
+ * grid, as the full call (for timing and profiling the decode step's dominant
+ * kernel, or for a scheduler that runs its own work between the stages).  A
+ * fp16 window short enough for the full call to attend to it after the fused
+ * kernel takes the dense slices here instead.  *plan (host memory, known at
+ * return) describes the slots; it is opaque: pass it unchanged to
+ * _combine_live with the same workspace, B, Hq, T and D. */
+typedef struct iq_split_plan {
+  int nsplit;   /* split slots written */
+  int nsf;      /* the first nsf of them belong to the packed range */
+  int grid;     /* workgroups of the fused kernel (0: not launched) */
+  int nrep;     /* query heads per KV head */
+  int pair_e0;  /* the fused kernel's work partition */
+  int reserved[3];
+} iq_split_plan;
+int iq_decode_attention_splits_live(const void* q, int64_t sq_b, int64_t sq_h, const void* norm,
+                                    const iq_segment* k, const iq_segment* v,
+                                    int B, int Hq, int Hkv, int T, int D, float scale,
+                                    void* workspace, size_t workspace_bytes, iq_split_plan* plan, void* stream);
+int iq_decode_attention_combine_live(const iq_split_plan* plan, int B, int Hq, int T, int D, void* out,
+                                     int64_t so_b, int64_t so_h, void* workspace, size_t workspace_bytes,
+                                     void* stream);
+
 /* iq_decode_attention without the workspace argument, for callers that
  * cannot allocate device memory (code under HIP graph capture, serving loops
  * and harnesses that forbid hipMalloc).  It has no counterpart in the

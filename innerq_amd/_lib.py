@@ -67,6 +67,11 @@ class iq_window(ctypes.Structure):
     ]
 
 
+class iq_split_plan(ctypes.Structure):
+    _fields_ = [("nsplit", ctypes.c_int), ("nsf", ctypes.c_int), ("grid", ctypes.c_int), ("nrep", ctypes.c_int),
+                ("pair_e0", ctypes.c_int), ("reserved", ctypes.c_int * 3)]
+
+
 SIGNATURES = {
     "iq_abi_version": (I, []),
     "iq_strerror": (ctypes.c_char_p, [I]),
@@ -93,6 +98,9 @@ SIGNATURES = {
     "iq_decode_attention_splits": (I, [P, L, L, P, ctypes.POINTER(iq_segment), ctypes.POINTER(iq_segment),
                                        I, I, I, I, I, F, P, S, ctypes.POINTER(I), P]),
     "iq_decode_attention_combine": (I, [I, I, I, I, I, P, L, L, P, S, P]),
+    "iq_decode_attention_splits_live": (I, [P, L, L, P, ctypes.POINTER(iq_segment), ctypes.POINTER(iq_segment),
+                                            I, I, I, I, I, F, P, S, ctypes.POINTER(iq_split_plan), P]),
+    "iq_decode_attention_combine_live": (I, [ctypes.POINTER(iq_split_plan), I, I, I, I, P, L, L, P, S, P]),
     "iq_decode_noalloc_max_bytes": (S, []),
     "iq_decode_attention_noalloc": (I, [P, L, L, P, ctypes.POINTER(iq_segment), ctypes.POINTER(iq_segment),
                                         I, I, I, I, I, F, P, L, L, P]),

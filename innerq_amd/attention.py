@@ -13,6 +13,8 @@ layouts the fused kernels do not take keep that path.
 """
 from __future__ import annotations
 
+import weakref
+
 import torch
 from transformers import AttentionInterface
 from transformers.integrations.sdpa_attention import sdpa_attention_forward
@@ -21,10 +23,14 @@ from transformers.masking_utils import AttentionMaskInterface, sdpa_mask
 from .cache import FUSED_ATTENTION
 
 
-# (mask tensor, answer) of the last mask inspected: every layer of one forward
-# pass receives the same mask object, so the device-to-host read that the
-# answer needs happens once per decode step, not once per layer
-_last_mask: list = [None, False]
+# (weak reference to the mask, its version counter, answer) of the last mask
+# inspected: every layer of one forward pass receives the same mask object,
+# so the device-to-host read that the answer needs happens once per decode
+# step, not once per layer.  The version counter changes with every in-place
+# edit, so a mask object reused and edited between passes is read again; the
+# weak reference keeps no mask alive, and a different mask (another model's,
+# another pass's) is a different object.
+_last_mask: list = [None, -1, False]
 
 
 def _masks_tokens(attention_mask) -> bool:
@@ -32,13 +38,14 @@ def _masks_tokens(attention_mask) -> bool:
     to every token."""
     if attention_mask is None:
         return False
-    if attention_mask is _last_mask[0]:
-        return _last_mask[1]
+    ref, ver, ans = _last_mask
+    if ref is not None and ref() is attention_mask and ver == attention_mask._version:
+        return ans
     if attention_mask.dtype == torch.bool:
         ans = not bool(attention_mask.all())
     else:
         ans = bool((attention_mask < 0).any())
-    _last_mask[0], _last_mask[1] = attention_mask, ans
+    _last_mask[:] = [weakref.ref(attention_mask), attention_mask._version, ans]
     return ans
 
 

@@ -16,12 +16,15 @@
 // splits in split order: no atomics, deterministic results.
 //
 // iq_av_gemv takes this path only where the persistent kernel cannot run (a
-// slice beyond 32-bit buffer offsets).  Its main path is the fused decode
-// kernel in attn.V-only mode (iq_flash.h): one workgroup per CU streams V
-// and the probabilities of its share of the token range (read straight into
-// the operand records, no record kernel), one partial per run, then the same
-// combine over each (batch, KV head)'s run slots.
-#include "iq_flash.h"
+// slice beyond 32-bit buffer offsets).  Its main path is the column-slice
+// kernel (iq_av_cols.h: a workgroup per (batch, KV head, 32 output columns)
+// over the whole token range, no partials, no combine) wherever that grid
+// fills the device; else the fused decode kernel in attn.V-only mode
+// (iq_flash.h): one workgroup per CU streams V and the probabilities of its
+// share of the token range (read straight into the operand records, no record
+// kernel), one partial per run, then the same combine over each (batch, KV
+// head)'s run slots.
+#include "iq_av_cols.h"
 
 using namespace iq;
 
@@ -216,6 +219,56 @@ int check_av(const void* p, const uint32_t* v_codes, const uint16_t* v_meta, int
 
 namespace iq::detail {
 
+int av_cols_launch_k2(const void* args, int group, int D, int nrep, bool hybrid, hipStream_t stream);
+int av_cols_launch_k3(const void* args, int group, int D, int nrep, bool hybrid, hipStream_t stream);
+int av_cols_launch_k4(const void* args, int group, int D, int nrep, bool hybrid, hipStream_t stream);
+
+// The column-slice kernel, where it applies: its B * Hkv * D/32 workgroups
+// fill the device, the probability rows are 16-byte aligned, and every
+// buffer offset (a head's V slice, the steps read past its end, a KV head's
+// probability rows) fits 32 bits.  *launched = false: nothing launched.
+int av_cols_launch(const void* p, int64_t sp_b, int64_t sp_h, const uint32_t* v_codes, const uint16_t* v_meta,
+                   int64_t t_cap, int B, int Hq, int Hkv, int t0, int T, int D, int group, int bits, int mode,
+                   const OutPair& o, int accumulate, bool* launched, hipStream_t stream) {
+  *launched = false;
+  const int nrep = Hq / Hkv;
+  const int nslice = D / AVC_CW;
+  const int64_t items = int64_t(B) * Hkv * nslice;
+  const int64_t lim = int64_t(1) << 31;
+  const int ngroups = T / group;
+  const int64_t vw = int64_t(group) * bits / 32;
+  // groups a launch may address past the range (the prefetches past a
+  // wave's last step)
+  const int64_t slack = int64_t(AVC_NW) * 6 * 8 + 8;
+  if (items < num_cus() || ngroups <= 0 || items > int64_t(1) << 30) return IQ_OK;
+  if (!aligned(p, 16) || sp_b % 8 || sp_h % 8 || sp_h < 0 || sp_b < 0) return IQ_OK;
+  if ((int64_t(nrep - 1) * sp_h + T) * 2 >= lim || (ngroups + slack) * D * vw * 4 >= lim ||
+      (ngroups + slack) * D * 4 >= lim || t_cap * D * bits / 8 >= lim)
+    return IQ_OK;
+  if (o.out32 && o.out16 && (o.s32b != o.s16b || o.s32h != o.s16h)) return IQ_OK;
+  AVCArgs a{};
+  a.p = (const uint16_t*)p; a.spb = sp_b; a.sph = sp_h;
+  a.vc = v_codes; a.vm = v_meta; a.cap_groups = t_cap / group; a.g0 = t0 / group;
+  a.Hkv = Hkv; a.ngroups = ngroups; a.vsym = mode == IQ_MODE_SYM;
+  a.nslice = nslice; a.nitems = int(items);
+  a.p_bytes = uint32_t((int64_t(nrep - 1) * sp_h + T) * 2);
+  a.v_code_bytes = uint32_t(int64_t(ngroups) * D * vw * 4);
+  a.v_meta_bytes = uint32_t(int64_t(ngroups) * D * meta_unit_bytes(mode));
+  a.out32 = o.out32; a.out16 = o.out16;
+  a.sob = o.out32 ? o.s32b : o.s16b;
+  a.soh = o.out32 ? o.s32h : o.s16h;
+  a.accumulate = accumulate;
+  const bool hyb = mode == IQ_MODE_HYBRID;
+  int e = IQ_ERR_BITS;
+  switch (bits) {
+    case 2: e = av_cols_launch_k2(&a, group, D, nrep, hyb, stream); break;
+    case 3: e = av_cols_launch_k3(&a, group, D, nrep, hyb, stream); break;
+    case 4: e = av_cols_launch_k4(&a, group, D, nrep, hyb, stream); break;
+  }
+  *launched = e == IQ_OK;
+  return e;
+}
+
 int av_splits(int B, int Hkv, int T, int group) {
   const int ng = T / group;
   if (ng <= 0) return 0;
@@ -319,13 +372,8 @@ int av_fused_launch(const void* p, int64_t sp_b, int64_t sp_h, const uint32_t* v
     auto* kern = hyb ? flash_fused_kernel<VB, VB, G, DD, R, false, true, false, true>
                      : flash_fused_kernel<VB, VB, G, DD, R, false, true>;
     const int nt = FusedShape<G, R, false, true>::NT;
-    static int per_cu[2] = {0, 0};  // workgroups per CU at once
-    int& pc = per_cu[hyb ? 1 : 0];
-    if (pc == 0) {
-      int n = 0;
-      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, nt, 0) != hipSuccess || n <= 0) n = 1;
-      pc = n;
-    }
+    static OccCache occ[2];  // workgroups per CU at once
+    const int pc = blocks_per_cu(kern, nt, occ[hyb ? 1 : 0]);
     *grid = int(std::min<int64_t>(a.nitems, int64_t(pc) * num_cus()));
     kern<<<dim3(*grid), nt, 0, stream>>>(a);
     return launch_status();
@@ -358,6 +406,11 @@ int iq_av_gemv(const void* p, int64_t sp_b, int64_t sp_h, const uint32_t* v_code
   IQ_CHECK(aligned(workspace, 16), IQ_ERR_ALIGN);
   uint32_t* rec = (uint32_t*)workspace;
   float* part = (float*)((char*)workspace + rb);
+  bool cols = false;
+  if (int e = detail::av_cols_launch(p, sp_b, sp_h, v_codes, v_meta, t_cap, B, Hq, Hkv, t0, T, D, group, bits, mode,
+                                     o, accumulate, &cols, st))
+    return e;
+  if (cols) return IQ_OK;
   int grid = 0;
   if (int e = detail::av_fused_launch(p, sp_b, sp_h, v_codes, v_meta, t_cap, B, Hq, Hkv, t0, T, D, group, bits, mode,
                                       part, &grid, st))

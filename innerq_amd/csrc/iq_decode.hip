@@ -796,6 +796,16 @@ int launch_splits(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, c
   // runs, at most one per workgroup, and the dense slices), so the context
   // length is bounded by the workspace alone.
   if (c && !(fused && live) && nsf + NSD_MAX > MAXSPLIT) return IQ_ERR_SHAPE;
+  // The live slots of a row: at most one fused run per workgroup, then the
+  // slices.  The fused kernel's grid (one workgroup per CU: far below the
+  // limit) is worked out and checked before anything is launched.
+  int fgrid = 0;
+  if (fused && live) {
+    if (int e = detail::flash_fused_launch(q, sq_b, sq_h, norm, fk, fv, B, Hq, Hkv, c, D, scale, w.ml, w.part,
+                                           &fgrid, st, false))
+      return e;
+    if (fgrid + NSD_MAX > MAXSPLIT) return IQ_ERR_SHAPE;
+  }
 
   // dense tokens -> split slots nsf, nsf + 1, ...: up to two workgroups per
   // CU (a workgroup's chunks run one after another, each a chain of memory
@@ -861,9 +871,6 @@ int launch_splits(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, c
       return e;
     plan->grid = grid;
     plan->pair_e0 = detail::fused_pair_e0(k[1].bits, v[1].bits, v[1].mode == IQ_MODE_HYBRID);
-    // live slots of a row: at most one run per workgroup, then the slices
-    // (one workgroup per CU: far below the limit)
-    if (live && grid + NSD_MAX > MAXSPLIT) return IQ_ERR_SHAPE;
     bool merge_dense = merge_cand;
     if (merge_cand) {
       const detail::ShareMap sm = detail::ShareMap::make(grid, int(bhs), nsf, plan->pair_e0);
@@ -1033,6 +1040,52 @@ int iq_decode_attention_splits(const void* q, int64_t sq_b, int64_t sq_h, const 
                               &plan, false, (hipStream_t)stream);
   *nsplit = plan.nsplit;
   return e;
+}
+
+int iq_decode_attention_splits_live(const void* q, int64_t sq_b, int64_t sq_h, const void* norm,
+                                    const iq_segment* k, const iq_segment* v, int B, int Hq, int Hkv, int T, int D,
+                                    float scale, void* workspace, size_t workspace_bytes, iq_split_plan* plan,
+                                    void* stream) {
+  IQ_CHECK(plan, IQ_ERR_NULL);
+  if (int e = check_decode(q, k, v, B, Hq, Hkv, T, D, workspace, workspace_bytes)) return e;
+  *plan = iq_split_plan{};
+  if (B == 0) return IQ_OK;
+  SplitPlan sp;
+  // the launches of iq_decode_attention with live slots; a short fp16 window
+  // takes the slices (there is no output to merge into here)
+  const int e = launch_splits(q, sq_b, sq_h, norm, k, v, B, Hq, Hkv, T, D, scale, carve(workspace, B, Hq, T, D), &sp,
+                              true, (hipStream_t)stream);
+  plan->nsplit = sp.nsplit;
+  plan->nsf = sp.nsf;
+  plan->grid = sp.grid;
+  plan->nrep = sp.nrep;
+  plan->pair_e0 = sp.pair_e0;
+  return e;
+}
+
+int iq_decode_attention_combine_live(const iq_split_plan* plan, int B, int Hq, int T, int D, void* out, int64_t so_b,
+                                     int64_t so_h, void* workspace, size_t workspace_bytes, void* stream) {
+  IQ_CHECK(plan && out && workspace, IQ_ERR_NULL);
+  IQ_CHECK(B >= 0 && Hq > 0 && T > 0 && d_ok(D), IQ_ERR_SHAPE);
+  const iq_split_plan& p = *plan;
+  IQ_CHECK(nrep_ok(p.nrep) && Hq % p.nrep == 0, IQ_ERR_SHAPE);
+  IQ_CHECK(p.nsplit >= 1 && p.nsplit <= nsplit_max(T) + NSD_MAX && p.nsf >= 0 && p.nsf <= p.nsplit, IQ_ERR_SHAPE);
+  IQ_CHECK(p.nsplit - p.nsf <= NSD_MAX && p.pair_e0 >= 0 && p.pair_e0 < detail::ShareMap::E0_DEN, IQ_ERR_SHAPE);
+  // a grid the plan's slots cannot hold (every run covers at least one split)
+  const int64_t heads = int64_t(B) * (Hq / p.nrep);
+  IQ_CHECK(p.grid >= 0 && p.grid + NSD_MAX <= MAXSPLIT && (p.grid == 0 || p.grid <= int64_t(p.nsf) * heads),
+           IQ_ERR_SHAPE);
+  IQ_CHECK(p.grid > 0 || p.nsplit <= MAXSPLIT, IQ_ERR_SHAPE);  // without a grid every slot is read
+  IQ_CHECK(workspace_bytes >= iq_decode_workspace_bytes(B, Hq, T, D), IQ_ERR_WORKSPACE);
+  IQ_CHECK(aligned(workspace, 256), IQ_ERR_ALIGN);
+  if (B == 0) return IQ_OK;
+  SplitPlan sp;
+  sp.nsplit = p.nsplit;
+  sp.nsf = p.nsf;
+  sp.grid = p.grid;
+  sp.nrep = p.nrep;
+  sp.pair_e0 = p.pair_e0;
+  return launch_combine(carve(workspace, B, Hq, T, D), sp, B, Hq, D, out, so_b, so_h, (hipStream_t)stream);
 }
 
 int iq_decode_attention_combine(int nsplit, int B, int Hq, int T, int D, void* out, int64_t so_b, int64_t so_h,

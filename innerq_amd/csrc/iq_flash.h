@@ -145,22 +145,22 @@ typedef __amdgpu_buffer_rsrc_t rsrc_t;
 __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, int(bytes), 0x00020000);
 }
-template <int N>
+template <int N, int POLICY = STREAM>
 __device__ __forceinline__ void bload_words(rsrc_t r, uint32_t voff, uint32_t soff, uint32_t (&w)[N]) {
 #pragma unroll
   for (int c = 0; c < N / 4; ++c) {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff + 16 * c, soff, STREAM);
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff + 16 * c, soff, POLICY);
     w[4 * c] = v[0]; w[4 * c + 1] = v[1]; w[4 * c + 2] = v[2]; w[4 * c + 3] = v[3];
   }
   constexpr int R = N % 4, C0 = N - N % 4;
   if constexpr (R == 3) {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b96(r, voff + 4 * C0, soff, STREAM);
+    const auto v = __builtin_amdgcn_raw_buffer_load_b96(r, voff + 4 * C0, soff, POLICY);
     w[C0] = v[0]; w[C0 + 1] = v[1]; w[C0 + 2] = v[2];
   } else if constexpr (R == 2) {
-    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, voff + 4 * C0, soff, STREAM);
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, voff + 4 * C0, soff, POLICY);
     w[C0] = v[0]; w[C0 + 1] = v[1];
   } else if constexpr (R == 1) {
-    w[C0] = __builtin_amdgcn_raw_buffer_load_b32(r, voff + 4 * C0, soff, STREAM);
+    w[C0] = __builtin_amdgcn_raw_buffer_load_b32(r, voff + 4 * C0, soff, POLICY);
   }
 }
 __device__ __forceinline__ uint32_t bload_u32(rsrc_t r, uint32_t voff, uint32_t soff) {
@@ -699,23 +699,20 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS, AVO>::NT), (fused_waves_pe
 
 // Launch of the fused kernel for K bit width KB (the arguments filled by
 // flash_fused_launch): persistent grid, one workgroup per CU.  VH: hybrid V.
+// launch = false: only the grid is computed.
 template <int KB, bool VH = false>
 int fused_launch_kb(const FusedArgs& a, int vbits, int group, int D, int nrep, bool norm, int* grid_out,
-                    hipStream_t stream) {
+                    hipStream_t stream, bool launch) {
   return dispatch_shape(vbits, group, D, nrep, 0, [&]<int VB, int G, int DD, int R, bool S>() {
     auto* kern = norm ? flash_fused_kernel<KB, VB, G, DD, R, true, false, false, VH>
                       : flash_fused_kernel<KB, VB, G, DD, R, false, false, false, VH>;
     const int nt = norm ? FusedShape<G, R, true>::NT : FusedShape<G, R, false>::NT;
     // as many workgroups as fit at once on the device
-    static int per_cu[2] = {0, 0};
-    int& pc = per_cu[norm ? 1 : 0];
-    if (pc == 0) {
-      int n = 0;
-      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, nt, 0) != hipSuccess || n <= 0) n = 1;
-      pc = n;
-    }
+    static detail::OccCache occ[2];
+    const int pc = detail::blocks_per_cu(kern, nt, occ[norm ? 1 : 0]);
     const int grid = int(std::min<int64_t>(a.nitems, int64_t(pc) * detail::num_cus()));
     if (grid_out) *grid_out = grid;
+    if (!launch) return int(IQ_OK);
     kern<<<dim3(grid), nt, 0, stream>>>(a);
     return launch_status();
   });

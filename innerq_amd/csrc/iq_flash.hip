@@ -26,7 +26,7 @@ bool flash_fused_supported(const void* q, int64_t sq_b, int64_t sq_h, const void
 
 int flash_fused_launch(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, const FusedStore& k,
                        const FusedStore& v, int B, int Hq, int Hkv, int T, int D, float scale, float* ml,
-                       float* part, int* grid, hipStream_t stream) {
+                       float* part, int* grid, hipStream_t stream, bool launch) {
   if (B == 0 || T == 0) return IQ_OK;
   if (k.group != v.group) return IQ_ERR_GROUP;
   if (T % k.group || FSPLIT != flash_split_tokens()) return IQ_ERR_GROUP;
@@ -55,16 +55,16 @@ int flash_fused_launch(const void* q, int64_t sq_b, int64_t sq_h, const void* no
   if (k.mode == IQ_MODE_HYBRID) return IQ_ERR_MODE;
   if (v.mode == IQ_MODE_HYBRID) {
     switch (k.bits) {
-      case 2: return flash_fused_launch_vh_k2(a, v.bits, k.group, D, Hq / Hkv, norm != nullptr, grid, stream);
-      case 3: return flash_fused_launch_vh_k3(a, v.bits, k.group, D, Hq / Hkv, norm != nullptr, grid, stream);
-      case 4: return flash_fused_launch_vh_k4(a, v.bits, k.group, D, Hq / Hkv, norm != nullptr, grid, stream);
+      case 2: return flash_fused_launch_vh_k2(a, v.bits, k.group, D, Hq / Hkv, norm != nullptr, grid, stream, launch);
+      case 3: return flash_fused_launch_vh_k3(a, v.bits, k.group, D, Hq / Hkv, norm != nullptr, grid, stream, launch);
+      case 4: return flash_fused_launch_vh_k4(a, v.bits, k.group, D, Hq / Hkv, norm != nullptr, grid, stream, launch);
       default: return IQ_ERR_BITS;
     }
   }
   switch (k.bits) {
-    case 2: return flash_fused_launch_k2(a, v.bits, k.group, D, Hq / Hkv, norm != nullptr, grid, stream);
-    case 3: return flash_fused_launch_k3(a, v.bits, k.group, D, Hq / Hkv, norm != nullptr, grid, stream);
-    case 4: return flash_fused_launch_k4(a, v.bits, k.group, D, Hq / Hkv, norm != nullptr, grid, stream);
+    case 2: return flash_fused_launch_k2(a, v.bits, k.group, D, Hq / Hkv, norm != nullptr, grid, stream, launch);
+    case 3: return flash_fused_launch_k3(a, v.bits, k.group, D, Hq / Hkv, norm != nullptr, grid, stream, launch);
+    case 4: return flash_fused_launch_k4(a, v.bits, k.group, D, Hq / Hkv, norm != nullptr, grid, stream, launch);
     default: return IQ_ERR_BITS;
   }
 }

@@ -5,8 +5,8 @@
 namespace iq::detail {
 
 int flash_fused_launch_k3(const FusedArgs& a, int vbits, int group, int D, int nrep, bool norm, int* grid,
-                          hipStream_t stream) {
-  return fused_launch_kb<3>(a, vbits, group, D, nrep, norm, grid, stream);
+                          hipStream_t stream, bool launch) {
+  return fused_launch_kb<3>(a, vbits, group, D, nrep, norm, grid, stream, launch);
 }
 
 }  // namespace iq::detail

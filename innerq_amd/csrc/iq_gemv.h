@@ -27,6 +27,7 @@
 // 2^8 code units (iq_device.h), so the fp32 partial sums stay small.
 #pragma once
 
+#include <atomic>
 #include <utility>
 
 #include "iq_common.h"
@@ -203,16 +204,18 @@ __device__ __forceinline__ void mfma_chunk(const uint32_t (&w)[NB][W], P rec, in
   }
 }
 
-template <int BITS, int G, int NREP, int NB, int C, int NCH, bool BIASED, bool SUMS = false, typename P>
+// (RS: the dwords from one record row to the next, G / 2 unless padded)
+template <int BITS, int G, int NREP, int NB, int C, int NCH, bool BIASED, bool SUMS = false, int RS = G / 2,
+          typename P>
 __device__ __forceinline__ void mfma_chunks(const uint32_t (&w)[NB][G * BITS / 32], P rec, int hl,
                                             const PlanRegs<BITS>& pr, f4_t (&dv)[NB][(NREP + 3) / 4],
                                             const SumRegs<BITS>* sr = nullptr, f4_t* dsum = nullptr) {
   if constexpr (C < NCH) {
     constexpr int CH = (G / 2) / NCH;
     static_assert(!SUMS || (CH % 2 == 0 && (C * CH) % 2 == 0), "sum steps cover whole pairs of pairs");
-    mfma_chunk<BITS, G * BITS / 32, NREP, NB, C * CH, BIASED, SUMS>(w, rec, G / 2, hl, pr, dv, sr, dsum,
+    mfma_chunk<BITS, G * BITS / 32, NREP, NB, C * CH, BIASED, SUMS>(w, rec, RS, hl, pr, dv, sr, dsum,
                                                                     std::make_integer_sequence<int, CH>{});
-    mfma_chunks<BITS, G, NREP, NB, C + 1, NCH, BIASED, SUMS>(w, rec, hl, pr, dv, sr, dsum);
+    mfma_chunks<BITS, G, NREP, NB, C + 1, NCH, BIASED, SUMS, RS>(w, rec, hl, pr, dv, sr, dsum);
   }
 }
 
@@ -301,7 +304,7 @@ __device__ __forceinline__ void group_mfma_biased(const uint32_t (&w)[NB][G * BI
 // group_mfma_biased from zero accumulators, plus the record rows' sums:
 // dsum[q] element i holds, in the lanes with hl = 0, sum(p) of head 4q + i
 // over the group and, in the lanes with hl = 1, sum(p * bias) (SumRegs).
-template <int BITS, int G, int NREP, int NB, typename P>
+template <int BITS, int G, int NREP, int NB, int RS = G / 2, typename P>
 __device__ __forceinline__ void group_mfma_biased_sums(const uint32_t (&w)[NB][G * BITS / 32], P rec, int hl,
                                                        const PlanRegs<BITS>& pr, const SumRegs<BITS>& sr,
                                                        f4_t (&dv)[NB][(NREP + 3) / 4], f4_t (&dsum)[(NREP + 3) / 4]) {
@@ -313,7 +316,7 @@ __device__ __forceinline__ void group_mfma_biased_sums(const uint32_t (&w)[NB][G
 #pragma unroll
     for (int j = 0; j < NB; ++j) dv[j][q] = f4_t{0.f, 0.f, 0.f, 0.f};
   }
-  mfma_chunks<BITS, G, NREP, NB, 0, NCH, true, true>(w, rec, hl, pr, dv, &sr, &dsum[0]);
+  mfma_chunks<BITS, G, NREP, NB, 0, NCH, true, true, RS>(w, rec, hl, pr, dv, &sr, &dsum[0]);
 }
 
 // Query dot products of NB code sets: d[j][h] = sum_i q'[h,i] c_j[i] over the
@@ -420,9 +423,11 @@ struct FusedStore {
 // the fused kernel reads each (batch, KV head) slice through 32-bit buffer offsets
 bool flash_fused_supported(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, const FusedStore& k,
                            const FusedStore& v, int Hq, int Hkv, int D);
+// launch = false: only *grid (the workgroup count the launch would take) is
+// set, nothing is launched
 int flash_fused_launch(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, const FusedStore& k,
                        const FusedStore& v, int B, int Hq, int Hkv, int T, int D, float scale, float* ml,
-                       float* part, int* grid, hipStream_t stream);
+                       float* part, int* grid, hipStream_t stream, bool launch = true);
 // Work partition of the persistent fused kernel: which splits of the
 // (batch, KV head)-major split list each workgroup streams, and in which
 // split slot each of its runs (maximal pieces of one (batch, KV head))
@@ -543,22 +548,41 @@ struct FusedArgs {
 };
 // its launch per K bit width (iq_flash_k{2,3,4}.hip)
 int flash_fused_launch_k2(const FusedArgs& a, int vbits, int group, int D, int nrep, bool norm, int* grid,
-                          hipStream_t stream);
+                          hipStream_t stream, bool launch);
 int flash_fused_launch_k3(const FusedArgs& a, int vbits, int group, int D, int nrep, bool norm, int* grid,
-                          hipStream_t stream);
+                          hipStream_t stream, bool launch);
 int flash_fused_launch_k4(const FusedArgs& a, int vbits, int group, int D, int nrep, bool norm, int* grid,
-                          hipStream_t stream);
+                          hipStream_t stream, bool launch);
 // and for a hybrid V store (iq_flash_vh_k{2,3,4}.hip)
 int flash_fused_launch_vh_k2(const FusedArgs& a, int vbits, int group, int D, int nrep, bool norm, int* grid,
-                             hipStream_t stream);
+                             hipStream_t stream, bool launch);
 int flash_fused_launch_vh_k3(const FusedArgs& a, int vbits, int group, int D, int nrep, bool norm, int* grid,
-                             hipStream_t stream);
+                             hipStream_t stream, bool launch);
 int flash_fused_launch_vh_k4(const FusedArgs& a, int vbits, int group, int D, int nrep, bool norm, int* grid,
-                             hipStream_t stream);
+                             hipStream_t stream, bool launch);
 size_t qk_record_bytes(int B, int Hq, int D);
 size_t av_record_bytes(int B, int Hq, int T, int group);
 size_t av_part_bytes(int B, int Hq, int T, int D, int group);
+// Per-device facts, looked up once per device (a process may drive several
+// GPUs): the current device's index (0 if it cannot be read) and its CU count
+constexpr int MAX_DEVICES = 64;
+int device_index();
 int num_cus();
+// workgroups of `kern` (nt threads) resident per CU at once on the current
+// device, queried once per device and kernel (`cache`: one per kernel)
+struct OccCache {
+  std::atomic<int> n[MAX_DEVICES];
+};
+template <typename K>
+int blocks_per_cu(K kern, int nt, OccCache& cache) {
+  std::atomic<int>& slot = cache.n[device_index()];
+  int v = slot.load(std::memory_order_relaxed);
+  if (v <= 0) {
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, kern, nt, 0) != hipSuccess || v <= 0) v = 1;
+    slot.store(v, std::memory_order_relaxed);
+  }
+  return v;
+}
 }  // namespace detail
 
 template <typename F>

@@ -251,16 +251,22 @@ int launch(const QKArgs& a, int B, int Hq, int Hkv, int D, int group, int bits, 
 
 namespace iq::detail {
 
-int g_num_cus = 0;
+int device_index() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= MAX_DEVICES) dev = 0;
+  return dev;
+}
+
+// CU count per device (MI355X: 256), read once per device
+std::atomic<int> g_num_cus[MAX_DEVICES];
 int num_cus() {
-  if (g_num_cus == 0) {
-    int dev = 0;
-    if (hipGetDevice(&dev) != hipSuccess ||
-        hipDeviceGetAttribute(&g_num_cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        g_num_cus <= 0)
-      g_num_cus = 256;
+  const int dev = device_index();
+  int n = g_num_cus[dev].load(std::memory_order_relaxed);
+  if (n <= 0) {
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    g_num_cus[dev].store(n, std::memory_order_relaxed);
   }
-  return g_num_cus;
+  return n;
 }
 
 int flash_split_tokens() { return SPLIT; }
@@ -343,13 +349,8 @@ int qk_fused_launch(const void* q, int64_t sq_b, int64_t sq_h, const void* norm,
     auto* kern = norm ? flash_fused_kernel<KB, KB, G, DD, R, true, false, true>
                       : flash_fused_kernel<KB, KB, G, DD, R, false, false, true>;
     const int nt = norm ? FusedShape<G, R, true>::NT : FusedShape<G, R, false>::NT;
-    static int per_cu[2] = {0, 0};  // workgroups per CU at once
-    int& pc = per_cu[norm ? 1 : 0];
-    if (pc == 0) {
-      int n = 0;
-      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, kern, nt, 0) != hipSuccess || n <= 0) n = 1;
-      pc = n;
-    }
+    static detail::OccCache occ[2];  // workgroups per CU at once
+    const int pc = detail::blocks_per_cu(kern, nt, occ[norm ? 1 : 0]);
     const int grid = int(std::min<int64_t>(a.nitems, int64_t(pc) * detail::num_cus()));
     kern<<<dim3(grid), nt, 0, stream>>>(a);
     return launch_status();

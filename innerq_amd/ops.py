@@ -243,11 +243,16 @@ class PackedStore:
     # 64-token block for axis 'channel', a G-token group for 'token'; the word
     # and half order inside a unit is the store layout), plus string metadata:
     # format "innerq-packed-store", version, axis, B, H, D, group, bits, mode
-    # ("asymmetric" | "symmetric" | "hybrid"), length, unit.  Codes are
-    # LSB-first fields of little-endian u32 words; sym fields are offset
-    # binary; a hybrid unit's meta is {scale | flag << 15, zero} (flag set: the
-    # group holds sym fields).
-    WIRE_FORMAT, WIRE_VERSION = "innerq-packed-store", "1"
+    # ("asymmetric" | "symmetric" | "hybrid"), length, unit, dtype ("float16" |
+    # "bfloat16").  Codes are LSB-first fields of little-endian u32 words; sym
+    # fields are offset binary; a hybrid unit's meta is {scale | flag << 15,
+    # zero} (flag set: the group holds sym fields).  Version "1" blobs hold
+    # fp16 asym or sym stores only (a reader of version 1 knows no dtype and no
+    # hybrid flag); a bf16 or hybrid store is written as version "2", which
+    # such a reader refuses instead of misreading its metadata.  Both are read.
+    WIRE_FORMAT = "innerq-packed-store"
+    WIRE_VERSION = "2"             # the newest version written
+    WIRE_VERSIONS = ("1", "2")     # versions read
 
     @staticmethod
     def _safetensors(tensors: dict, metadata: dict) -> bytes:
@@ -278,7 +283,8 @@ class PackedStore:
             torch.empty(bh, 0, 0, dtype=torch.int32)
         meta = self.meta.view(bh, nu, -1)[:, :used].contiguous().cpu() if nu else \
             torch.empty(bh, 0, 0, dtype=torch.int16)
-        md = {"format": self.WIRE_FORMAT, "version": self.WIRE_VERSION, "axis": self.axis, "B": self.B,
+        v2 = self.dtype == torch.bfloat16 or self.mode == IQ_MODE_HYBRID
+        md = {"format": self.WIRE_FORMAT, "version": "2" if v2 else "1", "axis": self.axis, "B": self.B,
               "H": self.H, "D": self.D, "group": self.group, "bits": self.bits,
               "mode": MODE_NAMES[self.mode], "length": self.length, "unit": u,
               "dtype": "bfloat16" if self.dtype == torch.bfloat16 else "float16"}
@@ -293,14 +299,16 @@ class PackedStore:
         from safetensors.torch import load
         n = struct.unpack("<Q", blob[:8])[0]
         md = json.loads(blob[8:8 + n].decode("utf-8")).get("__metadata__", {})
-        if md.get("format") != cls.WIRE_FORMAT or md.get("version") != cls.WIRE_VERSION:
-            raise ValueError(f"not an {cls.WIRE_FORMAT} v{cls.WIRE_VERSION} blob: {md.get('format')!r} "
-                             f"v{md.get('version')!r}")
+        if md.get("format") != cls.WIRE_FORMAT or md.get("version") not in cls.WIRE_VERSIONS:
+            raise ValueError(f"not an {cls.WIRE_FORMAT} blob of version {' or '.join(cls.WIRE_VERSIONS)}: "
+                             f"{md.get('format')!r} v{md.get('version')!r}")
         t = load(blob)
         B, H, D, group, bits, length = (int(md[k]) for k in ("B", "H", "D", "group", "bits", "length"))
         dtype = {"float16": torch.float16, "bfloat16": torch.bfloat16}.get(md.get("dtype", "float16"))
         if dtype is None:
             raise ValueError(f"unknown activation dtype {md.get('dtype')!r}")
+        if md["version"] == "1" and dtype != torch.float16 and md.get("dtype") is not None:
+            raise ValueError("a version 1 blob holds an fp16 store")
         st = cls(md["axis"], B, H, D, group, bits, md["mode"], device, t_cap=max(t_cap, length), dtype=dtype)
         u = st.unit
         used, nu = -(-length // u), st.t_cap // u
@@ -685,6 +693,32 @@ def decode_attention_combine(nsplit: int, B: int, Hq: int, T: int, D: int, devic
     ws = _workspace(device, _lib.lib().iq_decode_workspace_bytes(B, Hq, T, D))
     call("iq_decode_attention_combine", nsplit, B, Hq, T, D, _p(out), out.stride(0), out.stride(1), _p(ws),
          ws.numel(), _stream(device))
+    return out
+
+
+def decode_attention_splits_live(q, k_sink, k_store, k_recent, v_sink, v_store, v_recent, scale,
+                                 norm=None) -> "_lib.iq_split_plan":
+    """The split stage exactly as decode_attention launches it (live split slots,
+    the same fused-kernel grid); returns the plan for decode_attention_combine_live."""
+    q, B, Hq, Hkv, T, D, ks, vs, norm, ws = _decode_args(q, k_sink, k_store, k_recent, v_sink, v_store, v_recent,
+                                                         norm)
+    plan = _lib.iq_split_plan()
+    call("iq_decode_attention_splits_live", _p(q), q.stride(0), q.stride(1), _p(norm), ks, vs, B, Hq, Hkv, T, D,
+         float(scale), _p(ws), ws.numel(), ctypes.byref(plan), _stream(q.device))
+    return plan
+
+
+def decode_attention_combine_live(plan, B: int, Hq: int, T: int, D: int, device,
+                                  out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """The combine of a decode_attention_splits_live stage (the same workspace)."""
+    device = torch.device(device)
+    if out is None:
+        out = torch.empty(B, Hq, D, dtype=torch.float16, device=device)
+    require_device(out, "out")
+    check_out(out.shape, (B, Hq, D))
+    ws = _workspace(device, _lib.lib().iq_decode_workspace_bytes(B, Hq, T, D))
+    call("iq_decode_attention_combine_live", ctypes.byref(plan), B, Hq, T, D, _p(out), out.stride(0), out.stride(1),
+         _p(ws), ws.numel(), _stream(device))
     return out
 
 

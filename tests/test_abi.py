@@ -209,6 +209,37 @@ def test_decode_stage_rejects():
     assert lib.iq_decode_attention_combine(1, 1, 32, 64, 128, FAKE, 4096, 128, FAKE, 64, None) == -6
 
 
+def test_decode_live_stages_reject():
+    """iq_decode_attention_splits_live / _combine_live: bad arguments and plans are
+    refused before any launch, and a refused split call leaves the plan as it was."""
+    lib = _lib.lib()
+    seg = (_lib.iq_segment * 3)()
+    seg[2].n = 64
+    seg[2].dense = FAKE
+    plan = _lib.iq_split_plan(nsplit=-7)
+    assert lib.iq_decode_attention_splits_live(FAKE, 1024, 128, None, seg, seg, 1, 32, 8, 64, 128, 1.0, FAKE,
+                                               1 << 30, None, None) == -1
+    assert lib.iq_decode_attention_splits_live(FAKE, 1024, 128, None, seg, seg, 1, 32, 8, 64, 96, 1.0, FAKE,
+                                               1 << 30, ctypes.byref(plan), None) == -4
+    assert lib.iq_decode_attention_splits_live(FAKE, 1024, 128, None, seg, seg, 1, 32, 8, 64, 128, 1.0, FAKE,
+                                               64, ctypes.byref(plan), None) == -6
+    assert plan.nsplit == -7
+
+    def combine(p, B=8, Hq=32, T=32768, D=128, out=FAKE, ws_bytes=1 << 40):
+        return lib.iq_decode_attention_combine_live(ctypes.byref(p), B, Hq, T, D, out, 4096, 128, FAKE, ws_bytes,
+                                                    None)
+
+    ok = dict(nsplit=128, nsf=128, grid=256, nrep=4, pair_e0=68)
+    assert lib.iq_decode_attention_combine_live(None, 8, 32, 32768, 128, FAKE, 4096, 128, FAKE, 1 << 40, None) == -1
+    assert combine(_lib.iq_split_plan(**ok), out=None) == -1
+    assert combine(_lib.iq_split_plan(**ok), ws_bytes=64) == -6
+    for bad in (dict(nrep=3), dict(nsplit=0, nsf=0), dict(nsf=129), dict(nsplit=133), dict(pair_e0=128),
+                dict(pair_e0=-1), dict(grid=-1), dict(grid=1021), dict(nsf=1, nsplit=1, grid=65),
+                dict(nsplit=128, nsf=120)):
+        assert combine(_lib.iq_split_plan(**dict(ok, **bad))) == -4, bad
+    assert combine(_lib.iq_split_plan(**ok), D=96) == -4
+
+
 def test_decode_slot_limit_where_every_slot_is_read():
     """Past 1020 splits of 256 tokens (261,120 tokens), a combine that reads every
     split slot cannot hold them: the split stage alone and the unfused kernels (K

@@ -138,3 +138,31 @@ def test_fused_attention_untagged_keys_take_sdpa():
     a, _ = innerq_fused_attention(M(), q, k, v, None, scaling=0.25)
     b, _ = sdpa_attention_forward(M(), q, k, v, None, scaling=0.25)
     assert torch.equal(a, b)
+
+
+def test_mask_answer_follows_in_place_edits():
+    """The padding answer is cached per mask object and version: a mask reused and
+    edited in place between passes (padding added) is read again, so a padded
+    batch never reaches the fused kernels on a stale "no padding" answer; the
+    cache holds no reference that keeps a mask alive."""
+    import gc
+    import weakref
+
+    import torch
+    from innerq_amd import attention as att
+    m = torch.zeros(2, 1, 1, 8)  # additive mask: 0 = attend
+    assert att._masks_tokens(m) is False
+    assert att._masks_tokens(m) is False  # cached
+    m[1, 0, 0, :3] = float("-inf")        # padding added in place
+    assert att._masks_tokens(m) is True
+    m.zero_()
+    assert att._masks_tokens(m) is False
+    b = torch.ones(1, 1, 1, 8, dtype=torch.bool)
+    assert att._masks_tokens(b) is False
+    b[0, 0, 0, 0] = False
+    assert att._masks_tokens(b) is True
+    r = weakref.ref(b)
+    del b
+    gc.collect()
+    assert r() is None
+    assert att._masks_tokens(None) is False

@@ -675,3 +675,48 @@ def test_decode_stages_equal_decode_attention(fused):
         assert (np.abs(got.astype(np.float64) - ref.astype(np.float64)) <= ulp).all()
     else:
         np.testing.assert_array_equal(got.view(np.uint16), ref.view(np.uint16))
+
+
+@pytest.mark.parametrize("kbits,vbits,R", [(4, 4, 0), (2, 4, 0), (4, 4, 128)])
+def test_decode_live_stages_equal_decode_attention(kbits, vbits, R):
+    """iq_decode_attention_splits_live + _combine_live against decode_attention and
+    against fp32 attention over the library's dequantized K and V, at the headline
+    shape (B=8, 32/8 heads, 32k tokens): the split stage launches the step's own
+    fused kernel (live slots, the same grid: the 4/4-bit paired partition, the
+    plain one for 2/4-bit).  The fused kernel's waves claim token blocks
+    dynamically and round p to fp16 against their own running max, so two runs
+    of it agree to that rounding (the decode tolerance, 1e-3), not bit for bit.
+    With a 128-token window decode_attention merges it after the fused kernel,
+    while the stages take dense slices and the combine."""
+    B, Hkv, nrep, D, T, G = 8, 8, 4, 128, 32768, 32
+    print(f"live stages: kbits={kbits} vbits={vbits} R={R}", flush=True)
+    gen = torch.Generator(device=DEV).manual_seed(kbits * 10 + vbits + R)
+    Tq = T - R
+    kst = ops.PackedStore("channel", B, Hkv, D, G, kbits, "asymmetric", DEV, t_cap=Tq)
+    vst = ops.PackedStore("token", B, Hkv, D, G, vbits, "asymmetric", DEV, t_cap=Tq)
+    k = torch.randn(B, Hkv, T, D, generator=gen, device=DEV).to(torch.float16)
+    v = torch.randn(B, Hkv, T, D, generator=gen, device=DEV).to(torch.float16)
+    kst.append(k[:, :, :Tq])
+    vst.append(v[:, :, :Tq])
+    kr = k[:, :, Tq:] if R else None
+    vr = v[:, :, Tq:] if R else None
+    q = torch.randn(B, Hkv * nrep, D, generator=gen, device=DEV).to(torch.float16)
+    kd = torch.cat([kst.dequant(dtype=torch.float32), k[:, :, Tq:].float()], dim=2)
+    lg = torch.matmul(q.float().view(B, Hkv, nrep, D), kd.transpose(-1, -2).contiguous()) * D ** -0.5
+    del kd
+    vd = torch.cat([vst.dequant(dtype=torch.float32), v[:, :, Tq:].float()], dim=2)
+    ref32 = torch.matmul(torch.softmax(lg, dim=-1), vd).view(B, Hkv * nrep, D)
+    del vd, lg
+    ref = ops.decode_attention(q, None, kst, kr, None, vst, vr, D ** -0.5)
+    plan = ops.decode_attention_splits_live(q, None, kst, kr, None, vst, vr, D ** -0.5)
+    assert plan.grid > 0 and plan.nsf == -(-Tq // 256) and plan.nrep == nrep
+    assert plan.pair_e0 == (68 if kbits == vbits == 4 else 0)
+    assert (plan.nsplit > plan.nsf) == (R > 0)  # the window's dense slices
+    got = ops.decode_attention_combine_live(plan, B, Hkv * nrep, T, D, DEV)
+    torch.cuda.synchronize()
+
+    def err(a, b):
+        return ((a.float() - b.float()).abs().max() / b.float().abs().max()).item()
+    print(f"  vs decode_attention {err(got, ref):.2e}, vs fp32 {err(got, ref32):.2e}, "
+          f"decode_attention vs fp32 {err(ref, ref32):.2e}", flush=True)
+    assert err(got, ref32) < TOL and err(ref, ref32) < TOL and err(got, ref) < TOL

@@ -93,6 +93,39 @@ def test_foreign_and_inconsistent_blobs_are_refused():
     bad = dict(md, length="96")  # more tokens than the units hold
     with pytest.raises(ValueError):
         ops.PackedStore.from_bytes(save(t, metadata=bad), "cpu")
-    bad = dict(md, version="2")
+    bad = dict(md, version="3")
     with pytest.raises(ValueError):
         ops.PackedStore.from_bytes(save(t, metadata=bad), "cpu")
+
+
+def _version(blob):
+    n = struct.unpack("<Q", blob[:8])[0]
+    return json.loads(blob[8:8 + n])["__metadata__"]["version"]
+
+
+@pytest.mark.parametrize("mode,dtype,want", [("asymmetric", torch.float16, "1"), ("symmetric", torch.float16, "1"),
+                                             ("hybrid", torch.float16, "2"), ("asymmetric", torch.bfloat16, "2"),
+                                             ("hybrid", torch.bfloat16, "2")])
+def test_version_marks_what_a_version_1_reader_cannot_read(mode, dtype, want):
+    """fp16 asym / sym stores stay version 1 blobs; a bf16 or hybrid store is written
+    as version 2, which a strict version-1 reader (the earlier from_bytes, which
+    checked version == "1" and knew neither the dtype key nor the hybrid flag)
+    refuses instead of decoding its metadata halves as fp16 or its flags as signs.
+    This reader reads both."""
+    st = _filled("token", 3, mode, 96, 128, seed=5, dtype=dtype)
+    blob = st.to_bytes()
+    assert _version(blob) == want
+    strict_v1_accepts = _version(blob) == "1"
+    assert strict_v1_accepts == (mode != "hybrid" and dtype == torch.float16)
+    back = ops.PackedStore.from_bytes(blob, "cpu")
+    assert back.dtype == dtype and back.mode_arg == st.mode_arg
+
+
+def test_version_1_blob_claiming_bf16_is_refused():
+    from safetensors.torch import load, save
+    st = _filled("token", 3, "asymmetric", 96, 128, seed=6, dtype=torch.bfloat16)
+    blob = st.to_bytes()
+    n = struct.unpack("<Q", blob[:8])[0]
+    md = json.loads(blob[8:8 + n])["__metadata__"]
+    with pytest.raises(ValueError):
+        ops.PackedStore.from_bytes(save(load(blob), metadata=dict(md, version="1")), "cpu")

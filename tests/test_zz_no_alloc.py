@@ -44,7 +44,7 @@ def _err(a, b):
     return ((a.float() - b.float()).abs().max() / b.float().abs().max()).item()
 
 
-def _noalloc(q, kst, vst, kr, vr, scale):
+def _noalloc(q, kst, vst, kr, vr, scale, out=None, stream=None):
     B, Hq, D = q.shape
     kn = [0, kst.length, 0 if kr is None else kr.shape[2]]
     vn = [0, vst.length, 0 if vr is None else vr.shape[2]]
@@ -52,11 +52,13 @@ def _noalloc(q, kst, vst, kr, vr, scale):
                                ops._segment(kr, None, kn[2]))
     vs = (_lib.iq_segment * 3)(ops._segment(None, None, 0), ops._segment(None, vst, vn[1]),
                                ops._segment(vr, None, vn[2]))
-    out = torch.full((B, Hq, D), float("nan"), dtype=torch.float16, device=DEV)
+    if out is None:
+        out = torch.full((B, Hq, D), float("nan"), dtype=torch.float16, device=DEV)
+    stream = torch.cuda.current_stream() if stream is None else stream
     st = _lib.lib().iq_decode_attention_noalloc(
         ctypes.c_void_p(q.data_ptr()), q.stride(0), q.stride(1), None, ks, vs, B, Hq, kst.H, sum(kn), D,
         float(scale), ctypes.c_void_p(out.data_ptr()), out.stride(0), out.stride(1),
-        ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
+        ctypes.c_void_p(stream.cuda_stream))
     assert st == 0, _lib.strerror(st)
     return out
 
@@ -76,3 +78,37 @@ def test_noalloc_matches_decode_attention_twice():
         e_api, e_ref = _err(got, ref), _err(got, ref32)
         print(f"  vs iq_decode_attention {e_api:.2e}, vs fp32 attention {e_ref:.2e}", flush=True)
         assert e_api < 1e-3 and e_ref < 1e-3 and _err(ref, ref32) < 1e-3
+
+
+def test_noalloc_under_graph_capture():
+    """The no-allocation step captured in a HIP graph on a side stream and replayed
+    several times, with eager decode calls between the replays: every replay
+    equals eager decode_attention (decode tolerance).  As the header says, one
+    eager call on the device comes first: it looks up the scratch array's
+    address, which a capture must not be the first to do."""
+    B, Hkv, nrep, D, Tq, R = 4, 8, 4, 128, 8192, 96
+    q, kst, vst, kr, vr, ref32 = _inputs(B, Hkv, nrep, D, Tq, R, 4, 4, seed=3)
+    side = torch.cuda.Stream()
+    out = torch.empty(B, Hkv * nrep, D, dtype=torch.float16, device=DEV)
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        _noalloc(q, kst, vst, kr, vr, D ** -0.5, out=out, stream=side)  # the eager first call
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    eager = ops.decode_attention(q, None, kst, kr, None, vst, vr, D ** -0.5)
+    torch.cuda.synchronize()
+    assert _err(out, eager) < 1e-3 and _err(eager, ref32) < 1e-3
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=side):
+        _noalloc(q, kst, vst, kr, vr, D ** -0.5, out=out, stream=side)
+    for i in range(3):
+        out.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        print(f"replay {i}: vs eager {_err(out, eager):.2e}", flush=True)
+        assert not torch.isnan(out).any()
+        assert _err(out, eager) < 1e-3
+        ops.decode_attention(q, None, kst, kr, None, vst, vr, D ** -0.5)  # eager work between replays
+        _noalloc(q, kst, vst, kr, vr, D ** -0.5)                            # and on the same scratch
+        torch.cuda.synchronize()
