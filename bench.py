@@ -25,6 +25,8 @@ attention) on a sample of the same workload, timed on host cores
 
     python bench.py [--gpus 1] [--steps 100] [--warmup 10]
     python bench.py --config {H,1,2,3,4}    other BASELINE configs (not the headline line)
+    python bench.py --config {base,small_preset,hybrid}
+                                            the reference's presets at the config-4 shape
 """
 from __future__ import annotations
 
@@ -355,6 +357,50 @@ def bench_config(args):
                  + gemv_bytes(B, Hkv, Tq - Tq % G, D, G, 4, "asymmetric", "token"))
         res.update(us=us, us_per_layer=us / L, GBs=b / us / 1e3, us_graph=ug, us_per_layer_graph=ug / L,
                    GBs_graph=b / ug / 1e3, bytes=b)
+    elif cfg in ("base", "small_preset", "hybrid"):
+        # the reference's presets (scripts/run_lmeval.sh:94-153; innerq_amd.presets) at
+        # the config-4 shape: a drop-in cache layer prefilled with 32k tokens (32 fp16
+        # sinks, 32640 packed, 96 recent per role), then decode steps of the product
+        # path: append() (window append, the K token's and, every 32 steps, the V
+        # group's quantize-on-append) + attend() (fused kernel over the packed range,
+        # the merging dense kernel over sinks and windows).  Four layers rotate, so each
+        # step reads cold data; a timed loop covers whole 32-step V flush cycles of
+        # every layer.  Store capacity is reserved before timing (no reallocation).
+        from innerq_amd import cache as IC
+        from innerq_amd import presets
+        name = {"base": "innerq_base", "small_preset": "innerq_small", "hybrid": "innerq_hybrid"}[cfg]
+        B, Hq, Hkv, D, T, L = 8, 32, 8, 128, 32768, 4
+        gen = torch.Generator(device=dev).manual_seed(300)
+
+        def kv(n):
+            x = torch.randn(B, Hkv, n, D, generator=gen, device=dev)
+            x[..., :: D // 4] *= 8.0  # outlier channels
+            return x.to(torch.float16)
+
+        layers = []
+        for l in range(L):
+            layer = IC.InnerqDynamicLayer(presets.preset_config(name), l)
+            layer.update(kv(T), kv(T))
+            layer._kq.store.reserve(T + 4096)
+            layer._vq.store.reserve(T + 4096)
+            layers.append(layer)
+        kn, vn = kv(1), kv(1)
+        q = torch.randn(B, Hq, 1, D, generator=gen, device=dev).to(torch.float16)
+
+        def step(i):
+            layer = layers[i % L]
+            layer.append(kn, vn)
+            layer.attend(q, D ** -0.5)
+
+        clock_warmup(dev)
+        cyc = 32 * L
+        n = max(1, args.steps // cyc) * cyc
+        us = statistics.median(time_backlogged(step, n, cyc) for _ in range(3))
+        lay = layers[0]
+        b = lay._kq.store.nbytes() + lay._vq.store.nbytes()  # packed bytes one step reads (layer 0, at the end)
+        res.update(preset=name, us=us, GBs=b / us / 1e3, frac=b / us / 1e3 / PEAK_GBS, bytes=b, steps=n,
+                   k_packed=lay._kq.length, v_packed=lay._vq.length,
+                   k_window=lay.keys_recent.shape[2], v_window=lay.values_recent.shape[2])
     elif cfg == "small":
         # not a BASELINE config: one sequence (B=1) decode steps and attn.V
         # calls, where a head is spread over many workgroups (a fused run per

@@ -31,6 +31,12 @@ constexpr int DT = 64;        // dense tokens per chunk
 constexpr int NSD_MAX = 4;    // split slots of the dense tokens, at most
 constexpr int DSLICE = 32;    // dense tokens per split slot, at least
 constexpr int MERGE_RUNS_MAX = 4;  // fused runs per (batch, KV head) the merging dense kernel preloads
+// 256-thread sections of the merging dense kernel: three where the window
+// holds packed rows (the reference presets' steady state: 32 sinks, a 96-token
+// recent window and the <= 31 packed keys short of a V group, 129-159 tokens
+// that two sections take in two chunks each: 13.9 us against 15.2 us per
+// call), two for fp16 windows (configs 3 and 4: 7.5 us against 8.2 us)
+constexpr int merge_sections(bool pk) { return pk ? 3 : 2; }
 
 struct Seg {
   const uint16_t* dense;
@@ -129,148 +135,112 @@ struct DenseArgs {
 // ---- packed rows of a dense chunk (kernels with packed segments) ----
 // Tokens in the quantized segment of a list (the middle one: sinks and recent
 // windows are fp16) that fall in the dense range are dequantized into the
-// chunk's LDS tiles.  A chunk's rows form at most two runs of consecutive
-// tokens (one per dense range); per run, the packed units its tokens need -
-// at most two 64-token K blocks, at most three V groups - are copied into LDS
-// with 16-byte loads (one round trip, every load issued before the first LDS
-// write), then each element is decoded from LDS.  Per-element loads from
-// global memory paid one latency per few elements; unrolled per-element code
-// overflowed the instruction cache.
-template <int D>
-struct Stage {
-  static constexpr int KC = 2 * 64 * D * 4 / 32;  // K codes: two blocks at 4 bits (dwords)
-  static constexpr int VC = 32 * D;               // V codes: 3 x D x 4 (G 32), 2 x D x 8 (64), 2 x D x 16 (128)
-  static constexpr int KM = 2 * 64 * (D / 32);    // K meta: two blocks, D / 32 groups, a dword per unit
-  static constexpr int VM = 3 * D;                // V meta: three groups of D units
-  static constexpr int NM = D / 2;                // the key normalization factor
-  static constexpr int KC0 = 0, VC0 = KC, KM0 = VC0 + VC, VM0 = KM0 + KM, NM0 = VM0 + VM, N = NM0 + NM;
-};
+// chunk's fp16 tiles.  A chunk's rows form at most two runs of consecutive
+// tokens (one per dense range).  Each thread decodes 32 consecutive fields of
+// one unit straight from global memory into registers (the unit's `bits`
+// words and its meta word, one round trip, then compile-time shifts): a
+// 32-token piece of one V column (groups along tokens), or 32 columns of one
+// K row (groups along head_dim), and writes their fp16 values into the tile.
+// (Staging the units in LDS and decoding element by element from LDS was
+// LDS-bound: 21 us for a 128-token window at the presets' shape.)
 
-// meta halves per unit: 1 (sym: the scale), 2 ({scale, zero})
-__device__ __forceinline__ int meta_halves(const Seg& g) { return g.mode == IQ_MODE_SYM ? 1 : 2; }
-
-// field + meta of a staged unit -> value (u * s + z), as the reference computes it
-__device__ __forceinline__ float staged_value(const uint32_t* codes, const uint32_t* meta, const Seg& g, int u, int bit) {
-  const int W = (g.bits << g.gsh) >> 5;
-  const int wi = min(bit >> 5, W - 2);
-  const uint32_t* w = codes + u * W + wi;
-  const uint32_t f = uint32_t(((uint64_t(w[1]) << 32) | w[0]) >> (bit - 32 * wi)) & ((1u << g.bits) - 1u);
-  const uint32_t mw = g.mode == IQ_MODE_SYM ? uint32_t(reinterpret_cast<const uint16_t*>(meta)[u]) : meta[u];
-  float s, z;
-  unit_sz(mw, g.mode, g.bits, s, z);
-  return __fadd_rn(__fmul_rn(float(f), s), z);
+// fields i = 0..31 of the first BITS words of w: value u * s + z, as the
+// reference computes it (exact u * s in fp32, one rounding of the sum)
+template <int BITS>
+__device__ __forceinline__ void decode32(const uint32_t (&w)[4], float s, float z, float (&out)[32]) {
+#pragma unroll
+  for (int i = 0; i < 32; ++i) {
+    constexpr uint32_t M = (1u << BITS) - 1u;
+    const int bit = BITS * i, wi = bit >> 5, sh = bit & 31;
+    uint32_t f = w[wi] >> sh;
+    if (sh + BITS > 32) f |= w[wi + 1] << (32 - sh);
+    out[i] = __fadd_rn(__fmul_rn(float(f & M), s), z);
+  }
 }
 
-// one run of the chunk: rows [r0, r1) hold tokens base + r.  Stages, decodes
-// and leaves the workgroup synchronized (the tiles' packed rows written).
-// Run by 256 threads (a workgroup, or one half of a merging workgroup: ALLB,
-// whose halves share the barriers, so both always take both of them).
+// the `bits` words of a unit's 32-field piece and the unit's meta word
+struct Piece {
+  uint32_t w[4];
+  uint32_t m;
+};
+__device__ __forceinline__ void load_piece(const Seg& g, int64_t u, int piece, Piece& p) {
+  const int W = (g.bits << g.gsh) >> 5;  // words per unit
+  const uint32_t* wp = g.codes + u * W + piece * g.bits;
+  p.w[0] = wp[0];
+  p.w[1] = wp[1];
+  p.w[2] = g.bits > 2 ? wp[2] : 0u;
+  p.w[3] = g.bits > 3 ? wp[3] : 0u;
+  p.m = unit_meta(g, u);
+}
+__device__ __forceinline__ void decode_piece(const Seg& g, const Piece& p, float (&out)[32]) {
+  float s, z;
+  unit_sz(p.m, g.mode, g.bits, s, z);
+  switch (g.bits) {
+    case 2: decode32<2>(p.w, s, z, out); break;
+    case 3: decode32<3>(p.w, s, z, out); break;
+    default: decode32<4>(p.w, s, z, out); break;
+  }
+}
+
+// one run of the chunk: rows [r0, r1) hold tokens base + r.  Decodes its
+// packed rows into the tiles and leaves the workgroup synchronized.  Run by
+// 256 threads (a workgroup, or one section of a merging workgroup: ALLB,
+// whose sections share the barrier, so all of them always take it).  A
+// thread decodes K pieces (32 columns of a row), then V pieces (32 tokens of
+// a column), one at a time: loading every piece of the thread first measured
+// no faster and needed more registers than three sections of a merging
+// workgroup hold.
 template <int D, bool ALLB = false>
 __device__ __forceinline__ void packed_run(const Seg& K, const Seg& V, const uint16_t* norm, int64_t bh, int base,
-                                           int r0, int r1, uint32_t* stg, uint16_t* ktile, int kld,
-                                           uint16_t* vtile) {
-  using S = Stage<D>;
+                                           int r0, int r1, uint16_t* ktile, int kld, uint16_t* vtile, int vld) {
+  constexpr int NC = D / 32;  // K pieces per row
   const int tid = int(threadIdx.x) & 255;
   // the run's packed rows per list: [ka, kb) and [va, vb)
   const int ka = max(r0, K.start - base), kb = K.dense ? ka : min(r1, K.start + K.n - base);
   const int va = max(r0, V.start - base), vb = V.dense ? va : min(r1, V.start + V.n - base);
   const bool kon = kb > ka, von = vb > va;
   if (!ALLB && !kon && !von) return;  // uniform
-  // ---- stage: every load first ----
-  int kblk0 = 0, vg0 = 0, nk4 = 0, nv4 = 0, nkm = 0, nvm = 0;
-  const uint4 *kc = nullptr, *vc = nullptr;
-  const uint32_t *km = nullptr, *vm = nullptr;
-  if (kon) {
-    const int sa = K.t0 + (base + ka - K.start), sb = K.t0 + (base + kb - 1 - K.start);
-    kblk0 = sa >> 6;
-    const int nb = (sb >> 6) - kblk0 + 1;
-    const int upb = (D >> K.gsh) * TOKEN_BLOCK;  // units per block
-    const int W = (K.bits << K.gsh) >> 5;
-    const int64_t u0 = (bh * (K.t_cap >> 6) + kblk0) * upb;
-    kc = reinterpret_cast<const uint4*>(K.codes + u0 * W);
-    nk4 = nb * upb * W / 4;
-    km = reinterpret_cast<const uint32_t*>(K.meta + u0 * meta_halves(K));
-    nkm = nb * upb * meta_halves(K) / 2;
-  }
-  if (von) {
-    const int sa = V.t0 + (base + va - V.start), sb = V.t0 + (base + vb - 1 - V.start);
-    vg0 = sa >> V.gsh;
-    const int ng = (sb >> V.gsh) - vg0 + 1;
-    const int W = (V.bits << V.gsh) >> 5;
-    const int64_t u0 = (bh * V.cap_groups + vg0) * D;
-    vc = reinterpret_cast<const uint4*>(V.codes + u0 * W);
-    nv4 = ng * D * W / 4;
-    vm = reinterpret_cast<const uint32_t*>(V.meta + u0 * meta_halves(V));
-    nvm = ng * D * meta_halves(V) / 2;
-  }
-  constexpr int LK = S::KC / 4 / 256, LV = S::VC / 4 / 256, LKM = (S::KM + 255) / 256, LVM = (S::VM + 255) / 256;
-  // loads at clamped indices (straight-line code), then stores at the same
-  // indices: a repeated index stores the value it already holds.  Plain dword
-  // registers (an array of uint4 was kept in scratch).
-  uint32_t rk[4 * LK], rv[4 * LV], rkm[LKM], rvm[LVM], rn = 0;
-  if (kon) {
+  const int kcnt = kon ? (kb - ka) * NC : 0;
+  for (int it = tid; it < kcnt; it += 256) {
+    const int r = ka + it / NC, c = it % NC;
+    const int st = K.t0 + (base + r - K.start);  // the store token
+    const int g = (32 * c) >> K.gsh, piece = ((32 * c) & (K.group - 1)) >> 5;
+    const int64_t u = ((bh * (K.t_cap >> 6) + (st >> 6)) * (D >> K.gsh) + g) * TOKEN_BLOCK + (st & 63);
+    Piece p;
+    load_piece(K, u, piece, p);
+    float v[32];
+    decode_piece(K, p, v);
+    if (norm) {  // the key normalization factor, times the dequantized value (cache.py:128-133)
+      const uint32_t* nr = reinterpret_cast<const uint32_t*>(norm + bh * D + 32 * c);
 #pragma unroll
-    for (int j = 0; j < LK; ++j) {
-      const uint4 x = kc[min(tid + 256 * j, nk4 - 1)];
-      rk[4 * j] = x.x; rk[4 * j + 1] = x.y; rk[4 * j + 2] = x.z; rk[4 * j + 3] = x.w;
+      for (int j = 0; j < 16; ++j) {
+        const uint32_t x = nr[j];
+        v[2 * j] = __fmul_rn(v[2 * j], h2f(uint16_t(x)));
+        v[2 * j + 1] = __fmul_rn(v[2 * j + 1], h2f(uint16_t(x >> 16)));
+      }
     }
+    uint32_t* dst = reinterpret_cast<uint32_t*>(ktile + r * kld + 32 * c);
 #pragma unroll
-    for (int j = 0; j < LKM; ++j) rkm[j] = km[min(tid + 256 * j, nkm - 1)];
+    for (int j = 0; j < 16; ++j)
+      dst[j] = uint32_t(__half_as_ushort(__float2half_rn(v[2 * j]))) |
+               (uint32_t(__half_as_ushort(__float2half_rn(v[2 * j + 1]))) << 16);
   }
-  if (von) {
+  const int sa = V.t0 + (base + va - V.start), sb = sa + (vb - va);  // V store tokens [sa, sb)
+  const int p0 = sa >> 5, vcnt = von ? (((sb + 31) >> 5) - p0) * D : 0;
+  for (int it = tid; it < vcnt; it += 256) {
+    const int pc = p0 + it / D, d = it % D;
+    const int g = (32 * pc) >> V.gsh, piece = ((32 * pc) & (V.group - 1)) >> 5;
+    Piece p;
+    load_piece(V, (bh * V.cap_groups + g) * D + d, piece, p);
+    float v[32];
+    decode_piece(V, p, v);
 #pragma unroll
-    for (int j = 0; j < LV; ++j) {
-      const uint4 x = vc[min(tid + 256 * j, nv4 - 1)];
-      rv[4 * j] = x.x; rv[4 * j + 1] = x.y; rv[4 * j + 2] = x.z; rv[4 * j + 3] = x.w;
+    for (int j = 0; j < 32; ++j) {
+      const int st = 32 * pc + j;
+      if (st >= sa && st < sb) vtile[(va + st - sa) * vld + d] = __half_as_ushort(__float2half_rn(v[j]));
     }
-#pragma unroll
-    for (int j = 0; j < LVM; ++j) rvm[j] = vm[min(tid + 256 * j, nvm - 1)];
   }
-  const bool stn = kon && norm && tid < D / 2;
-  if (stn) rn = reinterpret_cast<const uint32_t*>(norm + bh * D)[tid];
-  if (kon) {
-#pragma unroll
-    for (int j = 0; j < LK; ++j)
-      reinterpret_cast<uint4*>(stg + S::KC0)[min(tid + 256 * j, nk4 - 1)] =
-          make_uint4(rk[4 * j], rk[4 * j + 1], rk[4 * j + 2], rk[4 * j + 3]);
-#pragma unroll
-    for (int j = 0; j < LKM; ++j) stg[S::KM0 + min(tid + 256 * j, nkm - 1)] = rkm[j];
-  }
-  if (von) {
-#pragma unroll
-    for (int j = 0; j < LV; ++j)
-      reinterpret_cast<uint4*>(stg + S::VC0)[min(tid + 256 * j, nv4 - 1)] =
-          make_uint4(rv[4 * j], rv[4 * j + 1], rv[4 * j + 2], rv[4 * j + 3]);
-#pragma unroll
-    for (int j = 0; j < LVM; ++j) stg[S::VM0 + min(tid + 256 * j, nvm - 1)] = rvm[j];
-  }
-  if (stn) stg[S::NM0 + tid] = rn;
   __syncthreads();
-  // ---- decode: element e of the rows, row-major, columns across lanes ----
-  if (kon) {
-    const int cnt = (kb - ka) * D;
-#pragma unroll 4
-    for (int e = tid; e < cnt; e += 256) {
-      const int r = ka + e / D, d = e % D;
-      const int st = K.t0 + (base + r - K.start);
-      const int u = (((st >> 6) - kblk0) * (D >> K.gsh) + (d >> K.gsh)) * TOKEN_BLOCK + (st & 63);
-      float v = staged_value(stg + S::KC0, stg + S::KM0, K, u, (d & (K.group - 1)) * K.bits);
-      if (norm) v = __fmul_rn(v, h2f(reinterpret_cast<const uint16_t*>(stg + S::NM0)[d]));
-      ktile[r * kld + d] = __half_as_ushort(__float2half_rn(v));
-    }
-  }
-  if (von) {
-    const int cnt = (vb - va) * D;
-#pragma unroll 4
-    for (int e = tid; e < cnt; e += 256) {
-      const int r = va + e / D, d = e % D;
-      const int st = V.t0 + (base + r - V.start);
-      const int u = ((st >> V.gsh) - vg0) * D + d;
-      const float v = staged_value(stg + S::VC0, stg + S::VM0, V, u, (st & (V.group - 1)) * V.bits);
-      vtile[r * D + d] = __half_as_ushort(__float2half_rn(v));
-    }
-  }
-  __syncthreads();  // the staging area is reused by the next run
 }
 
 // Online softmax over the dense tokens (fp16 sinks and recent windows, and
@@ -282,39 +252,39 @@ __device__ __forceinline__ void packed_run(const Seg& K, const Seg& V, const uin
 // running (m, l), and thread (head, column pair) accumulates the output.  The
 // probability that meets V is rounded to fp16, as the reference rounds its
 // softmax output; logits, sums and outputs are fp32.
-// MERGE (launched after the fused kernel, one workgroup of two 256-thread
-// halves per (batch, KV head)): each half takes half of the dense tokens as
-// its slice, side by side, and the workgroup then merges the two halves'
-// states with the fused kernel's run partials of the head and writes the
-// output, in place of the dense slots and the combine launch.
+// MERGE (launched after the fused kernel, one workgroup of merge_sections(PK)
+// 256-thread sections per (batch, KV head)): each section takes its share of
+// the dense tokens as its slice, side by side, and the workgroup then merges
+// the sections' states with the fused kernel's run partials of the head and
+// writes the output, in place of the dense slots and the combine launch.
 template <int D, int NREP, bool PK, bool MERGE = false>
-__global__ __launch_bounds__(MERGE ? 512 : 256) void dense_attn_kernel(DenseArgs a) {
-  constexpr int NH = MERGE ? 2 : 1;           // slices per workgroup (256-thread halves)
+__global__ __launch_bounds__(MERGE ? 256 * merge_sections(PK) : 256) void dense_attn_kernel(DenseArgs a) {
+  constexpr int NH = MERGE ? merge_sections(PK) : 1;  // slices per workgroup (256-thread sections)
   constexpr int NTH = 256 * NH;
   constexpr int KS = D / 2 + 1;               // K tile row stride in dwords (odd: no bank conflicts)
+  constexpr int VS = D / 2 + 1;               // V tile row stride: the same (the gather writes a row's
+                                              // quarter per thread; at D / 2 the rows shared their banks)
   constexpr int HPW = (NREP + 3) / 4;         // heads per wave
   constexpr int NPR = D / 2;                  // column pairs per head
   constexpr int OPT = (NREP * NPR + 255) / 256;  // (head, pair) items per thread
   constexpr int RE = D / 4;                   // row elements per gathering thread
   __shared__ uint32_t kts[NH][DT][KS];
-  __shared__ uint32_t vts[NH][DT][D / 2];
+  __shared__ uint32_t vts[NH][DT][VS];
   __shared__ uint32_t qs2[NREP][D / 2];  // the query heads' fp16 pairs
   __shared__ __align__(4) uint16_t pss[NH][NREP][DT];  // fp16 probabilities
   __shared__ float als[NH][NREP];
-  __shared__ __align__(16) uint32_t stgs[PK ? NH : 1][PK ? Stage<D>::N : 4];  // packed-row staging per half
   const int half = MERGE ? int(threadIdx.x >> 8) : 0;
   auto& kt = kts[half];
   auto& vt = vts[half];
   auto& ps = pss[half];
   auto& al = als[half];
-  uint32_t* stg = stgs[PK ? half : 0];
   const int tid = int(threadIdx.x) & 255, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave within the half
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave within the section
   const int bh = blockIdx.y, b = bh / a.Hkv, kvh = bh % a.Hkv;
   const int n0 = a.hi0 - a.lo0, n = n0 + (a.hi1 - a.lo1);
   const int nsl = MERGE ? NH : int(gridDim.x), sl = MERGE ? half : int(blockIdx.x);  // slices, this one
   const int i0 = int(int64_t(sl) * n / nsl), i1 = int(int64_t(sl + 1) * n / nsl);
-  // chunks: the same count in both halves (their barriers are shared)
+  // chunks: the same count in every section (their barriers are shared)
   const int nch = MERGE ? ((n + NH - 1) / NH + DT - 1) / DT : (i1 - i0 + DT - 1) / DT;
   const int64_t rows = int64_t(gridDim.y) * NREP;
 
@@ -360,7 +330,7 @@ __global__ __launch_bounds__(MERGE ? 512 : 256) void dense_attn_kernel(DenseArgs
   for (int it = 0; it < OPT; ++it) o[it][0] = o[it][1] = 0.f;
 
   for (int ci = 0; ci < nch; ++ci) {
-    // a chunk past the slice's tokens (MERGE: the shorter half) has no live
+    // a chunk past the slice's tokens (MERGE: a shorter section) has no live
     // token: its logits are -inf and no V row is read
     const int c0 = i0 + ci * DT;
     // the fp16 rows from registers; packed rows are decoded into the tiles
@@ -378,8 +348,8 @@ __global__ __launch_bounds__(MERGE ? 512 : 256) void dense_attn_kernel(DenseArgs
       const int rend = min(DT, i1 - c0), rs = min(max(n0 - c0, 0), rend);
       uint16_t* kth = reinterpret_cast<uint16_t*>(&kt[0][0]);
       uint16_t* vth = reinterpret_cast<uint16_t*>(&vt[0][0]);
-      packed_run<D, MERGE>(a.k[1], a.v[1], a.norm, bh64, a.lo0 + c0, 0, rs, stg, kth, 2 * KS, vth);
-      packed_run<D, MERGE>(a.k[1], a.v[1], a.norm, bh64, a.lo1 + c0 - n0, rs, rend, stg, kth, 2 * KS, vth);
+      packed_run<D, MERGE>(a.k[1], a.v[1], a.norm, bh64, a.lo0 + c0, 0, rs, kth, 2 * KS, vth, 2 * VS);
+      packed_run<D, MERGE>(a.k[1], a.v[1], a.norm, bh64, a.lo1 + c0 - n0, rs, rend, kth, 2 * KS, vth, 2 * VS);
     }
     __syncthreads();
     if (c0 + DT < i1) gather(c0 + DT);  // in flight through this chunk
@@ -467,7 +437,7 @@ __global__ __launch_bounds__(MERGE ? 512 : 256) void dense_attn_kernel(DenseArgs
     __syncthreads();
   }
   if constexpr (MERGE) {
-    // ---- merge: the two halves' states and the fused runs' partials ----
+    // ---- merge: the sections' states and the fused runs' partials ----
     __shared__ float mh[NH][NREP], lh[NH][NREP];
     __shared__ float oh[NH][NREP][D];
 #pragma unroll
@@ -500,7 +470,7 @@ __global__ __launch_bounds__(MERGE ? 512 : 256) void dense_attn_kernel(DenseArgs
         if (sp < nr) M = fmaxf(M, pre ? pm[sp] : a.fml[(int64_t(sp) * rows + row) * 2]);
       for (int sp = NRPRE; sp < nr; ++sp) M = fmaxf(M, a.fml[(int64_t(sp) * rows + row) * 2]);
       float L = 0.f, acc = 0.f;
-      auto add_run = [&](float ms, float ls, float pv) {  // the runs in slot order, then the halves
+      auto add_run = [&](float ms, float ls, float pv) {  // the runs in slot order, then the sections
         const float w = ms == -INFINITY ? 0.f : __expf(ms - M);
         L = fmaf(w, ls, L);
         acc = w != 0.f ? fmaf(w, pv, acc) : acc;
@@ -748,7 +718,8 @@ struct MergeOut {
   int64_t so_b, so_h;
 };
 // dense tokens per (batch, KV head), at most, that the merging dense kernel
-// takes (two halves of up to 2 chunks each); longer windows take the slices
+// takes (its sections' chunks: at most two per section); longer windows take
+// the slices
 constexpr int MERGE_DENSE_MAX = 4 * DT;
 
 // Launches everything up to the split statistics and partials.  `live`: the
@@ -889,8 +860,8 @@ int launch_splits(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, c
       da.soh = mo->so_h;
       const dim3 mgrid{1u, unsigned(bhs), 1u};
       auto go = [&]<int DD, int R>() {
-        if (pk) dense_attn_kernel<DD, R, true, true><<<mgrid, 512, 0, st>>>(da);
-        else dense_attn_kernel<DD, R, false, true><<<mgrid, 512, 0, st>>>(da);
+        if (pk) dense_attn_kernel<DD, R, true, true><<<mgrid, 256 * merge_sections(true), 0, st>>>(da);
+        else dense_attn_kernel<DD, R, false, true><<<mgrid, 256 * merge_sections(false), 0, st>>>(da);
       };
       auto by_r = [&]<int DD>() {
         switch (Hq / Hkv) {
