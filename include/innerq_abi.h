@@ -235,14 +235,15 @@ int iq_av_gemv(const void* p, int64_t sp_b, int64_t sp_h,
  * (s_b, s_h, s_t), D contiguous.  A quantized segment names a store and its
  * first token. */
 typedef struct iq_segment {
-  const void* dense;          /* fp16 segment or NULL */
+  const void* dense;          /* fp16 (bf16) segment or NULL */
   int64_t s_b, s_h, s_t;
   int n;                      /* tokens in this segment (0 = absent) */
   const uint32_t* codes;      /* packed store (quantized segment) or NULL */
   const uint16_t* meta;
   int64_t t_cap;
   int t0;
-  int bits, group, mode;
+  int bits, group, mode;      /* mode: the store's; of a dense segment only the
+                                 IQ_MODE_BF16 bit (its rows are bf16) */
 } iq_segment;
 
 /* One role (K or V) of a layer's decode-step append: the fp16 recent window
@@ -286,7 +287,13 @@ size_t iq_decode_workspace_bytes(int B, int Hq, int T, int D);
  * normalization factor of the quantized K segment; the quantized V segment
  * may be a hybrid store (K: asym or sym).  out fp16 [B,Hq,D]
  * (strides so_b, so_h).  Replaces update()'s dense read path (cache.py:278-281,
- * 395) plus the eager attention of TF/models/llama/modeling_llama.py:201-210. */
+ * 395) plus the eager attention of TF/models/llama/modeling_llama.py:201-210.
+ * A bf16 layer (LongBench/pred.py:240 loads the model in bf16): IQ_MODE_BF16
+ * on the mode of every segment that holds tokens (its stores were written
+ * with it); q, norm, the dense rows and out are then bf16, the probabilities
+ * of the packed range meet V as fp16 (finer than the reference's bf16 cast),
+ * those of the dense tokens as bf16.  Segments that disagree: IQ_ERR_MODE;
+ * bf16 K and V of different group sizes: IQ_ERR_MODE (fp16 only). */
 int iq_decode_attention(const void* q, int64_t sq_b, int64_t sq_h, const void* norm,
                         const iq_segment* k, const iq_segment* v,
                         int B, int Hq, int Hkv, int T, int D, float scale,
@@ -294,7 +301,9 @@ int iq_decode_attention(const void* q, int64_t sq_b, int64_t sq_h, const void* n
                         void* workspace, size_t workspace_bytes, void* stream);
 
 /* The two stages of iq_decode_attention, for callers that schedule them
- * separately (e.g. to time or overlap the split stage).  _splits validates as
+ * separately (e.g. to time or overlap the split stage); fp16 layers only
+ * (_combine cannot tell a bf16 call's output type: IQ_ERR_MODE; a bf16 layer
+ * takes the live stages below, whose plan records it).  _splits validates as
  * iq_decode_attention, launches every kernel up to the per-split softmax
  * statistics and unnormalized partial outputs (kept in the workspace) and
  * stores their count in *nsplit (host memory, known at return).  _combine
@@ -323,7 +332,8 @@ typedef struct iq_split_plan {
   int grid;     /* workgroups of the fused kernel (0: not launched) */
   int nrep;     /* query heads per KV head */
   int pair_e0;  /* the fused kernel's work partition */
-  int reserved[3];
+  int bf16;     /* the output's dtype: 1 bf16, 0 fp16 */
+  int reserved[2];
 } iq_split_plan;
 int iq_decode_attention_splits_live(const void* q, int64_t sq_b, int64_t sq_h, const void* norm,
                                     const iq_segment* k, const iq_segment* v,

@@ -69,7 +69,7 @@ class iq_window(ctypes.Structure):
 
 class iq_split_plan(ctypes.Structure):
     _fields_ = [("nsplit", ctypes.c_int), ("nsf", ctypes.c_int), ("grid", ctypes.c_int), ("nrep", ctypes.c_int),
-                ("pair_e0", ctypes.c_int), ("reserved", ctypes.c_int * 3)]
+                ("pair_e0", ctypes.c_int), ("bf16", ctypes.c_int), ("reserved", ctypes.c_int * 2)]
 
 
 SIGNATURES = {

@@ -63,7 +63,7 @@ def innerq_fused_attention(module, query, key, value, attention_mask, dropout: f
     if scaling is None:
         scaling = query.shape[-1] ** -0.5
     nrep = query.shape[1] // key.shape[1]
-    if (_masks_tokens(attention_mask) or dropout or query.dtype != torch.float16 or query.shape[-1] not in (64, 128)
+    if (_masks_tokens(attention_mask) or dropout or query.dtype != layer.dtype or query.shape[-1] not in (64, 128)
             or nrep not in (1, 2, 4, 8) or query.shape[1] != nrep * key.shape[1]):
         k, v = layer.get_deq_tensors()
         return sdpa_attention_forward(module, query, k, v, attention_mask, dropout=dropout, scaling=scaling,

@@ -340,9 +340,11 @@ class InnerqDynamicLayer(CacheLayerMixin):
 
     def _fused_refusal(self) -> Optional[str]:
         """Why attend() cannot read this layer's stores (None if it can): K must be
-        grouped along head_dim (asym or sym), V along tokens (asym, sym or hybrid), fp16."""
-        if self.dtype != torch.float16:
-            return "fused decode takes fp16 activations (bf16 layers take the dequantize-then-attend path)"
+        grouped along head_dim (asym or sym), V along tokens (asym, sym or hybrid), and
+        a bf16 layer's K and V of one group size."""
+        if (self.dtype == torch.bfloat16 and self._kq is not None and self._vq is not None
+                and self._kq.group != self._vq.group):
+            return "fused decode of a bf16 layer needs K and V of one group size"
         if self._kq is not None and (self._kq.axis != "channel" or self._kq.mode == QMode.HYBRID):
             return "fused decode reads keys grouped along the head_dim axis, asym or sym"
         if self._vq is not None and self._vq.axis != "token":
@@ -359,8 +361,9 @@ class InnerqDynamicLayer(CacheLayerMixin):
 
     def attend(self, query_states: torch.Tensor, scaling: float) -> torch.Tensor:
         """Decode attention of one new token per sequence over this layer's cache:
-        softmax(q K^T * scaling, fp32) -> fp16 -> @ V (TF/models/llama/modeling_llama.py:201-210),
-        with K and V read packed.  query_states [B, Hq, 1, D] fp16 -> [B, Hq, 1, D] fp16."""
+        softmax(q K^T * scaling, fp32) -> @ V (TF/models/llama/modeling_llama.py:201-210), with
+        K and V read packed.  query_states [B, Hq, 1, D] in the layer's dtype (fp16 or bf16)
+        -> [B, Hq, 1, D] of that dtype."""
         if query_states.dim() != 4 or query_states.shape[2] != 1:
             raise ValueError("attend() takes one query token per sequence: [B, Hq, 1, D]")
         if not self.is_initialized:

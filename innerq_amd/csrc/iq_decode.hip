@@ -36,7 +36,8 @@ constexpr int MERGE_RUNS_MAX = 4;  // fused runs per (batch, KV head) the mergin
 // recent window and the <= 31 packed keys short of a V group, 129-159 tokens
 // that two sections take in two chunks each: 13.9 us against 15.2 us per
 // call), two for fp16 windows (configs 3 and 4: 7.5 us against 8.2 us)
-constexpr int merge_sections(bool pk) { return pk ? 3 : 2; }
+// (bf16 layers: two, whose fp32 tiles fill the LDS)
+constexpr int merge_sections(bool pk, bool bf = false) { return pk && !bf ? 3 : 2; }
 
 struct Seg {
   const uint16_t* dense;
@@ -55,17 +56,34 @@ struct Seg {
 // its fp16 scale for sym) with value = u * s + z for its b-bit field u (exact
 // in fp32: sym offset binary folds into z = -2^(b-1) s; a hybrid unit as its
 // flag says)
-__device__ __forceinline__ void unit_sz(uint32_t mw, int mode, int bits, float& s, float& z) {
+// (bf: the halves hold bf16 values, a bf16 layer's store)
+__device__ __forceinline__ void unit_sz(uint32_t mw, int mode, int bits, float& s, float& z, bool bf = false) {
   if (mode == IQ_MODE_SYM) {
-    s = h2f(uint16_t(mw));
+    s = act2f(uint16_t(mw), bf);
     z = -float(1 << (bits - 1)) * s;
   } else if (mode == IQ_MODE_HYBRID) {
-    s = hyb_scale(mw);
-    z = hyb_sym(mw) ? -float(1 << (bits - 1)) * s : h2f(uint16_t(mw >> 16));
+    s = hyb_scale(mw, bf);
+    z = hyb_sym(mw) ? -float(1 << (bits - 1)) * s : act2f(uint16_t(mw >> 16), bf);
   } else {
-    s = h2f(uint16_t(mw & 0xffffu));
-    z = h2f(uint16_t(mw >> 16));
+    s = act2f(uint16_t(mw & 0xffffu), bf);
+    z = act2f(uint16_t(mw >> 16), bf);
   }
+}
+
+typedef __bf16 bf2_t __attribute__((ext_vector_type(2)));
+// c + a.x * b.x + a.y * b.y over two 16-bit pairs of the activation type
+// (v_dot2_f32_f16 / v_dot2_f32_bf16: exact products, fp32 accumulation)
+template <bool BF>
+__device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
+  if constexpr (BF)
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf2_t, a), __builtin_bit_cast(bf2_t, b), c, false);
+  else
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_t, a), __builtin_bit_cast(h2_t, b), c, false);
+}
+template <bool BF>
+__device__ __forceinline__ uint32_t to_act(float x) {
+  if constexpr (BF) return f2bf(x);
+  else return __half_as_ushort(__float2half_rn(x));
 }
 
 __device__ __forceinline__ uint32_t unit_meta(const Seg& g, int64_t unit) {
@@ -172,9 +190,10 @@ __device__ __forceinline__ void load_piece(const Seg& g, int64_t u, int piece, P
   p.w[3] = g.bits > 3 ? wp[3] : 0u;
   p.m = unit_meta(g, u);
 }
+template <bool BF>
 __device__ __forceinline__ void decode_piece(const Seg& g, const Piece& p, float (&out)[32]) {
   float s, z;
-  unit_sz(p.m, g.mode, g.bits, s, z);
+  unit_sz(p.m, g.mode, g.bits, s, z, BF);
   switch (g.bits) {
     case 2: decode32<2>(p.w, s, z, out); break;
     case 3: decode32<3>(p.w, s, z, out); break;
@@ -183,16 +202,17 @@ __device__ __forceinline__ void decode_piece(const Seg& g, const Piece& p, float
 }
 
 // one run of the chunk: rows [r0, r1) hold tokens base + r.  Decodes its
-// packed rows into the tiles and leaves the workgroup synchronized.  Run by
+// packed rows into the tiles (row strides kld, vld in dwords; fp16 pairs, or
+// fp32 values in a bf16 layer's tiles) and leaves the workgroup synchronized.  Run by
 // 256 threads (a workgroup, or one section of a merging workgroup: ALLB,
 // whose sections share the barrier, so all of them always take it).  A
 // thread decodes K pieces (32 columns of a row), then V pieces (32 tokens of
 // a column), one at a time: loading every piece of the thread first measured
 // no faster and needed more registers than three sections of a merging
 // workgroup hold.
-template <int D, bool ALLB = false>
+template <int D, bool ALLB = false, bool BF = false>
 __device__ __forceinline__ void packed_run(const Seg& K, const Seg& V, const uint16_t* norm, int64_t bh, int base,
-                                           int r0, int r1, uint16_t* ktile, int kld, uint16_t* vtile, int vld) {
+                                           int r0, int r1, uint32_t* ktile, int kld, uint32_t* vtile, int vld) {
   constexpr int NC = D / 32;  // K pieces per row
   const int tid = int(threadIdx.x) & 255;
   // the run's packed rows per list: [ka, kb) and [va, vb)
@@ -209,21 +229,27 @@ __device__ __forceinline__ void packed_run(const Seg& K, const Seg& V, const uin
     Piece p;
     load_piece(K, u, piece, p);
     float v[32];
-    decode_piece(K, p, v);
+    decode_piece<BF>(K, p, v);
     if (norm) {  // the key normalization factor, times the dequantized value (cache.py:128-133)
       const uint32_t* nr = reinterpret_cast<const uint32_t*>(norm + bh * D + 32 * c);
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
         const uint32_t x = nr[j];
-        v[2 * j] = __fmul_rn(v[2 * j], h2f(uint16_t(x)));
-        v[2 * j + 1] = __fmul_rn(v[2 * j + 1], h2f(uint16_t(x >> 16)));
+        v[2 * j] = __fmul_rn(v[2 * j], act2f(uint16_t(x), BF));
+        v[2 * j + 1] = __fmul_rn(v[2 * j + 1], act2f(uint16_t(x >> 16), BF));
       }
     }
-    uint32_t* dst = reinterpret_cast<uint32_t*>(ktile + r * kld + 32 * c);
+    if constexpr (BF) {  // fp32 tile: the dequantized values as they are
+      uint32_t* dst = ktile + r * kld + 32 * c;
 #pragma unroll
-    for (int j = 0; j < 16; ++j)
-      dst[j] = uint32_t(__half_as_ushort(__float2half_rn(v[2 * j]))) |
-               (uint32_t(__half_as_ushort(__float2half_rn(v[2 * j + 1]))) << 16);
+      for (int j = 0; j < 32; ++j) dst[j] = __float_as_uint(v[j]);
+    } else {
+      uint32_t* dst = ktile + r * kld + 16 * c;
+#pragma unroll
+      for (int j = 0; j < 16; ++j)
+        dst[j] = uint32_t(__half_as_ushort(__float2half_rn(v[2 * j]))) |
+                 (uint32_t(__half_as_ushort(__float2half_rn(v[2 * j + 1]))) << 16);
+    }
   }
   const int sa = V.t0 + (base + va - V.start), sb = sa + (vb - va);  // V store tokens [sa, sb)
   const int p0 = sa >> 5, vcnt = von ? (((sb + 31) >> 5) - p0) * D : 0;
@@ -233,11 +259,14 @@ __device__ __forceinline__ void packed_run(const Seg& K, const Seg& V, const uin
     Piece p;
     load_piece(V, (bh * V.cap_groups + g) * D + d, piece, p);
     float v[32];
-    decode_piece(V, p, v);
+    decode_piece<BF>(V, p, v);
 #pragma unroll
     for (int j = 0; j < 32; ++j) {
       const int st = 32 * pc + j;
-      if (st >= sa && st < sb) vtile[(va + st - sa) * vld + d] = __half_as_ushort(__float2half_rn(v[j]));
+      if (st >= sa && st < sb) {
+        if constexpr (BF) vtile[(va + st - sa) * vld + d] = __float_as_uint(v[j]);
+        else reinterpret_cast<uint16_t*>(vtile)[(va + st - sa) * 2 * vld + d] = __half_as_ushort(__float2half_rn(v[j]));
+      }
     }
   }
   __syncthreads();
@@ -257,26 +286,34 @@ __device__ __forceinline__ void packed_run(const Seg& K, const Seg& V, const uin
 // the dense tokens as its slice, side by side, and the workgroup then merges
 // the sections' states with the fused kernel's run partials of the head and
 // writes the output, in place of the dense slots and the combine launch.
-template <int D, int NREP, bool PK, bool MERGE = false>
-__global__ __launch_bounds__(MERGE ? 256 * merge_sections(PK) : 256) void dense_attn_kernel(DenseArgs a) {
-  constexpr int NH = MERGE ? merge_sections(PK) : 1;  // slices per workgroup (256-thread sections)
+// BF: a bf16 layer (query, rows, factor, metadata and output in bf16).  Its
+// tiles hold fp32 values (bf16 rows convert exactly, packed rows keep their
+// fp32 dequantized values) and the logits and p.V are fp32 products with the
+// unrounded probabilities: rounding the window's rows and probabilities to
+// bf16 put a window-heavy step at 1.005e-3 of fp32 attention.
+template <int D, int NREP, bool PK, bool MERGE = false, bool BF = false>
+__global__ __launch_bounds__(MERGE ? 256 * merge_sections(PK, BF) : 256) void dense_attn_kernel(DenseArgs a) {
+  constexpr int NH = MERGE ? merge_sections(PK, BF) : 1;  // slices per workgroup (256-thread sections)
   constexpr int NTH = 256 * NH;
-  constexpr int KS = D / 2 + 1;               // K tile row stride in dwords (odd: no bank conflicts)
-  constexpr int VS = D / 2 + 1;               // V tile row stride: the same (the gather writes a row's
-                                              // quarter per thread; at D / 2 the rows shared their banks)
+  constexpr int TW = BF ? D : D / 2;          // dwords of a row's values: fp32, or fp16 pairs
+  constexpr int KS = TW + 1;                  // K tile row stride in dwords (odd: no bank conflicts)
+  constexpr int VS = BF ? D + 2 : D / 2 + 1;  // V tile row stride (fp16: odd, the gather writes a row's
+                                              // quarter per thread and at D / 2 the rows shared their
+                                              // banks; fp32: even, for column-pair reads)
   constexpr int HPW = (NREP + 3) / 4;         // heads per wave
   constexpr int NPR = D / 2;                  // column pairs per head
   constexpr int OPT = (NREP * NPR + 255) / 256;  // (head, pair) items per thread
   constexpr int RE = D / 4;                   // row elements per gathering thread
   __shared__ uint32_t kts[NH][DT][KS];
-  __shared__ uint32_t vts[NH][DT][VS];
-  __shared__ uint32_t qs2[NREP][D / 2];  // the query heads' fp16 pairs
-  __shared__ __align__(4) uint16_t pss[NH][NREP][DT];  // fp16 probabilities
+  __shared__ __align__(8) uint32_t vts[NH][DT][VS];
+  __shared__ uint32_t qs2[NREP][TW];  // the query heads' fp16 pairs (fp32 values: BF)
+  __shared__ __align__(4) uint16_t pss[NH][NREP][BF ? 2 * DT : DT];  // probabilities: fp16 (fp32: BF)
   __shared__ float als[NH][NREP];
   const int half = MERGE ? int(threadIdx.x >> 8) : 0;
   auto& kt = kts[half];
   auto& vt = vts[half];
   auto& ps = pss[half];
+  float* psf = reinterpret_cast<float*>(&pss[half][0][0]);  // BF: [NREP][DT] fp32
   auto& al = als[half];
   const int tid = int(threadIdx.x) & 255, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave within the section
@@ -317,10 +354,14 @@ __global__ __launch_bounds__(MERGE ? 256 * merge_sections(PK) : 256) void dense_
     }
   }
   if (i0 < i1) gather(i0);
-  for (int i = int(threadIdx.x); i < NREP * D / 2; i += NTH) {
-    const int h = i / (D / 2), c = i % (D / 2);
-    const uint16_t* qr = a.q + b * a.sqb + (kvh * NREP + h) * a.sqh + 2 * c;
-    qs2[h][c] = uint32_t(qr[0]) | (uint32_t(qr[1]) << 16);
+  for (int i = int(threadIdx.x); i < NREP * TW; i += NTH) {
+    const int h = i / TW, c = i % TW;
+    if constexpr (BF) {
+      qs2[h][c] = __float_as_uint(bf2f(a.q[b * a.sqb + (kvh * NREP + h) * a.sqh + c]));
+    } else {
+      const uint16_t* qr = a.q + b * a.sqb + (kvh * NREP + h) * a.sqh + 2 * c;
+      qs2[h][c] = uint32_t(qr[0]) | (uint32_t(qr[1]) << 16);
+    }
   }
   float m[HPW], l[HPW];
 #pragma unroll
@@ -337,19 +378,32 @@ __global__ __launch_bounds__(MERGE ? 256 * merge_sections(PK) : 256) void dense_
     // (disjoint rows: no ordering needed between the two)
     if (!kpk) {
 #pragma unroll
-      for (int j = 0; j < RE / 2; ++j) kt[gr][gq * (RE / 2) + j] = kr[j];
+      for (int j = 0; j < RE / 2; ++j) {
+        if constexpr (BF) {
+          kt[gr][gq * RE + 2 * j] = kr[j] << 16;             // bf16 -> fp32: exact
+          kt[gr][gq * RE + 2 * j + 1] = kr[j] & 0xffff0000u;
+        } else {
+          kt[gr][gq * (RE / 2) + j] = kr[j];
+        }
+      }
     }
     if (!vpk) {
 #pragma unroll
-      for (int j = 0; j < RE / 2; ++j) vt[gr][gq * (RE / 2) + j] = vr[j];
+      for (int j = 0; j < RE / 2; ++j) {
+        if constexpr (BF) {
+          vt[gr][gq * RE + 2 * j] = vr[j] << 16;
+          vt[gr][gq * RE + 2 * j + 1] = vr[j] & 0xffff0000u;
+        } else {
+          vt[gr][gq * (RE / 2) + j] = vr[j];
+        }
+      }
     }
     if constexpr (PK) {  // runs: dense range 0 (rows < n0 - c0), then range 1
       const int64_t bh64 = int64_t(b) * a.Hkv + kvh;
       const int rend = min(DT, i1 - c0), rs = min(max(n0 - c0, 0), rend);
-      uint16_t* kth = reinterpret_cast<uint16_t*>(&kt[0][0]);
-      uint16_t* vth = reinterpret_cast<uint16_t*>(&vt[0][0]);
-      packed_run<D, MERGE>(a.k[1], a.v[1], a.norm, bh64, a.lo0 + c0, 0, rs, kth, 2 * KS, vth, 2 * VS);
-      packed_run<D, MERGE>(a.k[1], a.v[1], a.norm, bh64, a.lo1 + c0 - n0, rs, rend, kth, 2 * KS, vth, 2 * VS);
+      packed_run<D, MERGE, BF>(a.k[1], a.v[1], a.norm, bh64, a.lo0 + c0, 0, rs, &kt[0][0], KS, &vt[0][0], VS);
+      packed_run<D, MERGE, BF>(a.k[1], a.v[1], a.norm, bh64, a.lo1 + c0 - n0, rs, rend, &kt[0][0], KS, &vt[0][0],
+                               VS);
     }
     __syncthreads();
     if (c0 + DT < i1) gather(c0 + DT);  // in flight through this chunk
@@ -360,15 +414,16 @@ __global__ __launch_bounds__(MERGE ? 256 * merge_sections(PK) : 256) void dense_
     // no per-iteration guard on the head (a wave-uniform branch in the loop
     // serialized it on LDS latency): heads past NREP read the last head's
     // query and their logits are dropped below
-    // one v_dot2_f32_f16 per (head, column pair): both fp16 products exact,
-    // accumulated in fp32
+    // one v_dot2_f32_f16 per (head, column pair): both products exact,
+    // accumulated in fp32 (BF: one fp32 fma per column)
 #pragma unroll 16
-    for (int i = 0; i < D / 2; ++i) {
-      const h2_t k2 = __builtin_bit_cast(h2_t, kt[lane][i]);
+    for (int i = 0; i < TW; ++i) {
+      const uint32_t k2 = kt[lane][i];
 #pragma unroll
       for (int hh = 0; hh < HPW; ++hh) {
         const int h = min(wave + 4 * hh, NREP - 1);
-        dot[hh] = __builtin_amdgcn_fdot2(k2, __builtin_bit_cast(h2_t, qs2[h][i]), dot[hh], false);
+        if constexpr (BF) dot[hh] = fmaf(__uint_as_float(k2), __uint_as_float(qs2[h][i]), dot[hh]);
+        else dot[hh] = dot2<false>(k2, qs2[h][i], dot[hh]);
       }
     }
     const bool live = c0 + lane < i1;
@@ -391,7 +446,8 @@ __global__ __launch_bounds__(MERGE ? 256 * merge_sections(PK) : 256) void dense_
       for (int hh = 0; hh < HPW; ++hh) {
         const int h = wave + 4 * hh;
         if (h < NREP) {
-          ps[h][lane] = __half_as_ushort(__float2half_rn(x[hh]));
+          if constexpr (BF) psf[h * DT + lane] = x[hh];
+          else ps[h][lane] = __half_as_ushort(__float2half_rn(x[hh]));
           const float alpha = m[hh] == -INFINITY ? 0.f : __expf(m[hh] - mx[hh]);
           l[hh] = fmaf(l[hh], alpha, cs[hh]);
           m[hh] = mx[hh];
@@ -415,19 +471,27 @@ __global__ __launch_bounds__(MERGE ? 256 * merge_sections(PK) : 256) void dense_
         for (int j = 0; j < cnt8; j += 8) {
 #pragma unroll
           for (int u = 0; u < 8; u += 4) {
-            const uint32_t pq = *reinterpret_cast<const uint32_t*>(&ps[h][j + u]);
-            const uint32_t pr = *reinterpret_cast<const uint32_t*>(&ps[h][j + u + 2]);
-            const uint32_t va = vt[j + u][dp], vb = vt[j + u + 1][dp];
-            const uint32_t vc = vt[j + u + 2][dp], vd = vt[j + u + 3][dp];
-            // columns 2 dp and 2 dp + 1 of tokens (j+u, j+u+1), then (j+u+2, j+u+3)
-            o0 = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_t, __builtin_amdgcn_perm(vb, va, 0x05040100u)),
-                                        __builtin_bit_cast(h2_t, pq), o0, false);
-            o1 = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_t, __builtin_amdgcn_perm(vb, va, 0x07060302u)),
-                                        __builtin_bit_cast(h2_t, pq), o1, false);
-            e0 = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_t, __builtin_amdgcn_perm(vd, vc, 0x05040100u)),
-                                        __builtin_bit_cast(h2_t, pr), e0, false);
-            e1 = __builtin_amdgcn_fdot2(__builtin_bit_cast(h2_t, __builtin_amdgcn_perm(vd, vc, 0x07060302u)),
-                                        __builtin_bit_cast(h2_t, pr), e1, false);
+            if constexpr (BF) {  // fp32 values and probabilities: columns 2 dp, 2 dp + 1 of four tokens
+              const float* pf = psf + h * DT + j + u;
+              const float2 va = *reinterpret_cast<const float2*>(&vt[j + u][2 * dp]);
+              const float2 vb = *reinterpret_cast<const float2*>(&vt[j + u + 1][2 * dp]);
+              const float2 vc = *reinterpret_cast<const float2*>(&vt[j + u + 2][2 * dp]);
+              const float2 vd = *reinterpret_cast<const float2*>(&vt[j + u + 3][2 * dp]);
+              o0 = fmaf(vb.x, pf[1], fmaf(va.x, pf[0], o0));
+              o1 = fmaf(vb.y, pf[1], fmaf(va.y, pf[0], o1));
+              e0 = fmaf(vd.x, pf[3], fmaf(vc.x, pf[2], e0));
+              e1 = fmaf(vd.y, pf[3], fmaf(vc.y, pf[2], e1));
+            } else {
+              const uint32_t pq = *reinterpret_cast<const uint32_t*>(&ps[h][j + u]);
+              const uint32_t pr = *reinterpret_cast<const uint32_t*>(&ps[h][j + u + 2]);
+              const uint32_t va = vt[j + u][dp], vb = vt[j + u + 1][dp];
+              const uint32_t vc = vt[j + u + 2][dp], vd = vt[j + u + 3][dp];
+              // columns 2 dp and 2 dp + 1 of tokens (j+u, j+u+1), then (j+u+2, j+u+3)
+              o0 = dot2<false>(__builtin_amdgcn_perm(vb, va, 0x05040100u), pq, o0);
+              o1 = dot2<false>(__builtin_amdgcn_perm(vb, va, 0x07060302u), pq, o1);
+              e0 = dot2<false>(__builtin_amdgcn_perm(vd, vc, 0x05040100u), pr, e0);
+              e1 = dot2<false>(__builtin_amdgcn_perm(vd, vc, 0x07060302u), pr, e1);
+            }
           }
         }
         o[it][0] = o0 + e0;
@@ -493,7 +557,7 @@ __global__ __launch_bounds__(MERGE ? 256 * merge_sections(PK) : 256) void dense_
         L = fmaf(w, lh[hf][h], L);
         acc = fmaf(w, oh[hf][h][dd], acc);
       }
-      a.out[b * a.sob + (int64_t(kvh) * NREP + h) * a.soh + dd] = __half_as_ushort(__float2half_rn(acc / L));
+      a.out[b * a.sob + (int64_t(kvh) * NREP + h) * a.soh + dd] = uint16_t(to_act<BF>(acc / L));
     }
     return;
   }
@@ -548,7 +612,7 @@ template <int DPL, int E, int CSPEC>
 __global__ __launch_bounds__(64) void flash_combine_kernel(const float* __restrict__ ml, const float* __restrict__ part,
                                                            int nsplit, int nsf, int grid, int pair_e0, int nrep,
                                                            int64_t rows, int Hq, uint16_t* __restrict__ out,
-                                                           int64_t sob, int64_t soh) {
+                                                           int64_t sob, int64_t soh, int bf) {
   using Vec = float __attribute__((ext_vector_type(DPL)));
   constexpr int D = 64 * DPL;
   __shared__ int sidx[64 * E];
@@ -620,7 +684,7 @@ __global__ __launch_bounds__(64) void flash_combine_kernel(const float* __restri
   }
   uint16_t* o = out + (bq / Hq) * sob + (bq % Hq) * soh + DPL * lane;
 #pragma unroll
-  for (int i = 0; i < DPL; ++i) o[i] = __half_as_ushort(__float2half_rn(acc[i] / L));
+  for (int i = 0; i < DPL; ++i) o[i] = uint16_t(bf ? f2bf(acc[i] / L) : __half_as_ushort(__float2half_rn(acc[i] / L)));
 }
 
 size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
@@ -633,7 +697,7 @@ Seg to_seg(const iq_segment& s, int start) {
   g.sb = s.s_b; g.sh = s.s_h; g.st = s.s_t;
   g.n = s.n; g.start = start;
   g.codes = s.codes; g.meta = s.meta; g.t_cap = s.t_cap; g.t0 = s.t0;
-  g.bits = s.bits; g.group = s.group; g.mode = s.mode;
+  g.bits = s.bits; g.group = s.group; g.mode = base_mode(s.mode);
   g.gsh = s.group > 0 ? __builtin_ctz(unsigned(s.group)) : 0;
   g.cap_groups = s.group > 0 ? s.t_cap / s.group : 0;
   if (s.n && s.codes) g.dense = nullptr;
@@ -669,6 +733,20 @@ Workspace carve(void* workspace, int B, int Hq, int T, int D) {
   return w;
 }
 
+// 1: bf16 activations (IQ_MODE_BF16 on every segment holding tokens), 0:
+// fp16 (on none), -1: mixed
+int decode_act(const iq_segment* k, const iq_segment* v) {
+  int act = -1;
+  for (int s = 0; s < 3; ++s)
+    for (const iq_segment* g : {&k[s], &v[s]}) {
+      if (!g->n) continue;
+      const int a = act_bf16(g->mode) ? 1 : 0;
+      if (act >= 0 && a != act) return -1;
+      act = a;
+    }
+  return act < 0 ? 0 : act;
+}
+
 int check_decode(const void* q, const iq_segment* k, const iq_segment* v, int B, int Hq, int Hkv, int T, int D,
                  const void* workspace, size_t workspace_bytes) {
   IQ_CHECK(q && k && v, IQ_ERR_NULL);
@@ -680,10 +758,15 @@ int check_decode(const void* q, const iq_segment* k, const iq_segment* v, int B,
     IQ_CHECK(k[s].n == 0 || k[s].dense, IQ_ERR_NULL);
     IQ_CHECK(v[s].n == 0 || v[s].dense, IQ_ERR_NULL);
   }
+  // the call's activation dtype: IQ_MODE_BF16 on every segment that holds
+  // tokens or on none (a dense segment's mode carries only that bit)
+  if (decode_act(k, v) < 0) return IQ_ERR_MODE;
+  for (int s : {0, 2})
+    IQ_CHECK((k[s].n == 0 || base_mode(k[s].mode) == 0) && (v[s].n == 0 || base_mode(v[s].mode) == 0), IQ_ERR_MODE);
   if (k[1].n) {
     const iq_segment& g = k[1];
     IQ_CHECK(g.codes && g.meta, IQ_ERR_NULL);
-    if (int e = check_common(g.bits, g.group, g.mode)) return e;
+    if (int e = check_common(g.bits, g.group, base_mode(g.mode))) return e;
     IQ_CHECK(D % g.group == 0, IQ_ERR_GROUP);
     IQ_CHECK(g.t_cap % TOKEN_BLOCK == 0 && g.t0 % TOKEN_BLOCK == 0 && g.t0 >= 0, IQ_ERR_ALIGN);
     IQ_CHECK(int64_t(g.t0) + g.n <= g.t_cap, IQ_ERR_RANGE);
@@ -692,7 +775,7 @@ int check_decode(const void* q, const iq_segment* k, const iq_segment* v, int B,
   if (v[1].n) {
     const iq_segment& g = v[1];
     IQ_CHECK(g.codes && g.meta, IQ_ERR_NULL);
-    if (int e = check_v_common(g.bits, g.group, g.mode)) return e;
+    if (int e = check_v_common(g.bits, g.group, base_mode(g.mode))) return e;
     IQ_CHECK(g.n % g.group == 0 && g.t0 % g.group == 0 && g.t0 >= 0 && g.t_cap % g.group == 0, IQ_ERR_GROUP);
     IQ_CHECK(int64_t(g.t0) + g.n <= g.t_cap, IQ_ERR_RANGE);
     IQ_CHECK(aligned(g.codes, 16) && aligned(g.meta, 8), IQ_ERR_ALIGN);
@@ -708,6 +791,7 @@ int check_decode(const void* q, const iq_segment* k, const iq_segment* v, int B,
 // combine that scans every slot).
 struct SplitPlan {
   int nsplit = 0, nsf = 0, grid = 0, nrep = 1;
+  int bf = 0;           // bf16 activations (the output's dtype)
   int pair_e0 = 0;      // the fused kernel's partition (detail::ShareMap)
   bool merged = false;  // the output is written (dense window and merge after the fused kernel)
 };
@@ -733,6 +817,8 @@ int launch_splits(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, c
                   SplitPlan* plan, bool live, hipStream_t st, const MergeOut* mo = nullptr) {
   *plan = SplitPlan{};
   plan->nrep = Hq / Hkv;
+  const bool bf = decode_act(k, v) == 1;
+  plan->bf = bf;
   const int64_t rows = int64_t(B) * Hq;
   // fused range: packed in both K and V, aligned to K blocks and V groups
   const int ks = k[0].n, vs = v[0].n;
@@ -767,6 +853,9 @@ int launch_splits(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, c
   // runs, at most one per workgroup, and the dense slices), so the context
   // length is bounded by the workspace alone.
   if (c && !(fused && live) && nsf + NSD_MAX > MAXSPLIT) return IQ_ERR_SHAPE;
+  // bf16 layers: the fused kernel (K and V of one group size) and the dense
+  // kernels; the unfused packed kernels take fp16 only
+  if (c && !fused && bf) return IQ_ERR_MODE;
   // The live slots of a row: at most one fused run per workgroup, then the
   // slices.  The fused kernel's grid (one workgroup per CU: far below the
   // limit) is worked out and checked before anything is launched.
@@ -808,8 +897,13 @@ int launch_splits(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, c
     nsd = int(std::min<int64_t>({NSD_MAX, ceil_div(n_dense, DSLICE), std::max<int64_t>(1, ceil_div(2 * detail::num_cus(), bhs))}));
     const dim3 grid{unsigned(nsd), unsigned(bhs), 1u};
     auto go = [&]<int DD, int R>() {
-      if (pk) dense_attn_kernel<DD, R, true><<<grid, 256, 0, st>>>(da);
-      else dense_attn_kernel<DD, R, false><<<grid, 256, 0, st>>>(da);
+      if (bf) {
+        if (pk) dense_attn_kernel<DD, R, true, false, true><<<grid, 256, 0, st>>>(da);
+        else dense_attn_kernel<DD, R, false, false, true><<<grid, 256, 0, st>>>(da);
+      } else {
+        if (pk) dense_attn_kernel<DD, R, true><<<grid, 256, 0, st>>>(da);
+        else dense_attn_kernel<DD, R, false><<<grid, 256, 0, st>>>(da);
+      }
     };
     auto by_r = [&]<int DD>() {
       switch (Hq / Hkv) {
@@ -841,7 +935,7 @@ int launch_splits(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, c
                                            live ? &grid : nullptr, st))
       return e;
     plan->grid = grid;
-    plan->pair_e0 = detail::fused_pair_e0(k[1].bits, v[1].bits, v[1].mode == IQ_MODE_HYBRID);
+    plan->pair_e0 = detail::fused_pair_e0(k[1].bits, v[1].bits, base_mode(v[1].mode) == IQ_MODE_HYBRID);
     bool merge_dense = merge_cand;
     if (merge_cand) {
       const detail::ShareMap sm = detail::ShareMap::make(grid, int(bhs), nsf, plan->pair_e0);
@@ -860,8 +954,13 @@ int launch_splits(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, c
       da.soh = mo->so_h;
       const dim3 mgrid{1u, unsigned(bhs), 1u};
       auto go = [&]<int DD, int R>() {
-        if (pk) dense_attn_kernel<DD, R, true, true><<<mgrid, 256 * merge_sections(true), 0, st>>>(da);
-        else dense_attn_kernel<DD, R, false, true><<<mgrid, 256 * merge_sections(false), 0, st>>>(da);
+        if (bf) {
+          if (pk) dense_attn_kernel<DD, R, true, true, true><<<mgrid, 256 * merge_sections(true, true), 0, st>>>(da);
+          else dense_attn_kernel<DD, R, false, true, true><<<mgrid, 256 * merge_sections(false, true), 0, st>>>(da);
+        } else {
+          if (pk) dense_attn_kernel<DD, R, true, true><<<mgrid, 256 * merge_sections(true), 0, st>>>(da);
+          else dense_attn_kernel<DD, R, false, true><<<mgrid, 256 * merge_sections(false), 0, st>>>(da);
+        }
       };
       auto by_r = [&]<int DD>() {
         switch (Hq / Hkv) {
@@ -914,7 +1013,7 @@ int launch_combine(const Workspace& w, const SplitPlan& plan, int B, int Hq, int
     auto* kern = nlive > 8 ? flash_combine_kernel<DPL, E, 32> : flash_combine_kernel<DPL, E, 8>;
     kern<<<dim3(unsigned(rows)), 64, 0, st>>>(w.ml, w.part, nsplit, plan.nsf, plan.grid,
                                                                       plan.pair_e0, plan.nrep, rows, Hq,
-                                                                      (uint16_t*)out, so_b, so_h);
+                                                                      (uint16_t*)out, so_b, so_h, plan.bf);
   };
   auto by_e = [&]<int DPL>() {
     if (nlive <= 64) go.template operator()<DPL, 1>();
@@ -1003,6 +1102,7 @@ int iq_decode_attention_splits(const void* q, int64_t sq_b, int64_t sq_h, const 
   IQ_CHECK(nsplit, IQ_ERR_NULL);
   if (int e = check_decode(q, k, v, B, Hq, Hkv, T, D, workspace, workspace_bytes)) return e;
   IQ_CHECK(nsplit_max(T) + NSD_MAX <= MAXSPLIT, IQ_ERR_SHAPE);  // its combine reads every slot
+  IQ_CHECK(decode_act(k, v) == 0, IQ_ERR_MODE);  // its combine writes fp16 (bf16: the live stages)
   *nsplit = 0;
   if (B == 0) return IQ_OK;
   SplitPlan plan;
@@ -1031,6 +1131,7 @@ int iq_decode_attention_splits_live(const void* q, int64_t sq_b, int64_t sq_h, c
   plan->grid = sp.grid;
   plan->nrep = sp.nrep;
   plan->pair_e0 = sp.pair_e0;
+  plan->bf16 = sp.bf;
   return e;
 }
 
@@ -1056,6 +1157,7 @@ int iq_decode_attention_combine_live(const iq_split_plan* plan, int B, int Hq, i
   sp.grid = p.grid;
   sp.nrep = p.nrep;
   sp.pair_e0 = p.pair_e0;
+  sp.bf = p.bf16 != 0;
   return launch_combine(carve(workspace, B, Hq, T, D), sp, B, Hq, D, out, so_b, so_h, (hipStream_t)stream);
 }
 

@@ -179,20 +179,21 @@ __device__ __forceinline__ uint16_t bload_u16(rsrc_t r, uint32_t voff, uint32_t 
 // one select.
 __device__ __forceinline__ uint32_t meta_voff(int lane, int sym) { return sym ? uint32_t(lane & ~1) * 2 : uint32_t(lane) * 4; }
 __device__ __forceinline__ uint32_t meta_shift(int lane, int sym) { return sym ? uint32_t(lane & 1) * 16 : 0u; }
-template <int BITS>
+// (BF: the meta halves hold bf16 values, a bf16 layer's store)
+template <int BITS, bool BF = false>
 __device__ __forceinline__ void meta_sz(uint32_t mw, uint32_t sh, int sym, float& s, float& z) {
-  s = h2f(uint16_t(mw >> sh));
-  const float zh = h2f(uint16_t(mw >> 16));
+  s = act2f(uint16_t(mw >> sh), BF);
+  const float zh = act2f(uint16_t(mw >> 16), BF);
   z = sym ? -float(1 << (BITS - 1)) * s : zh;  // offset-binary sym codes: signed = u - 2^(b-1)
 }
 
 // {scale, zero} of a hybrid V group-column from its meta dword: the flag bit
 // (bit 15, tested as a bit) marks b-bit sym codes (offset binary, zero
 // -2^(b-1) |scale|), else (b-1)-bit asym codes with the stored zero.
-template <int BITS>
+template <int BITS, bool BF = false>
 __device__ __forceinline__ void meta_sz_hyb(uint32_t mw, float& s, float& z) {
-  s = hyb_scale(mw);
-  const float zh = h2f(uint16_t(mw >> 16));
+  s = hyb_scale(mw, BF);
+  const float zh = act2f(uint16_t(mw >> 16), BF);
   z = hyb_sym(mw) ? -float(1 << (BITS - 1)) * s : zh;
 }
 
@@ -223,7 +224,12 @@ __device__ __forceinline__ float seg_sum(float v) {
 // the fp32 output at part (element strides sob, soh per batch and query head,
 // 1 per token).
 // VH: the V store is hybrid (per-group flag in its meta, meta_sz_hyb).
-template <int KB, int VB, int G, int D, int NREP, bool QS, bool AVO = false, bool QKO = false, bool VH = false>
+// BF: a bf16 layer (query, key normalization factor, scales and zero points
+// in bf16): the query (times the factor, exact in fp32) goes into the hi/lo
+// fp16 query rows (QS) and the metadata decodes as bf16; the probabilities
+// meet V as fp16, finer than the reference's bf16 cast of the softmax.
+template <int KB, int VB, int G, int D, int NREP, bool QS, bool AVO = false, bool QKO = false, bool VH = false,
+          bool BF = false>
 __global__ __launch_bounds__((FusedShape<G, NREP, QS, AVO>::NT), (fused_waves_per_simd<G, NREP, QS, AVO>())) void flash_fused_kernel(FusedArgs a) {
   using FS = FusedShape<G, NREP, QS, AVO>;
   constexpr int NW = FS::NW, NT = FS::NT, WTOK = FS::WTOK, FBPW = FS::FBPW, VPW = FS::VPW;
@@ -324,7 +330,8 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS, AVO>::NT), (fused_waves_pe
       const int k = i % NP, h = (i / NP) % NREP, g = i / (NP * NREP);
       uint32_t hi = 0, lo = 0;
       float s = 0.f;
-      qrec_pair_vals(qq.a[r], qq.c[r], qq.na[r], qq.nc[r], qsplit, &hi, &lo, s);
+      if constexpr (BF) qrec_pair_vals_bf(qq.a[r], qq.c[r], qq.na[r], qq.nc[r], a.norm != nullptr, &hi, &lo, s);
+      else qrec_pair_vals(qq.a[r], qq.c[r], qq.na[r], qq.nc[r], qsplit, &hi, &lo, s);
       // -sum(x * bias) of the hi and lo rows (exact products: the biases are powers of two)
       const float ba = bias_a<KB>(k % Plan<KB>::NPAIR), bc = bias_c<KB>(k % Plan<KB>::NPAIR);
       float bh = -(h2f(uint16_t(hi & 0xffffu)) * ba + h2f(uint16_t(hi >> 16)) * bc);
@@ -506,7 +513,7 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS, AVO>::NT), (fused_waves_pe
 #pragma unroll
           for (int j = 0; j < FBPW; ++j) {
             float s, z;
-            meta_sz<KB>(kc.m[g][j], ksh, a.ksym, s, z);
+            meta_sz<KB, BF>(kc.m[g][j], ksh, a.ksym, s, z);
 #pragma unroll
             for (int h = 0; h < NREP; ++h) {
               const float qs = __uint_as_float(sm.qrec[g][QOS + h]);
@@ -632,8 +639,8 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS, AVO>::NT), (fused_waves_pe
 #pragma unroll
           for (int e = 0; e < DPL; ++e) {
             float s, z;
-            if constexpr (VH) meta_sz_hyb<VB>(v.m[u][e], s, z);
-            else meta_sz<VB>(v.m[u][e], vsh, a.vsym, s, z);
+            if constexpr (VH) meta_sz_hyb<VB, BF>(v.m[u][e], s, z);
+            else meta_sz<VB, BF>(v.m[u][e], vsh, a.vsym, s, z);
 #pragma unroll
             for (int h = 0; h < NREP; ++h)  // codes = biased codes - bias
               o_run[h][e] = fmaf(s, dv[e][h / 4][h % 4] - pbs[h], fmaf(z, ps[h], o_run[h][e]));
@@ -698,18 +705,21 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS, AVO>::NT), (fused_waves_pe
 }
 
 // Launch of the fused kernel for K bit width KB (the arguments filled by
-// flash_fused_launch): persistent grid, one workgroup per CU.  VH: hybrid V.
+// flash_fused_launch): persistent grid, one workgroup per CU.  VH: hybrid V;
+// BF: a bf16 layer (hi/lo query rows whether or not keys are normalized).
 // launch = false: only the grid is computed.
-template <int KB, bool VH = false>
+template <int KB, bool VH = false, bool BF = false>
 int fused_launch_kb(const FusedArgs& a, int vbits, int group, int D, int nrep, bool norm, int* grid_out,
                     hipStream_t stream, bool launch) {
   return dispatch_shape(vbits, group, D, nrep, 0, [&]<int VB, int G, int DD, int R, bool S>() {
-    auto* kern = norm ? flash_fused_kernel<KB, VB, G, DD, R, true, false, false, VH>
-                      : flash_fused_kernel<KB, VB, G, DD, R, false, false, false, VH>;
-    const int nt = norm ? FusedShape<G, R, true>::NT : FusedShape<G, R, false>::NT;
+    auto* kern = BF     ? flash_fused_kernel<KB, VB, G, DD, R, true, false, false, VH, true>
+                 : norm ? flash_fused_kernel<KB, VB, G, DD, R, true, false, false, VH>
+                        : flash_fused_kernel<KB, VB, G, DD, R, false, false, false, VH>;
+    const bool qs = BF || norm;
+    const int nt = qs ? FusedShape<G, R, true>::NT : FusedShape<G, R, false>::NT;
     // as many workgroups as fit at once on the device
     static detail::OccCache occ[2];
-    const int pc = detail::blocks_per_cu(kern, nt, occ[norm ? 1 : 0]);
+    const int pc = detail::blocks_per_cu(kern, nt, occ[qs ? 1 : 0]);
     const int grid = int(std::min<int64_t>(a.nitems, int64_t(pc) * detail::num_cus()));
     if (grid_out) *grid_out = grid;
     if (!launch) return int(IQ_OK);

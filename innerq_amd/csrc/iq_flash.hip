@@ -29,15 +29,19 @@ int flash_fused_launch(const void* q, int64_t sq_b, int64_t sq_h, const void* no
                        float* part, int* grid, hipStream_t stream, bool launch) {
   if (B == 0 || T == 0) return IQ_OK;
   if (k.group != v.group) return IQ_ERR_GROUP;
+  // a bf16 layer: IQ_MODE_BF16 on both stores (the query, factor and metadata in bf16)
+  const bool bf = act_bf16(k.mode);
+  if (bf != act_bf16(v.mode)) return IQ_ERR_MODE;
+  const int kmode = base_mode(k.mode), vmode = base_mode(v.mode);
   if (T % k.group || FSPLIT != flash_split_tokens()) return IQ_ERR_GROUP;
   if (k.t0 % TOKEN_BLOCK || v.t0 % v.group) return IQ_ERR_ALIGN;
   if (!flash_fused_supported(q, sq_b, sq_h, norm, k, v, Hq, Hkv, D)) return IQ_ERR_SHAPE;
   FusedArgs a{};
   a.q = (const uint16_t*)q; a.sqb = sq_b; a.sqh = sq_h; a.norm = (const uint16_t*)norm;
   a.kc = k.codes; a.km = k.meta; a.k_cap_blocks = k.t_cap / TOKEN_BLOCK; a.kblk0 = k.t0 / TOKEN_BLOCK;
-  a.ksym = k.mode == IQ_MODE_SYM;
+  a.ksym = kmode == IQ_MODE_SYM;
   a.vc = v.codes; a.vm = v.meta; a.v_cap_groups = v.t_cap / v.group; a.vg0 = v.t0 / v.group;
-  a.vsym = v.mode == IQ_MODE_SYM;
+  a.vsym = vmode == IQ_MODE_SYM;
   a.Hkv = Hkv; a.T = T;
   a.nsplit = int(ceil_div(T, FSPLIT));
   a.nitems = a.nsplit * B * Hkv;
@@ -51,9 +55,22 @@ int flash_fused_launch(const void* q, int64_t sq_b, int64_t sq_h, const void* no
   a.scale_log2 = scale * 1.4426950408889634f;
   a.ml = ml; a.part = part;
   a.empty_stats = grid ? 0 : 1;  // a caller that takes the workgroup count reads only the run slots
-  a.pair_e0 = fused_pair_e0(k.bits, v.bits, v.mode == IQ_MODE_HYBRID);
-  if (k.mode == IQ_MODE_HYBRID) return IQ_ERR_MODE;
-  if (v.mode == IQ_MODE_HYBRID) {
+  a.pair_e0 = fused_pair_e0(k.bits, v.bits, vmode == IQ_MODE_HYBRID);
+  if (kmode == IQ_MODE_HYBRID) return IQ_ERR_MODE;
+  const bool nm = norm != nullptr;
+  if (bf) {
+    const bool vh = vmode == IQ_MODE_HYBRID;
+    switch (k.bits) {
+      case 2: return vh ? flash_fused_launch_bf_vh_k2(a, v.bits, k.group, D, Hq / Hkv, nm, grid, stream, launch)
+                        : flash_fused_launch_bf_k2(a, v.bits, k.group, D, Hq / Hkv, nm, grid, stream, launch);
+      case 3: return vh ? flash_fused_launch_bf_vh_k3(a, v.bits, k.group, D, Hq / Hkv, nm, grid, stream, launch)
+                        : flash_fused_launch_bf_k3(a, v.bits, k.group, D, Hq / Hkv, nm, grid, stream, launch);
+      case 4: return vh ? flash_fused_launch_bf_vh_k4(a, v.bits, k.group, D, Hq / Hkv, nm, grid, stream, launch)
+                        : flash_fused_launch_bf_k4(a, v.bits, k.group, D, Hq / Hkv, nm, grid, stream, launch);
+      default: return IQ_ERR_BITS;
+    }
+  }
+  if (vmode == IQ_MODE_HYBRID) {
     switch (k.bits) {
       case 2: return flash_fused_launch_vh_k2(a, v.bits, k.group, D, Hq / Hkv, norm != nullptr, grid, stream, launch);
       case 3: return flash_fused_launch_vh_k3(a, v.bits, k.group, D, Hq / Hkv, norm != nullptr, grid, stream, launch);

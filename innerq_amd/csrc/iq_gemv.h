@@ -263,6 +263,17 @@ __device__ __forceinline__ void qrec_pair_vals(uint16_t ua, uint16_t uc, uint16_
         (uint32_t(__half_as_ushort(__float2half_rn(qc - h2f(hc)))) << 16);
   sum += qa + qc;
 }
+// the same for bf16 query (and factor) values: q * n is exact in fp32 (8-bit
+// significands), and its hi/lo fp16 parts hold it to 2^-22 (no factor: n = 1)
+__device__ __forceinline__ void qrec_pair_vals_bf(uint16_t ua, uint16_t uc, uint16_t na, uint16_t nc, bool norm,
+                                                  uint32_t* hi, uint32_t* lo, float& sum) {
+  const float qa = bf2f(ua) * (norm ? bf2f(na) : 1.f), qc = bf2f(uc) * (norm ? bf2f(nc) : 1.f);
+  const uint16_t ha = __half_as_ushort(__float2half_rn(qa)), hc = __half_as_ushort(__float2half_rn(qc));
+  *hi = uint32_t(ha) | (uint32_t(hc) << 16);
+  *lo = uint32_t(__half_as_ushort(__float2half_rn(qa - h2f(ha)))) |
+        (uint32_t(__half_as_ushort(__float2half_rn(qc - h2f(hc)))) << 16);
+  sum += qa + qc;
+}
 __device__ __forceinline__ void qrec_pair(const uint16_t* qrow, const uint16_t* nrow, int ia, int ic, uint32_t* hi,
                                           uint32_t* lo, float& sum) {
   qrec_pair_vals(qrow[ia], qrow[ic], nrow ? nrow[ia] : uint16_t(0), nrow ? nrow[ic] : uint16_t(0), nrow != nullptr,
@@ -553,6 +564,19 @@ int flash_fused_launch_k3(const FusedArgs& a, int vbits, int group, int D, int n
                           hipStream_t stream, bool launch);
 int flash_fused_launch_k4(const FusedArgs& a, int vbits, int group, int D, int nrep, bool norm, int* grid,
                           hipStream_t stream, bool launch);
+// for a bf16 layer (iq_flash_bf_k{2,3,4}.hip, iq_flash_bf_vh_k{2,3,4}.hip: hybrid V)
+int flash_fused_launch_bf_k2(const FusedArgs& a, int vbits, int group, int D, int nrep, bool norm, int* grid,
+                             hipStream_t stream, bool launch);
+int flash_fused_launch_bf_k3(const FusedArgs& a, int vbits, int group, int D, int nrep, bool norm, int* grid,
+                             hipStream_t stream, bool launch);
+int flash_fused_launch_bf_k4(const FusedArgs& a, int vbits, int group, int D, int nrep, bool norm, int* grid,
+                             hipStream_t stream, bool launch);
+int flash_fused_launch_bf_vh_k2(const FusedArgs& a, int vbits, int group, int D, int nrep, bool norm, int* grid,
+                                hipStream_t stream, bool launch);
+int flash_fused_launch_bf_vh_k3(const FusedArgs& a, int vbits, int group, int D, int nrep, bool norm, int* grid,
+                                hipStream_t stream, bool launch);
+int flash_fused_launch_bf_vh_k4(const FusedArgs& a, int vbits, int group, int D, int nrep, bool norm, int* grid,
+                                hipStream_t stream, bool launch);
 // and for a hybrid V store (iq_flash_vh_k{2,3,4}.hip)
 int flash_fused_launch_vh_k2(const FusedArgs& a, int vbits, int group, int D, int nrep, bool norm, int* grid,
                              hipStream_t stream, bool launch);

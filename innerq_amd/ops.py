@@ -607,16 +607,20 @@ def av_gemv(p: torch.Tensor, v: PackedStore, t0: int = 0, T: Optional[int] = Non
     return out if out is not None else out32
 
 
-def _segment(dense: Optional[torch.Tensor], store: Optional[PackedStore], n: int, t0: int = 0):
+def _segment(dense: Optional[torch.Tensor], store: Optional[PackedStore], n: int, t0: int = 0,
+             dtype=torch.float16):
+    """A decode segment (dtype: the call's activation dtype; a store's mode and a
+    dense segment's mode carry its bf16 bit)."""
     s = _lib.iq_segment()
     s.n = n
     if n == 0:
         return s
     if store is not None:
         s.codes, s.meta, s.t_cap, s.t0 = store.codes.data_ptr(), store.meta.data_ptr(), store.t_cap, t0
-        s.bits, s.group, s.mode = store.bits, store.group, store.mode
+        s.bits, s.group, s.mode = store.bits, store.group, store.mode_arg
     else:
-        require_device(dense, "segment")
+        require_device(dense, "segment", dtype)
+        s.mode = act_flag(dtype)
         if dense.stride(-1) != 1:
             _shape_error("a dense K/V segment must have a contiguous head_dim")
         s.dense = dense.data_ptr()
@@ -625,9 +629,13 @@ def _segment(dense: Optional[torch.Tensor], store: Optional[PackedStore], n: int
 
 
 def _decode_args(q, k_sink, k_store, k_recent, v_sink, v_store, v_recent, norm, out=None):
-    require_f16_store(k_store, "decode attention K")
-    require_f16_store(v_store, "decode attention V")
-    require_device(q, "q")
+    """Checks and C-ABI segments of a decode call; the activation dtype (fp16 or
+    bf16) is the query's, and every store, dense segment, factor and output has it."""
+    require_act(q, "q")
+    act = q.dtype
+    for role, st in (("K", k_store), ("V", v_store)):
+        if st is not None and st.dtype != act:
+            raise TypeError(f"decode attention {role}: a {st.dtype} store with a {act} query")
 
     def shp(t):
         return None if t is None else tuple(t.shape)
@@ -636,7 +644,7 @@ def _decode_args(q, k_sink, k_store, k_recent, v_sink, v_store, v_recent, norm, 
                                            shp(v_recent), None if norm is None else norm.numel(),
                                            None if out is None else tuple(out.shape))
     if out is not None:
-        require_device(out, "out")
+        require_device(out, "out", act)
         if out.stride(-1) != 1:
             _shape_error("decode output must have a contiguous head_dim")
     if q.stride(-1) != 1:
@@ -647,11 +655,12 @@ def _decode_args(q, k_sink, k_store, k_recent, v_sink, v_store, v_recent, norm, 
 
     kn = [n_of(k_sink), k_store.length if k_store is not None else 0, n_of(k_recent)]
     vn = [n_of(v_sink), v_store.length if v_store is not None else 0, n_of(v_recent)]
-    ks = (_lib.iq_segment * 3)(_segment(k_sink, None, kn[0]), _segment(None, k_store, kn[1]),
-                               _segment(k_recent, None, kn[2]))
-    vs = (_lib.iq_segment * 3)(_segment(v_sink, None, vn[0]), _segment(None, v_store, vn[1]),
-                               _segment(v_recent, None, vn[2]))
+    ks = (_lib.iq_segment * 3)(_segment(k_sink, None, kn[0], dtype=act), _segment(None, k_store, kn[1]),
+                               _segment(k_recent, None, kn[2], dtype=act))
+    vs = (_lib.iq_segment * 3)(_segment(v_sink, None, vn[0], dtype=act), _segment(None, v_store, vn[1]),
+                               _segment(v_recent, None, vn[2], dtype=act))
     if norm is not None:
+        require_device(norm, "norm", act)
         norm = norm.reshape(B, Hkv, D).contiguous()
     ws = _workspace(q.device, _lib.lib().iq_decode_workspace_bytes(B, Hq, T, D))
     return q, B, Hq, Hkv, T, D, ks, vs, norm, ws
@@ -661,11 +670,12 @@ def decode_attention(q: torch.Tensor, k_sink: Optional[torch.Tensor], k_store: O
                      k_recent: Optional[torch.Tensor], v_sink: Optional[torch.Tensor],
                      v_store: Optional[PackedStore], v_recent: Optional[torch.Tensor], scale: float,
                      norm: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """One decode step of attention for q [B,Hq,D] over [sink | packed | recent] K and V."""
+    """One decode step of attention for q [B,Hq,D] over [sink | packed | recent] K and V
+    (fp16 or bf16: the query's dtype, which every segment and the output share)."""
     q, B, Hq, Hkv, T, D, ks, vs, norm, ws = _decode_args(q, k_sink, k_store, k_recent, v_sink, v_store, v_recent,
                                                          norm, out)
     if out is None:
-        out = torch.empty(B, Hq, D, dtype=torch.float16, device=q.device)
+        out = torch.empty(B, Hq, D, dtype=q.dtype, device=q.device)
     call("iq_decode_attention", _p(q), q.stride(0), q.stride(1), _p(norm), ks, vs, B, Hq, Hkv, T, D, float(scale),
          _p(out), out.stride(0), out.stride(1), _p(ws), ws.numel(), _stream(q.device))
     return out
@@ -712,9 +722,10 @@ def decode_attention_combine_live(plan, B: int, Hq: int, T: int, D: int, device,
                                   out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """The combine of a decode_attention_splits_live stage (the same workspace)."""
     device = torch.device(device)
+    dtype = torch.bfloat16 if plan.bf16 else torch.float16
     if out is None:
-        out = torch.empty(B, Hq, D, dtype=torch.float16, device=device)
-    require_device(out, "out")
+        out = torch.empty(B, Hq, D, dtype=dtype, device=device)
+    require_device(out, "out", dtype)
     check_out(out.shape, (B, Hq, D))
     ws = _workspace(device, _lib.lib().iq_decode_workspace_bytes(B, Hq, T, D))
     call("iq_decode_attention_combine_live", ctypes.byref(plan), B, Hq, T, D, _p(out), out.stride(0), out.stride(1),

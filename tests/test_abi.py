@@ -240,6 +240,28 @@ def test_decode_live_stages_reject():
     assert combine(_lib.iq_split_plan(**ok), D=96) == -4
 
 
+def test_decode_activation_dtype_must_agree():
+    """The activation dtype of a decode call is the IQ_MODE_BF16 bit of its
+    segments' modes: segments holding tokens that disagree, or a dense segment
+    whose mode carries any other bit, are refused before any launch."""
+    lib = _lib.lib()
+    BF = _lib.IQ_MODE_BF16
+    k = (_lib.iq_segment * 3)()
+    v = (_lib.iq_segment * 3)()
+    for seg in (k, v):
+        seg[2].n, seg[2].dense, seg[2].s_b, seg[2].s_h, seg[2].s_t = 64, FAKE, 64 * 128, 64 * 128, 128
+    k[2].mode = BF  # bf16 keys, fp16 values
+    assert lib.iq_decode_attention(FAKE, 4096, 128, None, k, v, 1, 32, 8, 64, 128, 1.0, FAKE, 4096, 128, FAKE,
+                                   1 << 30, None) == -7
+    k[2].mode, v[2].mode = 1, 1  # a dense segment with a store mode
+    assert lib.iq_decode_attention(FAKE, 4096, 128, None, k, v, 1, 32, 8, 64, 128, 1.0, FAKE, 4096, 128, FAKE,
+                                   1 << 30, None) == -7
+    k[2].mode, v[2].mode = BF, BF  # bf16 throughout: the split stage alone refuses it (fp16 combine)
+    ns = ctypes.c_int(-7)
+    assert lib.iq_decode_attention_splits(FAKE, 4096, 128, None, k, v, 1, 32, 8, 64, 128, 1.0, FAKE, 1 << 30,
+                                          ctypes.byref(ns), None) == -7
+
+
 def test_decode_slot_limit_where_every_slot_is_read():
     """Past 1020 splits of 256 tokens (261,120 tokens), a combine that reads every
     split slot cannot hold them: the split stage alone and the unfused kernels (K

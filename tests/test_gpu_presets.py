@@ -95,3 +95,41 @@ def test_preset_decode_full_size(name):
         e = A.rel_err(_np(got[b:b + 1, h * nrep:(h + 1) * nrep]).astype(np.float64), o)
         print(f"  head ({b}, {h}) vs the oracle: {e:.2e}", flush=True)
         assert e < TOL
+
+
+@pytest.mark.parametrize("name", ["innerq_base", "innerq_hybrid"])
+def test_preset_decode_full_size_bf16(name):
+    """The same decode step of a bf16 layer (the model in bf16, LongBench/pred.py:240):
+    every head against fp32 attention over the layer's fp32 dequantized K and V
+    (the bf16 read path is pinned to the reference's by tests/test_gpu_bf16.py);
+    the output is the bf16 rounding of the fp32 result, so the bar is 1e-3
+    max-normwise beyond that rounding (2^-8 |ref| elementwise)."""
+    B, Hkv, nrep, T, D, steps = 8, 8, 4, 32768, 128, 3
+    print(f"preset {name} bf16: B={B} Hkv={Hkv} T={T}", flush=True)
+    cfg = presets.preset_config(name)
+    gen = torch.Generator(device=DEV).manual_seed(7 + sum(map(ord, name)))
+
+    def kv(n):
+        x = torch.randn(B, Hkv, n, D, generator=gen, device=DEV)
+        x[..., :: D // 4] *= 8.0
+        return x.to(torch.bfloat16)
+
+    k, v = kv(T + steps), kv(T + steps)
+    q = torch.randn(B, Hkv * nrep, 1, D, generator=gen, device=DEV).to(torch.bfloat16)
+    layer = C.InnerqDynamicLayer(cfg, 0)
+    layer.update(k[:, :, :T], v[:, :, :T])
+    for i in range(steps):
+        layer.append(k[:, :, T + i:T + i + 1], v[:, :, T + i:T + i + 1])
+    got = layer.attend(q, D ** -0.5)[:, :, 0]
+    assert got.dtype == torch.bfloat16
+    K = layer.get_keys_deq()
+    lg = torch.matmul(q[:, :, 0].float().view(B, Hkv, nrep, D), K.transpose(-1, -2).contiguous()) * D ** -0.5
+    del K
+    pr = torch.softmax(lg, dim=-1)
+    del lg
+    ref = torch.matmul(pr, layer.get_values_deq()).view(B, Hkv * nrep, D)
+    g, r = got.double(), ref.double()
+    excess = ((g - r).abs() - 2.0 ** -8 * r.abs()).max().item() / r.abs().max().item()
+    print(f"  max-normwise {((g - r).abs().max() / r.abs().max()).item():.2e}, beyond the bf16 rounding "
+          f"{excess:.2e}", flush=True)
+    assert excess <= TOL
