@@ -241,7 +241,8 @@ typedef struct iq_segment {
   const uint32_t* codes;      /* packed store (quantized segment) or NULL */
   const uint16_t* meta;
   int64_t t_cap;
-  int t0;
+  int t0;                     /* first store token of the segment (any: a sliding
+                                 window starts anywhere in the store) */
   int bits, group, mode;      /* mode: the store's; of a dense segment only the
                                  IQ_MODE_BF16 bit (its rows are bf16) */
 } iq_segment;

@@ -353,9 +353,9 @@ class InnerqDynamicLayer(CacheLayerMixin):
 
     def fused_decode_ready(self, key_states: torch.Tensor) -> bool:
         """Whether attend() can serve this step: one new token per sequence, a
-        prefilled full-attention layer, K grouped along head_dim (asym or sym) and
-        V along tokens (asym, sym or hybrid)."""
-        if self.is_sliding or not self.is_initialized or key_states.shape[-2] != 1:
+        prefilled layer, K grouped along head_dim (asym or sym) and V along tokens
+        (asym, sym or hybrid)."""
+        if not self.is_initialized or key_states.shape[-2] != 1:
             return False
         return self._fused_refusal() is None
 
@@ -371,14 +371,25 @@ class InnerqDynamicLayer(CacheLayerMixin):
         why = self._fused_refusal()
         if why is not None:
             raise NotImplementedError(why)
-        q = query_states[:, :, 0]
-        out = ops.decode_attention(
-            q, self.keys_sink if self.keys_sink.shape[-2] else None, self._kq.store if self._kq else None,
-            self.keys_recent if self.keys_recent.shape[-2] else None,
-            self.values_sink if self.values_sink.shape[-2] else None, self._vq.store if self._vq else None,
-            self.values_recent if self.values_recent.shape[-2] else None, scaling,
-            norm=self.key_normalization_factor if self._kq is not None else None)
-        return out[:, :, None]
+        return self._attend_from(query_states[:, :, 0], scaling, 0)[:, :, None]
+
+    def _attend_from(self, q: torch.Tensor, scaling: float, s0: int) -> torch.Tensor:
+        """decode_attention over this layer's tokens [s0, cumulative_length): the
+        parts of [sink | packed | recent] of K and of V from token s0 on."""
+        def parts(sink, quant, recent):
+            ns = sink.shape[-2]
+            nq = quant.length if quant is not None else 0
+            dense_sink = sink[:, :, s0:] if s0 < ns else None
+            t0 = min(max(s0 - ns, 0), nq)
+            r0 = max(s0 - ns - nq, 0)
+            dense_recent = recent[:, :, r0:] if recent.shape[-2] > r0 else None
+            return dense_sink, (quant.store if quant is not None else None), t0, dense_recent
+
+        ks, kst, kt0, kr = parts(self.keys_sink, self._kq, self.keys_recent)
+        vs, vst, vt0, vr = parts(self.values_sink, self._vq, self.values_recent)
+        return ops.decode_attention(q, ks, kst, kr, vs, vst, vr, scaling,
+                                    norm=self.key_normalization_factor if self._kq is not None else None,
+                                    k_t0=kt0, v_t0=vt0)
 
     def get_mask_sizes(self, query_length) -> tuple[int, int]:
         """(kv_length, kv_offset); takes the query length (transformers >= 5.15) or
@@ -444,6 +455,31 @@ class InnerqDynamicSlidingWindowLayer(InnerqDynamicLayer):
             full_key_states = full_key_states[:, :, -(w - 1 + q):]
             full_value_states = full_value_states[:, :, -(w - 1 + q):]
         return full_key_states, full_value_states
+
+    def fused_decode_ready(self, key_states: torch.Tensor) -> bool:
+        """With fix_sliding_window on, a one-token step attends to the last min(T, w)
+        tokens, which attend() reads packed; without it the reference's update()
+        (one token once the past exceeds the window) stays on the dense path."""
+        if not self.fix_sliding_window or not self.is_initialized or key_states.shape[-2] != 1:
+            return False
+        return self._fused_refusal() is None
+
+    def attend(self, query_states: torch.Tensor, scaling: float) -> torch.Tensor:
+        """Decode attention over the last min(T, w) tokens of the layer (T the tokens
+        so far, this step's included): the window update() returns with
+        fix_sliding_window on (w - 1 + q tokens of a q = 1 call once the past
+        reaches w), read packed."""
+        if not self.fix_sliding_window:
+            raise NotImplementedError("attend() of a sliding-window layer needs fix_sliding_window = True")
+        if query_states.dim() != 4 or query_states.shape[2] != 1:
+            raise ValueError("attend() takes one query token per sequence: [B, Hq, 1, D]")
+        if not self.is_initialized:
+            raise RuntimeError("attend() needs a prefilled cache")
+        why = self._fused_refusal()
+        if why is not None:
+            raise NotImplementedError(why)
+        s0 = max(self.cumulative_length - self.sliding_window, 0)
+        return self._attend_from(query_states[:, :, 0], scaling, s0)[:, :, None]
 
     def get_mask_sizes(self, query_length) -> tuple[int, int]:
         if isinstance(query_length, torch.Tensor):

@@ -768,7 +768,10 @@ int check_decode(const void* q, const iq_segment* k, const iq_segment* v, int B,
     IQ_CHECK(g.codes && g.meta, IQ_ERR_NULL);
     if (int e = check_common(g.bits, g.group, base_mode(g.mode))) return e;
     IQ_CHECK(D % g.group == 0, IQ_ERR_GROUP);
-    IQ_CHECK(g.t_cap % TOKEN_BLOCK == 0 && g.t0 % TOKEN_BLOCK == 0 && g.t0 >= 0, IQ_ERR_ALIGN);
+    // any store token may start the segment (a sliding window's start): the
+    // fused range begins at the first token where K blocks and V groups align,
+    // the tokens before it are decoded by the dense kernel
+    IQ_CHECK(g.t_cap % TOKEN_BLOCK == 0 && g.t0 >= 0, IQ_ERR_ALIGN);
     IQ_CHECK(int64_t(g.t0) + g.n <= g.t_cap, IQ_ERR_RANGE);
     IQ_CHECK(aligned(g.codes, 16) && aligned(g.meta, 4), IQ_ERR_ALIGN);
   }
@@ -776,7 +779,7 @@ int check_decode(const void* q, const iq_segment* k, const iq_segment* v, int B,
     const iq_segment& g = v[1];
     IQ_CHECK(g.codes && g.meta, IQ_ERR_NULL);
     if (int e = check_v_common(g.bits, g.group, base_mode(g.mode))) return e;
-    IQ_CHECK(g.n % g.group == 0 && g.t0 % g.group == 0 && g.t0 >= 0 && g.t_cap % g.group == 0, IQ_ERR_GROUP);
+    IQ_CHECK(g.t0 >= 0 && g.t_cap % g.group == 0, IQ_ERR_GROUP);
     IQ_CHECK(int64_t(g.t0) + g.n <= g.t_cap, IQ_ERR_RANGE);
     IQ_CHECK(aligned(g.codes, 16) && aligned(g.meta, 8), IQ_ERR_ALIGN);
   }

@@ -128,10 +128,11 @@ def check_av_shapes(p_shape, store, t0: int, T: int, out_shapes=()) -> None:
 
 
 def check_decode_shapes(q_shape, k_sink, k_store, k_recent, v_sink, v_store, v_recent, norm_numel=None,
-                        out_shape=None) -> tuple:
+                        out_shape=None, k_t0: int = 0, v_t0: int = 0) -> tuple:
     """Shapes of a decode-attention call (host only).  Dense segments are shapes
     [B,Hkv,n,D] or None; stores are PackedStores (or anything with their
-    attributes) or None.  Returns (B, Hq, Hkv, T, D)."""
+    attributes) or None, read from store token k_t0 / v_t0 on.  Returns
+    (B, Hq, Hkv, T, D)."""
     if len(q_shape) != 3:
         _shape_error(f"q must be [B, Hq, D], got {tuple(q_shape)}")
     B, Hq, D = q_shape
@@ -159,8 +160,12 @@ def check_decode_shapes(q_shape, k_sink, k_store, k_recent, v_sink, v_store, v_r
 
     def n_of(seg):
         return 0 if seg is None else seg[2]
-    T = n_of(k_sink) + (k_store.length if k_store is not None else 0) + n_of(k_recent)
-    Tv = n_of(v_sink) + (v_store.length if v_store is not None else 0) + n_of(v_recent)
+
+    for role, st, t0 in (("K", k_store, k_t0), ("V", v_store, v_t0)):
+        if t0 < 0 or (st is None and t0) or (st is not None and t0 > st.length):
+            _shape_error(f"{role} store offset {t0} outside the store")
+    T = n_of(k_sink) + (k_store.length - k_t0 if k_store is not None else 0) + n_of(k_recent)
+    Tv = n_of(v_sink) + (v_store.length - v_t0 if v_store is not None else 0) + n_of(v_recent)
     if T != Tv:
         _shape_error(f"K has {T} tokens but V has {Tv}")
     if out_shape is not None:
@@ -628,7 +633,7 @@ def _segment(dense: Optional[torch.Tensor], store: Optional[PackedStore], n: int
     return s
 
 
-def _decode_args(q, k_sink, k_store, k_recent, v_sink, v_store, v_recent, norm, out=None):
+def _decode_args(q, k_sink, k_store, k_recent, v_sink, v_store, v_recent, norm, out=None, k_t0=0, v_t0=0):
     """Checks and C-ABI segments of a decode call; the activation dtype (fp16 or
     bf16) is the query's, and every store, dense segment, factor and output has it."""
     require_act(q, "q")
@@ -642,7 +647,7 @@ def _decode_args(q, k_sink, k_store, k_recent, v_sink, v_store, v_recent, norm, 
 
     B, Hq, Hkv, T, D = check_decode_shapes(shp(q), shp(k_sink), k_store, shp(k_recent), shp(v_sink), v_store,
                                            shp(v_recent), None if norm is None else norm.numel(),
-                                           None if out is None else tuple(out.shape))
+                                           None if out is None else tuple(out.shape), k_t0, v_t0)
     if out is not None:
         require_device(out, "out", act)
         if out.stride(-1) != 1:
@@ -653,11 +658,11 @@ def _decode_args(q, k_sink, k_store, k_recent, v_sink, v_store, v_recent, norm, 
     def n_of(t):
         return 0 if t is None else t.shape[2]
 
-    kn = [n_of(k_sink), k_store.length if k_store is not None else 0, n_of(k_recent)]
-    vn = [n_of(v_sink), v_store.length if v_store is not None else 0, n_of(v_recent)]
-    ks = (_lib.iq_segment * 3)(_segment(k_sink, None, kn[0], dtype=act), _segment(None, k_store, kn[1]),
+    kn = [n_of(k_sink), k_store.length - k_t0 if k_store is not None else 0, n_of(k_recent)]
+    vn = [n_of(v_sink), v_store.length - v_t0 if v_store is not None else 0, n_of(v_recent)]
+    ks = (_lib.iq_segment * 3)(_segment(k_sink, None, kn[0], dtype=act), _segment(None, k_store, kn[1], k_t0),
                                _segment(k_recent, None, kn[2], dtype=act))
-    vs = (_lib.iq_segment * 3)(_segment(v_sink, None, vn[0], dtype=act), _segment(None, v_store, vn[1]),
+    vs = (_lib.iq_segment * 3)(_segment(v_sink, None, vn[0], dtype=act), _segment(None, v_store, vn[1], v_t0),
                                _segment(v_recent, None, vn[2], dtype=act))
     if norm is not None:
         require_device(norm, "norm", act)
@@ -669,11 +674,13 @@ def _decode_args(q, k_sink, k_store, k_recent, v_sink, v_store, v_recent, norm, 
 def decode_attention(q: torch.Tensor, k_sink: Optional[torch.Tensor], k_store: Optional[PackedStore],
                      k_recent: Optional[torch.Tensor], v_sink: Optional[torch.Tensor],
                      v_store: Optional[PackedStore], v_recent: Optional[torch.Tensor], scale: float,
-                     norm: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+                     norm: Optional[torch.Tensor] = None, out: Optional[torch.Tensor] = None,
+                     k_t0: int = 0, v_t0: int = 0) -> torch.Tensor:
     """One decode step of attention for q [B,Hq,D] over [sink | packed | recent] K and V
-    (fp16 or bf16: the query's dtype, which every segment and the output share)."""
+    (fp16 or bf16: the query's dtype, which every segment and the output share); the
+    stores are read from token k_t0 / v_t0 on (a sliding window's start)."""
     q, B, Hq, Hkv, T, D, ks, vs, norm, ws = _decode_args(q, k_sink, k_store, k_recent, v_sink, v_store, v_recent,
-                                                         norm, out)
+                                                         norm, out, k_t0, v_t0)
     if out is None:
         out = torch.empty(B, Hq, D, dtype=q.dtype, device=q.device)
     call("iq_decode_attention", _p(q), q.stride(0), q.stride(1), _p(norm), ks, vs, B, Hq, Hkv, T, D, float(scale),

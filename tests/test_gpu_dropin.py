@@ -359,6 +359,50 @@ def test_sliding_layer_fix_matches_oracle(name):
         np.testing.assert_array_equal(V.cpu().numpy(), Vr, err_msg=f"step {s}")
 
 
+@pytest.mark.parametrize("name", list(SLIDING))
+def test_sliding_attend_matches_oracle(name):
+    """fix_sliding_window = True: attend() (the fused decode path over the last
+    min(T, w) tokens, read packed from a store offset that need not align with a
+    K block or V group) at every step from 80 to 140 tokens with w = 96, against
+    float64 attention over the oracle's fixed sliding layer's window (its fp32
+    [sink | dequantized (times the key factor) | recent] tokens, the last
+    min(T, w) of them): within 1e-3."""
+    from oracle import attn_ref as A
+    from oracle import cache_ref
+    cfg = Cfg(**SLIDING[name], fix_sliding_window=True)
+    B, H, nrep, D, w = 2, 2, 4, 128, 96
+    kx = synth.kv_tensor(B, H, 140, D, seed=19, n_out=2, factor=8.0)
+    vx = synth.kv_tensor(B, H, 140, D, seed=20, n_out=2, factor=8.0)
+    qx = synth.normal((B, H * nrep, D), seed=21).astype(np.float16)
+    ref = cache_ref.SlidingLayerRef(cfg, w, fix=True)
+    layer = C.InnerqDynamicSlidingWindowLayer(cfg, 0, w)
+    kt, vt, qt = torch.from_numpy(kx).to(DEV), torch.from_numpy(vx).to(DEV), torch.from_numpy(qx).to(DEV)
+    layer.update(kt[:, :, :80], vt[:, :, :80])
+    ref.update(kx[:, :, :80], vx[:, :, :80])
+    worst = 0.0
+    for t in range(80, 140):
+        assert layer.fused_decode_ready(kt[:, :, t:t + 1])
+        layer.append(kt[:, :, t:t + 1], vt[:, :, t:t + 1])
+        ref.update(kx[:, :, t:t + 1], vx[:, :, t:t + 1])
+        got = layer.attend(qt[:, :, None], D ** -0.5)[:, :, 0].cpu().numpy().astype(np.float64)
+        kd = [ref.keys_sink.astype(np.float32)]
+        if ref.keys_q is not None:
+            d = ref.kdq(*ref.keys_q, ref.key_group_size)
+            kd.append(d * ref.norm.astype(np.float32) if ref.key_normalize else d)
+        kd.append(ref.keys_recent.astype(np.float32))
+        vd = [ref.values_sink.astype(np.float32)]
+        if ref.values_q is not None:
+            vd.append(ref.vdq(*ref.values_q, ref.value_group_size))
+        vd.append(ref.values_recent.astype(np.float32))
+        n = min(t + 1, w)
+        K = np.concatenate(kd, axis=2)[:, :, -n:]
+        V = np.concatenate(vd, axis=2)[:, :, -n:]
+        e = A.rel_err(got, A.decode_attention(qx, K, V, D ** -0.5, p_dtype=None))
+        worst = max(worst, e)
+        assert e < 1e-3, f"T={t + 1}: {e:.2e}"
+    print(f"sliding {name}: worst {worst:.2e} over T = 81..140 (w = {w})")
+
+
 def _tiny_mistral(preset, window=48):
     from transformers import MistralConfig
     from innerq_amd.models import InnerqMistralForCausalLM
@@ -401,3 +445,29 @@ def test_mistral_decodes_past_the_window_with_the_fix():
     cache = C.DynamicCache(config=model.config)
     got = _decode(model, cache, ids, dec)
     assert torch.isfinite(got).all() and cache.get_seq_length() == 70
+
+
+def test_mistral_decodes_past_the_window_through_attend(monkeypatch):
+    """The same Mistral with 4-bit K and V and the fix, now under the fused
+    attention: every decode step of both (sliding) layers goes through attend()
+    over the last w tokens, read packed, and the step logits match the eager
+    path on the same cache type (the dense window update() returns)."""
+    gen = torch.Generator(device=DEV).manual_seed(3)
+    ids = torch.randint(0, 64, (1, 40), generator=gen, device=DEV)
+    dec = torch.randint(0, 64, (1, 30), generator=gen, device=DEV)
+    model = _tiny_mistral(SLIDING["sliding_sym3_sinks"])
+    ref = _decode(model, C.DynamicCache(config=model.config), ids, dec)
+    calls = [0]
+    orig = C.InnerqDynamicSlidingWindowLayer.attend
+
+    def attend(self, *a, **kw):
+        calls[0] += 1
+        return orig(self, *a, **kw)
+
+    monkeypatch.setattr(C.InnerqDynamicSlidingWindowLayer, "attend", attend)
+    model.config._attn_implementation = "innerq_fused"
+    got = _decode(model, C.DynamicCache(config=model.config), ids, dec)
+    assert calls[0] == 2 * 30
+    err = ((got - ref).abs().max() / ref.abs().max()).item()
+    print(f"mistral fused vs eager past the window: {err:.2e}")
+    assert err < 2e-2
