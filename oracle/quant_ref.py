@@ -373,15 +373,3 @@ def v_store_to_codes(cw, meta, T, bits, group, mode):
     scale = m[..., 0].view(np.float16)
     zero = m[..., 1].view(np.float16) if m.shape[-1] == 2 else None
     return codes, scale, zero
-
-
-def dequant_signed(codes_signed, scale, zero, group, axis_token):
-    """fp32 dequant from stored (signed for sym) codes; equals the reference
-    dequant of (magnitude, sign) except for the sign of zero."""
-    if axis_token:
-        if zero is None:
-            return dequantize_tokendim_sym(codes_signed, scale, np.ones(codes_signed.shape, np.float16), group)
-        return dequantize_tokendim_asym(codes_signed, scale, zero, group)
-    if zero is None:
-        return dequantize_channeldim_sym(codes_signed, scale, np.ones(codes_signed.shape, np.float16), group)
-    return dequantize_channeldim_asym(codes_signed, scale, zero, group)

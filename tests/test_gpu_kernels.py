@@ -561,7 +561,8 @@ def test_decode_attention_full_size(kbits, vbits, R):
     32768 tokens, asym G=32; 4-bit K and V all packed (the headline step) and
     2-bit K / 4-bit V with a 128-token fp16 window (one layer of config 4).
     Reference: fp32 attention over K/V dequantized by the library (unpack is
-    bit-exact to the oracle elsewhere), query heads grouped per KV head."""
+    bit-exact to the oracle elsewhere), query heads grouped per KV head, and
+    three sampled heads end to end through the oracle."""
     B, Hkv, nrep, D, T = 8, 8, 4, 128, 32768
     Tq = T - R
     gen = torch.Generator(device=DEV).manual_seed(kbits * 10 + vbits + R)
@@ -577,12 +578,23 @@ def test_decode_attention_full_size(kbits, vbits, R):
     vr = v[:, :, Tq:] if R else None
     got = ops.decode_attention(q, None, kst, kr, None, vst, vr, D ** -0.5).float()
     kd = torch.cat([kst.dequant(dtype=torch.float32), k[:, :, Tq:].float()], dim=2)
-    del k
     lg = torch.matmul(q.float().view(B, Hkv, nrep, D), kd.transpose(-1, -2).contiguous()) * D ** -0.5
     del kd
     vd = torch.cat([vst.dequant(dtype=torch.float32), v[:, :, Tq:].float()], dim=2)
     ref = torch.matmul(torch.softmax(lg, dim=-1), vd).view(B, Hkv * nrep, D)
+    del vd, lg
     assert ((got - ref).abs().max() / ref.abs().max()).item() < TOL
+    # sampled (batch, KV head)s end to end through the oracle: its quantization
+    # of the same tokens, dequantization and float64 attention
+    for b, h in ((0, 0), (5, 3), (7, 7)):
+        kx, vx = k[b:b + 1, h:h + 1].cpu().numpy(), v[b:b + 1, h:h + 1].cpu().numpy()
+        kq = oracle_deq(*oracle_q(kx[:, :, :Tq], kbits, 32, "asymmetric", "channel"), 32, "asymmetric", "channel")
+        vq = oracle_deq(*oracle_q(vx[:, :, :Tq], vbits, 32, "asymmetric", "token"), 32, "asymmetric", "token")
+        kd = np.concatenate([kq, kx[:, :, Tq:].astype(np.float32)], axis=2)
+        vd = np.concatenate([vq, vx[:, :, Tq:].astype(np.float32)], axis=2)
+        qh = q[b:b + 1, h * nrep:(h + 1) * nrep].cpu().numpy()
+        o = A.decode_attention(qh, kd, vd, D ** -0.5, p_dtype=None)
+        assert A.rel_err(got[b:b + 1, h * nrep:(h + 1) * nrep].cpu().numpy().astype(np.float64), o) < TOL
 
 
 @pytest.mark.parametrize("B,Hkv,nrep,T", [(10, 10, 1, 768 + 40), (3, 8, 2, 4096 + 40)])
