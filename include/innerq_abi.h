@@ -292,8 +292,8 @@ size_t iq_decode_workspace_bytes(int B, int Hq, int T, int D);
  * A bf16 layer (LongBench/pred.py:240 loads the model in bf16): IQ_MODE_BF16
  * on the mode of every segment that holds tokens (its stores were written
  * with it); q, norm, the dense rows and out are then bf16, the probabilities
- * of the packed range meet V as fp16 (finer than the reference's bf16 cast),
- * those of the dense tokens as bf16.  Segments that disagree: IQ_ERR_MODE;
+ * of the packed range meet V as fp16 and those of the dense tokens as fp32
+ * (both finer than the reference's bf16 cast).  Segments that disagree: IQ_ERR_MODE;
  * bf16 K and V of different group sizes: IQ_ERR_MODE (fp16 only). */
 int iq_decode_attention(const void* q, int64_t sq_b, int64_t sq_h, const void* norm,
                         const iq_segment* k, const iq_segment* v,
