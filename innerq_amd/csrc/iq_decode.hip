@@ -36,8 +36,9 @@ constexpr int MERGE_RUNS_MAX = 4;  // fused runs per (batch, KV head) the mergin
 // recent window and the <= 31 packed keys short of a V group, 129-159 tokens
 // that two sections take in two chunks each: 13.9 us against 15.2 us per
 // call), two for fp16 windows (configs 3 and 4: 7.5 us against 8.2 us)
-// (bf16 layers: two, whose fp32 tiles fill the LDS)
-constexpr int merge_sections(bool pk, bool bf = false) { return pk && !bf ? 3 : 2; }
+// (bf16 layers: two, whose fp32 tiles fill the LDS; eight query heads per KV
+// head: two, whose fp16 accumulators would not fit three sections' registers)
+constexpr int merge_sections(bool pk, bool bf, int nrep) { return pk && !bf && nrep <= 4 ? 3 : 2; }
 
 struct Seg {
   const uint16_t* dense;
@@ -276,12 +277,16 @@ __device__ __forceinline__ void packed_run(const Seg& K, const Seg& V, const uin
 // tokens packed in only one of K and V).  Workgroup (s, b * Hkv + kvh) takes
 // slice s of the dense tokens for the NREP query heads of KV head kvh, in
 // chunks of DT tokens: the chunk's K and V rows are gathered as fp16 into
-// LDS (the next chunk's rows are loaded into registers meanwhile), wave w
-// computes the logits of heads w, w + 4, ... with lane = token and keeps their
-// running (m, l), and thread (head, column pair) accumulates the output.  The
+// LDS (the next chunk's rows are loaded into registers meanwhile); the logits
+// come from the four waves' quarters of head_dim (lane = token, every head),
+// wave w keeps the running (m, l) of heads w, w + 4, ..., and wave w
+// accumulates the output of every head over a quarter of the chunk's tokens
+// (lane = column pair), so a section reads its K and V tiles once per chunk
+// (per query head, when a wave took one head: 7.45 -> 7.01 us per merging
+// call at config 4's shape, 13.94 -> 13.33 us with packed rows, traced).  The
 // probability that meets V is rounded to fp16, as the reference rounds its
 // softmax output; logits, sums and outputs are fp32.
-// MERGE (launched after the fused kernel, one workgroup of merge_sections(PK)
+// MERGE (launched after the fused kernel, one workgroup of merge_sections
 // 256-thread sections per (batch, KV head)): each section takes its share of
 // the dense tokens as its slice, side by side, and the workgroup then merges
 // the sections' states with the fused kernel's run partials of the head and
@@ -290,10 +295,12 @@ __device__ __forceinline__ void packed_run(const Seg& K, const Seg& V, const uin
 // tiles hold fp32 values (bf16 rows convert exactly, packed rows keep their
 // fp32 dequantized values) and the logits and p.V are fp32 products with the
 // unrounded probabilities: rounding the window's rows and probabilities to
-// bf16 put a window-heavy step at 1.005e-3 of fp32 attention.
+// bf16 put a window-heavy step at 1.005e-3 of fp32 attention.  Its waves take
+// one head each for the logits and thread (head, column pair) accumulates
+// the output.
 template <int D, int NREP, bool PK, bool MERGE = false, bool BF = false>
-__global__ __launch_bounds__(MERGE ? 256 * merge_sections(PK, BF) : 256) void dense_attn_kernel(DenseArgs a) {
-  constexpr int NH = MERGE ? merge_sections(PK, BF) : 1;  // slices per workgroup (256-thread sections)
+__global__ __launch_bounds__(MERGE ? 256 * merge_sections(PK, BF, NREP) : 256) void dense_attn_kernel(DenseArgs a) {
+  constexpr int NH = MERGE ? merge_sections(PK, BF, NREP) : 1;  // slices per workgroup (256-thread sections)
   constexpr int NTH = 256 * NH;
   constexpr int TW = BF ? D : D / 2;          // dwords of a row's values: fp32, or fp16 pairs
   constexpr int KS = TW + 1;                  // K tile row stride in dwords (odd: no bank conflicts)
@@ -304,9 +311,21 @@ __global__ __launch_bounds__(MERGE ? 256 * merge_sections(PK, BF) : 256) void de
   constexpr int NPR = D / 2;                  // column pairs per head
   constexpr int OPT = (NREP * NPR + 255) / 256;  // (head, pair) items per thread
   constexpr int RE = D / 4;                   // row elements per gathering thread
+  // fp16: each section reads its K and V tiles once, not once per query head.
+  // For the logits wave w sums its quarter of head_dim (QW pair-dwords) for
+  // every head, lane = token, and the quarters meet in LDS (lgp); for attn.V
+  // wave w takes a quarter of the chunk's tokens for every head, lane =
+  // (column pair, token subgroup), and the waves' partial outputs are summed
+  // once, after the last chunk.
+  constexpr int QW = TW / 4;
+  constexpr int PPL = NPR < 64 ? NPR : 64;  // column pairs across a wave's lanes
+  constexpr int TSUB = 64 / PPL;            // token subgroups of a wave (D = 64: two)
+  constexpr int TPS = DT / 4 / TSUB;        // attn.V tokens per lane and chunk
+  static_assert(BF || (QW % 4 == 0 && TSUB <= 2 && TPS % 2 == 0 && 4 * NREP * D <= DT * KS), "fp16 split");
   __shared__ uint32_t kts[NH][DT][KS];
   __shared__ __align__(8) uint32_t vts[NH][DT][VS];
-  __shared__ uint32_t qs2[NREP][TW];  // the query heads' fp16 pairs (fp32 values: BF)
+  __shared__ __align__(16) uint32_t qs2[NREP][TW];  // the query heads' fp16 pairs (fp32 values: BF)
+  __shared__ float lgps[BF ? 1 : NH][BF ? 1 : 4][BF ? 1 : NREP][BF ? 1 : DT];  // fp16: logits per head_dim quarter
   __shared__ __align__(4) uint16_t pss[NH][NREP][BF ? 2 * DT : DT];  // probabilities: fp16 (fp32: BF)
   __shared__ float als[NH][NREP];
   const int half = MERGE ? int(threadIdx.x >> 8) : 0;
@@ -315,6 +334,7 @@ __global__ __launch_bounds__(MERGE ? 256 * merge_sections(PK, BF) : 256) void de
   auto& ps = pss[half];
   float* psf = reinterpret_cast<float*>(&pss[half][0][0]);  // BF: [NREP][DT] fp32
   auto& al = als[half];
+  auto& lgp = lgps[BF ? 0 : half];
   const int tid = int(threadIdx.x) & 255, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave within the section
   const int bh = blockIdx.y, b = bh / a.Hkv, kvh = bh % a.Hkv;
@@ -327,7 +347,8 @@ __global__ __launch_bounds__(MERGE ? 256 * merge_sections(PK, BF) : 256) void de
 
   // gathering: thread = (row tid / 4, quarter tid % 4 of the row)
   const int gr = tid >> 2, gq = tid & 3;
-  uint32_t kr[RE / 2], vr[RE / 2];
+  // (zero until the first gather: a section with no token stages zero rows)
+  uint32_t kr[RE / 2] = {}, vr[RE / 2] = {};
   bool kpk = false, vpk = false;  // the thread's row is in the packed K / V segment
   auto gather = [&](int c0) {
     const int i = c0 + gr;
@@ -366,9 +387,13 @@ __global__ __launch_bounds__(MERGE ? 256 * merge_sections(PK, BF) : 256) void de
   float m[HPW], l[HPW];
 #pragma unroll
   for (int hh = 0; hh < HPW; ++hh) { m[hh] = -INFINITY; l[hh] = 0.f; }
-  float o[OPT][2];
+  float o[OPT][2];  // BF: thread = (head, column pair) items
 #pragma unroll
   for (int it = 0; it < OPT; ++it) o[it][0] = o[it][1] = 0.f;
+  float ov[NREP][2];  // fp16: columns 2 pr, 2 pr + 1 of every head over the lane's tokens
+#pragma unroll
+  for (int h = 0; h < NREP; ++h) ov[h][0] = ov[h][1] = 0.f;
+  const int pr = lane % PPL, tl0 = wave * (DT / 4) + (lane / PPL) * TPS;  // fp16 attn.V: pair, first token
 
   for (int ci = 0; ci < nch; ++ci) {
     // a chunk past the slice's tokens (MERGE: a shorter section) has no live
@@ -411,19 +436,44 @@ __global__ __launch_bounds__(MERGE ? 256 * merge_sections(PK, BF) : 256) void de
     float dot[HPW];
 #pragma unroll
     for (int hh = 0; hh < HPW; ++hh) dot[hh] = 0.f;
-    // no per-iteration guard on the head (a wave-uniform branch in the loop
-    // serialized it on LDS latency): heads past NREP read the last head's
-    // query and their logits are dropped below
-    // one v_dot2_f32_f16 per (head, column pair): both products exact,
-    // accumulated in fp32 (BF: one fp32 fma per column)
+    if constexpr (BF) {
+      // no per-iteration guard on the head (a wave-uniform branch in the loop
+      // serialized it on LDS latency): heads past NREP read the last head's
+      // query and their logits are dropped below; one fp32 fma per column
 #pragma unroll 16
-    for (int i = 0; i < TW; ++i) {
-      const uint32_t k2 = kt[lane][i];
+      for (int i = 0; i < TW; ++i) {
+        const uint32_t k2 = kt[lane][i];
+#pragma unroll
+        for (int hh = 0; hh < HPW; ++hh) {
+          const int h = min(wave + 4 * hh, NREP - 1);
+          dot[hh] = fmaf(__uint_as_float(k2), __uint_as_float(qs2[h][i]), dot[hh]);
+        }
+      }
+    } else {
+      // wave w: its quarter of head_dim for every head, four of the row's
+      // pairs per step against each head's four query pairs (one broadcast
+      // read); one v_dot2_f32_f16 per (head, column pair): both products
+      // exact, accumulated in fp32.  The quarters are summed in wave order.
+      float dq[NREP];
+#pragma unroll
+      for (int h = 0; h < NREP; ++h) dq[h] = 0.f;
+      const uint32_t* krow = &kt[lane][wave * QW];
+#pragma unroll
+      for (int i = 0; i < QW; i += 4) {
+        const uint32_t k0 = krow[i], k1 = krow[i + 1], k2 = krow[i + 2], k3 = krow[i + 3];
+#pragma unroll
+        for (int h = 0; h < NREP; ++h) {
+          const uint4 qv = *reinterpret_cast<const uint4*>(&qs2[h][wave * QW + i]);
+          dq[h] = dot2<false>(k3, qv.w, dot2<false>(k2, qv.z, dot2<false>(k1, qv.y, dot2<false>(k0, qv.x, dq[h]))));
+        }
+      }
+#pragma unroll
+      for (int h = 0; h < NREP; ++h) lgp[wave][h][lane] = dq[h];
+      __syncthreads();
 #pragma unroll
       for (int hh = 0; hh < HPW; ++hh) {
         const int h = min(wave + 4 * hh, NREP - 1);
-        if constexpr (BF) dot[hh] = fmaf(__uint_as_float(k2), __uint_as_float(qs2[h][i]), dot[hh]);
-        else dot[hh] = dot2<false>(k2, qs2[h][i], dot[hh]);
+        dot[hh] = ((lgp[0][h][lane] + lgp[1][h][lane]) + lgp[2][h][lane]) + lgp[3][h][lane];
       }
     }
     const bool live = c0 + lane < i1;
@@ -456,22 +506,21 @@ __global__ __launch_bounds__(MERGE ? 256 * merge_sections(PK, BF) : 256) void de
       }
     }
     __syncthreads();
-    // ---- attn.V: thread = (head, column pair), eight tokens per step in two
-    // accumulation chains (the tile rows past the chunk's tokens are zero and
-    // their p is 0, so the chunk is read in whole steps); per two tokens and
-    // column a v_dot2_f32_f16 of (v_j, v_j+1) (one v_perm_b32 from the two
-    // rows' pairs) and the fp16 (p_j, p_j+1) ----
-    const int cnt8 = (min(DT, i1 - c0) + 7) & ~7;
+    if constexpr (BF) {
+      // ---- attn.V: thread = (head, column pair), eight tokens per step in
+      // two accumulation chains (the tile rows past the chunk's tokens are
+      // zero and their p is 0, so the chunk is read in whole steps); fp32
+      // values and probabilities ----
+      const int cnt8 = (min(DT, i1 - c0) + 7) & ~7;
 #pragma unroll
-    for (int it = 0; it < OPT; ++it) {
-      const int idx = tid + 256 * it;
-      if (idx < NREP * NPR) {
-        const int h = idx / NPR, dp = idx % NPR;
-        float o0 = o[it][0] * al[h], o1 = o[it][1] * al[h], e0 = 0.f, e1 = 0.f;
-        for (int j = 0; j < cnt8; j += 8) {
+      for (int it = 0; it < OPT; ++it) {
+        const int idx = tid + 256 * it;
+        if (idx < NREP * NPR) {
+          const int h = idx / NPR, dp = idx % NPR;
+          float o0 = o[it][0] * al[h], o1 = o[it][1] * al[h], e0 = 0.f, e1 = 0.f;
+          for (int j = 0; j < cnt8; j += 8) {
 #pragma unroll
-          for (int u = 0; u < 8; u += 4) {
-            if constexpr (BF) {  // fp32 values and probabilities: columns 2 dp, 2 dp + 1 of four tokens
+            for (int u = 0; u < 8; u += 4) {  // columns 2 dp, 2 dp + 1 of four tokens
               const float* pf = psf + h * DT + j + u;
               const float2 va = *reinterpret_cast<const float2*>(&vt[j + u][2 * dp]);
               const float2 vb = *reinterpret_cast<const float2*>(&vt[j + u + 1][2 * dp]);
@@ -481,29 +530,68 @@ __global__ __launch_bounds__(MERGE ? 256 * merge_sections(PK, BF) : 256) void de
               o1 = fmaf(vb.y, pf[1], fmaf(va.y, pf[0], o1));
               e0 = fmaf(vd.x, pf[3], fmaf(vc.x, pf[2], e0));
               e1 = fmaf(vd.y, pf[3], fmaf(vc.y, pf[2], e1));
-            } else {
-              const uint32_t pq = *reinterpret_cast<const uint32_t*>(&ps[h][j + u]);
-              const uint32_t pr = *reinterpret_cast<const uint32_t*>(&ps[h][j + u + 2]);
-              const uint32_t va = vt[j + u][dp], vb = vt[j + u + 1][dp];
-              const uint32_t vc = vt[j + u + 2][dp], vd = vt[j + u + 3][dp];
-              // columns 2 dp and 2 dp + 1 of tokens (j+u, j+u+1), then (j+u+2, j+u+3)
-              o0 = dot2<false>(__builtin_amdgcn_perm(vb, va, 0x05040100u), pq, o0);
-              o1 = dot2<false>(__builtin_amdgcn_perm(vb, va, 0x07060302u), pq, o1);
-              e0 = dot2<false>(__builtin_amdgcn_perm(vd, vc, 0x05040100u), pr, e0);
-              e1 = dot2<false>(__builtin_amdgcn_perm(vd, vc, 0x07060302u), pr, e1);
             }
           }
+          o[it][0] = o0 + e0;
+          o[it][1] = o1 + e1;
         }
-        o[it][0] = o0 + e0;
-        o[it][1] = o1 + e1;
+      }
+    } else {
+      // ---- attn.V: wave w takes tokens [DT/4 w, DT/4 (w+1)) of the chunk
+      // for every head, lane = (column pair pr, token subgroup); per two
+      // tokens and column a v_dot2_f32_f16 of (v_j, v_j+1) (one v_perm_b32
+      // from the two rows' pairs) and each head's fp16 (p_j, p_j+1).  Every
+      // row is read: rows past the chunk's tokens hold zeros (or, in a
+      // section with fewer chunks, its last chunk's rows) and have p = 0 ----
+#pragma unroll
+      for (int h = 0; h < NREP; ++h) {
+        ov[h][0] *= al[h];
+        ov[h][1] *= al[h];
+      }
+#pragma unroll
+      for (int j = 0; j < TPS; j += 2) {
+        const uint32_t va = vt[tl0 + j][pr], vb = vt[tl0 + j + 1][pr];
+        const uint32_t lo = __builtin_amdgcn_perm(vb, va, 0x05040100u);  // column 2 pr of tokens j, j + 1
+        const uint32_t hi = __builtin_amdgcn_perm(vb, va, 0x07060302u);  // column 2 pr + 1
+#pragma unroll
+        for (int h = 0; h < NREP; ++h) {
+          const uint32_t pp = *reinterpret_cast<const uint32_t*>(&ps[h][tl0 + j]);
+          ov[h][0] = dot2<false>(lo, pp, ov[h][0]);
+          ov[h][1] = dot2<false>(hi, pp, ov[h][1]);
+        }
       }
     }
     __syncthreads();
   }
+  // fp16: the waves' partial outputs go into the K tile (every wave is past
+  // its last read of it), [wave][head][column]; D = 64: lanes l and l + 32
+  // (the two token subgroups) first
+  if constexpr (!BF) {
+    float* opart = reinterpret_cast<float*>(&kt[0][0]);
+    if constexpr (TSUB == 2) {
+#pragma unroll
+      for (int h = 0; h < NREP; ++h) {
+        ov[h][0] += __shfl_xor(ov[h][0], 32, 64);
+        ov[h][1] += __shfl_xor(ov[h][1], 32, 64);
+      }
+    }
+    if (lane < PPL) {
+#pragma unroll
+      for (int h = 0; h < NREP; ++h) {
+        opart[(wave * NREP + h) * D + 2 * pr] = ov[h][0];
+        opart[(wave * NREP + h) * D + 2 * pr + 1] = ov[h][1];
+      }
+    }
+  }
+  // the section's output column dd of head h: its waves' partials in wave order
+  auto sec_out = [&](int hf, int h, int dd) {
+    const float* op = reinterpret_cast<const float*>(&kts[hf][0][0]) + h * D + dd;
+    return ((op[0] + op[NREP * D]) + op[2 * NREP * D]) + op[3 * NREP * D];
+  };
   if constexpr (MERGE) {
     // ---- merge: the sections' states and the fused runs' partials ----
     __shared__ float mh[NH][NREP], lh[NH][NREP];
-    __shared__ float oh[NH][NREP][D];
+    __shared__ float oh[BF ? NH : 1][BF ? NREP : 1][BF ? D : 1];  // BF: the sections' outputs
 #pragma unroll
     for (int hh = 0; hh < HPW; ++hh) {
       const int h = wave + 4 * hh;
@@ -512,13 +600,15 @@ __global__ __launch_bounds__(MERGE ? 256 * merge_sections(PK, BF) : 256) void de
         lh[half][h] = l[hh];
       }
     }
+    if constexpr (BF) {
 #pragma unroll
-    for (int it = 0; it < OPT; ++it) {
-      const int idx = tid + 256 * it;
-      if (idx < NREP * NPR) {
-        const int h = idx / NPR, dp = idx % NPR;
-        oh[half][h][2 * dp] = o[it][0];
-        oh[half][h][2 * dp + 1] = o[it][1];
+      for (int it = 0; it < OPT; ++it) {
+        const int idx = tid + 256 * it;
+        if (idx < NREP * NPR) {
+          const int h = idx / NPR, dp = idx % NPR;
+          oh[half][h][2 * dp] = o[it][0];
+          oh[half][h][2 * dp + 1] = o[it][1];
+        }
       }
     }
     __syncthreads();
@@ -555,7 +645,8 @@ __global__ __launch_bounds__(MERGE ? 256 * merge_sections(PK, BF) : 256) void de
       for (int hf = 0; hf < NH; ++hf) {
         const float w = mh[hf][h] == -INFINITY ? 0.f : __expf(mh[hf][h] - M);
         L = fmaf(w, lh[hf][h], L);
-        acc = fmaf(w, oh[hf][h][dd], acc);
+        if constexpr (BF) acc = fmaf(w, oh[hf][h][dd], acc);
+        else acc = fmaf(w, sec_out(hf, h, dd), acc);
       }
       a.out[b * a.sob + (int64_t(kvh) * NREP + h) * a.soh + dd] = uint16_t(to_act<BF>(acc / L));
     }
@@ -574,15 +665,20 @@ __global__ __launch_bounds__(MERGE ? 256 * merge_sections(PK, BF) : 256) void de
       mls[(row0 + h) * 2 + 1] = l[hh];
     }
   }
+  if constexpr (BF) {
 #pragma unroll
-  for (int it = 0; it < OPT; ++it) {
-    const int idx = tid + 256 * it;
-    if (idx < NREP * NPR) {
-      const int h = idx / NPR, dp = idx % NPR;
-      float* dst = os + (row0 + h) * D + 2 * dp;
-      dst[0] = o[it][0];
-      dst[1] = o[it][1];
+    for (int it = 0; it < OPT; ++it) {
+      const int idx = tid + 256 * it;
+      if (idx < NREP * NPR) {
+        const int h = idx / NPR, dp = idx % NPR;
+        float* dst = os + (row0 + h) * D + 2 * dp;
+        dst[0] = o[it][0];
+        dst[1] = o[it][1];
+      }
     }
+  } else {
+    __syncthreads();  // the waves' partials are in the K tile
+    for (int r = tid; r < NREP * D; r += 256) os[(row0 + r / D) * D + r % D] = sec_out(half, r / D, r % D);
   }
 }
 
@@ -958,11 +1054,11 @@ int launch_splits(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, c
       const dim3 mgrid{1u, unsigned(bhs), 1u};
       auto go = [&]<int DD, int R>() {
         if (bf) {
-          if (pk) dense_attn_kernel<DD, R, true, true, true><<<mgrid, 256 * merge_sections(true, true), 0, st>>>(da);
-          else dense_attn_kernel<DD, R, false, true, true><<<mgrid, 256 * merge_sections(false, true), 0, st>>>(da);
+          if (pk) dense_attn_kernel<DD, R, true, true, true><<<mgrid, 256 * merge_sections(true, true, R), 0, st>>>(da);
+          else dense_attn_kernel<DD, R, false, true, true><<<mgrid, 256 * merge_sections(false, true, R), 0, st>>>(da);
         } else {
-          if (pk) dense_attn_kernel<DD, R, true, true><<<mgrid, 256 * merge_sections(true), 0, st>>>(da);
-          else dense_attn_kernel<DD, R, false, true><<<mgrid, 256 * merge_sections(false), 0, st>>>(da);
+          if (pk) dense_attn_kernel<DD, R, true, true><<<mgrid, 256 * merge_sections(true, false, R), 0, st>>>(da);
+          else dense_attn_kernel<DD, R, false, true><<<mgrid, 256 * merge_sections(false, false, R), 0, st>>>(da);
         }
       };
       auto by_r = [&]<int DD>() {

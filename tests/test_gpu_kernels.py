@@ -23,13 +23,16 @@ def f16t(a):
     return torch.from_numpy(np.ascontiguousarray(a)).to(DEV)
 
 
+_MODE_TAG = {"asymmetric": "asym", "symmetric": "sym", "hybrid": "hybrid"}
+
+
 def oracle_q(x, bits, G, mode, axis):
-    fn = getattr(Q, f"quantize_{axis}dim_{'asym' if mode == 'asymmetric' else 'sym'}")
+    fn = getattr(Q, f"quantize_{axis}dim_{_MODE_TAG[mode]}")
     return fn(x, G, bits)
 
 
 def oracle_deq(c, s, z, G, mode, axis):
-    fn = getattr(Q, f"dequantize_{axis}dim_{'asym' if mode == 'asymmetric' else 'sym'}")
+    fn = getattr(Q, f"dequantize_{axis}dim_{_MODE_TAG[mode]}")
     return fn(c, s, z, G)
 
 
@@ -655,6 +658,31 @@ def test_decode_attention_fused_formats(fmt, nrep, D):
     vseg = (16, vq, 64 * 21 + 80 - vq)
     err = _decode_case(2, 2, nrep, D, kseg, vseg, (kbits, G, km), (vbits, G, vm), seed=kbits * G + nrep + vbits,
                        norm=True)
+    assert err < TOL
+
+
+# Windows attended after the fused kernel by the merging dense kernel: at the
+# BASELINE decode shapes (groups of 32, D = 128, four query heads per KV head)
+# with every store-mode instance of the fused kernel (asym, sym, mixed, hybrid
+# V), key normalization, rows packed in only one of K and V (three sections)
+# and windows of one chunk or two per section; then eight query heads per KV
+# head with packed rows (two sections), and D = 64 (two token subgroups per
+# wave in attn.V).
+@pytest.mark.parametrize("kfmt,vfmt,kseg,vseg,norm,nrep,D", [
+    ((2, 32, "asymmetric"), (4, 32, "asymmetric"), (0, 64 * 20, 128), (0, 64 * 20, 128), False, 4, 128),
+    ((3, 32, "symmetric"), (3, 32, "symmetric"), (0, 64 * 20, 128), (0, 64 * 20, 128), False, 4, 128),
+    ((3, 32, "symmetric"), (4, 32, "asymmetric"), (5, 64 * 12, 60), (5, 64 * 12, 60), False, 4, 128),
+    ((3, 32, "symmetric"), (3, 32, "symmetric"), (32, 64 * 9 + 20, 76), (32, 64 * 9, 96), True, 4, 128),
+    ((3, 32, "symmetric"), (2, 32, "hybrid"), (32, 64 * 9 + 20, 76), (32, 64 * 9, 96), True, 4, 128),
+    ((4, 32, "asymmetric"), (4, 32, "asymmetric"), (7, 64 * 10, 193), (7, 64 * 10, 193), False, 4, 128),
+    ((2, 32, "asymmetric"), (2, 32, "symmetric"), (32, 64 * 9 + 20, 150), (32, 64 * 9, 170), True, 4, 128),
+    ((3, 32, "symmetric"), (3, 32, "symmetric"), (32, 64 * 9 + 20, 76), (32, 64 * 9, 96), True, 8, 128),
+    ((4, 32, "asymmetric"), (4, 32, "asymmetric"), (16, 64 * 9 + 20, 120), (16, 64 * 9, 140), False, 2, 64),
+    ((2, 32, "asymmetric"), (4, 32, "asymmetric"), (3, 64 * 8, 200), (3, 64 * 8, 200), False, 1, 64),
+])
+def test_decode_attention_window_formats(kfmt, vfmt, kseg, vseg, norm, nrep, D):
+    print(f"window formats: K {kfmt} V {vfmt} segments {kseg} {vseg} norm={norm} nrep={nrep} D={D}", flush=True)
+    err = _decode_case(2, 2, nrep, D, kseg, vseg, kfmt, vfmt, seed=sum(kseg) + kfmt[0] * 7 + vfmt[0] + nrep, norm=norm)
     assert err < TOL
 
 
