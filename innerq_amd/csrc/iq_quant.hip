@@ -110,32 +110,72 @@ __device__ __forceinline__ uint32_t asym_field(int32_t c) { return asym_field_b(
 template <int BITS>
 __device__ __forceinline__ uint32_t sym_field(int32_t c, float sg) { return sym_field_b(c, sg, BITS); }
 
+// x / s in fp32, rounded to nearest, for a finite x >= 0 and a finite s > 0
+// that are fp16 values, given r = RN32(1 / s): q0 = RN32(x r), then one
+// correction by the residual x - q0 s, which an fma gives exactly
+// (Markstein's division step), so the result is RN32(x / s) and its fp16
+// rounding is the reference's fp16 division.  One divide per group and three
+// operations per value instead of a divide per value; checked over every
+// such pair of fp16 operands (tests/test_quant_division.py).
+__device__ __forceinline__ float div_rcp(float x, float s, float r) {
+  const float q0 = __fmul_rn(x, r);
+  return __fmaf_rn(__fmaf_rn(-q0, s, x), r, q0);
+}
+
 // Quantize G values held as fp32 copies of fp16 numbers.  fields[] receives
 // the b-bit stored field, codes[] the dense reference code, sgn[] the sign.
+// A group whose scale is finite and positive (every group but the constant,
+// NaN and infinite ones, which divide per value) divides through its
+// reciprocal: its dividends x - min (asym) and |x| (sym) are finite and >= 0.
 template <int BITS, int G>
 __device__ __forceinline__ void quantize_group(const float* v, bool sym, uint32_t* fields, int32_t* codes,
                                                float* sgn, float& s_out, float& z_out) {
   if (!sym) {
     float s, mn;
     asym_params<BITS, G>(v, s, mn);
+    if (s > 0.f && s < INFINITY) {
+      constexpr float L = float((1 << BITS) - 1);
+      const float r = __fdiv_rn(1.0f, s);
 #pragma unroll
-    for (int i = 0; i < G; ++i) {
-      const int32_t c = asym_code<BITS>(v[i], mn, s);
-      codes[i] = c;
-      fields[i] = asym_field<BITS>(c);
-      sgn[i] = 0.f;
+      for (int i = 0; i < G; ++i) {
+        const int32_t c = code_of(round_f16(div_rcp(round_f16(v[i] - mn), s, r)), L);  // quant.py:69-71
+        codes[i] = c;
+        fields[i] = asym_field<BITS>(c);
+        sgn[i] = 0.f;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < G; ++i) {
+        const int32_t c = asym_code<BITS>(v[i], mn, s);
+        codes[i] = c;
+        fields[i] = asym_field<BITS>(c);
+        sgn[i] = 0.f;
+      }
     }
     s_out = s;
     z_out = mn;
   } else {
     const float s = sym_scale<BITS, G>(v);
+    if (s > 0.f && s < INFINITY) {
+      constexpr float L = float((1 << (BITS - 1)) - 1);
+      const float r = __fdiv_rn(1.0f, s);
 #pragma unroll
-    for (int i = 0; i < G; ++i) {
-      const int32_t c = sym_code<BITS>(v[i], s);
-      const float sg = sign_of(v[i]);
-      codes[i] = c;
-      fields[i] = sym_field<BITS>(c, sg);
-      sgn[i] = sg;
+      for (int i = 0; i < G; ++i) {
+        const int32_t c = code_of(round_f16(div_rcp(fabsf(v[i]), s, r)), L);  // quant.py:108-109
+        const float sg = sign_of(v[i]);
+        codes[i] = c;
+        fields[i] = sym_field<BITS>(c, sg);
+        sgn[i] = sg;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < G; ++i) {
+        const int32_t c = sym_code<BITS>(v[i], s);
+        const float sg = sign_of(v[i]);
+        codes[i] = c;
+        fields[i] = sym_field<BITS>(c, sg);
+        sgn[i] = sg;
+      }
     }
     s_out = s;
     z_out = 0.f;
