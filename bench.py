@@ -281,7 +281,10 @@ def bench_headline(args):
 def bench_config(args):
     """Non-headline BASELINE configs, one JSON line each: us = per call through the
     Python API (host launch cost included), us_graph = the same calls replayed from
-    a captured HIP graph (GPU time)."""
+    a captured HIP graph (16 calls per graph: a replay's own launch gap, a few us,
+    is spread over them), us_gpu = the same calls enqueued behind a GPU backlog
+    (time_backlogged, median of three loops: back-to-back GPU time, the headline's
+    timing)."""
     import torch
     from innerq_amd import ops
     dev = torch.device("cuda:0")
@@ -297,8 +300,10 @@ def bench_config(args):
         clock_warmup(dev)
         us = time_loop(fn, args.steps, args.warmup)
         ug = time_graph(fn, 4 * C, max(1, args.steps // 4))
+        ub = statistics.median(time_backlogged(fn, args.steps, args.warmup) for _ in range(3))
         b = gemv_bytes(B, Hkv, T, D, G, 4, "asymmetric", "channel")
-        res.update(us=us, GBs=b / us / 1e3, us_graph=ug, GBs_graph=b / ug / 1e3, bytes=b)
+        res.update(us=us, GBs=b / us / 1e3, us_graph=ug, GBs_graph=b / ug / 1e3, us_gpu=ub, GBs_gpu=b / ub / 1e3,
+                   bytes=b)
     elif cfg == "2":
         B, Hq, Hkv, D, T, G = 8, 32, 8, 128, 32768, 64
         for mode in ("asymmetric", "symmetric"):
@@ -308,9 +313,11 @@ def bench_config(args):
             fn = lambda i: ops.av_gemv(p, vs[i % C], out=out)
             clock_warmup(dev)
             us = time_loop(fn, args.steps, args.warmup)
-            ug = time_graph(fn, C, max(1, args.steps // 4))
+            ug = time_graph(fn, 4 * C, max(1, args.steps // 4))
+            ub = statistics.median(time_backlogged(fn, args.steps, args.warmup) for _ in range(3))
             b = gemv_bytes(B, Hkv, T, D, G, 2, mode, "token")
-            res[mode] = dict(us=us, GBs=b / us / 1e3, us_graph=ug, GBs_graph=b / ug / 1e3, bytes=b)
+            res[mode] = dict(us=us, GBs=b / us / 1e3, us_graph=ug, GBs_graph=b / ug / 1e3, us_gpu=ub,
+                             GBs_gpu=b / ub / 1e3, frac_gpu=b / ub / 1e3 / PEAK_GBS, bytes=b)
             del vs
     elif cfg == "3":
         B, Hq, Hkv, D, T, G, R = 16, 32, 8, 128, 16384, 32, 128
@@ -332,9 +339,11 @@ def bench_config(args):
         clock_warmup(dev)
 
         us = time_loop(step, args.steps, args.warmup)
-        ug = time_graph(step, C, max(1, args.steps // 4))
+        ug = time_graph(step, 4 * C, max(1, args.steps // 4))
+        ub = statistics.median(time_backlogged(step, args.steps, args.warmup) for _ in range(3))
         b = 2 * gemv_bytes(B, Hkv, Tq, D, G, 3, "symmetric", "channel")
-        res.update(us=us, GBs=b / us / 1e3, us_graph=ug, GBs_graph=b / ug / 1e3, bytes=b)
+        res.update(us=us, GBs=b / us / 1e3, us_graph=ug, GBs_graph=b / ug / 1e3, us_gpu=ub, GBs_gpu=b / ub / 1e3,
+                   frac_gpu=b / ub / 1e3 / PEAK_GBS, bytes=b)
     elif cfg == "4":
         B, Hq, Hkv, D, T, G, R, L = 8, 32, 8, 128, 32768, 32, 128, 32
         Tq = T - R
@@ -353,10 +362,12 @@ def bench_config(args):
 
         us = time_loop(step, max(1, args.steps // 10), 2)
         ug = time_graph(step, 1, max(1, args.steps // 10))
+        ub = statistics.median(time_backlogged(step, max(1, args.steps // 10), 2) for _ in range(3))
         b = L * (gemv_bytes(B, Hkv, Tq, D, G, 2, "asymmetric", "channel")
                  + gemv_bytes(B, Hkv, Tq - Tq % G, D, G, 4, "asymmetric", "token"))
         res.update(us=us, us_per_layer=us / L, GBs=b / us / 1e3, us_graph=ug, us_per_layer_graph=ug / L,
-                   GBs_graph=b / ug / 1e3, bytes=b)
+                   GBs_graph=b / ug / 1e3, us_gpu=ub, us_per_layer_gpu=ub / L, GBs_gpu=b / ub / 1e3,
+                   frac_gpu=b / ub / 1e3 / PEAK_GBS, bytes=b)
     elif cfg in ("base", "small_preset", "hybrid"):
         # the reference's presets (scripts/run_lmeval.sh:94-153; innerq_amd.presets) at
         # the config-4 shape: a drop-in cache layer prefilled with 32k tokens (32 fp16
