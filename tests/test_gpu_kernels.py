@@ -155,6 +155,33 @@ def test_dequantize_dense_api(axis, mode):
     np.testing.assert_array_equal(got, ref)
 
 
+@pytest.mark.parametrize("D,T,layout", [
+    (128, 32768, "contiguous"),  # a prefill's prompt: the row kernel, 16-byte loads
+    (128, 4099, "token_stride"),  # every other token of a longer tensor, rows past a multiple of the lanes
+    (64, 1, "contiguous"),
+    (64, 777, "unaligned"),  # rows not 16-byte aligned: element loads
+    (96, 300, "contiguous"),  # head_dim outside {64, 128}: one thread per channel
+])
+def test_key_norm_factor_matches_numpy(D, T, layout):
+    """sqrt(max_t |k|) per (batch, head, channel) rounded to fp16 (cache.py:121-126),
+    bit for bit against numpy's float32 square root of the fp16 maxima, with an
+    infinity and a NaN planted (torch's and numpy's max propagate NaN)."""
+    B, H = 2, 3
+    x = synth.kv_tensor(B, H, 2 * T + 1, D + 1, seed=D + T, n_out=3, factor=9.0).astype(np.float16)
+    view = {"token_stride": np.s_[:, :, 1::2, :D], "unaligned": np.s_[:, :, :T, 1:]}.get(layout, np.s_[:, :, T + 1:, :D])
+    kn = x[view]  # a numpy view: the planted values land in x
+    kn[0, 1, min(5, T - 1), 7] = np.inf
+    kn[1, 2, T - 1, 3] = np.nan
+    k = f16t(x)[view]
+    if layout == "contiguous":
+        k = k.contiguous()
+    got = ops.key_norm_factor(k).cpu().numpy()
+    ref = np.sqrt(np.abs(kn).astype(np.float32).max(axis=2, keepdims=True)).astype(np.float16)
+    np.testing.assert_array_equal(np.isnan(got), np.isnan(ref))
+    ok = ~np.isnan(ref)
+    np.testing.assert_array_equal(got[ok].view(np.uint16), ref[ok].view(np.uint16))
+
+
 def test_key_normalized_store_dequant():
     B, H, T, D, G = 1, 2, 128, 128, 32
     x = special_input(B, H, T, D, seed=5)
