@@ -285,8 +285,10 @@ size_t iq_decode_workspace_bytes(int B, int Hq, int T, int D);
  * (TF/models/llama/modeling_llama.py:208), then p.V over V = [vs | vq | vr].
  * k[3] / v[3] are the sink, quantized and recent segments; the token counts of
  * K and V must each sum to T.  norm: optional fp16 [B,Hkv,D] key
- * normalization factor of the quantized K segment; the quantized V segment
- * may be a hybrid store (K: asym or sym).  out fp16 [B,Hq,D]
+ * normalization factor of the quantized K segment; either quantized segment
+ * may be a hybrid store (a hybrid K store with K and V of one group size
+ * only, key_quantize_mode='hybrid' of cache.py:92-98; else IQ_ERR_MODE).
+ * out fp16 [B,Hq,D]
  * (strides so_b, so_h).  Replaces update()'s dense read path (cache.py:278-281,
  * 395) plus the eager attention of TF/models/llama/modeling_llama.py:201-210.
  * A bf16 layer (LongBench/pred.py:240 loads the model in bf16): IQ_MODE_BF16

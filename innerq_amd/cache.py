@@ -340,21 +340,24 @@ class InnerqDynamicLayer(CacheLayerMixin):
 
     def _fused_refusal(self) -> Optional[str]:
         """Why attend() cannot read this layer's stores (None if it can): K must be
-        grouped along head_dim (asym or sym), V along tokens (asym, sym or hybrid), and
-        a bf16 layer's K and V of one group size."""
+        grouped along head_dim, V along tokens (each asym, sym or hybrid), and a bf16
+        layer's or a hybrid-K layer's K and V of one group size."""
         if (self.dtype == torch.bfloat16 and self._kq is not None and self._vq is not None
                 and self._kq.group != self._vq.group):
             return "fused decode of a bf16 layer needs K and V of one group size"
-        if self._kq is not None and (self._kq.axis != "channel" or self._kq.mode == QMode.HYBRID):
-            return "fused decode reads keys grouped along the head_dim axis, asym or sym"
+        if self._kq is not None and self._kq.axis != "channel":
+            return "fused decode reads keys grouped along the head_dim axis"
+        if (self._kq is not None and self._kq.mode == QMode.HYBRID and self._vq is not None
+                and self._kq.group != self._vq.group):
+            return "fused decode of hybrid keys needs K and V of one group size"
         if self._vq is not None and self._vq.axis != "token":
             return "fused decode reads values grouped along the token axis"
         return None
 
     def fused_decode_ready(self, key_states: torch.Tensor) -> bool:
         """Whether attend() can serve this step: one new token per sequence, a
-        prefilled layer, K grouped along head_dim (asym or sym) and V along tokens
-        (asym, sym or hybrid)."""
+        prefilled layer, K grouped along head_dim and V along tokens (asym, sym or
+        hybrid; hybrid K and bf16 layers with K and V of one group size)."""
         if not self.is_initialized or key_states.shape[-2] != 1:
             return False
         return self._fused_refusal() is None

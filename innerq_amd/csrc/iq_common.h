@@ -46,7 +46,8 @@ inline int check_store(int bits, int group, int mode) {
   return IQ_OK;
 }
 
-// a V store read by the attn.V GEMV / decode: asym, sym or hybrid
+// a V store read by the attn.V GEMV / decode, or a K store read by the
+// decode: asym, sym or hybrid
 inline int check_v_common(int bits, int group, int mode) {
   IQ_CHECK(bits_ok(bits), IQ_ERR_BITS);
   IQ_CHECK(group_ok(group), IQ_ERR_GROUP);

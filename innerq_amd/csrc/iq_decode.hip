@@ -862,7 +862,7 @@ int check_decode(const void* q, const iq_segment* k, const iq_segment* v, int B,
   if (k[1].n) {
     const iq_segment& g = k[1];
     IQ_CHECK(g.codes && g.meta, IQ_ERR_NULL);
-    if (int e = check_common(g.bits, g.group, base_mode(g.mode))) return e;
+    if (int e = check_v_common(g.bits, g.group, base_mode(g.mode))) return e;  // asym, sym or hybrid
     IQ_CHECK(D % g.group == 0, IQ_ERR_GROUP);
     // any store token may start the segment (a sliding window's start): the
     // fused range begins at the first token where K blocks and V groups align,
@@ -955,6 +955,8 @@ int launch_splits(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, c
   // bf16 layers: the fused kernel (K and V of one group size) and the dense
   // kernels; the unfused packed kernels take fp16 only
   if (c && !fused && bf) return IQ_ERR_MODE;
+  // hybrid K: the fused kernel (K and V of one group size) and the dense kernels
+  if (c && !fused && base_mode(k[1].mode) == IQ_MODE_HYBRID) return IQ_ERR_MODE;
   // The live slots of a row: at most one fused run per workgroup, then the
   // slices.  The fused kernel's grid (one workgroup per CU: far below the
   // limit) is worked out and checked before anything is launched.

@@ -197,6 +197,25 @@ __device__ __forceinline__ void meta_sz_hyb(uint32_t mw, float& s, float& z) {
   z = hyb_sym(mw) ? -float(1 << (BITS - 1)) * s : zh;
 }
 
+// {scale, zero} of a K token-group whose store form is known only at run
+// time (asym, sym or hybrid): the group is read as sym where its scale's
+// float class is in `cls` (meta_sym_classes: every class for a sym store,
+// none for asym, the negative ones for hybrid, whose flag is the scale's sign
+// bit, -0.0 included) and the scale is taken as |scale| (asym and sym scales
+// are never negative).  One compare more than meta_sz, no branch.
+template <int BITS, bool BF = false>
+__device__ __forceinline__ void meta_sz_rt(uint32_t mw, uint32_t sh, uint32_t cls, float& s, float& z) {
+  const float sr = act2f(uint16_t(mw >> sh), BF);
+  s = fabsf(sr);
+  const float zh = act2f(uint16_t(mw >> 16), BF);
+  z = __builtin_amdgcn_classf(sr, int(cls)) ? -float(1 << (BITS - 1)) * s : zh;
+}
+// float classes of v_cmp_class: bit 0 signaling NaN, 1 quiet NaN, 2 -inf,
+// 3 -normal, 4 -denormal, 5 -0, 6 +0, 7 +denormal, 8 +normal, 9 +inf
+__host__ __device__ constexpr uint32_t meta_sym_classes(int sym, int hyb) {
+  return hyb ? 0x3Cu : sym ? 0x3FFu : 0u;
+}
+
 // Workgroup barrier for data exchanged through LDS.  __syncthreads() would
 // also wait for every outstanding global load, i.e. for the next split's
 // prefetch; only the LDS writes need to be complete.
@@ -223,7 +242,9 @@ __device__ __forceinline__ float seg_sum(float v) {
 // softmax; each block's scaled logits (scale_log2 holds the plain scale) go to
 // the fp32 output at part (element strides sob, soh per batch and query head,
 // 1 per token).
-// VH: the V store is hybrid (per-group flag in its meta, meta_sz_hyb).
+// VH: the V store is hybrid (per-group flag in its meta, meta_sz_hyb).  A
+// hybrid K store (a.khyb: meta laid out as asym, the flag per group) is read
+// by the SM = 0 instances.
 // BF: a bf16 layer (query, key normalization factor, scales and zero points
 // in bf16): the query (times the factor, exact in fp32) goes into the hi/lo
 // fp16 query rows (QS) and the metadata decodes as bf16; the probabilities
@@ -258,6 +279,7 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS, AVO>::NT), (fused_waves_pe
   const int kms = ksym ? 2 : 4, vms = vsym ? 2 : 4;  // meta bytes per token / column
   const uint32_t kmv = meta_voff(lane, ksym), vmv = meta_voff(lane, vsym);
   const uint32_t ksh = meta_shift(lane, ksym), vsh = meta_shift(lane, vsym);
+  const uint32_t kcls = meta_sym_classes(ksym, a.khyb);  // SM == 0: the K groups read as sym
   const int64_t rows = int64_t(a.nitems / a.nsplit) * NREP;
 
   struct KRegs { uint32_t w[NG][FBPW][KW]; uint32_t m[NG][FBPW]; };
@@ -518,7 +540,8 @@ __global__ __launch_bounds__((FusedShape<G, NREP, QS, AVO>::NT), (fused_waves_pe
 #pragma unroll
           for (int j = 0; j < FBPW; ++j) {
             float s, z;
-            meta_sz<KB, BF>(kc.m[g][j], ksh, ksym, s, z);
+            if constexpr (SM == 0) meta_sz_rt<KB, BF>(kc.m[g][j], ksh, kcls, s, z);
+            else meta_sz<KB, BF>(kc.m[g][j], ksh, ksym, s, z);
 #pragma unroll
             for (int h = 0; h < NREP; ++h) {
               const float qs = __uint_as_float(sm.qrec[g][QOS + h]);
@@ -720,7 +743,7 @@ int fused_launch_kb(const FusedArgs& a, int vbits, int group, int D, int nrep, b
     // store modes known at compile time for groups of 32 at head_dim 128 (fp16
     // layers, K and V both asym or both sym): instance sm, else 0
     int sm = 0;
-    if constexpr (G == 32 && DD == 128 && !BF && !VH) sm = a.ksym == a.vsym ? 1 + (a.ksym != 0) : 0;
+    if constexpr (G == 32 && DD == 128 && !BF && !VH) sm = a.ksym == a.vsym && !a.khyb ? 1 + (a.ksym != 0) : 0;
     auto pick = [&]<int M>() {
       return BF     ? flash_fused_kernel<KB, VB, G, DD, R, true, false, false, VH, true>
              : norm ? flash_fused_kernel<KB, VB, G, DD, R, true, false, false, VH, false, M>

@@ -40,6 +40,7 @@ int flash_fused_launch(const void* q, int64_t sq_b, int64_t sq_h, const void* no
   a.q = (const uint16_t*)q; a.sqb = sq_b; a.sqh = sq_h; a.norm = (const uint16_t*)norm;
   a.kc = k.codes; a.km = k.meta; a.k_cap_blocks = k.t_cap / TOKEN_BLOCK; a.kblk0 = k.t0 / TOKEN_BLOCK;
   a.ksym = kmode == IQ_MODE_SYM;
+  a.khyb = kmode == IQ_MODE_HYBRID;  // meta as asym ({scale | flag << 15, zero})
   a.vc = v.codes; a.vm = v.meta; a.v_cap_groups = v.t_cap / v.group; a.vg0 = v.t0 / v.group;
   a.vsym = vmode == IQ_MODE_SYM;
   a.Hkv = Hkv; a.T = T;
@@ -56,7 +57,6 @@ int flash_fused_launch(const void* q, int64_t sq_b, int64_t sq_h, const void* no
   a.ml = ml; a.part = part;
   a.empty_stats = grid ? 0 : 1;  // a caller that takes the workgroup count reads only the run slots
   a.pair_e0 = fused_pair_e0(k.bits, v.bits, vmode == IQ_MODE_HYBRID);
-  if (kmode == IQ_MODE_HYBRID) return IQ_ERR_MODE;
   const bool nm = norm != nullptr;
   if (bf) {
     const bool vh = vmode == IQ_MODE_HYBRID;

@@ -556,6 +556,7 @@ struct FusedArgs {
   // launch's workgroup count reads only the run slots)
   int empty_stats;
   int pair_e0;  // the partition (ShareMap e0_num; 0: plain)
+  int khyb;     // 1: a hybrid K store (meta as asym, the group's flag picks sym)
 };
 // its launch per K bit width (iq_flash_k{2,3,4}.hip)
 int flash_fused_launch_k2(const FusedArgs& a, int vbits, int group, int D, int nrep, bool norm, int* grid,

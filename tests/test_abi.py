@@ -168,9 +168,13 @@ def test_decode_rejects():
     seg[1].codes, seg[1].meta, seg[1].t_cap, seg[1].bits, seg[1].group, seg[1].mode = 0x1000, 0x1000, 64, 7, 32, 0
     assert lib.iq_decode_attention(FAKE, 1, 1, None, seg, vseg, 1, 32, 8, 10, 128, 1.0, FAKE, 1, 1, FAKE, 1 << 30,
                                    None) == -2
-    # a hybrid store on the K side is refused (V side only)
+    # a hybrid K store is read by the fused kernel only (K and V of one group
+    # size): with V groups of 64 it is refused before any launch
+    seg[0].n, seg[1].n = 0, 64
     seg[1].bits, seg[1].mode = 4, 2
-    assert lib.iq_decode_attention(FAKE, 1, 1, None, seg, vseg, 1, 32, 8, 10, 128, 1.0, FAKE, 1, 1, FAKE, 1 << 30,
+    vseg[0].n, vseg[1].n = 0, 64
+    vseg[1].codes, vseg[1].meta, vseg[1].t_cap, vseg[1].bits, vseg[1].group, vseg[1].mode = 0x1000, 0x1000, 64, 4, 64, 1
+    assert lib.iq_decode_attention(FAKE, 1, 1, None, seg, vseg, 1, 32, 8, 64, 128, 1.0, FAKE, 1, 1, FAKE, 1 << 30,
                                    None) == -7
 
 

@@ -6,7 +6,9 @@ the windows, K flushes its oldest token, V its oldest 32 each step until its
 window drains to 3) and attend() over [sinks | packed | windows].  That step
 runs the fused kernel's key-normalized instances (hi/lo query rows) over 3-bit
 sym K and 3-bit sym / 2-bit sym / 2-bit hybrid V, and the merging dense kernel
-over a window whose V rows are partly packed.
+over a window whose V rows are partly packed.  "hybrid_k" is innerq_hybrid with
+3-bit hybrid K as well (key_quantize_mode='hybrid', which the reference accepts,
+cache.py:92-98, and no preset uses).
 
 References:
 * every head: fp32 attention over the layer's fp32 [sink | dequantized (times
@@ -40,11 +42,19 @@ def _err(got, ref):
     return ((got.double() - ref.double()).abs().max() / ref.double().abs().max()).item()
 
 
-@pytest.mark.parametrize("name", ["innerq_base", "innerq_small", "innerq_hybrid"])
+def _config(name):
+    """A preset's config; "hybrid_k": innerq_hybrid with hybrid keys as well
+    (key_quantize_mode='hybrid', cache.py:92-98; no reference preset uses it)."""
+    if name == "hybrid_k":
+        return presets.preset_config("innerq_hybrid", key_quantize_mode="hybrid")
+    return presets.preset_config(name)
+
+
+@pytest.mark.parametrize("name", ["innerq_base", "innerq_small", "innerq_hybrid", "hybrid_k"])
 def test_preset_decode_full_size(name):
     B, Hkv, nrep, T, D, steps = 8, 8, 4, 32768, 128, 3
     print(f"preset {name}: B={B} Hkv={Hkv} T={T}", flush=True)
-    cfg = presets.preset_config(name)
+    cfg = _config(name)
     gen = torch.Generator(device=DEV).manual_seed(sum(map(ord, name)))
 
     def kv(n):
@@ -60,6 +70,7 @@ def test_preset_decode_full_size(name):
         layer.append(k[:, :, T + i:T + i + 1], v[:, :, T + i:T + i + 1])
     assert layer._kq.length == T - 128 + steps and layer.keys_recent.shape[2] == 96
     assert layer._vq.length == T + steps - 32 - 3 and layer.values_recent.shape[2] == 3
+    assert layer.fused_decode_ready(k[:, :, :1])
     got = layer.attend(q, D ** -0.5)[:, :, 0]
     torch.cuda.synchronize()
 
@@ -97,7 +108,7 @@ def test_preset_decode_full_size(name):
         assert e < TOL
 
 
-@pytest.mark.parametrize("name", ["innerq_base", "innerq_hybrid"])
+@pytest.mark.parametrize("name", ["innerq_base", "innerq_hybrid", "hybrid_k"])
 def test_preset_decode_full_size_bf16(name):
     """The same decode step of a bf16 layer (the model in bf16, LongBench/pred.py:240):
     every head against fp32 attention over the layer's fp32 dequantized K and V
@@ -106,7 +117,7 @@ def test_preset_decode_full_size_bf16(name):
     max-normwise beyond that rounding (2^-8 |ref| elementwise)."""
     B, Hkv, nrep, T, D, steps = 8, 8, 4, 32768, 128, 3
     print(f"preset {name} bf16: B={B} Hkv={Hkv} T={T}", flush=True)
-    cfg = presets.preset_config(name)
+    cfg = _config(name)
     gen = torch.Generator(device=DEV).manual_seed(7 + sum(map(ord, name)))
 
     def kv(n):

@@ -15,7 +15,7 @@ import numpy as np
 import pytest
 import torch
 
-from innerq_amd import ops, synth
+from innerq_amd import _lib, ops, synth
 from oracle import attn_ref as A
 from oracle import quant_ref as Q
 
@@ -195,6 +195,61 @@ def test_hybrid_decode_attention_segments(kmode, vbits):
                          Q.dequantize_tokendim_hybrid(*Q.quantize_tokendim_hybrid(vx[:, :, vs:vs + vq], G, vbits), G),
                          vx[:, :, vs + vq:].astype(np.float32)], axis=2)
     assert A.rel_err(got, A.decode_attention(q, kd, vd, D ** -0.5, p_dtype=None)) < TOL
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("vmode", ["asymmetric", "symmetric", "hybrid"])
+@pytest.mark.parametrize("kbits,G", [(2, 32), (3, 32), (4, 32), (3, 64)])
+def test_hybrid_k_decode_attention_segments(vmode, kbits, G):
+    """[sink | packed | recent] with a hybrid K store (key_quantize_mode='hybrid',
+    cache.py:92-98; K groups of both kinds): the fused kernel reads each K group
+    as its flag says, the dense kernel the K rows packed in K only."""
+    B, Hkv, nrep, D = 2, 2, 4, 128
+    ks, kq, kr = 32, 1280 - 32 - 96, 96
+    T = ks + kq + kr
+    vs = 32
+    vq = (T - vs - 64) // G * G
+    vr = T - vs - vq
+    kx = _mixed_v(B, Hkv, T, D, seed=41 + kbits + G)
+    vx = _mixed_v(B, Hkv, T, D, seed=42)
+    kst = _store(kx[:, :, ks:ks + kq], "channel", kbits, G)
+    kc, ksc, kz = Q.quantize_channeldim_hybrid(kx[:, :, ks:ks + kq], G, kbits)
+    assert 0 < ksc["mask"].mean() < 1
+    kdq = Q.dequantize_channeldim_hybrid(kc, ksc, kz, G)
+    np.testing.assert_array_equal(kst.dequant(dtype=torch.float32).cpu().numpy() + np.float32(0),
+                                  kdq.astype(np.float32) + np.float32(0))
+    vpart = vx[:, :, vs:vs + vq]
+    if vmode == "hybrid":
+        vst = _store(vpart, "token", 2, G)
+        vdq = Q.dequantize_tokendim_hybrid(*Q.quantize_tokendim_hybrid(vpart, G, 2), G)
+    else:
+        vst = ops.PackedStore("token", B, Hkv, D, G, 4, vmode, DEV)
+        vst.append(_f16t(vpart))
+        qv = Q.quantize_tokendim_sym if vmode == "symmetric" else Q.quantize_tokendim_asym
+        dv = Q.dequantize_tokendim_sym if vmode == "symmetric" else Q.dequantize_tokendim_asym
+        vdq = dv(*qv(vpart, G, 4), G)
+    q = synth.normal((B, Hkv * nrep, D), seed=43).astype(np.float16)
+    kxt, vxt = _f16t(kx), _f16t(vx)
+    got = ops.decode_attention(_f16t(q), kxt[:, :, :ks], kst, kxt[:, :, ks + kq:], vxt[:, :, :vs], vst,
+                               vxt[:, :, vs + vq:], D ** -0.5).cpu().numpy().astype(np.float64)
+    kd = np.concatenate([kx[:, :, :ks].astype(np.float32), kdq, kx[:, :, ks + kq:].astype(np.float32)], axis=2)
+    vd = np.concatenate([vx[:, :, :vs].astype(np.float32), vdq, vx[:, :, vs + vq:].astype(np.float32)], axis=2)
+    assert A.rel_err(got, A.decode_attention(q, kd, vd, D ** -0.5, p_dtype=None)) < TOL
+
+
+@pytest.mark.gpu
+def test_hybrid_k_needs_one_group_size():
+    """A hybrid K store is read by the fused kernel only, which takes K and V of
+    one group size: K groups of 32 with V groups of 64 are refused (no launch)."""
+    B, Hkv, D, T = 1, 2, 128, 256
+    kx = _mixed_v(B, Hkv, T, D, seed=44)
+    kst = _store(kx, "channel", 3, 32)
+    vst = ops.PackedStore("token", B, Hkv, D, 64, 4, "symmetric", DEV)
+    vst.append(_f16t(kx))
+    q = synth.normal((B, Hkv * 4, D), seed=45).astype(np.float16)
+    with pytest.raises(_lib.IQError) as e:
+        ops.decode_attention(_f16t(q), None, kst, None, None, vst, None, D ** -0.5)
+    assert e.value.status == -7  # IQ_ERR_MODE
 
 
 @pytest.mark.gpu
