@@ -5,11 +5,13 @@ Registers the attention implementation ``"innerq_fused"``
 ``attn_implementation="innerq_fused"`` whose generation cache is the drop-in
 ``DynamicCache`` (``InnerqLlamaForCausalLM`` builds it) decodes each new token
 with ``InnerqDynamicLayer.attend()``: QK^T, softmax and attn.V over the packed
-K and V (``iq_decode_attention``), with no dense K/V in between.  The
-reference instead dequantizes the whole cache in ``update()`` and runs the
-model's attention over it (src/innerq/cache.py:242-270,
-TF/models/llama/modeling_llama.py:201-210); prefill, padded batches and
-layouts the fused kernels do not take keep that path.
+K and V (``iq_decode_attention``), with no dense K/V in between.  A padding
+mask that hides a prefix of each sequence (left padding, as generate() pads a
+batch) becomes per-sequence start tokens of that call.  The reference instead
+dequantizes the whole cache in ``update()`` and runs the model's attention
+over it (src/innerq/cache.py:242-270, TF/models/llama/modeling_llama.py:201-210);
+prefill, other mask patterns and layouts the fused kernels do not take keep
+that path.
 """
 from __future__ import annotations
 
@@ -30,21 +32,34 @@ from .cache import FUSED_ATTENTION
 # edit, so a mask object reused and edited between passes is read again; the
 # weak reference keeps no mask alive, and a different mask (another model's,
 # another pass's) is a different object.
-_last_mask: list = [None, -1, False]
+_last_mask: list = [None, -1, None]
 
 
-def _masks_tokens(attention_mask) -> bool:
-    """Whether the mask hides any cache token (padding): the fused kernels attend
-    to every token."""
+def _hidden_prefix(attention_mask):
+    """What the mask hides of the cache tokens its last query row covers: None
+    (nothing), the per-sequence counts of leading tokens it hides when each row
+    hides a prefix and nothing else (left padding; the fused kernels start each
+    sequence there), or False (any other pattern: the dense path)."""
     if attention_mask is None:
-        return False
+        return None
     ref, ver, ans = _last_mask
     if ref is not None and ref() is attention_mask and ver == attention_mask._version:
         return ans
-    if attention_mask.dtype == torch.bool:
-        ans = not bool(attention_mask.all())
-    else:
-        ans = bool((attention_mask < 0).any())
+    m = attention_mask
+    hide = ~m if m.dtype == torch.bool else m < 0
+    ans = False
+    if hide.dim() == 4:
+        last = hide[:, :, -1, :]                       # [B, heads or 1, kv]
+        n = last.shape[-1]
+        same = (last == last[:, :1]).all()             # every head row alike
+        row = last[:, 0]
+        count = row.sum(-1)
+        lead = row.to(torch.int32).cumprod(-1).sum(-1)  # leading hidden tokens
+        ok = same & (count == lead).all() & (count < n).all()
+        vals = torch.cat([ok.reshape(1).to(torch.int64), count.to(torch.int64)]).tolist()  # one read
+        if vals[0]:
+            pads = vals[1:]
+            ans = pads if any(pads) else None
     _last_mask[:] = [weakref.ref(attention_mask), attention_mask._version, ans]
     return ans
 
@@ -63,12 +78,16 @@ def innerq_fused_attention(module, query, key, value, attention_mask, dropout: f
     if scaling is None:
         scaling = query.shape[-1] ** -0.5
     nrep = query.shape[1] // key.shape[1]
-    if (_masks_tokens(attention_mask) or dropout or query.dtype != layer.dtype or query.shape[-1] not in (64, 128)
+    pads = _hidden_prefix(attention_mask)
+    if pads is not None and (pads is False or attention_mask.shape[-1] != layer.attend_length()
+                             or len(pads) != query.shape[0]):
+        pads = False  # a mask over other columns than the tokens attend() reads
+    if (pads is False or dropout or query.dtype != layer.dtype or query.shape[-1] not in (64, 128)
             or nrep not in (1, 2, 4, 8) or query.shape[1] != nrep * key.shape[1]):
         k, v = layer.get_deq_tensors()
         return sdpa_attention_forward(module, query, k, v, attention_mask, dropout=dropout, scaling=scaling,
                                       **kwargs)
-    out = layer.attend(query, scaling)  # [B, Hq, 1, D]
+    out = layer.attend(query, scaling, pads)  # [B, Hq, 1, D]
     return out.transpose(1, 2).contiguous(), None
 
 

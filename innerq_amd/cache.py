@@ -21,7 +21,7 @@ recent] in one gfx950 decode kernel chain (ops.decode_attention).
 from __future__ import annotations
 
 from collections.abc import Iterable
-from typing import Any, Optional
+from typing import Any, Optional, Sequence
 
 import torch
 from transformers.cache_utils import Cache, CacheLayerMixin
@@ -362,11 +362,25 @@ class InnerqDynamicLayer(CacheLayerMixin):
             return False
         return self._fused_refusal() is None
 
-    def attend(self, query_states: torch.Tensor, scaling: float) -> torch.Tensor:
+    def attend(self, query_states: torch.Tensor, scaling: float, pads: Optional[Sequence[int]] = None
+               ) -> torch.Tensor:
         """Decode attention of one new token per sequence over this layer's cache:
         softmax(q K^T * scaling, fp32) -> @ V (TF/models/llama/modeling_llama.py:201-210), with
         K and V read packed.  query_states [B, Hq, 1, D] in the layer's dtype (fp16 or bf16)
-        -> [B, Hq, 1, D] of that dtype."""
+        -> [B, Hq, 1, D] of that dtype.  pads: per sequence, how many of its first
+        tokens a padding mask hides (left padding; None: none)."""
+        self._check_attend(query_states)
+        return self._attend_rows(query_states[:, :, 0], scaling, self._attend_start(), pads)[:, :, None]
+
+    def _attend_start(self) -> int:
+        """The first token attend() reads (0: all of them)."""
+        return 0
+
+    def attend_length(self) -> int:
+        """How many tokens attend() reads: the columns of a decode step's mask."""
+        return self._n_tokens() - self._attend_start()
+
+    def _check_attend(self, query_states: torch.Tensor) -> None:
         if query_states.dim() != 4 or query_states.shape[2] != 1:
             raise ValueError("attend() takes one query token per sequence: [B, Hq, 1, D]")
         if not self.is_initialized:
@@ -374,25 +388,56 @@ class InnerqDynamicLayer(CacheLayerMixin):
         why = self._fused_refusal()
         if why is not None:
             raise NotImplementedError(why)
-        return self._attend_from(query_states[:, :, 0], scaling, 0)[:, :, None]
 
-    def _attend_from(self, q: torch.Tensor, scaling: float, s0: int) -> torch.Tensor:
+    def _n_tokens(self) -> int:
+        return self.keys_sink.shape[-2] + (self._kq.length if self._kq is not None else 0) + \
+            self.keys_recent.shape[-2]
+
+    def _attend_rows(self, q: torch.Tensor, scaling: float, s0: int,
+                     pads: Optional[Sequence[int]]) -> torch.Tensor:
+        """Sequence b attends to tokens [s0 + pads[b], T): one decode call over the
+        whole batch without padding, else one per run of consecutive sequences of
+        the same start, over batch views of the layer."""
+        if pads is None or not any(pads):
+            return self._attend_from(q, scaling, s0)
+        B, n = q.shape[0], self._n_tokens() - s0
+        pads = [int(p) for p in pads]
+        if len(pads) != B or min(pads) < 0 or max(pads) >= n:
+            raise ValueError(f"attend(): pads must give 0 <= pad < {n} for each of the {B} sequences, got {pads}")
+        out = torch.empty_like(q)
+        b0 = 0
+        while b0 < B:
+            b1 = b0 + 1
+            while b1 < B and pads[b1] == pads[b0]:
+                b1 += 1
+            out[b0:b1] = self._attend_from(q[b0:b1], scaling, s0 + pads[b0], (b0, b1))
+            b0 = b1
+        return out
+
+    def _attend_from(self, q: torch.Tensor, scaling: float, s0: int,
+                     rows: Optional[tuple] = None) -> torch.Tensor:
         """decode_attention over this layer's tokens [s0, cumulative_length): the
-        parts of [sink | packed | recent] of K and of V from token s0 on."""
+        parts of [sink | packed | recent] of K and of V from token s0 on (of the
+        sequences [rows[0], rows[1]) when rows is given, q holding theirs)."""
+        def part_rows(x):
+            return x if rows is None else x[rows[0]:rows[1]]
+
         def parts(sink, quant, recent):
             ns = sink.shape[-2]
             nq = quant.length if quant is not None else 0
-            dense_sink = sink[:, :, s0:] if s0 < ns else None
+            dense_sink = part_rows(sink[:, :, s0:]) if s0 < ns else None
             t0 = min(max(s0 - ns, 0), nq)
             r0 = max(s0 - ns - nq, 0)
-            dense_recent = recent[:, :, r0:] if recent.shape[-2] > r0 else None
-            return dense_sink, (quant.store if quant is not None else None), t0, dense_recent
+            dense_recent = part_rows(recent[:, :, r0:]) if recent.shape[-2] > r0 else None
+            store = None
+            if quant is not None:
+                store = quant.store if rows is None else quant.store.batch_view(*rows)
+            return dense_sink, store, t0, dense_recent
 
         ks, kst, kt0, kr = parts(self.keys_sink, self._kq, self.keys_recent)
         vs, vst, vt0, vr = parts(self.values_sink, self._vq, self.values_recent)
-        return ops.decode_attention(q, ks, kst, kr, vs, vst, vr, scaling,
-                                    norm=self.key_normalization_factor if self._kq is not None else None,
-                                    k_t0=kt0, v_t0=vt0)
+        norm = part_rows(self.key_normalization_factor) if self._kq is not None else None
+        return ops.decode_attention(q, ks, kst, kr, vs, vst, vr, scaling, norm=norm, k_t0=kt0, v_t0=vt0)
 
     def get_mask_sizes(self, query_length) -> tuple[int, int]:
         """(kv_length, kv_offset); takes the query length (transformers >= 5.15) or
@@ -467,22 +512,19 @@ class InnerqDynamicSlidingWindowLayer(InnerqDynamicLayer):
             return False
         return self._fused_refusal() is None
 
-    def attend(self, query_states: torch.Tensor, scaling: float) -> torch.Tensor:
+    def attend(self, query_states: torch.Tensor, scaling: float, pads: Optional[Sequence[int]] = None
+               ) -> torch.Tensor:
         """Decode attention over the last min(T, w) tokens of the layer (T the tokens
         so far, this step's included): the window update() returns with
         fix_sliding_window on (w - 1 + q tokens of a q = 1 call once the past
-        reaches w), read packed."""
+        reaches w), read packed; pads count from the window's first token."""
         if not self.fix_sliding_window:
             raise NotImplementedError("attend() of a sliding-window layer needs fix_sliding_window = True")
-        if query_states.dim() != 4 or query_states.shape[2] != 1:
-            raise ValueError("attend() takes one query token per sequence: [B, Hq, 1, D]")
-        if not self.is_initialized:
-            raise RuntimeError("attend() needs a prefilled cache")
-        why = self._fused_refusal()
-        if why is not None:
-            raise NotImplementedError(why)
-        s0 = max(self.cumulative_length - self.sliding_window, 0)
-        return self._attend_from(query_states[:, :, 0], scaling, s0)[:, :, None]
+        self._check_attend(query_states)
+        return self._attend_rows(query_states[:, :, 0], scaling, self._attend_start(), pads)[:, :, None]
+
+    def _attend_start(self) -> int:
+        return max(self.cumulative_length - self.sliding_window, 0)
 
     def get_mask_sizes(self, query_length) -> tuple[int, int]:
         if isinstance(query_length, torch.Tensor):

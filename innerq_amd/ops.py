@@ -6,6 +6,7 @@ path: a CPU tensor or a missing library raises.
 """
 from __future__ import annotations
 
+import copy
 import ctypes
 from typing import Optional, Sequence
 
@@ -233,6 +234,19 @@ class PackedStore:
         cv[:, ou:].zero_()
         mv[:, ou:].zero_()
         self.codes, self.meta, self.t_cap = codes, meta, new_cap
+
+    def batch_view(self, b0: int, b1: int) -> "PackedStore":
+        """Sequences [b0, b1) of this store as a store of B = b1 - b0 that shares its
+        memory (a read view: a reserve() or append() through either reaches only
+        that object's own tensors)."""
+        if not 0 <= b0 < b1 <= self.B:
+            raise ValueError(f"batch_view: [{b0}, {b1}) is not a range of the store's {self.B} sequences")
+        v = copy.copy(self)
+        v.B = b1 - b0
+        if self.t_cap:
+            v.codes = self.codes.view(self.B, -1)[b0:b1].reshape(-1)
+            v.meta = self.meta.view(self.B, -1)[b0:b1].reshape(-1)
+        return v
 
     def nbytes(self, n_tokens: Optional[int] = None) -> int:
         """Packed code + metadata bytes of ``n_tokens`` (default: length) tokens."""

@@ -151,18 +151,43 @@ def test_mask_answer_follows_in_place_edits():
     import torch
     from innerq_amd import attention as att
     m = torch.zeros(2, 1, 1, 8)  # additive mask: 0 = attend
-    assert att._masks_tokens(m) is False
-    assert att._masks_tokens(m) is False  # cached
+    assert att._hidden_prefix(m) is None
+    assert att._hidden_prefix(m) is None  # cached
     m[1, 0, 0, :3] = float("-inf")        # padding added in place
-    assert att._masks_tokens(m) is True
+    assert att._hidden_prefix(m) == [0, 3]
     m.zero_()
-    assert att._masks_tokens(m) is False
+    assert att._hidden_prefix(m) is None
     b = torch.ones(1, 1, 1, 8, dtype=torch.bool)
-    assert att._masks_tokens(b) is False
+    assert att._hidden_prefix(b) is None
     b[0, 0, 0, 0] = False
-    assert att._masks_tokens(b) is True
+    assert att._hidden_prefix(b) == [1]
     r = weakref.ref(b)
     del b
     gc.collect()
     assert r() is None
-    assert att._masks_tokens(None) is False
+    assert att._hidden_prefix(None) is None
+
+
+def test_mask_hidden_prefix_patterns():
+    """Left padding (a hidden prefix per sequence, nothing else) gives the
+    per-sequence start tokens the fused kernels take; a hole after the first
+    attended token, a fully hidden row, or head rows that differ give False
+    (the dense path).  The last query row decides (a decode step's mask)."""
+    import torch
+    from innerq_amd import attention as att
+    b = torch.ones(3, 1, 2, 10, dtype=torch.bool)
+    b[0, :, :, :4] = False
+    b[2, :, :, :1] = False
+    b[:, :, 0, :] = False                  # earlier query rows do not matter
+    assert att._hidden_prefix(b) == [4, 0, 1]
+    hole = b.clone()
+    hole[1, :, -1, 6] = False              # a hidden token after attended ones
+    assert att._hidden_prefix(hole) is False
+    full = b.clone()
+    full[1, :, -1, :] = False              # every token hidden
+    assert att._hidden_prefix(full) is False
+    f = torch.zeros(2, 4, 1, 6)
+    f[0, :, :, :2] = torch.finfo(torch.float32).min
+    assert att._hidden_prefix(f) == [2, 0]
+    f[0, 3, :, 2] = torch.finfo(torch.float32).min  # one head row differs
+    assert att._hidden_prefix(f) is False

@@ -148,6 +148,33 @@ def test_cache_attend_matches_dense_attention(cache_golden, name, nrep):
             assert A.rel_err(_np(out[:, :, 0]).astype(np.float64), ref) < 1e-3, f"step {s + 1}"
 
 
+@pytest.mark.parametrize("name", ["innerq_base", "innerq_hybrid"])
+@pytest.mark.parametrize("pads", [(0, 37, 300, 0), (5, 5, 700, 690)])
+def test_cache_attend_with_padding(name, pads):
+    """attend() with a padding mask's hidden prefix per sequence (left padding):
+    sequence b attends to tokens [pads[b], T) only, the batch split into runs of
+    one start (one decode call each, over batch views of the stores); starts in
+    the sinks, the packed range and the recent window.  Each sequence within 1e-3
+    of float64 attention over its own tokens of the layer's dequantized K and V."""
+    from innerq_amd import presets
+    B, H, nrep, D, T = 4, 2, 4, 128, 760
+    layer = C.InnerqDynamicLayer(presets.preset_config(name), 0)
+    kx = synth.kv_tensor(B, H, T + 3, D, seed=61, n_out=4, factor=8.0)
+    vx = synth.kv_tensor(B, H, T + 3, D, seed=62, n_out=4, factor=8.0)
+    kt, vt = torch.from_numpy(kx).to(DEV), torch.from_numpy(vx).to(DEV)
+    layer.update(kt[:, :, :T], vt[:, :, :T])
+    for i in range(3):
+        layer.append(kt[:, :, T + i:T + i + 1], vt[:, :, T + i:T + i + 1])
+    q = synth.normal((B, H * nrep, D), seed=63).astype(np.float16)
+    out = layer.attend(torch.from_numpy(q).to(DEV)[:, :, None], D ** -0.5, pads=list(pads))[:, :, 0]
+    K, V = _np(layer.get_keys_deq().float()), _np(layer.get_values_deq().float())
+    for b, p in enumerate(pads):
+        ref = A.decode_attention(q[b:b + 1], K[b:b + 1, :, p:], V[b:b + 1, :, p:], D ** -0.5, None)
+        assert A.rel_err(_np(out[b:b + 1]).astype(np.float64), ref) < 1e-3, f"sequence {b}, pad {p}"
+    with pytest.raises(ValueError):
+        layer.attend(torch.from_numpy(q).to(DEV)[:, :, None], D ** -0.5, pads=[0, 0, 0, T + 3])
+
+
 def test_cache_state_views_match_quantizer():
     """keys_q / keys_scale_factor / keys_zp_sign and values_* unpack to quant.py's tensors."""
     cfg = Cfg(k_bits=4, v_bits=3, key_flush_size=1, value_flush_size=64, key_group_size=32, value_group_size=64,
@@ -240,6 +267,38 @@ def test_fused_attention_in_llama_matches_reference_path(preset, monkeypatch):
     assert ((got - ref).abs().max() / ref.abs().max()).item() < 2e-2
     # every decode step of both layers went through attend()
     assert calls[0] == 2 * dec.shape[1]
+
+
+def test_fused_attention_padded_batch(monkeypatch):
+    """A left-padded batch (pads 0, 17 and 60 of a 150-token prefill; the mask
+    hides each sequence's prefix) teacher-forced through 12 decode steps: every
+    decode step of both layers goes through attend() with per-sequence start
+    tokens, and the logits match those of the reference's path with sdpa (same
+    prefill: both run it through sdpa with the mask) on every sequence."""
+    model = _tiny_llama("innerq_base")
+    gen = torch.Generator(device=DEV).manual_seed(11)
+    B, T0, steps = 3, 150, 12
+    ids = torch.randint(0, 64, (B, T0), generator=gen, device=DEV)
+    dec = torch.randint(0, 64, (B, steps), generator=gen, device=DEV)
+    mask = torch.ones(B, T0 + steps, dtype=torch.long, device=DEV)
+    for b, p in enumerate((0, 17, 60)):
+        mask[b, :p] = 0
+    logits = {}
+    calls = _count_attend(monkeypatch)
+    for attn in ("sdpa", "innerq_fused"):
+        model.config._attn_implementation = attn
+        cache = C.DynamicCache(config=model.config)
+        out = []
+        with torch.no_grad():
+            model(ids, attention_mask=mask[:, :T0], past_key_values=cache, use_cache=True)
+            for t in range(steps):
+                out.append(model(dec[:, t:t + 1], attention_mask=mask[:, :T0 + t + 1], past_key_values=cache,
+                                 use_cache=True).logits[:, -1].float())
+        logits[attn] = torch.stack(out)
+    ref, got = logits["sdpa"], logits["innerq_fused"]
+    assert torch.isfinite(got).all()
+    assert ((got - ref).abs().max() / ref.abs().max()).item() < 2e-2
+    assert calls[0] == 2 * steps
 
 
 def test_fused_attention_generate(monkeypatch):
@@ -470,4 +529,44 @@ def test_mistral_decodes_past_the_window_through_attend(monkeypatch):
     assert calls[0] == 2 * 30
     err = ((got - ref).abs().max() / ref.abs().max()).item()
     print(f"mistral fused vs eager past the window: {err:.2e}")
+    assert err < 2e-2
+
+
+def test_mistral_padded_batch_through_attend(monkeypatch):
+    """A left-padded batch (pads 0 and 10 of a 40-token prefill) on the Mistral
+    with the fix, under the fused attention: every decode step of both sliding
+    layers goes through attend(), with per-sequence starts while the window
+    still covers the padding and none once it has slid past; the step logits
+    match the sdpa path on the same cache type with the same mask."""
+    gen = torch.Generator(device=DEV).manual_seed(5)
+    B, T0, steps = 2, 40, 30
+    ids = torch.randint(0, 64, (B, T0), generator=gen, device=DEV)
+    dec = torch.randint(0, 64, (B, steps), generator=gen, device=DEV)
+    mask = torch.ones(B, T0 + steps, dtype=torch.long, device=DEV)
+    mask[1, :10] = 0
+    model = _tiny_mistral(SLIDING["sliding_sym3_sinks"])
+    calls = [0]
+    orig = C.InnerqDynamicSlidingWindowLayer.attend
+
+    def attend(self, *a, **kw):
+        calls[0] += 1
+        return orig(self, *a, **kw)
+
+    monkeypatch.setattr(C.InnerqDynamicSlidingWindowLayer, "attend", attend)
+    logits = {}
+    for attn in ("sdpa", "innerq_fused"):
+        model.config._attn_implementation = attn
+        cache = C.DynamicCache(config=model.config)
+        out = []
+        with torch.no_grad():
+            model(ids, attention_mask=mask[:, :T0], past_key_values=cache, use_cache=True)
+            for t in range(steps):
+                out.append(model(dec[:, t:t + 1], attention_mask=mask[:, :T0 + t + 1], past_key_values=cache,
+                                 use_cache=True).logits[:, -1].float())
+        logits[attn] = torch.stack(out)
+    assert calls[0] == 2 * steps
+    ref, got = logits["sdpa"], logits["innerq_fused"]
+    assert torch.isfinite(got).all()
+    err = ((got - ref).abs().max() / ref.abs().max()).item()
+    print(f"mistral padded fused vs sdpa: {err:.2e}")
     assert err < 2e-2

@@ -129,3 +129,23 @@ def test_version_1_blob_claiming_bf16_is_refused():
     md = json.loads(blob[8:8 + n])["__metadata__"]
     with pytest.raises(ValueError):
         ops.PackedStore.from_bytes(save(load(blob), metadata=dict(md, version="1")), "cpu")
+
+
+@pytest.mark.parametrize("axis", ["channel", "token"])
+def test_batch_view_shares_the_sequences_memory(axis):
+    """batch_view(b0, b1): the stores of sequences [b0, b1) as a B = b1 - b0 store
+    over the same memory (what a padded batch's per-start decode calls read)."""
+    st = ops.PackedStore(axis, 3, 2, 128, 32, 4, "asymmetric", "cpu", t_cap=128)
+    st.codes.copy_(torch.arange(st.codes.numel(), dtype=torch.int32))
+    st.meta.copy_(torch.arange(st.meta.numel(), dtype=torch.int32).to(torch.int16))
+    st.length = 96
+    v = st.batch_view(1, 3)
+    assert (v.B, v.H, v.t_cap, v.length, v.mode) == (2, 2, st.t_cap, 96, st.mode)
+    assert torch.equal(v.codes, st.codes.view(3, -1)[1:].reshape(-1))
+    assert torch.equal(v.meta, st.meta.view(3, -1)[1:].reshape(-1))
+    assert v.codes.data_ptr() == st.codes.data_ptr() + st.codes.numel() // 3 * 4
+    assert v.nbytes() == st.nbytes() * 2 // 3
+    with pytest.raises(ValueError):
+        st.batch_view(2, 2)
+    empty = ops.PackedStore(axis, 3, 2, 128, 32, 4, "symmetric", "cpu")
+    assert empty.batch_view(0, 1).B == 1
