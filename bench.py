@@ -25,8 +25,10 @@ attention) on a sample of the same workload, timed on host cores
 
     python bench.py [--gpus 1] [--steps 100] [--warmup 10]
     python bench.py --config {H,1,2,3,4}    other BASELINE configs (not the headline line)
-    python bench.py --config {base,small_preset,hybrid}
+    python bench.py --config {base,small_preset,hybrid,hybrid_k,base_padded}
                                             the reference's presets at the config-4 shape
+                                            (hybrid_k: innerq_hybrid with hybrid keys too;
+                                            base_padded: innerq_base, a left-padded batch)
 """
 from __future__ import annotations
 
@@ -368,7 +370,7 @@ def bench_config(args):
         res.update(us=us, us_per_layer=us / L, GBs=b / us / 1e3, us_graph=ug, us_per_layer_graph=ug / L,
                    GBs_graph=b / ug / 1e3, us_gpu=ub, us_per_layer_gpu=ub / L, GBs_gpu=b / ub / 1e3,
                    frac_gpu=b / ub / 1e3 / PEAK_GBS, bytes=b)
-    elif cfg in ("base", "small_preset", "hybrid"):
+    elif cfg in ("base", "small_preset", "hybrid", "hybrid_k", "base_padded"):
         # the reference's presets (scripts/run_lmeval.sh:94-153; innerq_amd.presets) at
         # the config-4 shape: a drop-in cache layer prefilled with 32k tokens (32 fp16
         # sinks, 32640 packed, 96 recent per role), then decode steps of the product
@@ -379,7 +381,12 @@ def bench_config(args):
         # every layer.  Store capacity is reserved before timing (no reallocation).
         from innerq_amd import cache as IC
         from innerq_amd import presets
-        name = {"base": "innerq_base", "small_preset": "innerq_small", "hybrid": "innerq_hybrid"}[cfg]
+        name = {"base": "innerq_base", "small_preset": "innerq_small", "hybrid": "innerq_hybrid",
+                "hybrid_k": "innerq_hybrid", "base_padded": "innerq_base"}[cfg]
+        over = {"key_quantize_mode": "hybrid"} if cfg == "hybrid_k" else {}  # cache.py:92-98
+        # base_padded: the leading tokens a left-padding mask hides per sequence
+        # (six distinct starts: six decode calls per step)
+        pads = [0, 0, 64, 64, 300, 1024, 4096, 9000] if cfg == "base_padded" else None
         B, Hq, Hkv, D, T, L = 8, 32, 8, 128, 32768, 4
         gen = torch.Generator(device=dev).manual_seed(300)
 
@@ -390,7 +397,7 @@ def bench_config(args):
 
         layers = []
         for l in range(L):
-            layer = IC.InnerqDynamicLayer(presets.preset_config(name), l)
+            layer = IC.InnerqDynamicLayer(presets.preset_config(name, **over), l)
             layer.update(kv(T), kv(T))
             layer._kq.store.reserve(T + 4096)
             layer._vq.store.reserve(T + 4096)
@@ -401,7 +408,7 @@ def bench_config(args):
         def step(i):
             layer = layers[i % L]
             layer.append(kn, vn)
-            layer.attend(q, D ** -0.5)
+            layer.attend(q, D ** -0.5, pads)
 
         clock_warmup(dev)
         cyc = 32 * L
@@ -409,7 +416,10 @@ def bench_config(args):
         us = statistics.median(time_backlogged(step, n, cyc) for _ in range(3))
         lay = layers[0]
         b = lay._kq.store.nbytes() + lay._vq.store.nbytes()  # packed bytes one step reads (layer 0, at the end)
-        res.update(preset=name, us=us, GBs=b / us / 1e3, frac=b / us / 1e3 / PEAK_GBS, bytes=b, steps=n,
+        if pads:
+            b = b * (1.0 - sum(pads) / (B * lay.attend_length()))  # the tokens the batch attends to
+        res.update(preset=name + (" + hybrid K" if over else "") + (" (left-padded batch)" if pads else ""),
+                   us=us, GBs=b / us / 1e3, frac=b / us / 1e3 / PEAK_GBS, bytes=b, steps=n, pads=pads,
                    k_packed=lay._kq.length, v_packed=lay._vq.length,
                    k_window=lay.keys_recent.shape[2], v_window=lay.values_recent.shape[2])
     elif cfg == "small":

@@ -337,8 +337,9 @@ __global__ __launch_bounds__(256) void quant_k_kernel(const uint16_t* __restrict
 // element i; the extremes, the NaN test and the packed words are reduced
 // across the segment.  The per-value arithmetic is quantize_group's /
 // quant_group_rt's, the extremes are exact and the words are ORs of disjoint
-// bit fields, so the fields and meta are the same bit for bit.  Asym and sym
-// only: hybrid's error sums keep the one-thread-per-group order.
+// bit fields, so the fields and meta are the same bit for bit.  Hybrid's two
+// error sums are added in element order (seg_sum_ordered), as the
+// one-thread path adds them.
 template <int G>
 __device__ __forceinline__ uint64_t seg_mask() {
   if constexpr (G == 64) {
@@ -382,6 +383,21 @@ __device__ __forceinline__ uint32_t seg_or(uint32_t x) {
   return seg_reduce<G>(x, [](uint32_t a, uint32_t b) { return a | b; });
 }
 
+// The segment's sum of x in lane (= element) order, in fp64, every lane of
+// the segment getting it: ((0 + x_0) + x_1) + ..., the order of the
+// one-thread-per-group loop, so the same roundings.  Lane j's value is read
+// by a shuffle (two 32-bit halves).
+template <int G>
+__device__ __forceinline__ double seg_sum_ordered(float x) {
+  const double xd = double(x);
+  const int lo = __double2loint(xd), hi = __double2hiint(xd);
+  const int base = int(threadIdx.x & 63) & ~(G - 1);
+  double acc = 0.0;
+#pragma unroll
+  for (int j = 0; j < G; ++j) acc += __hiloint2double(__shfl(hi, base + j, 64), __shfl(lo, base + j, 64));
+  return acc;
+}
+
 // lane i of the segment holds element v of the group; every lane of the
 // segment must be active.  Writes the group's words (lane w writes word w)
 // and its meta (lane 0) when `store`; returns the dense code and sets sg (the
@@ -393,6 +409,7 @@ __device__ __forceinline__ int32_t quant_group_lanes(float v, int i, int bits, i
   const bool nan = (__ballot(is_nan(v)) & seg_mask<G>()) != 0ull;
   int32_t c;
   uint32_t fld;
+  bool hsym = false;  // hybrid: the group keeps its sym codes
   if (mode == IQ_MODE_SYM) {
     float amx = seg_fmax<G>(fabsf(v));
     if (nan) amx = __builtin_nanf("");
@@ -401,6 +418,21 @@ __device__ __forceinline__ int32_t quant_group_lanes(float v, int i, int bits, i
     c = sym_code_b(v, s, bits, bf);
     sg = sign_of(v);
     fld = sym_field_b(c, sg, bits);
+  } else if (mode == IQ_MODE_HYBRID) {  // quant_group_rt's hybrid choice (quant.py:133-151)
+    float mn = seg_fmin<G>(v), mx = seg_fmax<G>(v), amx = seg_fmax<G>(fabsf(v));
+    if (nan) { mn = __builtin_nanf(""); mx = mn; amx = mn; }
+    const float sa = asym_scale_b(mn, mx, bits - 1, bf), ss = sym_scale_b(amx, bits, bf);
+    const int32_t ca = asym_code_b(v, mn, sa, bits - 1, bf), cs = sym_code_b(v, ss, bits, bf);
+    sg = sign_of(v);
+    const float da = __fadd_rn(__fmul_rn(float(ca), sa), mn);
+    const float ds = __fmul_rn(__fmul_rn(float(cs), ss), sg);
+    const double ea = seg_sum_ordered<G>(fabsf(__fsub_rn(da, v)));
+    const double es = seg_sum_ordered<G>(fabsf(__fsub_rn(ds, v)));
+    hsym = ea > es;
+    c = hsym ? cs : ca;
+    s = hsym ? ss : sa;
+    z = mn;
+    fld = hsym ? sym_field_b(cs, sg, bits) : asym_field_b(ca, bits);
   } else {
     float mn = seg_fmin<G>(v), mx = seg_fmax<G>(v);
     if (nan) { mn = __builtin_nanf(""); mx = mn; }
@@ -419,8 +451,14 @@ __device__ __forceinline__ int32_t quant_group_lanes(float v, int i, int bits, i
     if (store && w < W && i == w) out[w] = word;
   }
   if (store && i == 0) {
-    if (mode == IQ_MODE_SYM) meta[unit] = f2act(s, bf);
-    else reinterpret_cast<uint32_t*>(meta)[unit] = meta_word(s, z, bf);
+    if (mode == IQ_MODE_SYM) {
+      meta[unit] = f2act(s, bf);
+    } else if (mode == IQ_MODE_HYBRID) {
+      const uint32_t sh = f2act(s, bf);
+      reinterpret_cast<uint32_t*>(meta)[unit] = hsym ? (sh | HYB_FLAG) : ((sh & 0x7fffu) | (uint32_t(f2act(z, bf)) << 16));
+    } else {
+      reinterpret_cast<uint32_t*>(meta)[unit] = meta_word(s, z, bf);
+    }
   }
   return c;
 }
@@ -1015,9 +1053,10 @@ __device__ __forceinline__ void append_group_lanes(const WinRole& r, int H, int 
 }
 
 // lanes per group item of a role: one lane per element where quant_group_lanes
-// applies, else one thread per group
+// applies (groups of up to 64; asym, sym or hybrid), else one thread per group
 __host__ __device__ inline int role_lanes(int group, int mode) {
-  return group <= 64 && mode != IQ_MODE_HYBRID ? group : 1;
+  (void)mode;
+  return group <= 64 ? group : 1;
 }
 
 // element e of the new tokens (b, h, j, d) into the window buffer

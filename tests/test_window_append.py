@@ -92,3 +92,44 @@ def test_window_grows_and_keeps_old_views():
     assert w.n == 400 and torch.equal(w.tensor, x)
     for v, end in views:
         assert torch.equal(v, x[:, :, :end])
+
+
+@pytest.mark.parametrize("bits,G", [(2, 32), (4, 64)])
+def test_window_append_hybrid_special_groups(bits, G):
+    """Hybrid flushes (one lane per element, the error sums in element order)
+    against the one-thread-per-group quantize on groups that test the choice's
+    edges: a NaN, an all-zero group, constant groups (both errors zero: asym
+    kept), a group of one large and many tiny values (error terms far apart in
+    magnitude), and an fp16 subnormal group."""
+    B, H, D = 1, 2, 128
+    T = 3 * G
+    kx = synth.kv_tensor(B, H, T, D, seed=71, n_out=3, factor=8.0).astype(np.float32)
+    vx = synth.kv_tensor(B, H, T, D, seed=72, n_out=3, factor=8.0).astype(np.float32)
+    for x in (kx, vx):
+        x[0, 0, 3, 7] = np.nan                 # a K group and a V group with a NaN
+        x[0, 1, 5, :] = 0.0                    # an all-zero token (K groups)
+        x[0, 1, :, 9] = 0.25                   # a constant column (V groups)
+        x[0, 0, 9, :G] = 1e-4                  # tiny values ...
+        x[0, 0, 9, 3] = 3000.0                 # ... and one large one in a K group
+        x[0, 1, 11, G:2 * G] = 3e-6            # fp16 subnormals
+    kx, vx = kx.astype(np.float16), vx.astype(np.float16)
+    kt, vt = _t(kx), _t(vx)
+    ks = ops.PackedStore("channel", B, H, D, G, bits, "hybrid", DEV)
+    vs = ops.PackedStore("token", B, H, D, G, bits, "hybrid", DEV)
+    kref = ops.PackedStore("channel", B, H, D, G, bits, "hybrid", DEV)
+    vref = ops.PackedStore("token", B, H, D, G, bits, "hybrid", DEV)
+    kw, vw = ops.RecentWindow(kt[:, :, :1]), ops.RecentWindow(vt[:, :, :1])
+    # every token through the window: T - 1 new tokens, then all T flushed at once
+    ops.window_append(kw, kt[:, :, 1:], T, ks, None, vw, vt[:, :, 1:], T, vs)
+    kref.append(kt)
+    vref.append(vt)
+    torch.cuda.synchronize()
+    for a, b in ((ks, kref), (vs, vref)):
+        ca, ma = _bytes(a)
+        cb, mb = _bytes(b)
+        np.testing.assert_array_equal(ca, cb)
+        np.testing.assert_array_equal(ma, mb)
+    # both kinds of group occur
+    for st in (ks, vs):
+        mw = st.meta.view(torch.int32).cpu().numpy().astype(np.uint32)
+        assert ((mw & 0x8000) != 0).any() and ((mw & 0x8000) == 0).any()
