@@ -52,7 +52,7 @@
 extern "C" {
 #endif
 
-#define IQ_ABI_VERSION 2
+#define IQ_ABI_VERSION 3
 #define IQ_TOKEN_BLOCK 64
 
 enum iq_status {
@@ -265,6 +265,13 @@ typedef struct iq_window {
   int bits, group, mode;
   int axis;                   /* 0: groups along head_dim (K store layout), 1: along tokens (V layout) */
   const void* norm;           /* axis 0: fp16 [B,H,D] key normalization factor (x / norm in fp16 first), or NULL */
+  int deq_rows;               /* groups of 32 or 64: each flushed token's row of the buffer is
+                                 overwritten with its dequantized values (keys: times norm), rounded once
+                                 to the activation dtype: the values update() returns for it
+                                 (cache.py:235-276) and the reference's attention reads.  The caller may
+                                 then attend to the buffer rows before the window as dense rows (tokens
+                                 packed in one role whose other role is still in its window).  0: the
+                                 rows are left as they were. */
 } iq_window;
 
 /* One decode step of a layer's recent windows, both roles in one launch:

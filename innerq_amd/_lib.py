@@ -16,7 +16,7 @@ IQ_MODE_ASYM = 0
 IQ_MODE_SYM = 1
 IQ_MODE_HYBRID = 2
 IQ_MODE_BF16 = 0x100  # OR-ed into a mode: bf16 activations
-ABI_VERSION = 2
+ABI_VERSION = 3
 TOKEN_BLOCK = 64
 
 STATUS = {
@@ -64,6 +64,7 @@ class iq_window(ctypes.Structure):
         ("t_cap", ctypes.c_int64), ("t_off", ctypes.c_int64),
         ("bits", ctypes.c_int), ("group", ctypes.c_int), ("mode", ctypes.c_int), ("axis", ctypes.c_int),
         ("norm", ctypes.c_void_p),
+        ("deq_rows", ctypes.c_int),
     ]
 
 

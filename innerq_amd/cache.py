@@ -21,6 +21,7 @@ recent] in one gfx950 decode kernel chain (ops.decode_attention).
 from __future__ import annotations
 
 from collections.abc import Iterable
+import copy
 from typing import Any, Optional, Sequence
 
 import torch
@@ -248,7 +249,50 @@ class InnerqDynamicLayer(CacheLayerMixin):
         value_states = self.initialize_values_recent(value_states)
         self.initialize_keys_q(key_states)
         self.initialize_values_q(value_states)
+        self._keep_dequantized_rows()
         self.is_initialized = True
+
+    def _keep_dequantized_rows(self) -> None:
+        """Tokens packed in one role while the other role still holds them in its
+        window (K flushes token by token, V by groups of tokens) are attended as
+        dense rows: each window's buffer keeps its flushed tokens' rows with their
+        dequantized values (keys times the normalization factor; in the
+        activation dtype: what update() returns for them), so a decode's packed
+        segments of both roles can end at one V group boundary and the window
+        kernel reads no packed rows.  Set up after the prefill with the rows past
+        that boundary packed so far (window flushes keep them up).  fp16 layers:
+        a bf16 row would hold the values 8 bits short of the fp32 dequantization
+        that the packed reads give."""
+        if not (self.key_quantize and not self.key_quantize_over_token and self.value_quantize
+                and self.value_quantize_over_token and self.dtype == torch.float16):
+            return
+        kq = self._kq.length if self._kq is not None else 0
+        vq = self._vq.length if self._vq is not None else 0
+        e = self._packed_end()
+        kend, vend = self.keys_sink.shape[-2] + kq, self.values_sink.shape[-2] + vq
+        if self._kwin is not None and self.key_group_size <= 64:
+            keep = self.value_w_recent + self.value_flush_size + 64
+            p = min(kend - e, keep) if e is not None else 0
+            pre = self._kq.store.dequant(kq - p, p, norm=self.key_normalization_factor) if p > 0 else None
+            self._kwin = ops.RecentWindow(self._kwin.tensor, pre=pre, deq_rows=True, keep=keep)
+        if self._vwin is not None and self.value_group_size <= 64:
+            keep = self.key_w_recent + self.key_flush_size + self.value_group_size + 64
+            p = min(vend - e, keep) if e is not None else 0
+            pre = None
+            if p > 0:  # dequantized by whole groups, the last p rows kept
+                t0 = (vq - p) // self.value_group_size * self.value_group_size
+                pre = self._vq.store.dequant(t0, vq - t0)[:, :, vq - t0 - p:]
+            self._vwin = ops.RecentWindow(self._vwin.tensor, pre=pre, deq_rows=True, keep=keep)
+
+    def _packed_end(self) -> Optional[int]:
+        """The token where a decode's packed segments of both roles end: the end of
+        the shorter store, rounded down to a V group boundary (None: no store)."""
+        if self._kq is None or self._vq is None:
+            return None
+        nks, nvs = self.keys_sink.shape[-2], self.values_sink.shape[-2]
+        e = min(nks + self._kq.length, nvs + self._vq.length)
+        e = nvs + (e - nvs) // self.value_group_size * self.value_group_size
+        return e if e >= max(nks, nvs) else None
 
     # ---- decode (cache.py:283-396) ----
     def _flush_sizes(self, m: int) -> tuple[int, int]:
@@ -422,9 +466,9 @@ class InnerqDynamicLayer(CacheLayerMixin):
         def part_rows(x):
             return x if rows is None else x[rows[0]:rows[1]]
 
-        def parts(sink, quant, recent):
+        def parts(sink, quant, nq, recent):
+            # nq: the store's first nq tokens are read packed, then recent's rows
             ns = sink.shape[-2]
-            nq = quant.length if quant is not None else 0
             dense_sink = part_rows(sink[:, :, s0:]) if s0 < ns else None
             t0 = min(max(s0 - ns, 0), nq)
             r0 = max(s0 - ns - nq, 0)
@@ -432,10 +476,23 @@ class InnerqDynamicLayer(CacheLayerMixin):
             store = None
             if quant is not None:
                 store = quant.store if rows is None else quant.store.batch_view(*rows)
+                if nq < quant.length:
+                    store = copy.copy(store)
+                    store.length = nq
             return dense_sink, store, t0, dense_recent
 
-        ks, kst, kt0, kr = parts(self.keys_sink, self._kq, self.keys_recent)
-        vs, vst, vt0, vr = parts(self.values_sink, self._vq, self.values_recent)
+        kq = self._kq.length if self._kq is not None else 0
+        vq = self._vq.length if self._vq is not None else 0
+        krecent, vrecent = self.keys_recent, self.values_recent
+        e = self._packed_end()
+        if e is not None and self._kwin is not None and self._vwin is not None:
+            nk = self.keys_sink.shape[-2] + kq - e  # packed tokens past e, read as the rows kept
+            nv = self.values_sink.shape[-2] + vq - e
+            if nk <= self._kwin.shadow and nv <= self._vwin.shadow and (nk or nv):
+                kq, krecent = kq - nk, self._kwin.rows_before(nk)
+                vq, vrecent = vq - nv, self._vwin.rows_before(nv)
+        ks, kst, kt0, kr = parts(self.keys_sink, self._kq, kq, krecent)
+        vs, vst, vt0, vr = parts(self.values_sink, self._vq, vq, vrecent)
         norm = part_rows(self.key_normalization_factor) if self._kq is not None else None
         return ops.decode_attention(q, ks, kst, kr, vs, vst, vr, scaling, norm=norm, k_t0=kt0, v_t0=vt0)
 

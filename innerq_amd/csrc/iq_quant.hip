@@ -405,7 +405,7 @@ __device__ __forceinline__ double seg_sum_ordered(float x) {
 template <int G>
 __device__ __forceinline__ int32_t quant_group_lanes(float v, int i, int bits, int mode, bool bf, bool store,
                                                      uint32_t* out, uint16_t* meta, int64_t unit, float& sg, float& s,
-                                                     float& z) {
+                                                     float& z, float* deq = nullptr) {
   const bool nan = (__ballot(is_nan(v)) & seg_mask<G>()) != 0ull;
   int32_t c;
   uint32_t fld;
@@ -449,6 +449,11 @@ __device__ __forceinline__ int32_t quant_group_lanes(float v, int i, int bits, i
   for (int w = 0; w < (G * 4) / 32; ++w) {  // up to 4-bit fields
     const uint32_t word = seg_or<G>((wi == w ? lo : 0u) | (wi + 1 == w ? hi : 0u));
     if (store && w < W && i == w) out[w] = word;
+  }
+  if (deq) {  // the stored field's value, as group_deq_params + dequant_k_kernel decode it (quant.py:83-93, 121-131)
+    const bool symf = mode == IQ_MODE_SYM || hsym;
+    const float cf = symf ? float(int(fld) - (1 << (bits - 1))) : float(fld);
+    *deq = __fadd_rn(__fmul_rn(cf, s), symf ? 0.f : z);
   }
   if (store && i == 0) {
     if (mode == IQ_MODE_SYM) {
@@ -952,6 +957,7 @@ struct WinRole {
   int bf;                            // bf16 activations (mode's IQ_MODE_BF16 flag, stripped from mode)
   const uint16_t* norm;              // axis 0: fp16 [B,H,D] key normalization factor, or null
   int vec_buf, vec_x;                // rows of the buffer / of x are 16-byte aligned (base and strides)
+  int deq;                           // flushed tokens' buffer rows get their dequantized values
 };
 
 struct AppendArgs {
@@ -1047,9 +1053,13 @@ __device__ __forceinline__ void append_group_lanes(const WinRole& r, int H, int 
                               : r.x + b * r.sxb + h * r.sxh + int64_t(f - r.n) * r.sxt + d;
   float v = act2f(*p, r.bf != 0);
   if (r.norm) v = round_act(v / act2f(r.norm[bh * D + d], r.bf != 0), r.bf != 0);  // cache.py:125
-  float sg, sc, zp;
+  float sg, sc, zp, dq;
   quant_group_lanes<G>(v, i, r.bits, r.mode, r.bf, true, r.codes + unit * ((G * r.bits) >> 5), r.meta, unit, sg, sc,
-                       zp);
+                       zp, r.deq ? &dq : nullptr);
+  if (r.deq) {  // the token's buffer row (window or new token) as dequant_k_kernel gives it
+    if (r.norm) dq = __fmul_rn(dq, act2f(r.norm[bh * D + d], r.bf != 0));  // cache.py:132
+    r.buf[b * r.sb + h * r.sh + int64_t(r.start + f) * r.st + d] = f2act(dq, r.bf != 0);
+  }
 }
 
 // lanes per group item of a role: one lane per element where quant_group_lanes
@@ -1064,6 +1074,7 @@ __device__ __forceinline__ void window_copy(const WinRole& r, int H, int D, int6
   const int64_t per_bh = int64_t(r.m) * D;
   const int64_t bh = e / per_bh, b = bh / H, h = bh % H;
   const int j = int((e % per_bh) / D), d = int(e % D);
+  if (r.deq && r.n + j < r.F) return;  // a flushed new token: its row gets the dequantized values
   r.buf[b * r.sb + h * r.sh + int64_t(r.start + r.n + j) * r.st + d] = r.x[b * r.sxb + h * r.sxh + int64_t(j) * r.sxt + d];
 }
 
@@ -1303,6 +1314,8 @@ int check_window(const iq_window* w, int D) {
   if (int e = check_store(w->bits, w->group, base_mode(w->mode))) return e;
   IQ_CHECK(w->axis == 0 || w->axis == 1, IQ_ERR_SHAPE);
   IQ_CHECK(!w->norm || w->axis == 0, IQ_ERR_SHAPE);
+  // dequantized rows: from the lane quantizer (groups of up to 64)
+  IQ_CHECK(!w->deq_rows || w->group <= 64, IQ_ERR_SHAPE);
   IQ_CHECK(w->t_off >= 0 && w->t_off + w->flush <= w->t_cap, IQ_ERR_RANGE);
   if (w->axis == 0) {
     IQ_CHECK(D % w->group == 0, IQ_ERR_GROUP);
@@ -1328,6 +1341,7 @@ WinRole to_role(const iq_window* w) {
   r.norm = (const uint16_t*)w->norm;
   r.vec_buf = aligned(w->buf, 16) && w->s_b % 8 == 0 && w->s_h % 8 == 0 && w->s_t % 8 == 0;
   r.vec_x = aligned(w->x, 16) && w->sx_b % 8 == 0 && w->sx_h % 8 == 0 && w->sx_t % 8 == 0;
+  r.deq = w->flush ? w->deq_rows : 0;
   return r;
 }
 }  // namespace

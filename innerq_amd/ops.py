@@ -416,27 +416,46 @@ class RecentWindow:
     A decode step writes its new tokens after the window and advances
     ``start`` past the flushed ones (window_append), so no step copies the
     window.  When the buffer is full the window moves to the front of a new,
-    larger buffer; a view returned earlier keeps its old buffer and values."""
+    larger buffer; a view returned earlier keeps its old buffer and values.
 
-    def __init__(self, x: torch.Tensor):
+    With ``deq_rows`` (a K window), each flushed token's row keeps, in place,
+    its dequantized values (times the key normalization factor, in the
+    activation dtype): the ``shadow`` rows before ``start`` are the tokens
+    just before the window, as update() returns them (at most ``keep`` of them
+    survive a move to a larger buffer)."""
+
+    def __init__(self, x: torch.Tensor, pre: Optional[torch.Tensor] = None, deq_rows: bool = False,
+                 keep: int = 0):
         require_act(x, "recent window")
         B, H, n, D = x.shape
-        self.buf = torch.empty(B, H, max(2 * n, n + 64), D, dtype=x.dtype, device=x.device)
-        self.buf[:, :, :n].copy_(x)
-        self.start, self.n = 0, n
+        p = 0 if pre is None else pre.shape[2]
+        self.buf = torch.empty(B, H, max(2 * (n + p), n + p + 64), D, dtype=x.dtype, device=x.device)
+        if p:
+            self.buf[:, :, :p].copy_(pre)
+        self.buf[:, :, p:p + n].copy_(x)
+        self.start, self.n = p, n
+        self.deq_rows, self.keep, self.shadow = deq_rows, keep, p
 
     @property
     def tensor(self) -> torch.Tensor:
         return self.buf[:, :, self.start:self.start + self.n]
+
+    def rows_before(self, p: int) -> torch.Tensor:
+        """The p shadow rows before the window and the window: [B,H,p+n,D]."""
+        if not 0 <= p <= self.shadow:
+            raise ValueError(f"rows_before: {p} rows asked, {self.shadow} held")
+        return self.buf[:, :, self.start - p:self.start + self.n]
 
     def reserve(self, m: int) -> None:
         """Room for m more tokens after the window."""
         B, H, cap, D = self.buf.shape
         if self.start + self.n + m <= cap:
             return
-        buf = torch.empty(B, H, max(2 * (self.n + m), self.n + m + 64), D, dtype=self.buf.dtype, device=self.buf.device)
-        buf[:, :, :self.n].copy_(self.tensor)
-        self.buf, self.start = buf, 0
+        p = min(self.shadow, self.keep)
+        buf = torch.empty(B, H, max(2 * (p + self.n + m), p + self.n + m + 64), D, dtype=self.buf.dtype,
+                          device=self.buf.device)
+        buf[:, :, :p + self.n].copy_(self.buf[:, :, self.start - p:self.start + self.n])
+        self.buf, self.start, self.shadow = buf, p, p
 
 
 def window_append(kwin: Optional[RecentWindow], knew: Optional[torch.Tensor], kflush: int,
@@ -481,6 +500,7 @@ def window_append(kwin: Optional[RecentWindow], knew: Optional[torch.Tensor], kf
                 raise TypeError(f"window_append: {x.dtype} tokens into a {st.dtype} store")
             w.bits, w.group, w.mode = st.bits, st.group, st.mode_arg
             w.axis = 0 if st.axis == "channel" else 1
+            w.deq_rows = 1 if win.deq_rows else 0
             if norm is not None:
                 if st.axis != "channel":
                     raise NotImplementedError("key normalization is supported for keys grouped along head_dim")
@@ -499,6 +519,9 @@ def window_append(kwin: Optional[RecentWindow], knew: Optional[torch.Tensor], kf
             win.n += x.shape[-2] - fl
             if fl:
                 st.length += fl
+                # the flushed rows now hold their dequantized values (deq_rows), right
+                # after the shadow rows before them; else no row before the window does
+                win.shadow = win.shadow + fl if win.deq_rows else 0
 
 
 def quantize_dense(x: torch.Tensor, group: int, bits: int, mode, axis: str):

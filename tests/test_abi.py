@@ -32,7 +32,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_version_and_strerror():
     lib = _lib.lib()
-    assert lib.iq_abi_version() == 2
+    assert lib.iq_abi_version() == 3
     assert lib.iq_strerror(0) == b"ok"
     assert b"bits" in lib.iq_strerror(-2)
     assert lib.iq_strerror(12345) == b"unknown status"

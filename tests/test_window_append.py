@@ -133,3 +133,57 @@ def test_window_append_hybrid_special_groups(bits, G):
     for st in (ks, vs):
         mw = st.meta.view(torch.int32).cpu().numpy().astype(np.uint32)
         assert ((mw & 0x8000) != 0).any() and ((mw & 0x8000) == 0).any()
+
+
+@pytest.mark.parametrize("kmode", ["asymmetric", "symmetric", "hybrid"])
+@pytest.mark.parametrize("bits,G", [(2, 32), (3, 64)])
+@pytest.mark.parametrize("norm", [False, True])
+def test_window_append_keeps_dequantized_rows(kmode, bits, G, norm):
+    """deq_rows: each flushed key's buffer row holds its dequantized values
+    (times the normalization factor, rounded once to fp16), bit-exact to the
+    store's dequant of those tokens, including flushes that reach into the new
+    tokens and a move to a larger buffer (the last `keep` rows survive)."""
+    B, H, D = 2, 3, 128
+    kx = _mixed(B, H, 260, D, seed=bits * 11 + G)
+    kt = _t(kx)
+    knorm = ops.key_norm_factor(kt[:, :, :64]) if norm else None
+    ks = ops.PackedStore("channel", B, H, D, G, bits, kmode, DEV)
+    ks.append(kt[:, :, :64], norm=knorm)
+    kw = ops.RecentWindow(kt[:, :, 64:84], deq_rows=True, keep=48)
+    pos, done = 84, 64
+    steps = [(1, 1), (1, 3), (2, 0), (3, 22)] + [(1, 1)] * 90  # the single-token steps move the buffer
+    for m, kf in steps:
+        ops.window_append(kw, kt[:, :, pos:pos + m], kf, ks if kf else None, knorm if kf else None,
+                          None, None, 0, None)
+        pos, done = pos + m, done + kf
+    torch.cuda.synchronize()
+    assert torch.equal(kw.tensor, kt[:, :, done:pos])
+    p = kw.shadow
+    assert 0 < p <= done - 64 and p >= 48  # a move kept 48, the steps after it added theirs
+    ref = ks.dequant(done - p, p, norm=knorm)
+    np.testing.assert_array_equal(kw.rows_before(p)[:, :, :p].cpu().numpy(), ref.cpu().numpy())
+
+
+@pytest.mark.parametrize("vmode", ["asymmetric", "symmetric", "hybrid"])
+@pytest.mark.parametrize("bits,G", [(2, 32), (4, 64)])
+def test_window_append_keeps_dequantized_value_rows(vmode, bits, G):
+    """deq_rows on a V window (groups along tokens): each flushed group's buffer
+    rows hold its dequantized values, bit-exact to the store's dequant, through
+    flushes that reach into the new tokens and a move to a larger buffer."""
+    B, H, D = 2, 3, 128
+    vx = _mixed(B, H, 40 * G, D, seed=bits * 13 + G)
+    vt = _t(vx)
+    vs = ops.PackedStore("token", B, H, D, G, bits, vmode, DEV)
+    vs.append(vt[:, :, :2 * G])
+    vw = ops.RecentWindow(vt[:, :, 2 * G:2 * G + 5], deq_rows=True, keep=2 * G)
+    pos, done = 2 * G + 5, 2 * G
+    steps = [(G - 5, 0), (3, G), (1, 0), (2 * G, 2 * G)] + [(G // 2, 0), (G // 2, G)] * 30
+    for m, vf in steps:
+        ops.window_append(None, None, 0, None, None, vw, vt[:, :, pos:pos + m], vf, vs if vf else None)
+        pos, done = pos + m, done + vf
+    torch.cuda.synchronize()
+    assert torch.equal(vw.tensor, vt[:, :, done:pos])
+    p = vw.shadow
+    assert p >= 2 * G and p % G == 0
+    ref = vs.dequant(done - p, p)
+    np.testing.assert_array_equal(vw.rows_before(p)[:, :, :p].cpu().numpy(), ref.cpu().numpy())
