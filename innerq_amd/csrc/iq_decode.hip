@@ -32,13 +32,15 @@ constexpr int NSD_MAX = 4;    // split slots of the dense tokens, at most
 constexpr int DSLICE = 32;    // dense tokens per split slot, at least
 constexpr int MERGE_RUNS_MAX = 4;  // fused runs per (batch, KV head) the merging dense kernel preloads
 // 256-thread sections of the merging dense kernel: three where the window
-// holds packed rows (the reference presets' steady state: 32 sinks, a 96-token
-// recent window and the <= 31 packed keys short of a V group, 129-159 tokens
-// that two sections take in two chunks each: 13.9 us against 15.2 us per
-// call), two for fp16 windows (configs 3 and 4: 7.5 us against 8.2 us)
+// holds packed rows (32 sinks, a 96-token recent window and the <= 31 packed
+// keys short of a V group, 129-159 tokens that two sections take in two
+// chunks each: 13.9 us against 15.2 us per call), two for fp16 windows of up
+// to two chunks (configs 3 and 4: 7.5 us against 8.2 us); fp16 windows
+// longer than that take three (merge_sections_dense)
 // (bf16 layers: two, whose fp32 tiles fill the LDS; eight query heads per KV
 // head: two, whose fp16 accumulators would not fit three sections' registers)
 constexpr int merge_sections(bool pk, bool bf, int nrep) { return pk && !bf && nrep <= 4 ? 3 : 2; }
+constexpr int merge_sections_dense(int n_dense, int nrep) { return nrep <= 4 && n_dense > 2 * DT ? 3 : 2; }
 
 struct Seg {
   const uint16_t* dense;
@@ -298,9 +300,9 @@ __device__ __forceinline__ void packed_run(const Seg& K, const Seg& V, const uin
 // bf16 put a window-heavy step at 1.005e-3 of fp32 attention.  Its waves take
 // one head each for the logits and thread (head, column pair) accumulates
 // the output.
-template <int D, int NREP, bool PK, bool MERGE = false, bool BF = false>
-__global__ __launch_bounds__(MERGE ? 256 * merge_sections(PK, BF, NREP) : 256) void dense_attn_kernel(DenseArgs a) {
-  constexpr int NH = MERGE ? merge_sections(PK, BF, NREP) : 1;  // slices per workgroup (256-thread sections)
+template <int D, int NREP, bool PK, bool MERGE = false, bool BF = false, int NS = merge_sections(PK, BF, NREP)>
+__global__ __launch_bounds__(MERGE ? 256 * NS : 256) void dense_attn_kernel(DenseArgs a) {
+  constexpr int NH = MERGE ? NS : 1;  // slices per workgroup (256-thread sections)
   constexpr int NTH = 256 * NH;
   constexpr int TW = BF ? D : D / 2;          // dwords of a row's values: fp32, or fp16 pairs
   constexpr int KS = TW + 1;                  // K tile row stride in dwords (odd: no bank conflicts)
@@ -1059,8 +1061,13 @@ int launch_splits(const void* q, int64_t sq_b, int64_t sq_h, const void* norm, c
           if (pk) dense_attn_kernel<DD, R, true, true, true><<<mgrid, 256 * merge_sections(true, true, R), 0, st>>>(da);
           else dense_attn_kernel<DD, R, false, true, true><<<mgrid, 256 * merge_sections(false, true, R), 0, st>>>(da);
         } else {
-          if (pk) dense_attn_kernel<DD, R, true, true><<<mgrid, 256 * merge_sections(true, false, R), 0, st>>>(da);
-          else dense_attn_kernel<DD, R, false, true><<<mgrid, 256 * merge_sections(false, false, R), 0, st>>>(da);
+          if (pk) {
+            dense_attn_kernel<DD, R, true, true><<<mgrid, 256 * merge_sections(true, false, R), 0, st>>>(da);
+          } else if (merge_sections_dense(n_dense, R) == 3) {
+            if constexpr (R <= 4) dense_attn_kernel<DD, R, false, true, false, 3><<<mgrid, 768, 0, st>>>(da);
+          } else {
+            dense_attn_kernel<DD, R, false, true><<<mgrid, 256 * merge_sections(false, false, R), 0, st>>>(da);
+          }
         }
       };
       auto by_r = [&]<int DD>() {
