@@ -570,3 +570,61 @@ def test_mistral_padded_batch_through_attend(monkeypatch):
     err = ((got - ref).abs().max() / ref.abs().max()).item()
     print(f"mistral padded fused vs sdpa: {err:.2e}")
     assert err < 2e-2
+
+
+_ROW_LAYOUTS = {
+    # K flushed token by token, V by groups of 64 (group 64 rows, differing sinks)
+    "k1_v64_g64_sinks": dict(k_bits=3, v_bits=4, key_flush_size=1, value_flush_size=64, key_group_size=64,
+                             value_group_size=64, key_w_recent=50, value_w_recent=80, key_w_sink=16,
+                             value_w_sink=8, key_normalize=True, key_quantize_over_token=False,
+                             value_quantize_over_token=True, key_quantize_mode="hybrid",
+                             value_quantize_mode="asymmetric"),
+    # V flushed ahead of K (K by groups of 32 tokens, V every group)
+    "k32_v32_vahead": dict(k_bits=4, v_bits=2, key_flush_size=32, value_flush_size=32, key_group_size=32,
+                           value_group_size=32, key_w_recent=90, value_w_recent=20, key_w_sink=0,
+                           value_w_sink=4, key_normalize=False, key_quantize_over_token=False,
+                           value_quantize_over_token=True, key_quantize_mode="asymmetric",
+                           value_quantize_mode="hybrid"),
+    # groups of 128: no dequantized rows (the packed-row path)
+    "g128": dict(k_bits=4, v_bits=4, key_flush_size=1, value_flush_size=128, key_group_size=128,
+                 value_group_size=128, key_w_recent=32, value_w_recent=100, key_w_sink=0, value_w_sink=0,
+                 key_normalize=False, key_quantize_over_token=False, value_quantize_over_token=True,
+                 key_quantize_mode="symmetric", value_quantize_mode="symmetric"),
+}
+
+
+@pytest.mark.parametrize("name", list(_ROW_LAYOUTS))
+def test_attend_with_dequantized_window_rows(name):
+    """attend() over 150 decode steps of layouts where one role's store runs
+    ahead of the other's (its tokens still in the other role's window): the
+    windows' dequantized rows end both packed segments at one V group boundary
+    (K ahead, V ahead, groups of 64, sinks of different lengths, hybrid
+    stores), or, for groups of 128, the window kernel decodes the packed rows.
+    Every 7th step within 1e-3 of float64 attention over the layer's
+    dequantized K and V."""
+    cfg = Cfg(**_ROW_LAYOUTS[name])
+    B, H, nrep, D, prefill, steps = 2, 2, 4, 128, 600, 150
+    kx = synth.kv_tensor(B, H, prefill + steps, D, seed=91, n_out=2, factor=8.0)
+    vx = synth.kv_tensor(B, H, prefill + steps, D, seed=92, n_out=2, factor=8.0)
+    vx[..., :40] += 4.0  # offset columns: hybrid groups of both kinds
+    kt, vt = torch.from_numpy(kx).to(DEV), torch.from_numpy(vx).to(DEV)
+    layer = C.InnerqDynamicLayer(cfg, 0)
+    layer.update(kt[:, :, :prefill], vt[:, :, :prefill])
+    used = 0
+    for s in range(steps):
+        layer.append(kt[:, :, prefill + s:prefill + s + 1], vt[:, :, prefill + s:prefill + s + 1])
+        e = layer._packed_end()
+        if e is not None:  # the rows past e are read from the windows' kept rows (as _attend_from decides)
+            nk = layer.keys_sink.shape[-2] + layer._kq.length - e
+            nv = layer.values_sink.shape[-2] + layer._vq.length - e
+            used += int((nk or nv) and nk <= layer._kwin.shadow and nv <= layer._vwin.shadow)
+        if s % 7 == 3:
+            q = synth.normal((B, H * nrep, D), seed=s).astype(np.float16)
+            out = layer.attend(torch.from_numpy(q).to(DEV)[:, :, None], D ** -0.5)[:, :, 0]
+            ref = A.decode_attention(q, _np(layer.get_keys_deq().float()), _np(layer.get_values_deq().float()),
+                                     D ** -0.5, None)
+            assert A.rel_err(_np(out).astype(np.float64), ref) < 1e-3, f"step {s + 1}"
+    if name == "g128":
+        assert layer._kwin.deq_rows is False and used == 0
+    else:
+        assert layer._kwin.deq_rows and layer._vwin.deq_rows and used > steps // 2
