@@ -422,7 +422,8 @@ class RecentWindow:
     its dequantized values (times the key normalization factor, in the
     activation dtype): the ``shadow`` rows before ``start`` are the tokens
     just before the window, as update() returns them (at most ``keep`` of them
-    survive a move to a larger buffer)."""
+    survive a move to a larger buffer).  A view taken earlier then sees its
+    flushed rows change to those values."""
 
     def __init__(self, x: torch.Tensor, pre: Optional[torch.Tensor] = None, deq_rows: bool = False,
                  keep: int = 0):
