@@ -198,8 +198,10 @@ def quantize_hybrid(zp_func, nozp_func, zp_deq_func, nozp_deq_func):
     """quant.py:133-151: (b-1)-bit asym and b-bit sym per group; mask=True picks sym.
 
     The per-group L1 errors are summed in float64 here; the reference sums in
-    fp32, so an exact tie-break can differ only when the two errors agree to
-    fp32 precision (the golden fixtures pin the reference's choice).
+    fp32, so the choice can differ only when the two errors agree to fp32
+    precision.  Exact ties keep the asym codes (the strict comparison), as the
+    reference's masks in tests/golden/hybrid_ties.npz pin; near-ties that fp32
+    rounding in some summation order would split stay unpinned.
     """
     def hybrid_func(x, group_size, bit, act="f16"):
         x = _cast(x, act)

@@ -24,3 +24,9 @@ def quant_golden():
 def cache_golden():
     import numpy as np
     return np.load(os.path.join(GOLDEN, "cache_golden.npz"))
+
+
+@pytest.fixture(scope="session")
+def hybrid_ties():
+    import numpy as np
+    return np.load(os.path.join(GOLDEN, "hybrid_ties.npz"))

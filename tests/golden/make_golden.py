@@ -30,7 +30,11 @@ sliding_golden.npz  InnerqDynamicSlidingWindowLayer.update() traces
                     reference indexes [:, :, -w, :]), the recent-window lengths
                     and get_mask_sizes() before the call.
 
-Usage:  python tests/golden/make_golden.py [/root/reference] [--sliding-only | --bf16-only]
+hybrid_ties.npz     groups whose two hybrid L1 errors tie exactly (the
+                    comparison quant.py:144 makes is strict) and the
+                    reference's masks for them.
+
+Usage:  python tests/golden/make_golden.py [/root/reference] [--sliding-only | --bf16-only | --ties-only]
 """
 from __future__ import annotations
 
@@ -242,8 +246,51 @@ def bf16_fixtures(quant, cache, presets):
     return out
 
 
-def main(root, sliding_only=False, bf16_only=False):
+def hybrid_tie_fixtures(quant):
+    """Groups whose two hybrid L1 errors tie exactly: values on a coarse grid
+    (a few distinct quarter multiples), so every error term and both sums are
+    exact in fp32 whatever the summation order; chosen by the reference's own
+    quantize / dequantize functions (errors summed in float64 here, for the
+    choice only), then the reference's quantize_hybrid mask recorded (the
+    comparison is strict: a tie keeps the asym codes).  Both axes, bits 2-4,
+    groups of 32; 16 tied groups each, in a [1, 1, 16, 32] (channel) or
+    [1, 1, 32, 16] (token) fp16 tensor."""
+    out = {}
+    G, n = 32, 16
+    for axis in ("channel", "token"):
+        qa = getattr(quant, f"quantize_{axis}dim_asym")
+        qs = getattr(quant, f"quantize_{axis}dim_sym")
+        da = getattr(quant, f"dequantize_{axis}dim_asym")
+        ds = getattr(quant, f"dequantize_{axis}dim_sym")
+        hq = quant.quantize_hybrid(qa, qs, da, ds)
+        for bits in (2, 3, 4):
+            rng = np.random.default_rng(1000 + bits + (0 if axis == "channel" else 50))
+            groups = []
+            while len(groups) < n:
+                lv = rng.integers(-8, 9, size=int(rng.integers(2, 5))) / 4.0
+                g = rng.choice(lv, size=G).astype(np.float16)
+                x = torch.from_numpy(g.reshape(1, 1, 1, G) if axis == "channel" else g.reshape(1, 1, G, 1))
+                xa = da(*qa(x.clone(), G, bits - 1), G).double()
+                xs = ds(*qs(x.clone(), G, bits), G).double()
+                ea = (xa - x.double()).abs().sum().item()
+                es = (xs - x.double()).abs().sum().item()
+                if ea == es and ea > 0:
+                    groups.append(g)
+            x = np.stack(groups)                        # [n, G]
+            x = x.reshape(1, 1, n, G) if axis == "channel" else x.T.reshape(1, 1, G, n)
+            c, sc, z = hq(torch.from_numpy(np.ascontiguousarray(x)), G, bits)
+            key = f"{axis}_b{bits}"
+            out[key + "_x"] = np.ascontiguousarray(x).view(np.uint16)
+            out[key + "_mask"] = sc["mask"].cpu().numpy()
+    return out
+
+
+def main(root, sliding_only=False, bf16_only=False, ties_only=False):
     quant, cache = load_reference(root)
+    if ties_only:
+        np.savez_compressed(os.path.join(HERE, "hybrid_ties.npz"), **hybrid_tie_fixtures(quant))
+        print("wrote", os.path.join(HERE, "hybrid_ties.npz"))
+        return
     if bf16_only:
         np.savez_compressed(os.path.join(HERE, "bf16_golden.npz"), **bf16_fixtures(quant, cache, PRESETS))
         print("wrote", os.path.join(HERE, "bf16_golden.npz"))
@@ -342,4 +389,4 @@ def main(root, sliding_only=False, bf16_only=False):
 if __name__ == "__main__":
     args = [a for a in sys.argv[1:] if not a.startswith("--")]
     main(args[0] if args else "/root/reference", sliding_only="--sliding-only" in sys.argv,
-         bf16_only="--bf16-only" in sys.argv)
+         bf16_only="--bf16-only" in sys.argv, ties_only="--ties-only" in sys.argv)

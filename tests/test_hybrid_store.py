@@ -294,3 +294,35 @@ def test_hybrid_store_wire_round_trip(axis):
     for s in (st, back):
         s.append(_f16t(x[:, :, 160:]))
     assert torch.equal(back.dequant(dtype=torch.float32), st.dequant(dtype=torch.float32))
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("axis", ["channel", "token"])
+@pytest.mark.parametrize("bits", BITS)
+def test_hybrid_exact_ties_keep_asym(hybrid_ties, axis, bits):
+    """Groups whose two L1 errors tie exactly (the live reference's masks:
+    all False, quant.py:144 compares strictly) through every hybrid path: the
+    quant.py-API functional hybrid (iq_hybrid_mask), a hybrid store's append
+    (one thread per group) and a window flush (one lane per element)."""
+    from innerq_amd import quant as IQ
+    x = hybrid_ties[f"{axis}_b{bits}_x"].view(np.float16)
+    want = hybrid_ties[f"{axis}_b{bits}_mask"]
+    xt = _f16t(x)
+    qa, qs = getattr(IQ, f"quantize_{axis}dim_asym"), getattr(IQ, f"quantize_{axis}dim_sym")
+    da, ds = getattr(IQ, f"dequantize_{axis}dim_asym"), getattr(IQ, f"dequantize_{axis}dim_sym")
+    _, s, _ = IQ.quantize_hybrid(qa, qs, da, ds)(xt, 32, bits)
+    np.testing.assert_array_equal(s["mask"].cpu().numpy(), want)
+    # the store's flags (bit 15 of each unit's scale): none set
+    st = _store(x, axis, bits)
+    assert not ops.unpack_store(st)[1]["mask"].cpu().numpy().any()
+    # a window flush of the same tokens
+    w = ops.RecentWindow(xt[:, :, :1])
+    ws = ops.PackedStore(axis, 1, 1, x.shape[3], 32, bits, "hybrid", DEV)
+    n = x.shape[2]
+    if axis == "channel":
+        ops.window_append(w, xt[:, :, 1:], n, ws, None, None, None, 0, None)
+    else:
+        ops.window_append(None, None, 0, None, None, w, xt[:, :, 1:], n, ws)
+    torch.cuda.synchronize()
+    assert not ops.unpack_store(ws)[1]["mask"].cpu().numpy().any()
+    np.testing.assert_array_equal(ws.codes.cpu().numpy(), st.codes.cpu().numpy())

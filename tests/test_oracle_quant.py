@@ -58,6 +58,19 @@ def test_hybrid_matches_reference_golden(quant_golden, axis, bits):
     np.testing.assert_array_equal(_sha(d + np.float32(0.0)), quant_golden[key + "_deq_pz_sha256"])
 
 
+@pytest.mark.parametrize("axis", ["channel", "token"])
+@pytest.mark.parametrize("bits", [2, 3, 4])
+def test_hybrid_exact_ties_keep_asym(hybrid_ties, axis, bits):
+    """Groups whose two L1 errors tie exactly (every term and sum exact in fp32,
+    so every summation order agrees): the reference's strict comparison
+    (quant.py:144) keeps the asym codes, and so does the oracle."""
+    x = hybrid_ties[f"{axis}_b{bits}_x"].view(np.float16)
+    _, s, _ = getattr(Q, f"quantize_{axis}dim_hybrid")(x, 32, bits)
+    want = hybrid_ties[f"{axis}_b{bits}_mask"]
+    assert not want.any()
+    np.testing.assert_array_equal(s["mask"], want)
+
+
 def test_config0_digests(quant_golden):
     """Config 0: [1,8,4096,128] 4-bit asym G=32, K along D, V along T."""
     from innerq_amd import synth
