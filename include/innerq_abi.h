@@ -4,7 +4,7 @@
  * API of src/innerq/quant.py and src/innerq/cache.py, backed by torch ops.
  * Each entry point below replaces the torch work behind one piece of that API
  * (cited per function).  The Python package innerq_amd binds these through
- * ctypes; INTEGRATION.md shows the binding a maintainer of the reference adds.
+ * ctypes (innerq_amd/_lib.py holds the structures and signatures).
  *
  * Conventions
  *  - All tensor arguments are device pointers (hipMalloc'd or from a torch
@@ -23,7 +23,7 @@
  *    also IQ_MODE_HYBRID ('hybrid', bits 2-4, below), which the V side of
  *    iq_av_gemv and of the decode entry points reads.
  *
- * Packed stores (layout owned by this library; see DESIGN.md)
+ * Packed stores (layout owned by this library)
  *  K store, groups along head_dim (quant.py:75-77 channeldim):
  *     codes  uint32 [B, H, t_cap/64, D/G, 64, G*bits/32]
  *     meta   uint16 [B, H, t_cap/64, D/G, 64, M]      M = 2 (scale, zero) asym, 1 (scale) sym
