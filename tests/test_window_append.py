@@ -187,3 +187,22 @@ def test_window_append_keeps_dequantized_value_rows(vmode, bits, G):
     assert p >= 2 * G and p % G == 0
     ref = vs.dequant(done - p, p)
     np.testing.assert_array_equal(vw.rows_before(p)[:, :, :p].cpu().numpy(), ref.cpu().numpy())
+
+
+def test_recent_window_keeps_rows_before_it_when_it_moves():
+    """RecentWindow: the rows kept before the window (deq_rows) survive a move
+    to a larger buffer up to `keep` of them, right before the window;
+    rows_before(p) refuses more rows than are held."""
+    x = torch.arange(2 * 3 * 10 * 4, dtype=torch.float16, device=DEV).reshape(2, 3, 10, 4)
+    pre = -torch.arange(2 * 3 * 6 * 4, dtype=torch.float16, device=DEV).reshape(2, 3, 6, 4) - 1
+    w = ops.RecentWindow(x, pre=pre, deq_rows=True, keep=4)
+    assert (w.start, w.n, w.shadow) == (6, 10, 6)
+    assert torch.equal(w.tensor, x) and torch.equal(w.rows_before(6)[:, :, :6], pre)
+    cap = w.buf.shape[2]
+    w.reserve(cap)  # forces a move
+    assert w.buf.shape[2] >= 4 + 10 + cap and (w.start, w.shadow) == (4, 4)
+    assert torch.equal(w.tensor, x) and torch.equal(w.rows_before(4)[:, :, :4], pre[:, :, 2:])
+    with pytest.raises(ValueError):
+        w.rows_before(5)
+    plain = ops.RecentWindow(x)
+    assert (plain.shadow, plain.deq_rows) == (0, False)
