@@ -464,7 +464,7 @@ class InnerqDynamicLayer(CacheLayerMixin):
         parts of [sink | packed | recent] of K and of V from token s0 on (of the
         sequences [rows[0], rows[1]) when rows is given, q holding theirs)."""
         def part_rows(x):
-            return x if rows is None else x[rows[0]:rows[1]]
+            return x if rows is None or x is None else x[rows[0]:rows[1]]
 
         def parts(sink, quant, nq, recent):
             # nq: the store's first nq tokens are read packed, then recent's rows

@@ -150,7 +150,8 @@ def test_cache_attend_matches_dense_attention(cache_golden, name, nrep):
 
 @pytest.mark.parametrize("name", ["innerq_base", "innerq_hybrid"])
 @pytest.mark.parametrize("pads", [(0, 37, 300, 0), (5, 5, 700, 690)])
-def test_cache_attend_with_padding(name, pads):
+@pytest.mark.parametrize("norm", [True, False])
+def test_cache_attend_with_padding(name, pads, norm):
     """attend() with a padding mask's hidden prefix per sequence (left padding):
     sequence b attends to tokens [pads[b], T) only, the batch split into runs of
     one start (one decode call each, over batch views of the stores); starts in
@@ -158,7 +159,7 @@ def test_cache_attend_with_padding(name, pads):
     of float64 attention over its own tokens of the layer's dequantized K and V."""
     from innerq_amd import presets
     B, H, nrep, D, T = 4, 2, 4, 128, 760
-    layer = C.InnerqDynamicLayer(presets.preset_config(name), 0)
+    layer = C.InnerqDynamicLayer(presets.preset_config(name, key_normalize=norm), 0)
     kx = synth.kv_tensor(B, H, T + 3, D, seed=61, n_out=4, factor=8.0)
     vx = synth.kv_tensor(B, H, T + 3, D, seed=62, n_out=4, factor=8.0)
     kt, vt = torch.from_numpy(kx).to(DEV), torch.from_numpy(vx).to(DEV)
