@@ -153,14 +153,28 @@ class InnerqDynamicLayer(CacheLayerMixin):
         return self._ref(self._vq, 2)
 
     # ---- prefill (cache.py:121-233) ----
-    def normalize_keys(self, key_states: torch.Tensor) -> Optional[torch.Tensor]:
-        """The key normalization factor for these keys (computed once, cache.py:121-126);
-        the division itself happens in the quantize kernel."""
+    def _key_norm(self, key_states: torch.Tensor) -> Optional[torch.Tensor]:
+        """The key normalization factor, computed once from the first keys that are
+        quantized (cache.py:121-126); the quantize kernels divide by it."""
         if not self.key_normalize:
             return None
         if self.key_normalization_factor is None:
             self.key_normalization_factor = ops.key_norm_factor(key_states)
         return self.key_normalization_factor
+
+    def normalize_keys(self, key_states: torch.Tensor) -> torch.Tensor:
+        """cache.py:121-126: the keys divided by the normalization factor (set from
+        these keys if unset), as the reference's method returns them."""
+        norm = self._key_norm(key_states)
+        return key_states if norm is None else key_states / norm
+
+    def unnormalize_keys(self, key_states: torch.Tensor) -> torch.Tensor:
+        """cache.py:128-133."""
+        if self.key_normalize:
+            if self.key_normalization_factor is None:
+                raise Exception('key_normalize is set to True but key_normalization_factor is not set')
+            key_states = key_states * self.key_normalization_factor
+        return key_states
 
     def initialize_keys_sink(self, key_states: torch.Tensor) -> torch.Tensor:
         viable_w_sink_key = min(self.key_w_sink, key_states.shape[-2])
@@ -223,7 +237,7 @@ class InnerqDynamicLayer(CacheLayerMixin):
     def _quantize_keys(self, key_states: torch.Tensor) -> None:
         if key_states.numel() == 0:
             return
-        norm = self.normalize_keys(key_states)
+        norm = self._key_norm(key_states)
         self._kq_for(key_states).append(key_states, norm)
 
     def _quantize_values(self, value_states: torch.Tensor) -> None:
@@ -251,6 +265,30 @@ class InnerqDynamicLayer(CacheLayerMixin):
         self.initialize_values_q(value_states)
         self._keep_dequantized_rows()
         self.is_initialized = True
+
+    # the reference's prefill and decode helpers (cache.py:212-224, 309-365), kept
+    # for callers and subclasses that drive them; update() / append() run the same
+    # state changes through the fused launches above and below
+    def initialize_sinks(self, key_states: torch.Tensor, value_states: torch.Tensor):
+        return self.initialize_keys_sink(key_states), self.initialize_values_sink(value_states)
+
+    def initialize_recents(self, key_states: torch.Tensor, value_states: torch.Tensor):
+        return self.initialize_keys_recent(key_states), self.initialize_values_recent(value_states)
+
+    def initial_quantization(self, key_states: torch.Tensor, value_states: torch.Tensor) -> None:
+        self.initialize_keys_q(key_states)
+        self.initialize_values_q(value_states)
+
+    def update_recents(self, key_states: torch.Tensor, value_states: torch.Tensor):
+        return self.update_keys_recent(key_states), self.update_values_recent(value_states)
+
+    def quantize_new_keys(self, key_states: torch.Tensor) -> None:
+        """cache.py:314-339: quantize these keys (normalized) and append them."""
+        self._quantize_keys(key_states)
+
+    def quantize_new_values(self, value_states: torch.Tensor) -> None:
+        """cache.py:341-365: quantize these values and append them."""
+        self._quantize_values(value_states)
 
     def _keep_dequantized_rows(self) -> None:
         """Tokens packed in one role while the other role still holds them in its
@@ -324,7 +362,7 @@ class InnerqDynamicLayer(CacheLayerMixin):
             kq = self._kq_for(key_states)
             if self.key_normalize:
                 if self.key_normalization_factor is None:  # the first flushed keys set it (cache.py:121-126)
-                    self.normalize_keys(torch.cat([self.keys_recent, key_states], dim=-2)[:, :, :kf])
+                    self._key_norm(torch.cat([self.keys_recent, key_states], dim=-2)[:, :, :kf])
                 norm = self.key_normalization_factor
         if vf:
             self._vq_for(value_states)

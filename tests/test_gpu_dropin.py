@@ -629,3 +629,39 @@ def test_attend_with_dequantized_window_rows(name):
         assert layer._kwin.deq_rows is False and used == 0
     else:
         assert layer._kwin.deq_rows and layer._vwin.deq_rows and used > steps // 2
+
+
+def test_reference_helper_methods_drive_the_same_state():
+    """The reference's prefill / decode helpers (cache.py:121-133, 212-224,
+    309-381) called one by one, as the reference's add_to_cache does, leave the
+    layer in the state update() reaches: equal dense K/V at every step; and
+    normalize_keys / unnormalize_keys return the keys divided / multiplied by
+    the factor as the reference's methods do."""
+    from innerq_amd import presets
+    cfg = presets.preset_config("innerq_hybrid")
+    B, H, D, prefill, steps = 2, 2, 128, 300, 40
+    kx = torch.from_numpy(synth.kv_tensor(B, H, prefill + steps, D, seed=71, n_out=2, factor=8.0)).to(DEV)
+    vx = torch.from_numpy(synth.kv_tensor(B, H, prefill + steps, D, seed=72, n_out=2, factor=8.0)).to(DEV)
+    a, b = C.InnerqDynamicLayer(cfg, 0), C.InnerqDynamicLayer(cfg, 0)
+    a.update(kx[:, :, :prefill], vx[:, :, :prefill])
+    b.dtype, b.device = kx.dtype, kx.device
+    k, v = b.initialize_sinks(kx[:, :, :prefill], vx[:, :, :prefill])
+    k, v = b.initialize_recents(k, v)
+    b.initial_quantization(k, v)
+    b.is_initialized = True
+    b.cumulative_length = prefill
+    for s in range(steps):
+        tok = slice(prefill + s, prefill + s + 1)
+        ka, va = a.update(kx[:, :, tok], vx[:, :, tok])
+        b.cumulative_length += 1
+        kf, vf = b.update_recents(kx[:, :, tok], vx[:, :, tok])
+        if kf.numel():
+            (b.quantize_new_keys if b._kq is not None else b.initialize_keys_q)(kf)
+        if vf.numel():
+            (b.quantize_new_values if b._vq is not None else b.initialize_values_q)(vf)
+        kb, vb = b.get_deq_tensors()
+        assert torch.equal(ka, kb) and torch.equal(va, vb), f"step {s + 1}"
+    n = a.key_normalization_factor
+    x = kx[:, :, :5]
+    assert torch.equal(a.normalize_keys(x), x / n)
+    assert torch.equal(a.unnormalize_keys(x), x * n)
