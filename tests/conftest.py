@@ -27,6 +27,12 @@ def cache_golden():
 
 
 @pytest.fixture(scope="session")
+def axes_golden():
+    import numpy as np
+    return np.load(os.path.join(GOLDEN, "axes_golden.npz"))
+
+
+@pytest.fixture(scope="session")
 def hybrid_ties():
     import numpy as np
     return np.load(os.path.join(GOLDEN, "hybrid_ties.npz"))

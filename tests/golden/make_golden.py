@@ -30,11 +30,15 @@ sliding_golden.npz  InnerqDynamicSlidingWindowLayer.update() traces
                     reference indexes [:, :, -w, :]), the recent-window lengths
                     and get_mask_sizes() before the call.
 
+axes_golden.npz     update() traces, as in cache_golden.npz, of layers with keys
+                    grouped along tokens and values along head_dim (the KIVI
+                    presets of scripts/run_lmeval.sh:54-93, and sym keys with
+                    hybrid values on those axes).
 hybrid_ties.npz     groups whose two hybrid L1 errors tie exactly (the
                     comparison quant.py:144 makes is strict) and the
                     reference's masks for them.
 
-Usage:  python tests/golden/make_golden.py [/root/reference] [--sliding-only | --bf16-only | --ties-only]
+Usage:  python tests/golden/make_golden.py [/root/reference] [--sliding-only | --bf16-only | --ties-only | --axes-only]
 """
 from __future__ import annotations
 
@@ -285,11 +289,15 @@ def hybrid_tie_fixtures(quant):
     return out
 
 
-def main(root, sliding_only=False, bf16_only=False, ties_only=False):
+def main(root, sliding_only=False, bf16_only=False, ties_only=False, axes_only=False):
     quant, cache = load_reference(root)
     if ties_only:
         np.savez_compressed(os.path.join(HERE, "hybrid_ties.npz"), **hybrid_tie_fixtures(quant))
         print("wrote", os.path.join(HERE, "hybrid_ties.npz"))
+        return
+    if axes_only:
+        np.savez_compressed(os.path.join(HERE, "axes_golden.npz"), **cache_traces(cache, AXES_PRESETS))
+        print("wrote", os.path.join(HERE, "axes_golden.npz"))
         return
     if bf16_only:
         np.savez_compressed(os.path.join(HERE, "bf16_golden.npz"), **bf16_fixtures(quant, cache, PRESETS))
@@ -349,6 +357,37 @@ def main(root, sliding_only=False, bf16_only=False, ties_only=False):
     np.savez_compressed(os.path.join(HERE, "quant_golden.npz"), **out)
 
     # ---------------- cache traces ----------------
+    trace = cache_traces(cache, PRESETS)
+    np.savez_compressed(os.path.join(HERE, "cache_golden.npz"), **trace)
+    np.savez_compressed(os.path.join(HERE, "bf16_golden.npz"), **bf16_fixtures(quant, cache, PRESETS))
+    np.savez_compressed(os.path.join(HERE, "axes_golden.npz"), **cache_traces(cache, AXES_PRESETS))
+    print("wrote", os.path.join(HERE, "quant_golden.npz"), os.path.join(HERE, "cache_golden.npz"))
+
+
+# The KIVI axis choices (scripts/run_lmeval.sh:54-93): keys grouped along
+# tokens, values along head_dim, flushes of 32 keys and of single values.
+AXES_PRESETS = {
+    "kivi": dict(k_bits=2, v_bits=2, key_flush_size=32, value_flush_size=1, key_group_size=32,
+                 value_group_size=32, key_w_recent=128, value_w_recent=128, key_w_sink=0, value_w_sink=0,
+                 key_normalize=False, key_quantize_over_token=True, value_quantize_over_token=False,
+                 key_quantize_mode="asymmetric", value_quantize_mode="asymmetric"),
+    "kivi_sink": dict(k_bits=2, v_bits=2, key_flush_size=32, value_flush_size=1, key_group_size=32,
+                      value_group_size=32, key_w_recent=96, value_w_recent=96, key_w_sink=32, value_w_sink=32,
+                      key_normalize=False, key_quantize_over_token=True, value_quantize_over_token=False,
+                      key_quantize_mode="asymmetric", value_quantize_mode="asymmetric"),
+    # the same axes with sym keys and 3-bit hybrid values (every mode on both axes)
+    "axes_sym_hybrid": dict(k_bits=4, v_bits=3, key_flush_size=32, value_flush_size=1, key_group_size=32,
+                            value_group_size=32, key_w_recent=64, value_w_recent=48, key_w_sink=8,
+                            value_w_sink=4, key_normalize=False, key_quantize_over_token=True,
+                            value_quantize_over_token=False, key_quantize_mode="symmetric",
+                            value_quantize_mode="hybrid"),
+}
+
+
+def cache_traces(cache, presets):
+    """update() traces of the live reference's layer: per step the sha256 of
+    the returned K and V, their lengths and the recent windows' lengths, and
+    the last step's arrays."""
     class Layer(cache.InnerqDynamicLayer):
         def get_max_length(self):   # abstract in the installed transformers
             return -1
@@ -356,7 +395,6 @@ def main(root, sliding_only=False, bf16_only=False, ties_only=False):
     class Cfg:
         pass
 
-    presets = PRESETS
     trace = {}
     B, H, D = 1, 2, 64
     prefill, steps = 150, 70
@@ -381,12 +419,11 @@ def main(root, sliding_only=False, bf16_only=False, ties_only=False):
             trace[f"{name}_step{s + 1}_sha256"] = digest(np.concatenate([f16(K).ravel(), f16(V).ravel()]))
             trace[f"{name}_len{s + 1}"] = np.array([K.shape[-2], V.shape[-2],
                                                     layer.keys_recent.shape[-2], layer.values_recent.shape[-2]])
-    np.savez_compressed(os.path.join(HERE, "cache_golden.npz"), **trace)
-    np.savez_compressed(os.path.join(HERE, "bf16_golden.npz"), **bf16_fixtures(quant, cache, PRESETS))
-    print("wrote", os.path.join(HERE, "quant_golden.npz"), os.path.join(HERE, "cache_golden.npz"))
+    return trace
 
 
 if __name__ == "__main__":
     args = [a for a in sys.argv[1:] if not a.startswith("--")]
     main(args[0] if args else "/root/reference", sliding_only="--sliding-only" in sys.argv,
-         bf16_only="--bf16-only" in sys.argv, ties_only="--ties-only" in sys.argv)
+         bf16_only="--bf16-only" in sys.argv, ties_only="--ties-only" in sys.argv,
+         axes_only="--axes-only" in sys.argv)

@@ -18,7 +18,7 @@ from innerq_amd import quant as IQ
 from innerq_amd import synth
 from oracle import attn_ref as A
 from oracle import quant_ref as Q
-from tests.test_oracle_cache import PRESETS, Cfg, golden_inputs
+from tests.test_oracle_cache import AXES_PRESETS, PRESETS, Cfg, golden_inputs
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
@@ -102,12 +102,31 @@ def test_cache_update_matches_reference_trace(cache_golden, name):
     oracle's (pinned bit-exact to the reference traces) and to the reference's
     last-step arrays.  Values, not bits: the packed sym format does not keep the
     sign of a zero code, so the reference's -0.0 comes back as +0.0."""
+    _check_update_trace(cache_golden, name, PRESETS[name])
+
+
+@pytest.mark.parametrize("name", list(AXES_PRESETS))
+def test_cache_update_matches_axes_trace(axes_golden, name):
+    """The same with keys grouped along tokens and values along head_dim (the
+    KIVI presets, scripts/run_lmeval.sh:54-93; sym keys with hybrid values):
+    token-axis K stores flushed 32 tokens at a time, channel-axis V stores one
+    token at a time.  These layers decode through update()'s dense K/V (the
+    fused attend() reads K grouped along head_dim only and says so)."""
+    _check_update_trace(axes_golden, name, AXES_PRESETS[name])
+    layer = C.InnerqDynamicLayer(Cfg(**AXES_PRESETS[name]), 0)
+    x = torch.zeros(1, 2, 200, 64, dtype=torch.float16, device=DEV)
+    layer.update(x, x)
+    assert not layer.fused_decode_ready(x[:, :, :1])
+    with pytest.raises(NotImplementedError):
+        layer.attend(torch.zeros(1, 2, 1, 64, dtype=torch.float16, device=DEV), 0.125)
+
+
+def _check_update_trace(g, name, cfg):
     from oracle import cache_ref
-    g = cache_golden
     kx, vx, prefill, steps = golden_inputs(g, name)
     kt, vt = torch.from_numpy(kx).to(DEV), torch.from_numpy(vx).to(DEV)
-    layer = C.InnerqDynamicLayer(Cfg(**PRESETS[name]), 0)
-    ref = cache_ref.CacheLayerRef(Cfg(**PRESETS[name]))
+    layer = C.InnerqDynamicLayer(Cfg(**cfg), 0)
+    ref = cache_ref.CacheLayerRef(Cfg(**cfg))
     K, V = layer.update(kt[:, :, :prefill].clone(), vt[:, :, :prefill].clone())
     Kr, Vr = ref.update(kx[:, :, :prefill], vx[:, :, :prefill])
     np.testing.assert_array_equal(_sha16(_np(K), _np(V)), g[f"{name}_step0_sha256"])

@@ -51,11 +51,42 @@ def golden_inputs(g, name):
     return kx, vx, prefill, steps
 
 
+# Keys grouped along tokens and values along head_dim: the KIVI presets
+# (scripts/run_lmeval.sh:54-93) and sym keys with hybrid values on those axes
+# (traces in axes_golden.npz).
+AXES_PRESETS = {
+    "kivi": dict(k_bits=2, v_bits=2, key_flush_size=32, value_flush_size=1, key_group_size=32,
+                 value_group_size=32, key_w_recent=128, value_w_recent=128, key_w_sink=0, value_w_sink=0,
+                 key_normalize=False, key_quantize_over_token=True, value_quantize_over_token=False,
+                 key_quantize_mode="asymmetric", value_quantize_mode="asymmetric"),
+    "kivi_sink": dict(k_bits=2, v_bits=2, key_flush_size=32, value_flush_size=1, key_group_size=32,
+                      value_group_size=32, key_w_recent=96, value_w_recent=96, key_w_sink=32, value_w_sink=32,
+                      key_normalize=False, key_quantize_over_token=True, value_quantize_over_token=False,
+                      key_quantize_mode="asymmetric", value_quantize_mode="asymmetric"),
+    "axes_sym_hybrid": dict(k_bits=4, v_bits=3, key_flush_size=32, value_flush_size=1, key_group_size=32,
+                            value_group_size=32, key_w_recent=64, value_w_recent=48, key_w_sink=8,
+                            value_w_sink=4, key_normalize=False, key_quantize_over_token=True,
+                            value_quantize_over_token=False, key_quantize_mode="symmetric",
+                            value_quantize_mode="hybrid"),
+}
+
+
+@pytest.mark.parametrize("name", list(AXES_PRESETS))
+def test_cache_oracle_matches_axes_trace(axes_golden, name):
+    """the oracle's layer with keys over tokens and values over channels
+    (cache.py:93-119, the flush of 32 keys along the token axis) reproduces
+    the live reference's traces step for step"""
+    _check_oracle_trace(axes_golden, name, AXES_PRESETS[name])
+
+
 @pytest.mark.parametrize("name", list(PRESETS))
 def test_cache_oracle_matches_reference_trace(cache_golden, name):
-    g = cache_golden
+    _check_oracle_trace(cache_golden, name, PRESETS[name])
+
+
+def _check_oracle_trace(g, name, cfg):
     kx, vx, prefill, steps = golden_inputs(g, name)
-    layer = cache_ref.CacheLayerRef(Cfg(**PRESETS[name]))
+    layer = cache_ref.CacheLayerRef(Cfg(**cfg))
     K, V = layer.update(kx[:, :, :prefill], vx[:, :, :prefill])
     np.testing.assert_array_equal(_sha(K, V), g[f"{name}_step0_sha256"])
     for s in range(steps):
