@@ -71,6 +71,13 @@ AXES_PRESETS = {
 }
 
 
+def test_kivi_presets_are_the_traced_configs():
+    """innerq_amd.presets' KIVI entries are the configurations traced above"""
+    from innerq_amd import presets
+    for name in ("kivi", "kivi_sink"):
+        assert presets.PRESETS[name] == AXES_PRESETS[name]
+
+
 @pytest.mark.parametrize("name", list(AXES_PRESETS))
 def test_cache_oracle_matches_axes_trace(axes_golden, name):
     """the oracle's layer with keys over tokens and values over channels
