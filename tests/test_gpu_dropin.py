@@ -240,7 +240,7 @@ def _tiny_llama(preset):
     from innerq_amd.models import InnerqLlamaForCausalLM
     cfg = LlamaConfig(num_hidden_layers=2, num_attention_heads=8, num_key_value_heads=2, hidden_size=512,
                       intermediate_size=256, vocab_size=64, max_position_embeddings=512)
-    for k, v in PRESETS[preset].items():
+    for k, v in {**PRESETS, **AXES_PRESETS}[preset].items():
         setattr(cfg, k, v)
     torch.manual_seed(0)
     return InnerqLlamaForCausalLM(cfg).to(device=DEV, dtype=torch.float16).eval()
@@ -287,6 +287,32 @@ def test_fused_attention_in_llama_matches_reference_path(preset, monkeypatch):
     assert ((got - ref).abs().max() / ref.abs().max()).item() < 2e-2
     # every decode step of both layers went through attend()
     assert calls[0] == 2 * dec.shape[1]
+
+
+def test_kivi_llama_under_fused_attention_takes_the_dense_path(monkeypatch):
+    """A Llama whose cache groups keys along tokens (the kivi_sink preset) under
+    attn_implementation="innerq_fused": the cache hands its dequantized K/V to
+    sdpa at every step (attend() never runs), and the logits match the
+    reference's path (eager attention over the same dequantized K/V)."""
+    model = _tiny_llama("kivi_sink")
+    gen = torch.Generator(device=DEV).manual_seed(5)
+    ids = torch.randint(0, 64, (2, 200), generator=gen, device=DEV)
+    dec = torch.randint(0, 64, (2, 20), generator=gen, device=DEV)
+    calls = _count_attend(monkeypatch)
+    logits = {}
+    for attn in ("eager", "innerq_fused"):
+        model.config._attn_implementation = attn
+        cache = C.DynamicCache(config=model.config)
+        steps = []
+        with torch.no_grad():
+            model(ids, past_key_values=cache, use_cache=True)
+            for t in range(dec.shape[1]):
+                steps.append(model(dec[:, t:t + 1], past_key_values=cache, use_cache=True).logits[:, -1].float())
+        assert cache.get_seq_length() == 220
+        logits[attn] = torch.stack(steps)
+    ref, got = logits["eager"], logits["innerq_fused"]
+    assert ((got - ref).abs().max() / ref.abs().max()).item() < 1e-2
+    assert calls[0] == 0
 
 
 def test_fused_attention_padded_batch(monkeypatch):
